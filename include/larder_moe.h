@@ -1,0 +1,103 @@
+/* larder_moe.h: C ABI of the MI355X (gfx950) routed-expert MoE layer over GGUF Q4_0 / Q4_K blocks.
+ *
+ * Every entry point:
+ *   - takes device pointers and plain sizes, and a hipStream_t passed as void* (NULL = the null stream);
+ *   - only enqueues work on that stream: no host synchronisation, no allocation;
+ *   - returns 0 on success, a positive hipError_t when a HIP call failed, or a negative LMOE_E* code when an
+ *     argument was refused; lmoe_error() then returns a one-sentence reason (thread-local).
+ * Expert buffers are the reference's arena layout: uint8 [n_experts][rows][row bytes] with row bytes
+ * cols / 32 * 18 (Q4_0) or cols / 256 * 144 (Q4_K), 16-byte aligned (stream_fast.py:3936-3941).
+ * Workspaces are caller-owned device memory, sized by the matching *_workspace_bytes query, zero-filled once
+ * before first use; every kernel that uses one leaves it zero-filled again when it ends.
+ */
+#ifndef LARDER_MOE_H
+#define LARDER_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of activations, logits and outputs */
+enum { LMOE_F32 = 0, LMOE_F16 = 1, LMOE_BF16 = 2 };
+/* ggml block types, by ggml type id (gguf_ref.py:8-15) */
+enum { LMOE_Q4_0 = 2, LMOE_Q4_K = 12 };
+/* refusals */
+enum { LMOE_EINVAL = -1, LMOE_ETYPE = -2, LMOE_ESHAPE = -3, LMOE_EALIGN = -4, LMOE_EWORKSPACE = -5 };
+
+/* The reason for the last nonzero return on this thread ("" if none). */
+const char *lmoe_error(void);
+/* ABI version, bumped on any signature change. */
+int lmoe_abi_version(void);
+
+/* Router top-k over given logits. Replaces route_cuda.probs (route_cuda.py:280-288; kernel moe_probs
+ * route_cuda.py:193-254) and the block's softmax/argpartition/take/renorm ops (stream_fast.py:4352-4370).
+ * logits [T][E] in ldtype -> ids [T][k] best first (ties: lowest expert index), scores [T][k] fp32 softmax
+ * probabilities of the picked experts, renormalised to sum 1 when norm != 0. E <= 1024, k <= 32. */
+int lmoe_router_topk(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids, float *scores,
+                     void *stream);
+
+/* Decode router: logits[t][e] = x[t] . wr[e] (fp32 accumulation), optionally the shared-expert gate logit
+ * x[t] . wsg as logits[t][E] (row stride E + 1 then), then top-k as lmoe_router_topk. Replaces the block's
+ * gate linear plus route_cuda.probs on decode rows (route_cuda.py:433-444; stream_fast.py:4358, 4375).
+ * x [T][H] in xdtype, wr [E][H] and wsg [H] in wdtype (F16, BF16 or F32), T <= 16, H % 64 == 0.
+ * Workspace: lmoe_router_workspace_bytes(). */
+size_t lmoe_router_workspace_bytes(void);
+int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T, int H,
+                          int E, int k, int norm, float *logits, uint32_t *ids, float *scores, void *ws,
+                          void *stream);
+
+/* Decode chain, gate/up: h[s][i] = silu(x[s / topk] . wg[slots[s]][i]) * (x[s / topk] . wu[slots[s]][i]),
+ * fp32. Replaces gguf_experts kernel gguf_gate_up (gguf_experts.py:452-495) as driven by _chain
+ * (gguf_experts.py:610-623). x [n_slots / topk][H] in xdtype; slots >= n_experts give h rows of zeros.
+ * H % 64 == 0 (Q4_0) or H % 256 == 0 (Q4_K). */
+int lmoe_gemv_gate_up(const void *x, int xdtype, const uint32_t *slots, int n_slots, int topk, const uint8_t *wg,
+                      const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I, float *h,
+                      void *stream);
+
+/* Decode chain, down with the weighted combine fused:
+ *   out[t][n] = sum_j scores[t][j] * (h[t * k + j] . wd[ids[t][j]][n])
+ *               (+ sigmoid(gate[t * gate_stride]) * shared[t][n]) (+ residual[t][n])
+ * with scores == NULL meaning 1 (then out is gguf_experts kernel gguf_down's unweighted y, gguf_experts.py:499-526,
+ * with T = n_slots, k = 1). Replaces gguf_down plus route_cuda.tail / the block's combine (route_cuda.py:256-264,
+ * 291-298; stream_fast.py:4372-4376). h [T * k][I] fp32, shared [T][H] fp32 or NULL, gate fp32 or NULL,
+ * residual [T][H] in rdtype or NULL, out [T][H] in odtype. ids >= n_experts contribute zero. */
+int lmoe_gemv_down_combine(const float *h, const uint32_t *ids, const float *scores, int T, int k,
+                           const uint8_t *wd, int type_d, int n_experts, int I, int H, const float *shared,
+                           const float *gate, int gate_stride, const void *residual, int rdtype, void *out,
+                           int odtype, void *stream);
+
+/* Device-side ragged grouping: the stable counting sort of the flattened (token, k) expert ids, the device
+ * form of stream_fast.py:5466-5471 (argsort of the flat ids and its inverse) and gguf_experts.py:702-713.
+ * ids [R] -> counts [E], offsets [E + 1], order [R] (rows of expert 0 in flat order, then expert 1, ...; ids >= E
+ * after all of them), inv [R] (inv[order[p]] = p), and the grouped GEMM's work list (tiles [max_tiles] of
+ * (expert << 20 | first row / bm), n_tiles [1]) for m-tiles of bm rows. R <= 2^24, E <= 1024.
+ * Workspace: lmoe_group_workspace_bytes(R, E). */
+size_t lmoe_group_workspace_bytes(int R, int E);
+int lmoe_group_rows(const uint32_t *ids, int R, int E, int bm, uint32_t *counts, uint32_t *offsets,
+                    uint32_t *order, uint32_t *inv, uint32_t *tiles, uint32_t *n_tiles, void *ws, void *stream);
+/* Upper bound on the grouped GEMM tiles for R rows over E experts at bm rows a tile. */
+int lmoe_max_tiles(int R, int E, int bm);
+
+/* Weighted combine of rows kept in grouped (expert-sorted) order:
+ *   out[t][n] = sum_j scores[t][j] * y[inv[t * k + j]][n] (+ sigmoid(gate) * shared) (+ residual)
+ * y [R][H] in ydtype. Replaces the unsort plus combine of stream_fast.py:5525 and 4372-4376. */
+int lmoe_combine_sorted(const void *y, int ydtype, const uint32_t *inv, const float *scores, int T, int k, int H,
+                        const float *shared, const float *gate, int gate_stride, const void *residual,
+                        int rdtype, void *out, int odtype, void *stream);
+
+/* Experts at `slots` of buf [S][rows][row bytes] as dense weights q [n][rows][cols] in odtype (F16, BF16, F32).
+ * Replaces gguf_experts.dequant (gguf_experts.py:579-586; kernel gguf_dequant :529-539). */
+int lmoe_dequant(const uint8_t *buf, int type, int n_experts, int rows, int cols, const uint32_t *slots, int n,
+                 void *q, int odtype, void *stream);
+
+/* Q4_0 quantizer on the device, ggml's quantize_row_q4_0_ref rule (no counterpart in the reference, which only
+ * reads packs llama.cpp wrote): w [rows][cols] in wdtype -> out [rows][cols / 32 * 18]. */
+int lmoe_quantize_q4_0(const void *w, int wdtype, long long rows, int cols, uint8_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LARDER_MOE_H */

@@ -1,0 +1,107 @@
+"""ctypes binding of liblarder_moe.so (include/larder_moe.h) and torch-tensor helpers.
+
+The library is built in-tree by ``python3 -m larder_amd.build`` (or ``__graft_entry__.build()``). Loading fails
+loudly when it is missing: there is no CPU or eager fallback anywhere in this package. Errors follow the
+reference's native C-ABI convention (native/moe_pipe_cuda.py:95-97): every call returns an int and the reason is
+read from ``lmoe_error()``; a refused ggml type raises ValueError (the reference's load-time refusal,
+stream_fast.py:8058-8061), any other refusal or HIP failure raises RuntimeError.
+"""
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "liblarder_moe.so"
+
+F32, F16, BF16 = 0, 1, 2
+Q4_0, Q4_K = 2, 12
+EINVAL, ETYPE, ESHAPE, EALIGN, EWORKSPACE = -1, -2, -3, -4, -5
+ABI_VERSION = 1
+
+DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+# ggml type name -> (ggml type id, weights a block, bytes a block) (gguf_ref.py:8-15)
+TYPES = {"Q4_0": (2, 32, 18), "Q4_K": (12, 256, 144)}
+
+_P, _I, _SZ, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_longlong
+# name -> (restype, argtypes): every symbol include/larder_moe.h declares
+SIGNATURES = {
+    "lmoe_error": (ctypes.c_char_p, []),
+    "lmoe_abi_version": (_I, []),
+    "lmoe_router_topk": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "lmoe_router_workspace_bytes": (_SZ, []),
+    "lmoe_router_gemv_topk": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "lmoe_gemv_gate_up": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
+    "lmoe_gemv_down_combine": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
+    "lmoe_group_workspace_bytes": (_SZ, [_I, _I]),
+    "lmoe_group_rows": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "lmoe_max_tiles": (_I, [_I, _I, _I]),
+    "lmoe_combine_sorted": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
+    "lmoe_dequant": (_I, [_P, _I, _I, _I, _I, _P, _I, _P, _I, _P]),
+    "lmoe_quantize_q4_0": (_I, [_P, _I, _LL, _I, _P, _P]),
+}
+
+_LIB = None
+
+
+def lib():
+    """The loaded library (loaded once); raises RuntimeError when it is not built."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python3 -m larder_amd.build` (hipcc, gfx950)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        if L.lmoe_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH}: ABI {L.lmoe_abi_version()} but this package speaks {ABI_VERSION}")
+        _LIB = L
+    return _LIB
+
+
+def call(name, *args):
+    """Call an entry point; raise on a nonzero return with the library's reason."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        why = lib().lmoe_error().decode()
+        if rc == ETYPE:
+            raise ValueError(why)
+        raise RuntimeError(f"{name} returned {rc}: {why}")
+    return rc
+
+
+def ptr(t):
+    """Device pointer of a CUDA tensor (None -> NULL)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("larder_amd: tensors must live on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("larder_amd: tensors must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def dcode(dtype):
+    try:
+        return DTYPE_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"larder_amd: dtype {dtype} is not float32, float16 or bfloat16") from None
+
+
+def qcode(t):
+    """ggml type name -> ggml type id; ValueError for any type this path does not implement."""
+    if t not in TYPES:
+        raise ValueError(f"larder_amd: ggml type {t} is not supported (Q4_0 and Q4_K are)")
+    return TYPES[t][0]
+
+
+def stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def row_bytes(t, n):
+    _, be, bb = TYPES[t]
+    if n % be:
+        raise ValueError(f"{t}: a row of {n} weights is not a whole number of {be}-weight blocks")
+    return n // be * bb

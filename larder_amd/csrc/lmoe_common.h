@@ -1,0 +1,208 @@
+// Shared device helpers and host plumbing for the gfx950 MoE kernels.
+//
+// Weight "units": both block types this library reads are 0.5625 bytes a weight, so a run of 64 weights of a
+// row is 36 bytes in either of them: two Q4_0 blocks (18 bytes each: f16 d, 16 bytes of nibbles), or one quarter
+// of a Q4_K super-block (256 weights in 144 bytes: f16 d, f16 dmin, 12 bytes of 6-bit scales/mins, 128 bytes of
+// nibbles). Row bytes are 36 * (cols / 64) for both, so one staging scheme serves both types.
+//
+// Dot products run on v_dot2_f32_f16: x is held as f16 pairs arranged in the order the nibbles sit in a 32-bit
+// word, and a nibble q becomes the f16 value 16 + q by masking it into mantissa bits 6..9 under the exponent of
+// 16 (0x4C00). Then sum((16 + q) x) = 16 sum(x) + sum(q x): the block's exact sum(q x) follows from one fused
+// multiply-add with the block's precomputed sum(x). Products of f16 values are exact in fp32, so the dot is an
+// fp32-accumulated dot of the exact integer nibbles with the f16 activations.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/larder_moe.h"
+
+namespace lmoe {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- host-side error plumbing ----------------------------------------------------------------------------------
+
+void set_error(const char *fmt, ...);
+int fail(int code, const char *fmt, ...);
+int hip_fail(hipError_t e, const char *what);
+
+#define LMOE_REQUIRE(cond, code, ...)            \
+  do {                                           \
+    if (!(cond)) return ::lmoe::fail((code), __VA_ARGS__); \
+  } while (0)
+
+#define LMOE_LAUNCHED(what)                                  \
+  do {                                                       \
+    hipError_t _e = hipGetLastError();                       \
+    if (_e != hipSuccess) return ::lmoe::hip_fail(_e, what); \
+  } while (0)
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+inline bool dtype_ok(int t) { return t == LMOE_F32 || t == LMOE_F16 || t == LMOE_BF16; }
+inline bool qtype_ok(int t) { return t == LMOE_Q4_0 || t == LMOE_Q4_K; }
+inline int block_weights(int t) { return t == LMOE_Q4_K ? 256 : 32; }
+// bytes of a [rows][cols] matrix in block type t
+inline size_t matrix_bytes(int t, size_t rows, size_t cols) { return rows * (cols / 64) * 36; }
+
+// ---- element loads / stores ------------------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// round to nearest even, NaN kept quiet
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ float load_elt(const void *p, size_t i, int dt) {
+  if (dt == LMOE_F32) return static_cast<const float *>(p)[i];
+  if (dt == LMOE_F16) return float(static_cast<const _Float16 *>(p)[i]);
+  return bf16_to_f32(static_cast<const uint16_t *>(p)[i]);
+}
+
+__device__ __forceinline__ void store_elt(void *p, size_t i, float v, int dt) {
+  if (dt == LMOE_F32)
+    static_cast<float *>(p)[i] = v;
+  else if (dt == LMOE_F16)
+    static_cast<_Float16 *>(p)[i] = _Float16(v);
+  else
+    static_cast<uint16_t *>(p)[i] = f32_to_bf16(v);
+}
+
+__device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + __expf(-v)); }
+
+// silu(g) * u; the exponential only ever sees -|g|, so it never overflows
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float e = __expf(-fabsf(g));
+  const float s = g >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+  return g * s * u;
+}
+
+// ---- wavefront (64 lanes) reductions ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// ---- nibble words -> f16 pairs ----------------------------------------------------------------------------------
+
+// The f16 pair (16 + a, 16 + b) from nibbles a, b sitting at bits [s, s+4) and [s+16, s+20) of w (0 <= s <= 12).
+template <int S>
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w) {
+  const uint32_t t = S <= 6 ? (w << (6 - S)) : (w >> (S - 6));
+  return (t & 0x03C003C0u) | 0x4C004C00u;
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a), __builtin_bit_cast(h2_t, b), c, false);
+}
+
+// sum((16 + q) x) over the 8 nibbles of qs word w against x pairs xp[0..3] =
+// (x[j], x[j+2]), (x[j+H], x[j+H+2]), (x[j+1], x[j+3]), (x[j+H+1], x[j+H+3]) where the word's low nibbles are
+// weights j..j+3 and its high nibbles weights j+H..j+H+3 (H = 16 for Q4_0, 32 for Q4_K).
+__device__ __forceinline__ float word_dot(uint32_t w, const uint32_t *xp, float acc) {
+  acc = dot2(nib_pair<0>(w), xp[0], acc);
+  acc = dot2(nib_pair<4>(w), xp[1], acc);
+  acc = dot2(nib_pair<8>(w), xp[2], acc);
+  acc = dot2(nib_pair<12>(w), xp[3], acc);
+  return acc;
+}
+
+__device__ __forceinline__ float half_lo(uint32_t w) { return float(__builtin_bit_cast(h2_t, w)[0]); }
+__device__ __forceinline__ float half_hi(uint32_t w) { return float(__builtin_bit_cast(h2_t, w)[1]); }
+
+// ---- x arrangement ----------------------------------------------------------------------------------------------
+//
+// A unit of 64 weights takes 32 dwords of x pairs, arranged so that word i of a block's (or sub-block pair's)
+// nibbles meets the four pairs word_dot() expects.
+//
+// Q4_0 block (32 weights): qs word i (i = 0..3) holds weights 4i..4i+3 (low) and 16+4i..16+4i+3 (high).
+// Q4_K sub-block pair (64 weights): qs word i (i = 0..7) holds weights 4i..4i+3 of sub-block 2c (low nibbles) and
+//   the same of sub-block 2c+1 (high nibbles), i.e. unit weights 4i.. and 32+4i...
+// Both are "word i covers weights {4i..4i+3} + {H+4i..H+4i+3}" over a span of 2H weights, H = 16 (two spans a
+// unit) or 32 (one span). A span of 2H weights fills H dwords. Dword dw of the unit, half h, holds weight
+// span * 2H + hi * H + 4i + r with span = dw / H, i = (dw mod H) / 4, s = dw mod 4 the pair slot (A, B, C, D =
+// 0..3: r even / odd, low / high nibbles), hi = s & 1 and r = (s >> 1) + 2h.
+__device__ __forceinline__ int xelem(int dw, int h, int H) {
+  const int span = dw / H, i = (dw % H) >> 2, s = dw & 3;
+  return span * 2 * H + (s & 1) * H + 4 * i + (s >> 1) + 2 * h;
+}
+
+// qs word i of Q4_K sub-block pair c from the 12-byte scale field words s0, s1, s2: (sc, m) of sub-blocks 2c and
+// 2c + 1, ggml's get_scale_min_k4 (gguf_ref.py:253-258): j < 4: sc = q[j] & 63, m = q[j+4] & 63; j >= 4:
+// sc = (q[j+4] & 15) | (q[j-4] >> 6) << 4, m = (q[j+4] >> 4) | (q[j] >> 6) << 4.
+__device__ __forceinline__ uint32_t byte_of(uint32_t s0, uint32_t s1, uint32_t s2, int j) {
+  const uint32_t w = j < 4 ? s0 : (j < 8 ? s1 : s2);
+  return (w >> (8 * (j & 3))) & 0xFFu;
+}
+__device__ __forceinline__ void k4_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, float *sc, float *m) {
+  uint32_t a, b;
+  if (j < 4) {
+    a = byte_of(s0, s1, s2, j) & 63u;
+    b = byte_of(s0, s1, s2, j + 4) & 63u;
+  } else {
+    const uint32_t q8 = byte_of(s0, s1, s2, j + 4);
+    a = (q8 & 15u) | ((byte_of(s0, s1, s2, j - 4) >> 6) << 4);
+    b = (q8 >> 4) | ((byte_of(s0, s1, s2, j) >> 6) << 4);
+  }
+  *sc = float(a);
+  *m = float(b);
+}
+
+// One 64-weight unit's dot with x, given the unit's 36 bytes as 9 dwords u[0..8] (Q4_0: two blocks; the unit
+// starts 4-byte aligned) or, for Q4_K, the super-block header h[0..3] and the 8 qs words q[0..7] of pair c.
+// xp: the unit's 32 x-pair dwords; sx0/sx1: sum of x over the unit's first / last 32 weights.
+__device__ __forceinline__ float unit_dot_q4_0(const uint32_t *u, const uint32_t *xp, float sx0, float sx1) {
+  // block A: d = low half of u0, qs bytes at unit bytes 2..17 -> realign by 2 bytes
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a = word_dot(__builtin_amdgcn_alignbyte(u[i + 1], u[i], 2), xp + 4 * i, a);
+  // block B: d = high half of u4, qs = u5..u8
+  float b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b = word_dot(u[5 + i], xp + 16 + 4 * i, b);
+  const float dA = half_lo(u[0]), dB = half_hi(u[4]);
+  // sum((q - 8) x) = sum((16 + q) x) - 24 sum(x)
+  return dA * fmaf(-24.0f, sx0, a) + dB * fmaf(-24.0f, sx1, b);
+}
+
+__device__ __forceinline__ float unit_dot_q4_k(const uint32_t *hdr, const uint32_t *q, int c, const uint32_t *xp,
+                                               float sx0, float sx1) {
+  float a = 0.0f, b = 0.0f;
+  // word i: low nibbles -> sub-block 2c weights 4i..4i+3, high -> sub-block 2c+1; word_dot pairs (A, B, C, D)
+  // are (lo 4i/4i+2, hi 4i/4i+2, lo 4i+1/4i+3, hi 4i+1/4i+3): low-nibble pairs feed a, high-nibble pairs b.
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t w = q[i];
+    a = dot2(nib_pair<0>(w), xp[4 * i + 0], a);
+    b = dot2(nib_pair<4>(w), xp[4 * i + 1], b);
+    a = dot2(nib_pair<8>(w), xp[4 * i + 2], a);
+    b = dot2(nib_pair<12>(w), xp[4 * i + 3], b);
+  }
+  const float d = half_lo(hdr[0]), dmin = half_hi(hdr[0]);
+  float sc0, m0, sc1, m1;
+  k4_scale_min(hdr[1], hdr[2], hdr[3], 2 * c, &sc0, &m0);
+  k4_scale_min(hdr[1], hdr[2], hdr[3], 2 * c + 1, &sc1, &m1);
+  // w = (d sc) q - (dmin m): sum(w x) = (d sc) (sum((16 + q) x) - 16 sum(x)) - (dmin m) sum(x)
+  const float ra = (d * sc0) * fmaf(-16.0f, sx0, a) - (dmin * m0) * sx0;
+  const float rb = (d * sc1) * fmaf(-16.0f, sx1, b) - (dmin * m1) * sx1;
+  return ra + rb;
+}
+
+}  // namespace lmoe

@@ -1,0 +1,151 @@
+// Smaller kernels around the path: the weighted combine of grouped rows, the dequant of whole experts, and a
+// Q4_0 quantizer used to build synthetic packs on the device.
+#include "lmoe_common.h"
+
+namespace lmoe {
+
+// out[t][n] = sum_j scores[t][j] y[inv[t k + j]][n] (+ sigmoid(gate) shared) (+ residual); grid (H / 256, T).
+__global__ void __launch_bounds__(256)
+    k_combine_sorted(const void *y, int ydt, const uint32_t *inv, const float *scores, int k, int H,
+                     const float *shared, const float *gate, int gate_stride, const void *residual, int rdt,
+                     void *out, int odt) {
+  const int t = blockIdx.y;
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= H) return;
+  float acc = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const size_t row = inv[size_t(t) * k + j];
+    const float s = scores ? scores[size_t(t) * k + j] : 1.0f;
+    acc = fmaf(s, load_elt(y, row * H + n, ydt), acc);
+  }
+  const size_t o = size_t(t) * H + n;
+  if (shared) acc += sigmoidf_(gate[size_t(t) * gate_stride]) * shared[o];
+  if (residual) acc += load_elt(residual, o, rdt);
+  store_elt(out, o, acc, odt);
+}
+
+// One thread a 64-weight unit of one row of one expert: q[c][r][64 u .. 64 u + 63].
+template <int TQ>
+__global__ void __launch_bounds__(256) k_dequant(const uint8_t *buf, int n_experts, int rows, int cols,
+                                                 const uint32_t *slots, int n, void *q, int odt) {
+  const int P = cols / 64;
+  const size_t g = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (g >= size_t(n) * rows * P) return;
+  const int u = int(g % P);
+  const size_t rc = g / P;
+  const int r = int(rc % rows), c = int(rc / rows);
+  const uint32_t e = slots[c];
+  const size_t o = (size_t(c) * rows + r) * cols + 64 * size_t(u);
+  if (e >= uint32_t(n_experts)) {
+    for (int i = 0; i < 64; ++i) store_elt(q, o + i, 0.0f, odt);
+    return;
+  }
+  const uint8_t *row = buf + (size_t(e) * rows + r) * (size_t(36) * P);
+  if (TQ == LMOE_Q4_0) {
+    for (int b = 0; b < 2; ++b) {
+      const uint8_t *blk = row + 36 * u + 18 * b;
+      const float d = float(__builtin_bit_cast(_Float16, uint16_t(blk[0] | (blk[1] << 8))));
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t v = blk[2 + j];
+        store_elt(q, o + 32 * b + j, float(int(v & 15u) - 8) * d, odt);
+        store_elt(q, o + 32 * b + 16 + j, float(int(v >> 4) - 8) * d, odt);
+      }
+    }
+  } else {
+    const uint32_t *sb = reinterpret_cast<const uint32_t *>(row + 144 * (u >> 2));
+    const int c4 = u & 3;
+    const float d = half_lo(sb[0]), dmin = half_hi(sb[0]);
+    float sc0, m0, sc1, m1;
+    k4_scale_min(sb[1], sb[2], sb[3], 2 * c4, &sc0, &m0);
+    k4_scale_min(sb[1], sb[2], sb[3], 2 * c4 + 1, &sc1, &m1);
+    const float d1 = d * sc0, n1 = dmin * m0, d2 = d * sc1, n2 = dmin * m1;
+    const uint8_t *qs = row + 144 * (u >> 2) + 16 + 32 * c4;
+    for (int l = 0; l < 32; ++l) {
+      const uint32_t v = qs[l];
+      store_elt(q, o + l, __fsub_rn(__fmul_rn(d1, float(v & 15u)), n1), odt);
+      store_elt(q, o + 32 + l, __fsub_rn(__fmul_rn(d2, float(v >> 4)), n2), odt);
+    }
+  }
+}
+
+// ggml's quantize_row_q4_0_ref for one 32-weight block a thread, every step rounded on its own.
+__global__ void __launch_bounds__(256) k_quantize_q4_0(const void *w, int wdt, long long nblocks, uint8_t *out) {
+  const long long b = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (b >= nblocks) return;
+  float v[32];
+  float amax = 0.0f, mx = 0.0f;
+  for (int j = 0; j < 32; ++j) {
+    v[j] = load_elt(w, size_t(b) * 32 + j, wdt);
+    if (amax < fabsf(v[j])) {
+      amax = fabsf(v[j]);
+      mx = v[j];
+    }
+  }
+  const float d = __fdiv_rn(mx, -8.0f);
+  const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+  uint8_t *o = out + size_t(b) * 18;
+  const uint16_t dh = __builtin_bit_cast(uint16_t, _Float16(d));
+  o[0] = uint8_t(dh & 0xFF);
+  o[1] = uint8_t(dh >> 8);
+  for (int j = 0; j < 16; ++j) {
+    const int q0 = min(15, int(int8_t(__fadd_rn(__fmul_rn(v[j], id), 8.5f))));
+    const int q1 = min(15, int(int8_t(__fadd_rn(__fmul_rn(v[j + 16], id), 8.5f))));
+    o[2 + j] = uint8_t(q0 | (q1 << 4));
+  }
+}
+
+}  // namespace lmoe
+
+using namespace lmoe;
+
+extern "C" int lmoe_combine_sorted(const void *y, int ydtype, const uint32_t *inv, const float *scores, int T, int k,
+                                   int H, const float *shared, const float *gate, int gate_stride,
+                                   const void *residual, int rdtype, void *out, int odtype, void *stream) {
+  const char *fn = "lmoe_combine_sorted";
+  LMOE_REQUIRE(dtype_ok(ydtype) && dtype_ok(odtype) && (!residual || dtype_ok(rdtype)), LMOE_EINVAL,
+               "%s: bad dtype", fn);
+  LMOE_REQUIRE(T >= 0 && k > 0 && H > 0, LMOE_ESHAPE, "%s: bad shape", fn);
+  LMOE_REQUIRE(!shared == !gate, LMOE_EINVAL, "%s: shared and gate go together", fn);
+  if (T == 0) return 0;
+  LMOE_REQUIRE(y && inv && out, LMOE_EINVAL, "%s: null pointer", fn);
+  hipLaunchKernelGGL(k_combine_sorted, dim3((H + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y, ydtype, inv,
+                     scores, k, H, shared, gate, gate_stride, residual, rdtype, out, odtype);
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+extern "C" int lmoe_dequant(const uint8_t *buf, int type, int n_experts, int rows, int cols, const uint32_t *slots,
+                            int n, void *q, int odtype, void *stream) {
+  const char *fn = "lmoe_dequant";
+  LMOE_REQUIRE(qtype_ok(type), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn, type);
+  LMOE_REQUIRE(dtype_ok(odtype), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(rows > 0 && cols > 0 && cols % block_weights(type) == 0 && cols % 64 == 0 && n >= 0, LMOE_ESHAPE,
+               "%s: row length %d is not a multiple of %d", fn, cols, type == LMOE_Q4_K ? 256 : 64);
+  if (n == 0) return 0;
+  LMOE_REQUIRE(buf && slots && q, LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(type != LMOE_Q4_K || aligned4(buf), LMOE_EALIGN, "%s: Q4_K buffer must be 4-byte aligned", fn);
+  const size_t units = size_t(n) * rows * (cols / 64);
+  const dim3 grid(unsigned((units + 255) / 256));
+  if (type == LMOE_Q4_0)
+    hipLaunchKernelGGL(k_dequant<LMOE_Q4_0>, grid, dim3(256), 0, (hipStream_t)stream, buf, n_experts, rows, cols,
+                       slots, n, q, odtype);
+  else
+    hipLaunchKernelGGL(k_dequant<LMOE_Q4_K>, grid, dim3(256), 0, (hipStream_t)stream, buf, n_experts, rows, cols,
+                       slots, n, q, odtype);
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+extern "C" int lmoe_quantize_q4_0(const void *w, int wdtype, long long rows, int cols, uint8_t *out, void *stream) {
+  const char *fn = "lmoe_quantize_q4_0";
+  LMOE_REQUIRE(dtype_ok(wdtype), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(rows >= 0 && cols > 0 && cols % 32 == 0, LMOE_ESHAPE, "%s: row length %d is not a multiple of 32", fn,
+               cols);
+  const long long nb = rows * (cols / 32);
+  if (nb == 0) return 0;
+  LMOE_REQUIRE(w && out, LMOE_EINVAL, "%s: null pointer", fn);
+  hipLaunchKernelGGL(k_quantize_q4_0, dim3(unsigned((nb + 255) / 256)), dim3(256), 0, (hipStream_t)stream, w, wdtype,
+                     nb, out);
+  LMOE_LAUNCHED(fn);
+  return 0;
+}

@@ -1,0 +1,87 @@
+"""Synthetic workloads of the five benchmark configurations, built directly on the GPU.
+
+Weights are Gaussian N(0, 0.02^2) drawn with torch's seeded CUDA generator and quantized on the device
+(lmoe_quantize_q4_0), activations Gaussian N(0, 1). Shapes:
+
+  cfg1  H 2048, E 60, top-4, softmax without renormalisation, I 1408, shared expert Is 5632 with a sigmoid gate
+  cfg2  48 layers of H 2048, E 128, top-8 renormalised, I 768, no shared expert; batch-1 decode
+  cfg3  one cfg2 layer, 8192 tokens, logits N(0,1) + per-expert bias N(0,1) (skewed groups); bf16 activations
+  cfg4  one cfg2 layer, 64 sequences x 1 token, logits N(0,1) + a Zipf(1.1) log-prior (ragged groups 0..~40)
+  cfg5  H 4096, E 512, top-10, I 512, shared Is 512, Q4_K
+"""
+import torch
+
+from ._lib import F32, call, ptr, row_bytes, stream
+from .layer import MoELayer
+
+CONFIGS = {
+    1: dict(H=2048, E=60, k=4, I=1408, norm=False, Is=5632, types=("Q4_0",) * 3),
+    2: dict(H=2048, E=128, k=8, I=768, norm=True, Is=0, types=("Q4_0",) * 3, layers=48),
+    3: dict(H=2048, E=128, k=8, I=768, norm=True, Is=0, types=("Q4_0",) * 3, T=8192),
+    4: dict(H=2048, E=128, k=8, I=768, norm=True, Is=0, types=("Q4_0",) * 3, T=64),
+    5: dict(H=4096, E=512, k=10, I=512, norm=True, Is=512, types=("Q4_K",) * 3),
+}
+
+
+def q4_0_experts(n, rows, cols, gen, std=0.02, chunk_rows=1 << 18):
+    """n experts [n, rows, cols / 32 * 18] uint8 quantized from N(0, std^2) float32 weights drawn on the GPU."""
+    out = torch.empty((n, rows, row_bytes("Q4_0", cols)), dtype=torch.uint8, device="cuda")
+    flat = out.view(n * rows, -1)
+    total = n * rows
+    for r0 in range(0, total, chunk_rows):
+        r1 = min(total, r0 + chunk_rows)
+        w = torch.randn((r1 - r0, cols), generator=gen, device="cuda", dtype=torch.float32) * std
+        call("lmoe_quantize_q4_0", ptr(w), F32, r1 - r0, cols, ptr(flat[r0:r1]), stream())
+        del w
+    return out
+
+
+def router_weight(E, H, gen, std=0.02, dtype=torch.float16):
+    return (torch.randn((E, H), generator=gen, device="cuda", dtype=torch.float32) * std).to(dtype)
+
+
+def make_layer(cfg, gen, with_router=True):
+    """One MoE layer of configuration ``cfg`` (a CONFIGS entry) with Q4_0 weights made on the device."""
+    if cfg["types"][0] != "Q4_0":
+        raise ValueError("device-made weights are Q4_0 only; Q4_K layers come from the CPU quantizer")
+    H, E, I, Is = cfg["H"], cfg["E"], cfg["I"], cfg["Is"]
+    wg = q4_0_experts(E, I, H, gen)
+    wu = q4_0_experts(E, I, H, gen)
+    wd = q4_0_experts(E, H, I, gen)
+    wr = router_weight(E, H, gen) if with_router else None
+    shared = wsg = None
+    if Is:
+        shared = (q4_0_experts(1, Is, H, gen), q4_0_experts(1, Is, H, gen), q4_0_experts(1, H, Is, gen))
+        wsg = router_weight(1, H, gen).reshape(H)
+    return MoELayer(wg, wu, wd, cfg["types"], cfg["k"], cfg["norm"], wr=wr, shared=shared, wsg=wsg)
+
+
+def skewed_logits(T, E, gen, bias_std=1.0):
+    """cfg3 router logits: N(0, 1) per (token, expert) plus a per-expert bias N(0, bias_std^2)."""
+    bias = torch.randn((E,), generator=gen, device="cuda") * bias_std
+    return torch.randn((T, E), generator=gen, device="cuda") + bias
+
+
+def zipf_logits(T, E, gen, s=1.1, scale=1.0):
+    """cfg4 router logits: N(0, 1) plus scale * log of a Zipf(s) prior over a random permutation of the experts."""
+    rank = torch.randperm(E, generator=gen, device="cuda").to(torch.float32) + 1.0
+    prior = -s * torch.log(rank)
+    prior = prior - torch.logsumexp(prior, 0)
+    return torch.randn((T, E), generator=gen, device="cuda") + scale * prior
+
+
+def decode_bytes(cfg, n_unique):
+    """Algorithmic HBM bytes of one decode pass of one layer touching n_unique routed experts (weights only;
+    activations add T * H * (in + out) bytes)."""
+    H, I, Is, E = cfg["H"], cfg["I"], cfg["Is"], cfg["E"]
+    expert = 2 * I * row_bytes(cfg["types"][0], H) + H * row_bytes(cfg["types"][2], I)
+    shared = (2 * Is * row_bytes(cfg["types"][0], H) + H * row_bytes(cfg["types"][2], Is)) if Is else 0
+    router = E * H * 2 + (H * 2 if Is else 0)
+    return n_unique * expert + shared + router
+
+
+def expert_flops(cfg, rows):
+    """2 * rows * 3 * H * I: the routed experts' GEMM flops for ``rows`` (token, k) rows."""
+    return 2 * rows * 3 * cfg["H"] * cfg["I"]
+
+

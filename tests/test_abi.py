@@ -1,0 +1,67 @@
+"""The C ABI: the in-tree library loads, exports every entry point include/larder_moe.h declares, and refuses bad
+arguments with a negative code and a reason before it touches the GPU (so these run without one)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from larder_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "larder_moe.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(lmoe_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(built_lib):
+    names = declared()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(built_lib, n), f"{n} is declared in larder_moe.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature in larder_amd/_lib.py"
+
+
+def test_no_undeclared_signatures():
+    assert set(_lib.SIGNATURES) == set(declared())
+
+
+def test_abi_version(built_lib):
+    assert built_lib.lmoe_abi_version() == _lib.ABI_VERSION
+
+
+def test_refusals_without_a_gpu(built_lib):
+    L = built_lib
+    p = ctypes.c_void_p(16)   # never dereferenced: every call below is refused during argument checks
+    rc = L.lmoe_router_topk(p, 7, 1, 128, 8, 1, p, p, None)
+    assert rc == _lib.EINVAL and b"dtype" in L.lmoe_error()
+    rc = L.lmoe_router_topk(p, _lib.F32, 1, 2000, 8, 1, p, p, None)
+    assert rc == _lib.ESHAPE and b"experts" in L.lmoe_error()
+    rc = L.lmoe_router_topk(p, _lib.F32, 1, 128, 33, 1, p, p, None)
+    assert rc == _lib.ESHAPE and b"top-k" in L.lmoe_error()
+    rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, p, p, 8, 8, 128, 2048, 768, p, None)
+    assert rc == _lib.ETYPE and b"ggml type 8" in L.lmoe_error()
+    rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, p, p, _lib.Q4_0, _lib.Q4_0, 128, 2000, 768, p, None)
+    assert rc == _lib.ESHAPE
+    rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, p, p, _lib.Q4_K, _lib.Q4_K, 128, 2048 + 64, 768, p, None)
+    assert rc == _lib.ESHAPE and b"256" in L.lmoe_error()
+    rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, ctypes.c_void_p(18), p, _lib.Q4_0, _lib.Q4_0, 128, 2048, 768, p,
+                             None)
+    assert rc == _lib.EALIGN
+    rc = L.lmoe_gemv_down_combine(p, p, p, 1, 40, p, _lib.Q4_0, 128, 768, 2048, None, None, 0, None, 0, p,
+                                  _lib.F16, None)
+    assert rc == _lib.ESHAPE
+    rc = L.lmoe_group_rows(p, 10, 2000, 128, p, p, p, p, None, None, p, None)
+    assert rc == _lib.ESHAPE
+    rc = L.lmoe_dequant(p, 3, 4, 16, 64, p, 1, p, _lib.F32, None)
+    assert rc == _lib.ETYPE
+    rc = L.lmoe_quantize_q4_0(p, _lib.F32, 4, 33, p, None)
+    assert rc == _lib.ESHAPE
+    assert L.lmoe_max_tiles(65536, 128, 128) == 512 + 128
+
+
+def test_python_refuses_unsupported_types():
+    with pytest.raises(ValueError, match="Q5_K"):
+        _lib.qcode("Q5_K")

@@ -1,0 +1,206 @@
+"""GPU parity of the decode path against the CPU oracle, through the C ABI (larder_amd wrappers).
+
+Bars: expert ids and groupings bit-exact, ties to the lowest expert index; layer
+outputs within 2e-3 relative L2 of an fp32 dequant-then-matmul. Quantizer and dequant are integer/byte work and
+must be bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gguf, moe
+
+pytestmark = pytest.mark.gpu
+
+BAR = 2e-3
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def tie_logits(rng, T, E):
+    lg = rng.normal(0, 1.0, (T, E)).astype(np.float32) * rng.uniform(0.5, 4.0)
+    for r in range(T):
+        if r % 5 == 0:
+            j = rng.integers(0, E, 6)
+            lg[r, j] = lg[r, j[0]]
+        if r % 7 == 0:
+            lg[r] = np.round(lg[r] * 2) / 2
+        if r % 13 == 0:
+            lg[r] = 0.25
+    return lg
+
+
+@pytest.mark.parametrize("E,k,norm", [(60, 4, False), (128, 8, True), (512, 10, True), (1024, 32, False), (9, 9, True)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_router_topk_bit_exact(E, k, norm, dtype):
+    from larder_amd import route
+    rng = np.random.default_rng(E * 7 + k)
+    lg = tie_logits(rng, 67, E)
+    x = dev(lg).to(dtype)
+    ids, sc = route.topk(x, k, norm)
+    lg32 = host(x.float())
+    want_ids, want_sc = moe.router(lg32, k, norm)
+    assert (host(ids).astype(np.uint32) == want_ids).all()
+    assert np.allclose(host(sc), want_sc, rtol=2e-6, atol=1e-7)
+    inds, sc2 = route.probs(x, k, norm)
+    assert (host(inds)[:, ::-1].astype(np.uint32) == want_ids).all()
+
+
+def test_quantize_q4_0_bit_exact():
+    from larder_amd import _lib
+    rng = np.random.default_rng(11)
+    w = rng.standard_normal((300, 256)).astype(np.float32) * 0.02
+    w[0] = 0.0
+    w[1, :32] = np.float32(0.5)
+    w[1, 7] = -0.5                 # equal magnitudes: the first one sets the sign of d
+    w[2, :32] = (np.arange(32) - 16) / 4.0
+    w[3, 5] = 1e-30
+    for dt in (torch.float32, torch.float16, torch.bfloat16):
+        wt = dev(w).to(dt)
+        out = torch.empty((300, 256 // 32 * 18), dtype=torch.uint8, device="cuda")
+        _lib.call("lmoe_quantize_q4_0", _lib.ptr(wt), _lib.dcode(dt), 300, 256, _lib.ptr(out), _lib.stream())
+        want = gguf.quantize_q4_0(host(wt.float()))
+        assert (host(out) == want).all(), dt
+
+
+@pytest.mark.parametrize("t", ["Q4_0", "Q4_K"])
+@pytest.mark.parametrize("odt", [torch.float32, torch.float16])
+def test_dequant(t, odt):
+    from larder_amd import gguf_experts as ge
+    rng = np.random.default_rng(12)
+    buf = gguf.random_experts(rng, 5, 16, 512, t)
+    slots = np.array([3, 0, 9, 4], np.int32)          # 9: no such expert -> zeros
+    q = ge.dequant(dev(buf), dev(slots), t, odt)
+    want = np.zeros((4, 16, 512), np.float32)
+    for i, s in enumerate(slots):
+        if s < 5:
+            want[i] = gguf.dequant_matrix(buf[s], t)
+    got = host(q.float())
+    if odt == torch.float32:
+        assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    else:
+        assert (got == want.astype(np.float16).astype(np.float32)).all()
+
+
+MIXES = [(("Q4_0",) * 3, 2048, 768), (("Q4_0",) * 3, 2048, 1408), (("Q4_0",) * 3, 512, 256),
+         (("Q4_0",) * 3, 1344, 448), (("Q4_K",) * 3, 1024, 512), (("Q4_K",) * 3, 4096, 256),
+         (("Q4_0", "Q4_K", "Q4_0"), 1024, 512), (("Q4_K", "Q4_0", "Q4_K"), 512, 512)]
+
+
+@pytest.mark.parametrize("types,H,I", MIXES)
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.float32])
+def test_gemv_chain_vs_oracle(types, H, I, xdt):
+    from larder_amd import gguf_experts as ge
+    rng = np.random.default_rng(H + I)
+    E = 6
+    w = tuple(gguf.random_experts(rng, E, r, c, t) for (r, c), t in zip(((I, H), (I, H), (H, I)), types))
+    topk, rows = 2, 3
+    slots = rng.integers(0, E, rows * topk).astype(np.int32)
+    slots[-1] = E + 3                                    # no such expert: zero rows
+    x = dev(rng.standard_normal((rows, H)).astype(np.float32)).to(xdt)
+    h, y = ge._chain(x, tuple(dev(b) for b in w), dev(slots), topk, types, torch.float32)
+    # the kernels see x as f16; feed the oracle the same values
+    xs = host(x.float().half().float())
+    hw, yw = moe.gemv(xs, w, slots, topk, types)
+    assert (host(h)[-1] == 0).all() and (host(y)[-1] == 0).all()
+    assert moe.rel_l2(host(h), hw) < 1e-5
+    assert moe.rel_l2(host(y), yw) < BAR
+    y16 = ge.gemv(x, tuple(dev(b) for b in w), dev(slots), topk, "/".join(types), torch.float16)
+    assert moe.rel_l2(host(y16.float()), yw) < BAR
+
+
+@pytest.mark.parametrize("T,k,E,H,I", [(1, 8, 16, 2048, 768), (3, 4, 10, 1024, 1408), (5, 10, 12, 512, 512)])
+def test_down_combine_vs_oracle(T, k, E, H, I):
+    from larder_amd import _lib
+    rng = np.random.default_rng(T * 100 + k)
+    wd = gguf.random_experts(rng, E, H, I, "Q4_0")
+    h = rng.standard_normal((T * k, I)).astype(np.float32)
+    ids = rng.integers(0, E, (T, k)).astype(np.int32)
+    sc = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    shared = rng.standard_normal((T, H)).astype(np.float32)
+    gate = rng.standard_normal((T, 3)).astype(np.float32)
+    res = rng.standard_normal((T, H)).astype(np.float16)
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    hd, idd, scd, shd, gd, rd = dev(h), dev(ids), dev(sc), dev(shared), dev(gate), dev(res)
+    _lib.call("lmoe_gemv_down_combine", _lib.ptr(hd), _lib.ptr(idd), _lib.ptr(scd), T, k, _lib.ptr(dev(wd)),
+              _lib.Q4_0, E, I, H, _lib.ptr(shd), _lib.ptr(gd), 3, _lib.ptr(rd), _lib.F16, _lib.ptr(out), _lib.F32,
+              _lib.stream())
+    wdf = gguf.dequant_matrix(wd, "Q4_0")
+    h16 = h.astype(np.float16).astype(np.float32)            # h meets the weights as f16
+    y = np.einsum("tki,tkhi->tkh", h16.reshape(T, k, I), wdf[ids])
+    want = moe.combine(y, sc, shared, gate[:, 0], res.astype(np.float32))
+    assert moe.rel_l2(host(out), want) < 1e-5
+
+
+def _layer_from_device(cfg, seed):
+    from larder_amd import workloads
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return workloads.make_layer(cfg, g)
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_decode_layer_cfg1_vs_oracle(T):
+    """Config 1's layer (E 60, top-4, no renorm, I 1408, shared 5632 + sigmoid gate) at T tokens."""
+    from larder_amd import layer as lay, workloads
+    cfg = workloads.CONFIGS[1]
+    L = _layer_from_device(cfg, 0)
+    rng = np.random.default_rng(T)
+    x = dev(rng.standard_normal((T, cfg["H"])).astype(np.float16))
+    B = lay.DecodeBuffers(L, T)
+    out = torch.empty((T, cfg["H"]), dtype=torch.float32, device="cuda")
+    lay.decode(L, x, B, out)
+    torch.cuda.synchronize()
+    xs = host(x.float())
+    lg_gpu = host(B.logits)
+    lg_ref = xs @ host(L.wr.float()).T
+    assert moe.rel_l2(lg_gpu[:, :cfg["E"]], lg_ref) < 1e-5
+    assert moe.rel_l2(lg_gpu[:, cfg["E"]], xs @ host(L.wsg.float())) < 1e-5
+    ids, _, want = moe.layer(xs, lg_gpu[:, :cfg["E"]], tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"],
+                             cfg["k"], cfg["norm"], shared=tuple(host(b[0]) for b in L.shared),
+                             shared_gate_w=host(L.wsg.float()))
+    assert (host(B.ids).astype(np.uint32) == ids).all()
+    assert moe.rel_l2(host(out), want) < BAR
+
+
+def test_decode_layer_cfg2_residual():
+    from larder_amd import layer as lay, workloads
+    cfg = workloads.CONFIGS[2]
+    L = _layer_from_device(cfg, 1)
+    rng = np.random.default_rng(9)
+    x = dev(rng.standard_normal((1, cfg["H"])).astype(np.float16))
+    B = lay.DecodeBuffers(L, 1)
+    out = torch.empty((1, cfg["H"]), dtype=torch.float32, device="cuda")
+    lay.decode(L, x, B, out, residual=x)
+    torch.cuda.synchronize()
+    xs = host(x.float())
+    lg = host(B.logits)
+    ids, _, want = moe.layer(xs, lg, tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"], cfg["k"],
+                             cfg["norm"], residual=xs)
+    assert (host(B.ids).astype(np.uint32) == ids).all()
+    assert moe.rel_l2(host(out.float()) - xs, want - xs) < BAR
+
+
+def test_graph_replay_matches_eager():
+    """A captured 3-layer step replays to the eager result, bit for bit, with eager work between replays."""
+    from larder_amd import layer as lay, workloads
+    cfg = dict(workloads.CONFIGS[2], E=16)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    layers = [workloads.make_layer(cfg, g) for _ in range(3)]
+    st = lay.DecodeStack(layers, 1)
+    xs = torch.randn((4, 1, cfg["H"]), generator=g, device="cuda").half()
+    eager = []
+    for i in range(4):
+        st.x_in.copy_(xs[i])
+        eager.append(st.step().clone())
+    graph = st.capture()
+    for i in range(4):
+        st.x_in.copy_(xs[i])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(st.x_out, eager[i]), i
+        _ = torch.randn(1000, device="cuda").sum().item()     # eager work and a sync between replays
