@@ -204,3 +204,46 @@ def test_graph_replay_matches_eager():
         torch.cuda.synchronize()
         assert torch.equal(st.x_out, eager[i]), i
         _ = torch.randn(1000, device="cuda").sum().item()     # eager work and a sync between replays
+
+
+@pytest.mark.parametrize("R,E,bm", [(1, 4, 16), (8, 128, 16), (512, 128, 32), (65536, 128, 128), (5000, 60, 64),
+                                    (3000, 1024, 16)])
+def test_group_rows_bit_exact(R, E, bm):
+    from larder_amd import _lib
+    rng = np.random.default_rng(R + E)
+    ids = rng.integers(0, E, R).astype(np.int32)
+    if R > 10:
+        ids[rng.integers(0, R, R // 50)] = E + 5            # rows with no such expert go last
+        ids[: R // 3] = rng.integers(0, 3, R // 3)          # skew: a few experts take many rows
+    d = dev(ids)
+    counts = torch.empty(E, dtype=torch.int32, device="cuda")
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    order = torch.empty(R, dtype=torch.int32, device="cuda")
+    inv = torch.empty(R, dtype=torch.int32, device="cuda")
+    mt = _lib.lib().lmoe_max_tiles(R, E, bm)
+    tiles = torch.empty(mt, dtype=torch.int32, device="cuda")
+    nt = torch.empty(1, dtype=torch.int32, device="cuda")
+    ws = torch.empty(_lib.lib().lmoe_group_workspace_bytes(R, E) // 4 + 1, dtype=torch.int32, device="cuda")
+    _lib.call("lmoe_group_rows", _lib.ptr(d), R, E, bm, _lib.ptr(counts), _lib.ptr(offsets), _lib.ptr(order),
+              _lib.ptr(inv), _lib.ptr(tiles), _lib.ptr(nt), _lib.ptr(ws), _lib.stream())
+    c, o, od, iv = moe.group_rows(ids.astype(np.uint32), E)
+    assert (host(counts).astype(np.uint32) == c).all()
+    assert (host(offsets).astype(np.uint32) == o).all()
+    assert (host(order).astype(np.uint32) == od).all()
+    assert (host(inv).astype(np.uint32) == iv).all()
+    n = int(host(nt)[0])
+    want = [(e << 20) | m for e in range(E) for m in range(-(-int(c[e]) // bm))]
+    assert n == len(want) <= mt and host(tiles)[:n].tolist() == want
+
+
+def test_tail_combine_vs_oracle():
+    from larder_amd import route
+    rng = np.random.default_rng(21)
+    T, k, D = 5, 8, 2048
+    y = rng.standard_normal((1, T, k, D)).astype(np.float32)
+    sc = rng.uniform(0, 1, (1, T, k)).astype(np.float32)
+    sh = rng.standard_normal((1, T, D)).astype(np.float32)
+    gt = rng.standard_normal((1, T, 1)).astype(np.float32)
+    got = route.tail(dev(y), dev(sc), dev(sh), dev(gt))
+    want = moe.combine(y[0], sc[0], sh[0], gt[0, :, 0])
+    assert moe.rel_l2(host(got)[0], want) < 1e-6
