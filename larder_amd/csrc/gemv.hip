@@ -268,6 +268,7 @@ static int launch_gate_up(const void *x, int xdt, const uint32_t *slots, int n_s
   const size_t lds = size_t(4) * ((TG == TU ? 1 : 2) * P * XS + sum_sz + NW * 2 * RB * 9 * P + NW * 2 * RB * (P + 1));
   LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "lmoe_gemv_gate_up: hidden %d needs %zu bytes of LDS", H, lds);
   const dim3 grid((I + RB * NW - 1) / (RB * NW), n_slots);
+  if (int rc = allow_lds(k_gate_up<TG, TU, PT, NW>, lds, "lmoe_gemv_gate_up")) return rc;
   hipLaunchKernelGGL((k_gate_up<TG, TU, PT, NW>), grid, dim3(64 * NW), lds, st, x, xdt, slots, topk, wg, wu,
                      n_experts, I, h, P);
   LMOE_LAUNCHED("lmoe_gemv_gate_up");
@@ -344,6 +345,8 @@ extern "C" int lmoe_gemv_down_combine(const float *h, const uint32_t *ids, const
   LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "%s: k %d at width %d needs %zu bytes of LDS", fn, k, I, lds);
   const dim3 grid((H + RB * NW - 1) / (RB * NW), T);
   hipStream_t st = (hipStream_t)stream;
+  if (int rc = allow_lds(type_d == LMOE_Q4_0 ? k_down_combine<LMOE_Q4_0, NW> : k_down_combine<LMOE_Q4_K, NW>, lds, fn))
+    return rc;
   if (type_d == LMOE_Q4_0)
     hipLaunchKernelGGL((k_down_combine<LMOE_Q4_0, NW>), grid, dim3(64 * NW), lds, st, h, ids, scores, k, wd,
                        n_experts, I, H, shared, gate, gate_stride, residual, rdtype, out, odtype);

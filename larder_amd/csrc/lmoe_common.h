@@ -42,6 +42,15 @@ int hip_fail(hipError_t e, const char *what);
     if (_e != hipSuccess) return ::lmoe::hip_fail(_e, what); \
   } while (0)
 
+// Dynamic LDS above 64 KiB must be allowed per kernel before the launch.
+template <typename K>
+inline int allow_lds(K kernel, size_t bytes, const char *what) {
+  if (bytes <= 65536) return 0;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+  return e == hipSuccess ? 0 : hip_fail(e, what);
+}
+
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 inline bool dtype_ok(int t) { return t == LMOE_F32 || t == LMOE_F16 || t == LMOE_BF16; }
