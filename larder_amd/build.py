@@ -3,7 +3,8 @@
     python3 -m larder_amd.build          # compile every .hip under larder_amd/csrc and link the library
 
 Each source compiles to larder_amd/_build/<name>.o in parallel, then one link. Packed-FP32 instruction
-selection is switched off (-Xclang -target-feature -Xclang -packed-fp32-ops) for every device compile.
+selection is switched off (-Xclang -target-feature -Xclang -packed-fp32-ops) and floating-point contraction is off
+(-ffp-contract=off) for every compile.
 """
 import os
 import subprocess
@@ -18,8 +19,11 @@ LIB = PKG / "liblarder_moe.so"
 ARCH = os.environ.get("LMOE_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-CFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-          "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
+# -ffp-contract=off: every multiply and add rounds on its own unless written as an explicit fmaf / builtin (the
+# reference's CUDA prelude does the same with MUL/ADD _rn, gguf_cuda.py:4-20), so dequant and quantizer rounding
+# follow ggml's exactly.
+CFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off", "-Xclang", "-target-feature",
+          "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 
 
 def _run(cmd):

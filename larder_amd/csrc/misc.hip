@@ -62,13 +62,15 @@ __global__ void __launch_bounds__(256) k_dequant(const uint8_t *buf, int n_exper
     const uint8_t *qs = row + 144 * (u >> 2) + 16 + 32 * c4;
     for (int l = 0; l < 32; ++l) {
       const uint32_t v = qs[l];
-      store_elt(q, o + l, __fsub_rn(__fmul_rn(d1, float(v & 15u)), n1), odt);
-      store_elt(q, o + 32 + l, __fsub_rn(__fmul_rn(d2, float(v >> 4)), n2), odt);
+      store_elt(q, o + l, d1 * float(v & 15u) - n1, odt);
+      store_elt(q, o + 32 + l, d2 * float(v >> 4) - n2, odt);
     }
   }
 }
 
-// ggml's quantize_row_q4_0_ref for one 32-weight block a thread, every step rounded on its own.
+// ggml's quantize_row_q4_0_ref for one 32-weight block a thread, every step rounded on its own (the library is
+// built with -ffp-contract=off: a fused x * id + 8.5 can truncate differently, and a multiply folded into the f16
+// conversion as a mixed FMA with a +0 addend would turn d = -0 into +0).
 __global__ void __launch_bounds__(256) k_quantize_q4_0(const void *w, int wdt, long long nblocks, uint8_t *out) {
   const long long b = (long long)blockIdx.x * 256 + threadIdx.x;
   if (b >= nblocks) return;
@@ -81,15 +83,17 @@ __global__ void __launch_bounds__(256) k_quantize_q4_0(const void *w, int wdt, l
       mx = v[j];
     }
   }
-  const float d = __fdiv_rn(mx, -8.0f);
-  const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+  const float d = mx / -8.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
   uint8_t *o = out + size_t(b) * 18;
-  const uint16_t dh = __builtin_bit_cast(uint16_t, _Float16(d));
+  // the backend folds this conversion with the multiply above into a mixed FMA with a +0 addend, which drops the
+  // sign of d = -0 (max = 0); the sign bit is restored from d itself
+  const uint16_t dh = __builtin_bit_cast(uint16_t, _Float16(d)) | uint16_t((__float_as_uint(d) >> 16) & 0x8000u);
   o[0] = uint8_t(dh & 0xFF);
   o[1] = uint8_t(dh >> 8);
   for (int j = 0; j < 16; ++j) {
-    const int q0 = min(15, int(int8_t(__fadd_rn(__fmul_rn(v[j], id), 8.5f))));
-    const int q1 = min(15, int(int8_t(__fadd_rn(__fmul_rn(v[j + 16], id), 8.5f))));
+    const int q0 = min(15, int(int8_t(v[j] * id + 8.5f)));
+    const int q1 = min(15, int(int8_t(v[j + 16] * id + 8.5f)));
     o[2 + j] = uint8_t(q0 | (q1 << 4));
   }
 }

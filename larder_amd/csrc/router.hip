@@ -79,56 +79,64 @@ __global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt
             scores + size_t(t) * k);
 }
 
-// 8 consecutive elements starting at element i (i % 8 == 0) as floats.
-__device__ __forceinline__ void load8(const void *p, size_t i, int dt, float *o) {
-  if (dt == LMOE_F32) {
-    const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
-    const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i + 4);
-    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
-    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
-  } else {
-    const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
-    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (dt == LMOE_F16) {
-        o[2 * j] = half_lo(u[j]);
-        o[2 * j + 1] = half_hi(u[j]);
-      } else {
-        o[2 * j] = __uint_as_float(u[j] << 16);
-        o[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
-      }
-    }
-  }
-}
-
 constexpr int kRouterWaves = 4;
 constexpr int kRouterMaxT = 16;
+constexpr int kRouterMaxXs = 16384;  // T * H floats of x held in LDS
+constexpr int kRouterNc = 16;        // 16-byte weight chunks a lane (H * element size <= 16 KiB)
 
-// Each wavefront one router row (the last row the shared-expert gate when wsg is given) for all T tokens, then
-// the last workgroup to finish runs the top-k of every token; its counter returns to zero for the next launch.
+// Each wavefront one router row (the last row the shared-expert gate when wsg is given) for all T tokens: its
+// weight chunks load first, x is staged in LDS as f32 meanwhile; then the last workgroup to finish runs the top-k
+// of every token and returns the counter to zero for the next launch. WDT: the weights' element type.
+template <int WDT>
 __global__ void __launch_bounds__(64 * kRouterWaves)
-    k_router_gemv(const void *x, int xdt, const void *wr, const void *wsg, int wdt, int T, int H, int E, int k,
-                  int norm, float *logits, uint32_t *ids, float *scores, uint32_t *counter) {
+    k_router_gemv(const void *x, int xdt, const void *wr, const void *wsg, int T, int H, int E, int k, int norm,
+                  float *logits, uint32_t *ids, float *scores, uint32_t *counter) {
+  constexpr int EPC = WDT == LMOE_F32 ? 4 : 8;  // elements a 16-byte chunk
+  __shared__ float xs[kRouterMaxXs];
+  __shared__ int last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rows = E + (wsg != nullptr ? 1 : 0);
   const int row = blockIdx.x * kRouterWaves + wave;
+  const int nch = H / EPC;
+  u32x4 w[kRouterNc];
   if (row < rows) {
-    const void *w = row < E ? wr : wsg;
-    const size_t wbase = row < E ? size_t(row) * H : 0;
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(row < E ? static_cast<const char *>(wr) +
+                                                                     size_t(row) * H * (WDT == LMOE_F32 ? 4 : 2)
+                                                               : static_cast<const char *>(wsg));
+#pragma unroll
+    for (int i = 0; i < kRouterNc; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nch) w[i] = __builtin_nontemporal_load(src + c);
+    }
+  }
+  for (int i = threadIdx.x; i < T * H; i += 64 * kRouterWaves) xs[i] = load_elt(x, i, xdt);
+  __syncthreads();
+  if (row < rows) {
     float acc[kRouterMaxT];
 #pragma unroll
     for (int t = 0; t < kRouterMaxT; ++t) acc[t] = 0.0f;
-    for (int g = lane; g < H / 8; g += 64) {
-      float wv[8];
-      load8(w, wbase + 8 * size_t(g), wdt, wv);
 #pragma unroll
-      for (int t = 0; t < kRouterMaxT; ++t) {
-        if (t < T) {
-          float xv[8];
-          load8(x, size_t(t) * H + 8 * size_t(g), xdt, xv);
+    for (int i = 0; i < kRouterNc; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nch) {
+        float wv[EPC];
+        const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[t] = fmaf(xv[j], wv[j], acc[t]);
+        for (int j = 0; j < 4; ++j) {
+          if (WDT == LMOE_F32) {
+            wv[j] = __uint_as_float(u[j]);
+          } else if (WDT == LMOE_F16) {
+            wv[2 * j] = half_lo(u[j]);
+            wv[2 * j + 1] = half_hi(u[j]);
+          } else {
+            wv[2 * j] = __uint_as_float(u[j] << 16);
+            wv[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+          }
+        }
+        for (int t = 0; t < T; ++t) {
+          const float *xt = xs + t * H + c * EPC;
+#pragma unroll
+          for (int j = 0; j < EPC; ++j) acc[t] = fmaf(xt[j], wv[j], acc[t]);
         }
       }
     }
@@ -140,7 +148,6 @@ __global__ void __launch_bounds__(64 * kRouterWaves)
       }
     }
   }
-  __shared__ int last;
   __threadfence();
   __syncthreads();
   if (threadIdx.x == 0) last = atomicAdd(counter, 1u) == gridDim.x - 1;
@@ -187,12 +194,26 @@ extern "C" int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, 
   LMOE_REQUIRE(k > 0 && k <= E && k <= 32, LMOE_ESHAPE, "lmoe_router_gemv_topk: top-k %d is outside 1..min(E, 32)",
                k);
   LMOE_REQUIRE(x && wr && logits && ids && scores && ws, LMOE_EINVAL, "lmoe_router_gemv_topk: null pointer");
-  LMOE_REQUIRE(aligned16(x) && aligned16(wr) && (!wsg || aligned16(wsg)), LMOE_EALIGN,
-               "lmoe_router_gemv_topk: x, wr and wsg must be 16-byte aligned");
+  LMOE_REQUIRE(aligned16(wr) && (!wsg || aligned16(wsg)), LMOE_EALIGN,
+               "lmoe_router_gemv_topk: wr and wsg must be 16-byte aligned");
+  LMOE_REQUIRE(size_t(T) * H <= size_t(kRouterMaxXs), LMOE_ESHAPE,
+               "lmoe_router_gemv_topk: %d tokens x hidden %d is above the %d activations this kernel stages", T, H,
+               kRouterMaxXs);
+  LMOE_REQUIRE(size_t(H) * (wdtype == LMOE_F32 ? 4 : 2) <= size_t(kRouterNc) * 64 * 16, LMOE_ESHAPE,
+               "lmoe_router_gemv_topk: a router row of %d weights is above what a wavefront holds", H);
   const int rows = E + (wsg ? 1 : 0);
-  hipLaunchKernelGGL(k_router_gemv, dim3((rows + kRouterWaves - 1) / kRouterWaves), dim3(64 * kRouterWaves), 0,
-                     (hipStream_t)stream, x, xdtype, wr, wsg, wdtype, T, H, E, k, norm, logits, ids, scores,
-                     static_cast<uint32_t *>(ws));
+  const dim3 grid((rows + kRouterWaves - 1) / kRouterWaves), block(64 * kRouterWaves);
+  hipStream_t st = (hipStream_t)stream;
+  uint32_t *ctr = static_cast<uint32_t *>(ws);
+  if (wdtype == LMOE_F16)
+    hipLaunchKernelGGL(k_router_gemv<LMOE_F16>, grid, block, 0, st, x, xdtype, wr, wsg, T, H, E, k, norm, logits, ids,
+                       scores, ctr);
+  else if (wdtype == LMOE_BF16)
+    hipLaunchKernelGGL(k_router_gemv<LMOE_BF16>, grid, block, 0, st, x, xdtype, wr, wsg, T, H, E, k, norm, logits,
+                       ids, scores, ctr);
+  else
+    hipLaunchKernelGGL(k_router_gemv<LMOE_F32>, grid, block, 0, st, x, xdtype, wr, wsg, T, H, E, k, norm, logits, ids,
+                       scores, ctr);
   LMOE_LAUNCHED("lmoe_router_gemv_topk");
   return 0;
 }
