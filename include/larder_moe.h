@@ -7,8 +7,8 @@
  *     argument was refused; lmoe_error() then returns a one-sentence reason (thread-local).
  * Expert buffers are the reference's arena layout: uint8 [n_experts][rows][row bytes] with row bytes
  * cols / 32 * 18 (Q4_0) or cols / 256 * 144 (Q4_K), 16-byte aligned (stream_fast.py:3936-3941).
- * Workspaces are caller-owned device memory, sized by the matching *_workspace_bytes query, zero-filled once
- * before first use; every kernel that uses one leaves it zero-filled again when it ends.
+ * Workspaces are caller-owned device memory sized by the matching *_workspace_bytes query; their contents on entry
+ * do not matter.
  */
 #ifndef LARDER_MOE_H
 #define LARDER_MOE_H
@@ -39,15 +39,23 @@ int lmoe_abi_version(void);
 int lmoe_router_topk(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids, float *scores,
                      void *stream);
 
-/* Decode router: logits[t][e] = x[t] . wr[e] (fp32 accumulation), optionally the shared-expert gate logit
- * x[t] . wsg as logits[t][E] (row stride E + 1 then), then top-k as lmoe_router_topk. Replaces the block's
- * gate linear plus route_cuda.probs on decode rows (route_cuda.py:433-444; stream_fast.py:4358, 4375).
- * x [T][H] in xdtype, wr [E][H] and wsg [H] in wdtype (F16, BF16 or F32), T <= 16, H % 64 == 0.
- * Workspace: lmoe_router_workspace_bytes(). */
-size_t lmoe_router_workspace_bytes(void);
+/* Prepared activation rows: an activation row of 64 P values as P units of 36 dwords (32 dwords of f16 pairs in
+ * the nibble order of block type qtype, the sums of the unit's two 32-value halves as fp32, two zero dwords), the
+ * form the expert kernels read. x [rows][H] in xdtype -> xprep [rows][H / 64 * 36] uint32. */
+int lmoe_prep_x(const void *x, int xdtype, int rows, int H, int qtype, uint32_t *xprep, void *stream);
+
+/* Router GEMV: logits[t][e] = x[t] . wr[e] (fp32 accumulation), and when wsg is given the shared-expert gate logit
+ * x[t] . wsg as logits[t][E] (row stride E + 1 then); when xprep is given, also x's prepared rows for block type
+ * qtype. Replaces the block's gate linear (stream_fast.py:4358) and shared_expert_gate (:4375).
+ * x [T][H] in xdtype, wr [E][H] and wsg [H] in wdtype (F16, BF16 or F32), T <= 16, H % 64 == 0. */
+int lmoe_router_gemv(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T, int H, int E,
+                     float *logits, uint32_t *xprep, int qtype, void *stream);
+
+/* lmoe_router_gemv then lmoe_router_topk on its logits: the decode rows of route_cuda.probs after the gate linear
+ * (route_cuda.py:433-444). */
 int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T, int H,
-                          int E, int k, int norm, float *logits, uint32_t *ids, float *scores, void *ws,
-                          void *stream);
+                          int E, int k, int norm, float *logits, uint32_t *ids, float *scores, uint32_t *xprep,
+                          int qtype, void *stream);
 
 /* Decode chain, gate/up: h[s][i] = silu(x[s / topk] . wg[slots[s]][i]) * (x[s / topk] . wu[slots[s]][i]),
  * fp32. Replaces gguf_experts kernel gguf_gate_up (gguf_experts.py:452-495) as driven by _chain
@@ -56,6 +64,23 @@ int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, const void 
 int lmoe_gemv_gate_up(const void *x, int xdtype, const uint32_t *slots, int n_slots, int topk, const uint8_t *wg,
                       const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I, float *h,
                       void *stream);
+
+/* lmoe_gemv_gate_up on prepared rows: xg_prep (and xu_prep when type_u differs from type_g) [n_slots / topk][...];
+ * writes h (fp32, may be NULL) and / or hprep, h's prepared rows for the down matrix's type_d without their sums
+ * ([n_slots][I / 64 * 36], may be NULL). */
+int lmoe_gemv_gate_up_prepped(const uint32_t *xg_prep, const uint32_t *xu_prep, const uint32_t *slots, int n_slots,
+                              int topk, const uint8_t *wg, const uint8_t *wu, int type_g, int type_u, int n_experts,
+                              int H, int I, float *h, uint32_t *hprep, int type_d, void *stream);
+
+/* The decode layer's gate/up with the router's top-k fused in: each workgroup ranks its token's logits
+ * [T][ld_stride] (as lmoe_router_topk: ties to the lowest expert index, softmax scores, renormalised when norm),
+ * takes its slot's expert, writes ids [T][k] and scores [T][k], and runs lmoe_gemv_gate_up_prepped's work on
+ * prepared rows xg_prep / xu_prep [T][...] into hprep [T * k][I / 64 * 36]. Replaces route_cuda.probs plus
+ * gguf_gate_up on decode rows (route_cuda.py:433-444; gguf_experts.py:452-495). E <= 1024, k <= 32. */
+int lmoe_moe_gate_up(const float *logits, int ld_stride, int T, int k, int norm, const uint32_t *xg_prep,
+                     const uint32_t *xu_prep, const uint8_t *wg, const uint8_t *wu, int type_g, int type_u,
+                     int n_experts, int H, int I, uint32_t *ids, float *scores, uint32_t *hprep, int type_d,
+                     void *stream);
 
 /* Decode chain, down with the weighted combine fused:
  *   out[t][n] = sum_j scores[t][j] * (h[t * k + j] . wd[ids[t][j]][n])
@@ -68,6 +93,13 @@ int lmoe_gemv_down_combine(const float *h, const uint32_t *ids, const float *sco
                            const uint8_t *wd, int type_d, int n_experts, int I, int H, const float *shared,
                            const float *gate, int gate_stride, const void *residual, int rdtype, void *out,
                            int odtype, void *stream);
+
+/* lmoe_gemv_down_combine on h's prepared rows [T * k][I / 64 * 36] (has_sums 0: their half sums are derived from
+ * the pairs, as lmoe_gemv_gate_up_prepped leaves them). */
+int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sums, const uint32_t *ids, const float *scores,
+                                   int T, int k, const uint8_t *wd, int type_d, int n_experts, int I, int H,
+                                   const float *shared, const float *gate, int gate_stride, const void *residual,
+                                   int rdtype, void *out, int odtype, void *stream);
 
 /* Device-side ragged grouping: the stable counting sort of the flattened (token, k) expert ids, the device
  * form of stream_fast.py:5466-5471 (argsort of the flat ids and its inverse) and gguf_experts.py:702-713.

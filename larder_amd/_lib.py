@@ -28,10 +28,15 @@ SIGNATURES = {
     "lmoe_error": (ctypes.c_char_p, []),
     "lmoe_abi_version": (_I, []),
     "lmoe_router_topk": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
-    "lmoe_router_workspace_bytes": (_SZ, []),
-    "lmoe_router_gemv_topk": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "lmoe_prep_x": (_I, [_P, _I, _I, _I, _I, _P, _P]),
+    "lmoe_router_gemv": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
+    "lmoe_router_gemv_topk": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P]),
     "lmoe_gemv_gate_up": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
+    "lmoe_gemv_gate_up_prepped": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P]),
+    "lmoe_moe_gate_up": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P]),
     "lmoe_gemv_down_combine": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
+    "lmoe_gemv_down_combine_prepped": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I,
+                                            _P]),
     "lmoe_group_workspace_bytes": (_SZ, [_I, _I]),
     "lmoe_group_rows": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "lmoe_max_tiles": (_I, [_I, _I, _I]),

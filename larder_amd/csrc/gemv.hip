@@ -7,9 +7,11 @@
 //     registers, so the HBM round trip overlaps the staging of the activations; they land in the wavefront's own
 //     LDS region and are read back as 36-byte "units" (64 weights: two Q4_0 blocks or a quarter Q4_K
 //     super-block), each lane a unit, 9 dword reads at a 9-dword lane stride (bank-conflict free);
-//   * activations are fetched with 16-byte loads into LDS, then rearranged there into f16 pairs in nibble order;
-//     each unit's nibbles meet them in v_dot2_f32_f16 (lmoe_common.h), fp32 accumulation;
-//   * per-unit partial sums go to LDS and are added in a fixed order (deterministic results);
+//   * activations arrive prepared (f16 pairs in nibble order plus half-unit sums, lmoe_common.h) and are copied
+//     into LDS as they are; gate/up writes h prepared for down the same way. Raw activations are also accepted
+//     and rearranged in LDS by the workgroup;
+//   * each unit's nibbles meet the activations in v_dot2_f32_f16, fp32 accumulation; per-unit partial sums go to
+//     LDS and are added in a fixed order, the last steps on DPP (deterministic results);
 //   * down adds the k experts of a token, weighted by the router scores, plus the shared expert and a residual,
 //     in the same kernel, so no [T * k, H] intermediate is written.
 #include <algorithm>
@@ -18,16 +20,14 @@
 
 namespace lmoe {
 
-constexpr int XS = 36;  // dwords an x unit takes in LDS: 32 pairs + 4 pad (keeps lanes on distinct banks)
-constexpr int RB = 4;   // rows a wavefront task covers, of each matrix
 
 __device__ __forceinline__ int elt_size(int dt) { return dt == LMOE_F32 ? 4 : 2; }
 
-// nbytes (a multiple of 16) from global src to LDS dst, 16 bytes a thread a step.
-__device__ __forceinline__ void copy_to_lds(const void *src, void *dst, int nbytes, int tid, int nthr) {
+// ndw dwords (a multiple of 4, 16-byte aligned) from global src to LDS dst, 16 bytes a thread a step.
+__device__ __forceinline__ void copy_to_lds(const void *src, void *dst, int ndw, int tid, int nthr) {
   const u32x4 *s = static_cast<const u32x4 *>(src);
   u32x4 *d = static_cast<u32x4 *>(dst);
-  for (int i = tid; i < nbytes / 16; i += nthr) d[i] = s[i];
+  for (int i = tid; i < ndw / 4; i += nthr) d[i] = s[i];
 }
 
 __device__ __forceinline__ float lds_elt(const void *raw, int i, int dt) {
@@ -36,30 +36,29 @@ __device__ __forceinline__ float lds_elt(const void *raw, int i, int dt) {
   return dt == LMOE_F16 ? float(__builtin_bit_cast(_Float16, b)) : bf16_to_f32(b);
 }
 
-// An activation row staged raw in LDS (64 P elements of dtype dt) -> f16 pairs in block type TQ's nibble order,
-// and the sums of each 32-weight half-unit over the f16-rounded values (8 lanes a half-unit, fixed order).
+// A raw activation row in LDS (64 P values of dtype dt) -> prepared units (pairs and sums) in LDS.
 template <int TQ>
-__device__ __forceinline__ void permute_x(const void *raw, int dt, int P, uint32_t *xs, float *sums, int tid,
-                                          int nthr) {
-  constexpr int H = TQ == LMOE_Q4_K ? 32 : 16;
-  for (int idx = tid; idx < 32 * P; idx += nthr) {
-    const int p = idx >> 5, dw = idx & 31;
-    const h2_t v = {_Float16(lds_elt(raw, 64 * p + xelem(dw, 0, H), dt)),
-                    _Float16(lds_elt(raw, 64 * p + xelem(dw, 1, H), dt))};
-    xs[p * XS + dw] = __builtin_bit_cast(uint32_t, v);
+__device__ __forceinline__ void prep_in_lds(const void *raw, int dt, int P, uint32_t *xs, int tid, int nthr) {
+  for (int idx = tid; idx < XS * P; idx += nthr) {
+    const int p = idx / XS, dw = idx - p * XS;
+    xs[idx] = prep_dword<TQ>([&](int i) { return lds_elt(raw, i, dt); }, p, dw);
   }
-  if (!sums) return;
-  for (int base = 0; base < 16 * P; base += nthr) {
-    const int idx = base + tid, hu = idx >> 3, part = idx & 7;
+}
+
+// The half-unit sums of prepared units written without them, from their pairs: a unit's first 32 weights sit in
+// dwords 0..15 (Q4_0) or in the even dwords (Q4_K).
+template <int TQ>
+__device__ __forceinline__ void sums_in_lds(uint32_t *xs, int units, int tid, int nthr) {
+  for (int hu = tid; hu < 2 * units; hu += nthr) {
+    const int p = hu >> 1, half = hu & 1;
+    const uint32_t *u = xs + p * XS;
     float s = 0.0f;
-    if (idx < 16 * P) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s += float(_Float16(lds_elt(raw, 32 * hu + 4 * part + i, dt)));
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t w = TQ == LMOE_Q4_K ? u[2 * i + half] : u[16 * half + i];
+      s += half_lo(w) + half_hi(w);
     }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
-    if (idx < 16 * P && part == 0) sums[hu] = s;
+    xs[p * XS + 32 + half] = __builtin_bit_cast(uint32_t, s);
   }
 }
 
@@ -75,9 +74,12 @@ __device__ __forceinline__ void load_x32(const uint32_t *xs, uint32_t *xv) {
   }
 }
 
-// The dot of unit p of a staged row (9 P dwords) with x pairs xv.
+// The dot of unit p of a staged row (9 P dwords) with a prepared unit xu (pairs at 0..31, sums at 32, 33).
 template <int TQ>
-__device__ __forceinline__ float row_unit_dot(const uint32_t *row, int p, const uint32_t *xv, float sx0, float sx1) {
+__device__ __forceinline__ float row_unit_dot(const uint32_t *row, int p, const uint32_t *xu) {
+  uint32_t xv[32];
+  load_x32(xu, xv);
+  const float sx0 = __builtin_bit_cast(float, xu[32]), sx1 = __builtin_bit_cast(float, xu[33]);
   if (TQ == LMOE_Q4_0) {
     uint32_t u[9];
 #pragma unroll
@@ -99,35 +101,56 @@ __device__ __forceinline__ float row_unit_dot(const uint32_t *row, int p, const 
 //
 // Grid (I / (4 NW), n_slots), NW wavefronts a workgroup; wavefront w of block (bx, s) takes rows
 // [(bx NW + w) 4, +4) of gate and up of expert slots[s]; NC >= ceil(9 P / 64) 16-byte chunks a lane a matrix.
-// LDS: x pairs for TG (and TU when it differs), the half-unit sums, then a region that first holds the raw x row
-// and then each wavefront's 8 staged rows, then each wavefront's 8 x (P + 1) partial sums.
-template <int TG, int TU, int NC, int NW>
-__global__ void __launch_bounds__(64 * NW)
-    k_gate_up(const void *x, int xdt, const uint32_t *slots, int topk, const uint8_t *wg, const uint8_t *wu,
-              int n_experts, int I, float *h, int P) {
+// Activations: prepared rows xg (and xu, for an up type other than gate's), or raw rows x of dtype xdt when xg is
+// null. Outputs: h (fp32, [n_slots][I]) and / or hprep (prepared rows of width I for block type td, pairs only:
+// the consumer derives the sums).
+// LDS: the prepared unit rows (gate's, then up's when the types differ), then a region that first holds the raw x
+// row (raw input only) and then each wavefront's 8 staged weight rows, then each wavefront's 8 x (P + 1) partials.
+template <int TG, int TU, int RB, int NC, int NW>
+__global__ void __launch_bounds__(64 * NW, 3)
+    k_gate_up(const uint32_t *xg_prep, const uint32_t *xu_prep, const void *x, int xdt, const uint32_t *slots,
+              int topk, const uint8_t *wg, const uint8_t *wu, int n_experts, int I, float *h, uint32_t *hprep,
+              int td, int P, const float *logits, int ld_stride, int norm, uint32_t *ids_out, float *scores_out) {
   constexpr bool SAME = TG == TU;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int s = blockIdx.y;
-  const uint32_t e = slots[s];
   const int r0 = (blockIdx.x * NW + wave) * RB;
-  if (e >= uint32_t(n_experts)) {  // no such expert: zero rows (cpu_kern.cpp:316-318)
-    if (lane < RB && r0 + lane < I) h[size_t(s) * I + r0 + lane] = 0.0f;
-    return;
+  uint32_t e;
+  if (logits) {  // the router's top-k of this slot's token, by wavefront 0, the slot's pick through LDS
+    __shared__ uint32_t pick_id[32];
+    __shared__ float pick_sc[32];
+    if (wave == 0) {
+      const int t = s / topk;
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int i = lane + 64 * j;
+        v[j] = i < n_experts ? logits[size_t(t) * ld_stride + i] : -INFINITY;
+      }
+      topk_wave<16>(v, n_experts, topk, norm, pick_id, pick_sc);
+    }
+    __syncthreads();
+    e = pick_id[s % topk];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      ids_out[s] = e;
+      scores_out[s] = pick_sc[s % topk];
+    }
+  } else {
+    e = slots[s];
   }
   extern __shared__ u32x4 lds4[];
   uint32_t *xg = reinterpret_cast<uint32_t *>(lds4);
   uint32_t *xu = SAME ? xg : xg + P * XS;
-  float *sums = reinterpret_cast<float *>(xu + P * XS);
-  const int sum_sz = (2 * P + 3) & ~3;
-  uint32_t *region = reinterpret_cast<uint32_t *>(sums + sum_sz);
+  uint32_t *region = xu + P * XS;
   const int stage_dw = 2 * RB * 9 * P;
-  const int xraw_dw = 16 * P * elt_size(xdt);  // 64 P elements
+  const int xraw_dw = xg_prep ? 0 : 16 * P * elt_size(xdt);  // 64 P elements
   uint32_t *stage = region + wave * stage_dw;
   float *red = reinterpret_cast<float *>(region + max(NW * stage_dw, xraw_dw)) + wave * (2 * RB * (P + 1));
+  const bool valid = e < uint32_t(n_experts);  // no such expert: zero rows (cpu_kern.cpp:316-318)
+  const bool rows_ok = valid && r0 < I;
 
-  // 1) this wavefront's 8 rows, 9 P 16-byte chunks a matrix, into registers
-  const int C = 9 * P;
-  const bool rows_ok = r0 < I;
+  // 1) this wavefront's 2 RB rows, RB 9 P / 4 16-byte chunks a matrix, into registers
+  const int C = RB * 9 * P / 4;
   const size_t rowb = size_t(36) * P;
   const u32x4 *gsrc = reinterpret_cast<const u32x4 *>(wg + (size_t(e) * I + r0) * rowb);
   const u32x4 *usrc = reinterpret_cast<const u32x4 *>(wu + (size_t(e) * I + r0) * rowb);
@@ -140,14 +163,33 @@ __global__ void __launch_bounds__(64 * NW)
       vu[i] = __builtin_nontemporal_load(usrc + c);
     }
   }
-  // 2) the x row, raw, then rearranged
-  const int xbytes = 64 * P * elt_size(xdt);
-  copy_to_lds(static_cast<const char *>(x) + size_t(s / topk) * xbytes, region, xbytes, threadIdx.x, 64 * NW);
-  __syncthreads();
-  permute_x<TG>(region, xdt, P, xg, sums, threadIdx.x, 64 * NW);
-  if (!SAME) permute_x<TU>(region, xdt, P, xu, nullptr, threadIdx.x, 64 * NW);
-  __syncthreads();
-  if (!rows_ok) return;
+  // 2) the activation row
+  const size_t xrow = size_t(s / topk);
+  if (xg_prep) {
+    copy_to_lds(xg_prep + xrow * P * XS, xg, P * XS, threadIdx.x, 64 * NW);
+    if (!SAME) copy_to_lds(xu_prep + xrow * P * XS, xu, P * XS, threadIdx.x, 64 * NW);
+    __syncthreads();
+  } else {
+    copy_to_lds(static_cast<const char *>(x) + xrow * 64 * P * elt_size(xdt), region, 16 * P * elt_size(xdt),
+                threadIdx.x, 64 * NW);
+    __syncthreads();
+    prep_in_lds<TG>(region, xdt, P, xg, threadIdx.x, 64 * NW);
+    if (!SAME) prep_in_lds<TU>(region, xdt, P, xu, threadIdx.x, 64 * NW);
+    __syncthreads();
+  }
+  if (r0 >= I) return;
+  if (!valid) {
+    if (lane < RB) {
+      if (h) h[size_t(s) * I + r0 + lane] = 0.0f;
+      if (hprep) {
+        int dw, half;
+        const int n = r0 + lane;
+        xslot(n & 63, td == LMOE_Q4_K ? 32 : 16, &dw, &half);
+        reinterpret_cast<_Float16 *>(hprep + (size_t(s) * (I / 64) + (n >> 6)) * XS + dw)[half] = _Float16(0.0f);
+      }
+    }
+    return;
+  }
   u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
@@ -160,73 +202,66 @@ __global__ void __launch_bounds__(64 * NW)
   __builtin_amdgcn_wave_barrier();
 
   const int U = 2 * RB * P;
-  if (SAME && (64 % P) == 0) {  // each lane keeps one unit column: its x pairs load once
-    const int p = lane % P;
-    uint32_t xv[32];
-    load_x32(xg + p * XS, xv);
-    const float sx0 = sums[2 * p], sx1 = sums[2 * p + 1];
-    for (int u = lane; u < U; u += 64) {
-      const int row = u / P;
-      red[row * (P + 1) + p] = row_unit_dot<TG>(stage + row * 9 * P, p, xv, sx0, sx1);
-    }
-  } else {
-    for (int u = lane; u < U; u += 64) {
-      const int row = u / P, p = u - row * P;
-      uint32_t xv[32];
-      const float sx0 = sums[2 * p], sx1 = sums[2 * p + 1];
-      float part;
-      if (row < RB) {
-        load_x32(xg + p * XS, xv);
-        part = row_unit_dot<TG>(stage + row * 9 * P, p, xv, sx0, sx1);
-      } else {
-        load_x32(xu + p * XS, xv);
-        part = row_unit_dot<TU>(stage + row * 9 * P, p, xv, sx0, sx1);
-      }
-      red[row * (P + 1) + p] = part;
-    }
+#pragma unroll 2
+  for (int u = lane; u < U; u += 64) {
+    const int row = u / P, p = u - row * P;
+    float part;
+    if (row < RB)
+      part = row_unit_dot<TG>(stage + row * 9 * P, p, xg + p * XS);
+    else
+      part = row_unit_dot<TU>(stage + row * 9 * P, p, xu + p * XS);
+    red[row * (P + 1) + p] = part;
   }
   __builtin_amdgcn_wave_barrier();
 
-  // 8 rows x P partials: 8 lanes a row, fixed order
+  // 2 RB rows x P partials: LPR lanes a row, fixed order
   constexpr int LPR = 64 / (2 * RB);
   const int rr = lane / LPR, sub = lane % LPR;
   float acc = 0.0f;
   for (int p = sub; p < P; p += LPR) acc += red[rr * (P + 1) + p];
-#pragma unroll
-  for (int m = LPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m, 64);
-  const float up = __shfl_xor(acc, RB * LPR, 64);  // up row rr sits RB * LPR = 32 lanes above gate row rr
-  if (rr < RB && sub == 0 && r0 + rr < I) h[size_t(s) * I + r0 + rr] = silu_mul(acc, up);
+  acc = LPR == 8 ? sum8(acc) : sum16(acc);
+  const float up = lane_xor32(acc);  // up row rr sits RB * LPR = 32 lanes above gate row rr
+  if (rr < RB && sub == 0) {
+    const int n = r0 + rr;
+    const float v = silu_mul(acc, up);
+    if (h) h[size_t(s) * I + n] = v;
+    if (hprep) {
+      int dw, half;
+      xslot(n & 63, td == LMOE_Q4_K ? 32 : 16, &dw, &half);
+      reinterpret_cast<_Float16 *>(hprep + (size_t(s) * (I / 64) + (n >> 6)) * XS + dw)[half] = _Float16(v);
+    }
+  }
 }
 
 // ---- down + combine -------------------------------------------------------------------------------------------
 //
-// Grid (H / (4 NW), T). Block (bx, t) stages h rows t k .. t k + k - 1 as x pairs, then wavefront w takes output
-// rows [(bx NW + w) 4, +4) of all k experts of token t, adds them weighted by scores[t] (1 when scores is null),
-// then the gated shared-expert row and the residual, and writes out[t]. When k 9 P <= 64 NC the weight chunks are
-// fetched into registers before the h staging; otherwise after it.
-template <int TD, int NC, int NW>
-__global__ void __launch_bounds__(64 * NW)
-    k_down_combine(const float *h, const uint32_t *ids, const float *scores, int k, const uint8_t *wd,
-                   int n_experts, int I, int H, const float *shared, const float *gate, int gate_stride,
-                   const void *residual, int rdt, void *out, int odt) {
+// Grid (H / (4 NW), T). Block (bx, t) stages the k h rows of token t as prepared units (copied from hprep, sums
+// derived when has_sums is 0; or rearranged from fp32 h), then wavefront w takes output rows [(bx NW + w) 4, +4)
+// of all k experts of token t, adds them weighted by scores[t] (1 when scores is null), then the gated
+// shared-expert row and the residual, and writes out[t]. When k 9 P <= 64 NC the weight chunks are fetched into
+// registers before the h staging; otherwise after it.
+template <int TD, int RB, int NC, int NW>
+__global__ void __launch_bounds__(64 * NW, 3)
+    k_down_combine(const uint32_t *hprep, int has_sums, const float *h, const uint32_t *ids, const float *scores,
+                   int k, const uint8_t *wd, int n_experts, int I, int H, const float *shared, const float *gate,
+                   int gate_stride, const void *residual, int rdt, void *out, int odt) {
   const int P = I / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.y;
   const int n0 = (blockIdx.x * NW + wave) * RB;
   extern __shared__ u32x4 lds4[];
-  const int sum_sz = (2 * P + 3) & ~3;
-  uint32_t *hx = reinterpret_cast<uint32_t *>(lds4);                // k * P * XS
-  float *hs = reinterpret_cast<float *>(hx + k * P * XS);            // k * sum_sz
-  uint32_t *eid = reinterpret_cast<uint32_t *>(hs + k * sum_sz);    // 32
-  float *esc = reinterpret_cast<float *>(eid + 32);                 // 32
+  uint32_t *hx = reinterpret_cast<uint32_t *>(lds4);          // k * P * XS
+  uint32_t *eid = hx + k * P * XS;                             // 32
+  float *esc = reinterpret_cast<float *>(eid + 32);           // 32
   uint32_t *region = reinterpret_cast<uint32_t *>(esc + 32);
   const int stage_dw = k * RB * 9 * P;
+  const int hraw_dw = hprep ? 0 : k * I;
   uint32_t *stage = region + wave * stage_dw;
   const int red_ld = k * P + 1;
-  float *red = reinterpret_cast<float *>(region + max(NW * stage_dw, k * I)) + wave * (RB * red_ld);
+  float *red = reinterpret_cast<float *>(region + max(NW * stage_dw, hraw_dw)) + wave * (RB * red_ld);
 
   const size_t rowb = size_t(36) * P;
-  const int C = 9 * P;  // 16-byte chunks of 4 rows
+  const int C = RB * 9 * P / 4;  // 16-byte chunks of RB rows
   const bool rows_ok = n0 < H;
   const bool pre = k * C <= 64 * NC;
   const uint32_t *tid_ids = ids + size_t(t) * k;
@@ -243,15 +278,23 @@ __global__ void __launch_bounds__(64 * NW)
       }
     }
   }
-  copy_to_lds(h + size_t(t) * k * I, region, k * I * 4, threadIdx.x, 64 * NW);
   if (threadIdx.x < k) {
     eid[threadIdx.x] = tid_ids[threadIdx.x];
     esc[threadIdx.x] = scores ? scores[size_t(t) * k + threadIdx.x] : 1.0f;
   }
-  __syncthreads();
-  for (int j = 0; j < k; ++j)
-    permute_x<TD>(region + j * I, LMOE_F32, P, hx + j * P * XS, hs + j * sum_sz, threadIdx.x, 64 * NW);
-  __syncthreads();
+  if (hprep) {
+    copy_to_lds(hprep + size_t(t) * k * P * XS, hx, k * P * XS, threadIdx.x, 64 * NW);
+    __syncthreads();
+    if (!has_sums) {
+      sums_in_lds<TD>(hx, k * P, threadIdx.x, 64 * NW);
+      __syncthreads();
+    }
+  } else {
+    copy_to_lds(h + size_t(t) * k * I, region, k * I, threadIdx.x, 64 * NW);
+    __syncthreads();
+    for (int j = 0; j < k; ++j) prep_in_lds<TD>(region + j * I, LMOE_F32, P, hx + j * P * XS, threadIdx.x, 64 * NW);
+    __syncthreads();
+  }
   if (!rows_ok) return;
 
   u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
@@ -272,15 +315,12 @@ __global__ void __launch_bounds__(64 * NW)
   __builtin_amdgcn_wave_barrier();
 
   const int U = k * RB * P;
+#pragma unroll 2
   for (int u = lane; u < U; u += 64) {
     const int j = u / (RB * P), rem = u - j * (RB * P), row = rem / P, p = rem - row * P;
     float part = 0.0f;
-    if (eid[j] < uint32_t(n_experts)) {
-      uint32_t xv[32];
-      load_x32(hx + (j * P + p) * XS, xv);
-      const float *sj = hs + j * sum_sz;
-      part = esc[j] * row_unit_dot<TD>(stage + (j * RB + row) * 9 * P, p, xv, sj[2 * p], sj[2 * p + 1]);
-    }
+    if (eid[j] < uint32_t(n_experts))
+      part = esc[j] * row_unit_dot<TD>(stage + (j * RB + row) * 9 * P, p, hx + (j * P + p) * XS);
     red[row * red_ld + j * P + p] = part;
   }
   __builtin_amdgcn_wave_barrier();
@@ -289,8 +329,8 @@ __global__ void __launch_bounds__(64 * NW)
   const int rr = lane / LPR, sub = lane % LPR;
   float acc = 0.0f;
   for (int i = sub; i < k * P; i += LPR) acc += red[rr * red_ld + i];
-#pragma unroll
-  for (int m = LPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  acc = sum16(acc);
+  if (LPR == 32) acc += lane_xor16(acc);
   const int n = n0 + rr;
   if (sub == 0 && n < H) {
     const size_t o = size_t(t) * H + n;
@@ -302,33 +342,58 @@ __global__ void __launch_bounds__(64 * NW)
 
 // ---- host dispatch ----------------------------------------------------------------------------------------------
 
-template <int TG, int TU, int NC, int NW>
-static int launch_gate_up(const void *x, int xdt, const uint32_t *slots, int n_slots, int topk, const uint8_t *wg,
-                          const uint8_t *wu, int n_experts, int H, int I, float *h, hipStream_t st) {
-  const int P = H / 64;
-  const int sum_sz = (2 * P + 3) & ~3;
-  const size_t stage_dw = size_t(2) * RB * 9 * P, xraw_dw = size_t(16) * P * (xdt == LMOE_F32 ? 4 : 2);
-  const size_t lds = size_t(4) * ((TG == TU ? 1 : 2) * P * XS + sum_sz + std::max(NW * stage_dw, xraw_dw) +
+struct GateUpArgs {
+  const uint32_t *xg_prep, *xu_prep;
+  const void *x;
+  int xdt;
+  const uint32_t *slots;
+  int n_slots, topk;
+  const uint8_t *wg, *wu;
+  int n_experts, H, I;
+  float *h;
+  uint32_t *hprep;
+  int td;
+  const float *logits;
+  int ld_stride, norm;
+  uint32_t *ids_out;
+  float *scores_out;
+};
+
+template <int TG, int TU, int RB, int NC, int NW>
+static int launch_gate_up(const GateUpArgs &a, hipStream_t st) {
+  const int P = a.H / 64;
+  const size_t stage_dw = size_t(2) * RB * 9 * P;
+  const size_t xraw_dw = a.xg_prep ? 0 : size_t(16) * P * (a.xdt == LMOE_F32 ? 4 : 2);
+  const size_t lds = size_t(4) * ((TG == TU ? 1 : 2) * P * XS + std::max(NW * stage_dw, xraw_dw) +
                                   NW * 2 * RB * (P + 1));
-  LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "lmoe_gemv_gate_up: hidden %d needs %zu bytes of LDS", H, lds);
-  const dim3 grid((I + RB * NW - 1) / (RB * NW), n_slots);
-  if (int rc = allow_lds(k_gate_up<TG, TU, NC, NW>, lds, "lmoe_gemv_gate_up")) return rc;
-  hipLaunchKernelGGL((k_gate_up<TG, TU, NC, NW>), grid, dim3(64 * NW), lds, st, x, xdt, slots, topk, wg, wu,
-                     n_experts, I, h, P);
+  LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "lmoe_gemv_gate_up: hidden %d needs %zu bytes of LDS", a.H, lds);
+  const dim3 grid((a.I + RB * NW - 1) / (RB * NW), a.n_slots);
+  if (int rc = allow_lds(k_gate_up<TG, TU, RB, NC, NW>, lds, "lmoe_gemv_gate_up")) return rc;
+  hipLaunchKernelGGL((k_gate_up<TG, TU, RB, NC, NW>), grid, dim3(64 * NW), lds, st, a.xg_prep, a.xu_prep, a.x,
+                     a.xdt, a.slots, a.topk, a.wg, a.wu, a.n_experts, a.I, a.h, a.hprep, a.td, P, a.logits,
+                     a.ld_stride, a.norm, a.ids_out, a.scores_out);
   LMOE_LAUNCHED("lmoe_gemv_gate_up");
   return 0;
 }
 
+// 2 rows a task when the row chunks split evenly (P even), else 4; NC covers a task's 16-byte chunks a lane.
 template <int TG, int TU>
-static int gate_up_p(const void *x, int xdt, const uint32_t *slots, int n_slots, int topk, const uint8_t *wg,
-                     const uint8_t *wu, int n_experts, int H, int I, float *h, hipStream_t st) {
-  const int nc = (9 * (H / 64) + 63) / 64;  // 16-byte chunks a lane a matrix
-  if (nc <= 2) return launch_gate_up<TG, TU, 2, 4>(x, xdt, slots, n_slots, topk, wg, wu, n_experts, H, I, h, st);
-  if (nc <= 4) return launch_gate_up<TG, TU, 4, 4>(x, xdt, slots, n_slots, topk, wg, wu, n_experts, H, I, h, st);
-  if (nc <= 6) return launch_gate_up<TG, TU, 6, 4>(x, xdt, slots, n_slots, topk, wg, wu, n_experts, H, I, h, st);
-  if (nc <= 9) return launch_gate_up<TG, TU, 9, 2>(x, xdt, slots, n_slots, topk, wg, wu, n_experts, H, I, h, st);
-  if (nc <= 12) return launch_gate_up<TG, TU, 12, 2>(x, xdt, slots, n_slots, topk, wg, wu, n_experts, H, I, h, st);
-  return fail(LMOE_ESHAPE, "lmoe_gemv_gate_up: hidden %d is above the 5376 this kernel stages", H);
+static int gate_up_p(const GateUpArgs &a, hipStream_t st) {
+  const int P = a.H / 64;
+  if (P % 2 == 0) {
+    const int nc = (2 * 9 * P / 4 + 63) / 64;
+    if (nc <= 2) return launch_gate_up<TG, TU, 2, 2, 4>(a, st);
+    if (nc <= 3) return launch_gate_up<TG, TU, 2, 3, 4>(a, st);
+    if (nc <= 5) return launch_gate_up<TG, TU, 2, 5, 4>(a, st);
+    if (nc <= 6) return launch_gate_up<TG, TU, 2, 6, 4>(a, st);
+  }
+  const int nc = (9 * P + 63) / 64;
+  if (nc <= 2) return launch_gate_up<TG, TU, 4, 2, 4>(a, st);
+  if (nc <= 4) return launch_gate_up<TG, TU, 4, 4, 4>(a, st);
+  if (nc <= 6) return launch_gate_up<TG, TU, 4, 6, 4>(a, st);
+  if (nc <= 9) return launch_gate_up<TG, TU, 4, 9, 2>(a, st);
+  if (nc <= 12) return launch_gate_up<TG, TU, 4, 12, 2>(a, st);
+  return fail(LMOE_ESHAPE, "lmoe_gemv_gate_up: hidden %d is above the 5376 this kernel stages", a.H);
 }
 
 static int check_matrix(const char *fn, int type, int rows, int cols, const void *buf) {
@@ -337,6 +402,74 @@ static int check_matrix(const char *fn, int type, int rows, int cols, const void
                "%s: row length %d is not a multiple of %d", fn, cols, type == LMOE_Q4_K ? 256 : 64);
   LMOE_REQUIRE(rows > 0 && rows % 4 == 0, LMOE_ESHAPE, "%s: %d rows is not a multiple of 4", fn, rows);
   LMOE_REQUIRE(buf && aligned16(buf), LMOE_EALIGN, "%s: expert buffer must be 16-byte aligned", fn);
+  return 0;
+}
+
+static int gate_up(const char *fn, const GateUpArgs &a, int type_g, int type_u, void *stream) {
+  LMOE_REQUIRE(a.n_slots >= 0 && a.topk > 0 && a.n_slots % a.topk == 0, LMOE_ESHAPE,
+               "%s: %d slots is not a multiple of topk %d", fn, a.n_slots, a.topk);
+  LMOE_REQUIRE(a.n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
+  if (int rc = check_matrix(fn, type_g, a.I, a.H, a.wg)) return rc;
+  if (int rc = check_matrix(fn, type_u, a.I, a.H, a.wu)) return rc;
+  LMOE_REQUIRE(!a.hprep || qtype_ok(a.td), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)",
+               fn, a.td);
+  LMOE_REQUIRE(!a.hprep || (a.I % 64 == 0 && (a.td != LMOE_Q4_K || a.I % 256 == 0)), LMOE_ESHAPE,
+               "%s: width %d cannot be prepared for ggml type %d", fn, a.I, a.td);
+  if (a.n_slots == 0) return 0;
+  LMOE_REQUIRE((a.slots || a.logits) && (a.h || a.hprep), LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(!a.logits || (a.ids_out && a.scores_out && a.topk <= 32 && a.topk <= a.n_experts &&
+                             a.n_experts <= 1024),
+               LMOE_ESHAPE, "%s: top-k %d of %d experts is outside what the fused router takes", fn, a.topk,
+               a.n_experts);
+  hipStream_t st = (hipStream_t)stream;
+  if (type_g == LMOE_Q4_0 && type_u == LMOE_Q4_0) return gate_up_p<LMOE_Q4_0, LMOE_Q4_0>(a, st);
+  if (type_g == LMOE_Q4_K && type_u == LMOE_Q4_K) return gate_up_p<LMOE_Q4_K, LMOE_Q4_K>(a, st);
+  if (type_g == LMOE_Q4_0) return gate_up_p<LMOE_Q4_0, LMOE_Q4_K>(a, st);
+  return gate_up_p<LMOE_Q4_K, LMOE_Q4_0>(a, st);
+}
+
+struct DownArgs {
+  const uint32_t *hprep;
+  int has_sums;
+  const float *h;
+  const uint32_t *ids;
+  const float *scores;
+  int T, k;
+  const uint8_t *wd;
+  int type_d, n_experts, I, H;
+  const float *shared, *gate;
+  int gate_stride;
+  const void *residual;
+  int rdt;
+  void *out;
+  int odt;
+};
+
+static int down(const char *fn, const DownArgs &a, void *stream) {
+  LMOE_REQUIRE(dtype_ok(a.odt) && (!a.residual || dtype_ok(a.rdt)), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(a.T >= 0 && a.k > 0 && a.k <= 32, LMOE_ESHAPE, "%s: k %d is outside 1..32", fn, a.k);
+  LMOE_REQUIRE(a.n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
+  LMOE_REQUIRE(!a.shared == !a.gate, LMOE_EINVAL, "%s: shared and gate go together", fn);
+  if (int rc = check_matrix(fn, a.type_d, a.H, a.I, a.wd)) return rc;
+  if (a.T == 0) return 0;
+  LMOE_REQUIRE((a.h || a.hprep) && a.ids && a.out, LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(a.hprep ? aligned16(a.hprep) : aligned16(a.h), LMOE_EALIGN, "%s: h must be 16-byte aligned", fn);
+  constexpr int NW = 2, NC = 16;
+  const int P = a.I / 64;
+  const int RB = P % 2 == 0 ? 2 : 4;
+  const size_t stage_dw = size_t(a.k) * RB * 9 * P;
+  const size_t hraw_dw = a.hprep ? 0 : size_t(a.k) * a.I;
+  const size_t lds = size_t(4) * (size_t(a.k) * P * XS + 64 + std::max(NW * stage_dw, hraw_dw) +
+                                  NW * RB * (a.k * P + 1));
+  LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "%s: k %d at width %d needs %zu bytes of LDS", fn, a.k, a.I, lds);
+  const dim3 grid((a.H + RB * NW - 1) / (RB * NW), a.T);
+  hipStream_t st = (hipStream_t)stream;
+  auto kern = a.type_d == LMOE_Q4_0 ? (RB == 2 ? k_down_combine<LMOE_Q4_0, 2, NC, NW> : k_down_combine<LMOE_Q4_0, 4, NC, NW>)
+                                    : (RB == 2 ? k_down_combine<LMOE_Q4_K, 2, NC, NW> : k_down_combine<LMOE_Q4_K, 4, NC, NW>);
+  if (int rc = allow_lds(kern, lds, fn)) return rc;
+  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, st, a.hprep, a.has_sums, a.h, a.ids, a.scores, a.k, a.wd,
+                     a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt);
+  LMOE_LAUNCHED(fn);
   return 0;
 }
 
@@ -349,55 +482,54 @@ extern "C" int lmoe_gemv_gate_up(const void *x, int xdtype, const uint32_t *slot
                                  int I, float *h, void *stream) {
   const char *fn = "lmoe_gemv_gate_up";
   LMOE_REQUIRE(dtype_ok(xdtype), LMOE_EINVAL, "%s: x dtype %d is not F32, F16 or BF16", fn, xdtype);
-  LMOE_REQUIRE(n_slots >= 0 && topk > 0 && n_slots % topk == 0, LMOE_ESHAPE,
-               "%s: %d slots is not a multiple of topk %d", fn, n_slots, topk);
-  LMOE_REQUIRE(n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
-  if (int rc = check_matrix(fn, type_g, I, H, wg)) return rc;
-  if (int rc = check_matrix(fn, type_u, I, H, wu)) return rc;
-  if (n_slots == 0) return 0;
-  LMOE_REQUIRE(x && slots && h, LMOE_EINVAL, "%s: null pointer", fn);
-  LMOE_REQUIRE(aligned16(x), LMOE_EALIGN, "%s: x must be 16-byte aligned", fn);
-  hipStream_t st = (hipStream_t)stream;
-  if (type_g == LMOE_Q4_0 && type_u == LMOE_Q4_0)
-    return gate_up_p<LMOE_Q4_0, LMOE_Q4_0>(x, xdtype, slots, n_slots, topk, wg, wu, n_experts, H, I, h, st);
-  if (type_g == LMOE_Q4_K && type_u == LMOE_Q4_K)
-    return gate_up_p<LMOE_Q4_K, LMOE_Q4_K>(x, xdtype, slots, n_slots, topk, wg, wu, n_experts, H, I, h, st);
-  if (type_g == LMOE_Q4_0)
-    return gate_up_p<LMOE_Q4_0, LMOE_Q4_K>(x, xdtype, slots, n_slots, topk, wg, wu, n_experts, H, I, h, st);
-  return gate_up_p<LMOE_Q4_K, LMOE_Q4_0>(x, xdtype, slots, n_slots, topk, wg, wu, n_experts, H, I, h, st);
+  LMOE_REQUIRE(n_slots == 0 || (x && aligned16(x)), LMOE_EALIGN, "%s: x must be 16-byte aligned", fn);
+  GateUpArgs a{nullptr, nullptr, x, xdtype, slots, n_slots, topk, wg, wu, n_experts, H, I, h, nullptr, 0,
+               nullptr, 0, 0, nullptr, nullptr};
+  return gate_up(fn, a, type_g, type_u, stream);
+}
+
+extern "C" int lmoe_gemv_gate_up_prepped(const uint32_t *xg_prep, const uint32_t *xu_prep, const uint32_t *slots,
+                                         int n_slots, int topk, const uint8_t *wg, const uint8_t *wu, int type_g,
+                                         int type_u, int n_experts, int H, int I, float *h, uint32_t *hprep,
+                                         int type_d, void *stream) {
+  const char *fn = "lmoe_gemv_gate_up_prepped";
+  LMOE_REQUIRE(n_slots == 0 || (xg_prep && aligned16(xg_prep) && (type_g == type_u || (xu_prep && aligned16(xu_prep)))),
+               LMOE_EALIGN, "%s: prepared rows must be given and 16-byte aligned", fn);
+  GateUpArgs a{xg_prep, type_g == type_u ? xg_prep : xu_prep, nullptr, 0, slots, n_slots, topk, wg, wu, n_experts,
+               H, I, h, hprep, type_d, nullptr, 0, 0, nullptr, nullptr};
+  return gate_up(fn, a, type_g, type_u, stream);
+}
+
+extern "C" int lmoe_moe_gate_up(const float *logits, int ld_stride, int T, int k, int norm, const uint32_t *xg_prep,
+                                const uint32_t *xu_prep, const uint8_t *wg, const uint8_t *wu, int type_g,
+                                int type_u, int n_experts, int H, int I, uint32_t *ids, float *scores,
+                                uint32_t *hprep, int type_d, void *stream) {
+  const char *fn = "lmoe_moe_gate_up";
+  LMOE_REQUIRE(T == 0 || (logits && xg_prep && aligned16(xg_prep) && (type_g == type_u || (xu_prep && aligned16(xu_prep)))),
+               LMOE_EALIGN, "%s: logits and 16-byte aligned prepared rows must be given", fn);
+  LMOE_REQUIRE(ld_stride >= n_experts, LMOE_ESHAPE, "%s: logits row stride %d is below %d experts", fn, ld_stride,
+               n_experts);
+  GateUpArgs a{xg_prep, type_g == type_u ? xg_prep : xu_prep, nullptr, 0, nullptr, T * k, k, wg, wu, n_experts,
+               H, I, nullptr, hprep, type_d, logits, ld_stride, norm, ids, scores};
+  return gate_up(fn, a, type_g, type_u, stream);
 }
 
 extern "C" int lmoe_gemv_down_combine(const float *h, const uint32_t *ids, const float *scores, int T, int k,
                                       const uint8_t *wd, int type_d, int n_experts, int I, int H, const float *shared,
                                       const float *gate, int gate_stride, const void *residual, int rdtype,
                                       void *out, int odtype, void *stream) {
-  const char *fn = "lmoe_gemv_down_combine";
-  LMOE_REQUIRE(dtype_ok(odtype) && (!residual || dtype_ok(rdtype)), LMOE_EINVAL, "%s: bad dtype", fn);
-  LMOE_REQUIRE(T >= 0 && k > 0 && k <= 32, LMOE_ESHAPE, "%s: k %d is outside 1..32", fn, k);
-  LMOE_REQUIRE(n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
-  LMOE_REQUIRE(!shared == !gate, LMOE_EINVAL, "%s: shared and gate go together", fn);
-  if (int rc = check_matrix(fn, type_d, H, I, wd)) return rc;
-  if (T == 0) return 0;
-  LMOE_REQUIRE(h && ids && out, LMOE_EINVAL, "%s: null pointer", fn);
-  LMOE_REQUIRE(aligned16(h), LMOE_EALIGN, "%s: h must be 16-byte aligned", fn);
-  constexpr int NW = 2, NC = 16;
-  const int P = I / 64;
-  const int sum_sz = (2 * P + 3) & ~3;
-  const size_t stage_dw = size_t(k) * RB * 9 * P;
-  const size_t lds = size_t(4) * (k * P * XS + k * sum_sz + 64 + std::max(NW * stage_dw, size_t(k) * I) +
-                                  NW * RB * (k * P + 1));
-  LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "%s: k %d at width %d needs %zu bytes of LDS", fn, k, I, lds);
-  const dim3 grid((H + RB * NW - 1) / (RB * NW), T);
-  hipStream_t st = (hipStream_t)stream;
-  if (type_d == LMOE_Q4_0) {
-    if (int rc = allow_lds(k_down_combine<LMOE_Q4_0, NC, NW>, lds, fn)) return rc;
-    hipLaunchKernelGGL((k_down_combine<LMOE_Q4_0, NC, NW>), grid, dim3(64 * NW), lds, st, h, ids, scores, k, wd,
-                       n_experts, I, H, shared, gate, gate_stride, residual, rdtype, out, odtype);
-  } else {
-    if (int rc = allow_lds(k_down_combine<LMOE_Q4_K, NC, NW>, lds, fn)) return rc;
-    hipLaunchKernelGGL((k_down_combine<LMOE_Q4_K, NC, NW>), grid, dim3(64 * NW), lds, st, h, ids, scores, k, wd,
-                       n_experts, I, H, shared, gate, gate_stride, residual, rdtype, out, odtype);
-  }
-  LMOE_LAUNCHED(fn);
-  return 0;
+  DownArgs a{nullptr, 0, h, ids, scores, T, k, wd, type_d, n_experts, I, H, shared, gate, gate_stride, residual,
+             rdtype, out, odtype};
+  return down("lmoe_gemv_down_combine", a, stream);
+}
+
+extern "C" int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sums, const uint32_t *ids,
+                                              const float *scores, int T, int k, const uint8_t *wd, int type_d,
+                                              int n_experts, int I, int H, const float *shared, const float *gate,
+                                              int gate_stride, const void *residual, int rdtype, void *out,
+                                              int odtype, void *stream) {
+  LMOE_REQUIRE(hprep, LMOE_EINVAL, "lmoe_gemv_down_combine_prepped: null pointer");
+  DownArgs a{hprep, has_sums, nullptr, ids, scores, T, k, wd, type_d, n_experts, I, H, shared, gate, gate_stride,
+             residual, rdtype, out, odtype};
+  return down("lmoe_gemv_down_combine_prepped", a, stream);
 }

@@ -10,6 +10,10 @@
 // 16 (0x4C00). Then sum((16 + q) x) = 16 sum(x) + sum(q x): the block's exact sum(q x) follows from one fused
 // multiply-add with the block's precomputed sum(x). Products of f16 values are exact in fp32, so the dot is an
 // fp32-accumulated dot of the exact integer nibbles with the f16 activations.
+//
+// Prepared activations ("prep" rows): an activation row of 64 P values is kept as P units of 36 dwords, the
+// layout the kernels use in LDS: dwords 0..31 the unit's f16 pairs in nibble order (xelem below), dwords 32 and 33
+// the sums of the unit's two 32-value halves over the f16-rounded values, dwords 34 and 35 zero.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -24,6 +28,8 @@ namespace lmoe {
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int XS = 36;  // dwords a prepared unit takes (32 pairs, 2 sums, 2 pad)
 
 // ---- host-side error plumbing ----------------------------------------------------------------------------------
 
@@ -56,8 +62,6 @@ inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3
 inline bool dtype_ok(int t) { return t == LMOE_F32 || t == LMOE_F16 || t == LMOE_BF16; }
 inline bool qtype_ok(int t) { return t == LMOE_Q4_0 || t == LMOE_Q4_K; }
 inline int block_weights(int t) { return t == LMOE_Q4_K ? 256 : 32; }
-// bytes of a [rows][cols] matrix in block type t
-inline size_t matrix_bytes(int t, size_t rows, size_t cols) { return rows * (cols / 64) * 36; }
 
 // ---- element loads / stores ------------------------------------------------------------------------------------
 
@@ -95,18 +99,118 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * s * u;
 }
 
-// ---- wavefront (64 lanes) reductions ---------------------------------------------------------------------------
+// ---- cross-lane exchanges on the VALU (DPP and gfx950's permlane swaps) ------------------------------------------
+//
+// A dependent ds_bpermute / ds_swizzle round trip costs ~70 ns here; these stay in the vector ALU.
 
+#define LMOE_DPP(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16
+
+// the value of lane ^ 16 / lane ^ 32
+__device__ __forceinline__ float lane_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+// sums over aligned groups of 8 / 16 / 64 lanes, the result in every lane of the group (fixed order: deterministic)
+__device__ __forceinline__ float sum8(float v) {
+  v += LMOE_DPP(v, kDppXor1);
+  v += LMOE_DPP(v, kDppXor2);
+  v += LMOE_DPP(v, kDppHalfMirror);
+  return v;
+}
+__device__ __forceinline__ float sum16(float v) {
+  v = sum8(v);
+  return v + LMOE_DPP(v, kDppMirror);
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+  v = sum16(v);
+  v += lane_xor16(v);
+  v += lane_xor32(v);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, LMOE_DPP(v, kDppXor1));
+  v = fmaxf(v, LMOE_DPP(v, kDppXor2));
+  v = fmaxf(v, LMOE_DPP(v, kDppHalfMirror));
+  v = fmaxf(v, LMOE_DPP(v, kDppMirror));
+  v = fmaxf(v, lane_xor16(v));
+  v = fmaxf(v, lane_xor32(v));
   return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+// ---- top-k over a wavefront -------------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppXor1, 0xF, 0xF, false)));
+  v = min(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppXor2, 0xF, 0xF, false)));
+  v = min(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppHalfMirror, 0xF, 0xF, false)));
+  v = min(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), kDppMirror, 0xF, 0xF, false)));
+  v = min(v, __builtin_bit_cast(uint32_t, lane_xor16(__builtin_bit_cast(float, v))));
+  v = min(v, __builtin_bit_cast(uint32_t, lane_xor32(__builtin_bit_cast(float, v))));
   return v;
+}
+
+// One wavefront, a token's logits v[j] = row[lane + 64 j] (j < NPL, E <= 64 NPL) -> ids[0..k) best first,
+// scores[0..k). Each of k rounds takes the largest untaken logit (a max over the wavefront) and, among the lanes
+// holding it, the lowest expert index (a min over the wavefront): both reductions stay on the VALU.
+template <int NPL>
+__device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm, uint32_t *ids, float *scores) {
+  const int lane = threadIdx.x & 63;
+  uint32_t taken = 0;
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    if (lane + 64 * j < E)
+      m = fmaxf(m, v[j]);
+    else
+      taken |= 1u << j;
+  }
+  m = wave_max(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j)
+    if (!((taken >> j) & 1u)) s += __expf(v[j] - m);
+  s = wave_sum(s);
+  float mine = 0.0f;
+  uint32_t my_id = 0;
+  for (int r = 0; r < k; ++r) {
+    float best = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+      if (!((taken >> j) & 1u)) best = fmaxf(best, v[j]);
+    best = wave_max(best);
+    uint32_t cand = 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = NPL - 1; j >= 0; --j)
+      if (!((taken >> j) & 1u) && v[j] == best) cand = uint32_t(lane + 64 * j);
+    const uint32_t win = wave_min_u32(cand);
+    if ((win & 63u) == uint32_t(lane)) taken |= 1u << (win >> 6);
+    if (lane == r) {
+      my_id = win;
+      mine = __expf(best - m) / s;
+    }
+  }
+  if (norm) {
+    float tot = 0.0f;  // the k picked probabilities summed in rank order
+    for (int r = 0; r < k; ++r)
+      tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), r));
+    mine = mine / tot;
+  }
+  if (lane < k) {
+    ids[lane] = my_id;
+    scores[lane] = mine;
+  }
 }
 
 // ---- nibble words -> f16 pairs ----------------------------------------------------------------------------------
@@ -151,6 +255,12 @@ __device__ __forceinline__ float half_hi(uint32_t w) { return float(__builtin_bi
 __device__ __forceinline__ int xelem(int dw, int h, int H) {
   const int span = dw / H, i = (dw % H) >> 2, s = dw & 3;
   return span * 2 * H + (s & 1) * H + 4 * i + (s >> 1) + 2 * h;
+}
+// the inverse: unit weight e -> (dword, half)
+__device__ __forceinline__ void xslot(int e, int H, int *dw, int *half) {
+  const int span = e / (2 * H), f = e % (2 * H), hi = f >= H ? 1 : 0, g = f % H, i = g >> 2, r = g & 3;
+  *dw = span * H + 4 * i + 2 * (r & 1) + hi;
+  *half = r >> 1;
 }
 
 // qs word i of Q4_K sub-block pair c from the 12-byte scale field words s0, s1, s2: (sc, m) of sub-blocks 2c and
@@ -212,6 +322,24 @@ __device__ __forceinline__ float unit_dot_q4_k(const uint32_t *hdr, const uint32
   const float ra = (d * sc0) * fmaf(-16.0f, sx0, a) - (dmin * m0) * sx0;
   const float rb = (d * sc1) * fmaf(-16.0f, sx1, b) - (dmin * m1) * sx1;
   return ra + rb;
+}
+
+// ---- preparing activation rows -----------------------------------------------------------------------------------
+
+// Unit dword (p, dw) of a prepared row for block type TQ, from an element reader ld(i) over the row's 64 P values.
+template <int TQ, typename Ld>
+__device__ __forceinline__ uint32_t prep_dword(Ld ld, int p, int dw) {
+  constexpr int H = TQ == LMOE_Q4_K ? 32 : 16;
+  if (dw < 32) {
+    const h2_t v = {_Float16(ld(64 * p + xelem(dw, 0, H))), _Float16(ld(64 * p + xelem(dw, 1, H)))};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  if (dw < 34) {
+    float s = 0.0f;
+    for (int j = 0; j < 32; ++j) s += float(_Float16(ld(64 * p + 32 * (dw - 32) + j)));
+    return __builtin_bit_cast(uint32_t, s);
+  }
+  return 0u;
 }
 
 }  // namespace lmoe

@@ -1,82 +1,35 @@
-// Router: softmax + top-k, one wavefront per token (the reference's moe_probs runs one 32-lane warp a row,
-// route_cuda.py:193-254; here a 64-lane wavefront holds E <= 1024 logits as 16 registers a lane).
+// Router: the gate GEMV (logits = x . Wr) and softmax + top-k.
 //
-// Selection is made on the fp32 logits, larger first, equal values ordered by the lower expert index; the
-// scores are the softmax probabilities of the picked experts (max-subtracted, fp32), renormalised when asked.
-#include <cfloat>
-
+// The reference runs the gate linear as an MLX matmul and the top-k in moe_probs, one 32-lane warp a row doing k
+// rounds of shuffle argmax (route_cuda.py:193-254). Here:
+//   * k_router_gemv spreads the E router rows over wavefronts (one row each, all T tokens), the row's weights
+//     fetched with 16-byte loads while x is staged in LDS, and emits the prepared activation rows the expert
+//     kernels read (lmoe_common.h), so no later kernel rearranges x again;
+//   * k_router_topk takes k rounds of a wavefront argmax, one wavefront a token, its max and min-index reductions
+//     on DPP and gfx950's permlane swaps rather than LDS shuffles.
+// Selection is on the fp32 logits, larger first, ties to the lower expert index; scores are the softmax
+// probabilities of the picked experts (max-subtracted, fp32), renormalised when asked.
 #include "lmoe_common.h"
 
 namespace lmoe {
 
 constexpr int kMaxNpl = 16;  // logits a lane: E <= 64 * 16
 
-// One wavefront: row[0..E) -> ids[0..k) best first, scores[0..k).
-template <typename Load>
-__device__ __forceinline__ void topk_wave(Load ld, int E, int k, int norm, uint32_t *ids, float *scores) {
+// Four tokens a workgroup, one wavefront each.
+template <int NPL>
+__global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt, int ld_stride, int T, int E,
+                                                     int k, int norm, uint32_t *ids, float *scores) {
   const int lane = threadIdx.x & 63;
-  float v[kMaxNpl];
-  float m = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < kMaxNpl; ++j) {
-    const int i = lane + 64 * j;
-    v[j] = i < E ? ld(i) : -INFINITY;
-    m = fmaxf(m, v[j]);
-  }
-  m = wave_max(m);
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kMaxNpl; ++j)
-    if (lane + 64 * j < E) s += __expf(v[j] - m);
-  s = wave_sum(s);
-  uint32_t taken = 0;
-  float mine = 0.0f;
-  uint32_t my_id = 0;
-  for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < kMaxNpl; ++j) {
-      const int i = lane + 64 * j;
-      if (i < E && !((taken >> j) & 1u) && (v[j] > bv || (v[j] == bv && i < bi))) {
-        bv = v[j];
-        bi = i;
-      }
-    }
-#pragma unroll
-    for (int msk = 32; msk > 0; msk >>= 1) {
-      const float ov = __shfl_xor(bv, msk, 64);
-      const int oi = __shfl_xor(bi, msk, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1u << ((bi >> 6) & 31);
-    if (lane == r) {
-      my_id = uint32_t(bi);
-      mine = __expf(bv - m) / s;
-    }
-  }
-  if (norm) {
-    float tot = 0.0f;
-    // the k picked probabilities summed in pick order (lane 0 reads them one by one)
-    for (int r = 0; r < k; ++r) tot += __shfl(mine, r, 64);
-    mine = mine / tot;
-  }
-  if (lane < k) {
-    ids[lane] = my_id;
-    scores[lane] = mine;
-  }
-}
-
-__global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt, int T, int E, int k, int norm,
-                                                     uint32_t *ids, float *scores) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const size_t base = size_t(t) * E;
-  topk_wave([&](int i) { return load_elt(logits, base + i, ldt); }, E, k, norm, ids + size_t(t) * k,
-            scores + size_t(t) * k);
+  const size_t base = size_t(t) * ld_stride;
+  float v[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int i = lane + 64 * j;
+    v[j] = i < E ? load_elt(logits, base + i, ldt) : -INFINITY;
+  }
+  topk_wave<NPL>(v, E, k, norm, ids + size_t(t) * k, scores + size_t(t) * k);
 }
 
 constexpr int kRouterWaves = 4;
@@ -85,15 +38,14 @@ constexpr int kRouterMaxXs = 16384;  // T * H floats of x held in LDS
 constexpr int kRouterNc = 16;        // 16-byte weight chunks a lane (H * element size <= 16 KiB)
 
 // Each wavefront one router row (the last row the shared-expert gate when wsg is given) for all T tokens: its
-// weight chunks load first, x is staged in LDS as f32 meanwhile; then the last workgroup to finish runs the top-k
-// of every token and returns the counter to zero for the next launch. WDT: the weights' element type.
-template <int WDT>
+// weight chunks load first, x is staged in LDS as f32 meanwhile. When xprep is given the workgroups also write
+// the prepared activation rows for block type TQ, a slice of units each. WDT: the weights' element type.
+template <int WDT, int TQ>
 __global__ void __launch_bounds__(64 * kRouterWaves)
-    k_router_gemv(const void *x, int xdt, const void *wr, const void *wsg, int T, int H, int E, int k, int norm,
-                  float *logits, uint32_t *ids, float *scores, uint32_t *counter) {
+    k_router_gemv(const void *x, int xdt, const void *wr, const void *wsg, int T, int H, int E, float *logits,
+                  uint32_t *xprep) {
   constexpr int EPC = WDT == LMOE_F32 ? 4 : 8;  // elements a 16-byte chunk
   __shared__ float xs[kRouterMaxXs];
-  __shared__ int last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rows = E + (wsg != nullptr ? 1 : 0);
   const int row = blockIdx.x * kRouterWaves + wave;
@@ -111,109 +63,155 @@ __global__ void __launch_bounds__(64 * kRouterWaves)
   }
   for (int i = threadIdx.x; i < T * H; i += 64 * kRouterWaves) xs[i] = load_elt(x, i, xdt);
   __syncthreads();
-  if (row < rows) {
-    float acc[kRouterMaxT];
+  if (xprep) {  // prepared rows: units spread over the workgroups
+    const int P = H / 64, units = T * P;
+    const int per = (units + gridDim.x - 1) / gridDim.x;
+    const int u0 = blockIdx.x * per, u1 = min(units, u0 + per);
+    for (int idx = u0 * XS + threadIdx.x; idx < u1 * XS; idx += 64 * kRouterWaves) {
+      const int u = idx / XS, dw = idx - u * XS, t = u / P, p = u - t * P;
+      const float *xt = xs + t * H;
+      xprep[size_t(u) * XS + dw] = prep_dword<TQ>([&](int i) { return xt[i]; }, p, dw);
+    }
+  }
+  if (row >= rows) return;
+  float acc[kRouterMaxT];
 #pragma unroll
-    for (int t = 0; t < kRouterMaxT; ++t) acc[t] = 0.0f;
+  for (int t = 0; t < kRouterMaxT; ++t) acc[t] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kRouterNc; ++i) {
-      const int c = lane + 64 * i;
-      if (c < nch) {
-        float wv[EPC];
-        const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+  for (int i = 0; i < kRouterNc; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nch) {
+      float wv[EPC];
+      const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (WDT == LMOE_F32) {
-            wv[j] = __uint_as_float(u[j]);
-          } else if (WDT == LMOE_F16) {
-            wv[2 * j] = half_lo(u[j]);
-            wv[2 * j + 1] = half_hi(u[j]);
-          } else {
-            wv[2 * j] = __uint_as_float(u[j] << 16);
-            wv[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
-          }
-        }
-        for (int t = 0; t < T; ++t) {
-          const float *xt = xs + t * H + c * EPC;
-#pragma unroll
-          for (int j = 0; j < EPC; ++j) acc[t] = fmaf(xt[j], wv[j], acc[t]);
+      for (int j = 0; j < 4; ++j) {
+        if (WDT == LMOE_F32) {
+          wv[j] = __uint_as_float(u[j]);
+        } else if (WDT == LMOE_F16) {
+          wv[2 * j] = half_lo(u[j]);
+          wv[2 * j + 1] = half_hi(u[j]);
+        } else {
+          wv[2 * j] = __uint_as_float(u[j] << 16);
+          wv[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
         }
       }
-    }
+      for (int t = 0; t < T; ++t) {
+        const float *xt = xs + t * H + c * EPC;
 #pragma unroll
-    for (int t = 0; t < kRouterMaxT; ++t) {
-      if (t < T) {
-        const float v = wave_sum(acc[t]);
-        if (lane == 0) logits[size_t(t) * rows + row] = v;
+        for (int j = 0; j < EPC; ++j) acc[t] = fmaf(xt[j], wv[j], acc[t]);
       }
     }
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last = atomicAdd(counter, 1u) == gridDim.x - 1;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  for (int t = wave; t < T; t += kRouterWaves) {
-    const float *row_l = logits + size_t(t) * rows;
-    topk_wave([&](int i) { return __builtin_nontemporal_load(row_l + i); }, E, k, norm, ids + size_t(t) * k,
-              scores + size_t(t) * k);
+#pragma unroll
+  for (int t = 0; t < kRouterMaxT; ++t) {
+    if (t < T) {
+      const float v = wave_sum(acc[t]);
+      if (lane == 0) logits[size_t(t) * rows + row] = v;
+    }
   }
-  if (threadIdx.x == 0) atomicExch(counter, 0u);
+}
+
+// Prepared activation rows on their own: one workgroup a row, one thread a unit dword.
+template <int TQ>
+__global__ void __launch_bounds__(256) k_prep_x(const void *x, int xdt, int H, uint32_t *xprep) {
+  const int P = H / 64;
+  const size_t r = blockIdx.y;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= P * XS) return;
+  const int p = idx / XS, dw = idx - p * XS;
+  xprep[r * P * XS + idx] = prep_dword<TQ>([&](int i) { return load_elt(x, r * H + i, xdt); }, p, dw);
+}
+
+template <int WDT>
+static void launch_router(int qt, dim3 grid, dim3 block, hipStream_t st, const void *x, int xdt, const void *wr,
+                          const void *wsg, int T, int H, int E, float *logits, uint32_t *xprep) {
+  if (qt == LMOE_Q4_K)
+    hipLaunchKernelGGL((k_router_gemv<WDT, LMOE_Q4_K>), grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+  else
+    hipLaunchKernelGGL((k_router_gemv<WDT, LMOE_Q4_0>), grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
 }
 
 }  // namespace lmoe
 
 using namespace lmoe;
 
-extern "C" int lmoe_router_topk(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids,
-                                float *scores, void *stream) {
-  LMOE_REQUIRE(dtype_ok(ldtype), LMOE_EINVAL, "lmoe_router_topk: logits dtype %d is not F32, F16 or BF16", ldtype);
-  LMOE_REQUIRE(T >= 0 && E > 0 && E <= 64 * kMaxNpl, LMOE_ESHAPE,
-               "lmoe_router_topk: %d experts is outside 1..%d", E, 64 * kMaxNpl);
-  LMOE_REQUIRE(k > 0 && k <= E && k <= 32, LMOE_ESHAPE, "lmoe_router_topk: top-k %d is outside 1..min(E, 32)", k);
+static int topk_launch(const void *logits, int ldtype, int stride, int T, int E, int k, int norm, uint32_t *ids,
+                       float *scores, hipStream_t st, const char *fn) {
+  LMOE_REQUIRE(dtype_ok(ldtype), LMOE_EINVAL, "%s: logits dtype %d is not F32, F16 or BF16", fn, ldtype);
+  LMOE_REQUIRE(T >= 0 && E > 0 && E <= 64 * kMaxNpl, LMOE_ESHAPE, "%s: %d experts is outside 1..%d", fn, E,
+               64 * kMaxNpl);
+  LMOE_REQUIRE(k > 0 && k <= E && k <= 32, LMOE_ESHAPE, "%s: top-k %d is outside 1..min(E, 32)", fn, k);
   if (T == 0) return 0;
-  LMOE_REQUIRE(logits && ids && scores, LMOE_EINVAL, "lmoe_router_topk: null pointer");
-  hipLaunchKernelGGL(k_router_topk, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream, logits, ldtype, T, E, k,
-                     norm, ids, scores);
-  LMOE_LAUNCHED("lmoe_router_topk");
+  LMOE_REQUIRE(logits && ids && scores, LMOE_EINVAL, "%s: null pointer", fn);
+  const dim3 grid((T + 3) / 4), block(256);
+  if (E <= 64)
+    hipLaunchKernelGGL(k_router_topk<1>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+  else if (E <= 128)
+    hipLaunchKernelGGL(k_router_topk<2>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+  else if (E <= 256)
+    hipLaunchKernelGGL(k_router_topk<4>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+  else if (E <= 512)
+    hipLaunchKernelGGL(k_router_topk<8>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+  else
+    hipLaunchKernelGGL(k_router_topk<16>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+  LMOE_LAUNCHED(fn);
   return 0;
 }
 
-extern "C" size_t lmoe_router_workspace_bytes(void) { return 256; }
+extern "C" int lmoe_router_topk(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids,
+                                float *scores, void *stream) {
+  return topk_launch(logits, ldtype, E, T, E, k, norm, ids, scores, (hipStream_t)stream, "lmoe_router_topk");
+}
 
-extern "C" int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T,
-                                     int H, int E, int k, int norm, float *logits, uint32_t *ids, float *scores,
-                                     void *ws, void *stream) {
-  LMOE_REQUIRE(dtype_ok(xdtype) && dtype_ok(wdtype), LMOE_EINVAL, "lmoe_router_gemv_topk: bad dtype");
-  LMOE_REQUIRE(T > 0 && T <= kRouterMaxT, LMOE_ESHAPE, "lmoe_router_gemv_topk: %d tokens is outside 1..%d", T,
-               kRouterMaxT);
-  LMOE_REQUIRE(H > 0 && H % 64 == 0, LMOE_ESHAPE, "lmoe_router_gemv_topk: hidden %d is not a multiple of 64", H);
-  LMOE_REQUIRE(E > 0 && E <= 64 * kMaxNpl, LMOE_ESHAPE, "lmoe_router_gemv_topk: %d experts is outside 1..%d", E,
-               64 * kMaxNpl);
-  LMOE_REQUIRE(k > 0 && k <= E && k <= 32, LMOE_ESHAPE, "lmoe_router_gemv_topk: top-k %d is outside 1..min(E, 32)",
-               k);
-  LMOE_REQUIRE(x && wr && logits && ids && scores && ws, LMOE_EINVAL, "lmoe_router_gemv_topk: null pointer");
-  LMOE_REQUIRE(aligned16(wr) && (!wsg || aligned16(wsg)), LMOE_EALIGN,
-               "lmoe_router_gemv_topk: wr and wsg must be 16-byte aligned");
+extern "C" int lmoe_prep_x(const void *x, int xdtype, int rows, int H, int qtype, uint32_t *xprep, void *stream) {
+  const char *fn = "lmoe_prep_x";
+  LMOE_REQUIRE(dtype_ok(xdtype), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(qtype_ok(qtype), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn, qtype);
+  LMOE_REQUIRE(rows >= 0 && H > 0 && H % 64 == 0, LMOE_ESHAPE, "%s: width %d is not a multiple of 64", fn, H);
+  if (rows == 0) return 0;
+  LMOE_REQUIRE(x && xprep, LMOE_EINVAL, "%s: null pointer", fn);
+  const dim3 grid(((H / 64) * XS + 255) / 256, rows);
+  if (qtype == LMOE_Q4_K)
+    hipLaunchKernelGGL(k_prep_x<LMOE_Q4_K>, grid, dim3(256), 0, (hipStream_t)stream, x, xdtype, H, xprep);
+  else
+    hipLaunchKernelGGL(k_prep_x<LMOE_Q4_0>, grid, dim3(256), 0, (hipStream_t)stream, x, xdtype, H, xprep);
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+extern "C" int lmoe_router_gemv(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T, int H,
+                                int E, float *logits, uint32_t *xprep, int qtype, void *stream) {
+  const char *fn = "lmoe_router_gemv";
+  LMOE_REQUIRE(dtype_ok(xdtype) && dtype_ok(wdtype), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(T > 0 && T <= kRouterMaxT, LMOE_ESHAPE, "%s: %d tokens is outside 1..%d", fn, T, kRouterMaxT);
+  LMOE_REQUIRE(H > 0 && H % 64 == 0, LMOE_ESHAPE, "%s: hidden %d is not a multiple of 64", fn, H);
+  LMOE_REQUIRE(E > 0, LMOE_ESHAPE, "%s: no experts", fn);
+  LMOE_REQUIRE(!xprep || qtype_ok(qtype), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn,
+               qtype);
+  LMOE_REQUIRE(x && wr && logits, LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(aligned16(wr) && (!wsg || aligned16(wsg)), LMOE_EALIGN, "%s: wr and wsg must be 16-byte aligned",
+               fn);
   LMOE_REQUIRE(size_t(T) * H <= size_t(kRouterMaxXs), LMOE_ESHAPE,
-               "lmoe_router_gemv_topk: %d tokens x hidden %d is above the %d activations this kernel stages", T, H,
-               kRouterMaxXs);
+               "%s: %d tokens x hidden %d is above the %d activations this kernel stages", fn, T, H, kRouterMaxXs);
   LMOE_REQUIRE(size_t(H) * (wdtype == LMOE_F32 ? 4 : 2) <= size_t(kRouterNc) * 64 * 16, LMOE_ESHAPE,
-               "lmoe_router_gemv_topk: a router row of %d weights is above what a wavefront holds", H);
+               "%s: a router row of %d weights is above what a wavefront holds", fn, H);
   const int rows = E + (wsg ? 1 : 0);
   const dim3 grid((rows + kRouterWaves - 1) / kRouterWaves), block(64 * kRouterWaves);
   hipStream_t st = (hipStream_t)stream;
-  uint32_t *ctr = static_cast<uint32_t *>(ws);
   if (wdtype == LMOE_F16)
-    hipLaunchKernelGGL(k_router_gemv<LMOE_F16>, grid, block, 0, st, x, xdtype, wr, wsg, T, H, E, k, norm, logits, ids,
-                       scores, ctr);
+    launch_router<LMOE_F16>(qtype, grid, block, st, x, xdtype, wr, wsg, T, H, E, logits, xprep);
   else if (wdtype == LMOE_BF16)
-    hipLaunchKernelGGL(k_router_gemv<LMOE_BF16>, grid, block, 0, st, x, xdtype, wr, wsg, T, H, E, k, norm, logits,
-                       ids, scores, ctr);
+    launch_router<LMOE_BF16>(qtype, grid, block, st, x, xdtype, wr, wsg, T, H, E, logits, xprep);
   else
-    hipLaunchKernelGGL(k_router_gemv<LMOE_F32>, grid, block, 0, st, x, xdtype, wr, wsg, T, H, E, k, norm, logits, ids,
-                       scores, ctr);
-  LMOE_LAUNCHED("lmoe_router_gemv_topk");
+    launch_router<LMOE_F32>(qtype, grid, block, st, x, xdtype, wr, wsg, T, H, E, logits, xprep);
+  LMOE_LAUNCHED(fn);
   return 0;
+}
+
+extern "C" int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T,
+                                     int H, int E, int k, int norm, float *logits, uint32_t *ids, float *scores,
+                                     uint32_t *xprep, int qtype, void *stream) {
+  if (int rc = lmoe_router_gemv(x, xdtype, wr, wsg, wdtype, T, H, E, logits, xprep, qtype, stream)) return rc;
+  return topk_launch(logits, LMOE_F32, E + (wsg ? 1 : 0), T, E, k, norm, ids, scores, (hipStream_t)stream,
+                     "lmoe_router_gemv_topk");
 }

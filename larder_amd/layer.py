@@ -4,10 +4,10 @@ The layer is the reference block's sequence (stream_fast.py:4352-4377 over gguf_
 gguf_experts.py:803-819): router logits x . Wr, softmax top-k, the k experts' SwiGLU chains read straight from
 GGUF blocks, the weighted combine, and a sigmoid-gated shared expert when the model has one. Two drivers:
 
-  * decode (T <= 16 tokens): lmoe_router_gemv_topk -> lmoe_gemv_gate_up [-> shared expert gate/up + down]
-    -> lmoe_gemv_down_combine (down, weighted combine, shared expert, residual in one kernel); 3 launches a layer
-    without a shared expert, no host synchronisation, every buffer preallocated so a whole step can be captured
-    in a HIP graph;
+  * decode (T <= 16 tokens): router GEMV (which also writes x prepared for the expert kernels) -> top-k fused
+    into gate/up + SwiGLU (writing h prepared for down) [-> the shared expert's gate/up and down] -> down +
+    weighted combine + shared expert + residual in one kernel; 3 launches a layer without a shared expert, no
+    host synchronisation, every buffer preallocated so a whole step can be captured in a HIP graph;
   * prefill / batched decode (any T): the device grouping and the grouped MFMA GEMMs (larder_amd.grouped).
 """
 import ctypes
@@ -61,51 +61,60 @@ class DecodeBuffers:
         self.T = T
         rows = L.E + (1 if L.shared is not None else 0)
         f32 = dict(dtype=torch.float32, device=device)
-        self.ws = torch.zeros(max(64, _lib.lib().lmoe_router_workspace_bytes() // 4), dtype=torch.int32,
-                              device=device)
+        u32 = dict(dtype=torch.int32, device=device)
         self.logits = torch.empty((T, rows), **f32)
-        self.ids = torch.empty((T, L.k), dtype=torch.int32, device=device)
+        self.ids = torch.empty((T, L.k), **u32)
         self.scores = torch.empty((T, L.k), **f32)
-        self.h = torch.empty((T * L.k, L.I), **f32)
+        # prepared rows (36 dwords a 64-value unit): x for the gate / up type, h for the down type
+        self.xprep = torch.empty((T, L.H // 64 * 36), **u32)
+        self.xprep_u = torch.empty((T, L.H // 64 * 36), **u32) if L.types[1] != L.types[0] else None
+        self.hprep = torch.empty((T * L.k, L.I // 64 * 36), **u32)
         if L.shared is not None:
-            self.zero_slots = torch.zeros(T, dtype=torch.int32, device=device)
-            self.hs = torch.empty((T, L.Is), **f32)
+            self.zero_slots = torch.zeros(T, **u32)
+            self.hprep_s = torch.empty((T, L.Is // 64 * 36), **u32)
             self.shared_y = torch.empty((T, L.H), **f32)
 
 
 def decode(layer, x, bufs, out, residual=None, logits=None):
-    """out [T, H] = layer(x) (+ residual) for x [T, H] (float16 / bfloat16 / float32) through the decode chain.
-    ``logits`` [T, E] replaces the router GEMV when the layer has no router weight."""
+    """out [T, H] = layer(x) (+ residual) for x [T, H] (float16 / bfloat16 / float32) through the decode chain:
+    router GEMV (+ x prepared for the experts) and top-k, gate/up + SwiGLU (writing h prepared for down),
+    [the shared expert's gate/up and down], then down + weighted combine + shared + residual. ``logits`` [T, E]
+    replaces the router GEMV when the layer has no router weight."""
     L, B = layer, bufs
     T = x.shape[0]
     st = stream()
     tg, tu, td = (qcode(t) for t in L.types)
+    xd = dcode(x.dtype)
     if logits is None:
         if L.wr is None:
             raise ValueError("this layer has no router weight: pass logits")
-        call("lmoe_router_gemv_topk", ptr(x), dcode(x.dtype), ptr(L.wr), ptr(L.wsg), dcode(L.wr.dtype), T, L.H,
-             L.E, L.k, int(L.norm), ptr(B.logits), ptr(B.ids), ptr(B.scores), ptr(B.ws), st)
-        gate, gate_stride = (B.logits[:, L.E:], L.E + 1) if L.shared is not None else (None, 0)
+        call("lmoe_router_gemv", ptr(x), xd, ptr(L.wr), ptr(L.wsg), dcode(L.wr.dtype), T, L.H, L.E, ptr(B.logits),
+             ptr(B.xprep), tg, st)
+        lg, stride = B.logits, B.logits.shape[1]
     else:
-        lg = logits.contiguous()
-        call("lmoe_router_topk", ptr(lg), dcode(lg.dtype), T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
-        gate, gate_stride = None, 0
         if L.shared is not None:
             raise ValueError("a shared expert's gate logit comes from the router GEMV: use the router weight")
-    call("lmoe_gemv_gate_up", ptr(x), dcode(x.dtype), ptr(B.ids), T * L.k, L.k, ptr(L.wg), ptr(L.wu), tg, tu, L.E,
-         L.H, L.I, ptr(B.h), st)
-    shared_y = None
+        lg, stride = logits.to(torch.float32).contiguous(), L.E
+        call("lmoe_prep_x", ptr(x), xd, T, L.H, tg, ptr(B.xprep), st)
+    xu = B.xprep
+    if B.xprep_u is not None:
+        call("lmoe_prep_x", ptr(x), xd, T, L.H, tu, ptr(B.xprep_u), st)
+        xu = B.xprep_u
+    call("lmoe_moe_gate_up", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(xu), ptr(L.wg), ptr(L.wu), tg,
+         tu, L.E, L.H, L.I, ptr(B.ids), ptr(B.scores), ptr(B.hprep), td, st)
+    shared_y = gptr = None
+    gate_stride = 0
     if L.shared is not None:
         sg, su, sd = L.shared
-        call("lmoe_gemv_gate_up", ptr(x), dcode(x.dtype), ptr(B.zero_slots), T, 1, ptr(sg), ptr(su), tg, tu, 1, L.H,
-             L.Is, ptr(B.hs), st)
-        call("lmoe_gemv_down_combine", ptr(B.hs), ptr(B.zero_slots), None, T, 1, ptr(sd), td, 1, L.Is, L.H, None,
-             None, 0, None, 0, ptr(B.shared_y), _lib.F32, st)
+        call("lmoe_gemv_gate_up_prepped", ptr(B.xprep), ptr(xu), ptr(B.zero_slots), T, 1, ptr(sg), ptr(su), tg, tu,
+             1, L.H, L.Is, None, ptr(B.hprep_s), td, st)
+        call("lmoe_gemv_down_combine_prepped", ptr(B.hprep_s), 0, ptr(B.zero_slots), None, T, 1, ptr(sd), td, 1,
+             L.Is, L.H, None, None, 0, None, 0, ptr(B.shared_y), _lib.F32, st)
         shared_y = B.shared_y
-    gptr = _ptr_offset(B.logits, L.E) if gate is not None else None
-    call("lmoe_gemv_down_combine", ptr(B.h), ptr(B.ids), ptr(B.scores), T, L.k, ptr(L.wd), td, L.E, L.I, L.H,
-         ptr(shared_y), gptr, gate_stride, ptr(residual), dcode(residual.dtype) if residual is not None else 0,
-         ptr(out), dcode(out.dtype), st)
+        gptr, gate_stride = _ptr_offset(B.logits, L.E), L.E + 1
+    call("lmoe_gemv_down_combine_prepped", ptr(B.hprep), 0, ptr(B.ids), ptr(B.scores), T, L.k, ptr(L.wd), td, L.E,
+         L.I, L.H, ptr(shared_y), gptr, gate_stride, ptr(residual),
+         dcode(residual.dtype) if residual is not None else 0, ptr(out), dcode(out.dtype), st)
     return out
 
 
