@@ -15,6 +15,7 @@
 //   * down adds the k experts of a token, weighted by the router scores, plus the shared expert and a residual,
 //     in the same kernel, so no [T * k, H] intermediate is written.
 #include <algorithm>
+#include <type_traits>
 
 #include "lmoe_common.h"
 
@@ -120,14 +121,24 @@ __global__ void __launch_bounds__(64 * NW, 3)
     __shared__ uint32_t pick_id[32];
     __shared__ float pick_sc[32];
     if (wave == 0) {
-      const int t = s / topk;
-      float v[16];
+      const float *row = logits + size_t(s / topk) * ld_stride;
+      auto run = [&](auto npl) {
+        constexpr int N = decltype(npl)::value;
+        float v[N];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int i = lane + 64 * j;
-        v[j] = i < n_experts ? logits[size_t(t) * ld_stride + i] : -INFINITY;
-      }
-      topk_wave<16>(v, n_experts, topk, norm, pick_id, pick_sc);
+        for (int j = 0; j < N; ++j) v[j] = lane + 64 * j < n_experts ? row[lane + 64 * j] : -INFINITY;
+        topk_wave<N>(v, n_experts, topk, norm, pick_id, pick_sc);
+      };
+      if (n_experts <= 64)
+        run(std::integral_constant<int, 1>());
+      else if (n_experts <= 128)
+        run(std::integral_constant<int, 2>());
+      else if (n_experts <= 256)
+        run(std::integral_constant<int, 4>());
+      else if (n_experts <= 512)
+        run(std::integral_constant<int, 8>());
+      else
+        run(std::integral_constant<int, 16>());
     }
     __syncthreads();
     e = pick_id[s % topk];
