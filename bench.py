@@ -10,6 +10,7 @@ replays as one HIP graph. Weights are Gaussian N(0, 0.02^2) quantized to Q4_0 on
 takes a fresh N(0, 1) fp16 activation row, all resident in HBM before timing. One JSON line on stdout.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -67,33 +68,42 @@ def gpu_leg(args):
     secs = e0.elapsed_time(e1) / 1e3
     step_ms = secs / args.steps * 1e3
 
-    # the dominant kernel, timed launch by launch with HIP events on the stream it runs on, over the layers of the
-    # stack in turn: the fused top-k + gate/up + SwiGLU (lmoe_moe_gate_up)
+    # each decode kernel timed kernel-exactly (start / stop events recorded by the launches themselves, the
+    # timestamps rocprofv3 reads) over the layers of the stack in turn, outside the graph, same shapes and inputs
     B = st.bufs
     Q = _lib.Q4_0
     x = xs[0]
-    for L in layers[:2]:
-        lay.decode(L, x, B, st.ping, residual=x)
+    L0 = layers[0]
+    k, I, H, E = cfg["k"], cfg["I"], cfg["H"], cfg["E"]
+    lay.decode(L0, x, B, st.ping, residual=x)
     torch.cuda.synchronize()
+    P = lambda t: _lib.ptr(t)  # noqa: E731
+    kernels = {
+        "k_router_gemv": (lambda L: _lib.call("lmoe_router_gemv", P(x), _lib.F16, P(L.wr), None, _lib.F16, 1, H, E,
+                                              P(B.logits), P(B.xprep), Q, _lib.stream()),
+                          E * H * 2 + H * 2 + E * 4 + H // 64 * 144),
+        "k_gate_up": (lambda L: _lib.call("lmoe_moe_gate_up", P(B.logits), E, 1, k, 1, P(B.xprep), P(B.xprep),
+                                          P(L.wg), P(L.wu), Q, Q, E, H, I, P(B.ids), P(B.scores), P(B.hprep), Q,
+                                          _lib.stream()),
+                      k * 2 * I * (H // 32 * 18) + E * 4 + H // 64 * 144 + k * (I // 64 * 144)),
+        "k_down_combine": (lambda L: _lib.call("lmoe_gemv_down_combine_prepped", P(B.hprep), 0, P(B.ids),
+                                               P(B.scores), 1, k, P(L.wd), Q, E, I, H, None, None, 0, P(x), _lib.F16,
+                                               P(st.ping), _lib.F16, _lib.stream()),
+                           k * H * (I // 32 * 18) + k * (I // 64 * 144) + 3 * H * 2),
+    }
     M = 4 * args.layers
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(M)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(M)]
-    for i in range(M):
-        L = layers[i % args.layers]
-        starts[i].record()
-        _lib.call("lmoe_moe_gate_up", _lib.ptr(B.logits), L.E, 1, L.k, int(L.norm), _lib.ptr(B.xprep),
-                  _lib.ptr(B.xprep), _lib.ptr(L.wg), _lib.ptr(L.wu), Q, Q, L.E, L.H, L.I, _lib.ptr(B.ids),
-                  _lib.ptr(B.scores), _lib.ptr(B.hprep), Q, _lib.stream())
-        ends[i].record()
-    torch.cuda.synchronize()
-    kern_us = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / M * 1e3
-    k, I, H = cfg["k"], cfg["I"], cfg["H"]
-    # algorithmic bytes a launch: k experts x (gate + up) x I rows x H / 32 Q4_0 blocks x 18 B, + the logits row,
-    # the prepared x row and the prepared h rows written
-    kern_bytes = k * 2 * I * (H // 32 * 18) + cfg["E"] * 4 + (H // 64 * 144) + k * (I // 64 * 144)
+    timing = {}
+    for name, (fn, byts) in kernels.items():
+        _lib.call("lmoe_profile_arm", M)
+        for i in range(M):
+            fn(layers[i % args.layers])
+        tot, cnt = ctypes.c_double(), ctypes.c_int()
+        _lib.call("lmoe_profile_read", ctypes.byref(tot), ctypes.byref(cnt))
+        us = tot.value / max(cnt.value, 1) * 1e3
+        timing[name] = dict(us=round(us, 3), bytes=byts, gbps=round(byts / (us * 1e-6) / 1e9, 1))
+    dom = max(timing, key=lambda n: timing[n]["us"])
     token_bytes = args.layers * (workloads.decode_bytes(cfg, k) + 2 * H * 2)
-    return dict(secs=secs, step_ms=step_ms, kern_us=kern_us, kern_bytes=kern_bytes, token_bytes=token_bytes,
-                cfg=cfg, layers=layers)
+    return dict(secs=secs, step_ms=step_ms, timing=timing, dom=dom, token_bytes=token_bytes, cfg=cfg, layers=layers)
 
 
 def cpu_leg(args, g):
@@ -140,7 +150,8 @@ def main():
     g = gpu_leg(args)
     cpu = None if args.no_cpu else cpu_leg(args, g)
     value = args.steps / g["secs"]
-    achieved = g["kern_bytes"] / (g["kern_us"] * 1e-6)
+    dom = g["timing"][g["dom"]]
+    achieved = dom["bytes"] / (dom["us"] * 1e-6)
     out = {
         "metric": "MoE-layer tokens/s (decode, batch 1, 48-layer stack)",
         "value": round(value, 2),
@@ -160,10 +171,10 @@ def main():
                    "intermediate": g["cfg"]["I"], "weights": "Q4_0", "renorm": True, "parallelism": "none"},
         "step_hbm_gbps": round(g["token_bytes"] / (g["step_ms"] * 1e-3) / 1e9, 1),
         "step_hbm_frac": round(g["token_bytes"] / (g["step_ms"] * 1e-3) / HBM_PEAK, 4),
-        "roofline": {"kernel": "lmoe_moe_gate_up (k_gate_up: top-k + gate/up + SwiGLU)", "bound": "hbm",
-                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
-                     "bytes_per_launch": g["kern_bytes"], "us_per_launch": round(g["kern_us"], 3)},
+        "roofline": {"kernel": g["dom"], "bound": "hbm", "achieved": round(achieved / 1e9, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"]},
+        "kernels": g["timing"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -32,6 +32,13 @@ const char *lmoe_error(void);
 /* ABI version, bumped on any signature change. */
 int lmoe_abi_version(void);
 
+/* Kernel-exact timing for benchmarks (no counterpart in the reference): after lmoe_profile_arm(n), the next n
+ * router / gate-up / down kernels this thread launches are each bracketed by a start / stop event pair recorded at
+ * the kernel's own begin and end (hipExtLaunchKernelGGL); lmoe_profile_read waits for them, returns the summed
+ * duration and the count, and disarms. Not for use under graph capture. */
+int lmoe_profile_arm(int max_launches);
+int lmoe_profile_read(double *total_ms, int *count);
+
 /* Router top-k over given logits. Replaces route_cuda.probs (route_cuda.py:280-288; kernel moe_probs
  * route_cuda.py:193-254) and the block's softmax/argpartition/take/renorm ops (stream_fast.py:4352-4370).
  * logits [T][E] in ldtype -> ids [T][k] best first (ties: lowest expert index), scores [T][k] fp32 softmax

@@ -27,6 +27,8 @@ _P, _I, _SZ, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_long
 SIGNATURES = {
     "lmoe_error": (ctypes.c_char_p, []),
     "lmoe_abi_version": (_I, []),
+    "lmoe_profile_arm": (_I, [_I]),
+    "lmoe_profile_read": (_I, [_P, _P]),
     "lmoe_router_topk": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "lmoe_prep_x": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "lmoe_router_gemv": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),

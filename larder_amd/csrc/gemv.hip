@@ -380,7 +380,7 @@ static int launch_gate_up(const GateUpArgs &a, hipStream_t st) {
   LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "lmoe_gemv_gate_up: hidden %d needs %zu bytes of LDS", a.H, lds);
   const dim3 grid((a.I + RB * NW - 1) / (RB * NW), a.n_slots);
   if (int rc = allow_lds(k_gate_up<TG, TU, RB, NC, NW>, lds, "lmoe_gemv_gate_up")) return rc;
-  hipLaunchKernelGGL((k_gate_up<TG, TU, RB, NC, NW>), grid, dim3(64 * NW), lds, st, a.xg_prep, a.xu_prep, a.x,
+  launch(k_gate_up<TG, TU, RB, NC, NW>, grid, dim3(64 * NW), lds, st, a.xg_prep, a.xu_prep, a.x,
                      a.xdt, a.slots, a.topk, a.wg, a.wu, a.n_experts, a.I, a.h, a.hprep, a.td, P, a.logits,
                      a.ld_stride, a.norm, a.ids_out, a.scores_out);
   LMOE_LAUNCHED("lmoe_gemv_gate_up");
@@ -478,7 +478,7 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   auto kern = a.type_d == LMOE_Q4_0 ? (RB == 2 ? k_down_combine<LMOE_Q4_0, 2, NC, NW> : k_down_combine<LMOE_Q4_0, 4, NC, NW>)
                                     : (RB == 2 ? k_down_combine<LMOE_Q4_K, 2, NC, NW> : k_down_combine<LMOE_Q4_K, 4, NC, NW>);
   if (int rc = allow_lds(kern, lds, fn)) return rc;
-  hipLaunchKernelGGL(kern, grid, dim3(64 * NW), lds, st, a.hprep, a.has_sums, a.h, a.ids, a.scores, a.k, a.wd,
+  launch(kern, grid, dim3(64 * NW), lds, st, a.hprep, a.has_sums, a.h, a.ids, a.scores, a.k, a.wd,
                      a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt);
   LMOE_LAUNCHED(fn);
   return 0;

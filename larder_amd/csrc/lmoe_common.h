@@ -17,6 +17,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
 #include <stdint.h>
@@ -55,6 +56,19 @@ inline int allow_lds(K kernel, size_t bytes, const char *what) {
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
   return e == hipSuccess ? 0 : hip_fail(e, what);
+}
+
+// Kernel-exact timing of the library's own launches (lmoe_profile_arm / lmoe_profile_read): while armed, launch()
+// brackets each kernel with a start / stop event pair recorded by the launch itself.
+bool profile_next(hipEvent_t *start, hipEvent_t *stop);
+
+template <typename K, typename... Args>
+inline void launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
+  hipEvent_t a, b;
+  if (profile_next(&a, &b))
+    hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(lds), st, a, b, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
 }
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

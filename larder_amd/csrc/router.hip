@@ -126,9 +126,9 @@ template <int WDT>
 static void launch_router(int qt, dim3 grid, dim3 block, hipStream_t st, const void *x, int xdt, const void *wr,
                           const void *wsg, int T, int H, int E, float *logits, uint32_t *xprep) {
   if (qt == LMOE_Q4_K)
-    hipLaunchKernelGGL((k_router_gemv<WDT, LMOE_Q4_K>), grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+    launch(k_router_gemv<WDT, LMOE_Q4_K>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
   else
-    hipLaunchKernelGGL((k_router_gemv<WDT, LMOE_Q4_0>), grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+    launch(k_router_gemv<WDT, LMOE_Q4_0>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
 }
 
 }  // namespace lmoe
