@@ -68,39 +68,29 @@ def gpu_leg(args):
     secs = e0.elapsed_time(e1) / 1e3
     step_ms = secs / args.steps * 1e3
 
-    # each decode kernel timed kernel-exactly (start / stop events recorded by the launches themselves, the
-    # timestamps rocprofv3 reads) over the layers of the stack in turn, outside the graph, same shapes and inputs
-    B = st.bufs
-    Q = _lib.Q4_0
-    x = xs[0]
-    L0 = layers[0]
+    # each decode kernel timed kernel-exactly: the stack runs eagerly for min(K, 64) more steps with the library's
+    # launch hook armed, so every router / gate-up / down launch is bracketed by start / stop events that the HIP
+    # runtime records at the kernel's own begin and end (the timestamps rocprofv3 reads), on the stream it runs on
     k, I, H, E = cfg["k"], cfg["I"], cfg["H"], cfg["E"]
-    lay.decode(L0, x, B, st.ping, residual=x)
-    torch.cuda.synchronize()
-    P = lambda t: _lib.ptr(t)  # noqa: E731
-    kernels = {
-        "k_router_gemv": (lambda L: _lib.call("lmoe_router_gemv", P(x), _lib.F16, P(L.wr), None, _lib.F16, 1, H, E,
-                                              P(B.logits), P(B.xprep), Q, _lib.stream()),
-                          E * H * 2 + H * 2 + E * 4 + H // 64 * 144),
-        "k_gate_up": (lambda L: _lib.call("lmoe_moe_gate_up", P(B.logits), E, 1, k, 1, P(B.xprep), P(B.xprep),
-                                          P(L.wg), P(L.wu), Q, Q, E, H, I, P(B.ids), P(B.scores), P(B.hprep), Q,
-                                          _lib.stream()),
-                      k * 2 * I * (H // 32 * 18) + E * 4 + H // 64 * 144 + k * (I // 64 * 144)),
-        "k_down_combine": (lambda L: _lib.call("lmoe_gemv_down_combine_prepped", P(B.hprep), 0, P(B.ids),
-                                               P(B.scores), 1, k, P(L.wd), Q, E, I, H, None, None, 0, P(x), _lib.F16,
-                                               P(st.ping), _lib.F16, _lib.stream()),
-                           k * H * (I // 32 * 18) + k * (I // 64 * 144) + 3 * H * 2),
-    }
-    M = 4 * args.layers
+    per_layer = [("k_router_gemv", E * H * 2 + H * 2 + E * 4 + H // 64 * 144),
+                 ("k_gate_up", k * 2 * I * (H // 32 * 18) + E * 4 + H // 64 * 144 + k * (I // 64 * 144)),
+                 ("k_down_combine", k * H * (I // 32 * 18) + k * (I // 64 * 144) + 3 * H * 2)]
+    prof_steps = min(args.steps, 64)
+    M = prof_steps * args.layers * len(per_layer)
+    _lib.call("lmoe_profile_arm", M)
+    for i in range(prof_steps):
+        st.x_in.copy_(xs[args.warmup + i])
+        st.step()
+    ms = (ctypes.c_float * M)()
+    cnt = ctypes.c_int()
+    _lib.call("lmoe_profile_read", ms, M, ctypes.byref(cnt))
+    if cnt.value != M:
+        raise RuntimeError(f"expected {M} timed launches, recorded {cnt.value}")
     timing = {}
-    for name, (fn, byts) in kernels.items():
-        _lib.call("lmoe_profile_arm", M)
-        for i in range(M):
-            fn(layers[i % args.layers])
-        tot, cnt = ctypes.c_double(), ctypes.c_int()
-        _lib.call("lmoe_profile_read", ctypes.byref(tot), ctypes.byref(cnt))
-        us = tot.value / max(cnt.value, 1) * 1e3
-        timing[name] = dict(us=round(us, 3), bytes=byts, gbps=round(byts / (us * 1e-6) / 1e9, 1))
+    for j, (name, byts) in enumerate(per_layer):
+        us = sum(ms[j::len(per_layer)]) / (M // len(per_layer)) * 1e3
+        timing[name] = dict(us=round(us, 3), bytes=byts, gbps=round(byts / (us * 1e-6) / 1e9, 1),
+                            launches=M // len(per_layer))
     dom = max(timing, key=lambda n: timing[n]["us"])
     token_bytes = args.layers * (workloads.decode_bytes(cfg, k) + 2 * H * 2)
     return dict(secs=secs, step_ms=step_ms, timing=timing, dom=dom, token_bytes=token_bytes, cfg=cfg, layers=layers)

@@ -33,11 +33,12 @@ const char *lmoe_error(void);
 int lmoe_abi_version(void);
 
 /* Kernel-exact timing for benchmarks (no counterpart in the reference): after lmoe_profile_arm(n), the next n
- * router / gate-up / down kernels this thread launches are each bracketed by a start / stop event pair recorded at
- * the kernel's own begin and end (hipExtLaunchKernelGGL); lmoe_profile_read waits for them, returns the summed
- * duration and the count, and disarms. Not for use under graph capture. */
+ * kernels this thread launches through the library (router, top-k, gate/up, down, grouping, grouped GEMMs,
+ * combine) are each bracketed by a start / stop event pair recorded at the kernel's own begin and end
+ * (hipExtLaunchKernelGGL); lmoe_profile_read waits for them, writes each launch's duration in launch order into
+ * ms[0 .. min(count, cap)), the number recorded into *count, and disarms. Not for use under graph capture. */
 int lmoe_profile_arm(int max_launches);
-int lmoe_profile_read(double *total_ms, int *count);
+int lmoe_profile_read(float *ms, int cap, int *count);
 
 /* Router top-k over given logits. Replaces route_cuda.probs (route_cuda.py:280-288; kernel moe_probs
  * route_cuda.py:193-254) and the block's softmax/argpartition/take/renorm ops (stream_fast.py:4352-4370).
@@ -119,6 +120,27 @@ int lmoe_group_rows(const uint32_t *ids, int R, int E, int bm, uint32_t *counts,
                     uint32_t *order, uint32_t *inv, uint32_t *tiles, uint32_t *n_tiles, void *ws, void *stream);
 /* Upper bound on the grouped GEMM tiles for R rows over E experts at bm rows a tile. */
 int lmoe_max_tiles(int R, int E, int bm);
+
+/* Rows a grouped-GEMM m-tile covers: the bm that lmoe_group_rows and lmoe_max_tiles take for the grouped GEMMs. */
+int lmoe_grouped_tile_rows(void);
+
+/* Grouped gate/up + SwiGLU on the matrix cores over rows grouped by lmoe_group_rows (bm = lmoe_grouped_tile_rows):
+ *   h[p][f] = silu(x[order[p] / topk] . wg[e][f]) * (x[order[p] / topk] . wu[e][f])  for grouped row p of expert e,
+ * h [R][I] float16 in grouped order (rows past offsets[E] untouched). x [T][H] in xdtype (F16 / BF16 / F32, meets
+ * the weights as f16); wg / wu [E][I][row bytes], one ggml type (Q4_0 or Q4_K); H a multiple of 64 (Q4_K: 256),
+ * I of 64. The work list is read on the device: max_tiles = lmoe_max_tiles(R, E, bm). Replaces the reference's
+ * dense path dequant + gather_mm gate/up + silu-mul (gguf_experts.py:698-720; DEQ_SRC :529-539). */
+int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, const uint32_t *order, const uint32_t *offsets,
+                         const uint32_t *tiles, const uint32_t *n_tiles, int max_tiles, const uint8_t *wg,
+                         const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I, void *h,
+                         void *stream);
+
+/* Grouped down on the matrix cores: y[p][n] = h[p] . wd[e][n] for grouped row p of expert e, y [R][H] in ydtype
+ * (F16 / F32) in grouped order, unweighted. h [R][I] float16 as lmoe_grouped_gate_up leaves it; I a multiple of
+ * 64 (Q4_K: 256), H of 128. Replaces the dense path's gather_mm down (gguf_experts.py:720-721). */
+int lmoe_grouped_down(const void *h, const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
+                      int max_tiles, const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
+                      void *stream);
 
 /* Weighted combine of rows kept in grouped (expert-sorted) order:
  *   out[t][n] = sum_j scores[t][j] * y[inv[t * k + j]][n] (+ sigmoid(gate) * shared) (+ residual)

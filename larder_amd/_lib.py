@@ -28,7 +28,7 @@ SIGNATURES = {
     "lmoe_error": (ctypes.c_char_p, []),
     "lmoe_abi_version": (_I, []),
     "lmoe_profile_arm": (_I, [_I]),
-    "lmoe_profile_read": (_I, [_P, _P]),
+    "lmoe_profile_read": (_I, [_P, _I, _P]),
     "lmoe_router_topk": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "lmoe_prep_x": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "lmoe_router_gemv": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
@@ -42,6 +42,9 @@ SIGNATURES = {
     "lmoe_group_workspace_bytes": (_SZ, [_I, _I]),
     "lmoe_group_rows": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "lmoe_max_tiles": (_I, [_I, _I, _I]),
+    "lmoe_grouped_tile_rows": (_I, []),
+    "lmoe_grouped_gate_up": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
+    "lmoe_grouped_down": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_combine_sorted": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_dequant": (_I, [_P, _I, _I, _I, _I, _P, _I, _P, _I, _P]),
     "lmoe_quantize_q4_0": (_I, [_P, _I, _LL, _I, _P, _P]),

@@ -72,18 +72,17 @@ extern "C" int lmoe_profile_arm(int max_launches) {
   return 0;
 }
 
-extern "C" int lmoe_profile_read(double *total_ms, int *count) {
+extern "C" int lmoe_profile_read(float *ms, int cap, int *count) {
   using namespace lmoe;
   Profile &p = g_prof;
-  double sum = 0.0;
+  LMOE_REQUIRE(cap >= 0 && (ms || cap == 0), LMOE_EINVAL, "lmoe_profile_read: bad buffer");
   for (int i = 0; i < p.used; ++i) {
     hipError_t e = hipEventSynchronize(p.stop[i]);
-    float ms = 0.0f;
-    if (e == hipSuccess) e = hipEventElapsedTime(&ms, p.start[i], p.stop[i]);
+    float t = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, p.start[i], p.stop[i]);
     if (e != hipSuccess) return hip_fail(e, "lmoe_profile_read");
-    sum += ms;
+    if (i < cap) ms[i] = t;
   }
-  if (total_ms) *total_ms = sum;
   if (count) *count = p.used;
   p.armed = 0;
   p.used = 0;

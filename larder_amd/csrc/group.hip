@@ -121,9 +121,9 @@ extern "C" int lmoe_group_rows(const uint32_t *ids, int R, int E, int bm, uint32
   hipStream_t st = (hipStream_t)stream;
   const int nchunk = R > 0 ? (R + kGroupChunk - 1) / kGroupChunk : 1;
   uint32_t *hist = static_cast<uint32_t *>(ws);
-  hipLaunchKernelGGL(k_group_hist, dim3(nchunk), dim3(256), 0, st, ids, R, E, hist);
+  launch(k_group_hist, dim3(nchunk), dim3(256), 0, st, ids, R, E, hist);
   LMOE_LAUNCHED(fn);
-  hipLaunchKernelGGL(k_group_scatter, dim3(nchunk), dim3(256), 0, st, ids, R, E, bm, hist, nchunk, counts, offsets,
+  launch(k_group_scatter, dim3(nchunk), dim3(256), 0, st, ids, R, E, bm, hist, nchunk, counts, offsets,
                      order, inv, tiles, n_tiles);
   LMOE_LAUNCHED(fn);
   return 0;

@@ -112,7 +112,7 @@ extern "C" int lmoe_combine_sorted(const void *y, int ydtype, const uint32_t *in
   LMOE_REQUIRE(!shared == !gate, LMOE_EINVAL, "%s: shared and gate go together", fn);
   if (T == 0) return 0;
   LMOE_REQUIRE(y && inv && out, LMOE_EINVAL, "%s: null pointer", fn);
-  hipLaunchKernelGGL(k_combine_sorted, dim3((H + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y, ydtype, inv,
+  launch(k_combine_sorted, dim3((H + 255) / 256, T), dim3(256), 0, (hipStream_t)stream, y, ydtype, inv,
                      scores, k, H, shared, gate, gate_stride, residual, rdtype, out, odtype);
   LMOE_LAUNCHED(fn);
   return 0;

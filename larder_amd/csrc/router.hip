@@ -145,15 +145,15 @@ static int topk_launch(const void *logits, int ldtype, int stride, int T, int E,
   LMOE_REQUIRE(logits && ids && scores, LMOE_EINVAL, "%s: null pointer", fn);
   const dim3 grid((T + 3) / 4), block(256);
   if (E <= 64)
-    hipLaunchKernelGGL(k_router_topk<1>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<1>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
   else if (E <= 128)
-    hipLaunchKernelGGL(k_router_topk<2>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<2>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
   else if (E <= 256)
-    hipLaunchKernelGGL(k_router_topk<4>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<4>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
   else if (E <= 512)
-    hipLaunchKernelGGL(k_router_topk<8>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<8>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
   else
-    hipLaunchKernelGGL(k_router_topk<16>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<16>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
   LMOE_LAUNCHED(fn);
   return 0;
 }

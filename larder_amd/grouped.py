@@ -1,0 +1,169 @@
+"""The grouped (prefill / batched decode) expert path: device grouping, grouped MFMA GEMMs, weighted combine.
+
+The reference's dense path (gguf_experts.py:698-722) sorts rows by slot on the host (np.argsort / np.unique /
+searchsorted), dequantizes DENSE_CHUNK experts at a time to f16 and runs MLX gather_mm twice, syncing between
+chunks. Here every step stays on the device with no host round trip:
+
+    lmoe_group_rows        ids -> counts, offsets, order, inv, work list (expert, m-tile), its length
+    lmoe_grouped_gate_up   h [R, I] f16 = silu(x . wg) * (x . wu), rows gathered through `order`
+    lmoe_grouped_down      y [R, H] = h . wd, grouped order
+    lmoe_combine_sorted    out [T, H] = sum_j scores[t, j] y[inv[t k + j]] (+ shared) (+ residual)
+
+`expert_rows` mirrors gguf_experts.dense (one slot a row, unweighted rows in the caller's order); `prefill` is a
+whole layer over T tokens from router logits.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import call, dcode, ptr, qcode, stream
+
+
+def tile_rows():
+    """Rows of one grouped-GEMM m-tile (the grouping's bm)."""
+    return _lib.lib().lmoe_grouped_tile_rows()
+
+
+class Grouping:
+    """Device buffers of one grouping of R rows over E experts (allocated once, reusable for any ids of R rows)."""
+
+    def __init__(self, R, E, device="cuda"):
+        self.R, self.E, self.bm = int(R), int(E), tile_rows()
+        self.max_tiles = _lib.lib().lmoe_max_tiles(self.R, self.E, self.bm)
+        i32 = dict(dtype=torch.int32, device=device)
+        self.counts = torch.empty(E, **i32)
+        self.offsets = torch.empty(E + 1, **i32)
+        self.order = torch.empty(max(R, 1), **i32)
+        self.inv = torch.empty(max(R, 1), **i32)
+        self.tiles = torch.empty(max(self.max_tiles, 1), **i32)
+        self.n_tiles = torch.empty(1, **i32)
+        nws = _lib.lib().lmoe_group_workspace_bytes(self.R, self.E)
+        self.ws = torch.empty(max(nws // 4, 1), **i32)
+
+    def run(self, ids):
+        """Group the flat expert ids [R] (int32 / uint32 on the device); ids >= E go after every expert."""
+        if ids.numel() != self.R:
+            raise ValueError(f"grouping holds {self.R} rows, got {ids.numel()} ids")
+        call("lmoe_group_rows", ptr(ids), self.R, self.E, self.bm, ptr(self.counts), ptr(self.offsets),
+             ptr(self.order), ptr(self.inv), ptr(self.tiles), ptr(self.n_tiles), ptr(self.ws), stream())
+        return self
+
+    @classmethod
+    def identity(cls, R, device="cuda"):
+        """All R rows on expert 0 in their own order (a dense FFN, such as the shared expert, on the same kernels);
+        built on the host once."""
+        g = cls.__new__(cls)
+        g.R, g.E, g.bm = int(R), 1, tile_rows()
+        nt = -(-g.R // g.bm)
+        g.max_tiles = nt
+        i32 = dict(dtype=torch.int32)
+        g.counts = torch.tensor([g.R], **i32).to(device)
+        g.offsets = torch.tensor([0, g.R], **i32).to(device)
+        g.order = torch.arange(max(g.R, 1), **i32).to(device)
+        g.inv = g.order
+        g.tiles = torch.arange(max(nt, 1), **i32).to(device)
+        g.n_tiles = torch.tensor([nt], **i32).to(device)
+        g.ws = None
+        return g
+
+
+def gate_up(x, G, topk, wg, wu, types, h):
+    """h [R, I] f16 (grouped order) = silu(x . wg) * (x . wu) over the grouping G of x's rows (row p reads x[order[p]
+    // topk])."""
+    tg, tu = qcode(types[0]), qcode(types[1])
+    T, H = x.shape
+    E, I = wg.shape[0], wg.shape[1]
+    call("lmoe_grouped_gate_up", ptr(x), dcode(x.dtype), T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
+         ptr(G.n_tiles), G.max_tiles, ptr(wg), ptr(wu), tg, tu, E, H, I, ptr(h), stream())
+    return h
+
+
+def down(h, G, wd, t, y):
+    """y [R, H] (f16 / f32, grouped order) = h . wd over the grouping G."""
+    E, H = wd.shape[0], wd.shape[1]
+    I = h.shape[1]
+    call("lmoe_grouped_down", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, ptr(wd), qcode(t),
+         E, I, H, ptr(y), dcode(y.dtype), stream())
+    return y
+
+
+def expert_rows(x, w, host, types, out_dtype):
+    """Every row's expert output, unweighted, in the caller's row order: x [R, H], host [R] slot a row (device or
+    host ints), w = (wg, wu, wd) uint8 experts [S, rows, row bytes]. Rows whose slot is outside 0..S-1 come out
+    zero. The device form of gguf_experts.dense (gguf_experts.py:698-722)."""
+    wg, wu, wd = w
+    R, H = x.shape
+    E, I = wg.shape[0], wg.shape[1]
+    dev = x.device
+    ids = torch.as_tensor(host).reshape(-1).to(device=dev, dtype=torch.int32)
+    G = Grouping(R, E, dev).run(ids)
+    h = torch.empty((R, I), dtype=torch.float16, device=dev)
+    y = torch.empty((R, H), dtype=torch.float16, device=dev)
+    gate_up(x.contiguous(), G, 1, wg, wu, types, h)
+    down(h, G, wd, types[2], y)
+    out = torch.empty((R, H), dtype=out_dtype, device=dev)
+    call("lmoe_combine_sorted", ptr(y), _lib.F16, ptr(G.inv), None, R, 1, H, None, None, 0, None, 0, ptr(out),
+         dcode(out_dtype), stream())
+    bad = (ids < 0) | (ids >= E)
+    return out.masked_fill_(bad[:, None], 0)
+
+
+class PrefillBuffers:
+    """Every intermediate of a prefill pass of T tokens through layers of one shape, allocated once."""
+
+    def __init__(self, layer, T, device="cuda"):
+        L = layer
+        self.T = T
+        R = T * L.k
+        f32 = dict(dtype=torch.float32, device=device)
+        self.logits = torch.empty((T, L.E + (1 if L.shared is not None else 0)), **f32)
+        self.ids = torch.empty((T, L.k), dtype=torch.int32, device=device)
+        self.scores = torch.empty((T, L.k), **f32)
+        self.G = Grouping(R, L.E, device)
+        self.h = torch.empty((R, L.I), dtype=torch.float16, device=device)
+        self.y = torch.empty((R, L.H), dtype=torch.float16, device=device)
+        if L.shared is not None:
+            self.Gs = Grouping.identity(T, device)
+            self.hs = torch.empty((T, L.Is), dtype=torch.float16, device=device)
+            self.ys = torch.empty((T, L.H), **f32)
+
+
+def prefill(layer, x, bufs, out, residual=None, logits=None):
+    """out [T, H] = layer(x) (+ residual) for x [T, H] through the grouped path: router logits (given, or x . Wr as
+    one library GEMM), top-k, device grouping, grouped gate/up + SwiGLU, grouped down, [the shared expert on the
+    same kernels], weighted combine (+ sigmoid-gated shared) (+ residual). No host synchronisation."""
+    L, B = layer, bufs
+    T, H = x.shape
+    st = stream()
+    x = x.contiguous()
+    if logits is None:
+        if L.wr is None:
+            raise ValueError("this layer has no router weight: pass logits")
+        w = L.wr if L.shared is None else torch.cat([L.wr, L.wsg.reshape(1, -1)], 0)
+        torch.matmul(x.float(), w.float().t(), out=B.logits)
+        lg, stride = B.logits, B.logits.shape[1]
+    else:
+        if L.shared is not None:
+            raise ValueError("a shared expert's gate logit comes from the router: use the router weight")
+        lg, stride = logits.to(torch.float32).contiguous(), L.E
+    if stride == L.E:
+        call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
+    else:
+        sel = lg[:, :L.E].contiguous()
+        call("lmoe_router_topk", ptr(sel), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
+    B.G.run(B.ids.reshape(-1))
+    gate_up(x, B.G, L.k, L.wg, L.wu, L.types, B.h)
+    down(B.h, B.G, L.wd, L.types[2], B.y)
+    shared = gate = None
+    if L.shared is not None:
+        sg, su, sd = L.shared
+        gate_up(x, B.Gs, 1, sg, su, L.types, B.hs)
+        down(B.hs, B.Gs, sd, L.types[2], B.ys)
+        shared = ptr(B.ys)
+        gate = ctypes.c_void_p(B.logits.data_ptr() + L.E * B.logits.element_size())
+    call("lmoe_combine_sorted", ptr(B.y), _lib.F16, ptr(B.G.inv), ptr(B.scores), T, L.k, H, shared, gate,
+         stride if shared is not None else 0, ptr(residual), dcode(residual.dtype) if residual is not None else 0,
+         ptr(out), dcode(out.dtype), st)
+    return out
+

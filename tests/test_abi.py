@@ -62,6 +62,26 @@ def test_refusals_without_a_gpu(built_lib):
     assert L.lmoe_max_tiles(65536, 128, 128) == 512 + 128
 
 
+def test_grouped_refusals_without_a_gpu(built_lib):
+    L = built_lib
+    p = ctypes.c_void_p(16)   # never dereferenced: refused during argument checks
+    z = None
+    assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 3, 3, 4, 512, 256, p, z) == _lib.ETYPE
+    assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 2, 12, 4, 512, 256, p, z) == _lib.ETYPE
+    assert b"share one type" in L.lmoe_error()
+    assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 12, 12, 4, 512 + 64, 256, p, z) == _lib.ESHAPE
+    assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256 + 32, p, z) == _lib.ESHAPE
+    assert L.lmoe_grouped_gate_up(p, 9, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, p, z) == _lib.EINVAL
+    assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, z, z) == _lib.EINVAL
+    assert L.lmoe_grouped_gate_up(ctypes.c_void_p(8), 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, p, z) == \
+        _lib.EALIGN
+    assert L.lmoe_grouped_down(p, p, p, p, 4, p, 2, 4, 256, 512 + 64, p, 1, z) == _lib.ESHAPE
+    assert L.lmoe_grouped_down(p, p, p, p, 4, p, 2, 4, 256 + 32, 512, p, 1, z) == _lib.ESHAPE
+    assert L.lmoe_grouped_down(p, p, p, p, 4, p, 2, 4, 256, 512, p, 2, z) == _lib.EINVAL
+    assert L.lmoe_grouped_down(p, p, p, p, 4, p, 5, 4, 256, 512, p, 1, z) == _lib.ETYPE
+    assert L.lmoe_grouped_tile_rows() == 128
+
+
 def test_python_refuses_unsupported_types():
     with pytest.raises(ValueError, match="Q5_K"):
         _lib.qcode("Q5_K")

@@ -1,0 +1,199 @@
+"""GPU parity of the grouped (prefill / batched decode) path against the CPU oracle, through the C ABI.
+
+Bars: expert ids and groupings bit-exact, ties to the lowest expert index; outputs
+within 2e-3 relative L2 of an fp32 dequant-then-matmul (oracle.moe). Every row is also held to a per-row bar, so
+one wrong row or tile cannot hide inside a large tensor."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gguf, moe
+
+pytestmark = pytest.mark.gpu
+
+BAR = 2e-3
+ROW_BAR = 1e-2
+
+_W = {}
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def experts(types, H, I, E, seed):
+    """CPU-quantized experts (gate, up, down), cached across parametrized cases."""
+    key = (types, H, I, E, seed)
+    if key not in _W:
+        rng = np.random.default_rng(seed)
+        _W[key] = tuple(gguf.random_experts(rng, E, r, c, t) for (r, c), t in zip(((I, H), (I, H), (H, I)), types))
+    return _W[key]
+
+
+def ragged_slots(rng, R, E):
+    """One expert takes ~40% of the rows (several m-tiles), one ~10%, experts 1 and 2 none, the rest scattered."""
+    s = rng.integers(3, E, R)
+    s[: int(R * 0.4)] = 0
+    s[int(R * 0.4): int(R * 0.5)] = E - 1
+    return s[rng.permutation(R)].astype(np.int32)
+
+
+def rows_ok(got, want, bar=ROW_BAR):
+    num = np.linalg.norm(got.astype(np.float64) - want, axis=-1)
+    den = np.maximum(np.linalg.norm(want.astype(np.float64), axis=-1), 1e-30)
+    return float((num / den).max())
+
+
+MIXES = [(("Q4_0",) * 3, 2048, 768, 8), (("Q4_K",) * 3, 1024, 512, 6), (("Q4_0",) * 3, 512, 1408, 5),
+         (("Q4_K",) * 3, 4096, 256, 4), (("Q4_0",) * 3, 256, 64, 4)]
+
+
+@pytest.mark.parametrize("types,H,I,E", MIXES)
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.float32])
+def test_expert_rows_vs_oracle(types, H, I, E, xdt):
+    """gguf_experts.dense's contract: each row through its own slot, unweighted, rows in the caller's order."""
+    from larder_amd import grouped
+    w = experts(types, H, I, E, H + I)
+    rng = np.random.default_rng(H * 3 + I)
+    R = 333
+    slots = ragged_slots(rng, R, E)
+    slots[5] = E + 2                                     # no such expert: a zero row
+    x = dev(rng.standard_normal((R, H)).astype(np.float32)).to(xdt)
+    y = grouped.expert_rows(x, tuple(dev(b) for b in w), dev(slots), types, torch.float32)
+    xs = host(x.float().half().float())                  # the kernels meet x as f16
+    _, want = moe.gemv(xs, w, slots, 1, types)
+    got = host(y)
+    assert (got[5] == 0).all()
+    assert moe.rel_l2(got, want) < BAR
+    keep = np.arange(R) != 5
+    assert rows_ok(got[keep], want[keep]) < ROW_BAR
+
+
+@pytest.mark.parametrize("types,H,I,E", MIXES[:2])
+def test_gate_up_h_matches_oracle(types, H, I, E):
+    """h in grouped order against the oracle's h, element by element (f16 output rounding plus f16 weights)."""
+    from larder_amd import grouped
+    w = experts(types, H, I, E, H + I)
+    rng = np.random.default_rng(5)
+    T, k = 70, 3
+    ids = rng.integers(0, E, (T, k)).astype(np.int32)
+    ids[:20] = 0
+    x = dev(rng.standard_normal((T, H)).astype(np.float16))
+    G = grouped.Grouping(T * k, E).run(dev(ids.reshape(-1)))
+    h = torch.empty((T * k, I), dtype=torch.float16, device="cuda")
+    grouped.gate_up(x, G, k, dev(w[0]), dev(w[1]), types, h)
+    order = host(G.order)
+    hw, _ = moe.gemv(host(x.float()), w, ids.reshape(-1), k, types)
+    got = host(h.float())
+    assert moe.rel_l2(got, hw[order]) < BAR
+    assert rows_ok(got, hw[order]) < ROW_BAR
+
+
+def _device_layer(cfg, seed):
+    from larder_amd import workloads
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return workloads.make_layer(cfg, g), g
+
+
+@pytest.mark.parametrize("cfgid,T,xdt", [(2, 300, torch.bfloat16), (4, 64, torch.float16), (2, 1, torch.float16),
+                                         (2, 129, torch.float32)])
+def test_prefill_layer_vs_oracle(cfgid, T, xdt):
+    """A whole layer from given logits (cfg3's skewed draw, cfg4's Zipf prior) with the residual fused."""
+    from larder_amd import grouped, workloads
+    cfg = workloads.CONFIGS[cfgid]
+    L, g = _device_layer(cfg, 7 + T)
+    lg = (workloads.zipf_logits if cfgid == 4 else workloads.skewed_logits)(T, cfg["E"], g)
+    x = torch.randn((T, cfg["H"]), generator=g, device="cuda").to(xdt)
+    B = grouped.PrefillBuffers(L, T)
+    out = torch.empty((T, cfg["H"]), dtype=torch.float32, device="cuda")
+    grouped.prefill(L, x, B, out, residual=x, logits=lg)
+    torch.cuda.synchronize()
+    xs = host(x.float().half().float())
+    ids, scores, want = moe.layer(xs, host(lg), tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"], cfg["k"],
+                                  cfg["norm"], residual=host(x.float()))
+    assert (host(B.ids).astype(np.uint32) == ids).all()
+    assert np.allclose(host(B.scores), scores, rtol=2e-6, atol=1e-7)
+    xr = host(x.float())
+    assert moe.rel_l2(host(out) - xr, want - xr) < BAR
+    assert rows_ok(host(out) - xr, want - xr) < ROW_BAR
+
+
+def test_prefill_layer_cfg1_shared_expert():
+    """Config 1's layer (E 60, top-4 without renorm, I 1408, shared 5632 + sigmoid gate) with router logits from
+    the router weight."""
+    from larder_amd import grouped, workloads
+    cfg = workloads.CONFIGS[1]
+    L, g = _device_layer(cfg, 3)
+    T = 150
+    x = torch.randn((T, cfg["H"]), generator=g, device="cuda").half()
+    B = grouped.PrefillBuffers(L, T)
+    out = torch.empty((T, cfg["H"]), dtype=torch.float32, device="cuda")
+    grouped.prefill(L, x, B, out)
+    torch.cuda.synchronize()
+    xs = host(x.float())
+    lg = host(B.logits)
+    assert moe.rel_l2(lg[:, :cfg["E"]], xs @ host(L.wr.float()).T) < 1e-5
+    ids, _, want = moe.layer(xs, lg[:, :cfg["E"]], tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"],
+                             cfg["k"], cfg["norm"], shared=tuple(host(b[0]) for b in L.shared),
+                             shared_gate_w=host(L.wsg.float()))
+    assert (host(B.ids).astype(np.uint32) == ids).all()
+    assert moe.rel_l2(host(out), want) < BAR
+    assert rows_ok(host(out), want) < ROW_BAR
+
+
+def test_prefill_matches_decode_chain():
+    """The grouped path and the decode chain (separately checked against the oracle) agree on the same tokens."""
+    from larder_amd import grouped, layer as lay, workloads
+    cfg = workloads.CONFIGS[2]
+    L, g = _device_layer(cfg, 11)
+    T = 16
+    x = torch.randn((T, cfg["H"]), generator=g, device="cuda").half()
+    lg = workloads.skewed_logits(T, cfg["E"], g)
+    out_g = torch.empty((T, cfg["H"]), dtype=torch.float32, device="cuda")
+    out_d = torch.empty_like(out_g)
+    B = grouped.PrefillBuffers(L, T)
+    grouped.prefill(L, x, B, out_g, logits=lg)
+    D = lay.DecodeBuffers(L, T)
+    lay.decode(L, x, D, out_d, logits=lg)
+    torch.cuda.synchronize()
+    assert torch.equal(B.ids, D.ids)
+    assert moe.rel_l2(host(out_g), host(out_d)) < BAR
+
+
+def test_prefill_cfg3_full_size():
+    """Config 3 at its full size (8192 bf16 tokens, top-8 of 128, skewed logits): ids and grouping bit-exact for all
+    65,536 rows, and 48 sampled tokens against the oracle (tokens are independent, so the sample is exact)."""
+    from larder_amd import grouped, workloads
+    cfg = workloads.CONFIGS[3]
+    L, g = _device_layer(cfg, 0)
+    T, E, k = cfg["T"], cfg["E"], cfg["k"]
+    lg = workloads.skewed_logits(T, E, g)
+    x = torch.randn((T, cfg["H"]), generator=g, device="cuda").bfloat16()
+    B = grouped.PrefillBuffers(L, T)
+    out = torch.empty((T, cfg["H"]), dtype=torch.bfloat16, device="cuda")
+    grouped.prefill(L, x, B, out, logits=lg)
+    torch.cuda.synchronize()
+    lgh = host(lg)
+    ids, _ = moe.router(lgh, k, cfg["norm"])
+    assert (host(B.ids).astype(np.uint32) == ids).all()
+    c, o, od, iv = moe.group_rows(ids.reshape(-1), E)
+    assert (host(B.G.offsets).astype(np.uint32) == o).all()
+    assert (host(B.G.order).astype(np.uint32) == od).all()
+    assert (host(B.G.inv).astype(np.uint32) == iv).all()
+    rng = np.random.default_rng(0)
+    sample = np.sort(rng.choice(T, 48, replace=False))
+    sample[0] = 0
+    sample[-1] = T - 1
+    xs = host(x.float())[sample]
+    _, _, want = moe.layer(xs, lgh[sample], tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"], k,
+                           cfg["norm"])
+    got = host(out.float())[sample]
+    # the bf16 output rounding (2^-9 relative) dominates here
+    assert moe.rel_l2(got, want) < 4e-3
+    assert rows_ok(got, want) < ROW_BAR
+    assert np.isfinite(host(out.float())).all()
+
