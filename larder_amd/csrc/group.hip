@@ -2,100 +2,143 @@
 //
 // The reference groups on the host: mx.argsort of the flat ids and its inverse (stream_fast.py:5466-5471), then
 // np.unique / searchsorted between units (gguf_experts.py:702-713; stream_fast.py:92-122), with an mx.eval sync
-// each layer. Here two kernels do it on the device with no host round trip:
-//   1. k_group_hist: each workgroup histograms one chunk of CH rows into LDS and writes its counts;
-//   2. k_group_scatter: each workgroup derives its chunk's start in every bucket from the counts of the chunks
-//      before it (so the sort is stable across chunks), then one wavefront walks its chunk 64 rows at a time,
-//      ranking equal ids inside a group of 64 by ballot, so rows keep flat order within an expert.
-// Workgroup 0 also writes counts, offsets and the grouped GEMM's work list.
+// each layer. Here three kernels do it on the device with no host round trip, for R rows in chunks of 256:
+//   1. k_group_count: each workgroup histograms its chunk in LDS and writes the counts bucket-major,
+//      hist[bucket][chunk];
+//   2. k_group_scan: one workgroup a bucket turns its row of hist into the exclusive prefix over chunks (the
+//      bucket's rows in earlier chunks) and writes the bucket total;
+//   3. k_group_scatter: each workgroup scans the totals into bucket offsets, and every row goes to
+//      offset[bucket] + rows of its bucket in earlier chunks + rows of its bucket earlier in its own chunk (found
+//      by comparing against the chunk's keys in LDS), so rows keep flat order within an expert. Workgroup 0 also
+//      writes counts, offsets and the grouped GEMM's work list.
+// Bucket E collects ids >= E, which therefore sort after every expert.
 #include "lmoe_common.h"
 
 namespace lmoe {
 
-constexpr int kGroupChunk = 512;
+constexpr int kGroupChunk = 256;
 constexpr int kGroupMaxE = 1024;
 
-__global__ void __launch_bounds__(256) k_group_hist(const uint32_t *ids, int R, int E, uint32_t *hist) {
+// exclusive prefix sum of v over the 256 threads of the block; *total gets the sum. tmp: 4 words of LDS.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *tmp, uint32_t *total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  uint32_t base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t t = tmp[w];
+    base += w < wave ? t : 0u;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return base + x - v;
+}
+
+__global__ void __launch_bounds__(256) k_group_count(const uint32_t *ids, int R, int E, int nchunk,
+                                                      uint32_t *hist) {
   __shared__ uint32_t cnt[kGroupMaxE + 1];
   for (int e = threadIdx.x; e <= E; e += 256) cnt[e] = 0;
   __syncthreads();
-  const int r0 = blockIdx.x * kGroupChunk, r1 = min(R, r0 + kGroupChunk);
-  for (int r = r0 + threadIdx.x; r < r1; r += 256) {
+  const int r = blockIdx.x * kGroupChunk + threadIdx.x;
+  if (r < R) {
     const uint32_t v = ids[r];
     atomicAdd(&cnt[v < uint32_t(E) ? v : uint32_t(E)], 1u);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e <= E; e += 256) hist[size_t(blockIdx.x) * (E + 1) + e] = cnt[e];
+  for (int e = threadIdx.x; e <= E; e += 256) hist[size_t(e) * nchunk + blockIdx.x] = cnt[e];
+}
+
+// grid E + 1: bucket blockIdx.x
+__global__ void __launch_bounds__(256) k_group_scan(int nchunk, uint32_t *hist, uint32_t *totals) {
+  __shared__ uint32_t tmp[4];
+  uint32_t *row = hist + size_t(blockIdx.x) * nchunk;
+  uint32_t carry = 0;
+  for (int c0 = 0; c0 < nchunk; c0 += 256) {
+    const int c = c0 + threadIdx.x;
+    const uint32_t v = c < nchunk ? row[c] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_exclusive_scan(v, tmp, &tot);
+    if (c < nchunk) row[c] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
 __global__ void __launch_bounds__(256)
-    k_group_scatter(const uint32_t *ids, int R, int E, int bm, const uint32_t *hist, int nchunk, uint32_t *counts,
-                    uint32_t *offsets, uint32_t *order, uint32_t *inv, uint32_t *tiles, uint32_t *n_tiles) {
-  __shared__ uint32_t base[kGroupMaxE + 1];
-  __shared__ uint32_t tot[kGroupMaxE + 1];
-  const int c = blockIdx.x;
-  // per bucket: rows in all chunks (tot) and rows in chunks before this one (base)
-  for (int e = threadIdx.x; e <= E; e += 256) {
-    uint32_t before = 0, all = 0;
-    for (int j = 0; j < nchunk; ++j) {
-      const uint32_t v = hist[size_t(j) * (E + 1) + e];
-      all += v;
-      before += j < c ? v : 0u;
+    k_group_scatter(const uint32_t *ids, int R, int E, int bm, const uint32_t *hist, const uint32_t *totals,
+                    int nchunk, uint32_t *counts, uint32_t *offsets, uint32_t *order, uint32_t *inv, uint32_t *tiles,
+                    uint32_t *n_tiles) {
+  __shared__ uint32_t off[kGroupMaxE + 1];
+  __shared__ uint32_t keys[kGroupChunk];
+  __shared__ uint32_t tmp[4];
+  const int c = blockIdx.x, tid = threadIdx.x;
+  // bucket offsets: exclusive scan of the totals, 4 consecutive buckets a thread (E + 1 <= 1025 < 1028)
+  {
+    uint32_t t[4], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * tid + i;
+      t[i] = e <= E ? totals[e] : 0u;
+      sum += t[i];
     }
-    tot[e] = all;
-    base[e] = before;
+    uint32_t tot;
+    uint32_t run = block_exclusive_scan(sum, tmp, &tot);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * tid + i;
+      if (e <= E) off[e] = run;
+      run += t[i];
+    }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {  // exclusive scan over buckets (E + 1 of them: the last holds ids >= E)
-    uint32_t run = 0;
-    for (int e = 0; e <= E; ++e) {
-      const uint32_t v = tot[e];
-      tot[e] = run;
-      run += v;
-    }
+  if (E == kGroupMaxE) {  // the 1025th bucket (ids >= 1024) falls outside the 4-a-thread scan
+    if (tid == 0) off[kGroupMaxE] = off[kGroupMaxE - 1] + totals[kGroupMaxE - 1];
+    __syncthreads();
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e <= E; e += 256) base[e] += tot[e];
   if (c == 0) {
-    for (int e = threadIdx.x; e < E; e += 256) counts[e] = tot[e + 1] - tot[e];
-    for (int e = threadIdx.x; e <= E; e += 256) offsets[e] = tot[e];
-    if (threadIdx.x == 0 && tiles) {
-      uint32_t nt = 0;
-      for (int e = 0; e < E; ++e) {
-        const uint32_t n = tot[e + 1] - tot[e];
-        for (uint32_t m = 0; m * uint32_t(bm) < n; ++m) tiles[nt++] = (uint32_t(e) << 20) | m;
+    for (int e = tid; e < E; e += 256) counts[e] = totals[e];
+    for (int e = tid; e <= E; e += 256) offsets[e] = off[e];
+    if (tiles) {  // the work list: each expert's m-tiles in order, experts ascending
+      const int per = (E + 255) / 256;  // experts a thread: tid * per ..
+      uint32_t nt[4] = {0, 0, 0, 0}, sum = 0;
+      for (int i = 0; i < per; ++i) {
+        const int e = tid * per + i;
+        nt[i] = e < E ? (totals[e] + uint32_t(bm) - 1) / uint32_t(bm) : 0u;
+        sum += nt[i];
       }
-      *n_tiles = nt;
+      uint32_t tot;
+      uint32_t run = block_exclusive_scan(sum, tmp, &tot);
+      for (int i = 0; i < per; ++i) {
+        const int e = tid * per + i;
+        for (uint32_t m = 0; m < nt[i]; ++m) tiles[run + m] = (uint32_t(e) << 20) | m;
+        run += nt[i];
+      }
+      if (tid == 0) *n_tiles = tot;
     }
   }
+  const int r = c * kGroupChunk + tid;
+  const bool act = r < R;
+  uint32_t key = uint32_t(E);
+  if (act) {
+    const uint32_t v = ids[r];
+    key = v < uint32_t(E) ? v : uint32_t(E);
+  }
+  keys[tid] = act ? key : 0xFFFFFFFFu;
   __syncthreads();
-  if (threadIdx.x >= 64) return;
-  const int lane = threadIdx.x;
-  const int r0 = c * kGroupChunk, r1 = min(R, r0 + kGroupChunk);
-  for (int g = r0; g < r1; g += 64) {
-    const int r = g + lane;
-    const bool act = r < r1;
-    const uint32_t v = act ? ids[r] : 0u;
-    const uint32_t key = v < uint32_t(E) ? v : uint32_t(E);
-    uint64_t pending = __ballot(act);
-    uint32_t pos = 0;
-    while (pending) {
-      const int leader = __ffsll((unsigned long long)pending) - 1;
-      const uint32_t k0 = __shfl(key, leader, 64);
-      const uint64_t same = __ballot(act && key == k0);
-      if (act && key == k0) {
-        const uint64_t below = same & ((uint64_t(1) << lane) - 1);
-        pos = base[k0] + __popcll(below);
-      }
-      if (lane == leader) base[k0] += __popcll(same);
-      pending &= ~same;
-      __builtin_amdgcn_wave_barrier();
-    }
-    if (act) {
-      order[pos] = uint32_t(r);
-      inv[r] = pos;
-    }
-  }
+  if (!act) return;
+  uint32_t rank = 0;  // rows of this bucket earlier in the chunk
+  for (int j = 0; j < tid; ++j) rank += keys[j] == key ? 1u : 0u;
+  const uint32_t pos = off[key] + hist[size_t(key) * nchunk + c] + rank;
+  order[pos] = uint32_t(r);
+  inv[r] = pos;
 }
 
 }  // namespace lmoe
@@ -104,7 +147,7 @@ using namespace lmoe;
 
 extern "C" size_t lmoe_group_workspace_bytes(int R, int E) {
   const size_t nchunk = (size_t(R > 0 ? R : 1) + kGroupChunk - 1) / kGroupChunk;
-  return nchunk * size_t(E + 1) * 4;
+  return (nchunk + 1) * size_t(E + 1) * 4;
 }
 
 extern "C" int lmoe_max_tiles(int R, int E, int bm) { return bm > 0 ? (R + bm - 1) / bm + E : 0; }
@@ -121,10 +164,13 @@ extern "C" int lmoe_group_rows(const uint32_t *ids, int R, int E, int bm, uint32
   hipStream_t st = (hipStream_t)stream;
   const int nchunk = R > 0 ? (R + kGroupChunk - 1) / kGroupChunk : 1;
   uint32_t *hist = static_cast<uint32_t *>(ws);
-  launch(k_group_hist, dim3(nchunk), dim3(256), 0, st, ids, R, E, hist);
+  uint32_t *totals = hist + size_t(nchunk) * (E + 1);
+  launch(k_group_count, dim3(nchunk), dim3(256), 0, st, ids, R, E, nchunk, hist);
   LMOE_LAUNCHED(fn);
-  launch(k_group_scatter, dim3(nchunk), dim3(256), 0, st, ids, R, E, bm, hist, nchunk, counts, offsets,
-                     order, inv, tiles, n_tiles);
+  launch(k_group_scan, dim3(E + 1), dim3(256), 0, st, nchunk, hist, totals);
+  LMOE_LAUNCHED(fn);
+  launch(k_group_scatter, dim3(nchunk), dim3(256), 0, st, ids, R, E, bm, static_cast<const uint32_t *>(hist),
+         static_cast<const uint32_t *>(totals), nchunk, counts, offsets, order, inv, tiles, n_tiles);
   LMOE_LAUNCHED(fn);
   return 0;
 }

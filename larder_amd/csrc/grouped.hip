@@ -8,16 +8,21 @@
 //     for the most tiles R rows can make and workgroups past the device-side count exit at once. Workgroups are
 //     dealt round-robin over the 8 XCDs, so the linear id is remapped to give each XCD one contiguous stretch of
 //     work (neighbouring n-tiles of one m-tile share A rows and the expert's weights in that XCD's L2);
-//   * each K step of 64 stages an A tile of 128 rows (gate/up: rows of x gathered through the grouped order and
-//     converted to f16; down: the grouped h rows) and a W tile of 128 weight rows decoded from Q4_0 / Q4_K to f16
-//     ((q - 8) d, d sc q - dmin m) into LDS, double-buffered: the next step's global loads are in flight while the
-//     current step's MFMAs run;
-//   * four wavefronts each own a 64 x 64 corner (4 x 4 accumulators of 16 x 16). The weights are the MFMA's first
-//     operand, so each lane ends with 4 consecutive output features of one row and stores 8 bytes;
-//   * gate/up tiles hold 64 gate and 64 up rows of the same intermediate features: SwiGLU happens in registers and
-//     h leaves as f16 in grouped row order. Down writes y [R][H] f16 in grouped order for lmoe_combine_sorted.
+//   * each K step of 64 stages an A tile of 128 rows (gate/up: rows of x, already f16, gathered through the
+//     grouped order; down: the grouped h rows) and a W tile of 128 weight rows decoded from Q4_0 / Q4_K to f16
+//     ((q - 8) d, d sc q - dmin m) into LDS, double-buffered, 16-byte chunks XOR-swizzled by row so that both the
+//     staging writes and the MFMA fragment reads are free of bank conflicts. Each thread moves 64 contiguous bytes
+//     of one A row a step, so the row gather costs few address transactions; global loads run two steps ahead
+//     of the MFMAs that use them;
+//   * four wavefronts each own a 64 x 64 corner (4 x 4 accumulators of 16 x 16, in VGPRs; two workgroups a CU,
+//     so two waves share each SIMD and cover each other's waits). The weights are the MFMA's first operand, so
+//     each lane ends with 4 consecutive output features of one row;
+//   * gate/up tiles hold 64 gate and 64 up rows of the same intermediate features: SwiGLU happens in registers
+//     and h leaves as f16 in grouped row order. Down writes y [R][H] (f16 or f32) in grouped order.
 // Operands are f16 with fp32 accumulation. A single rounding of (q - 8) d to f16 keeps the layer well inside the
 // 2e-3 relative L2 bar; bf16 operands would not.
+#include <type_traits>
+
 #include "lmoe_common.h"
 
 namespace lmoe {
@@ -26,22 +31,27 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int GM = 128;       // rows a tile (the grouping kernel's bm)
-constexpr int GN = 128;       // output columns a tile (gate/up: 64 gate + 64 up features)
-constexpr int GK = 64;        // K a step
-constexpr int LDA = GK + 8;   // halves a staged row: the 16-byte pad spreads 16-byte lane reads over all banks
+constexpr int GM = 128;  // rows a tile (the grouping kernel's bm)
+constexpr int GN = 256;  // weight rows a tile (gate/up: 128 gate + 128 up features; down: 256 outputs)
+constexpr int GK = 64;   // K a step
+constexpr int kThreads = 512;
 constexpr int kTileMask = (1 << 20) - 1;
 
 enum { MODE_GATE_UP = 0, MODE_DOWN = 1 };
 
-// four f16 (1024 + q) from the low nibbles of a byte-wise masked word: {q0, q1} and {q2, q3}
+template <int N>
+using IC = std::integral_constant<int, N>;
+
+// 16-byte chunk c (0..7) of W row r in a stage: rows are 128 bytes, chunks XOR-swizzled by the row's low 3 bits
+__device__ __forceinline__ int wchunk(int r, int c) { return r * 8 + (c ^ (r & 7)); }
+
+// four f16 (1024 + q) from a byte-wise masked word: {q0, q1} and {q2, q3}
 __device__ __forceinline__ uint32_t magic_pair(uint32_t nib, uint32_t sel) {
   return __builtin_amdgcn_perm(0x64646464u, nib, sel);
 }
 constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
 
-// 8 f16 weights (one lane's LDS quadword) from the 4 nibbles of `nib` (already masked to one nibble a byte):
-// values (1024 + q - bias) * scale - sub, written as pairs in natural order
+// 4 f16 weights from the 4 nibbles of `nib` (one nibble a byte): ((1024 + q) - bias) * scale - sub, as 2 pairs
 __device__ __forceinline__ void decode4(uint32_t nib, h2_t bias, h2_t scale, h2_t sub, uint32_t *o) {
   const h2_t a = __builtin_bit_cast(h2_t, magic_pair(nib, kSel01));
   const h2_t b = __builtin_bit_cast(h2_t, magic_pair(nib, kSel23));
@@ -49,53 +59,93 @@ __device__ __forceinline__ void decode4(uint32_t nib, h2_t bias, h2_t scale, h2_
   o[1] = __builtin_bit_cast(uint32_t, (b - bias) * scale - sub);
 }
 
-// Q4_0 block (f16 d, 16 qs words) -> 32 f16 (q - 8) d in natural order, as 16 words
-__device__ __forceinline__ void dequant_q4_0_block(const uint32_t qs[4], float d, uint32_t o[16]) {
-  const _Float16 dh = _Float16(d);
-  const h2_t bias = {_Float16(1032.0f), _Float16(1032.0f)}, scale = {dh, dh}, zero = {_Float16(0.0f), _Float16(0.0f)};
+// Raw words a thread loads for one (weight row, part) of a K step
+template <int TB>
+struct Raw {
+  static constexpr int N = TB == LMOE_Q4_0 ? 5 : 12;
+};
+
+// Load the raw words of (row `wrow`, part h) for K step kk. Q4_0: block h of unit kk is words 4h .. 4h + 4 of
+// the 36-byte unit. Q4_K: super-block kk / 4 header words 0..3 and the 8 qs words of sub-block pair kk % 4.
+template <int TB>
+__device__ __forceinline__ void load_raw(const uint8_t *wrow, int h, int kk, uint32_t *r) {
+  if (TB == LMOE_Q4_0) {
+    const uint32_t *u = reinterpret_cast<const uint32_t *>(wrow + size_t(kk) * 36) + 4 * h;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    decode4(qs[i] & 0x0F0F0F0Fu, bias, scale, zero, o + 2 * i);             // elements 4i .. 4i + 3
-    decode4((qs[i] >> 4) & 0x0F0F0F0Fu, bias, scale, zero, o + 8 + 2 * i);  // elements 16 + 4i ..
-  }
-}
-
-// Q4_K: 16 consecutive qs bytes of one sub-block pair -> 16 f16 of sub-block lo (low nibbles, scale d1 / min m1)
-// and 16 of sub-block hi (high nibbles, d2 / m2): d sc q - dmin m, scale and min rounded to f16 first
-__device__ __forceinline__ void dequant_q4_k_half(const uint32_t qs[4], float d1, float m1, float d2, float m2,
-                                                  uint32_t lo[8], uint32_t hi[8]) {
-  const h2_t bias = {_Float16(1024.0f), _Float16(1024.0f)};
-  const h2_t s1 = {_Float16(d1), _Float16(d1)}, n1 = {_Float16(m1), _Float16(m1)};
-  const h2_t s2 = {_Float16(d2), _Float16(d2)}, n2 = {_Float16(m2), _Float16(m2)};
+    for (int i = 0; i < 5; ++i) r[i] = u[i];
+  } else {
+    const uint32_t *sb = reinterpret_cast<const uint32_t *>(wrow + size_t(kk >> 2) * 144);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    decode4(qs[i] & 0x0F0F0F0Fu, bias, s1, n1, lo + 2 * i);
-    decode4((qs[i] >> 4) & 0x0F0F0F0Fu, bias, s2, n2, hi + 2 * i);
+    for (int i = 0; i < 4; ++i) r[i] = sb[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[4 + i] = sb[4 + 8 * (kk & 3) + i];
   }
 }
 
-// x elements -> f16 pairs
-template <int ADT>
-__device__ __forceinline__ uint32_t to_f16_pair(uint32_t a, uint32_t b) {
-  if (ADT == LMOE_BF16) {  // bf16 pair in one word; exact in f16 over f16's normal range
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(a << 16),
-                                                                 __uint_as_float(a & 0xFFFF0000u)));
-  } else {  // two f32 words, rounded to nearest
-    const h2_t v = {_Float16(__uint_as_float(a)), _Float16(__uint_as_float(b))};
-    return __builtin_bit_cast(uint32_t, v);
+// Decoding one (row, part h) of K step kk to 32 f16 weights = chunks 4h .. 4h + 3 of the row, one 16-byte chunk
+// (8 weights) at a time so the work can sit between MFMAs. Q4_0 part h is block h: elements 0..15 from the low
+// nibbles of qs bytes 0..15, 16..31 from the high ones; w = ((1024 + q) - 1032) d. Q4_K part h is sub-block
+// 2 (kk % 4) + h, the low (h = 0) or high (h = 1) nibbles of the pair's 32 qs bytes; w = (q (d sc)) - dmin m.
+struct Dq {
+  h2_t bias, scale, sub;
+};
+
+template <int TB>
+__device__ __forceinline__ Dq dq_params(const uint32_t *r, int h, int kk) {
+  Dq q;
+  if (TB == LMOE_Q4_0) {
+    const _Float16 dh = _Float16(h == 0 ? half_lo(r[0]) : half_hi(r[0]));  // d of block 0 / block 1
+    q.bias = h2_t{_Float16(1032.0f), _Float16(1032.0f)};
+    q.scale = h2_t{dh, dh};
+    q.sub = h2_t{_Float16(0.0f), _Float16(0.0f)};
+  } else {
+    float sc, mn;
+    k4_scale_min(r[1], r[2], r[3], 2 * (kk & 3) + h, &sc, &mn);
+    const _Float16 d1 = _Float16(half_lo(r[0]) * sc), m1 = _Float16(half_hi(r[0]) * mn);
+    q.bias = h2_t{_Float16(1024.0f), _Float16(1024.0f)};
+    q.scale = h2_t{d1, d1};
+    q.sub = h2_t{m1, m1};
   }
+  return q;
 }
 
-// Grid: n_ntile * max_tiles workgroups of 256 threads (1-D). GATE_UP: n-tile j covers intermediate features
-// 64 j .. 64 j + 63 (gate rows in W rows 0..63 of the tile, up rows in 64..127), K = H, A rows x[order[p] / topk],
-// out h [R][I] f16. DOWN: n-tile j covers output features 128 j .., K = I, A rows h[p], out y [R][H] f16.
-template <int MODE, int TB, int ADT>
-__global__ void __launch_bounds__(256, 2)
-    k_grouped(const void *a_src, int topk, const uint32_t *order, const uint32_t *offsets, const uint32_t *tiles,
-              const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1, int K, int n_rows,
-              void *out, int ldo, int odt) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][GM * LDA];
-  __shared__ __attribute__((aligned(16))) _Float16 Ws[2][GN * LDA];
+// chunk j (0..3) of (row, part h): weights 8 j .. 8 j + 7 of the part
+template <int TB>
+__device__ __forceinline__ u32x4 dq_chunk(const uint32_t *r, int h, const Dq &q, int j) {
+  uint32_t w0, w1, o[4];
+  int shift;
+  if (TB == LMOE_Q4_0) {  // qs words (2j, 2j + 1) mod 4, low nibbles for j < 2, high for j >= 2
+    const int i = 2 * (j & 1);
+    if (h == 0) {  // block 0's qs start at byte 2
+      w0 = __builtin_amdgcn_alignbyte(r[i + 1], r[i], 2);
+      w1 = __builtin_amdgcn_alignbyte(r[i + 2], r[i + 1], 2);
+    } else {  // block 1's qs are words 5..8 (r[1..4])
+      w0 = r[i + 1];
+      w1 = r[i + 2];
+    }
+    shift = j < 2 ? 0 : 4;
+  } else {  // qs words 2j, 2j + 1 of the pair, nibble h
+    w0 = r[4 + 2 * j];
+    w1 = r[5 + 2 * j];
+    shift = 4 * h;
+  }
+  decode4((w0 >> shift) & 0x0F0F0F0Fu, q.bias, q.scale, q.sub, o);
+  decode4((w1 >> shift) & 0x0F0F0F0Fu, q.bias, q.scale, q.sub, o + 2);
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// Grid: n_ntile * max_tiles workgroups of 512 threads (1-D), one a CU, two waves a SIMD. GATE_UP: n-tile j
+// covers intermediate features 128 j .. 128 j + 127 (W rows 0..127 of the tile are their gate rows, 128..255
+// their up rows), K = H, A rows x[order[p] / topk], out h [R][I] f16. DOWN: n-tile j covers output features
+// 256 j .., K = I, A rows h[p], out y [R][H] in odt (F16 / F32).
+template <int MODE, int TB>
+__global__ void __launch_bounds__(kThreads, 1)
+k_grouped(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets, const uint32_t *tiles,
+          const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1, int K, int n_rows, void *out,
+          int ldo, int odt) {
+  // A and W tiles, 2 stages each: rows of 64 halves = 8 chunks of 16 bytes, chunks swizzled by wchunk()
+  __shared__ __attribute__((aligned(16))) u32x4 As[2][GM * 8];
+  __shared__ __attribute__((aligned(16))) u32x4 Ws[2][GN * 8];
 
   // XCD-aware remap: workgroup `wid` runs on XCD wid % 8; XCD x gets logical work [start_x, start_x + count_x)
   const uint32_t W = n_tiles[0] * uint32_t(n_ntile);
@@ -110,188 +160,153 @@ __global__ void __launch_bounds__(256, 2)
   const int rows = min(GM, int(offsets[e + 1]) - row0);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int P = K / 64;  // 64-weight units a weight row
-  const size_t wrow_bytes = size_t(36) * P;
+  const int wm = wave & 1, wn = wave >> 1;  // 2 x 4 waves of 64 x 64
+  const int fr = lane & 15, g = lane >> 4;
+  const size_t wrow_bytes = size_t(36) * (K / 64);
 
-  // A staging: thread -> row am of the tile, 32 elements from k offset ak of each step
-  constexpr int AES = ADT == LMOE_F32 ? 4 : 2;  // bytes an element
-  constexpr int AV = 32 * AES / 16;              // 16-byte loads a step
-  const int am = tid >> 1, ak = (tid & 1) * 32;
-  const bool a_ok = am < rows;
-  const u32x4 *a_ptr = nullptr;
-  if (a_ok) {
-    const int p = row0 + am;
+  // A staging: thread -> tile row ar = tid >> 2, chunks 2 ac, 2 ac + 1 (32 contiguous bytes of the step).
+  // Rows past the tile's end read the tile's first row instead (their results are never stored).
+  const int ar = tid >> 2, ac = tid & 3;
+  const u32x4 *a_ptr;
+  {
+    const int p = row0 + (ar < rows ? ar : 0);
     const size_t r = MODE == MODE_GATE_UP ? size_t(order[p] / uint32_t(topk)) : size_t(p);
-    a_ptr = reinterpret_cast<const u32x4 *>(static_cast<const char *>(a_src) + (r * K + ak) * AES);
+    a_ptr = reinterpret_cast<const u32x4 *>(a_src + r * K + 16 * ac);
   }
-  // W staging: thread -> weight row wn of the tile, part wp (Q4_0: block wp of the unit; Q4_K: qs bytes 16 wp ..)
-  const int wn = tid >> 1, wp = tid & 1;
+  // W staging: thread -> tile row sr = tid >> 1, part sh = tid & 1 (Q4_0 block / Q4_K sub-block sh = chunks
+  // 4 sh .. 4 sh + 3)
+  const int sr = tid >> 1, sh = tid & 1;
   const uint8_t *w_row;
   if (MODE == MODE_GATE_UP)
-    w_row = (wn < 64 ? w0 : w1) + (size_t(e) * n_rows + nt * 64 + (wn & 63)) * wrow_bytes;
+    w_row = (sr < GN / 2 ? w0 : w1) + (size_t(e) * n_rows + nt * (GN / 2) + (sr % (GN / 2))) * wrow_bytes;
   else
-    w_row = w0 + (size_t(e) * n_rows + nt * GN + wn) * wrow_bytes;
+    w_row = w0 + (size_t(e) * n_rows + nt * GN + sr) * wrow_bytes;
 
-  u32x4 areg[AV];
-  uint32_t wreg[TB == LMOE_Q4_0 ? 5 : 8];
-  auto load = [&](int kk) {
-    if (a_ok) {
-#pragma unroll
-      for (int i = 0; i < AV; ++i) areg[i] = a_ptr[size_t(kk) * (GK * AES / 16) + i];
-    }
-    if (TB == LMOE_Q4_0) {  // block wp of unit kk: words 4 wp .. 4 wp + 4 of the 36-byte unit
-      const uint32_t *u = reinterpret_cast<const uint32_t *>(w_row + size_t(kk) * 36) + 4 * wp;
-#pragma unroll
-      for (int i = 0; i < 5; ++i) wreg[i] = u[i];
-    } else {  // superblock kk / 4, sub-block pair kk % 4: header words 0..3, qs words 4 + 8 (kk % 4) + 4 wp ..
-      const uint32_t *sb = reinterpret_cast<const uint32_t *>(w_row + size_t(kk >> 2) * 144);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wreg[i] = sb[i];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wreg[4 + i] = sb[4 + 8 * (kk & 3) + 4 * wp + i];
-    }
-  };
-  auto store = [&](int buf, int kk) {
-    if (a_ok) {
-      u32x4 *ad = reinterpret_cast<u32x4 *>(&As[buf][am * LDA + ak]);
-      if (ADT == LMOE_F16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ad[i] = areg[i];
-      } else if (ADT == LMOE_BF16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          ad[i] = u32x4{to_f16_pair<ADT>(areg[i].x, 0), to_f16_pair<ADT>(areg[i].y, 0),
-                        to_f16_pair<ADT>(areg[i].z, 0), to_f16_pair<ADT>(areg[i].w, 0)};
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          ad[i] = u32x4{to_f16_pair<ADT>(areg[2 * i].x, areg[2 * i].y), to_f16_pair<ADT>(areg[2 * i].z, areg[2 * i].w),
-                        to_f16_pair<ADT>(areg[2 * i + 1].x, areg[2 * i + 1].y),
-                        to_f16_pair<ADT>(areg[2 * i + 1].z, areg[2 * i + 1].w)};
-      }
-    }
-    if (TB == LMOE_Q4_0) {
-      uint32_t qs[4], o[16];
-      float d;
-      if (wp == 0) {  // block 0 starts at byte 0: d in the low half of word 0, qs at bytes 2..17
-        d = half_lo(wreg[0]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qs[i] = __builtin_amdgcn_alignbyte(wreg[i + 1], wreg[i], 2);
-      } else {  // block 1 starts at byte 18: d in the high half of word 4, qs in words 5..8
-        d = half_hi(wreg[0]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qs[i] = wreg[i + 1];
-      }
-      dequant_q4_0_block(qs, d, o);
-      u32x4 *wd = reinterpret_cast<u32x4 *>(&Ws[buf][wn * LDA + 32 * wp]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wd[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
-    } else {
-      const int c = kk & 3;
-      float sc1, mn1, sc2, mn2;
-      k4_scale_min(wreg[1], wreg[2], wreg[3], 2 * c, &sc1, &mn1);
-      k4_scale_min(wreg[1], wreg[2], wreg[3], 2 * c + 1, &sc2, &mn2);
-      const float d = half_lo(wreg[0]), dmin = half_hi(wreg[0]);
-      uint32_t lo[8], hi[8];
-      dequant_q4_k_half(wreg + 4, d * sc1, dmin * mn1, d * sc2, dmin * mn2, lo, hi);
-      u32x4 *wl = reinterpret_cast<u32x4 *>(&Ws[buf][wn * LDA + 16 * wp]);       // k = 16 wp + j
-      u32x4 *wh = reinterpret_cast<u32x4 *>(&Ws[buf][wn * LDA + 32 + 16 * wp]);  // k = 32 + 16 wp + j
-      wl[0] = u32x4{lo[0], lo[1], lo[2], lo[3]};
-      wl[1] = u32x4{lo[4], lo[5], lo[6], lo[7]};
-      wh[0] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-      wh[1] = u32x4{hi[4], hi[5], hi[6], hi[7]};
-    }
-  };
-
-  // wavefront corner: token rows 64 wm .. (A rows of the tile), weight rows per jn (gate/up: 32 gate rows
-  // 32 wv .. and the 32 up rows 64 + 32 wv .. of the same features; down: 64 wv ..)
-  const int wm = wave >> 1, wv = wave & 1;
+  // fragment rows of W this wave reads: gate/up: gate rows 32 wn + 16 nb (nb < 2) and the up rows GN/2 + 32 wn +
+  // 16 (nb - 2) of the same features; down: 64 wn + 16 nb
   int wbase[4];
 #pragma unroll
-  for (int jn = 0; jn < 4; ++jn)
-    wbase[jn] = MODE == MODE_GATE_UP ? (jn < 2 ? 32 * wv + 16 * jn : 64 + 32 * wv + 16 * (jn - 2)) : 64 * wv + 16 * jn;
-  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  for (int nb = 0; nb < 4; ++nb)
+    wbase[nb] =
+        MODE == MODE_GATE_UP ? (nb < 2 ? 32 * wn + 16 * nb : GN / 2 + 32 * wn + 16 * (nb - 2)) : 64 * wn + 16 * nb;
 
+  u32x4 areg[2][2];
+  uint32_t wraw[2][Raw<TB>::N];
   f32x4 acc[4][4];
 #pragma unroll
-  for (int jn = 0; jn < 4; ++jn)
+  for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-    for (int im = 0; im < 4; ++im) acc[jn][im] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  auto load = [&](auto s, int kk) {  // raw W, then A, of step kk into register stage s
+    constexpr int S = decltype(s)::value;
+    load_raw<TB>(w_row, sh, kk, wraw[S]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) areg[S][i] = a_ptr[size_t(kk) * (GK / 8) + i];
+  };
+  auto stage = [&](auto s, auto l, int kk) {  // register stage s -> LDS stage l
+    constexpr int S = decltype(s)::value, L = decltype(l)::value;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) As[L][wchunk(ar, 2 * ac + j)] = areg[S][j];
+    const Dq q = dq_params<TB>(wraw[S], sh, kk);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Ws[L][wchunk(sr, 4 * sh + j)] = dq_chunk<TB>(wraw[S], sh, q, j);
+  };
   const int nk = K / GK;
-  load(0);
-  store(0, 0);
-  __syncthreads();
-  for (int kk = 0; kk < nk; ++kk) {
-    const int cur = kk & 1;
-    if (kk + 1 < nk) load(kk + 1);
+  // Step kk: the global loads of step kk + 2 are issued into the register stage that step kk's data left (it went
+  // to LDS at the end of step kk - 1); step kk multiplies out of LDS stage kk % 2 while step kk + 1 (loaded during
+  // step kk - 1) is staged into the other LDS stage, its A chunks and decoded W chunks written between groups of
+  // 4 MFMAs so that a wave keeps the matrix core, the VALU and the LDS busy at once (the waves of a workgroup run
+  // in lockstep between barriers, so the overlap has to come from within each wave); one barrier closes the step.
+  // Past the end the step index clamps instead of branching, so the compiler's memory-counter waits stay exact.
+  auto step = [&](auto sl, int kk) {
+    constexpr int SL = decltype(sl)::value, SN = 1 - SL;
+    load(IC<SL>{}, min(kk + 2, nk - 1));
+    const int kn = min(kk + 1, nk - 1);
+    const Dq q = dq_params<TB>(wraw[SN], sh, kn);
+    half8 wf[2][4], xf[2][4];
 #pragma unroll
-    for (int ks = 0; ks < GK; ks += 32) {
-      half8 wf[4], xf[4];
+    for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-      for (int jn = 0; jn < 4; ++jn)
-        wf[jn] = *reinterpret_cast<const half8 *>(&Ws[cur][(wbase[jn] + fr) * LDA + ks + fk]);
+      for (int nb = 0; nb < 4; ++nb)
+        wf[ks][nb] = __builtin_bit_cast(half8, Ws[SL][wchunk(wbase[nb] + fr, 2 * g + ks)]);
 #pragma unroll
-      for (int im = 0; im < 4; ++im)
-        xf[im] = *reinterpret_cast<const half8 *>(&As[cur][(64 * wm + 16 * im + fr) * LDA + ks + fk]);
-#pragma unroll
-      for (int jn = 0; jn < 4; ++jn)
-#pragma unroll
-        for (int im = 0; im < 4; ++im)
-          acc[jn][im] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[jn], xf[im], acc[jn][im], 0, 0, 0);
+      for (int mb = 0; mb < 4; ++mb)
+        xf[ks][mb] = __builtin_bit_cast(half8, As[SL][wchunk(64 * wm + 16 * mb + fr, 2 * g + ks)]);
     }
-    if (kk + 1 < nk) store(cur ^ 1, kk + 1);
-    __syncthreads();
-  }
-
-  // acc[jn][im][r] = D[weight row wbase[jn] + 4 (lane / 16) + r][token row 64 wm + 16 im + lane % 16]
-  const int orow = 4 * (lane >> 4);
 #pragma unroll
-  for (int im = 0; im < 4; ++im) {
-    const int m = 64 * wm + 16 * im + fr;
+    for (int grp = 0; grp < 8; ++grp) {
+      const int ks = grp >> 2, mb = grp & 3;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[ks][nb], xf[ks][mb], acc[nb][mb], 0, 0, 0);
+      if (grp == 0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) As[SN][wchunk(ar, 2 * ac + j)] = areg[SN][j];
+      } else if (grp <= 4) {
+        Ws[SN][wchunk(sr, 4 * sh + grp - 1)] = dq_chunk<TB>(wraw[SN], sh, q, grp - 1);
+      }
+    }
+    __syncthreads();
+  };
+
+  load(IC<0>{}, 0);
+  load(IC<1>{}, min(1, nk - 1));
+  stage(IC<0>{}, IC<0>{}, 0);
+  __syncthreads();
+  int kk = 0;
+  for (; kk + 1 < nk; kk += 2) {
+    step(IC<0>{}, kk);
+    step(IC<1>{}, kk + 1);
+  }
+  if (kk < nk) step(IC<0>{}, kk);
+
+  // acc[nb][mb][r] = D[W row wbase[nb] + 4 g + r][token row 64 wm + 16 mb + fr]
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int m = 64 * wm + 16 * mb + fr;
     if (m >= rows) continue;
     const size_t o = size_t(row0 + m) * ldo;
     if (MODE == MODE_GATE_UP) {
 #pragma unroll
-      for (int jn = 0; jn < 2; ++jn) {
-        h2_t v01 = {_Float16(silu_mul(acc[jn][im][0], acc[jn + 2][im][0])),
-                    _Float16(silu_mul(acc[jn][im][1], acc[jn + 2][im][1]))};
-        h2_t v23 = {_Float16(silu_mul(acc[jn][im][2], acc[jn + 2][im][2])),
-                    _Float16(silu_mul(acc[jn][im][3], acc[jn + 2][im][3]))};
-        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + nt * 64 + wbase[jn] + orow) =
+      for (int nb = 0; nb < 2; ++nb) {
+        h2_t v01 = {_Float16(silu_mul(acc[nb][mb][0], acc[nb + 2][mb][0])),
+                    _Float16(silu_mul(acc[nb][mb][1], acc[nb + 2][mb][1]))};
+        h2_t v23 = {_Float16(silu_mul(acc[nb][mb][2], acc[nb + 2][mb][2])),
+                    _Float16(silu_mul(acc[nb][mb][3], acc[nb + 2][mb][3]))};
+        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + nt * (GN / 2) + wbase[nb] + 4 * g) =
             u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
       }
     } else if (odt == LMOE_F32) {
 #pragma unroll
-      for (int jn = 0; jn < 4; ++jn)
-        *reinterpret_cast<f32x4 *>(static_cast<float *>(out) + o + nt * GN + wbase[jn] + orow) = acc[jn][im];
+      for (int nb = 0; nb < 4; ++nb)
+        *reinterpret_cast<f32x4 *>(static_cast<float *>(out) + o + nt * GN + wbase[nb] + 4 * g) = acc[nb][mb];
     } else {
 #pragma unroll
-      for (int jn = 0; jn < 4; ++jn) {
-        h2_t v01 = {_Float16(acc[jn][im][0]), _Float16(acc[jn][im][1])};
-        h2_t v23 = {_Float16(acc[jn][im][2]), _Float16(acc[jn][im][3])};
-        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + nt * GN + wbase[jn] + orow) =
+      for (int nb = 0; nb < 4; ++nb) {
+        h2_t v01 = {_Float16(acc[nb][mb][0]), _Float16(acc[nb][mb][1])};
+        h2_t v23 = {_Float16(acc[nb][mb][2]), _Float16(acc[nb][mb][3])};
+        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + nt * GN + wbase[nb] + 4 * g) =
             u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
       }
     }
   }
 }
 
-template <int MODE, int TB>
-static void grouped_launch(int adt, int grid, hipStream_t st, const void *a, int topk, const uint32_t *order,
-                           const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile,
-                           const uint8_t *w0, const uint8_t *w1, int K, int n_rows, void *out, int ldo, int odt) {
-  if (MODE == MODE_DOWN || adt == LMOE_F16)
-    launch(k_grouped<MODE, TB, LMOE_F16>, dim3(grid), dim3(256), 0, st, a, topk, order, offsets, tiles, n_tiles,
-           n_ntile, w0, w1, K, n_rows, out, ldo, odt);
-  else if constexpr (MODE == MODE_GATE_UP) {
-    if (adt == LMOE_BF16)
-      launch(k_grouped<MODE, TB, LMOE_BF16>, dim3(grid), dim3(256), 0, st, a, topk, order, offsets, tiles, n_tiles,
-           n_ntile, w0, w1, K, n_rows, out, ldo, odt);
-    else
-      launch(k_grouped<MODE, TB, LMOE_F32>, dim3(grid), dim3(256), 0, st, a, topk, order, offsets, tiles, n_tiles,
-             n_ntile, w0, w1, K, n_rows, out, ldo, odt);
+// x [n] in dt -> f16 (round to nearest even), 8 elements a thread (vector loads when the whole range allows)
+__global__ void __launch_bounds__(256) k_to_f16(const void *x, int dt, long long n, _Float16 *out, int vec) {
+  const long long i0 = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (i0 >= n) return;
+  if (vec) {
+    float v[8];
+    load8(x, size_t(i0), dt, v);
+    store8(out, size_t(i0), LMOE_F16, v);
+    return;
   }
+  const int cnt = int(min(8ll, n - i0));
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < cnt) out[i0 + i] = _Float16(load_elt(x, size_t(i0 + i), dt));
 }
 
 }  // namespace lmoe
@@ -299,6 +314,21 @@ static void grouped_launch(int adt, int grid, hipStream_t st, const void *a, int
 using namespace lmoe;
 
 extern "C" int lmoe_grouped_tile_rows(void) { return GM; }
+
+extern "C" int lmoe_to_f16(const void *x, int xdtype, long long n, void *out, void *stream) {
+  const char *fn = "lmoe_to_f16";
+  LMOE_REQUIRE(dtype_ok(xdtype), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(n >= 0, LMOE_ESHAPE, "%s: negative length", fn);
+  if (n == 0) return 0;
+  LMOE_REQUIRE(x && out, LMOE_EINVAL, "%s: null pointer", fn);
+  const long long blocks = (n + 2047) / 2048;
+  LMOE_REQUIRE(blocks < (1ll << 31), LMOE_ESHAPE, "%s: %lld elements", fn, n);
+  const int vec = n % 8 == 0 && aligned16(x) && aligned16(out);
+  launch(k_to_f16, dim3(unsigned(blocks)), dim3(256), 0, (hipStream_t)stream, x, xdtype, n,
+         static_cast<_Float16 *>(out), vec);
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
 
 extern "C" int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, const uint32_t *order,
                                     const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
@@ -309,25 +339,28 @@ extern "C" int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, 
                "%s: ggml types %d/%d are not supported (Q4_0 = 2, Q4_K = 12)", fn, type_g, type_u);
   LMOE_REQUIRE(type_g == type_u, LMOE_ETYPE, "%s: gate and up must share one type on this path (%d vs %d)", fn,
                type_g, type_u);
-  LMOE_REQUIRE(dtype_ok(xdtype), LMOE_EINVAL, "%s: bad x dtype", fn);
+  LMOE_REQUIRE(xdtype == LMOE_F16, LMOE_EINVAL,
+               "%s: x must be float16 here (convert once with lmoe_to_f16; the matrix cores read f16)", fn);
   LMOE_REQUIRE(T >= 0 && topk > 0 && n_experts > 0 && max_tiles >= 0, LMOE_ESHAPE, "%s: bad shape", fn);
   LMOE_REQUIRE(H > 0 && H % block_weights(type_g) == 0 && H % 64 == 0, LMOE_ESHAPE,
                "%s: hidden size %d is not a multiple of %d", fn, H, type_g == LMOE_Q4_K ? 256 : 64);
-  LMOE_REQUIRE(I > 0 && I % 64 == 0, LMOE_ESHAPE, "%s: intermediate size %d is not a multiple of 64", fn, I);
+  LMOE_REQUIRE(I > 0 && I % (GN / 2) == 0, LMOE_ESHAPE, "%s: intermediate size %d is not a multiple of %d", fn, I,
+               GN / 2);
   if (T == 0 || max_tiles == 0) return 0;
   LMOE_REQUIRE(x && order && offsets && tiles && n_tiles && wg && wu && h, LMOE_EINVAL, "%s: null pointer", fn);
   LMOE_REQUIRE(aligned16(x) && aligned16(h) && aligned4(wg) && aligned4(wu), LMOE_EALIGN,
                "%s: x and h must be 16-byte aligned, weights 4-byte aligned", fn);
-  const int n_ntile = I / 64;
+  const int n_ntile = I / (GN / 2);
   const long long grid = (long long)n_ntile * max_tiles;
   LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
   hipStream_t st = (hipStream_t)stream;
+  const _Float16 *a = static_cast<const _Float16 *>(x);
   if (type_g == LMOE_Q4_0)
-    grouped_launch<MODE_GATE_UP, LMOE_Q4_0>(xdtype, int(grid), st, x, topk, order, offsets, tiles, n_tiles, n_ntile,
-                                            wg, wu, H, I, h, I, LMOE_F16);
+    launch(k_grouped<MODE_GATE_UP, LMOE_Q4_0>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets,
+           tiles, n_tiles, n_ntile, wg, wu, H, I, h, I, int(LMOE_F16));
   else
-    grouped_launch<MODE_GATE_UP, LMOE_Q4_K>(xdtype, int(grid), st, x, topk, order, offsets, tiles, n_tiles, n_ntile,
-                                            wg, wu, H, I, h, I, LMOE_F16);
+    launch(k_grouped<MODE_GATE_UP, LMOE_Q4_K>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets,
+           tiles, n_tiles, n_ntile, wg, wu, H, I, h, I, int(LMOE_F16));
   LMOE_LAUNCHED(fn);
   return 0;
 }
@@ -350,12 +383,15 @@ extern "C" int lmoe_grouped_down(const void *h, const uint32_t *offsets, const u
   const long long grid = (long long)n_ntile * max_tiles;
   LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
   hipStream_t st = (hipStream_t)stream;
+  const _Float16 *a = static_cast<const _Float16 *>(h);
   if (type_d == LMOE_Q4_0)
-    grouped_launch<MODE_DOWN, LMOE_Q4_0>(LMOE_F16, int(grid), st, h, 1, nullptr, offsets, tiles, n_tiles, n_ntile, wd,
-                                         nullptr, I, H, y, H, ydtype);
+    launch(k_grouped<MODE_DOWN, LMOE_Q4_0>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1,
+           static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile, wd,
+           static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
   else
-    grouped_launch<MODE_DOWN, LMOE_Q4_K>(LMOE_F16, int(grid), st, h, 1, nullptr, offsets, tiles, n_tiles, n_ntile, wd,
-                                         nullptr, I, H, y, H, ydtype);
+    launch(k_grouped<MODE_DOWN, LMOE_Q4_K>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1,
+           static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile, wd,
+           static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
   LMOE_LAUNCHED(fn);
   return 0;
 }

@@ -104,6 +104,48 @@ __device__ __forceinline__ void store_elt(void *p, size_t i, float v, int dt) {
     static_cast<uint16_t *>(p)[i] = f32_to_bf16(v);
 }
 
+// 8 consecutive elements at index i (16-byte aligned) as floats, and back
+__device__ __forceinline__ void load8(const void *p, size_t i, int dt, float *v) {
+  if (dt == LMOE_F32) {
+    const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
+    const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+    const u32x4 w = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(p) + i);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (dt == LMOE_F16) {
+        const h2_t hv = __builtin_bit_cast(h2_t, ws[j]);
+        v[2 * j] = float(hv[0]);
+        v[2 * j + 1] = float(hv[1]);
+      } else {
+        v[2 * j] = __uint_as_float(ws[j] << 16);
+        v[2 * j + 1] = __uint_as_float(ws[j] & 0xFFFF0000u);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void store8(void *p, size_t i, int dt, const float *v) {
+  if (dt == LMOE_F32) {
+    *reinterpret_cast<float4 *>(static_cast<float *>(p) + i) = float4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<float4 *>(static_cast<float *>(p) + i + 4) = float4{v[4], v[5], v[6], v[7]};
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (dt == LMOE_F16) {
+        const h2_t h = {_Float16(v[2 * j]), _Float16(v[2 * j + 1])};
+        w[j] = __builtin_bit_cast(uint32_t, h);
+      } else {
+        w[j] = uint32_t(f32_to_bf16(v[2 * j])) | (uint32_t(f32_to_bf16(v[2 * j + 1])) << 16);
+      }
+    }
+    *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(p) + i) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
 __device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + __expf(-v)); }
 
 // silu(g) * u; the exponential only ever sees -|g|, so it never overflows

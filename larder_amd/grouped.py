@@ -68,13 +68,26 @@ class Grouping:
         return g
 
 
-def gate_up(x, G, topk, wg, wu, types, h):
+def as_f16(x, out=None):
+    """x as a contiguous float16 tensor: x itself when it already is one, else converted on the device (into
+    ``out`` when given)."""
+    x = x.contiguous()
+    if x.dtype == torch.float16:
+        return x
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    call("lmoe_to_f16", ptr(x), dcode(x.dtype), x.numel(), ptr(out), stream())
+    return out
+
+
+def gate_up(x, G, topk, wg, wu, types, h, xh=None):
     """h [R, I] f16 (grouped order) = silu(x . wg) * (x . wu) over the grouping G of x's rows (row p reads x[order[p]
-    // topk])."""
+    // topk]); x meets the weights as f16 (converted into ``xh`` when it is not)."""
     tg, tu = qcode(types[0]), qcode(types[1])
+    x = as_f16(x, xh)
     T, H = x.shape
     E, I = wg.shape[0], wg.shape[1]
-    call("lmoe_grouped_gate_up", ptr(x), dcode(x.dtype), T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
+    call("lmoe_grouped_gate_up", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
          ptr(G.n_tiles), G.max_tiles, ptr(wg), ptr(wu), tg, tu, E, H, I, ptr(h), stream())
     return h
 
@@ -121,6 +134,7 @@ class PrefillBuffers:
         self.ids = torch.empty((T, L.k), dtype=torch.int32, device=device)
         self.scores = torch.empty((T, L.k), **f32)
         self.G = Grouping(R, L.E, device)
+        self.xh = torch.empty((T, L.H), dtype=torch.float16, device=device)
         self.h = torch.empty((R, L.I), dtype=torch.float16, device=device)
         self.y = torch.empty((R, L.H), dtype=torch.float16, device=device)
         if L.shared is not None:
@@ -153,12 +167,13 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
         sel = lg[:, :L.E].contiguous()
         call("lmoe_router_topk", ptr(sel), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
     B.G.run(B.ids.reshape(-1))
-    gate_up(x, B.G, L.k, L.wg, L.wu, L.types, B.h)
+    xh = as_f16(x, B.xh)
+    gate_up(xh, B.G, L.k, L.wg, L.wu, L.types, B.h)
     down(B.h, B.G, L.wd, L.types[2], B.y)
     shared = gate = None
     if L.shared is not None:
         sg, su, sd = L.shared
-        gate_up(x, B.Gs, 1, sg, su, L.types, B.hs)
+        gate_up(xh, B.Gs, 1, sg, su, L.types, B.hs)
         down(B.hs, B.Gs, sd, L.types[2], B.ys)
         shared = ptr(B.ys)
         gate = ctypes.c_void_p(B.logits.data_ptr() + L.E * B.logits.element_size())

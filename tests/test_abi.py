@@ -72,6 +72,9 @@ def test_grouped_refusals_without_a_gpu(built_lib):
     assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 12, 12, 4, 512 + 64, 256, p, z) == _lib.ESHAPE
     assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256 + 32, p, z) == _lib.ESHAPE
     assert L.lmoe_grouped_gate_up(p, 9, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, p, z) == _lib.EINVAL
+    assert L.lmoe_grouped_gate_up(p, 2, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, p, z) == _lib.EINVAL
+    assert b"lmoe_to_f16" in L.lmoe_error()
+    assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 576, 200, p, z) == _lib.ESHAPE
     assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, z, z) == _lib.EINVAL
     assert L.lmoe_grouped_gate_up(ctypes.c_void_p(8), 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, p, z) == \
         _lib.EALIGN
@@ -79,6 +82,9 @@ def test_grouped_refusals_without_a_gpu(built_lib):
     assert L.lmoe_grouped_down(p, p, p, p, 4, p, 2, 4, 256 + 32, 512, p, 1, z) == _lib.ESHAPE
     assert L.lmoe_grouped_down(p, p, p, p, 4, p, 2, 4, 256, 512, p, 2, z) == _lib.EINVAL
     assert L.lmoe_grouped_down(p, p, p, p, 4, p, 5, 4, 256, 512, p, 1, z) == _lib.ETYPE
+    assert L.lmoe_grouped_down(p, p, p, p, 4, p, 2, 4, 320, 600, p, 1, z) == _lib.ESHAPE
+    assert L.lmoe_to_f16(p, 7, 10, p, z) == _lib.EINVAL
+    assert L.lmoe_to_f16(p, 0, -1, p, z) == _lib.ESHAPE
     assert L.lmoe_grouped_tile_rows() == 128
 
 

@@ -49,7 +49,7 @@ def rows_ok(got, want, bar=ROW_BAR):
 
 
 MIXES = [(("Q4_0",) * 3, 2048, 768, 8), (("Q4_K",) * 3, 1024, 512, 6), (("Q4_0",) * 3, 512, 1408, 5),
-         (("Q4_K",) * 3, 4096, 256, 4), (("Q4_0",) * 3, 256, 64, 4)]
+         (("Q4_K",) * 3, 4096, 256, 4), (("Q4_0",) * 3, 256, 128, 4)]
 
 
 @pytest.mark.parametrize("types,H,I,E", MIXES)
