@@ -21,6 +21,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK = 8.0e12  # MI355X published HBM3E bandwidth, bytes/s
+MFMA_PEAK = 2.5e15  # MI355X dense f16 / bf16 matrix peak, flop/s
+# HBM bytes a launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled by a 256 MiB copy) at the cfg2 shape,
+# per kernel; see profiles/decode_cfg2_traffic.md for the commands. Reported as roofline.traffic for that kernel.
+MEASURED_TRAFFIC = {"k_down_combine": 7753318, "k_gate_up": 14439938, "k_router_gemv": 808960}
 
 
 def parse():
@@ -31,6 +35,10 @@ def parse():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-grouped", action="store_true", help="skip the cfg3 prefill / cfg4 batched lines")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run a plain device copy of this many MiB (the scale for rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -96,6 +104,107 @@ def gpu_leg(args):
     return dict(secs=secs, step_ms=step_ms, timing=timing, dom=dom, token_bytes=token_bytes, cfg=cfg, layers=layers)
 
 
+def grouped_leg():
+    """The grouped path's own configurations, reported beside the decode line:
+    cfg3 = one 8192-token bf16 prefill chunk through one cfg-2 layer with skewed router logits (MFMA roofline over
+    the routed experts' 2 R 3 H I flops); cfg4 = 512 steps of 64 tokens with a fresh Zipf-prior draw each step
+    (HBM roofline over the unique experts touched)."""
+    import ctypes
+
+    import torch
+
+    from larder_amd import _lib, grouped, workloads
+
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(3)
+    cfg = workloads.CONFIGS[3]
+    T = cfg["T"]
+    L = workloads.make_layer(cfg, g, with_router=False)
+    lg = workloads.skewed_logits(T, cfg["E"], g)
+    x = torch.randn((T, cfg["H"]), generator=g, device="cuda").bfloat16()
+    B = grouped.PrefillBuffers(L, T)
+    y = torch.empty((T, cfg["H"]), dtype=torch.bfloat16, device="cuda")
+    for _ in range(3):
+        grouped.prefill(L, x, B, y, logits=lg)
+    torch.cuda.synchronize()
+    n = 20
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        grouped.prefill(L, x, B, y, logits=lg)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / n * 1e3
+    flops = workloads.expert_flops(cfg, T * cfg["k"])
+    # per-kernel, kernel-exact, over 5 more passes (8 launches a pass: top-k, 3 grouping, f16 copy, gate/up,
+    # down, combine)
+    names = ["k_router_topk", "k_group_count", "k_group_scan", "k_group_scatter", "k_to_f16", "k_grouped<gate_up>",
+             "k_grouped<down>", "k_combine_sorted"]
+    M = 5 * len(names)
+    _lib.call("lmoe_profile_arm", M)
+    for _ in range(5):
+        grouped.prefill(L, x, B, y, logits=lg)
+    ms = (ctypes.c_float * M)()
+    cnt = ctypes.c_int()
+    _lib.call("lmoe_profile_read", ms, M, ctypes.byref(cnt))
+    kern = {nm: round(sum(ms[j:cnt.value:len(names)]) / 5 * 1e3, 2) for j, nm in enumerate(names)}
+    R = T * cfg["k"]
+    gu, dn = 2 * R * 2 * cfg["H"] * cfg["I"], 2 * R * cfg["H"] * cfg["I"]
+    out["cfg3_prefill"] = {
+        "us_per_chunk": round(us, 1), "tokens_per_s": round(T / (us * 1e-6), 1),
+        "mfma_frac": round(flops / (us * 1e-6) / MFMA_PEAK, 4), "flops": flops,
+        "kernels_us": kern,
+        "gate_up_mfma_frac": round(gu / (kern["k_grouped<gate_up>"] * 1e-6) / MFMA_PEAK, 4),
+        "down_mfma_frac": round(dn / (kern["k_grouped<down>"] * 1e-6) / MFMA_PEAK, 4),
+        "rows_per_expert_max": int(B.G.counts.max().item()), "experts_empty": int((B.G.counts == 0).sum().item())}
+    del B, x, y, lg
+    # cfg4: 64 sequences x 1 token a step, 512 steps, a fresh draw of logits and x each step
+    cfg4 = workloads.CONFIGS[4]
+    T4, steps = cfg4["T"], 512
+    lgs = [workloads.zipf_logits(T4, cfg4["E"], g) for _ in range(steps)]
+    xs = torch.randn((steps, T4, cfg4["H"]), generator=g, device="cuda").half()
+    B4 = grouped.PrefillBuffers(L, T4)
+    y4 = torch.empty((T4, cfg4["H"]), dtype=torch.float16, device="cuda")
+    x4 = xs[0].clone()
+    lg4 = lgs[0].clone()
+    # one step as a HIP graph over static input buffers (a serving loop would capture it the same way)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        grouped.prefill(L, x4, B4, y4, logits=lg4)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        grouped.prefill(L, x4, B4, y4, logits=lg4)
+    for i in range(8):
+        x4.copy_(xs[i])
+        lg4.copy_(lgs[i])
+        graph.replay()
+    uniq = 0
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(steps):
+        x4.copy_(xs[i])
+        lg4.copy_(lgs[i])
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us4 = e0.elapsed_time(e1) / steps * 1e3
+    for i in range(0, steps, 64):  # unique experts a step (for the HBM roofline), sampled
+        x4.copy_(xs[i])
+        lg4.copy_(lgs[i])
+        graph.replay()
+        uniq += int((B4.G.counts > 0).sum().item())
+    uniq /= len(range(0, steps, 64))
+    byts = uniq * (2 * cfg4["I"] * workloads.row_bytes("Q4_0", cfg4["H"]) +
+                   cfg4["H"] * workloads.row_bytes("Q4_0", cfg4["I"])) + T4 * cfg4["H"] * 2 * 2
+    out["cfg4_batched"] = {"us_per_step": round(us4, 1), "tokens_per_s": round(T4 / (us4 * 1e-6), 1),
+                           "note": "one HIP graph a step; input copies of x and logits inside the timed loop",
+                           "unique_experts_per_step": round(uniq, 1),
+                           "hbm_frac": round(byts / (us4 * 1e-6) / HBM_PEAK, 4)}
+    return out
+
+
 def cpu_leg(args, g):
     """The C++ restatement of the reference CPU kernel (cpu_kern gather_qmm) over the same experts, converted to
     its affine 4-bit layout, run layer after layer for about --cpu-seconds; tokens/s = 1 / (48 x mean layer time)."""
@@ -137,8 +246,17 @@ def main():
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for {args.gpus})", file=sys.stderr)
         sys.exit(2)
     os.environ.setdefault("HSA_ENABLE_IPC_MODE_LEGACY", "0")
+    if args.copy_probe_mib:
+        import torch
+        src = torch.empty(args.copy_probe_mib << 18, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     g = gpu_leg(args)
     cpu = None if args.no_cpu else cpu_leg(args, g)
+    secondary = None if args.no_grouped else grouped_leg()
     value = args.steps / g["secs"]
     dom = g["timing"][g["dom"]]
     achieved = dom["bytes"] / (dom["us"] * 1e-6)
@@ -162,10 +280,13 @@ def main():
         "step_hbm_gbps": round(g["token_bytes"] / (g["step_ms"] * 1e-3) / 1e9, 1),
         "step_hbm_frac": round(g["token_bytes"] / (g["step_ms"] * 1e-3) / HBM_PEAK, 4),
         "roofline": {"kernel": g["dom"], "bound": "hbm", "achieved": round(achieved / 1e9, 1),
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": MEASURED_TRAFFIC.get(g["dom"]),
+                     "traffic_source": "profiles/decode_cfg2_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE)",
                      "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"]},
         "kernels": g["timing"],
         "cpu_baseline": cpu,
+        "secondary": secondary,
     }
     print(json.dumps(out), flush=True)
 
