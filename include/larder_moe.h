@@ -128,7 +128,7 @@ int lmoe_grouped_tile_rows(void);
  *   h[p][f] = silu(x[order[p] / topk] . wg[e][f]) * (x[order[p] / topk] . wu[e][f])  for grouped row p of expert e,
  * h [R][I] float16 in grouped order (rows past offsets[E] untouched). x [T][H] float16 (xdtype must be LMOE_F16:
  * convert other activations once with lmoe_to_f16); wg / wu [E][I][row bytes], one ggml type (Q4_0 or Q4_K);
- * H a multiple of 128 (Q4_K: 256), I of 64. The work list is read on the device: max_tiles = lmoe_max_tiles(R, E,
+ * H a multiple of 64 (Q4_K: 256), I of 128. The work list is read on the device: max_tiles = lmoe_max_tiles(R, E,
  * bm). Replaces the reference's dense path dequant + gather_mm gate/up + silu-mul (gguf_experts.py:698-720;
  * DEQ_SRC :529-539). */
 int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, const uint32_t *order, const uint32_t *offsets,
@@ -138,7 +138,7 @@ int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, const uint3
 
 /* Grouped down on the matrix cores: y[p][n] = h[p] . wd[e][n] for grouped row p of expert e, y [R][H] in ydtype
  * (F16 / F32) in grouped order, unweighted. h [R][I] float16 as lmoe_grouped_gate_up leaves it; I a multiple of
- * 128 (Q4_K: 256), H of 128. Replaces the dense path's gather_mm down (gguf_experts.py:720-721). */
+ * 64 (Q4_K: 256), H of 256. Replaces the dense path's gather_mm down (gguf_experts.py:720-721). */
 int lmoe_grouped_down(const void *h, const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
                       int max_tiles, const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
                       void *stream);
@@ -162,6 +162,11 @@ int lmoe_dequant(const uint8_t *buf, int type, int n_experts, int rows, int cols
 /* Q4_0 quantizer on the device, ggml's quantize_row_q4_0_ref rule (no counterpart in the reference, which only
  * reads packs llama.cpp wrote): w [rows][cols] in wdtype -> out [rows][cols / 32 * 18]. */
 int lmoe_quantize_q4_0(const void *w, int wdtype, long long rows, int cols, uint8_t *out, void *stream);
+
+/* Q4_K quantizer on the device (no counterpart in the reference or in ggml): a plain min/scale fit, bit-for-bit the
+ * CPU oracle's quantize_q4_k. w [rows][cols] in wdtype (cols % 256 == 0) -> out [rows][cols / 256 * 144]. Builds the
+ * Q4_K test and benchmark packs (configuration 5). */
+int lmoe_quantize_q4_k(const void *w, int wdtype, long long rows, int cols, uint8_t *out, void *stream);
 
 #ifdef __cplusplus
 }

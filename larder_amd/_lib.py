@@ -49,6 +49,7 @@ SIGNATURES = {
     "lmoe_combine_sorted": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_dequant": (_I, [_P, _I, _I, _I, _I, _P, _I, _P, _I, _P]),
     "lmoe_quantize_q4_0": (_I, [_P, _I, _LL, _I, _P, _P]),
+    "lmoe_quantize_q4_k": (_I, [_P, _I, _LL, _I, _P, _P]),
 }
 
 _LIB = None

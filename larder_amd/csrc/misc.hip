@@ -125,6 +125,64 @@ __global__ void __launch_bounds__(256) k_quantize_q4_0(const void *w, int wdt, l
   }
 }
 
+// One thread a Q4_K super-block of 256 weights (8 sub-blocks of 32), by a plain min/scale fit with no counterpart in
+// ggml or the reference (which only read packs): sub-block j gets scale (max - min) / 15 and min -min(x, 0); the
+// super-block's d and dmin are the largest of those over 63 (stored f16, round to nearest even); the 6-bit sc_j,
+// m_j round (half to even) against the stored d, dmin; each weight takes q = clip(rint((x + dmin m_j) / (d sc_j)),
+// 0, 15). Scales pack as ggml's get_scale_min_k4 reads them. Every step rounds on its own (no contraction).
+__global__ void __launch_bounds__(256) k_quantize_q4_k(const void *w, int wdt, long long nblocks, uint8_t *out) {
+  const long long b = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (b >= nblocks) return;
+  const size_t base = size_t(b) * 256;
+  float scale[8], mins[8];
+  for (int j = 0; j < 8; ++j) {
+    float lo = 0.0f, hi = -INFINITY;
+    for (int i = 0; i < 32; ++i) {
+      const float v = load_elt(w, base + 32 * j + i, wdt);
+      lo = fminf(lo, v);
+      hi = fmaxf(hi, v);
+    }
+    scale[j] = (hi - lo) / 15.0f;
+    mins[j] = -lo;  // -0 when the sub-block has no negative weight
+  }
+  // maxima seeded with the first sub-block, so an all -0 set of mins keeps its sign (stored dmin = -0)
+  float smax = scale[0], mmax = mins[0];
+  for (int j = 1; j < 8; ++j) {
+    smax = fmaxf(smax, scale[j]);
+    mmax = fmaxf(mmax, mins[j]);
+  }
+  const float dq = smax / 63.0f, mq = mmax / 63.0f;
+  const _Float16 d16 = _Float16(dq), m16 = _Float16(mq);
+  const float d = float(d16), dm = float(m16);
+  uint32_t sc[8], m[8];
+  for (int j = 0; j < 8; ++j) {
+    sc[j] = d > 0.0f ? uint32_t(fminf(fmaxf(rintf(scale[j] / d), 0.0f), 63.0f)) : 0u;
+    m[j] = dm > 0.0f ? uint32_t(fminf(fmaxf(rintf(mins[j] / dm), 0.0f), 63.0f)) : 0u;
+  }
+  uint8_t *o = out + size_t(b) * 144;
+  const uint16_t db = __builtin_bit_cast(uint16_t, d16), mb = __builtin_bit_cast(uint16_t, m16);
+  o[0] = uint8_t(db & 0xFF);
+  o[1] = uint8_t(db >> 8);
+  o[2] = uint8_t(mb & 0xFF);
+  o[3] = uint8_t(mb >> 8);
+  for (int j = 0; j < 4; ++j) {
+    o[4 + j] = uint8_t((sc[j] & 63u) | ((sc[j + 4] >> 4) << 6));
+    o[8 + j] = uint8_t((m[j] & 63u) | ((m[j + 4] >> 4) << 6));
+    o[12 + j] = uint8_t((sc[j + 4] & 15u) | ((m[j + 4] & 15u) << 4));
+  }
+  // sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles) share qs bytes 32c .. 32c + 31
+  for (int c = 0; c < 4; ++c) {
+    const float dj0 = d * float(sc[2 * c]), mj0 = dm * float(m[2 * c]);
+    const float dj1 = d * float(sc[2 * c + 1]), mj1 = dm * float(m[2 * c + 1]);
+    for (int i = 0; i < 32; ++i) {
+      const float x0 = load_elt(w, base + 64 * c + i, wdt), x1 = load_elt(w, base + 64 * c + 32 + i, wdt);
+      const uint32_t q0 = dj0 > 0.0f ? uint32_t(fminf(fmaxf(rintf((x0 + mj0) / dj0), 0.0f), 15.0f)) : 0u;
+      const uint32_t q1 = dj1 > 0.0f ? uint32_t(fminf(fmaxf(rintf((x1 + mj1) / dj1), 0.0f), 15.0f)) : 0u;
+      o[16 + 32 * c + i] = uint8_t(q0 | (q1 << 4));
+    }
+  }
+}
+
 }  // namespace lmoe
 
 using namespace lmoe;
@@ -182,6 +240,20 @@ extern "C" int lmoe_quantize_q4_0(const void *w, int wdtype, long long rows, int
   if (nb == 0) return 0;
   LMOE_REQUIRE(w && out, LMOE_EINVAL, "%s: null pointer", fn);
   hipLaunchKernelGGL(k_quantize_q4_0, dim3(unsigned((nb + 255) / 256)), dim3(256), 0, (hipStream_t)stream, w, wdtype,
+                     nb, out);
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+extern "C" int lmoe_quantize_q4_k(const void *w, int wdtype, long long rows, int cols, uint8_t *out, void *stream) {
+  const char *fn = "lmoe_quantize_q4_k";
+  LMOE_REQUIRE(dtype_ok(wdtype), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(rows >= 0 && cols > 0 && cols % 256 == 0, LMOE_ESHAPE, "%s: row length %d is not a multiple of 256", fn,
+               cols);
+  const long long nb = rows * (cols / 256);
+  if (nb == 0) return 0;
+  LMOE_REQUIRE(w && out, LMOE_EINVAL, "%s: null pointer", fn);
+  hipLaunchKernelGGL(k_quantize_q4_k, dim3(unsigned((nb + 255) / 256)), dim3(256), 0, (hipStream_t)stream, w, wdtype,
                      nb, out);
   LMOE_LAUNCHED(fn);
   return 0;

@@ -1,7 +1,7 @@
 """Synthetic workloads of the five benchmark configurations, built directly on the GPU.
 
 Weights are Gaussian N(0, 0.02^2) drawn with torch's seeded CUDA generator and quantized on the device
-(lmoe_quantize_q4_0), activations Gaussian N(0, 1). Shapes:
+(lmoe_quantize_q4_0 / lmoe_quantize_q4_k), activations Gaussian N(0, 1). Shapes:
 
   cfg1  H 2048, E 60, top-4, softmax without renormalisation, I 1408, shared expert Is 5632 with a sigmoid gate
   cfg2  48 layers of H 2048, E 128, top-8 renormalised, I 768, no shared expert; batch-1 decode
@@ -23,17 +23,24 @@ CONFIGS = {
 }
 
 
-def q4_0_experts(n, rows, cols, gen, std=0.02, chunk_rows=1 << 18):
-    """n experts [n, rows, cols / 32 * 18] uint8 quantized from N(0, std^2) float32 weights drawn on the GPU."""
-    out = torch.empty((n, rows, row_bytes("Q4_0", cols)), dtype=torch.uint8, device="cuda")
+def quantized_experts(t, n, rows, cols, gen, std=0.02, chunk_rows=1 << 18):
+    """n experts [n, rows, row bytes] in ggml type t (Q4_0 or Q4_K) quantized on the device from N(0, std^2) float32
+    weights drawn on the GPU (lmoe_quantize_q4_0 / lmoe_quantize_q4_k)."""
+    fn = {"Q4_0": "lmoe_quantize_q4_0", "Q4_K": "lmoe_quantize_q4_k"}[t]
+    out = torch.empty((n, rows, row_bytes(t, cols)), dtype=torch.uint8, device="cuda")
     flat = out.view(n * rows, -1)
     total = n * rows
     for r0 in range(0, total, chunk_rows):
         r1 = min(total, r0 + chunk_rows)
         w = torch.randn((r1 - r0, cols), generator=gen, device="cuda", dtype=torch.float32) * std
-        call("lmoe_quantize_q4_0", ptr(w), F32, r1 - r0, cols, ptr(flat[r0:r1]), stream())
+        call(fn, ptr(w), F32, r1 - r0, cols, ptr(flat[r0:r1]), stream())
         del w
     return out
+
+
+def q4_0_experts(n, rows, cols, gen, std=0.02, chunk_rows=1 << 18):
+    """n experts [n, rows, cols / 32 * 18] uint8 quantized from N(0, std^2) float32 weights drawn on the GPU."""
+    return quantized_experts("Q4_0", n, rows, cols, gen, std, chunk_rows)
 
 
 def router_weight(E, H, gen, std=0.02, dtype=torch.float16):
@@ -41,17 +48,17 @@ def router_weight(E, H, gen, std=0.02, dtype=torch.float16):
 
 
 def make_layer(cfg, gen, with_router=True):
-    """One MoE layer of configuration ``cfg`` (a CONFIGS entry) with Q4_0 weights made on the device."""
-    if cfg["types"][0] != "Q4_0":
-        raise ValueError("device-made weights are Q4_0 only; Q4_K layers come from the CPU quantizer")
+    """One MoE layer of configuration ``cfg`` (a CONFIGS entry) with its weights quantized on the device."""
     H, E, I, Is = cfg["H"], cfg["E"], cfg["I"], cfg["Is"]
-    wg = q4_0_experts(E, I, H, gen)
-    wu = q4_0_experts(E, I, H, gen)
-    wd = q4_0_experts(E, H, I, gen)
+    tg, tu, td = cfg["types"]
+    wg = quantized_experts(tg, E, I, H, gen)
+    wu = quantized_experts(tu, E, I, H, gen)
+    wd = quantized_experts(td, E, H, I, gen)
     wr = router_weight(E, H, gen) if with_router else None
     shared = wsg = None
     if Is:
-        shared = (q4_0_experts(1, Is, H, gen), q4_0_experts(1, Is, H, gen), q4_0_experts(1, H, Is, gen))
+        shared = (quantized_experts(tg, 1, Is, H, gen), quantized_experts(tu, 1, Is, H, gen),
+                  quantized_experts(td, 1, H, Is, gen))
         wsg = router_weight(1, H, gen).reshape(H)
     return MoELayer(wg, wu, wd, cfg["types"], cfg["k"], cfg["norm"], wr=wr, shared=shared, wsg=wsg)
 
