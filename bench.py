@@ -105,10 +105,11 @@ def gpu_leg(args):
 
 
 def grouped_leg():
-    """The grouped path's own configurations, reported beside the decode line:
+    """The other configurations (BASELINE.json configs[2..4]), reported beside the decode line:
     cfg3 = one 8192-token bf16 prefill chunk through one cfg-2 layer with skewed router logits (MFMA roofline over
     the routed experts' 2 R 3 H I flops); cfg4 = 512 steps of 64 tokens with a fresh Zipf-prior draw each step
-    (HBM roofline over the unique experts touched)."""
+    (HBM roofline over the unique experts touched); cfg5 = the 512-expert Q4_K layer at T = 1 (decode chain) and
+    T = 2048 (grouped path)."""
     import ctypes
 
     import torch
@@ -202,6 +203,50 @@ def grouped_leg():
                            "note": "one HIP graph a step; input copies of x and logits inside the timed loop",
                            "unique_experts_per_step": round(uniq, 1),
                            "hbm_frac": round(byts / (us4 * 1e-6) / HBM_PEAK, 4)}
+    del B4, xs, lgs
+    # cfg5: H 4096, 512 experts top-10, I 512, shared expert, Q4_K. T = 1 through the decode chain (one layer as a
+    # HIP graph, a fresh x each step so the touched experts change), T = 2048 through the grouped path.
+    from larder_amd import layer as lay
+    cfg5 = workloads.CONFIGS[5]
+    L5 = workloads.make_layer(cfg5, g)
+    st5 = lay.DecodeStack([L5], 1)
+    st5.capture()
+    n5 = 256
+    x5 = torch.randn((n5 + 16, 1, cfg5["H"]), generator=g, device="cuda").half()
+    for i in range(16):
+        st5.x_in.copy_(x5[i])
+        st5.graph.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(16, 16 + n5):
+        st5.x_in.copy_(x5[i])
+        st5.graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us5 = e0.elapsed_time(e1) / n5 * 1e3
+    b5 = workloads.decode_bytes(cfg5, cfg5["k"]) + 2 * cfg5["H"] * 2
+    out["cfg5_decode_T1"] = {"us_per_token": round(us5, 2), "tokens_per_s": round(1 / (us5 * 1e-6), 1),
+                             "bytes": b5, "hbm_frac": round(b5 / (us5 * 1e-6) / HBM_PEAK, 4)}
+    T5 = 2048
+    x5p = torch.randn((T5, cfg5["H"]), generator=g, device="cuda").bfloat16()
+    B5 = grouped.PrefillBuffers(L5, T5)
+    y5 = torch.empty((T5, cfg5["H"]), dtype=torch.bfloat16, device="cuda")
+    for _ in range(3):
+        grouped.prefill(L5, x5p, B5, y5)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(10):
+        grouped.prefill(L5, x5p, B5, y5)
+    e1.record()
+    torch.cuda.synchronize()
+    us5p = e0.elapsed_time(e1) / 10 * 1e3
+    f5 = workloads.expert_flops(cfg5, T5 * cfg5["k"]) + 2 * T5 * 3 * cfg5["H"] * cfg5["Is"]
+    u5 = int((B5.G.counts > 0).sum().item())
+    by5 = workloads.decode_bytes(cfg5, u5) + T5 * cfg5["H"] * 2 * 2
+    out["cfg5_prefill_T2048"] = {"us": round(us5p, 1), "tokens_per_s": round(T5 / (us5p * 1e-6), 1),
+                                 "mfma_frac": round(f5 / (us5p * 1e-6) / MFMA_PEAK, 4),
+                                 "hbm_frac": round(by5 / (us5p * 1e-6) / HBM_PEAK, 4), "experts_touched": u5,
+                                 "note": "router logits by one f32 library GEMM (torch.matmul) inside the timing"}
     return out
 
 

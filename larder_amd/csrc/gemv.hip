@@ -24,11 +24,21 @@ namespace lmoe {
 
 __device__ __forceinline__ int elt_size(int dt) { return dt == LMOE_F32 ? 4 : 2; }
 
-// ndw dwords (a multiple of 4, 16-byte aligned) from global src to LDS dst, 16 bytes a thread a step.
+// ndw dwords (a multiple of 4, 16-byte aligned) from global src to LDS dst, 16 bytes a thread a step. A thread's
+// loads go out 8 at a time, none predicated (indices clamped to the last chunk), ahead of its stores, so their
+// round trips overlap instead of queueing one behind the other.
 __device__ __forceinline__ void copy_to_lds(const void *src, void *dst, int ndw, int tid, int nthr) {
   const u32x4 *s = static_cast<const u32x4 *>(src);
   u32x4 *d = static_cast<u32x4 *>(dst);
-  for (int i = tid; i < ndw / 4; i += nthr) d[i] = s[i];
+  const int n = ndw / 4;
+  for (int b = tid; b < n; b += 8 * nthr) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = s[min(b + j * nthr, n - 1)];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (b + j * nthr < n) d[b + j * nthr] = v[j];
+  }
 }
 
 __device__ __forceinline__ float lds_elt(const void *raw, int i, int dt) {
@@ -120,6 +130,7 @@ __global__ void __launch_bounds__(64 * NW, 3)
   if (logits) {  // the router's top-k of this slot's token, by wavefront 0, the slot's pick through LDS
     __shared__ uint32_t pick_id[32];
     __shared__ float pick_sc[32];
+    __shared__ __attribute__((aligned(16))) uint32_t scr[64];
     if (wave == 0) {
       const float *row = logits + size_t(s / topk) * ld_stride;
       auto run = [&](auto npl) {
@@ -127,7 +138,13 @@ __global__ void __launch_bounds__(64 * NW, 3)
         float v[N];
 #pragma unroll
         for (int j = 0; j < N; ++j) v[j] = lane + 64 * j < n_experts ? row[lane + 64 * j] : -INFINITY;
-        topk_wave<N>(v, n_experts, topk, norm, pick_id, pick_sc);
+        uint32_t id;
+        float sc;
+        topk_wave<N>(v, n_experts, topk, norm, scr, &id, &sc);
+        if (lane < topk) {
+          pick_id[lane] = id;
+          pick_sc[lane] = sc;
+        }
       };
       if (n_experts <= 64)
         run(std::integral_constant<int, 1>());
@@ -158,21 +175,21 @@ __global__ void __launch_bounds__(64 * NW, 3)
   uint32_t *stage = region + wave * stage_dw;
   float *red = reinterpret_cast<float *>(region + max(NW * stage_dw, xraw_dw)) + wave * (2 * RB * (P + 1));
   const bool valid = e < uint32_t(n_experts);  // no such expert: zero rows (cpu_kern.cpp:316-318)
-  const bool rows_ok = valid && r0 < I;
 
-  // 1) this wavefront's 2 RB rows, RB 9 P / 4 16-byte chunks a matrix, into registers
+  // 1) this wavefront's 2 RB rows, RB 9 P / 4 16-byte chunks a matrix, into registers. The loads are not
+  // predicated (a lane past the end re-reads the last chunk; a wavefront with no rows or no expert reads expert 0's
+  // last row block), so they issue back to back with no wait between them.
   const int C = RB * 9 * P / 4;
   const size_t rowb = size_t(36) * P;
-  const u32x4 *gsrc = reinterpret_cast<const u32x4 *>(wg + (size_t(e) * I + r0) * rowb);
-  const u32x4 *usrc = reinterpret_cast<const u32x4 *>(wu + (size_t(e) * I + r0) * rowb);
+  const size_t rsafe = size_t(valid ? e : 0u) * I + min(r0, I - RB);
+  const u32x4 *gsrc = reinterpret_cast<const u32x4 *>(wg + rsafe * rowb);
+  const u32x4 *usrc = reinterpret_cast<const u32x4 *>(wu + rsafe * rowb);
   u32x4 vg[NC], vu[NC];
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
-    const int c = lane + 64 * i;
-    if (rows_ok && c < C) {
-      vg[i] = __builtin_nontemporal_load(gsrc + c);
-      vu[i] = __builtin_nontemporal_load(usrc + c);
-    }
+    const int c = min(lane + 64 * i, C - 1);
+    vg[i] = __builtin_nontemporal_load(gsrc + c);
+    vu[i] = __builtin_nontemporal_load(usrc + c);
   }
   // 2) the activation row
   const size_t xrow = size_t(s / topk);
@@ -244,6 +261,177 @@ __global__ void __launch_bounds__(64 * NW, 3)
   }
 }
 
+// The dot of unit p of a staged row (9 P dwords) with an activation unit held in registers (pairs xv, sums sx0 / sx1).
+template <int TQ>
+__device__ __forceinline__ float row_unit_dot_r(const uint32_t *row, int p, const uint32_t *xv, float sx0, float sx1) {
+  if (TQ == LMOE_Q4_0) {
+    uint32_t u[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) u[i] = row[9 * p + i];
+    return unit_dot_q4_0(u, xv, sx0, sx1);
+  } else {
+    const uint32_t *sb = row + 36 * (p >> 2);
+    const int c = p & 3;
+    uint32_t hdr[4], q[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hdr[i] = sb[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = sb[4 + 8 * c + i];
+    return unit_dot_q4_k(hdr, q, c, xv, sx0, sx1);
+  }
+}
+
+// sum over the aligned group of P lanes (P = 32 or 64), the result in every lane of the group
+template <int P>
+__device__ __forceinline__ float group_sum(float v) {
+  v = sum16(v);
+  v += lane_xor16(v);
+  if (P == 64) v += lane_xor32(v);
+  return v;
+}
+
+// ---- gate/up with the activation unit in registers (H = 64 P, P = 32 or 64; one block type for gate and up) ----
+//
+// Grid (ceil(I / (4 RB)), n_slots): four wavefronts a workgroup; wavefront w of block (bx, s) takes gate and up
+// rows [(4 bx + w) RB, +RB) of expert e(s). The token's prepared activation row comes into LDS once a workgroup
+// (one workgroup barrier); lane l then holds unit p = l % P of it in registers (36 dwords) for the rows
+// g, g + G, ... of both matrices (g = l / P, G = 64 / P lane groups). The wavefront's weight rows come in with 16-byte
+// loads, go to its own LDS region and are read back a 36-byte unit a lane; each row's P partials are summed over
+// the lane group on DPP and permlane swaps. NPL > 0: each wavefront picks the slot's expert from the logits itself
+// (NPL a lane; softmax scores only in the one wavefront that writes ids / scores, wavefront 0 of the slot's first
+// workgroup); NPL = 0: expert ids from slots. Memory order: logits,
+// activation chunks, then (once the id is known) the weights, none predicated, so each group goes out back to back.
+template <int TQ, int P, int RB, int NPL>
+__global__ void __launch_bounds__(256)
+    k_gate_up_xr(const uint32_t *xprep, const uint32_t *slots, int topk, const uint8_t *wg, const uint8_t *wu,
+                 int n_experts, int I, float *h, uint32_t *hprep, int td, const float *logits, int ld_stride,
+                 int norm, uint32_t *ids_out, float *scores_out) {
+  constexpr int G = 64 / P, RG = RB / G;
+  static_assert(P == 32 || P == 64, "32 or 64 units a row");
+  static_assert(RB % G == 0, "rows split evenly over the lane groups");
+  constexpr int C = RB * 9 * P / 4;  // 16-byte chunks of RB rows of one matrix
+  constexpr int NC = (C + 63) / 64;
+  constexpr int STAGE = 2 * RB * 9 * P;  // dwords a wavefront
+  constexpr int XC = 9 * P;              // 16-byte chunks of the prepared activation row
+  constexpr int XPT = (XC + 255) / 256;  // of them a thread
+  // LDS (16-byte chunks): the activation row, 4 stages, 4 x 64 dwords of top-k scratch
+  __shared__ u32x4 lds4[XC + STAGE + 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int s = blockIdx.y;
+  const int r0 = (blockIdx.x * 4 + wave) * RB;
+  const int g = lane / P, p = lane % P;
+  u32x4 *xl = lds4;
+  uint32_t *stage = reinterpret_cast<uint32_t *>(lds4 + XC) + wave * STAGE;
+  uint32_t *scr = reinterpret_cast<uint32_t *>(lds4 + XC + STAGE) + wave * 64;
+  const size_t xrow = size_t(s / topk);
+
+  float v[NPL > 0 ? NPL : 1];
+  uint32_t e = 0;
+  if (NPL > 0) {
+    const float *row = logits + xrow * ld_stride;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) v[j] = row[min(lane + 64 * j, n_experts - 1)];  // lanes past E: masked by topk_wave
+  } else {
+    e = slots[s];
+  }
+  const u32x4 *xg4 = reinterpret_cast<const u32x4 *>(xprep + xrow * P * XS);
+  u32x4 xc[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) xc[i] = xg4[min(int(threadIdx.x) + 256 * i, XC - 1)];
+  if (NPL > 0) {  // each wavefront picks the slot's expert itself (no barrier before its weight loads)
+    constexpr int N = NPL > 0 ? NPL : 1;
+    const int j = s % topk;
+    uint32_t id;
+    if (blockIdx.x == 0 && wave == 0) {  // the slot's scores: one wavefront computes and writes them
+      float sc;
+      topk_wave<N, true>(v, n_experts, topk, norm, scr, &id, &sc);
+      if (lane == j) {
+        ids_out[s] = id;
+        scores_out[s] = sc;
+      }
+    } else {
+      topk_wave<N, false>(v, n_experts, topk, norm, scr, &id, nullptr);
+    }
+    e = uint32_t(__builtin_amdgcn_readlane(int(id), j));
+  }
+  const bool valid = e < uint32_t(n_experts);  // no such expert: zero rows (cpu_kern.cpp:316-318)
+  const size_t rsafe = size_t(valid ? e : 0u) * I + min(r0, I - RB);
+  const u32x4 *gsrc = reinterpret_cast<const u32x4 *>(wg + rsafe * (36 * P));
+  const u32x4 *usrc = reinterpret_cast<const u32x4 *>(wu + rsafe * (36 * P));
+  u32x4 vg[NC], vu[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = min(lane + 64 * i, C - 1);
+    vg[i] = __builtin_nontemporal_load(gsrc + c);
+    vu[i] = __builtin_nontemporal_load(usrc + c);
+  }
+  // the activation row into LDS (a thread past the end rewrites the last chunk with its own value), then the
+  // weights into the wavefront's stage, with no branch between loads and stores so that no load is sunk into a
+  // conditional block behind the others' wait
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) xl[min(int(threadIdx.x) + 256 * i, XC - 1)] = xc[i];
+  __syncthreads();
+  u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = min(lane + 64 * i, C - 1);
+    st4[c] = vg[i];
+    st4[C + c] = vu[i];
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (r0 >= I) return;
+  if (!valid) {
+    if (lane < RB) {
+      const int n = r0 + lane;
+      if (h) h[size_t(s) * I + n] = 0.0f;
+      if (hprep) {
+        int dw, half;
+        xslot(n & 63, td == LMOE_Q4_K ? 32 : 16, &dw, &half);
+        reinterpret_cast<_Float16 *>(hprep + (size_t(s) * (I / 64) + (n >> 6)) * XS + dw)[half] = _Float16(0.0f);
+      }
+    }
+    return;
+  }
+  uint32_t xv[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const u32x4 q = xl[9 * p + i];
+    xv[4 * i] = q.x;
+    xv[4 * i + 1] = q.y;
+    xv[4 * i + 2] = q.z;
+    xv[4 * i + 3] = q.w;
+  }
+  // the two half-unit sums; __uint_as_float, not __builtin_bit_cast: this compiler lowers a bit cast of an
+  // ext_vector element lvalue (qs.y) to element 0
+  const u32x4 qs = xl[9 * p + 8];
+  const float sx0 = __uint_as_float(qs.x), sx1 = __uint_as_float(qs.y);
+  float pg[RG], pu[RG];
+#pragma unroll
+  for (int i = 0; i < RG; ++i) {
+    const int rr = g + G * i;
+    pg[i] = row_unit_dot_r<TQ>(stage + rr * 9 * P, p, xv, sx0, sx1);
+    pu[i] = row_unit_dot_r<TQ>(stage + (RB + rr) * 9 * P, p, xv, sx0, sx1);
+  }
+#pragma unroll
+  for (int i = 0; i < RG; ++i) {
+    pg[i] = group_sum<P>(pg[i]);
+    pu[i] = group_sum<P>(pu[i]);
+  }
+  if (p == 0) {
+#pragma unroll
+    for (int i = 0; i < RG; ++i) {
+      const int n = r0 + g + G * i;
+      const float hv = silu_mul(pg[i], pu[i]);
+      if (h) h[size_t(s) * I + n] = hv;
+      if (hprep) {
+        int dw, half;
+        xslot(n & 63, td == LMOE_Q4_K ? 32 : 16, &dw, &half);
+        reinterpret_cast<_Float16 *>(hprep + (size_t(s) * (I / 64) + (n >> 6)) * XS + dw)[half] = _Float16(hv);
+      }
+    }
+  }
+}
+
 // ---- down + combine -------------------------------------------------------------------------------------------
 //
 // Grid (H / (4 NW), T). Block (bx, t) stages the k h rows of token t as prepared units (copied from hprep, sums
@@ -251,7 +439,7 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // of all k experts of token t, adds them weighted by scores[t] (1 when scores is null), then the gated
 // shared-expert row and the residual, and writes out[t]. When k 9 P <= 64 NC the weight chunks are fetched into
 // registers before the h staging; otherwise after it.
-template <int TD, int RB, int NC, int NW>
+template <int TD, int RB, int NC, int NW, bool HP, bool PRE>
 __global__ void __launch_bounds__(64 * NW, 3)
     k_down_combine(const uint32_t *hprep, int has_sums, const float *h, const uint32_t *ids, const float *scores,
                    int k, const uint8_t *wd, int n_experts, int I, int H, const float *shared, const float *gate,
@@ -274,42 +462,60 @@ __global__ void __launch_bounds__(64 * NW, 3)
   const size_t rowb = size_t(36) * P;
   const int C = RB * 9 * P / 4;  // 16-byte chunks of RB rows
   const bool rows_ok = n0 < H;
-  const bool pre = k * C <= 64 * NC;
+  // Memory order of the prologue: the token's ids and scores (one a lane), the first 8 16-byte chunks a thread of
+  // its prepared h rows, then the weights, whose addresses need only the ids. No load is predicated (clamped
+  // indices; expert 0 stands in for an id past the experts, the last row block for a wavefront past H), so each
+  // group issues back to back and the h stores to LDS wait only for the h loads.
   const uint32_t *tid_ids = ids + size_t(t) * k;
+  const int kl = min(lane, k - 1);
+  const uint32_t my_id = tid_ids[kl];
+  const float sc_ld = (scores ? scores + size_t(t) * k : reinterpret_cast<const float *>(tid_ids))[kl];
+  const float my_sc = scores ? sc_ld : 1.0f;  // read by lane exchange in the dot loop, once the weights are in
+  const int nthr = 64 * NW;
+  const int hn = HP ? k * P * XS / 4 : 0;
+  const u32x4 *hsrc = reinterpret_cast<const u32x4 *>(hprep + size_t(t) * k * P * XS);
+  u32x4 hv[8];
+  if (HP) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) hv[j] = hsrc[min(int(threadIdx.x) + j * nthr, hn - 1)];
+  }
   u32x4 v[NC];
-  if (pre && rows_ok) {
+  if (PRE) {
+    const size_t nsafe = size_t(min(n0, H - RB));
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
-      const int c = lane + 64 * i;
-      if (c < k * C) {
-        const int j = c / C, cc = c - j * C;
-        const uint32_t e = tid_ids[j];
-        if (e < uint32_t(n_experts))
-          v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wd + (size_t(e) * H + n0) * rowb) + cc);
-      }
+      const int c = min(lane + 64 * i, k * C - 1);
+      const int j = c / C, cc = c - j * C;
+      uint32_t e = uint32_t(__shfl(int(my_id), j, 64));
+      e = e < uint32_t(n_experts) ? e : 0u;
+      v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wd + (size_t(e) * H + nsafe) * rowb) + cc);
     }
   }
-  if (threadIdx.x < k) {
-    eid[threadIdx.x] = tid_ids[threadIdx.x];
-    esc[threadIdx.x] = scores ? scores[size_t(t) * k + threadIdx.x] : 1.0f;
+  if (threadIdx.x < k) {  // wavefront 0, lane = threadIdx.x < k <= 32
+    eid[threadIdx.x] = my_id;
   }
-  if (hprep) {
-    copy_to_lds(hprep + size_t(t) * k * P * XS, hx, k * P * XS, threadIdx.x, 64 * NW);
+  if (HP) {
+    u32x4 *hx4 = reinterpret_cast<u32x4 *>(hx);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (int(threadIdx.x) + j * nthr < hn) hx4[threadIdx.x + j * nthr] = hv[j];
+    if (hn > 8 * nthr)
+      copy_to_lds(hsrc + 8 * nthr, hx4 + 8 * nthr, 4 * (hn - 8 * nthr), threadIdx.x, nthr);
     __syncthreads();
     if (!has_sums) {
-      sums_in_lds<TD>(hx, k * P, threadIdx.x, 64 * NW);
+      sums_in_lds<TD>(hx, k * P, threadIdx.x, nthr);
       __syncthreads();
     }
   } else {
-    copy_to_lds(h + size_t(t) * k * I, region, k * I, threadIdx.x, 64 * NW);
+    copy_to_lds(h + size_t(t) * k * I, region, k * I, threadIdx.x, nthr);
     __syncthreads();
-    for (int j = 0; j < k; ++j) prep_in_lds<TD>(region + j * I, LMOE_F32, P, hx + j * P * XS, threadIdx.x, 64 * NW);
+    for (int j = 0; j < k; ++j) prep_in_lds<TD>(region + j * I, LMOE_F32, P, hx + j * P * XS, threadIdx.x, nthr);
     __syncthreads();
   }
   if (!rows_ok) return;
 
   u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
-  if (pre) {
+  if (PRE) {
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int c = lane + 64 * i;
@@ -327,12 +533,16 @@ __global__ void __launch_bounds__(64 * NW, 3)
 
   const int U = k * RB * P;
 #pragma unroll 2
-  for (int u = lane; u < U; u += 64) {
+  for (int u0 = 0; u0 < U; u0 += 64) {  // uniform trip count: the score exchange runs with every lane active
+    const int u = min(u0 + lane, U - 1);
     const int j = u / (RB * P), rem = u - j * (RB * P), row = rem / P, p = rem - row * P;
-    float part = 0.0f;
-    if (eid[j] < uint32_t(n_experts))
-      part = esc[j] * row_unit_dot<TD>(stage + (j * RB + row) * 9 * P, p, hx + (j * P + p) * XS);
-    red[row * red_ld + j * P + p] = part;
+    const float sc = __shfl(my_sc, j, 64);
+    if (u0 + lane < U) {
+      float part = 0.0f;
+      if (eid[j] < uint32_t(n_experts))
+        part = sc * row_unit_dot<TD>(stage + (j * RB + row) * 9 * P, p, hx + (j * P + p) * XS);
+      red[row * red_ld + j * P + p] = part;
+    }
   }
   __builtin_amdgcn_wave_barrier();
 
@@ -388,9 +598,33 @@ static int launch_gate_up(const GateUpArgs &a, hipStream_t st) {
 }
 
 // 2 rows a task when the row chunks split evenly (P even), else 4; NC covers a task's 16-byte chunks a lane.
+template <int TQ, int P, int RB, int NPL>
+static int launch_gate_up_xr(const GateUpArgs &a, hipStream_t st) {
+  const dim3 grid((a.I + 4 * RB - 1) / (4 * RB), a.n_slots);
+  launch(k_gate_up_xr<TQ, P, RB, NPL>, grid, dim3(256), 0, st, a.xg_prep, a.slots, a.topk, a.wg, a.wu,
+         a.n_experts, a.I, a.h, a.hprep, a.td, a.logits, a.ld_stride, a.norm, a.ids_out, a.scores_out);
+  LMOE_LAUNCHED("lmoe_gemv_gate_up");
+  return 0;
+}
+
+template <int TQ, int P, int RB>
+static int gate_up_xr_npl(const GateUpArgs &a, hipStream_t st) {
+  if (!a.logits) return launch_gate_up_xr<TQ, P, RB, 0>(a, st);
+  if (a.n_experts <= 64) return launch_gate_up_xr<TQ, P, RB, 1>(a, st);
+  if (a.n_experts <= 128) return launch_gate_up_xr<TQ, P, RB, 2>(a, st);
+  if (a.n_experts <= 256) return launch_gate_up_xr<TQ, P, RB, 4>(a, st);
+  if (a.n_experts <= 512) return launch_gate_up_xr<TQ, P, RB, 8>(a, st);
+  return launch_gate_up_xr<TQ, P, RB, 16>(a, st);
+}
+
 template <int TG, int TU>
 static int gate_up_p(const GateUpArgs &a, hipStream_t st) {
   const int P = a.H / 64;
+  // prepared activations, one block type, 32 or 64 units a row: the register-resident kernel
+  if (TG == TU && a.xg_prep && a.I % 2 == 0) {
+    if (P == 32) return gate_up_xr_npl<TG, 32, 2>(a, st);
+    if (P == 64) return gate_up_xr_npl<TG, 64, 2>(a, st);
+  }
   if (P % 2 == 0) {
     const int nc = (2 * 9 * P / 4 + 63) / 64;
     if (nc <= 2) return launch_gate_up<TG, TU, 2, 2, 4>(a, st);
@@ -475,8 +709,19 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "%s: k %d at width %d needs %zu bytes of LDS", fn, a.k, a.I, lds);
   const dim3 grid((a.H + RB * NW - 1) / (RB * NW), a.T);
   hipStream_t st = (hipStream_t)stream;
-  auto kern = a.type_d == LMOE_Q4_0 ? (RB == 2 ? k_down_combine<LMOE_Q4_0, 2, NC, NW> : k_down_combine<LMOE_Q4_0, 4, NC, NW>)
-                                    : (RB == 2 ? k_down_combine<LMOE_Q4_K, 2, NC, NW> : k_down_combine<LMOE_Q4_K, 4, NC, NW>);
+  // weights fetched into registers ahead of the h staging when a wavefront's k RB rows fit in NC chunks a lane
+  const bool pre = size_t(a.k) * RB * 9 * P / 4 <= size_t(64) * NC;
+  auto pick = [&](auto td, auto rb) {
+    constexpr int TD = decltype(td)::value, R = decltype(rb)::value;
+    if (a.hprep) return pre ? k_down_combine<TD, R, NC, NW, true, true> : k_down_combine<TD, R, NC, NW, true, false>;
+    return pre ? k_down_combine<TD, R, NC, NW, false, true> : k_down_combine<TD, R, NC, NW, false, false>;
+  };
+  using Q0 = std::integral_constant<int, LMOE_Q4_0>;
+  using QK = std::integral_constant<int, LMOE_Q4_K>;
+  using R2 = std::integral_constant<int, 2>;
+  using R4 = std::integral_constant<int, 4>;
+  auto kern = a.type_d == LMOE_Q4_0 ? (RB == 2 ? pick(Q0(), R2()) : pick(Q0(), R4()))
+                                    : (RB == 2 ? pick(QK(), R2()) : pick(QK(), R4()));
   if (int rc = allow_lds(kern, lds, fn)) return rc;
   launch(kern, grid, dim3(64 * NW), lds, st, a.hprep, a.has_sums, a.h, a.ids, a.scores, a.k, a.wd,
                      a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt);

@@ -167,15 +167,17 @@ constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8
 constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16
 
 // the value of lane ^ 16 / lane ^ 32
+// (the swapped pair's elements are copied out as values before the cast: a bit cast of a vector element lvalue is
+// lowered to element 0 by this compiler)
 __device__ __forceinline__ float lane_xor16(float v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
-                                                  false, false);
-  return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return __uint_as_float((threadIdx.x & 16) ? r0 : r1);
 }
 __device__ __forceinline__ float lane_xor32(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
-                                                  false, false);
-  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return __uint_as_float((threadIdx.x & 32) ? r0 : r1);
 }
 
 // sums over aligned groups of 8 / 16 / 64 lanes, the result in every lane of the group (fixed order: deterministic)
@@ -217,56 +219,106 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   return v;
 }
 
-// One wavefront, a token's logits v[j] = row[lane + 64 j] (j < NPL, E <= 64 NPL) -> ids[0..k) best first,
-// scores[0..k). Each of k rounds takes the largest untaken logit (a max over the wavefront) and, among the lanes
-// holding it, the lowest expert index (a min over the wavefront): both reductions stay on the VALU.
-template <int NPL>
-__device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm, uint32_t *ids, float *scores) {
+// Order-preserving key of a logit: a larger logit has a larger key; -0 is folded into +0 so the two tie.
+__device__ __forceinline__ uint32_t logit_key(float f) {
+  const uint32_t u = f == 0.0f ? 0u : __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_logit(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
+// One wavefront, a token's logits v[j] = row[lane + 64 j] (j < NPL, E <= 64 NPL): lane r < k gets the rank-r pick
+// (largest logit first, equal logits by lower expert index) in *id_out and its softmax probability (max-subtracted,
+// fp32), renormalised over the k picks in rank order when norm, in *score_out (SCORES false: ids only, score_out
+// untouched). lds: 64 dwords of this wavefront's LDS, 16-byte aligned. No step loops over k:
+//   1. thr = the k-th largest key, by a 32-step bitwise search on the scalar unit: bit b stays set when at least k
+//      keys are >= the prefix (one compare a value and a ballot popcount a step);
+//   2. the picks are the keys above thr, then the lowest-index keys equal to thr up to k, compacted into LDS in
+//      index order;
+//   3. each pick's rank is the number of picks ahead of it, then a lane permute puts rank r in lane r.
+template <int NPL, bool SCORES = true>
+__device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm, uint32_t *lds, uint32_t *id_out,
+                                          float *score_out) {
   const int lane = threadIdx.x & 63;
-  uint32_t taken = 0;
+  uint32_t key[NPL];
   float m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    if (lane + 64 * j < E)
-      m = fmaxf(m, v[j]);
-    else
-      taken |= 1u << j;
+    const bool ok = lane + 64 * j < E;
+    key[j] = ok ? logit_key(v[j]) : 0u;  // every real key is above 0 (-inf has key 0x007FFFFF)
+    if (ok) m = fmaxf(m, v[j]);
   }
-  m = wave_max(m);
   float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NPL; ++j)
-    if (!((taken >> j) & 1u)) s += __expf(v[j] - m);
-  s = wave_sum(s);
-  float mine = 0.0f;
-  uint32_t my_id = 0;
-  for (int r = 0; r < k; ++r) {
-    float best = -INFINITY;
+  if (SCORES) {  // the softmax terms only where the scores are wanted
+    m = wave_max(m);
 #pragma unroll
     for (int j = 0; j < NPL; ++j)
-      if (!((taken >> j) & 1u)) best = fmaxf(best, v[j]);
-    best = wave_max(best);
-    uint32_t cand = 0xFFFFFFFFu;
+      if (lane + 64 * j < E) s += __expf(v[j] - m);
+    s = wave_sum(s);
+  }
+  // 1. the k-th largest key
+  uint32_t thr = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = thr | (1u << b);
+    int cnt = 0;
 #pragma unroll
-    for (int j = NPL - 1; j >= 0; --j)
-      if (!((taken >> j) & 1u) && v[j] == best) cand = uint32_t(lane + 64 * j);
-    const uint32_t win = wave_min_u32(cand);
-    if ((win & 63u) == uint32_t(lane)) taken |= 1u << (win >> 6);
-    if (lane == r) {
-      my_id = win;
-      mine = __expf(best - m) / s;
+    for (int j = 0; j < NPL; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+    thr = cnt >= k ? cand : thr;
+  }
+  // 2. the picks, compacted in index order (expert lane + 64 j: j major, then lane)
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  int n_gt = 0;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) n_gt += __popcll(__ballot(key[j] > thr));
+  const int need = k - n_gt;  // >= 1 ties at thr are picked, lowest index first
+  int eq_before = 0, sel_before = 0;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const uint64_t eq = __ballot(key[j] == thr);
+    const bool tie = (eq >> lane) & 1u;
+    const bool sel = key[j] > thr || (tie && eq_before + __popcll(eq & below) < need);
+    const uint64_t selm = __ballot(sel);
+    const int pos = sel_before + __popcll(selm & below);
+    if (sel && pos < 32) {  // at most k <= 32 picks; the bound keeps every write inside this wavefront's 64 dwords
+      lds[pos] = key[j];
+      lds[32 + pos] = uint32_t(lane + 64 * j);
+    }
+    eq_before += __popcll(eq);
+    sel_before += __popcll(selm);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // 3. ranks, then rank order
+  uint32_t my_key = 0, my_idx = 0;
+  int rank = lane;
+  if (lane < k) {
+    my_key = lds[lane];
+    my_idx = lds[32 + lane];
+    rank = 0;
+    const u32x4 *k4 = reinterpret_cast<const u32x4 *>(lds), *i4 = reinterpret_cast<const u32x4 *>(lds + 32);
+    for (int o = 0; o < k; o += 8) {  // 8 picks a step, two 16-byte broadcast reads each of keys and ids
+      const u32x4 ka = k4[o / 4], kb = k4[o / 4 + 1], ia = i4[o / 4], ib = i4[o / 4 + 1];
+      const uint32_t ko[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+      const uint32_t io[8] = {ia.x, ia.y, ia.z, ia.w, ib.x, ib.y, ib.z, ib.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        rank += (o + q < k && (ko[q] > my_key || (ko[q] == my_key && io[q] < my_idx))) ? 1 : 0;
     }
   }
+  __builtin_amdgcn_wave_barrier();
+  const int dst = (rank & 63) * 4;
+  const uint32_t id = uint32_t(__builtin_amdgcn_ds_permute(dst, int(my_idx)));
+  *id_out = id;
+  if (!SCORES) return;
+  const uint32_t kr = uint32_t(__builtin_amdgcn_ds_permute(dst, int(my_key)));
+  float mine = lane < k ? __expf(key_logit(kr) - m) / s : 0.0f;
   if (norm) {
     float tot = 0.0f;  // the k picked probabilities summed in rank order
     for (int r = 0; r < k; ++r)
       tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), r));
     mine = mine / tot;
   }
-  if (lane < k) {
-    ids[lane] = my_id;
-    scores[lane] = mine;
-  }
+  *score_out = mine;
 }
 
 // ---- nibble words -> f16 pairs ----------------------------------------------------------------------------------

@@ -19,8 +19,9 @@ constexpr int kMaxNpl = 16;  // logits a lane: E <= 64 * 16
 template <int NPL>
 __global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt, int ld_stride, int T, int E,
                                                      int k, int norm, uint32_t *ids, float *scores) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  __shared__ __attribute__((aligned(16))) uint32_t scr[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
   const size_t base = size_t(t) * ld_stride;
   float v[NPL];
@@ -29,7 +30,13 @@ __global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt
     const int i = lane + 64 * j;
     v[j] = i < E ? load_elt(logits, base + i, ldt) : -INFINITY;
   }
-  topk_wave<NPL>(v, E, k, norm, ids + size_t(t) * k, scores + size_t(t) * k);
+  uint32_t id;
+  float sc;
+  topk_wave<NPL>(v, E, k, norm, scr[wave], &id, &sc);
+  if (lane < k) {
+    ids[size_t(t) * k + lane] = id;
+    scores[size_t(t) * k + lane] = sc;
+  }
 }
 
 constexpr int kRouterWaves = 4;
@@ -40,7 +47,7 @@ constexpr int kRouterNc = 16;        // 16-byte weight chunks a lane (H * elemen
 // Each wavefront one router row (the last row the shared-expert gate when wsg is given) for all T tokens: its
 // weight chunks load first, x is staged in LDS as f32 meanwhile. When xprep is given the workgroups also write
 // the prepared activation rows for block type TQ, a slice of units each. WDT: the weights' element type.
-template <int WDT, int TQ>
+template <int WDT, int TQ, int XB>
 __global__ void __launch_bounds__(64 * kRouterWaves)
     k_router_gemv(const void *x, int xdt, const void *wr, const void *wsg, int T, int H, int E, float *logits,
                   uint32_t *xprep) {
@@ -50,18 +57,45 @@ __global__ void __launch_bounds__(64 * kRouterWaves)
   const int rows = E + (wsg != nullptr ? 1 : 0);
   const int row = blockIdx.x * kRouterWaves + wave;
   const int nch = H / EPC;
-  u32x4 w[kRouterNc];
-  if (row < rows) {
-    const u32x4 *src = reinterpret_cast<const u32x4 *>(row < E ? static_cast<const char *>(wr) +
-                                                                     size_t(row) * H * (WDT == LMOE_F32 ? 4 : 2)
-                                                               : static_cast<const char *>(wsg));
+  // x's 16-byte chunks (XB a thread, XB * 256 >= T H / elements a chunk) go out first, since they gate the LDS
+  // staging; then the row's weights, needed only by the dot. No load is predicated (indices clamped; a wavefront
+  // past the last row re-reads it), so each group issues back to back.
+  const int epc = xdt == LMOE_F32 ? 4 : 8, nx = T * H / epc;
+  const u32x4 *x4 = static_cast<const u32x4 *>(x);
+  constexpr int NT = 64 * kRouterWaves;
+  u32x4 xv[XB];
 #pragma unroll
-    for (int i = 0; i < kRouterNc; ++i) {
-      const int c = lane + 64 * i;
-      if (c < nch) w[i] = __builtin_nontemporal_load(src + c);
+  for (int j = 0; j < XB; ++j) xv[j] = x4[min(int(threadIdx.x) + j * NT, nx - 1)];
+  u32x4 w[kRouterNc];
+  {
+    const int rs = min(row, rows - 1);
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(rs < E ? static_cast<const char *>(wr) +
+                                                                    size_t(rs) * H * (WDT == LMOE_F32 ? 4 : 2)
+                                                              : static_cast<const char *>(wsg));
+#pragma unroll
+    for (int i = 0; i < kRouterNc; ++i) w[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, nch - 1));
+  }
+  // x into LDS as f32
+#pragma unroll
+  for (int j = 0; j < XB; ++j) {
+    const int q = threadIdx.x + j * NT;
+    if (q >= nx) continue;
+    const uint32_t u[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+    float *o = xs + q * epc;
+    if (xdt == LMOE_F32) {
+      *reinterpret_cast<float4 *>(o) =
+          float4{__uint_as_float(u[0]), __uint_as_float(u[1]), __uint_as_float(u[2]), __uint_as_float(u[3])};
+    } else {
+      float f[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[2 * i] = xdt == LMOE_F16 ? half_lo(u[i]) : __uint_as_float(u[i] << 16);
+        f[2 * i + 1] = xdt == LMOE_F16 ? half_hi(u[i]) : __uint_as_float(u[i] & 0xFFFF0000u);
+      }
+      *reinterpret_cast<float4 *>(o) = float4{f[0], f[1], f[2], f[3]};
+      *reinterpret_cast<float4 *>(o + 4) = float4{f[4], f[5], f[6], f[7]};
     }
   }
-  for (int i = threadIdx.x; i < T * H; i += 64 * kRouterWaves) xs[i] = load_elt(x, i, xdt);
   __syncthreads();
   if (xprep) {  // prepared rows: units spread over the workgroups
     const int P = H / 64, units = T * P;
@@ -122,13 +156,29 @@ __global__ void __launch_bounds__(256) k_prep_x(const void *x, int xdt, int H, u
   xprep[r * P * XS + idx] = prep_dword<TQ>([&](int i) { return load_elt(x, r * H + i, xdt); }, p, dw);
 }
 
+template <int WDT, int TQ>
+static void launch_router_q(dim3 grid, dim3 block, hipStream_t st, const void *x, int xdt, const void *wr,
+                            const void *wsg, int T, int H, int E, float *logits, uint32_t *xprep) {
+  const int nx = T * H / (xdt == LMOE_F32 ? 4 : 8), xb = (nx + 64 * kRouterWaves - 1) / (64 * kRouterWaves);
+  if (xb <= 1)
+    launch(k_router_gemv<WDT, TQ, 1>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+  else if (xb <= 2)
+    launch(k_router_gemv<WDT, TQ, 2>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+  else if (xb <= 4)
+    launch(k_router_gemv<WDT, TQ, 4>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+  else if (xb <= 8)
+    launch(k_router_gemv<WDT, TQ, 8>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+  else
+    launch(k_router_gemv<WDT, TQ, 16>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+}
+
 template <int WDT>
 static void launch_router(int qt, dim3 grid, dim3 block, hipStream_t st, const void *x, int xdt, const void *wr,
                           const void *wsg, int T, int H, int E, float *logits, uint32_t *xprep) {
   if (qt == LMOE_Q4_K)
-    launch(k_router_gemv<WDT, LMOE_Q4_K>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+    launch_router_q<WDT, LMOE_Q4_K>(grid, block, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
   else
-    launch(k_router_gemv<WDT, LMOE_Q4_0>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+    launch_router_q<WDT, LMOE_Q4_0>(grid, block, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
 }
 
 }  // namespace lmoe
@@ -189,8 +239,8 @@ extern "C" int lmoe_router_gemv(const void *x, int xdtype, const void *wr, const
   LMOE_REQUIRE(!xprep || qtype_ok(qtype), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn,
                qtype);
   LMOE_REQUIRE(x && wr && logits, LMOE_EINVAL, "%s: null pointer", fn);
-  LMOE_REQUIRE(aligned16(wr) && (!wsg || aligned16(wsg)), LMOE_EALIGN, "%s: wr and wsg must be 16-byte aligned",
-               fn);
+  LMOE_REQUIRE(aligned16(x) && aligned16(wr) && (!wsg || aligned16(wsg)), LMOE_EALIGN,
+               "%s: x, wr and wsg must be 16-byte aligned", fn);
   LMOE_REQUIRE(size_t(T) * H <= size_t(kRouterMaxXs), LMOE_ESHAPE,
                "%s: %d tokens x hidden %d is above the %d activations this kernel stages", fn, T, H, kRouterMaxXs);
   LMOE_REQUIRE(size_t(H) * (wdtype == LMOE_F32 ? 4 : 2) <= size_t(kRouterNc) * 64 * 16, LMOE_ESHAPE,

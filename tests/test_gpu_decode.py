@@ -114,6 +114,42 @@ def test_gemv_chain_vs_oracle(types, H, I, xdt):
     assert moe.rel_l2(host(y16.float()), yw) < BAR
 
 
+@pytest.mark.parametrize("t,H,I", [("Q4_0", 2048, 768), ("Q4_K", 4096, 512), ("Q4_0", 4096, 512),
+                                   ("Q4_K", 2048, 768), ("Q4_0", 2048, 1408)])
+def test_gate_up_prepped_vs_oracle(t, H, I):
+    """lmoe_gemv_gate_up_prepped (activations prepared once, the register-resident kernel at H = 2048 / 4096) with
+    f32 h and with prepared h, slots in no particular order and one past the experts."""
+    from larder_amd._lib import call, dcode, ptr, qcode, stream
+    rng = np.random.default_rng(H * 3 + I)
+    E, T, topk = 5, 2, 3
+    wg = gguf.random_experts(rng, E, I, H, t)
+    wu = gguf.random_experts(rng, E, I, H, t)
+    x = dev(rng.standard_normal((T, H)).astype(np.float32)).half()
+    xprep = torch.empty((T, H // 64 * 36), dtype=torch.int32, device="cuda")
+    call("lmoe_prep_x", ptr(x), dcode(x.dtype), T, H, qcode(t), ptr(xprep), stream())
+    slots = np.array([3, 0, 4, 1, E + 2, 2], np.int32)
+    h = torch.full((T * topk, I), 7.0, dtype=torch.float32, device="cuda")
+    hp = torch.zeros((T * topk, I // 64 * 36), dtype=torch.int32, device="cuda")
+    sd, wgd, wud = dev(slots), dev(wg), dev(wu)  # held until the kernel has run
+    call("lmoe_gemv_gate_up_prepped", ptr(xprep), ptr(xprep), ptr(sd), T * topk, topk, ptr(wgd), ptr(wud), qcode(t),
+         qcode(t), E, H, I, ptr(h), ptr(hp), qcode(t), stream())
+    torch.cuda.synchronize()
+    xs = host(x.float())
+    hw, _ = moe.gemv(xs, (wg, wu, gguf.random_experts(rng, E, H, I, t)), slots, topk, (t, t, t))
+    got = host(h)
+    assert (got[4] == 0).all()
+    assert moe.rel_l2(got, hw) < 1e-5
+    # the prepared copy holds the same values as f16, at the unit dword / half the layout gives each element
+    hs = 32 if t == "Q4_K" else 16
+    halves = host(hp).view(np.float16).reshape(T * topk, I // 64, 72)
+    for e in (0, 1, 63, I - 1):
+        span, f = divmod(e % 64, 2 * hs)
+        hi, g = divmod(f, hs)
+        dw = span * hs + 4 * (g >> 2) + 2 * ((g & 3) & 1) + hi
+        half = (g & 3) >> 1
+        assert (halves[:, e // 64, 2 * dw + half].astype(np.float32) == got[:, e].astype(np.float16)).all()
+
+
 @pytest.mark.parametrize("T,k,E,H,I", [(1, 8, 16, 2048, 768), (3, 4, 10, 1024, 1408), (5, 10, 12, 512, 512)])
 def test_down_combine_vs_oracle(T, k, E, H, I):
     from larder_amd import _lib
@@ -126,8 +162,8 @@ def test_down_combine_vs_oracle(T, k, E, H, I):
     gate = rng.standard_normal((T, 3)).astype(np.float32)
     res = rng.standard_normal((T, H)).astype(np.float16)
     out = torch.empty((T, H), dtype=torch.float32, device="cuda")
-    hd, idd, scd, shd, gd, rd = dev(h), dev(ids), dev(sc), dev(shared), dev(gate), dev(res)
-    _lib.call("lmoe_gemv_down_combine", _lib.ptr(hd), _lib.ptr(idd), _lib.ptr(scd), T, k, _lib.ptr(dev(wd)),
+    hd, idd, scd, shd, gd, rd, wdd = dev(h), dev(ids), dev(sc), dev(shared), dev(gate), dev(res), dev(wd)
+    _lib.call("lmoe_gemv_down_combine", _lib.ptr(hd), _lib.ptr(idd), _lib.ptr(scd), T, k, _lib.ptr(wdd),
               _lib.Q4_0, E, I, H, _lib.ptr(shd), _lib.ptr(gd), 3, _lib.ptr(rd), _lib.F16, _lib.ptr(out), _lib.F32,
               _lib.stream())
     wdf = gguf.dequant_matrix(wd, "Q4_0")
