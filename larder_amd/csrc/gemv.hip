@@ -561,6 +561,119 @@ __global__ void __launch_bounds__(64 * NW, 3)
   }
 }
 
+// ---- down + combine with the h units in registers ---------------------------------------------------------------
+//
+// For prepared h and k P <= 64 NU (k experts of P = I / 64 units; NU = 1 or 2 units a lane), P even. Grid
+// (H / (4 RB), T), four independent wavefronts a workgroup (no barrier); wavefront w of block (bx, t) takes output
+// rows [(4 bx + w) RB, +RB) of token t. Lane l holds h units u = l, l + 64 (u = j P + p: expert j, unit p) in
+// registers and their half-unit sums, computed there while the weights are in flight. The wavefront's RB rows of all
+// k experts (k RB 36 P bytes) come in with 16-byte loads, go to its own LDS region, and each lane dots its units with
+// the RB rows of its expert (a 36-byte unit read a dot), weighted by the router score; the rows' sums over the
+// wavefront finish on DPP / permlane swaps, then the gated shared-expert row and the residual are added. Memory order:
+// h units, ids and scores (one a lane), then the weights, whose addresses need only the ids; no load is predicated
+// (clamped indices; expert 0 stands in for an id past the experts, with a zero weight).
+template <int TD, int NU, int NCW>
+__global__ void __launch_bounds__(256)
+    k_down_xr(const uint32_t *hprep, const uint32_t *ids, const float *scores, int k, const uint8_t *wd,
+              int n_experts, int I, int H, const float *shared, const float *gate, int gate_stride,
+              const void *residual, int rdt, void *out, int odt) {
+  constexpr int RB = 2;
+  const int P = I / 64, U = k * P;
+  const int CJ = RB * 9 * P / 4, CW = k * CJ;  // 16-byte chunks of one expert's RB rows, of all k
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.y;
+  const int n0 = (blockIdx.x * 4 + wave) * RB;
+  extern __shared__ u32x4 lds4[];
+  uint32_t *stage = reinterpret_cast<uint32_t *>(lds4) + wave * (CW * 4);
+
+  // 1. the token's ids and scores (lane j < k holds expert j's), then the h units. The empty asm with a memory
+  // clobber keeps the compiler from sinking these loads below the weights' (the count of outstanding loads is in
+  // order, so the weight addresses then wait only for the ids and scores, and the h sums only for the h units)
+  const int kl = min(lane, k - 1);
+  const uint32_t my_id = ids[size_t(t) * k + kl];
+  const float sc_ld = (scores ? scores + size_t(t) * k : reinterpret_cast<const float *>(ids))[kl];
+  const float my_sc = scores ? sc_ld : 1.0f;
+  const u32x4 *hb = reinterpret_cast<const u32x4 *>(hprep + size_t(t) * U * XS);
+  u32x4 hq[NU][9];
+#pragma unroll
+  for (int a = 0; a < NU; ++a) {
+    const int u = min(lane + 64 * a, U - 1);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) hq[a][i] = hb[u * 9 + i];
+  }
+  asm volatile("" ::: "memory");
+  // 2. the weights: chunk c of expert j's block at rows [n0, n0 + RB)
+  const size_t rowb = size_t(36) * P, nsafe = size_t(min(n0, H - RB));
+  u32x4 w[NCW];
+#pragma unroll
+  for (int i = 0; i < NCW; ++i) {
+    const int c = min(lane + 64 * i, CW - 1);
+    const int j = c / CJ, cc = c - j * CJ;
+    uint32_t e = uint32_t(__shfl(int(my_id), j, 64));
+    e = e < uint32_t(n_experts) ? e : 0u;
+    w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wd + (size_t(e) * H + nsafe) * rowb) + cc);
+  }
+  asm volatile("" ::: "memory");
+  // 3. each unit's expert, weight (0 past the units or the experts) and half-unit sums
+  int ja[NU], pa[NU];
+  float fa[NU], s0[NU], s1[NU];
+  uint32_t xv[NU][32];
+  const h2_t one2 = {_Float16(1.0f), _Float16(1.0f)};
+#pragma unroll
+  for (int a = 0; a < NU; ++a) {
+    const int u = lane + 64 * a, uc = min(u, U - 1);
+    ja[a] = uc / P;
+    pa[a] = uc - ja[a] * P;
+    const uint32_t e = uint32_t(__shfl(int(my_id), ja[a], 64));
+    const float sj = __shfl(my_sc, ja[a], 64);
+    fa[a] = (u < U && e < uint32_t(n_experts)) ? sj : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xv[a][4 * i] = hq[a][i].x;
+      xv[a][4 * i + 1] = hq[a][i].y;
+      xv[a][4 * i + 2] = hq[a][i].z;
+      xv[a][4 * i + 3] = hq[a][i].w;
+    }
+    float x0 = 0.0f, x1 = 0.0f;  // a unit's first / last 32 values: dwords 0..15 / 16..31 (Q4_0), even / odd (Q4_K)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t d0 = TD == LMOE_Q4_K ? xv[a][2 * i] : xv[a][i];
+      const uint32_t d1 = TD == LMOE_Q4_K ? xv[a][2 * i + 1] : xv[a][16 + i];
+      x0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, d0), one2, x0, false);
+      x1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, d1), one2, x1, false);
+    }
+    s0[a] = x0;
+    s1[a] = x1;
+  }
+  // 4. the weights into the wavefront's stage (no branch between loads and stores)
+  u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
+#pragma unroll
+  for (int i = 0; i < NCW; ++i) st4[min(lane + 64 * i, CW - 1)] = w[i];
+  __builtin_amdgcn_wave_barrier();
+  if (n0 >= H) return;
+  // 5. dots
+  float acc[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int a = 0; a < NU; ++a)
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      acc[r] = fmaf(fa[a], row_unit_dot_r<TD>(stage + (ja[a] * RB + r) * 9 * P, pa[a], xv[a], s0[a], s1[a]), acc[r]);
+  // 6. the rows' sums, then shared expert and residual
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane < RB) {
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < RB; ++r) v = lane == r ? acc[r] : v;
+    const size_t o = size_t(t) * H + n0 + lane;
+    if (shared) v += sigmoidf_(gate[size_t(t) * gate_stride]) * shared[o];
+    if (residual) v += load_elt(residual, o, rdt);
+    store_elt(out, o, v, odt);
+  }
+}
+
 // ---- host dispatch ----------------------------------------------------------------------------------------------
 
 struct GateUpArgs {
@@ -699,6 +812,39 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   if (a.T == 0) return 0;
   LMOE_REQUIRE((a.h || a.hprep) && a.ids && a.out, LMOE_EINVAL, "%s: null pointer", fn);
   LMOE_REQUIRE(a.hprep ? aligned16(a.hprep) : aligned16(a.h), LMOE_EALIGN, "%s: h must be 16-byte aligned", fn);
+  hipStream_t st = (hipStream_t)stream;
+  {  // prepared h, at most 128 units a token, P even, H a multiple of 8: the register-resident kernel
+    const int P = a.I / 64, U = a.k * P, CW = a.k * 9 * P / 2;
+    if (a.hprep && U <= 128 && P % 2 == 0 && a.H % 8 == 0 && CW <= 64 * 9) {
+      const int NU = U <= 64 ? 1 : 2, ncw = (CW + 63) / 64;
+      auto go = [&](auto td, auto nu, auto nc) {
+        constexpr int TD = decltype(td)::value, N = decltype(nu)::value, C = decltype(nc)::value;
+        launch(k_down_xr<TD, N, C>, dim3(a.H / 8, a.T), dim3(256), size_t(4) * 4 * CW * 4, st, a.hprep, a.ids,
+               a.scores, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt,
+               a.out, a.odt);
+      };
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using C5 = std::integral_constant<int, 5>;
+      using C7 = std::integral_constant<int, 7>;
+      using C9 = std::integral_constant<int, 9>;
+      auto by_c = [&](auto td, auto nu) {
+        if (ncw <= 5) go(td, nu, C5());
+        else if (ncw <= 7) go(td, nu, C7());
+        else go(td, nu, C9());
+      };
+      auto by_nu = [&](auto td) {
+        if (NU == 1) by_c(td, I1());
+        else by_c(td, I2());
+      };
+      if (a.type_d == LMOE_Q4_0)
+        by_nu(std::integral_constant<int, LMOE_Q4_0>());
+      else
+        by_nu(std::integral_constant<int, LMOE_Q4_K>());
+      LMOE_LAUNCHED(fn);
+      return 0;
+    }
+  }
   constexpr int NW = 2, NC = 16;
   const int P = a.I / 64;
   const int RB = P % 2 == 0 ? 2 : 4;
@@ -708,7 +854,6 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
                                   NW * RB * (a.k * P + 1));
   LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "%s: k %d at width %d needs %zu bytes of LDS", fn, a.k, a.I, lds);
   const dim3 grid((a.H + RB * NW - 1) / (RB * NW), a.T);
-  hipStream_t st = (hipStream_t)stream;
   // weights fetched into registers ahead of the h staging when a wavefront's k RB rows fit in NC chunks a lane
   const bool pre = size_t(a.k) * RB * 9 * P / 4 <= size_t(64) * NC;
   auto pick = [&](auto td, auto rb) {
