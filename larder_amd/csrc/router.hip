@@ -2,9 +2,9 @@
 //
 // The reference runs the gate linear as an MLX matmul and the top-k in moe_probs, one 32-lane warp a row doing k
 // rounds of shuffle argmax (route_cuda.py:193-254). Here:
-//   * k_router_gemv spreads the E router rows over wavefronts (one row each, all T tokens), the row's weights
-//     fetched with 16-byte loads while x is staged in LDS, and emits the prepared activation rows the expert
-//     kernels read (lmoe_common.h), so no later kernel rearranges x again;
+//   * k_router_gemv gives each router row a workgroup (256 threads, 8 weights a thread a step, x read straight
+//     into registers), and emits the prepared activation rows the expert kernels read (lmoe_common.h), so no
+//     later kernel rearranges x again;
 //   * k_router_topk takes k rounds of a wavefront argmax, one wavefront a token, its max and min-index reductions
 //     on DPP and gfx950's permlane swaps rather than LDS shuffles.
 // Selection is on the fp32 logits, larger first, ties to the lower expert index; scores are the softmax
@@ -39,110 +39,90 @@ __global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt
   }
 }
 
-constexpr int kRouterWaves = 4;
 constexpr int kRouterMaxT = 16;
-constexpr int kRouterMaxXs = 16384;  // T * H floats of x held in LDS
-constexpr int kRouterNc = 16;        // 16-byte weight chunks a lane (H * element size <= 16 KiB)
+constexpr int kRouterMaxNi = 4;  // 8-weight items a thread: H <= 8192
 
-// Each wavefront one router row (the last row the shared-expert gate when wsg is given) for all T tokens: its
-// weight chunks load first, x is staged in LDS as f32 meanwhile. When xprep is given the workgroups also write
-// the prepared activation rows for block type TQ, a slice of units each. WDT: the weights' element type.
-template <int WDT, int TQ, int XB>
-__global__ void __launch_bounds__(64 * kRouterWaves)
+// 8 values at element index i of a row of dtype dt, from one or two 16-byte chunks already loaded
+__device__ __forceinline__ void unpack8(const u32x4 &a, const u32x4 &b, int dt, float *v) {
+  const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  if (dt == LMOE_F32) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(u[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = dt == LMOE_F16 ? half_lo(u[e]) : __uint_as_float(u[e] << 16);
+      v[2 * e + 1] = dt == LMOE_F16 ? half_hi(u[e]) : __uint_as_float(u[e] & 0xFFFF0000u);
+    }
+  }
+}
+
+// One workgroup a router row (row E: the shared-expert gate, when wsg is given). Thread i holds the row's 8-weight
+// items i, i + 256, ... (NI of them, 16-byte loads issued first) and, token by token, the matching 8 values of x
+// straight from memory (no staging); a wavefront sum and a fixed-order sum of the four wavefronts' partials give
+// the logit. Workgroups past the rows write the prepared activation units for block type TQ (when xprep is given),
+// four units a workgroup, one a wavefront through its own LDS. WDT: the weights' element type.
+template <int WDT, int TQ, int NI>
+__global__ void __launch_bounds__(256)
     k_router_gemv(const void *x, int xdt, const void *wr, const void *wsg, int T, int H, int E, float *logits,
                   uint32_t *xprep) {
-  constexpr int EPC = WDT == LMOE_F32 ? 4 : 8;  // elements a 16-byte chunk
-  __shared__ float xs[kRouterMaxXs];
+  constexpr int WQ = WDT == LMOE_F32 ? 2 : 1;  // 16-byte chunks an item of weights
+  __shared__ float part[4][kRouterMaxT];
+  __shared__ float xu[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rows = E + (wsg != nullptr ? 1 : 0);
-  const int row = blockIdx.x * kRouterWaves + wave;
-  const int nch = H / EPC;
-  // x's 16-byte chunks (XB a thread, XB * 256 >= T H / elements a chunk) go out first, since they gate the LDS
-  // staging; then the row's weights, needed only by the dot. No load is predicated (indices clamped; a wavefront
-  // past the last row re-reads it), so each group issues back to back.
-  const int epc = xdt == LMOE_F32 ? 4 : 8, nx = T * H / epc;
-  const u32x4 *x4 = static_cast<const u32x4 *>(x);
-  constexpr int NT = 64 * kRouterWaves;
-  u32x4 xv[XB];
-#pragma unroll
-  for (int j = 0; j < XB; ++j) xv[j] = x4[min(int(threadIdx.x) + j * NT, nx - 1)];
-  u32x4 w[kRouterNc];
-  {
-    const int rs = min(row, rows - 1);
-    const u32x4 *src = reinterpret_cast<const u32x4 *>(rs < E ? static_cast<const char *>(wr) +
-                                                                    size_t(rs) * H * (WDT == LMOE_F32 ? 4 : 2)
-                                                              : static_cast<const char *>(wsg));
-#pragma unroll
-    for (int i = 0; i < kRouterNc; ++i) w[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, nch - 1));
+  const int row = blockIdx.x;
+  const int nit = H / 8;
+  if (row >= rows) {  // a prepared-activation workgroup: one unit a wavefront, wavefront-private LDS
+    const int P = H / 64;
+    const int u = (row - rows) * 4 + wave;
+    if (u >= T * P) return;
+    const int t = u / P, p = u - t * P;
+    xu[wave][lane] = load_elt(x, size_t(t) * H + 64 * p + lane, xdt);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < XS) xprep[size_t(u) * XS + lane] = prep_dword<TQ>([&](int i) { return xu[wave][i]; }, 0, lane);
+    return;
   }
-  // x into LDS as f32
+  const u32x4 *w4 = reinterpret_cast<const u32x4 *>(
+      row < E ? static_cast<const char *>(wr) + size_t(row) * H * (WDT == LMOE_F32 ? 4 : 2)
+              : static_cast<const char *>(wsg));
+  u32x4 wq[NI][2];
 #pragma unroll
-  for (int j = 0; j < XB; ++j) {
-    const int q = threadIdx.x + j * NT;
-    if (q >= nx) continue;
-    const uint32_t u[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-    float *o = xs + q * epc;
-    if (xdt == LMOE_F32) {
-      *reinterpret_cast<float4 *>(o) =
-          float4{__uint_as_float(u[0]), __uint_as_float(u[1]), __uint_as_float(u[2]), __uint_as_float(u[3])};
-    } else {
-      float f[8];
+  for (int i = 0; i < NI; ++i) {
+    const int it = min(int(threadIdx.x) + 256 * i, nit - 1);  // not predicated: past the row, the last item again
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f[2 * i] = xdt == LMOE_F16 ? half_lo(u[i]) : __uint_as_float(u[i] << 16);
-        f[2 * i + 1] = xdt == LMOE_F16 ? half_hi(u[i]) : __uint_as_float(u[i] & 0xFFFF0000u);
-      }
-      *reinterpret_cast<float4 *>(o) = float4{f[0], f[1], f[2], f[3]};
-      *reinterpret_cast<float4 *>(o + 4) = float4{f[4], f[5], f[6], f[7]};
+    for (int q = 0; q < WQ; ++q) wq[i][q] = __builtin_nontemporal_load(w4 + it * WQ + q);
+  }
+  float wv[NI][8];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) unpack8(wq[i][0], wq[i][WQ - 1], WDT, wv[i]);
+  const int xq = xdt == LMOE_F32 ? 2 : 1;  // 16-byte chunks an item of x
+  for (int t = 0; t < T; ++t) {
+    const u32x4 *x4 = reinterpret_cast<const u32x4 *>(static_cast<const char *>(x) +
+                                                      size_t(t) * H * (xdt == LMOE_F32 ? 4 : 2));
+    u32x4 xc[NI][2];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int it = min(int(threadIdx.x) + 256 * i, nit - 1);
+      xc[i][0] = x4[it * xq];
+      xc[i][1] = x4[it * xq + xq - 1];
     }
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      if (int(threadIdx.x) + 256 * i >= nit) continue;
+      float xv[8];
+      unpack8(xc[i][0], xc[i][1], xdt, xv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf(xv[e], wv[i][e], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) part[wave][t] = acc;
   }
   __syncthreads();
-  if (xprep) {  // prepared rows: units spread over the workgroups
-    const int P = H / 64, units = T * P;
-    const int per = (units + gridDim.x - 1) / gridDim.x;
-    const int u0 = blockIdx.x * per, u1 = min(units, u0 + per);
-    for (int idx = u0 * XS + threadIdx.x; idx < u1 * XS; idx += 64 * kRouterWaves) {
-      const int u = idx / XS, dw = idx - u * XS, t = u / P, p = u - t * P;
-      const float *xt = xs + t * H;
-      xprep[size_t(u) * XS + dw] = prep_dword<TQ>([&](int i) { return xt[i]; }, p, dw);
-    }
-  }
-  if (row >= rows) return;
-  float acc[kRouterMaxT];
-#pragma unroll
-  for (int t = 0; t < kRouterMaxT; ++t) acc[t] = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kRouterNc; ++i) {
-    const int c = lane + 64 * i;
-    if (c < nch) {
-      float wv[EPC];
-      const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (WDT == LMOE_F32) {
-          wv[j] = __uint_as_float(u[j]);
-        } else if (WDT == LMOE_F16) {
-          wv[2 * j] = half_lo(u[j]);
-          wv[2 * j + 1] = half_hi(u[j]);
-        } else {
-          wv[2 * j] = __uint_as_float(u[j] << 16);
-          wv[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
-        }
-      }
-      for (int t = 0; t < T; ++t) {
-        const float *xt = xs + t * H + c * EPC;
-#pragma unroll
-        for (int j = 0; j < EPC; ++j) acc[t] = fmaf(xt[j], wv[j], acc[t]);
-      }
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < kRouterMaxT; ++t) {
-    if (t < T) {
-      const float v = wave_sum(acc[t]);
-      if (lane == 0) logits[size_t(t) * rows + row] = v;
-    }
-  }
+  if (threadIdx.x < T)
+    logits[size_t(threadIdx.x) * rows + row] =
+        ((part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x]) + part[3][threadIdx.x];
 }
 
 // Prepared activation rows on their own: one workgroup a row, one thread a unit dword.
@@ -159,17 +139,13 @@ __global__ void __launch_bounds__(256) k_prep_x(const void *x, int xdt, int H, u
 template <int WDT, int TQ>
 static void launch_router_q(dim3 grid, dim3 block, hipStream_t st, const void *x, int xdt, const void *wr,
                             const void *wsg, int T, int H, int E, float *logits, uint32_t *xprep) {
-  const int nx = T * H / (xdt == LMOE_F32 ? 4 : 8), xb = (nx + 64 * kRouterWaves - 1) / (64 * kRouterWaves);
-  if (xb <= 1)
+  const int ni = (H / 8 + 255) / 256;
+  if (ni <= 1)
     launch(k_router_gemv<WDT, TQ, 1>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
-  else if (xb <= 2)
+  else if (ni <= 2)
     launch(k_router_gemv<WDT, TQ, 2>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
-  else if (xb <= 4)
-    launch(k_router_gemv<WDT, TQ, 4>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
-  else if (xb <= 8)
-    launch(k_router_gemv<WDT, TQ, 8>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
   else
-    launch(k_router_gemv<WDT, TQ, 16>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+    launch(k_router_gemv<WDT, TQ, 4>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
 }
 
 template <int WDT>
@@ -241,12 +217,10 @@ extern "C" int lmoe_router_gemv(const void *x, int xdtype, const void *wr, const
   LMOE_REQUIRE(x && wr && logits, LMOE_EINVAL, "%s: null pointer", fn);
   LMOE_REQUIRE(aligned16(x) && aligned16(wr) && (!wsg || aligned16(wsg)), LMOE_EALIGN,
                "%s: x, wr and wsg must be 16-byte aligned", fn);
-  LMOE_REQUIRE(size_t(T) * H <= size_t(kRouterMaxXs), LMOE_ESHAPE,
-               "%s: %d tokens x hidden %d is above the %d activations this kernel stages", fn, T, H, kRouterMaxXs);
-  LMOE_REQUIRE(size_t(H) * (wdtype == LMOE_F32 ? 4 : 2) <= size_t(kRouterNc) * 64 * 16, LMOE_ESHAPE,
-               "%s: a router row of %d weights is above what a wavefront holds", fn, H);
+  LMOE_REQUIRE(H <= 8 * 256 * kRouterMaxNi, LMOE_ESHAPE, "%s: hidden %d is above the %d this kernel takes", fn, H,
+               8 * 256 * kRouterMaxNi);
   const int rows = E + (wsg ? 1 : 0);
-  const dim3 grid((rows + kRouterWaves - 1) / kRouterWaves), block(64 * kRouterWaves);
+  const dim3 grid(rows + (xprep ? (T * (H / 64) + 3) / 4 : 0)), block(256);
   hipStream_t st = (hipStream_t)stream;
   if (wdtype == LMOE_F16)
     launch_router<LMOE_F16>(qtype, grid, block, st, x, xdtype, wr, wsg, T, H, E, logits, xprep);
