@@ -284,10 +284,10 @@ __device__ __forceinline__ float row_unit_dot_r(const uint32_t *row, int p, cons
 // sum over the aligned group of P lanes (P = 32 or 64), the result in every lane of the group
 template <int P>
 __device__ __forceinline__ float group_sum(float v) {
+  if (P == 64) return wave_sum(v);
   v = sum16(v);
-  v += lane_xor16(v);
-  if (P == 64) v += lane_xor32(v);
-  return v;
+  const float g0 = lane_value(v, 0) + lane_value(v, 16), g1 = lane_value(v, 32) + lane_value(v, 48);
+  return (threadIdx.x & 32) ? g1 : g0;
 }
 
 // ---- gate/up with the activation unit in registers (H = 64 P, P = 32 or 64; one block type for gate and up) ----

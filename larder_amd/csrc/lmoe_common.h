@@ -191,20 +191,23 @@ __device__ __forceinline__ float sum16(float v) {
   v = sum8(v);
   return v + LMOE_DPP(v, kDppMirror);
 }
+// lane l's value (wave-uniform result)
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// The cross-row steps read the four rows' totals with readlane (scalar results, no lane exchange round trip);
+// the association, (row 0 + row 1) + (row 2 + row 3), is the pairwise tree of a butterfly, so every lane gets the
+// same bits a butterfly would give it.
 __device__ __forceinline__ float wave_sum(float v) {
   v = sum16(v);
-  v += lane_xor16(v);
-  v += lane_xor32(v);
-  return v;
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, LMOE_DPP(v, kDppXor1));
   v = fmaxf(v, LMOE_DPP(v, kDppXor2));
   v = fmaxf(v, LMOE_DPP(v, kDppHalfMirror));
   v = fmaxf(v, LMOE_DPP(v, kDppMirror));
-  v = fmaxf(v, lane_xor16(v));
-  v = fmaxf(v, lane_xor32(v));
-  return v;
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
 // ---- top-k over a wavefront -------------------------------------------------------------------------------
