@@ -24,7 +24,7 @@ HBM_PEAK = 8.0e12  # MI355X published HBM3E bandwidth, bytes/s
 MFMA_PEAK = 2.5e15  # MI355X dense f16 / bf16 matrix peak, flop/s
 # HBM bytes a launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled by a 256 MiB copy) at the cfg2 shape,
 # per kernel; see profiles/decode_cfg2_traffic.md for the commands. Reported as roofline.traffic for that kernel.
-MEASURED_TRAFFIC = {"k_down_combine": 7753318, "k_gate_up": 14439938, "k_router_gemv": 808960}
+MEASURED_TRAFFIC = {"k_gate_up_xr": 14373990, "k_down_xr": 7370547, "k_router_gemv": 615936}
 
 
 def parse():
@@ -81,8 +81,8 @@ def gpu_leg(args):
     # runtime records at the kernel's own begin and end (the timestamps rocprofv3 reads), on the stream it runs on
     k, I, H, E = cfg["k"], cfg["I"], cfg["H"], cfg["E"]
     per_layer = [("k_router_gemv", E * H * 2 + H * 2 + E * 4 + H // 64 * 144),
-                 ("k_gate_up", k * 2 * I * (H // 32 * 18) + E * 4 + H // 64 * 144 + k * (I // 64 * 144)),
-                 ("k_down_combine", k * H * (I // 32 * 18) + k * (I // 64 * 144) + 3 * H * 2)]
+                 ("k_gate_up_xr", k * 2 * I * (H // 32 * 18) + E * 4 + H // 64 * 144 + k * (I // 64 * 144)),
+                 ("k_down_xr", k * H * (I // 32 * 18) + k * (I // 64 * 144) + 3 * H * 2)]
     prof_steps = min(args.steps, 64)
     M = prof_steps * args.layers * len(per_layer)
     _lib.call("lmoe_profile_arm", M)
