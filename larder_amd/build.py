@@ -25,6 +25,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off", "-Xclang", "-target-feature",
           "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 
+# Per-file extras. grouped.hip: MFMA accumulators in arch VGPRs. Left to its heuristics the compiler puts them in
+# AGPRs with the untied MFMA form, and every K step then rotates them through ~130 accvgpr moves; in VGPRs they
+# stay put and the kernel fits two workgroups a CU (237 VGPRs, no AGPRs).
+FILE_FLAGS = {"grouped.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def _run(cmd):
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -42,7 +47,7 @@ def build(verbose=False):
     OUT_DIR.mkdir(exist_ok=True)
     srcs = sources()
     objs = [OUT_DIR / (s.stem + ".o") for s in srcs]
-    cmds = [[HIPCC, *CFLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(srcs, objs)]
+    cmds = [[HIPCC, *CFLAGS, *FILE_FLAGS.get(s.name, []), "-c", str(s), "-o", str(o)] for s, o in zip(srcs, objs)]
     with ThreadPoolExecutor(max_workers=min(8, len(cmds))) as ex:
         for c, _ in zip(cmds, ex.map(_run, cmds)):
             if verbose:
