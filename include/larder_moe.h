@@ -126,8 +126,9 @@ int lmoe_grouped_tile_rows(void);
 
 /* Grouped gate/up + SwiGLU on the matrix cores over rows grouped by lmoe_group_rows (bm = lmoe_grouped_tile_rows):
  *   h[p][f] = silu(x[order[p] / topk] . wg[e][f]) * (x[order[p] / topk] . wu[e][f])  for grouped row p of expert e,
- * h [R][I] float16 in grouped order (rows past offsets[E] untouched). x [T][H] float16 (xdtype must be LMOE_F16:
- * convert other activations once with lmoe_to_f16); wg / wu [E][I][row bytes], one ggml type (Q4_0 or Q4_K);
+ * h [R][I] float16 in grouped order (rows past offsets[E] untouched), each row in the GEMM K order (below).
+ * x [T][H] float16 in the GEMM K order (xdtype must be LMOE_F16: lmoe_to_gemm_f16 makes it from any activation
+ * dtype); wg / wu [E][I][row bytes], one ggml type (Q4_0 or Q4_K);
  * H a multiple of 64 (Q4_K: 256), I of 128. The work list is read on the device: max_tiles = lmoe_max_tiles(R, E,
  * bm). Replaces the reference's dense path dequant + gather_mm gate/up + silu-mul (gguf_experts.py:698-720;
  * DEQ_SRC :529-539). */
@@ -137,15 +138,22 @@ int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, const uint3
                          void *stream);
 
 /* Grouped down on the matrix cores: y[p][n] = h[p] . wd[e][n] for grouped row p of expert e, y [R][H] in ydtype
- * (F16 / F32) in grouped order, unweighted. h [R][I] float16 as lmoe_grouped_gate_up leaves it; I a multiple of
+ * (F16 / F32) in grouped order, natural columns, unweighted. h [R][I] float16 in the GEMM K order, as
+ * lmoe_grouped_gate_up leaves it; I a multiple of
  * 64 (Q4_K: 256), H of 256. Replaces the dense path's gather_mm down (gguf_experts.py:720-721). */
 int lmoe_grouped_down(const void *h, const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
                       int max_tiles, const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
                       void *stream);
 
-/* x [n] (F32 / BF16 / F16) -> out [n] float16, round to nearest even: the grouped GEMMs' activation operand.
+/* x [n] (F32 / BF16 / F16) -> out [n] float16, round to nearest even.
  * No counterpart in the reference (its dense path casts with MLX, gguf_experts.py:716). */
 int lmoe_to_f16(const void *x, int xdtype, long long n, void *out, void *stream);
+
+/* The grouped GEMMs' activation operand: x [n] (F32 / BF16 / F16, rows of a length divisible by 32, n % 32 == 0,
+ * x and out 16-byte aligned) -> out [n] float16 (round to nearest even) in the GEMM K order: inside every 32-wide
+ * block the elements run 0-3, 16-19, 4-7, 20-23, 8-11, 24-27, 12-15, 28-31. In that order each matrix-core lane's
+ * 8 weights are the low and high nibbles of one 4-byte word of a Q4 block. No counterpart in the reference. */
+int lmoe_to_gemm_f16(const void *x, int xdtype, long long n, void *out, void *stream);
 
 /* Weighted combine of rows kept in grouped (expert-sorted) order:
  *   out[t][n] = sum_j scores[t][j] * y[inv[t * k + j]][n] (+ sigmoid(gate) * shared) (+ residual)

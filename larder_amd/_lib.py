@@ -44,6 +44,7 @@ SIGNATURES = {
     "lmoe_max_tiles": (_I, [_I, _I, _I]),
     "lmoe_grouped_tile_rows": (_I, []),
     "lmoe_to_f16": (_I, [_P, _I, _LL, _P, _P]),
+    "lmoe_to_gemm_f16": (_I, [_P, _I, _LL, _P, _P]),
     "lmoe_grouped_gate_up": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "lmoe_grouped_down": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_combine_sorted": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),

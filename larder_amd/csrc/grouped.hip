@@ -9,21 +9,22 @@
 //     dealt round-robin over the 8 XCDs, so the linear id is remapped to give each XCD one contiguous stretch of
 //     work (neighbouring n-tiles of one m-tile share A rows and the expert's weights in that XCD's L2);
 //   * four wavefronts, each 128 rows x 64 features (8 x 4 accumulators of 16 x 16). The A tile (128 rows x 64 of
-//     K, f16: x gathered through the grouped order, or the grouped h rows) goes through LDS, shared by the four;
-//     the weights do not: each K step, thread t loads the Q4 unit (64 weights) of tile feature t and repacks it
-//     into LDS as one nibble word per (MFMA K slice, lane group) plus its scales, so an MFMA lane reads one word
-//     and one scale word and decodes its 8 weights to f16 in registers (w = ((1024 + q) - 1032) d for Q4_0,
-//     ((1024 + q) - 1024) (d sc) - dmin m for Q4_K), straight into the MFMA's weight operand. LDS then carries
-//     the A tile (16 KB written, 64 KB read a step) and 10 KB of packed weights instead of a 32 KB f16 weight
-//     tile written and read twice;
-//   * the global loads of step k + 1 are in flight while step k's MFMAs run; one barrier a step;
+//     K, f16: x gathered through the grouped order, or the grouped h rows) goes through LDS, shared by the four.
+//     The weights reach LDS as raw Q4 bytes (Q4_0) or as one nibble word per (MFMA K slice, lane group) plus
+//     scales (Q4_K), and each MFMA lane decodes its own 8 weights to f16 in registers, straight into the MFMA's
+//     weight operand: w = ((1024 + q) - 1032) d for Q4_0, ((1024 + q) - 1024) (d sc) - dmin m for Q4_K;
+//   * the K order. Inside every 32-wide block of K the GEMMs take the elements in the order
+//     0-3, 16-19, 4-7, 20-23, 8-11, 24-27, 12-15, 28-31 (kperm): then MFMA lane group g's 8 weights are the low
+//     and high nibbles of qs bytes 4g..4g+3, one Q4 word. x comes in that order (lmoe_to_gemm_f16), gate/up writes
+//     h in it, and down reads it; results are the same sums, in another order;
+//   * Q4_0 (k_grouped_q4_0): A and the raw weight units go global -> LDS directly (global_load_lds, no registers,
+//     no VALU), two K steps ahead through a ring of three LDS stages, one barrier a step. Q4_K (k_grouped_q4_k):
+//     thread t loads the unit of tile feature t into registers one step ahead and repacks it with its scales;
 //   * the weights are the MFMA's first operand, so each lane ends with 4 consecutive output features of one row;
 //     gate/up tiles hold 128 gate and 128 up features (a wavefront: 32 of each, the same ones), SwiGLU happens in
 //     registers and h leaves as f16 in grouped row order. Down writes y [R][H] (f16 or f32) in grouped order.
 // Operands are f16 with fp32 accumulation. A single rounding of (q - 8) d to f16 keeps the layer well inside the
 // 2e-3 relative L2 bar; bf16 operands would not.
-#include <type_traits>
-
 #include "lmoe_common.h"
 
 namespace lmoe {
@@ -36,16 +37,19 @@ constexpr int GM = 128;  // rows a tile (the grouping kernel's bm)
 constexpr int GN = 256;  // weight rows a tile (gate/up: 128 gate + 128 up features; down: 256 outputs)
 constexpr int GK = 64;   // K a step (one 64-weight unit of every weight row)
 constexpr int kThreads = 256;
-constexpr int kWp = 10;  // LDS words a weight row a step: 8 nibble words, 2 scale words
 constexpr int kTileMask = (1 << 20) - 1;
 
 enum { MODE_GATE_UP = 0, MODE_DOWN = 1 };
 
-template <int N>
-using IC = std::integral_constant<int, N>;
-
 // 16-byte chunk c (0..7) of A row r in a stage: rows are 128 bytes, chunks XOR-swizzled by the row's low 3 bits
 __device__ __forceinline__ int achunk(int r, int c) { return r * 8 + (c ^ (r & 7)); }
+
+// Position of natural element n (a multiple of 4) of a row in the GEMMs' K order: within each 32-wide block,
+// group n4 = (n % 32) / 4 sits at 8 n4 (n4 < 4) or 8 (n4 - 4) + 4
+__device__ __forceinline__ int kperm4(int n) {
+  const int n4 = (n & 31) >> 2;
+  return (n & ~31) | (n4 < 4 ? 8 * n4 : 8 * (n4 - 4) + 4);
+}
 
 // two f16 (1024 + q) from a byte-wise masked word: {q0, q1} or {q2, q3}
 __device__ __forceinline__ uint32_t magic_pair(uint32_t nib, uint32_t sel) {
@@ -53,83 +57,17 @@ __device__ __forceinline__ uint32_t magic_pair(uint32_t nib, uint32_t sel) {
 }
 constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
 
-// Raw words of one weight row's unit kk: Q4_0 the unit's 9 words (two 18-byte blocks); Q4_K the super-block's
-// header (d, dmin, 12 scale bytes) and the 8 qs words of sub-block pair kk % 4
+// An MFMA lane's 8 f16 weights from its nibble word x (low nibbles: K positions 0-3 of the lane group, high
+// nibbles: 4-7). Q4_0: w = ((1024 + q) - 1032) d, d = the selected half of sw. Q4_K: sw = {f16(d sc), f16(dmin m)},
+// w = ((1024 + q) - 1024) (d sc) - dmin m.
 template <int TB>
-struct RawW {
-  static constexpr int N = TB == LMOE_Q4_0 ? 9 : 12;
-};
-
-template <int TB>
-__device__ __forceinline__ void load_w(const uint8_t *wrow, int kk, uint32_t *r) {
-  if (TB == LMOE_Q4_0) {
-    const uint32_t *u = reinterpret_cast<const uint32_t *>(wrow + size_t(kk) * 36);
-#pragma unroll
-    for (int i = 0; i < 9; ++i) r[i] = u[i];
-  } else {
-    const uint32_t *sb = reinterpret_cast<const uint32_t *>(wrow + size_t(kk >> 2) * 144);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = sb[i];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[4 + i] = sb[4 + 8 * (kk & 3) + i];
-  }
-}
-
-// 8 nibbles of bytes j (low nibble) and j + 4 (high nibble) of a byte group: weights 0..3 / 4..7 of an MFMA lane
-__device__ __forceinline__ uint32_t pack_lo(uint32_t w0, uint32_t w1) {
-  return (w0 & 0x0F0F0F0Fu) | ((w1 & 0x0F0F0F0Fu) << 4);
-}
-__device__ __forceinline__ uint32_t pack_hi(uint32_t w0, uint32_t w1) {
-  return ((w0 >> 4) & 0x0F0F0F0Fu) | (w1 & 0xF0F0F0F0u);
-}
-
-// A unit's packed words: o[4 ks + g] holds the weights 32 ks + 8 g .. + 7 of the unit (MFMA K slice ks, lane group
-// g) as nibbles, o[8 + ks] the slice's scales. Q4_0 slice ks is block ks (qs byte i: weight i low, i + 16 high):
-// lane group g reads bytes 8 (g % 2) .. + 7, low nibbles for g < 2; scales {d0, d1} in o[8]. Q4_K slice ks is
-// sub-block 2 (kk % 4) + ks, the low (ks = 0) or high (ks = 1) nibbles of the pair's bytes 8 g .. 8 g + 7;
-// o[8 + ks] = {f16(d sc), f16(dmin m)} of that sub-block (get_scale_min_k4, gguf_ref.py:253-258).
-template <int TB>
-__device__ __forceinline__ void pack_w(const uint32_t *r, int kk, uint32_t *o) {
-  if (TB == LMOE_Q4_0) {
-    uint32_t q0[4];  // block 0's qs start at unit byte 2
-#pragma unroll
-    for (int i = 0; i < 4; ++i) q0[i] = __builtin_amdgcn_alignbyte(r[i + 1], r[i], 2);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const uint32_t *q = ks ? r + 5 : q0;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        o[4 * ks + b] = pack_lo(q[2 * b], q[2 * b + 1]);
-        o[4 * ks + 2 + b] = pack_hi(q[2 * b], q[2 * b + 1]);
-      }
-    }
-    o[8] = (r[0] & 0xFFFFu) | (r[4] & 0xFFFF0000u);
-    o[9] = 0u;
-  } else {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      o[g] = pack_lo(r[4 + 2 * g], r[5 + 2 * g]);
-      o[4 + g] = pack_hi(r[4 + 2 * g], r[5 + 2 * g]);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      float sc, mn;
-      k4_scale_min(r[1], r[2], r[3], 2 * (kk & 3) + ks, &sc, &mn);
-      const h2_t v = {_Float16(half_lo(r[0]) * sc), _Float16(half_hi(r[0]) * mn)};
-      o[8 + ks] = __builtin_bit_cast(uint32_t, v);
-    }
-  }
-}
-
-// An MFMA lane's 8 f16 weights from its packed word and the slice's scale word
-template <int TB>
-__device__ __forceinline__ half8 decode8(uint32_t x, uint32_t sw, int ks) {
+__device__ __forceinline__ half8 decode8(uint32_t x, uint32_t sw, int half) {
   const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
   const h2_t p[4] = {__builtin_bit_cast(h2_t, magic_pair(lo, kSel01)), __builtin_bit_cast(h2_t, magic_pair(lo, kSel23)),
                      __builtin_bit_cast(h2_t, magic_pair(hi, kSel01)), __builtin_bit_cast(h2_t, magic_pair(hi, kSel23))};
   h2_t bias, scale, sub;
   if (TB == LMOE_Q4_0) {
-    const _Float16 d = __builtin_bit_cast(h2_t, sw)[ks];
+    const _Float16 d = __builtin_bit_cast(h2_t, sw)[half];
     bias = h2_t{_Float16(1032.0f), _Float16(1032.0f)};
     scale = h2_t{d, d};
     sub = h2_t{_Float16(0.0f), _Float16(0.0f)};
@@ -145,61 +83,335 @@ __device__ __forceinline__ half8 decode8(uint32_t x, uint32_t sw, int ks) {
   return __builtin_bit_cast(half8, u32x4{o[0], o[1], o[2], o[3]});
 }
 
-// Grid: n_ntile * max_tiles workgroups of 256 threads (1-D), two a CU. GATE_UP: n-tile j covers intermediate
-// features 128 j .. 128 j + 127 (tile features 0..127 their gate rows, 128..255 their up rows), K = H, A rows
-// x[order[p] / topk], out h [R][I] f16. DOWN: n-tile j covers output features 256 j .., K = I, A rows h[p], out
-// y [R][H] in odt (F16 / F32).
-template <int MODE, int TB>
-__global__ void __launch_bounds__(kThreads, 2)
-k_grouped(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets, const uint32_t *tiles,
-          const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1, int K, int n_rows, void *out,
-          int ldo, int odt) {
-  // A tile: rows of 64 halves = 8 swizzled 16-byte chunks; packed weights: kWp words a tile feature; 2 stages each
-  __shared__ __attribute__((aligned(16))) u32x4 As[2][GM * 8];
-  __shared__ __attribute__((aligned(16))) uint32_t Wp[2][GN * kWp];
+// Tile bookkeeping shared by both kernels
+struct Tile {
+  int e, nt, row0, rows;
+};
 
-  // XCD-aware remap: workgroup `wid` runs on XCD wid % 8; XCD x gets logical work [start_x, start_x + count_x)
+// XCD-aware remap: workgroup `wid` runs on XCD wid % 8; XCD x gets logical work [start_x, start_x + count_x).
+// Returns false for workgroups past the device-side work count.
+__device__ __forceinline__ bool tile_of(const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
+                                        int n_ntile, Tile *t) {
   const uint32_t W = n_tiles[0] * uint32_t(n_ntile);
   const uint32_t wid = blockIdx.x;
-  if (wid >= W) return;
+  if (wid >= W) return false;
   const uint32_t q8 = W >> 3, r8 = W & 7, xcd = wid & 7;
   const uint32_t logical = xcd * q8 + min(xcd, r8) + (wid >> 3);
   const uint32_t tile = tiles[logical / uint32_t(n_ntile)];
-  const int nt = int(logical % uint32_t(n_ntile));
-  const int e = int(tile >> 20);
-  const int row0 = int(offsets[e]) + int(tile & kTileMask) * GM;
-  const int rows = min(GM, int(offsets[e + 1]) - row0);
+  t->nt = int(logical % uint32_t(n_ntile));
+  t->e = int(tile >> 20);
+  t->row0 = int(offsets[t->e]) + int(tile & kTileMask) * GM;
+  t->rows = min(GM, int(offsets[t->e + 1]) - t->row0);
+  return true;
+}
 
+// Tile features of a wavefront's 4 fragments: gate/up: gate 32 w + 16 nb (nb < 2), up 128 + 32 w + 16 (nb - 2)
+// (the same intermediate features); down: 64 w + 16 nb
+template <int MODE>
+__device__ __forceinline__ int frag_feature(int wave, int nb) {
+  return MODE == MODE_GATE_UP ? (nb < 2 ? 32 * wave + 16 * nb : GN / 2 + 32 * wave + 16 * (nb - 2))
+                              : 64 * wave + 16 * nb;
+}
+
+// acc[nb][mb][r] = D[tile feature frag_feature(nb) + 4 g + r][tile row 16 mb + fr]. Gate/up: h (f16, K order) =
+// silu(gate) * up; down: y (F32 / F16, natural order).
+template <int MODE>
+__device__ __forceinline__ void store_tile(f32x4 (&acc)[4][8], const Tile &t, int wave, int fr, int g, void *out,
+                                           int ldo, int odt) {
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) {
+    const int m = 16 * mb + fr;
+    if (m >= t.rows) continue;
+    const size_t o = size_t(t.row0 + m) * ldo;
+    if (MODE == MODE_GATE_UP) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        h2_t v01 = {_Float16(silu_mul(acc[nb][mb][0], acc[nb + 2][mb][0])),
+                    _Float16(silu_mul(acc[nb][mb][1], acc[nb + 2][mb][1]))};
+        h2_t v23 = {_Float16(silu_mul(acc[nb][mb][2], acc[nb + 2][mb][2])),
+                    _Float16(silu_mul(acc[nb][mb][3], acc[nb + 2][mb][3]))};
+        const int n = t.nt * (GN / 2) + frag_feature<MODE>(wave, nb) + 4 * g;
+        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + kperm4(n)) =
+            u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
+      }
+    } else if (odt == LMOE_F32) {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        *reinterpret_cast<f32x4 *>(static_cast<float *>(out) + o + t.nt * GN + frag_feature<MODE>(wave, nb) +
+                                   4 * g) = acc[nb][mb];
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        h2_t v01 = {_Float16(acc[nb][mb][0]), _Float16(acc[nb][mb][1])};
+        h2_t v23 = {_Float16(acc[nb][mb][2]), _Float16(acc[nb][mb][3])};
+        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + t.nt * GN + frag_feature<MODE>(wave, nb) +
+                                   4 * g) = u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
+      }
+    }
+  }
+}
+
+// ---- Q4_0: global -> LDS directly, three stages ------------------------------------------------------------------
+
+constexpr int kQ0AStage = GM * 128;             // A tile bytes a stage
+constexpr int kQ0WHead = GN * 32;               // the first 32 bytes of every unit (words 0-7), 32 a feature
+constexpr int kQ0Stage = kQ0AStage + GN * 36;   // + word 8 of every unit, 4 bytes a feature: 25600
+constexpr int kQ0DmaA = GM * 128 / 1024 / 4;    // 16-byte A copies a lane a step (4)
+constexpr int kQ0DmaW = GN * 32 / 1024 / 4;     // 16-byte unit-head copies a lane a step (2), plus one 4-byte copy
+
+// One wavefront-wide global -> LDS copy: lane l's `BYTES` (4 or 16) at base + voff land at LDS address
+// lds + l * BYTES (global_load_lds_dwordx3 would also step 16 bytes a lane). M0 carries the LDS address; nothing
+// else in these kernels uses M0.
+template <int BYTES>
+__device__ __forceinline__ void dma(const void *base, uint32_t voff, uint32_t lds) {
+  if (BYTES == 16)
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "memory");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "memory");
+}
+
+// s_barrier with compiler memory fences on both sides: the intrinsic alone does not order memory accesses, and
+// __syncthreads' release fence would wait for every copy in flight, including the ones meant to stay in flight
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Grid: n_ntile * max_tiles workgroups of 256 threads, two a CU. GATE_UP: n-tile j covers intermediate features
+// 128 j .. 128 j + 127 (tile features 0..127 their gate rows, 128..255 their up rows), K = H, A rows
+// x[order[p] / topk], out h [R][I] f16. DOWN: n-tile j covers output features 256 j .., K = I, A rows h[p], out
+// y [R][H] in odt (F16 / F32). Host guarantees: K % 64 == 0, rows x K x 2 and the expert's weight block under 4 GiB.
+template <int MODE>
+__global__ void __launch_bounds__(kThreads, 2)
+k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
+               const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
+               int K, int n_rows, void *out, int ldo, int odt) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kQ0Stage];
+  Tile t;
+  if (!tile_of(offsets, tiles, n_tiles, n_ntile, &t)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, g = lane >> 4;
+  const uint32_t wrow = 36u * uint32_t(K / 64);
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(lds));
+
+  // A: wavefront w's load i fills LDS bytes [1024 (4 w + i), +1024) of a stage: 16-byte granule q = 64 (4 w + i) +
+  // lane holds chunk (q % 8) ^ (r & 7) of tile row r = q / 8. Rows past the tile's end read its first row.
+  uint32_t a_off[kQ0DmaA];
+#pragma unroll
+  for (int i = 0; i < kQ0DmaA; ++i) {
+    const int q = 64 * (kQ0DmaA * wave + i) + lane, r = q >> 3, c = (q & 7) ^ (r & 7);
+    const int p = t.row0 + (r < t.rows ? r : 0);
+    const uint32_t row = MODE == MODE_GATE_UP ? order[p] / uint32_t(topk) : uint32_t(p);
+    a_off[i] = row * uint32_t(K) * 2u + 16u * uint32_t(c);
+  }
+  // weights: wavefront w covers tile features 64 w .. 64 w + 63 (gate/up: waves 0-1 gate rows, 2-3 up rows).
+  // Its 16-byte copy i fills bytes [1024 (2 w + i), +1024) of the stage's head area: granule q = 64 (2 w + i) +
+  // lane is half q % 2 of words 0-7 of tile feature q / 2 (heads at 32 f); its 4-byte copy puts word 8 of tile
+  // feature 64 w + lane at 4 f of the tail area.
+  const uint8_t *wbase;
+  uint32_t w_off[kQ0DmaW + 1];
+  {
+    const uint8_t *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
+    const int row_base = MODE == MODE_GATE_UP ? t.nt * (GN / 2) - (wave >= 2 ? GN / 2 : 0) : t.nt * GN;
+    wbase = m + (size_t(t.e) * n_rows) * wrow;
+#pragma unroll
+    for (int i = 0; i < kQ0DmaW; ++i) {
+      const int q = 64 * (kQ0DmaW * wave + i) + lane;
+      w_off[i] = uint32_t(row_base + (q >> 1)) * wrow + 16u * uint32_t(q & 1);
+    }
+    w_off[kQ0DmaW] = uint32_t(row_base + 64 * wave + lane) * wrow + 32u;
+  }
+  const int nk = K / GK;
+  auto issue = [&](int kk) {  // step kk into stage kk % 3
+    const uint32_t st = lds0 + uint32_t(kk % 3) * kQ0Stage;
+    const _Float16 *ab = a_src + size_t(kk) * GK;
+#pragma unroll
+    for (int i = 0; i < kQ0DmaA; ++i)
+      dma<16>(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kQ0DmaA * wave + i)));
+    const uint8_t *wb = wbase + size_t(kk) * 36;
+#pragma unroll
+    for (int i = 0; i < kQ0DmaW; ++i)
+      dma<16>(wb, w_off[i], __builtin_amdgcn_readfirstlane(st + kQ0AStage + 1024u * uint32_t(kQ0DmaW * wave + i)));
+    dma<4>(wb, w_off[kQ0DmaW], __builtin_amdgcn_readfirstlane(st + kQ0AStage + kQ0WHead + 256u * uint32_t(wave)));
+  };
+
+  int wfeat[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) wfeat[nb] = frag_feature<MODE>(wave, nb) + fr;
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // 64 MFMAs out of stage s. Lane (fr, g) of fragment nb decodes feature wfeat[nb]'s unit: block 0 qs bytes 4g..+3
+  // (unit bytes 2 + 4g.., straddling words g and g + 1), block 1 qs bytes 4g..+3 (word 5 + g; word 8 sits in the
+  // tail area), d0 / d1 in the low half of word 0 / the high half of word 4.
+  int w1_at[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+    w1_at[nb] = g < 3 ? kQ0AStage + 32 * wfeat[nb] + 4 * (5 + g) : kQ0AStage + kQ0WHead + 4 * wfeat[nb];
+  // The MFMA order is written out by hand. The step's 8 weight fragments (K slice ks = i / 4, fragment nb = i % 4)
+  // go in turn; fragment i's 8 MFMAs issue in pairs with a quarter of fragment i + 1's decode (4 VALU) between
+  // pairs, so the decode issues while the matrix core works; fragment i + 2's weight word is read from LDS one
+  // fragment ahead of its decode and the second K slice's A fragments two fragments ahead of their use.
+  // sched_barrier keeps the compiler from regrouping them.
+  auto compute = [&](int s) {
+    const uint8_t *st = lds + s * kQ0Stage;
+    const u32x4 *as = reinterpret_cast<const u32x4 *>(st);
+    auto word = [&](int i) -> uint32_t {
+      const int ks = i / 4, nb = i % 4;
+      const uint32_t *u = reinterpret_cast<const uint32_t *>(st + kQ0AStage + 32 * wfeat[nb]);
+      return ks == 0 ? __builtin_amdgcn_alignbyte(u[g + 1], u[g], 2)
+                     : *reinterpret_cast<const uint32_t *>(st + w1_at[nb]);
+    };
+    auto scale = [&](int i) -> uint32_t {
+      return reinterpret_cast<const uint32_t *>(st + kQ0AStage + 32 * wfeat[i % 4])[4 * (i / 4)];
+    };
+    const h2_t bias = {_Float16(1032.0f), _Float16(1032.0f)};
+    half8 xf[2][8];
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) xf[0][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, g)]);
+    uint32_t xw[8], sw[8];  // fully unrolled: each element lives in its own registers
+    xw[0] = word(0);
+    sw[0] = scale(0);
+    xw[1] = word(1);
+    sw[1] = scale(1);
+    u32x4 wcur = __builtin_bit_cast(u32x4, decode8<LMOE_Q4_0>(xw[0], sw[0], 0));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int ks = i / 4, nb = i % 4;
+      if (i + 2 < 8) {
+        xw[i + 2] = word(i + 2);
+        sw[i + 2] = scale(i + 2);
+      }
+      if (i == 2) {
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb) xf[1][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 + g)]);
+      }
+      const int n = i + 1 < 8 ? i + 1 : 7;  // the next fragment (a repeat of the last, unused, after it)
+      const _Float16 d = __builtin_bit_cast(h2_t, sw[n])[n / 4];
+      const h2_t dd = {d, d};
+      uint32_t lo = 0, hi = 0;
+      u32x4 wnext;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[nb][2 * q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur), xf[ks][2 * q],
+                                                                 acc[nb][2 * q], 0, 0, 0);
+        acc[nb][2 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur),
+                                                                     xf[ks][2 * q + 1], acc[nb][2 * q + 1], 0, 0, 0);
+        if (i + 1 < 8) {
+          if (q == 0) {
+            lo = xw[n] & 0x0F0F0F0Fu;
+            hi = (xw[n] >> 4) & 0x0F0F0F0Fu;
+          }
+          const uint32_t p = magic_pair(q < 2 ? lo : hi, q % 2 == 0 ? kSel01 : kSel23);
+          wnext[q] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2_t, p) - bias) * dd);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (i + 1 < 8) wcur = wnext;
+    }
+  };
+
+  // Step kk: the copies of step kk + 2 go out, step kk multiplies out of its stage, then each wavefront waits for
+  // its own copies of step kk + 1 (the counter counts in issue order: the 7 copies of kk + 2 may still be out)
+  // and the barrier publishes the stage. The barrier also tells the step after that stage kk % 3,
+  // which it refills, has been read by every wavefront.
+  issue(0);
+  if (nk > 1) {
+    issue(1);
+    asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  static_assert(kQ0DmaA + kQ0DmaW + 1 == 7, "the wait counts below assume 7 copies a step");
+  barrier_lds();
+  for (int kk = 0; kk < nk; ++kk) {
+    const bool more = kk + 2 < nk;
+    if (more) issue(kk + 2);
+    compute(kk % 3);
+    if (kk + 1 < nk) {
+      if (more)
+        asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      barrier_lds();
+    }
+  }
+  store_tile<MODE>(acc, t, wave, fr, g, out, ldo, odt);
+}
+
+// ---- Q4_K: register staging with repack --------------------------------------------------------------------------
+
+constexpr int kWp = 10;  // LDS words a weight row a step: 8 nibble words, 2 scale words
+
+// The super-block header (d, dmin, 12 scale bytes) and the 8 qs words of sub-block pair kk % 4 of a row
+__device__ __forceinline__ void load_w_q4_k(const uint8_t *wrow, int kk, uint32_t *r) {
+  const uint32_t *sb = reinterpret_cast<const uint32_t *>(wrow + size_t(kk >> 2) * 144);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = sb[i];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[4 + i] = sb[4 + 8 * (kk & 3) + i];
+}
+
+// o[4 ks + g]: slice ks = sub-block 2 (kk % 4) + ks (the low / high nibbles of the pair's 32 bytes); lane group g
+// takes bytes 4g..4g+3 (low nibbles of the word) and 16 + 4g.. (high nibbles). o[8 + ks] = {f16(d sc), f16(dmin m)}
+// of that sub-block (get_scale_min_k4, gguf_ref.py:253-258).
+__device__ __forceinline__ void pack_w_q4_k(const uint32_t *r, int kk, uint32_t *o) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t a = r[4 + g], b = r[8 + g];
+    o[g] = (a & 0x0F0F0F0Fu) | ((b & 0x0F0F0F0Fu) << 4);
+    o[4 + g] = ((a >> 4) & 0x0F0F0F0Fu) | (b & 0xF0F0F0F0u);
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    float sc, mn;
+    k4_scale_min(r[1], r[2], r[3], 2 * (kk & 3) + ks, &sc, &mn);
+    const h2_t v = {_Float16(half_lo(r[0]) * sc), _Float16(half_hi(r[0]) * mn)};
+    o[8 + ks] = __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+// Same grid and arguments as k_grouped_q4_0.
+template <int MODE>
+__global__ void __launch_bounds__(kThreads, 2)
+k_grouped_q4_k(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
+               const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
+               int K, int n_rows, void *out, int ldo, int odt) {
+  // A tile: rows of 64 halves = 8 swizzled 16-byte chunks; packed weights: kWp words a tile feature; 2 stages each
+  __shared__ __attribute__((aligned(16))) u32x4 As[2][GM * 8];
+  __shared__ __attribute__((aligned(16))) uint32_t Wp[2][GN * kWp];
+  Tile t;
+  if (!tile_of(offsets, tiles, n_tiles, n_ntile, &t)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
-  const size_t wrow_bytes = size_t(36) * (K / 64);
+  const size_t wrow_bytes = size_t(144) * (K / 256);
 
   // A staging: thread -> tile row ar = tid >> 1, chunks 4 ac .. 4 ac + 3 (64 contiguous bytes of the step).
   // Rows past the tile's end read the tile's first row instead (their results are never stored).
   const int ar = tid >> 1, ac = tid & 1;
   const u32x4 *a_ptr;
   {
-    const int p = row0 + (ar < rows ? ar : 0);
+    const int p = t.row0 + (ar < t.rows ? ar : 0);
     const size_t r = MODE == MODE_GATE_UP ? size_t(order[p] / uint32_t(topk)) : size_t(p);
     a_ptr = reinterpret_cast<const u32x4 *>(a_src + r * K + 32 * ac);
   }
   // weight staging: thread -> tile feature tid
   const uint8_t *w_row;
   if (MODE == MODE_GATE_UP)
-    w_row = (tid < GN / 2 ? w0 : w1) + (size_t(e) * n_rows + nt * (GN / 2) + (tid % (GN / 2))) * wrow_bytes;
+    w_row = (tid < GN / 2 ? w0 : w1) + (size_t(t.e) * n_rows + t.nt * (GN / 2) + (tid % (GN / 2))) * wrow_bytes;
   else
-    w_row = w0 + (size_t(e) * n_rows + nt * GN + tid) * wrow_bytes;
+    w_row = w0 + (size_t(t.e) * n_rows + t.nt * GN + tid) * wrow_bytes;
 
-  // tile features of this wave's 4 fragments: gate/up: gate 32 w + 16 nb (nb < 2), up 128 + 32 w + 16 (nb - 2)
-  // (the same features); down: 64 w + 16 nb
-  int fbase[4];
+  int wfeat[4];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-    fbase[nb] = MODE == MODE_GATE_UP ? (nb < 2 ? 32 * wave + 16 * nb : GN / 2 + 32 * wave + 16 * (nb - 2))
-                                     : 64 * wave + 16 * nb;
+  for (int nb = 0; nb < 4; ++nb) wfeat[nb] = frag_feature<MODE>(wave, nb) + fr;
 
   u32x4 areg[4];
-  uint32_t wraw[RawW<TB>::N];
+  uint32_t wraw[12];
   f32x4 acc[4][8];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
@@ -207,7 +419,7 @@ k_grouped(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t
     for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto load = [&](int kk) {  // raw weights and A of step kk into registers
-    load_w<TB>(w_row, kk, wraw);
+    load_w_q4_k(w_row, kk, wraw);
 #pragma unroll
     for (int i = 0; i < 4; ++i) areg[i] = a_ptr[size_t(kk) * (GK / 8) + i];
   };
@@ -215,7 +427,7 @@ k_grouped(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t
 #pragma unroll
     for (int j = 0; j < 4; ++j) As[l][achunk(ar, 4 * ac + j)] = areg[j];
     uint32_t o[kWp];
-    pack_w<TB>(wraw, kk, o);
+    pack_w_q4_k(wraw, kk, o);
 #pragma unroll
     for (int j = 0; j < kWp; ++j) Wp[l][tid * kWp + j] = o[j];
   };
@@ -226,10 +438,8 @@ k_grouped(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t
     for (int ks = 0; ks < 2; ++ks) {
       half8 wf[4];
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const int f = fbase[nb] + fr;
-        wf[nb] = decode8<TB>(Wp[l][f * kWp + 4 * ks + g], Wp[l][f * kWp + 8 + (TB == LMOE_Q4_K ? ks : 0)], ks);
-      }
+      for (int nb = 0; nb < 4; ++nb)
+        wf[nb] = decode8<LMOE_Q4_K>(Wp[l][wfeat[nb] * kWp + 4 * ks + g], Wp[l][wfeat[nb] * kWp + 8 + ks], 0);
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb) {
         const half8 xf = __builtin_bit_cast(half8, As[l][achunk(16 * mb + fr, 4 * ks + g)]);
@@ -253,47 +463,29 @@ k_grouped(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t
     __syncthreads();
   }
   compute((nk - 1) & 1);
-
-  // acc[nb][mb][r] = D[tile feature fbase[nb] + 4 g + r][token row 16 mb + fr]
-#pragma unroll
-  for (int mb = 0; mb < 8; ++mb) {
-    const int m = 16 * mb + fr;
-    if (m >= rows) continue;
-    const size_t o = size_t(row0 + m) * ldo;
-    if (MODE == MODE_GATE_UP) {
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        h2_t v01 = {_Float16(silu_mul(acc[nb][mb][0], acc[nb + 2][mb][0])),
-                    _Float16(silu_mul(acc[nb][mb][1], acc[nb + 2][mb][1]))};
-        h2_t v23 = {_Float16(silu_mul(acc[nb][mb][2], acc[nb + 2][mb][2])),
-                    _Float16(silu_mul(acc[nb][mb][3], acc[nb + 2][mb][3]))};
-        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + nt * (GN / 2) + fbase[nb] + 4 * g) =
-            u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
-      }
-    } else if (odt == LMOE_F32) {
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        *reinterpret_cast<f32x4 *>(static_cast<float *>(out) + o + nt * GN + fbase[nb] + 4 * g) = acc[nb][mb];
-    } else {
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        h2_t v01 = {_Float16(acc[nb][mb][0]), _Float16(acc[nb][mb][1])};
-        h2_t v23 = {_Float16(acc[nb][mb][2]), _Float16(acc[nb][mb][3])};
-        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + nt * GN + fbase[nb] + 4 * g) =
-            u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
-      }
-    }
-  }
+  store_tile<MODE>(acc, t, wave, fr, g, out, ldo, odt);
 }
 
-// x [n] in dt -> f16 (round to nearest even), 8 elements a thread (vector loads when the whole range allows)
-__global__ void __launch_bounds__(256) k_to_f16(const void *x, int dt, long long n, _Float16 *out, int vec) {
+// x [n] in dt -> f16 (round to nearest even), 8 elements a thread (vector loads when the whole range allows).
+// kperm: element i lands at its position in the grouped GEMMs' K order (n % 32 == 0, vector path only).
+__global__ void __launch_bounds__(256) k_to_f16(const void *x, int dt, long long n, _Float16 *out, int vec,
+                                                int kperm) {
   const long long i0 = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 8;
   if (i0 >= n) return;
   if (vec) {
     float v[8];
     load8(x, size_t(i0), dt, v);
-    store8(out, size_t(i0), LMOE_F16, v);
+    if (kperm) {
+      const long long b = i0 & ~31ll;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const h2_t p0 = {_Float16(v[4 * h]), _Float16(v[4 * h + 1])}, p1 = {_Float16(v[4 * h + 2]), _Float16(v[4 * h + 3])};
+        *reinterpret_cast<u32x2 *>(out + b + kperm4(int(i0 & 31) + 4 * h)) =
+            u32x2{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1)};
+      }
+    } else {
+      store8(out, size_t(i0), LMOE_F16, v);
+    }
     return;
   }
   const int cnt = int(min(8ll, n - i0));
@@ -308,19 +500,28 @@ using namespace lmoe;
 
 extern "C" int lmoe_grouped_tile_rows(void) { return GM; }
 
-extern "C" int lmoe_to_f16(const void *x, int xdtype, long long n, void *out, void *stream) {
-  const char *fn = "lmoe_to_f16";
+static int to_f16(const char *fn, const void *x, int xdtype, long long n, void *out, void *stream, int kperm) {
   LMOE_REQUIRE(dtype_ok(xdtype), LMOE_EINVAL, "%s: bad dtype", fn);
   LMOE_REQUIRE(n >= 0, LMOE_ESHAPE, "%s: negative length", fn);
+  LMOE_REQUIRE(!kperm || n % 32 == 0, LMOE_ESHAPE, "%s: length %lld is not a multiple of 32", fn, n);
   if (n == 0) return 0;
   LMOE_REQUIRE(x && out, LMOE_EINVAL, "%s: null pointer", fn);
   const long long blocks = (n + 2047) / 2048;
   LMOE_REQUIRE(blocks < (1ll << 31), LMOE_ESHAPE, "%s: %lld elements", fn, n);
   const int vec = n % 8 == 0 && aligned16(x) && aligned16(out);
+  LMOE_REQUIRE(vec || !kperm, LMOE_EALIGN, "%s: x and out must be 16-byte aligned", fn);
   launch(k_to_f16, dim3(unsigned(blocks)), dim3(256), 0, (hipStream_t)stream, x, xdtype, n,
-         static_cast<_Float16 *>(out), vec);
+         static_cast<_Float16 *>(out), vec, kperm);
   LMOE_LAUNCHED(fn);
   return 0;
+}
+
+extern "C" int lmoe_to_f16(const void *x, int xdtype, long long n, void *out, void *stream) {
+  return to_f16("lmoe_to_f16", x, xdtype, n, out, stream, 0);
+}
+
+extern "C" int lmoe_to_gemm_f16(const void *x, int xdtype, long long n, void *out, void *stream) {
+  return to_f16("lmoe_to_gemm_f16", x, xdtype, n, out, stream, 1);
 }
 
 extern "C" int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, const uint32_t *order,
@@ -333,7 +534,7 @@ extern "C" int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, 
   LMOE_REQUIRE(type_g == type_u, LMOE_ETYPE, "%s: gate and up must share one type on this path (%d vs %d)", fn,
                type_g, type_u);
   LMOE_REQUIRE(xdtype == LMOE_F16, LMOE_EINVAL,
-               "%s: x must be float16 here (convert once with lmoe_to_f16; the matrix cores read f16)", fn);
+               "%s: x must be float16 in the GEMM K order here (convert once with lmoe_to_gemm_f16)", fn);
   LMOE_REQUIRE(T >= 0 && topk > 0 && n_experts > 0 && max_tiles >= 0, LMOE_ESHAPE, "%s: bad shape", fn);
   LMOE_REQUIRE(H > 0 && H % block_weights(type_g) == 0 && H % 64 == 0, LMOE_ESHAPE,
                "%s: hidden size %d is not a multiple of %d", fn, H, type_g == LMOE_Q4_K ? 256 : 64);
@@ -348,12 +549,15 @@ extern "C" int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, 
   LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
   hipStream_t st = (hipStream_t)stream;
   const _Float16 *a = static_cast<const _Float16 *>(x);
-  if (type_g == LMOE_Q4_0)
-    launch(k_grouped<MODE_GATE_UP, LMOE_Q4_0>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets,
-           tiles, n_tiles, n_ntile, wg, wu, H, I, h, I, int(LMOE_F16));
-  else
-    launch(k_grouped<MODE_GATE_UP, LMOE_Q4_K>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets,
-           tiles, n_tiles, n_ntile, wg, wu, H, I, h, I, int(LMOE_F16));
+  if (type_g == LMOE_Q4_0) {
+    LMOE_REQUIRE((long long)T * H * 2 <= 0xFFFFFFFFll && (long long)I * (H / 64) * 36 <= 0xFFFFFFFFll, LMOE_ESHAPE,
+                 "%s: x or one expert's weights exceed 4 GiB", fn);
+    launch(k_grouped_q4_0<MODE_GATE_UP>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles,
+           n_tiles, n_ntile, wg, wu, H, I, h, I, int(LMOE_F16));
+  } else {
+    launch(k_grouped_q4_k<MODE_GATE_UP>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles,
+           n_tiles, n_ntile, wg, wu, H, I, h, I, int(LMOE_F16));
+  }
   LMOE_LAUNCHED(fn);
   return 0;
 }
@@ -377,14 +581,18 @@ extern "C" int lmoe_grouped_down(const void *h, const uint32_t *offsets, const u
   LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
   hipStream_t st = (hipStream_t)stream;
   const _Float16 *a = static_cast<const _Float16 *>(h);
-  if (type_d == LMOE_Q4_0)
-    launch(k_grouped<MODE_DOWN, LMOE_Q4_0>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1,
+  if (type_d == LMOE_Q4_0) {
+    // R is not passed: offsets[E] <= max_tiles * bm rows of h can be read
+    LMOE_REQUIRE((long long)max_tiles * GM * I * 2 <= 0xFFFFFFFFll && (long long)H * (I / 64) * 36 <= 0xFFFFFFFFll,
+                 LMOE_ESHAPE, "%s: h or one expert's weights exceed 4 GiB", fn);
+    launch(k_grouped_q4_0<MODE_DOWN>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1,
            static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile, wd,
            static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
-  else
-    launch(k_grouped<MODE_DOWN, LMOE_Q4_K>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1,
+  } else {
+    launch(k_grouped_q4_k<MODE_DOWN>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1,
            static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile, wd,
            static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
+  }
   LMOE_LAUNCHED(fn);
   return 0;
 }

@@ -68,23 +68,35 @@ class Grouping:
         return g
 
 
-def as_f16(x, out=None):
-    """x as a contiguous float16 tensor: x itself when it already is one, else converted on the device (into
-    ``out`` when given)."""
+def kperm_index(n, device="cuda"):
+    """Position of natural column j (0..n-1) in the grouped GEMMs' K order: within each 32-wide block the columns
+    run 0-3, 16-19, 4-7, 20-23, 8-11, 24-27, 12-15, 28-31."""
+    j = torch.arange(n, device=device)
+    g4 = (j % 32) // 4
+    return j - j % 32 + torch.where(g4 < 4, 8 * g4, 8 * (g4 - 4) + 4) + j % 4
+
+
+def as_gemm_f16(x, out=None):
+    """x [rows, K] as float16 in the grouped GEMMs' K order (lmoe_to_gemm_f16), into ``out`` when given."""
     x = x.contiguous()
-    if x.dtype == torch.float16:
-        return x
     if out is None:
         out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
-    call("lmoe_to_f16", ptr(x), dcode(x.dtype), x.numel(), ptr(out), stream())
+    call("lmoe_to_gemm_f16", ptr(x), dcode(x.dtype), x.numel(), ptr(out), stream())
     return out
 
 
-def gate_up(x, G, topk, wg, wu, types, h, xh=None):
-    """h [R, I] f16 (grouped order) = silu(x . wg) * (x . wu) over the grouping G of x's rows (row p reads x[order[p]
-    // topk]); x meets the weights as f16 (converted into ``xh`` when it is not)."""
+def from_kperm(h):
+    """h [rows, K] in the grouped GEMMs' K order (as gate_up leaves it) back in natural column order."""
+    return h[:, kperm_index(h.shape[1], h.device)]
+
+
+def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False):
+    """h [R, I] f16 (grouped order, columns in the GEMMs' K order: from_kperm undoes it) = silu(x . wg) * (x . wu)
+    over the grouping G of x's rows (row p reads x[order[p] // topk]); x [T, H] in natural order, any float dtype,
+    meets the weights as f16 in the K order (converted into ``xh``; prepped: x already is that form)."""
     tg, tu = qcode(types[0]), qcode(types[1])
-    x = as_f16(x, xh)
+    if not prepped:
+        x = as_gemm_f16(x, xh)
     T, H = x.shape
     E, I = wg.shape[0], wg.shape[1]
     call("lmoe_grouped_gate_up", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
@@ -93,7 +105,7 @@ def gate_up(x, G, topk, wg, wu, types, h, xh=None):
 
 
 def down(h, G, wd, t, y):
-    """y [R, H] (f16 / f32, grouped order) = h . wd over the grouping G."""
+    """y [R, H] (f16 / f32, grouped order, natural columns) = h . wd over the grouping G; h as gate_up leaves it."""
     E, H = wd.shape[0], wd.shape[1]
     I = h.shape[1]
     call("lmoe_grouped_down", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, ptr(wd), qcode(t),
@@ -167,13 +179,12 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
         sel = lg[:, :L.E].contiguous()
         call("lmoe_router_topk", ptr(sel), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
     B.G.run(B.ids.reshape(-1))
-    xh = as_f16(x, B.xh)
-    gate_up(xh, B.G, L.k, L.wg, L.wu, L.types, B.h)
+    gate_up(x, B.G, L.k, L.wg, L.wu, L.types, B.h, B.xh)
     down(B.h, B.G, L.wd, L.types[2], B.y)
     shared = gate = None
     if L.shared is not None:
         sg, su, sd = L.shared
-        gate_up(xh, B.Gs, 1, sg, su, L.types, B.hs)
+        gate_up(B.xh, B.Gs, 1, sg, su, L.types, B.hs, prepped=True)
         down(B.hs, B.Gs, sd, L.types[2], B.ys)
         shared = ptr(B.ys)
         gate = ctypes.c_void_p(B.logits.data_ptr() + L.E * B.logits.element_size())

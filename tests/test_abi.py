@@ -73,7 +73,7 @@ def test_grouped_refusals_without_a_gpu(built_lib):
     assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256 + 32, p, z) == _lib.ESHAPE
     assert L.lmoe_grouped_gate_up(p, 9, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, p, z) == _lib.EINVAL
     assert L.lmoe_grouped_gate_up(p, 2, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, p, z) == _lib.EINVAL
-    assert b"lmoe_to_f16" in L.lmoe_error()
+    assert b"lmoe_to_gemm_f16" in L.lmoe_error()
     assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 576, 200, p, z) == _lib.ESHAPE
     assert L.lmoe_grouped_gate_up(p, 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, z, z) == _lib.EINVAL
     assert L.lmoe_grouped_gate_up(ctypes.c_void_p(8), 1, 4, 1, p, p, p, p, 4, p, p, 2, 2, 4, 512, 256, p, z) == \
@@ -85,9 +85,23 @@ def test_grouped_refusals_without_a_gpu(built_lib):
     assert L.lmoe_grouped_down(p, p, p, p, 4, p, 2, 4, 320, 600, p, 1, z) == _lib.ESHAPE
     assert L.lmoe_to_f16(p, 7, 10, p, z) == _lib.EINVAL
     assert L.lmoe_to_f16(p, 0, -1, p, z) == _lib.ESHAPE
+    assert L.lmoe_to_gemm_f16(p, 0, 48, p, z) == _lib.ESHAPE  # not a multiple of 32
+    assert L.lmoe_to_gemm_f16(ctypes.c_void_p(8), 0, 64, p, z) == _lib.EALIGN
     assert L.lmoe_grouped_tile_rows() == 128
 
 
 def test_python_refuses_unsupported_types():
     with pytest.raises(ValueError, match="Q5_K"):
         _lib.qcode("Q5_K")
+
+
+def test_gemm_k_order_index():
+    """kperm_index against the order written out by hand: inside a 32-wide block, positions 0..31 hold natural
+    columns 0-3, 16-19, 4-7, 20-23, 8-11, 24-27, 12-15, 28-31."""
+    from larder_amd import grouped
+    block = [0, 1, 2, 3, 16, 17, 18, 19, 4, 5, 6, 7, 20, 21, 22, 23, 8, 9, 10, 11, 24, 25, 26, 27,
+             12, 13, 14, 15, 28, 29, 30, 31]
+    pos = grouped.kperm_index(96, "cpu").tolist()
+    for j in range(96):
+        assert 32 * (j // 32) + block[pos[j] % 32] == j
+    assert sorted(pos) == list(range(96))

@@ -73,6 +73,16 @@ def test_expert_rows_vs_oracle(types, H, I, E, xdt):
     assert rows_ok(got[keep], want[keep]) < ROW_BAR
 
 
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32, torch.float16])
+def test_to_gemm_f16_k_order(xdt):
+    """lmoe_to_gemm_f16: every element rounded to f16 once and placed at its K-order position."""
+    from larder_amd import grouped
+    x = torch.randn((7, 160), device="cuda").to(xdt)
+    got = grouped.as_gemm_f16(x)
+    torch.cuda.synchronize()
+    assert torch.equal(got[:, grouped.kperm_index(160)], x.half())
+
+
 @pytest.mark.parametrize("types,H,I,E", MIXES[:2])
 def test_gate_up_h_matches_oracle(types, H, I, E):
     """h in grouped order against the oracle's h, element by element (f16 output rounding plus f16 weights)."""
@@ -88,7 +98,7 @@ def test_gate_up_h_matches_oracle(types, H, I, E):
     grouped.gate_up(x, G, k, dev(w[0]), dev(w[1]), types, h)
     order = host(G.order)
     hw, _ = moe.gemv(host(x.float()), w, ids.reshape(-1), k, types)
-    got = host(h.float())
+    got = host(grouped.from_kperm(h).float())
     assert moe.rel_l2(got, hw[order]) < BAR
     assert rows_ok(got, hw[order]) < ROW_BAR
 
