@@ -207,8 +207,10 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   }
   // weights: wavefront w covers tile features 64 w .. 64 w + 63 (gate/up: waves 0-1 gate rows, 2-3 up rows).
   // Its 16-byte copy i fills bytes [1024 (2 w + i), +1024) of the stage's head area: granule q = 64 (2 w + i) +
-  // lane is half q % 2 of words 0-7 of tile feature q / 2 (heads at 32 f); its 4-byte copy puts word 8 of tile
-  // feature 64 w + lane at 4 f of the tail area.
+  // lane is half h = (q / 16) % 2 (words 4h .. 4h + 3) of tile feature f = 16 (q / 32) + q % 16. So each group of
+  // 16 features keeps its 16 first halves in one 256-byte row and its 16 second halves in the next: the 16
+  // features an MFMA fragment reads sit in 16 different 16-byte columns, and its 64 lanes in 64 different banks.
+  // Its 4-byte copy puts word 8 of tile feature 64 w + lane at 4 f of the tail area.
   const uint8_t *wbase;
   uint32_t w_off[kQ0DmaW + 1];
   {
@@ -218,7 +220,7 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
 #pragma unroll
     for (int i = 0; i < kQ0DmaW; ++i) {
       const int q = 64 * (kQ0DmaW * wave + i) + lane;
-      w_off[i] = uint32_t(row_base + (q >> 1)) * wrow + 16u * uint32_t(q & 1);
+      w_off[i] = uint32_t(row_base + 16 * (q >> 5) + (q & 15)) * wrow + 16u * uint32_t((q >> 4) & 1);
     }
     w_off[kQ0DmaW] = uint32_t(row_base + 64 * wave + lane) * wrow + 32u;
   }
@@ -245,13 +247,17 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // 64 MFMAs out of stage s. Lane (fr, g) of fragment nb decodes feature wfeat[nb]'s unit: block 0 qs bytes 4g..+3
-  // (unit bytes 2 + 4g.., straddling words g and g + 1), block 1 qs bytes 4g..+3 (word 5 + g; word 8 sits in the
-  // tail area), d0 / d1 in the low half of word 0 / the high half of word 4.
-  int w1_at[4];
+  // Lane (fr, g) of fragment nb decodes feature wfeat[nb]'s unit: block 0 qs bytes 4g..+3 (unit bytes 2 + 4g..,
+  // straddling words g and g + 1), block 1 qs bytes 4g..+3 (word 5 + g; word 8 sits in the tail area), d0 / d1 in
+  // the low half of word 0 / the high half of word 4. Byte offsets in a stage: the feature's first half at
+  // head[nb], its second half 256 bytes on; word g + 1 at head[nb] + w1_of; block 1's word at blk1[nb].
+  int head[4], blk1[4];
+  const int w1_of = g < 3 ? 4 * g + 4 : 256;
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-    w1_at[nb] = g < 3 ? kQ0AStage + 32 * wfeat[nb] + 4 * (5 + g) : kQ0AStage + kQ0WHead + 4 * wfeat[nb];
+  for (int nb = 0; nb < 4; ++nb) {
+    head[nb] = kQ0AStage + 512 * (wfeat[nb] >> 4) + 16 * (wfeat[nb] & 15);
+    blk1[nb] = g < 3 ? head[nb] + 256 + 4 * (1 + g) : kQ0AStage + kQ0WHead + 4 * wfeat[nb];
+  }
   // The MFMA order is written out by hand. The step's 8 weight fragments (K slice ks = i / 4, fragment nb = i % 4)
   // go in turn; fragment i's 8 MFMAs issue in pairs with a quarter of fragment i + 1's decode (4 VALU) between
   // pairs, so the decode issues while the matrix core works; fragment i + 2's weight word is read from LDS one
@@ -260,15 +266,12 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   auto compute = [&](int s) {
     const uint8_t *st = lds + s * kQ0Stage;
     const u32x4 *as = reinterpret_cast<const u32x4 *>(st);
+    auto at = [&](int byte) -> uint32_t { return *reinterpret_cast<const uint32_t *>(st + byte); };
     auto word = [&](int i) -> uint32_t {
       const int ks = i / 4, nb = i % 4;
-      const uint32_t *u = reinterpret_cast<const uint32_t *>(st + kQ0AStage + 32 * wfeat[nb]);
-      return ks == 0 ? __builtin_amdgcn_alignbyte(u[g + 1], u[g], 2)
-                     : *reinterpret_cast<const uint32_t *>(st + w1_at[nb]);
+      return ks == 0 ? __builtin_amdgcn_alignbyte(at(head[nb] + w1_of), at(head[nb] + 4 * g), 2) : at(blk1[nb]);
     };
-    auto scale = [&](int i) -> uint32_t {
-      return reinterpret_cast<const uint32_t *>(st + kQ0AStage + 32 * wfeat[i % 4])[4 * (i / 4)];
-    };
+    auto scale = [&](int i) -> uint32_t { return at(head[i % 4] + 256 * (i / 4)); };
     const h2_t bias = {_Float16(1032.0f), _Float16(1032.0f)};
     half8 xf[2][8];
 #pragma unroll
