@@ -36,6 +36,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-grouped", action="store_true", help="skip the cfg3 prefill / cfg4 batched lines")
+    ap.add_argument("--grouped-only", action="store_true",
+                    help="run only the grouped-path lines (cfg3 prefill, cfg4, cfg5) and print them: a short run to "
+                         "profile the grouped GEMMs with rocprofv3 counters, not a benchmark line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (the scale for rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE counters)")
@@ -299,6 +302,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.grouped_only:
+        print(json.dumps({"secondary": grouped_leg()}), flush=True)
+        return
     g = gpu_leg(args)
     cpu = None if args.no_cpu else cpu_leg(args, g)
     secondary = None if args.no_grouped else grouped_leg()
