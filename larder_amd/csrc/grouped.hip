@@ -25,9 +25,14 @@
 //     registers and h leaves as f16 in grouped row order. Down writes y [R][H] (f16 or f32) in grouped order.
 // Operands are f16 with fp32 accumulation. A single rounding of (q - 8) d to f16 keeps the layer well inside the
 // 2e-3 relative L2 bar; bf16 operands would not.
+#include <type_traits>
+
 #include "lmoe_common.h"
 
 namespace lmoe {
+
+template <int N>
+using IC = std::integral_constant<int, N>;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -262,8 +267,10 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   // go in turn; fragment i's 8 MFMAs issue in pairs with a quarter of fragment i + 1's decode (4 VALU) between
   // pairs, so the decode issues while the matrix core works; fragment i + 2's weight word is read from LDS one
   // fragment ahead of its decode and the second K slice's A fragments two fragments ahead of their use.
-  // sched_barrier keeps the compiler from regrouping them.
-  auto compute = [&](int s) {
+  // sched_barrier keeps the compiler from regrouping them. QN: the 32-row pairs of fragments the tile has rows
+  // in (a tile's last m-tile is often short): the MFMAs and A reads of empty pairs are left out.
+  auto compute = [&](int s, auto qn) {
+    constexpr int QN = decltype(qn)::value;
     const uint8_t *st = lds + s * kQ0Stage;
     const u32x4 *as = reinterpret_cast<const u32x4 *>(st);
     auto at = [&](int byte) -> uint32_t { return *reinterpret_cast<const uint32_t *>(st + byte); };
@@ -275,7 +282,7 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
     const h2_t bias = {_Float16(1032.0f), _Float16(1032.0f)};
     half8 xf[2][8];
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) xf[0][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, g)]);
+    for (int mb = 0; mb < 2 * QN; ++mb) xf[0][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, g)]);
     uint32_t xw[8], sw[8];  // fully unrolled: each element lives in its own registers
     xw[0] = word(0);
     sw[0] = scale(0);
@@ -291,7 +298,7 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
       }
       if (i == 2) {
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb) xf[1][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 + g)]);
+        for (int mb = 0; mb < 2 * QN; ++mb) xf[1][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 + g)]);
       }
       const int n = i + 1 < 8 ? i + 1 : 7;  // the next fragment (a repeat of the last, unused, after it)
       const _Float16 d = __builtin_bit_cast(h2_t, sw[n])[n / 4];
@@ -300,10 +307,12 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
       u32x4 wnext;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        acc[nb][2 * q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur), xf[ks][2 * q],
-                                                                 acc[nb][2 * q], 0, 0, 0);
-        acc[nb][2 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur),
-                                                                     xf[ks][2 * q + 1], acc[nb][2 * q + 1], 0, 0, 0);
+        if (q < QN) {
+          acc[nb][2 * q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur), xf[ks][2 * q],
+                                                                   acc[nb][2 * q], 0, 0, 0);
+          acc[nb][2 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur),
+                                                                       xf[ks][2 * q + 1], acc[nb][2 * q + 1], 0, 0, 0);
+        }
         if (i + 1 < 8) {
           if (q == 0) {
             lo = xw[n] & 0x0F0F0F0Fu;
@@ -331,17 +340,25 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   }
   static_assert(kQ0DmaA + kQ0DmaW + 1 == 7, "the wait counts below assume 7 copies a step");
   barrier_lds();
-  for (int kk = 0; kk < nk; ++kk) {
-    const bool more = kk + 2 < nk;
-    if (more) issue(kk + 2);
-    compute(kk % 3);
-    if (kk + 1 < nk) {
-      if (more)
-        asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      barrier_lds();
+  auto run = [&](auto qn) {
+    for (int kk = 0; kk < nk; ++kk) {
+      const bool more = kk + 2 < nk;
+      if (more) issue(kk + 2);
+      compute(kk % 3, qn);
+      if (kk + 1 < nk) {
+        if (more)
+          asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        barrier_lds();
+      }
     }
+  };
+  switch ((t.rows + 31) / 32) {  // uniform across the workgroup
+    case 1: run(IC<1>{}); break;
+    case 2: run(IC<2>{}); break;
+    case 3: run(IC<3>{}); break;
+    default: run(IC<4>{}); break;
   }
   store_tile<MODE>(acc, t, wave, fr, g, out, ldo, odt);
 }
@@ -436,7 +453,8 @@ k_grouped_q4_k(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   };
   // 64 MFMAs out of LDS stage l: per K slice, the 4 weight fragments are decoded from their packed words, then
   // each A fragment meets all 4
-  auto compute = [&](int l) {
+  auto compute = [&](int l, auto qn) {  // qn: the 32-row pairs the tile has rows in, as in the Q4_0 kernel
+    constexpr int QN = decltype(qn)::value;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       half8 wf[4];
@@ -444,7 +462,7 @@ k_grouped_q4_k(const _Float16 *a_src, int topk, const uint32_t *order, const uin
       for (int nb = 0; nb < 4; ++nb)
         wf[nb] = decode8<LMOE_Q4_K>(Wp[l][wfeat[nb] * kWp + 4 * ks + g], Wp[l][wfeat[nb] * kWp + 8 + ks], 0);
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
+      for (int mb = 0; mb < 2 * QN; ++mb) {
         const half8 xf = __builtin_bit_cast(half8, As[l][achunk(16 * mb + fr, 4 * ks + g)]);
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
@@ -458,14 +476,22 @@ k_grouped_q4_k(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   load(0);
   stage(0, 0);
   __syncthreads();
-  for (int kk = 0; kk + 1 < nk; ++kk) {
-    load(kk + 1);
-    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs (the scheduler sinks them otherwise)
-    compute(kk & 1);
-    stage((kk + 1) & 1, kk + 1);
-    __syncthreads();
+  auto run = [&](auto qn) {
+    for (int kk = 0; kk + 1 < nk; ++kk) {
+      load(kk + 1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs (the scheduler sinks them otherwise)
+      compute(kk & 1, qn);
+      stage((kk + 1) & 1, kk + 1);
+      __syncthreads();
+    }
+    compute((nk - 1) & 1, qn);
+  };
+  switch ((t.rows + 31) / 32) {  // uniform across the workgroup
+    case 1: run(IC<1>{}); break;
+    case 2: run(IC<2>{}); break;
+    case 3: run(IC<3>{}); break;
+    default: run(IC<4>{}); break;
   }
-  compute((nk - 1) & 1);
   store_tile<MODE>(acc, t, wave, fr, g, out, ldo, odt);
 }
 
