@@ -65,6 +65,19 @@ int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, const void 
                           int E, int k, int norm, float *logits, uint32_t *ids, float *scores, uint32_t *xprep,
                           int qtype, void *stream);
 
+/* The cache-biased route of route_cuda.route / route_cuda.bias_probs (route_cuda.py:42-121, 158-178, 306-417), which
+ * reproduce CacheBiasedMoE._select: per row of gates g [E] in gdtype T (softmax: the row holds logits and
+ * g = T(softmax)), spread = T(max g - min g), rank = float(g) + float(T(T(lam) * spread)) * m with m = mask[e]
+ * (mask NULL: table mode, m = 0 <= slot_of[e] < lim), inds = the k largest of rank with MLX's rule (equal values to
+ * the LARGER index; the k ascending, best last). With tau > 0 the budget: honest = the same on g, the two k-gate
+ * sums in T in MLX's row_reduce order, and honest replaces inds when T(m_h - m_b) > T(T(tau) * m_h).
+ * Outputs: inds [T][k] uint32; with slot_of: rhs [T][k] = max(slot_of[inds], 0) and ok [1] = all(slot_of[inds] >= 0)
+ * (either may be NULL); scores [T][k] in gdtype = the picked gates, divided by their sum (taken in output order in
+ * T) when norm, or NULL. T <= 16, E <= 1024, k <= 32. */
+int lmoe_route_bias(const void *gates, int gdtype, int T, int E, int k, const float *mask, const int32_t *slot_of,
+                    int lim, float lam, float tau, int softmax, int norm, uint32_t *inds, uint32_t *ok, int32_t *rhs,
+                    void *scores, void *stream);
+
 /* Decode chain, gate/up: h[s][i] = silu(x[s / topk] . wg[slots[s]][i]) * (x[s / topk] . wu[slots[s]][i]),
  * fp32. Replaces gguf_experts kernel gguf_gate_up (gguf_experts.py:452-495) as driven by _chain
  * (gguf_experts.py:610-623). x [n_slots / topk][H] in xdtype; slots >= n_experts give h rows of zeros.

@@ -22,7 +22,7 @@ DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 # ggml type name -> (ggml type id, weights a block, bytes a block) (gguf_ref.py:8-15)
 TYPES = {"Q4_0": (2, 32, 18), "Q4_K": (12, 256, 144)}
 
-_P, _I, _SZ, _LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_longlong
+_P, _I, _SZ, _LL, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_longlong, ctypes.c_float
 # name -> (restype, argtypes): every symbol include/larder_moe.h declares
 SIGNATURES = {
     "lmoe_error": (ctypes.c_char_p, []),
@@ -33,6 +33,7 @@ SIGNATURES = {
     "lmoe_prep_x": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "lmoe_router_gemv": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
     "lmoe_router_gemv_topk": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P]),
+    "lmoe_route_bias": (_I, [_P, _I, _I, _I, _I, _P, _P, _I, _F, _F, _I, _I, _P, _P, _P, _P, _P]),
     "lmoe_gemv_gate_up": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "lmoe_gemv_gate_up_prepped": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P]),
     "lmoe_moe_gate_up": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P]),

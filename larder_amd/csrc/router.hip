@@ -157,6 +157,232 @@ static void launch_router(int qt, dim3 grid, dim3 block, hipStream_t st, const v
     launch_router_q<WDT, LMOE_Q4_0>(grid, block, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
 }
 
+
+// ---- cache-biased route (route_cuda.route / bias_probs) -------------------------------------------------------
+//
+// The reference's CacheBiasedMoE selection as one kernel (route_cuda.py:42-174 route, 306-416 bias_probs), on its
+// own numeric contract: MLX's tie rule and output order (ties to the LARGER index, the k picks ascending, best
+// last), the bias and budget arithmetic in the gates' dtype T, and the budget's two k-gate sums in MLX's
+// row_reduce_simple order. One wavefront a row, one workgroup (T <= 16).
+
+constexpr int kRouteMaxT = 16;
+constexpr int kRouteMaxE = 1024;
+
+struct RouteArgs {
+  const void *gates;  // [T][E] in gdt: gates, or logits when softmax
+  int gdt, T, E, k;
+  const float *mask;      // [E], or nullptr: table mode, mask = 0 <= slot_of < lim
+  const int32_t *slot_of;  // [E] (nullptr: no table, no rhs / ok)
+  int lim;
+  float lam, tau;
+  int softmax, norm;
+  uint32_t *inds;  // [T][k]
+  uint32_t *ok;    // [1] or nullptr
+  int32_t *rhs;    // [T][k] or nullptr
+  void *scores;    // [T][k] in gdt, or nullptr
+};
+
+// x rounded to nearest even in dtype dt (the value as a float)
+__device__ __forceinline__ float round_dt(float x, int dt) {
+  if (dt == LMOE_F16) return float(_Float16(x));
+  if (dt == LMOE_BF16) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return x;  // NaN stays
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return __uint_as_float(u & 0xFFFF0000u);
+  }
+  return x;
+}
+
+// The k largest of v (expert lane + 64 j, j < NPL, E <= 64 NPL) by MLX's stable ascending sort read from the
+// back: equal values go to the larger index. Lanes < k get an expert in *idx and its position in the ascending
+// output (best at k - 1) in *pos. A 32-step bit search for the k-th largest key, then the keys above it and the
+// highest-index keys equal to it, compacted into lds (64 dwords), ranked by (key, index) descending.
+template <int NPL>
+__device__ void select_mlx(const float (&v)[NPL], int E, int k, uint32_t *lds, uint32_t *idx, int *pos) {
+  const int lane = threadIdx.x & 63;
+  uint32_t key[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) key[j] = lane + 64 * j < E ? logit_key(v[j]) : 0u;
+  uint32_t thr = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = thr | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+    thr = cnt >= k ? cand : thr;
+  }
+  int n_gt = 0;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) n_gt += __popcll(__ballot(key[j] > thr));
+  const int need = k - n_gt;  // >= 1 ties at thr are taken, highest index first
+  const uint64_t above = lane == 63 ? 0ull : (~0ull << (lane + 1));
+  bool sel[NPL];
+  int eq_after = 0;  // ties at thr with a higher j
+#pragma unroll
+  for (int j = NPL - 1; j >= 0; --j) {
+    const uint64_t eq = __ballot(key[j] == thr);
+    const bool tie = (eq >> lane) & 1u;
+    sel[j] = key[j] > thr || (tie && eq_after + __popcll(eq & above) < need);
+    eq_after += __popcll(eq);
+  }
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  int sel_before = 0;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const uint64_t selm = __ballot(sel[j]);
+    const int p = sel_before + __popcll(selm & below);
+    if (sel[j] && p < 32) {  // k <= 32 picks; the bound keeps every write inside this wavefront's 64 dwords
+      lds[p] = key[j];
+      lds[32 + p] = uint32_t(lane + 64 * j);
+    }
+    sel_before += __popcll(selm);
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (lane < k) {
+    const uint32_t my_key = lds[lane], my_idx = lds[32 + lane];
+    int rank = 0;
+    for (int q = 0; q < k; ++q) {
+      const uint32_t kq = lds[q], iq = lds[32 + q];
+      rank += (kq > my_key || (kq == my_key && iq > my_idx)) ? 1 : 0;
+    }
+    *idx = my_idx;
+    *pos = k - 1 - rank;
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// The reference budget's sum of k values in T (route_cuda.py:36-37, 98-113): lane l < 32 adds positions l*N .. l*N+N-1
+// from 0 in order (N = 16 / sizeof(T)), each add rounded to T, then the 32 lanes combine by xor 16, 8, 4, 2, 1.
+// sv: the k values by position (LDS). Wave-uniform result.
+__device__ float budget_sum(const float *sv, int k, int dt) {
+  const int lane = threadIdx.x & 63;
+  const int n = dt == LMOE_F32 ? 4 : 8;
+  float a = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    const int j = (lane & 31) * n + i;
+    a = round_dt(a + (j < k ? sv[j] : 0.0f), dt);
+  }
+#pragma unroll
+  for (int m = 16; m > 0; m >>= 1) a = round_dt(a + __shfl_xor(a, m, 32), dt);
+  return lane_value(a, 0);
+}
+
+template <int NPL>
+__device__ void route_row(const RouteArgs &a, int r, float *gl, uint32_t *scr, float *sv, uint32_t *okf) {
+  const int lane = threadIdx.x & 63;
+  const int E = a.E, k = a.k, dt = a.gdt;
+  float g[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int e = min(lane + 64 * j, E - 1);
+    g[j] = load_elt(a.gates, size_t(r) * E + e, dt);
+  }
+  if (a.softmax) {  // gates = T(exp(v - max) / sum), the sum over the row's experts
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+      if (lane + 64 * j < E) mx = fmaxf(mx, g[j]);
+    mx = wave_max(mx);
+    float ex[NPL], sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      ex[j] = lane + 64 * j < E ? expf(g[j] - mx) : 0.0f;
+      sum += ex[j];
+    }
+    const float inv = 1.0f / wave_sum(sum);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) g[j] = round_dt(ex[j] * inv, dt);
+  }
+  float lmx = -INFINITY, lmn = INFINITY, m[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) {
+      gl[e] = g[j];
+      lmx = fmaxf(lmx, g[j]);
+      lmn = fminf(lmn, g[j]);
+    }
+    const int ec = min(e, E - 1);
+    if (a.mask) {
+      m[j] = a.mask[ec];
+    } else {
+      const int sl = a.slot_of[ec];
+      m[j] = (sl >= 0 && sl < a.lim) ? 1.0f : 0.0f;
+    }
+  }
+  lmx = wave_max(lmx);
+  lmn = -wave_max(-lmn);
+  const float spread = round_dt(lmx - lmn, dt);
+  const float ls = round_dt(round_dt(a.lam, dt) * spread, dt);
+  float rank[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) rank[j] = g[j] + ls * m[j];  // two roundings (no contraction in this library)
+  uint32_t bi = 0, hi = 0;
+  int bp = 0, hp = 0;
+  select_mlx<NPL>(rank, E, k, scr, &bi, &bp);
+  bool back = false;
+  if (a.tau > 0.0f) {  // the budget: honest mass against biased mass
+    select_mlx<NPL>(g, E, k, scr, &hi, &hp);
+    if (lane < k) {
+      sv[hp] = gl[min(hi, uint32_t(E - 1))];
+      sv[32 + bp] = gl[min(bi, uint32_t(E - 1))];
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float mh = budget_sum(sv, k, dt), mb = budget_sum(sv + 32, k, dt);
+    back = round_dt(mh - mb, dt) > round_dt(round_dt(a.tau, dt) * mh, dt);
+    __builtin_amdgcn_wave_barrier();
+  }
+  const uint32_t idx = min(back ? hi : bi, uint32_t(E - 1));  // always < E for finite gates; NaN rows stay in bounds
+  const int p = back ? hp : bp;
+  bool bad = false;
+  if (lane < k) {
+    a.inds[size_t(r) * k + p] = idx;
+    if (a.slot_of) {
+      const int sl = a.slot_of[idx];
+      if (a.rhs) a.rhs[size_t(r) * k + p] = sl > 0 ? sl : 0;
+      bad = sl < 0;
+    }
+  }
+  if (__ballot(bad) != 0 && lane == 0) *okf = 0u;
+  if (a.scores) {  // the picked gates, divided by their sum taken in position order from 0 in T when norm
+    float sc = lane < k ? gl[idx] : 0.0f;
+    if (a.norm) {
+      if (lane < k) sv[p] = sc;
+      __builtin_amdgcn_wave_barrier();
+      float tot = 0.0f;
+      for (int j = 0; j < k; ++j) tot = round_dt(tot + sv[j], dt);
+      sc = round_dt(sc / tot, dt);
+    }
+    if (lane < k) store_elt(a.scores, size_t(r) * k + p, sc, dt);
+  }
+}
+
+__global__ void __launch_bounds__(1024) k_route_bias(RouteArgs a) {
+  __shared__ float gl[kRouteMaxT][kRouteMaxE];
+  __shared__ __attribute__((aligned(16))) uint32_t scr[kRouteMaxT][64];
+  __shared__ float sv[kRouteMaxT][64];
+  __shared__ uint32_t okf;
+  const int wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) okf = 1u;
+  __syncthreads();
+  if (wave < a.T) {
+    const int npl = (a.E + 63) / 64;
+    if (npl <= 1)
+      route_row<1>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
+    else if (npl <= 2)
+      route_row<2>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
+    else if (npl <= 4)
+      route_row<4>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
+    else if (npl <= 8)
+      route_row<8>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
+    else
+      route_row<16>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && a.ok) a.ok[0] = okf;
+}
+
 }  // namespace lmoe
 
 using namespace lmoe;
@@ -238,4 +464,22 @@ extern "C" int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, 
   if (int rc = lmoe_router_gemv(x, xdtype, wr, wsg, wdtype, T, H, E, logits, xprep, qtype, stream)) return rc;
   return topk_launch(logits, LMOE_F32, E + (wsg ? 1 : 0), T, E, k, norm, ids, scores, (hipStream_t)stream,
                      "lmoe_router_gemv_topk");
+}
+
+extern "C" int lmoe_route_bias(const void *gates, int gdtype, int T, int E, int k, const float *mask,
+                               const int32_t *slot_of, int lim, float lam, float tau, int softmax, int norm,
+                               uint32_t *inds, uint32_t *ok, int32_t *rhs, void *scores, void *stream) {
+  const char *fn = "lmoe_route_bias";
+  LMOE_REQUIRE(dtype_ok(gdtype), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(T > 0 && T <= kRouteMaxT, LMOE_ESHAPE, "%s: %d rows is outside 1..%d", fn, T, kRouteMaxT);
+  LMOE_REQUIRE(E > 0 && E <= kRouteMaxE && k > 0 && k <= 32 && k <= E, LMOE_ESHAPE,
+               "%s: E = %d, k = %d (E <= %d, k <= 32)", fn, E, k, kRouteMaxE);
+  LMOE_REQUIRE(lam >= 0.0f && tau >= 0.0f, LMOE_EINVAL, "%s: lam and tau must be >= 0", fn);
+  LMOE_REQUIRE(gates && inds, LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(mask || slot_of, LMOE_EINVAL, "%s: give a mask or a slot table (table mode)", fn);
+  LMOE_REQUIRE(slot_of || (!rhs && !ok), LMOE_EINVAL, "%s: rhs and ok need the slot table", fn);
+  RouteArgs a{gates, gdtype, T, E, k, mask, slot_of, lim, lam, tau, softmax, norm, inds, ok, rhs, scores};
+  launch(k_route_bias, dim3(1), dim3(64 * T), 0, (hipStream_t)stream, a);
+  LMOE_LAUNCHED(fn);
+  return 0;
 }

@@ -86,6 +86,13 @@ def test_grouped_refusals_without_a_gpu(built_lib):
     assert L.lmoe_to_f16(p, 7, 10, p, z) == _lib.EINVAL
     assert L.lmoe_to_f16(p, 0, -1, p, z) == _lib.ESHAPE
     assert L.lmoe_to_gemm_f16(p, 0, 48, p, z) == _lib.ESHAPE  # not a multiple of 32
+    f = ctypes.c_float
+    assert L.lmoe_route_bias(p, 0, 17, 256, 8, p, p, 10, f(0.5), f(0.0), 0, 0, p, None, None, None, z) == _lib.ESHAPE
+    assert L.lmoe_route_bias(p, 0, 2, 256, 33, p, p, 10, f(0.5), f(0.0), 0, 0, p, None, None, None, z) == _lib.ESHAPE
+    assert L.lmoe_route_bias(p, 0, 2, 256, 8, None, None, 10, f(0.5), f(0.0), 0, 0, p, None, None, None, z) == \
+        _lib.EINVAL
+    assert L.lmoe_route_bias(p, 0, 2, 256, 8, p, p, 10, f(-1.0), f(0.0), 0, 0, p, None, None, None, z) == _lib.EINVAL
+    assert L.lmoe_route_bias(p, 0, 2, 256, 8, p, None, 10, f(0.5), f(0.0), 0, 0, p, p, p, None, z) == _lib.EINVAL
     assert L.lmoe_to_gemm_f16(ctypes.c_void_p(8), 0, 64, p, z) == _lib.EALIGN
     assert L.lmoe_grouped_tile_rows() == 128
 
