@@ -36,6 +36,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-grouped", action="store_true", help="skip the cfg3 prefill / cfg4 batched lines")
+    ap.add_argument("--types-only", action="store_true",
+                    help="only the Q4_1 / Q8_0 / Q5_K / Q6_K lines (decode chain and grouped path), one JSON line")
     ap.add_argument("--grouped-only", action="store_true",
                     help="run only the grouped-path lines (cfg3 prefill, cfg4, cfg5) and print them: a short run to "
                          "profile the grouped GEMMs with rocprofv3 counters, not a benchmark line")
@@ -253,6 +255,66 @@ def grouped_leg():
     return out
 
 
+def types_leg():
+    """The block types beyond Q4_0 / Q4_K on a cfg2-shaped layer (H 2048, E 128, I 768, top-8), each type for all
+    three projections, plus the 35B's Q4_K / Q4_K / Q6_K mix: the decode chain for one token (the general gate/up
+    and down kernels, kernel-exact durations against the HBM roofline over the 8 experts' bytes) and the grouped
+    path for 2048 tokens (dequant of the experts to f16, then the f16-weight grouped GEMMs; MFMA roofline over the
+    routed GEMM flops)."""
+    import ctypes
+
+    import torch
+
+    from larder_amd import _lib, gguf_experts as ge, workloads
+
+    H, E, I, k = 2048, 128, 768, 8
+    g = torch.Generator(device="cuda").manual_seed(5)
+    out = {}
+
+    def kernels(fn, n_launch, reps):
+        M = n_launch * reps
+        _lib.call("lmoe_profile_arm", M)
+        for _ in range(reps):
+            fn()
+        ms = (ctypes.c_float * M)()
+        cnt = ctypes.c_int()
+        _lib.call("lmoe_profile_read", ms, M, ctypes.byref(cnt))
+        return [sum(ms[j:cnt.value:n_launch]) / reps * 1e3 for j in range(n_launch)]
+
+    for types in (("Q4_1",) * 3, ("Q8_0",) * 3, ("Q5_K",) * 3, ("Q6_K",) * 3, ("Q4_K", "Q4_K", "Q6_K")):
+        w = tuple(workloads.random_blocks(t, E, r, c, g) for (r, c), t in zip(((I, H), (I, H), (H, I)), types))
+        x = torch.randn((1, H), generator=g, device="cuda").half()
+        picks = torch.randperm(E, generator=g, device="cuda")[:k].to(torch.int32)
+        dec = lambda: ge.gemv(x, w, picks, k, types, torch.float16)  # noqa: E731
+        for _ in range(8):
+            dec()
+        torch.cuda.synchronize()
+        gu, dn = kernels(dec, 2, 32)
+        wbytes = k * (2 * I * _lib.row_bytes(types[0], H) + H * _lib.row_bytes(types[2], I))
+        byts = wbytes + H * 2 + k * I * 4 * 2 + k * H * 2
+        T = 2048
+        xt = torch.randn((T * k, H), generator=g, device="cuda").half()
+        rows = torch.randint(0, E, (T * k,), generator=g, device="cuda", dtype=torch.int32)
+        den = lambda: ge.dense(xt, w, rows, types, torch.float16)  # noqa: E731
+        for _ in range(2):
+            den()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            den()
+        e1.record()
+        torch.cuda.synchronize()
+        us_dense = e0.elapsed_time(e1) / 5 * 1e3
+        flops = 2 * T * k * 3 * H * I
+        out["/".join(types)] = {
+            "decode_gate_up_us": round(gu, 2), "decode_down_us": round(dn, 2), "decode_bytes": byts,
+            "decode_hbm_frac": round(byts / ((gu + dn) * 1e-6) / HBM_PEAK, 4),
+            "dense_2048x8_us": round(us_dense, 1), "dense_mfma_frac": round(flops / (us_dense * 1e-6) / MFMA_PEAK, 4)}
+        del w, xt, rows
+    return out
+
+
 def cpu_leg(args, g):
     """The C++ restatement of the reference CPU kernel (cpu_kern gather_qmm) over the same experts, converted to
     its affine 4-bit layout, run layer after layer for about --cpu-seconds; tokens/s = 1 / (48 x mean layer time)."""
@@ -305,9 +367,14 @@ def main():
     if args.grouped_only:
         print(json.dumps({"secondary": grouped_leg()}), flush=True)
         return
+    if args.types_only:
+        print(json.dumps({"types": types_leg()}), flush=True)
+        return
     g = gpu_leg(args)
     cpu = None if args.no_cpu else cpu_leg(args, g)
     secondary = None if args.no_grouped else grouped_leg()
+    if secondary is not None:
+        secondary["types"] = types_leg()
     value = args.steps / g["secs"]
     dom = g["timing"][g["dom"]]
     achieved = dom["bytes"] / (dom["us"] * 1e-6)

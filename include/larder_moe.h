@@ -23,7 +23,11 @@ extern "C" {
 /* element types of activations, logits and outputs */
 enum { LMOE_F32 = 0, LMOE_F16 = 1, LMOE_BF16 = 2 };
 /* ggml block types, by ggml type id (gguf_ref.py:8-15) */
-enum { LMOE_Q4_0 = 2, LMOE_Q4_K = 12 };
+enum { LMOE_Q4_0 = 2, LMOE_Q4_1 = 3, LMOE_Q8_0 = 8, LMOE_Q4_K = 12, LMOE_Q5_K = 13, LMOE_Q6_K = 14 };
+/* Q4_0 and Q4_K run on every kernel. Q4_1, Q8_0, Q5_K and Q6_K run on the general decode chain
+ * (lmoe_gemv_gate_up / lmoe_gemv_down_combine with raw x and float32 h: one lane a 32-weight chunk,
+ * gguf_experts.py:78-373's task decoders restated), in lmoe_dequant, and on the grouped path through
+ * lmoe_dequant_gemm_f16 + lmoe_grouped_*_f16w; the prepared-row entry points take Q4_0 and Q4_K only. */
 /* refusals */
 enum { LMOE_EINVAL = -1, LMOE_ETYPE = -2, LMOE_ESHAPE = -3, LMOE_EALIGN = -4, LMOE_EWORKSPACE = -5 };
 
@@ -158,6 +162,17 @@ int lmoe_grouped_down(const void *h, const uint32_t *offsets, const uint32_t *ti
                       int max_tiles, const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
                       void *stream);
 
+/* lmoe_grouped_gate_up / lmoe_grouped_down with f16 weights in the K order (lmoe_dequant_gemm_f16's output:
+ * wg16 / wu16 [n_experts][I][H], wd16 [n_experts][H][I]) instead of Q4 blocks: the grouped path of Q4_1, Q8_0,
+ * Q5_K and Q6_K experts (the reference's gather_mm on dequantized f16 experts, gguf_experts.py:698-722). Same
+ * grouping arguments, shapes (I % 128, H % 256 for down, K % 64) and outputs. */
+int lmoe_grouped_gate_up_f16w(const void *x, int xdtype, int T, int topk, const uint32_t *order,
+                              const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles, int max_tiles,
+                              const void *wg16, const void *wu16, int n_experts, int H, int I, void *h, void *stream);
+int lmoe_grouped_down_f16w(const void *h, const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
+                           int max_tiles, const void *wd16, int n_experts, int I, int H, void *y, int ydtype,
+                           void *stream);
+
 /* x [n] (F32 / BF16 / F16) -> out [n] float16, round to nearest even.
  * No counterpart in the reference (its dense path casts with MLX, gguf_experts.py:716). */
 int lmoe_to_f16(const void *x, int xdtype, long long n, void *out, void *stream);
@@ -179,6 +194,12 @@ int lmoe_combine_sorted(const void *y, int ydtype, const uint32_t *inv, const fl
  * Replaces gguf_experts.dequant (gguf_experts.py:579-586; kernel gguf_dequant :529-539). */
 int lmoe_dequant(const uint8_t *buf, int type, int n_experts, int rows, int cols, const uint32_t *slots, int n,
                  void *q, int odtype, void *stream);
+
+/* Every expert of buf [n_experts][rows][row bytes] (any of the six types) as f16 weights out [n_experts][rows][cols]
+ * in the grouped GEMMs' K order (within each 32 columns: 0-3, 16-19, 4-7, 20-23, 8-11, 24-27, 12-15, 28-31), the
+ * operand of lmoe_grouped_*_f16w. The reference's prefill path dequantizes to f16 the same way before gather_mm
+ * (gguf_experts.py:698-722, DEQ_SRC :529-539); cols % 32 (Q4_0/Q4_1/Q8_0) or % 256 (K types). */
+int lmoe_dequant_gemm_f16(const uint8_t *buf, int type, int n_experts, int rows, int cols, void *out, void *stream);
 
 /* Q4_0 quantizer on the device, ggml's quantize_row_q4_0_ref rule (no counterpart in the reference, which only
  * reads packs llama.cpp wrote): w [rows][cols] in wdtype -> out [rows][cols / 32 * 18]. */

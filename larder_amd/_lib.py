@@ -20,7 +20,11 @@ ABI_VERSION = 1
 
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 # ggml type name -> (ggml type id, weights a block, bytes a block) (gguf_ref.py:8-15)
-TYPES = {"Q4_0": (2, 32, 18), "Q4_K": (12, 256, 144)}
+TYPES = {"Q4_0": (2, 32, 18), "Q4_K": (12, 256, 144), "Q4_1": (3, 32, 20), "Q8_0": (8, 32, 34),
+         "Q5_K": (13, 256, 176), "Q6_K": (14, 256, 210)}
+# the two types every kernel (prepared rows, fused top-k, nibble-decoding grouped GEMMs) takes; the others run on
+# the general decode chain and on the grouped path over f16-dequantized experts
+Q4_TYPES = ("Q4_0", "Q4_K")
 
 _P, _I, _SZ, _LL, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_longlong, ctypes.c_float
 # name -> (restype, argtypes): every symbol include/larder_moe.h declares
@@ -50,6 +54,9 @@ SIGNATURES = {
     "lmoe_grouped_down": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_combine_sorted": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_dequant": (_I, [_P, _I, _I, _I, _I, _P, _I, _P, _I, _P]),
+    "lmoe_dequant_gemm_f16": (_I, [_P, _I, _I, _I, _I, _P, _P]),
+    "lmoe_grouped_gate_up_f16w": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P, _P]),
+    "lmoe_grouped_down_f16w": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P]),
     "lmoe_quantize_q4_0": (_I, [_P, _I, _LL, _I, _P, _P]),
     "lmoe_quantize_q4_k": (_I, [_P, _I, _LL, _I, _P, _P]),
 }
@@ -106,7 +113,7 @@ def dcode(dtype):
 def qcode(t):
     """ggml type name -> ggml type id; ValueError for any type this path does not implement."""
     if t not in TYPES:
-        raise ValueError(f"larder_amd: ggml type {t} is not supported (Q4_0 and Q4_K are)")
+        raise ValueError(f"larder_amd: ggml type {t} is not supported ({', '.join(TYPES)} are)")
     return TYPES[t][0]
 
 

@@ -767,6 +767,15 @@ static int gate_up(const char *fn, const GateUpArgs &a, int type_g, int type_u, 
   LMOE_REQUIRE(a.n_slots >= 0 && a.topk > 0 && a.n_slots % a.topk == 0, LMOE_ESHAPE,
                "%s: %d slots is not a multiple of topk %d", fn, a.n_slots, a.topk);
   LMOE_REQUIRE(a.n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
+  if (!qtype_ok(type_g) || !qtype_ok(type_u)) {  // a type beyond Q4_0 / Q4_K: the general chain
+    LMOE_REQUIRE(qtype_any(type_g) && qtype_any(type_u), LMOE_ETYPE,
+                 "%s: ggml types %d/%d are not supported (Q4_0 = 2, Q4_1 = 3, Q8_0 = 8, Q4_K = 12, Q5_K = 13, "
+                 "Q6_K = 14)", fn, type_g, type_u);
+    LMOE_REQUIRE((a.x || a.n_slots == 0) && !a.hprep && !a.logits && !a.xg_prep, LMOE_ETYPE,
+                 "%s: ggml types %d/%d run on the general chain only (raw x in, float32 h out)", fn, type_g, type_u);
+    return gate_up_any(fn, a.x, a.xdt, a.slots, a.n_slots, a.topk, a.wg, a.wu, type_g, type_u, a.n_experts, a.H,
+                       a.I, a.h, (hipStream_t)stream);
+  }
   if (int rc = check_matrix(fn, type_g, a.I, a.H, a.wg)) return rc;
   if (int rc = check_matrix(fn, type_u, a.I, a.H, a.wu)) return rc;
   LMOE_REQUIRE(!a.hprep || qtype_ok(a.td), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)",
@@ -808,6 +817,13 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   LMOE_REQUIRE(a.T >= 0 && a.k > 0 && a.k <= 32, LMOE_ESHAPE, "%s: k %d is outside 1..32", fn, a.k);
   LMOE_REQUIRE(a.n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
   LMOE_REQUIRE(!a.shared == !a.gate, LMOE_EINVAL, "%s: shared and gate go together", fn);
+  if (!qtype_ok(a.type_d)) {  // a type beyond Q4_0 / Q4_K: the general chain
+    LMOE_REQUIRE(!a.hprep, LMOE_ETYPE, "%s: ggml type %d runs on the general chain only (float32 h in)", fn,
+                 a.type_d);
+    LMOE_REQUIRE(a.T == 0 || aligned16(a.h), LMOE_EALIGN, "%s: h must be 16-byte aligned", fn);
+    return down_any(fn, a.h, a.ids, a.scores, a.T, a.k, a.wd, a.type_d, a.n_experts, a.I, a.H, a.shared, a.gate,
+                    a.gate_stride, a.residual, a.rdt, a.out, a.odt, (hipStream_t)stream);
+  }
   if (int rc = check_matrix(fn, a.type_d, a.H, a.I, a.wd)) return rc;
   if (a.T == 0) return 0;
   LMOE_REQUIRE((a.h || a.hprep) && a.ids && a.out, LMOE_EINVAL, "%s: null pointer", fn);

@@ -363,6 +363,118 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   store_tile<MODE>(acc, t, wave, fr, g, out, ldo, odt);
 }
 
+// ---- f16 weights (the other block types, dequantized in the K order): both operands global -> LDS ---------------
+
+constexpr int kFwAStage = GM * 128;                  // A tile bytes a stage (16 KB)
+constexpr int kFwStage = kFwAStage + GN * 128;       // + 256 weight rows of 64 halves (32 KB)
+constexpr int kFwDmaA = GM * 128 / 1024 / 4;         // 16-byte A copies a lane a step (4)
+constexpr int kFwDmaW = GN * 128 / 1024 / 4;         // 16-byte weight copies a lane a step (8)
+
+// The grouped GEMMs over f16 weights [E][n_rows][K] already in the K order (lmoe_dequant_gemm_f16): the tiles,
+// wavefront split, MFMA fragments and epilogue of k_grouped_q4_0, with the weight tile copied like the A tile
+// (rows of 128 bytes, 16-byte chunks XOR-swizzled by the row's low 3 bits) and no decode. Two 48 KB stages, one
+// workgroup a CU: step kk + 1's copies go out while step kk multiplies. Host guarantees: K % 64 == 0, rows x K x 2
+// of A and of one expert's weights under 4 GiB.
+template <int MODE>
+__global__ void __launch_bounds__(kThreads, 1)
+k_grouped_f16w(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
+               const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const _Float16 *w0, const _Float16 *w1,
+               int K, int n_rows, void *out, int ldo, int odt) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kFwStage];
+  Tile t;
+  if (!tile_of(offsets, tiles, n_tiles, n_ntile, &t)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, g = lane >> 4;
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(lds));
+
+  // A as in k_grouped_q4_0: granule q = 64 (4 w + i) + lane holds chunk (q % 8) ^ (r & 7) of tile row r = q / 8
+  uint32_t a_off[kFwDmaA];
+#pragma unroll
+  for (int i = 0; i < kFwDmaA; ++i) {
+    const int q = 64 * (kFwDmaA * wave + i) + lane, r = q >> 3, c = (q & 7) ^ (r & 7);
+    const int p = t.row0 + (r < t.rows ? r : 0);
+    const uint32_t row = MODE == MODE_GATE_UP ? order[p] / uint32_t(topk) : uint32_t(p);
+    a_off[i] = row * uint32_t(K) * 2u + 16u * uint32_t(c);
+  }
+  // weights: wavefront w covers tile features 64 w .. 64 w + 63 (gate/up: waves 0-1 gate rows, 2-3 up rows);
+  // granule q = 64 (8 w + i) + lane holds chunk (q % 8) ^ (f & 7) of tile feature f = q / 8
+  const _Float16 *wbase;
+  uint32_t w_off[kFwDmaW];
+  {
+    const _Float16 *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
+    const int row_base = MODE == MODE_GATE_UP ? t.nt * (GN / 2) - (wave >= 2 ? GN / 2 : 0) : t.nt * GN;
+    wbase = m + size_t(t.e) * n_rows * K;
+#pragma unroll
+    for (int i = 0; i < kFwDmaW; ++i) {
+      const int q = 64 * (kFwDmaW * wave + i) + lane, f = q >> 3, c = (q & 7) ^ (f & 7);
+      w_off[i] = uint32_t(row_base + f) * uint32_t(K) * 2u + 16u * uint32_t(c);
+    }
+  }
+  const int nk = K / GK;
+  auto issue = [&](int kk) {  // step kk into stage kk % 2
+    const uint32_t st = lds0 + uint32_t(kk & 1) * kFwStage;
+    const _Float16 *ab = a_src + size_t(kk) * GK;
+#pragma unroll
+    for (int i = 0; i < kFwDmaA; ++i)
+      dma<16>(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kFwDmaA * wave + i)));
+    const _Float16 *wb = wbase + size_t(kk) * GK;
+#pragma unroll
+    for (int i = 0; i < kFwDmaW; ++i)
+      dma<16>(wb, w_off[i], __builtin_amdgcn_readfirstlane(st + kFwAStage + 1024u * uint32_t(kFwDmaW * wave + i)));
+  };
+
+  int wfeat[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) wfeat[nb] = frag_feature<MODE>(wave, nb) + fr;
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](int s, auto qn) {
+    constexpr int QN = decltype(qn)::value;
+    const u32x4 *as = reinterpret_cast<const u32x4 *>(lds + s * kFwStage);
+    const u32x4 *ws = reinterpret_cast<const u32x4 *>(lds + s * kFwStage + kFwAStage);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      half8 xf[8];
+#pragma unroll
+      for (int mb = 0; mb < 2 * QN; ++mb) xf[mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 * ks + g)]);
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const half8 wf = __builtin_bit_cast(half8, ws[achunk(wfeat[nb], 4 * ks + g)]);
+#pragma unroll
+        for (int mb = 0; mb < 2 * QN; ++mb)
+          acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, xf[mb], acc[nb][mb], 0, 0, 0);
+      }
+    }
+  };
+
+  // Step kk: step kk + 1's copies go out into the other stage (read in step kk - 1, released by its barrier),
+  // step kk multiplies, then each wavefront waits for its own copies and the barrier publishes the stage.
+  issue(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  barrier_lds();
+  auto run = [&](auto qn) {
+    for (int kk = 0; kk < nk; ++kk) {
+      if (kk + 1 < nk) issue(kk + 1);
+      compute(kk & 1, qn);
+      if (kk + 1 < nk) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        barrier_lds();
+      }
+    }
+  };
+  switch ((t.rows + 31) / 32) {  // uniform across the workgroup
+    case 1: run(IC<1>{}); break;
+    case 2: run(IC<2>{}); break;
+    case 3: run(IC<3>{}); break;
+    default: run(IC<4>{}); break;
+  }
+  store_tile<MODE>(acc, t, wave, fr, g, out, ldo, odt);
+}
+
 // ---- Q4_K: register staging with repack --------------------------------------------------------------------------
 
 constexpr int kWp = 10;  // LDS words a weight row a step: 8 nibble words, 2 scale words
@@ -622,6 +734,58 @@ extern "C" int lmoe_grouped_down(const void *h, const uint32_t *offsets, const u
            static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile, wd,
            static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
   }
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+extern "C" int lmoe_grouped_gate_up_f16w(const void *x, int xdtype, int T, int topk, const uint32_t *order,
+                                         const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
+                                         int max_tiles, const void *wg16, const void *wu16, int n_experts, int H, int I,
+                                         void *h, void *stream) {
+  const char *fn = "lmoe_grouped_gate_up_f16w";
+  LMOE_REQUIRE(xdtype == LMOE_F16, LMOE_EINVAL,
+               "%s: x must be float16 in the GEMM K order here (convert once with lmoe_to_gemm_f16)", fn);
+  LMOE_REQUIRE(T >= 0 && topk > 0 && n_experts > 0 && max_tiles >= 0, LMOE_ESHAPE, "%s: bad shape", fn);
+  LMOE_REQUIRE(H > 0 && H % GK == 0, LMOE_ESHAPE, "%s: hidden size %d is not a multiple of %d", fn, H, GK);
+  LMOE_REQUIRE(I > 0 && I % (GN / 2) == 0, LMOE_ESHAPE, "%s: intermediate size %d is not a multiple of %d", fn, I,
+               GN / 2);
+  if (T == 0 || max_tiles == 0) return 0;
+  LMOE_REQUIRE(x && order && offsets && tiles && n_tiles && wg16 && wu16 && h, LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(aligned16(x) && aligned16(h) && aligned16(wg16) && aligned16(wu16), LMOE_EALIGN,
+               "%s: x, h and the weights must be 16-byte aligned", fn);
+  LMOE_REQUIRE((long long)T * H * 2 <= 0xFFFFFFFFll && (long long)I * H * 2 <= 0xFFFFFFFFll, LMOE_ESHAPE,
+               "%s: x or one expert's weights exceed 4 GiB", fn);
+  const int n_ntile = I / (GN / 2);
+  const long long grid = (long long)n_ntile * max_tiles;
+  LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
+  launch(k_grouped_f16w<MODE_GATE_UP>, dim3(unsigned(grid)), dim3(kThreads), 0, (hipStream_t)stream,
+         static_cast<const _Float16 *>(x), topk, order, offsets, tiles, n_tiles, n_ntile,
+         static_cast<const _Float16 *>(wg16), static_cast<const _Float16 *>(wu16), H, I, h, I, int(LMOE_F16));
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+extern "C" int lmoe_grouped_down_f16w(const void *h, const uint32_t *offsets, const uint32_t *tiles,
+                                      const uint32_t *n_tiles, int max_tiles, const void *wd16, int n_experts, int I,
+                                      int H, void *y, int ydtype, void *stream) {
+  const char *fn = "lmoe_grouped_down_f16w";
+  LMOE_REQUIRE(n_experts > 0 && max_tiles >= 0, LMOE_ESHAPE, "%s: bad shape", fn);
+  LMOE_REQUIRE(I > 0 && I % GK == 0, LMOE_ESHAPE, "%s: intermediate size %d is not a multiple of %d", fn, I, GK);
+  LMOE_REQUIRE(H > 0 && H % GN == 0, LMOE_ESHAPE, "%s: hidden size %d is not a multiple of %d", fn, H, GN);
+  LMOE_REQUIRE(ydtype == LMOE_F16 || ydtype == LMOE_F32, LMOE_EINVAL, "%s: y must be float16 or float32", fn);
+  if (max_tiles == 0) return 0;
+  LMOE_REQUIRE(h && offsets && tiles && n_tiles && wd16 && y, LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(aligned16(h) && aligned16(y) && aligned16(wd16), LMOE_EALIGN,
+               "%s: h, y and the weights must be 16-byte aligned", fn);
+  // R is not passed: offsets[E] <= max_tiles * bm rows of h can be read
+  LMOE_REQUIRE((long long)max_tiles * GM * I * 2 <= 0xFFFFFFFFll && (long long)H * I * 2 <= 0xFFFFFFFFll,
+               LMOE_ESHAPE, "%s: h or one expert's weights exceed 4 GiB", fn);
+  const int n_ntile = H / GN;
+  const long long grid = (long long)n_ntile * max_tiles;
+  LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
+  launch(k_grouped_f16w<MODE_DOWN>, dim3(unsigned(grid)), dim3(kThreads), 0, (hipStream_t)stream,
+         static_cast<const _Float16 *>(h), 1, static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile,
+         static_cast<const _Float16 *>(wd16), static_cast<const _Float16 *>(nullptr), I, H, y, H, ydtype);
   LMOE_LAUNCHED(fn);
   return 0;
 }

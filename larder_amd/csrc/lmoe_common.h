@@ -77,6 +77,19 @@ inline bool dtype_ok(int t) { return t == LMOE_F32 || t == LMOE_F16 || t == LMOE
 inline bool qtype_ok(int t) { return t == LMOE_Q4_0 || t == LMOE_Q4_K; }
 inline int block_weights(int t) { return t == LMOE_Q4_K ? 256 : 32; }
 
+// The general decode chain and dequant over every supported block type (anytype.hip)
+bool qtype_any(int t);
+int block_weights_any(int t);
+int block_bytes_any(int t);
+int gate_up_any(const char *fn, const void *x, int xdt, const uint32_t *slots, int n_slots, int topk,
+                const uint8_t *wg, const uint8_t *wu, int tg, int tu, int n_experts, int H, int I, float *h,
+                hipStream_t st);
+int down_any(const char *fn, const float *h, const uint32_t *ids, const float *scores, int T, int k,
+             const uint8_t *wd, int td, int n_experts, int I, int H, const float *shared, const float *gate,
+             int gate_stride, const void *residual, int rdt, void *out, int odt, hipStream_t st);
+int dequant_any(const char *fn, const uint8_t *buf, int type, int n_experts, int rows, int cols,
+                const uint32_t *slots, int n, void *q, int odt, int kperm, hipStream_t st);
+
 // ---- element loads / stores ------------------------------------------------------------------------------------
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }

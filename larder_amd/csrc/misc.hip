@@ -212,7 +212,10 @@ extern "C" int lmoe_combine_sorted(const void *y, int ydtype, const uint32_t *in
 extern "C" int lmoe_dequant(const uint8_t *buf, int type, int n_experts, int rows, int cols, const uint32_t *slots,
                             int n, void *q, int odtype, void *stream) {
   const char *fn = "lmoe_dequant";
-  LMOE_REQUIRE(qtype_ok(type), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn, type);
+  if (!qtype_ok(type)) {
+    LMOE_REQUIRE(n == 0 || slots, LMOE_EINVAL, "%s: null pointer", fn);
+    return dequant_any(fn, buf, type, n_experts, rows, cols, slots, n, q, odtype, 0, (hipStream_t)stream);
+  }
   LMOE_REQUIRE(dtype_ok(odtype), LMOE_EINVAL, "%s: bad dtype", fn);
   LMOE_REQUIRE(rows > 0 && cols > 0 && cols % block_weights(type) == 0 && cols % 64 == 0 && n >= 0, LMOE_ESHAPE,
                "%s: row length %d is not a multiple of %d", fn, cols, type == LMOE_Q4_K ? 256 : 64);

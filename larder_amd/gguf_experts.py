@@ -1,5 +1,6 @@
-"""Routed experts in llama.cpp's GGUF Q4_0 / Q4_K block formats on MI355X: the call surface of the reference's
-gguf_experts module (gguf_experts.py:573-819) over torch tensors, backed by liblarder_moe.so.
+"""Routed experts in llama.cpp's GGUF block formats (Q4_0, Q4_K, Q4_1, Q8_0, Q5_K, Q6_K) on MI355X: the call
+surface of the reference's gguf_experts module (gguf_experts.py:573-819) over torch tensors, backed by
+liblarder_moe.so.
 
     experts(x, bufs, rhs, types, host=None)    gguf_experts.py:803-819
     gemv(x, w, slots, topk, types, out_dtype)  gguf_experts.py:600-607  (the decode chain)
@@ -137,16 +138,24 @@ def _measure(hid, inter, types):
     return [max(float(v), 0.0) for v in (*cg, *cd)]
 
 
+# byte offsets of each block type's f16 scale fields
+_SCALE_AT = {"Q4_0": (0,), "Q4_K": (0, 2), "Q4_1": (0, 2), "Q8_0": (0,), "Q5_K": (0, 2), "Q6_K": (208,)}
+
+
 def _random_q4(n, rows, cols, t, gen):
-    """n random experts [n, rows, row bytes] of type t with finite scales, made on the device."""
+    """n random experts [n, rows, row bytes] of type t with finite scales, made on the device (Q4_0 through the
+    device quantizer, the other types as random blocks with small f16 scales)."""
     if t == "Q4_0":
         wf = torch.randn((n * rows, cols), generator=gen, device="cuda", dtype=torch.float32) * 0.02
         out = torch.empty((n, rows, _lib.row_bytes(t, cols)), dtype=torch.uint8, device="cuda")
         call("lmoe_quantize_q4_0", ptr(wf), _lib.F32, n * rows, cols, ptr(out), stream())
         return out
-    b = torch.randint(0, 256, (n, rows, cols // 256, 144), generator=gen, device="cuda", dtype=torch.uint8)
-    d = (torch.rand((n, rows, cols // 256, 2), generator=gen, device="cuda") * 1e-3).to(torch.float16)
-    b[..., 0:4] = d.view(torch.uint8).reshape(n, rows, cols // 256, 4)
+    _, be, bb = TYPES[t]
+    nb = cols // be
+    b = torch.randint(0, 256, (n, rows, nb, bb), generator=gen, device="cuda", dtype=torch.uint8)
+    for at in _SCALE_AT[t]:
+        d = (torch.rand((n, rows, nb, 1), generator=gen, device="cuda") * 1e-3).to(torch.float16)
+        b[..., at:at + 2] = d.view(torch.uint8).reshape(n, rows, nb, 2)
     return b.reshape(n, rows, -1).contiguous()
 
 

@@ -46,7 +46,7 @@ GGML_BLOCKS = {
 
 # The types the expert kernels decode, with the byte offsets of each block's f16 scale fields (the fields
 # llama.cpp's ggml_validate_row_data checks for finiteness; gguf_ref.py:557-560 in the reference).
-DECODED = {"Q4_0": (0,), "Q4_K": (0, 2)}
+DECODED = {"Q4_0": (0,), "Q4_K": (0, 2), "Q4_1": (0, 2), "Q8_0": (0,), "Q5_K": (0, 2), "Q6_K": (208,)}
 
 RECORD_ALIGN = 4096          # every record starts 4 KiB aligned (direct reads), a pad part filling the stride
 _CHUNK = 32                  # experts copied at a time while packing

@@ -90,17 +90,34 @@ def from_kperm(h):
     return h[:, kperm_index(h.shape[1], h.device)]
 
 
+def gemm_weights(w, t):
+    """Every expert of w [E, rows, row bytes] in ggml type t as f16 [E, rows, cols] in the GEMMs' K order
+    (lmoe_dequant_gemm_f16): the weight operand of the grouped path for the types beyond Q4_0 / Q4_K."""
+    E, rows = w.shape[0], w.shape[1]
+    _, be, bb = _lib.TYPES[t]
+    cols = w.shape[2] // bb * be
+    out = torch.empty((E, rows, cols), dtype=torch.float16, device=w.device)
+    call("lmoe_dequant_gemm_f16", ptr(w), qcode(t), E, rows, cols, ptr(out), stream())
+    return out
+
+
 def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False):
     """h [R, I] f16 (grouped order, columns in the GEMMs' K order: from_kperm undoes it) = silu(x . wg) * (x . wu)
     over the grouping G of x's rows (row p reads x[order[p] // topk]); x [T, H] in natural order, any float dtype,
-    meets the weights as f16 in the K order (converted into ``xh``; prepped: x already is that form)."""
+    meets the weights as f16 in the K order (converted into ``xh``; prepped: x already is that form). Q4_0 / Q4_K
+    weights are decoded inside the GEMM; the other types are dequantized to f16 first (gemm_weights)."""
     tg, tu = qcode(types[0]), qcode(types[1])
     if not prepped:
         x = as_gemm_f16(x, xh)
     T, H = x.shape
     E, I = wg.shape[0], wg.shape[1]
-    call("lmoe_grouped_gate_up", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
-         ptr(G.n_tiles), G.max_tiles, ptr(wg), ptr(wu), tg, tu, E, H, I, ptr(h), stream())
+    if types[0] in _lib.Q4_TYPES and types[1] == types[0]:
+        call("lmoe_grouped_gate_up", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
+             ptr(G.n_tiles), G.max_tiles, ptr(wg), ptr(wu), tg, tu, E, H, I, ptr(h), stream())
+    else:
+        wg16, wu16 = gemm_weights(wg, types[0]), gemm_weights(wu, types[1])
+        call("lmoe_grouped_gate_up_f16w", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
+             ptr(G.n_tiles), G.max_tiles, ptr(wg16), ptr(wu16), E, H, I, ptr(h), stream())
     return h
 
 
@@ -108,8 +125,13 @@ def down(h, G, wd, t, y):
     """y [R, H] (f16 / f32, grouped order, natural columns) = h . wd over the grouping G; h as gate_up leaves it."""
     E, H = wd.shape[0], wd.shape[1]
     I = h.shape[1]
-    call("lmoe_grouped_down", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, ptr(wd), qcode(t),
-         E, I, H, ptr(y), dcode(y.dtype), stream())
+    if t in _lib.Q4_TYPES:
+        call("lmoe_grouped_down", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, ptr(wd),
+             qcode(t), E, I, H, ptr(y), dcode(y.dtype), stream())
+    else:
+        wd16 = gemm_weights(wd, t)
+        call("lmoe_grouped_down_f16w", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles,
+             ptr(wd16), E, I, H, ptr(y), dcode(y.dtype), stream())
     return y
 
 

@@ -38,6 +38,25 @@ def quantized_experts(t, n, rows, cols, gen, std=0.02, chunk_rows=1 << 18):
     return out
 
 
+# byte offsets of each block type's f16 scale fields
+SCALE_AT = {"Q4_0": (0,), "Q4_K": (0, 2), "Q4_1": (0, 2), "Q8_0": (0,), "Q5_K": (0, 2), "Q6_K": (208,)}
+
+
+def random_blocks(t, n, rows, cols, gen, scale=1e-3):
+    """n experts [n, rows, row bytes] of ggml type t as random blocks with finite f16 scales in [0, scale), made on
+    the device: timing inputs for the types without a device quantizer (the kernels' time does not depend on the
+    values)."""
+    rb = row_bytes(t, cols)
+    from ._lib import TYPES
+    _, be, bb = TYPES[t]
+    nb = cols // be
+    b = torch.randint(0, 256, (n, rows, nb, bb), generator=gen, device="cuda", dtype=torch.uint8)
+    for at in SCALE_AT[t]:
+        d = (torch.rand((n, rows, nb, 1), generator=gen, device="cuda") * scale).to(torch.float16)
+        b[..., at:at + 2] = d.view(torch.uint8).reshape(n, rows, nb, 2)
+    return b.reshape(n, rows, rb).contiguous()
+
+
 def q4_0_experts(n, rows, cols, gen, std=0.02, chunk_rows=1 << 18):
     """n experts [n, rows, cols / 32 * 18] uint8 quantized from N(0, std^2) float32 weights drawn on the GPU."""
     return quantized_experts("Q4_0", n, rows, cols, gen, std, chunk_rows)

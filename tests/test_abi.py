@@ -41,8 +41,28 @@ def test_refusals_without_a_gpu(built_lib):
     assert rc == _lib.ESHAPE and b"experts" in L.lmoe_error()
     rc = L.lmoe_router_topk(p, _lib.F32, 1, 128, 33, 1, p, p, None)
     assert rc == _lib.ESHAPE and b"top-k" in L.lmoe_error()
-    rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, p, p, 8, 8, 128, 2048, 768, p, None)
-    assert rc == _lib.ETYPE and b"ggml type 8" in L.lmoe_error()
+    rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, p, p, 9, 9, 128, 2048, 768, p, None)
+    assert rc == _lib.ETYPE and b"types 9/9" in L.lmoe_error()
+    # the types beyond Q4_0 / Q4_K: the general chain only, their own row-length and alignment rules
+    rc = L.lmoe_gemv_gate_up_prepped(p, p, p, 8, 8, p, p, 14, 14, 128, 2048, 768, p, None, 14, None)
+    assert rc == _lib.ETYPE and b"general chain" in L.lmoe_error()
+    rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, p, p, 14, 14, 128, 2048 + 32, 768, p, None)
+    assert rc == _lib.ESHAPE and b"256" in L.lmoe_error()
+    rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, ctypes.c_void_p(18), p, 13, 13, 128, 2048, 768, p, None)
+    assert rc == _lib.EALIGN and b"16-byte" in L.lmoe_error()
+    rc = L.lmoe_gemv_down_combine_prepped(p, 0, p, p, 1, 8, p, 8, 128, 768, 2048, None, None, 0, None, 0, p,
+                                          _lib.F16, None)
+    assert rc == _lib.ETYPE and b"general chain" in L.lmoe_error()
+    rc = L.lmoe_dequant_gemm_f16(p, 9, 4, 16, 64, p, None)
+    assert rc == _lib.ETYPE
+    rc = L.lmoe_dequant_gemm_f16(p, 8, 4, 16, 48, p, None)
+    assert rc == _lib.ESHAPE
+    rc = L.lmoe_grouped_gate_up_f16w(p, _lib.F32, 64, 1, p, p, p, p, 4, p, p, 8, 2048, 768, p, None)
+    assert rc == _lib.EINVAL and b"float16" in L.lmoe_error()
+    rc = L.lmoe_grouped_gate_up_f16w(p, _lib.F16, 64, 1, p, p, p, p, 4, p, p, 8, 2048, 100, p, None)
+    assert rc == _lib.ESHAPE
+    rc = L.lmoe_grouped_down_f16w(p, p, p, p, 4, p, 8, 768, 2000, p, _lib.F16, None)
+    assert rc == _lib.ESHAPE
     rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, p, p, _lib.Q4_0, _lib.Q4_0, 128, 2000, 768, p, None)
     assert rc == _lib.ESHAPE
     rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, p, p, _lib.Q4_K, _lib.Q4_K, 128, 2048 + 64, 768, p, None)
@@ -55,7 +75,7 @@ def test_refusals_without_a_gpu(built_lib):
     assert rc == _lib.ESHAPE
     rc = L.lmoe_group_rows(p, 10, 2000, 128, p, p, p, p, None, None, p, None)
     assert rc == _lib.ESHAPE
-    rc = L.lmoe_dequant(p, 3, 4, 16, 64, p, 1, p, _lib.F32, None)
+    rc = L.lmoe_dequant(p, 9, 4, 16, 64, p, 1, p, _lib.F32, None)
     assert rc == _lib.ETYPE
     rc = L.lmoe_quantize_q4_0(p, _lib.F32, 4, 33, p, None)
     assert rc == _lib.ESHAPE
@@ -98,8 +118,9 @@ def test_grouped_refusals_without_a_gpu(built_lib):
 
 
 def test_python_refuses_unsupported_types():
-    with pytest.raises(ValueError, match="Q5_K"):
-        _lib.qcode("Q5_K")
+    with pytest.raises(ValueError, match="IQ4_XS"):
+        _lib.qcode("IQ4_XS")
+    assert [_lib.qcode(t) for t in ("Q4_0", "Q4_1", "Q8_0", "Q4_K", "Q5_K", "Q6_K")] == [2, 3, 8, 12, 13, 14]
 
 
 def test_gemm_k_order_index():

@@ -19,7 +19,8 @@ def host(t):
 
 
 @pytest.mark.parametrize("types,H,I", [(("Q4_0", "Q4_0", "Q4_0"), 2048, 768), (("Q4_K", "Q4_K", "Q4_K"), 1024, 512),
-                                       (("Q4_K", "Q4_K", "Q4_0"), 1024, 256)])
+                                       (("Q4_K", "Q4_K", "Q4_0"), 1024, 256), (("Q4_K", "Q4_K", "Q6_K"), 1024, 512),
+                                       (("Q8_0", "Q8_0", "Q5_K"), 1024, 256)])
 def test_packed_layer_through_kernels(tmp_path, types, H, I):
     from larder_amd import gguf_experts as ge, gguf_pack as gp
     rng = np.random.default_rng(H + I)

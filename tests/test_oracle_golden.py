@@ -1,5 +1,5 @@
 """The oracle's block decoding against vectors from the reference's own gguf_ref.ref_dequant
-(tests/golden/make_golden.py wrote them; gguf_ref.py:546-553, 564-581): bit for bit, NaN for NaN."""
+(tests/golden/make_golden.py and make_golden_types.py wrote them; gguf_ref.py:546-553, 564-581): bit for bit, NaN for NaN."""
 from pathlib import Path
 
 import numpy as np
@@ -8,11 +8,14 @@ import pytest
 from oracle import gguf
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "dequant_q4.npz"
+GOLDEN_TYPES = Path(__file__).resolve().parent / "golden" / "dequant_types.npz"
+ALL = [("Q4_0", GOLDEN), ("Q4_K", GOLDEN), ("Q4_1", GOLDEN_TYPES), ("Q5_K", GOLDEN_TYPES), ("Q6_K", GOLDEN_TYPES),
+       ("Q8_0", GOLDEN_TYPES)]
 
 
-@pytest.mark.parametrize("t", ["Q4_0", "Q4_K"])
-def test_dequant_matches_reference_vectors(t):
-    z = np.load(GOLDEN)
+@pytest.mark.parametrize("t,path", ALL)
+def test_dequant_matches_reference_vectors(t, path):
+    z = np.load(path)
     blocks, want = z[f"{t}_blocks"], z[f"{t}_want"]
     got = gguf.dequant(blocks.reshape(-1), t)
     assert got.dtype == np.float32 and got.shape == want.shape
@@ -20,9 +23,9 @@ def test_dequant_matches_reference_vectors(t):
     assert same.all(), f"{t}: {int((~same).sum())} weights differ from gguf_ref.ref_dequant"
 
 
-@pytest.mark.parametrize("t", ["Q4_0", "Q4_K"])
-def test_valid_matches_reference_vectors(t):
-    z = np.load(GOLDEN)
+@pytest.mark.parametrize("t,path", ALL)
+def test_valid_matches_reference_vectors(t, path):
+    z = np.load(path)
     blocks, want = z[f"{t}_blocks"], z[f"{t}_valid"]
     got = np.array([gguf.valid(b, t) for b in blocks])
     assert (got == want).all()
