@@ -36,8 +36,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-grouped", action="store_true", help="skip the cfg3 prefill / cfg4 batched lines")
-    ap.add_argument("--types-only", action="store_true",
-                    help="only the Q4_1 / Q8_0 / Q5_K / Q6_K lines (decode chain and grouped path), one JSON line")
+    ap.add_argument("--extra-only", action="store_true",
+                    help="only the Q4_1 / Q8_0 / Q5_K / Q6_K lines (decode chain and grouped path) and the trunk's "
+                         "qmv_rows lines, one JSON line")
     ap.add_argument("--grouped-only", action="store_true",
                     help="run only the grouped-path lines (cfg3 prefill, cfg4, cfg5) and print them: a short run to "
                          "profile the grouped GEMMs with rocprofv3 counters, not a benchmark line")
@@ -315,6 +316,43 @@ def types_leg():
     return out
 
 
+def trunk_leg():
+    """The trunk's 4-bit affine matmul (lmoe_qmv_rows) at the 35B's dense shapes the reference's test uses (K -> N,
+    group 64), T = 1 and T = 5 rows: kernel-exact durations against the HBM roofline over the weight, scale and
+    bias bytes plus x and out."""
+    import ctypes
+
+    import torch
+
+    from larder_amd import _lib, trunk
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    out = {}
+    for K, N in ((2048, 8192), (2048, 4096), (4096, 2048), (2048, 512)):
+        G = 64
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K // 8), generator=g, device="cuda", dtype=torch.int32)
+        sc = (torch.rand((N, K // G), generator=g, device="cuda") * 0.01).bfloat16()
+        bi = (torch.rand((N, K // G), generator=g, device="cuda") * -0.05).bfloat16()
+        for T in (1, 5):
+            x = torch.randn((T, K), generator=g, device="cuda").bfloat16()
+            for _ in range(5):
+                trunk.qmv_rows(x, w, sc, bi, G)
+            torch.cuda.synchronize()
+            reps = 50
+            _lib.call("lmoe_profile_arm", reps)
+            for _ in range(reps):
+                trunk.qmv_rows(x, w, sc, bi, G)
+            ms = (ctypes.c_float * reps)()
+            cnt = ctypes.c_int()
+            _lib.call("lmoe_profile_read", ms, reps, ctypes.byref(cnt))
+            us = sum(ms[:cnt.value]) / cnt.value * 1e3
+            byts = N * K // 2 + 2 * N * (K // G) * 2 + T * K * 2 + T * N * 2
+            out[f"{K}->{N} T{T}"] = {"us": round(us, 2), "bytes": byts,
+                                     "hbm_frac": round(byts / (us * 1e-6) / HBM_PEAK, 4)}
+        del w, sc, bi
+    return out
+
+
 def cpu_leg(args, g):
     """The C++ restatement of the reference CPU kernel (cpu_kern gather_qmm) over the same experts, converted to
     its affine 4-bit layout, run layer after layer for about --cpu-seconds; tokens/s = 1 / (48 x mean layer time)."""
@@ -367,14 +405,15 @@ def main():
     if args.grouped_only:
         print(json.dumps({"secondary": grouped_leg()}), flush=True)
         return
-    if args.types_only:
-        print(json.dumps({"types": types_leg()}), flush=True)
+    if args.extra_only:
+        print(json.dumps({"types": types_leg(), "trunk": trunk_leg()}), flush=True)
         return
     g = gpu_leg(args)
     cpu = None if args.no_cpu else cpu_leg(args, g)
     secondary = None if args.no_grouped else grouped_leg()
     if secondary is not None:
         secondary["types"] = types_leg()
+        secondary["trunk"] = trunk_leg()
     value = args.steps / g["secs"]
     dom = g["timing"][g["dom"]]
     achieved = dom["bytes"] / (dom["us"] * 1e-6)

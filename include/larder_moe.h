@@ -173,6 +173,19 @@ int lmoe_grouped_down_f16w(const void *h, const uint32_t *offsets, const uint32_
                            int max_tiles, const void *wd16, int n_experts, int I, int H, void *y, int ydtype,
                            void *stream);
 
+/* The trunk's 4-bit affine matmul of T bf16 rows: out [T][N] bf16 = x [T][K] bf16 . W^T with W in MLX's
+ * affine 4-bit layout (w uint32 [N][K / 8], element j of a word at bits 4j; scales, biases bf16 [N][K / G];
+ * weight = q s + b), each row with the bits of the reference's route_cuda.qmv_rows (route_cuda.py:460-541; MLX
+ * 0.32.4's one-row qmv): bf16 weights and bf16 fused multiply-add slots, float32 slot sum and lane butterfly.
+ * K % 16 == 0, G % 16 == 0, K % G == 0; x 16-byte and w 8-byte aligned. */
+int lmoe_qmv_rows(const void *x, int T, const uint32_t *w, const void *scales, const void *biases, int N, int K,
+                  int group_size, void *out, void *stream);
+
+/* out [n] bf16 = bf16(silu(g) u), float32 inside, one rounding: the SwiGLU of a shared expert run on
+ * lmoe_qmv_rows projections (mlx_lm's nn.silu(gate) * up between the reference's qmv_rows calls; the reference
+ * leaves it to MLX ops, whose bf16 bits are not reproduced here). */
+int lmoe_swiglu_bf16(const void *g, const void *u, long long n, void *out, void *stream);
+
 /* x [n] (F32 / BF16 / F16) -> out [n] float16, round to nearest even.
  * No counterpart in the reference (its dense path casts with MLX, gguf_experts.py:716). */
 int lmoe_to_f16(const void *x, int xdtype, long long n, void *out, void *stream);
