@@ -215,3 +215,37 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
          ptr(out), dcode(out.dtype), st)
     return out
 
+
+
+class PrefillStack:
+    """A chunk of T tokens through a stack of MoE layers of one shape, layer-major: x -> x + layer_l(x) for l = 0 ..
+    L-1, each layer's whole chunk on the device (router GEMM, top-k, grouping, grouped GEMMs, combine with the
+    residual fused) and no host synchronisation between layers.
+
+    The reference's layer-major prefill (stream_fast.py:5058-5210, _call_resident) schedules each layer's experts as
+    units through a ring of GPU slots, on the host, because its experts stream from SSD into a small arena. With
+    the model's experts resident in HBM (288 GB holds the 48-layer stack's 16 GB many times over) a layer is one
+    pass over its grouped rows, and the host only queues launches."""
+
+    def __init__(self, layers, T, dtype=torch.bfloat16, device="cuda"):
+        if any(L.wr is None for L in layers):
+            raise ValueError("PrefillStack: every layer needs its router weight")
+        self.layers = layers
+        self.T = T
+        self.bufs = PrefillBuffers(layers[0], T, device)
+        H = layers[0].H
+        self.ping = torch.empty((T, H), dtype=dtype, device=device)
+        self.pong = torch.empty((T, H), dtype=dtype, device=device)
+
+    def run(self, x, keep=False):
+        """The stack's output for x [T, H] (a view of ping or pong). keep: also return every layer's input and router
+        logits (copies), for checking a layer at a time."""
+        cur = x
+        trace = []
+        for i, L in enumerate(self.layers):
+            nxt = self.ping if i % 2 == 0 else self.pong
+            prefill(L, cur, self.bufs, nxt, residual=cur)
+            if keep:
+                trace.append((cur.clone(), self.bufs.logits.clone()))
+            cur = nxt
+        return (cur, trace) if keep else cur

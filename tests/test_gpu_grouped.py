@@ -207,3 +207,24 @@ def test_prefill_cfg3_full_size():
     assert rows_ok(got, want) < ROW_BAR
     assert np.isfinite(host(out.float())).all()
 
+
+
+def test_prefill_stack_layer_major():
+    """PrefillStack: 3 layers, each layer's output against the oracle on the GPU's own input to that layer (and its
+    router logits, so near-ties pick the same experts), the residual fused."""
+    from larder_amd import grouped, workloads
+    cfg = dict(workloads.CONFIGS[2], E=32)
+    g = torch.Generator(device="cuda").manual_seed(21)
+    layers = [workloads.make_layer(cfg, g) for _ in range(3)]
+    T = 200
+    S = grouped.PrefillStack(layers, T, dtype=torch.float32)
+    x = torch.randn((T, cfg["H"]), generator=g, device="cuda")
+    out, trace = S.run(x, keep=True)
+    torch.cuda.synchronize()
+    outs = [t[0] for t in trace[1:]] + [out]
+    for L, (xin, lg), xo in zip(layers, trace, outs):
+        xs = host(xin.half().float())
+        _, _, want = moe.layer(xs, host(lg), tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"], cfg["k"],
+                               cfg["norm"], residual=host(xin))
+        xr = host(xin)
+        assert moe.rel_l2(host(xo) - xr, want - xr) < BAR
