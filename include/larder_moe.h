@@ -162,6 +162,22 @@ int lmoe_grouped_down(const void *h, const uint32_t *offsets, const uint32_t *ti
                       int max_tiles, const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
                       void *stream);
 
+/* lmoe_grouped_gate_up / lmoe_grouped_down over a grouping made with tile rows bm (lmoe_group_rows' bm): 128, or
+ * 32 for Q4_0, whose 32-row tiles keep five K steps of weights in flight instead of three, for groups of few rows
+ * (batched decode, prefill over many experts), where the GEMMs stream weights rather than reuse them. ksplit > 1
+ * (32-row Q4_0 only; K / 64 divisible by it): split-K, ksplit workgroups a tile each taking a slice of K, their
+ * fp32 sums in ws (16-byte aligned, ksplit * R * 2I floats for gate/up, ksplit * R * H for down; R = T * topk rows,
+ * passed to down), then one finishing launch adds the slices in slice order and applies SwiGLU / the output
+ * conversion: more workgroups when few tiles have work. No counterpart in the reference (its dense path has no
+ * tile size). The entry points without bm use 128 and no split. */
+int lmoe_grouped_gate_up_bm(const void *x, int xdtype, int T, int topk, const uint32_t *order,
+                            const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles, int max_tiles,
+                            int bm, int ksplit, float *ws, const uint8_t *wg, const uint8_t *wu, int type_g,
+                            int type_u, int n_experts, int H, int I, void *h, void *stream);
+int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offsets, const uint32_t *tiles,
+                         const uint32_t *n_tiles, int max_tiles, int bm, int ksplit, float *ws, const uint8_t *wd,
+                         int type_d, int n_experts, int I, int H, void *y, int ydtype, void *stream);
+
 /* lmoe_grouped_gate_up / lmoe_grouped_down with f16 weights in the K order (lmoe_dequant_gemm_f16's output:
  * wg16 / wu16 [n_experts][I][H], wd16 [n_experts][H][I]) instead of Q4 blocks: the grouped path of Q4_1, Q8_0,
  * Q5_K and Q6_K experts (the reference's gather_mm on dequantized f16 experts, gguf_experts.py:698-722). Same

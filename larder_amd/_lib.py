@@ -52,6 +52,9 @@ SIGNATURES = {
     "lmoe_to_gemm_f16": (_I, [_P, _I, _LL, _P, _P]),
     "lmoe_grouped_gate_up": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "lmoe_grouped_down": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
+    "lmoe_grouped_gate_up_bm": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P,
+                                     _P]),
+    "lmoe_grouped_down_bm": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_combine_sorted": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_dequant": (_I, [_P, _I, _I, _I, _I, _P, _I, _P, _I, _P]),
     "lmoe_dequant_gemm_f16": (_I, [_P, _I, _I, _I, _I, _P, _P]),

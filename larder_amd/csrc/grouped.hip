@@ -90,23 +90,28 @@ __device__ __forceinline__ half8 decode8(uint32_t x, uint32_t sw, int half) {
 
 // Tile bookkeeping shared by both kernels
 struct Tile {
-  int e, nt, row0, rows;
+  int e, nt, row0, rows, kpart;
 };
 
 // XCD-aware remap: workgroup `wid` runs on XCD wid % 8; XCD x gets logical work [start_x, start_x + count_x).
 // Returns false for workgroups past the device-side work count.
+// ksplit > 1: each (tile, n-tile) is worked by ksplit workgroups, one a slice of K (t->kpart), next to each other
+// in the logical order.
+template <int GMT = GM>
 __device__ __forceinline__ bool tile_of(const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
-                                        int n_ntile, Tile *t) {
-  const uint32_t W = n_tiles[0] * uint32_t(n_ntile);
+                                        int n_ntile, Tile *t, int ksplit = 1) {
+  const uint32_t W = n_tiles[0] * uint32_t(n_ntile) * uint32_t(ksplit);
   const uint32_t wid = blockIdx.x;
   if (wid >= W) return false;
   const uint32_t q8 = W >> 3, r8 = W & 7, xcd = wid & 7;
-  const uint32_t logical = xcd * q8 + min(xcd, r8) + (wid >> 3);
+  const uint32_t logical0 = xcd * q8 + min(xcd, r8) + (wid >> 3);
+  t->kpart = int(logical0 % uint32_t(ksplit));
+  const uint32_t logical = logical0 / uint32_t(ksplit);
   const uint32_t tile = tiles[logical / uint32_t(n_ntile)];
   t->nt = int(logical % uint32_t(n_ntile));
   t->e = int(tile >> 20);
-  t->row0 = int(offsets[t->e]) + int(tile & kTileMask) * GM;
-  t->rows = min(GM, int(offsets[t->e + 1]) - t->row0);
+  t->row0 = int(offsets[t->e]) + int(tile & kTileMask) * GMT;
+  t->rows = min(GMT, int(offsets[t->e + 1]) - t->row0);
   return true;
 }
 
@@ -120,11 +125,11 @@ __device__ __forceinline__ int frag_feature(int wave, int nb) {
 
 // acc[nb][mb][r] = D[tile feature frag_feature(nb) + 4 g + r][tile row 16 mb + fr]. Gate/up: h (f16, K order) =
 // silu(gate) * up; down: y (F32 / F16, natural order).
-template <int MODE>
-__device__ __forceinline__ void store_tile(f32x4 (&acc)[4][8], const Tile &t, int wave, int fr, int g, void *out,
+template <int MODE, int MB = 8>
+__device__ __forceinline__ void store_tile(f32x4 (&acc)[4][MB], const Tile &t, int wave, int fr, int g, void *out,
                                            int ldo, int odt) {
 #pragma unroll
-  for (int mb = 0; mb < 8; ++mb) {
+  for (int mb = 0; mb < MB; ++mb) {
     const int m = 16 * mb + fr;
     if (m >= t.rows) continue;
     const size_t o = size_t(t.row0 + m) * ldo;
@@ -158,10 +163,11 @@ __device__ __forceinline__ void store_tile(f32x4 (&acc)[4][8], const Tile &t, in
 
 // ---- Q4_0: global -> LDS directly, three stages ------------------------------------------------------------------
 
-constexpr int kQ0AStage = GM * 128;             // A tile bytes a stage
+// Per tile-row count GMT (128, or 32 for groups of few rows): A tile bytes a stage, the stage, A copies a lane.
+template <int GMT> constexpr int q0_astage() { return GMT * 128; }
 constexpr int kQ0WHead = GN * 32;               // the first 32 bytes of every unit (words 0-7), 32 a feature
-constexpr int kQ0Stage = kQ0AStage + GN * 36;   // + word 8 of every unit, 4 bytes a feature: 25600
-constexpr int kQ0DmaA = GM * 128 / 1024 / 4;    // 16-byte A copies a lane a step (4)
+template <int GMT> constexpr int q0_stage() { return q0_astage<GMT>() + GN * 36; }  // + word 8 of every unit
+template <int GMT> constexpr int q0_dma_a() { return GMT * 128 / 1024 / 4; }      // 16-byte A copies a lane a step
 constexpr int kQ0DmaW = GN * 32 / 1024 / 4;     // 16-byte unit-head copies a lane a step (2), plus one 4-byte copy
 
 // One wavefront-wide global -> LDS copy: lane l's `BYTES` (4 or 16) at base + voff land at LDS address
@@ -183,18 +189,33 @@ __device__ __forceinline__ void barrier_lds() {
   asm volatile("" ::: "memory");
 }
 
+// s_waitcnt on the vector-memory counter only (the copies this wavefront issued), N outstanding at most
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Grid: n_ntile * max_tiles workgroups of 256 threads, two a CU. GATE_UP: n-tile j covers intermediate features
 // 128 j .. 128 j + 127 (tile features 0..127 their gate rows, 128..255 their up rows), K = H, A rows
 // x[order[p] / topk], out h [R][I] f16. DOWN: n-tile j covers output features 256 j .., K = I, A rows h[p], out
 // y [R][H] in odt (F16 / F32). Host guarantees: K % 64 == 0, rows x K x 2 and the expert's weight block under 4 GiB.
-template <int MODE>
+// GMT: tile rows (the grouping's bm): 128 with NST = 3 stages, or 32 with NST = 5 for groups of few rows, where
+// the kernel streams weights and more steps in flight matter more than A reuse.
+// ksplit > 1 (32-row tiles): workgroup kpart takes K steps [kpart nk / ksplit, +nk / ksplit) and writes its fp32
+// sums to ws[kpart][row][feature] (features: gate/up = gate 0..I-1, up I..2I-1; down = 0..H-1; ldw of them a row,
+// R rows a slice); k_splitk_finish adds the slices and applies the epilogue.
+template <int MODE, int GMT = GM, int NST = 3>
 __global__ void __launch_bounds__(kThreads, 2)
 k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
                const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
-               int K, int n_rows, void *out, int ldo, int odt) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kQ0Stage];
+               int K, int n_rows, void *out, int ldo, int odt, int ksplit = 1, float *ws = nullptr, int R = 0,
+               int ldw = 0) {
+  constexpr int kQ0AStage = q0_astage<GMT>(), kQ0Stage = q0_stage<GMT>(), kQ0DmaA = q0_dma_a<GMT>();
+  constexpr int MB = GMT / 16, QMAX = GMT / 32;
+  static_assert(kQ0DmaA >= 1 && NST >= 3, "tile and pipeline shape");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[NST * kQ0Stage];
   Tile t;
-  if (!tile_of(offsets, tiles, n_tiles, n_ntile, &t)) return;
+  if (!tile_of<GMT>(offsets, tiles, n_tiles, n_ntile, &t, ksplit)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, g = lane >> 4;
   const uint32_t wrow = 36u * uint32_t(K / 64);
@@ -229,14 +250,14 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
     }
     w_off[kQ0DmaW] = uint32_t(row_base + 64 * wave + lane) * wrow + 32u;
   }
-  const int nk = K / GK;
-  auto issue = [&](int kk) {  // step kk into stage kk % 3
-    const uint32_t st = lds0 + uint32_t(kk % 3) * kQ0Stage;
-    const _Float16 *ab = a_src + size_t(kk) * GK;
+  const int nk = K / GK / ksplit, k0 = t.kpart * nk;  // this workgroup's K steps: k0 .. k0 + nk - 1
+  auto issue = [&](int kk) {  // step kk (of the slice) into stage kk % NST
+    const uint32_t st = lds0 + uint32_t(kk % NST) * kQ0Stage;
+    const _Float16 *ab = a_src + size_t(k0 + kk) * GK;
 #pragma unroll
     for (int i = 0; i < kQ0DmaA; ++i)
       dma<16>(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kQ0DmaA * wave + i)));
-    const uint8_t *wb = wbase + size_t(kk) * 36;
+    const uint8_t *wb = wbase + size_t(k0 + kk) * 36;
 #pragma unroll
     for (int i = 0; i < kQ0DmaW; ++i)
       dma<16>(wb, w_off[i], __builtin_amdgcn_readfirstlane(st + kQ0AStage + 1024u * uint32_t(kQ0DmaW * wave + i)));
@@ -246,11 +267,11 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   int wfeat[4];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) wfeat[nb] = frag_feature<MODE>(wave, nb) + fr;
-  f32x4 acc[4][8];
+  f32x4 acc[4][MB];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // Lane (fr, g) of fragment nb decodes feature wfeat[nb]'s unit: block 0 qs bytes 4g..+3 (unit bytes 2 + 4g..,
   // straddling words g and g + 1), block 1 qs bytes 4g..+3 (word 5 + g; word 8 sits in the tail area), d0 / d1 in
@@ -327,40 +348,96 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
     }
   };
 
-  // Step kk: the copies of step kk + 2 go out, step kk multiplies out of its stage, then each wavefront waits for
-  // its own copies of step kk + 1 (the counter counts in issue order: the 7 copies of kk + 2 may still be out)
-  // and the barrier publishes the stage. The barrier also tells the step after that stage kk % 3,
+  // Step kk: the copies of step kk + NST - 1 go out, step kk multiplies out of its stage, then each wavefront waits
+  // for its own copies of step kk + 1 (the counter counts in issue order: the copies of the steps after kk + 1 may
+  // still be out) and the barrier publishes the stage. The barrier also tells the next step that stage kk % NST,
   // which it refills, has been read by every wavefront.
-  issue(0);
-  if (nk > 1) {
-    issue(1);
-    asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
-  } else {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
-  static_assert(kQ0DmaA + kQ0DmaW + 1 == 7, "the wait counts below assume 7 copies a step");
+  constexpr int C = kQ0DmaA + kQ0DmaW + 1;  // copies a lane a step
+  static_assert(NST <= 5 && 3 * C <= 63, "the wait counts below");
+  auto wait_steps = [&](int later) {  // until at most `later` steps' copies are still out
+    if (later <= 0)
+      wait_vm<0>();
+    else if (later == 1)
+      wait_vm<C>();
+    else if (later == 2)
+      wait_vm<2 * C>();
+    else
+      wait_vm<3 * C>();
+  };
+  const int pre = min(NST - 1, nk);
+  for (int j = 0; j < pre; ++j) issue(j);
+  wait_steps(pre - 1);
   barrier_lds();
   auto run = [&](auto qn) {
     for (int kk = 0; kk < nk; ++kk) {
-      const bool more = kk + 2 < nk;
-      if (more) issue(kk + 2);
-      compute(kk % 3, qn);
+      if (kk + NST - 1 < nk) issue(kk + NST - 1);
+      compute(kk % NST, qn);
       if (kk + 1 < nk) {
-        if (more)
-          asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
-        else
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        wait_steps(min(kk + NST - 1, nk - 1) - (kk + 1));
         barrier_lds();
       }
     }
   };
-  switch ((t.rows + 31) / 32) {  // uniform across the workgroup
-    case 1: run(IC<1>{}); break;
-    case 2: run(IC<2>{}); break;
-    case 3: run(IC<3>{}); break;
-    default: run(IC<4>{}); break;
+  if constexpr (QMAX == 1) {
+    run(IC<1>{});
+  } else {
+    switch ((t.rows + 31) / 32) {  // uniform across the workgroup
+      case 1: run(IC<1>{}); break;
+      case 2: run(IC<2>{}); break;
+      case 3: run(IC<3>{}); break;
+      default: run(IC<4>{}); break;
+    }
   }
-  store_tile<MODE>(acc, t, wave, fr, g, out, ldo, odt);
+  if (ksplit > 1) {
+    // fp32 partial sums of this K slice: 4 consecutive features of one row a store
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = 16 * mb + fr;
+      if (m >= t.rows) continue;
+      float *wrow = ws + (size_t(t.kpart) * R + t.row0 + m) * ldw;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const int f = frag_feature<MODE>(wave, nb) + 4 * g;
+        const int n = MODE == MODE_GATE_UP ? (f < GN / 2 ? t.nt * (GN / 2) + f : ldw / 2 + t.nt * (GN / 2) + f - GN / 2)
+                                           : t.nt * GN + f;
+        *reinterpret_cast<f32x4 *>(wrow + n) = acc[nb][mb];
+      }
+    }
+    return;
+  }
+  store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
+}
+
+// Finishes a split-K grouped GEMM: rows p < offsets[E] (the grouped rows of real experts), 4 features a thread:
+// the ksplit slices of ws added in slice order, then gate/up: h[p][K order of i] = f16(silu(g) u) for features
+// i .. i + 3 of I; down: y[p][n] (F16 / F32). Grid (ceil(N / 1024), R): N = I (gate/up) or H (down).
+template <int MODE>
+__global__ void __launch_bounds__(256) k_splitk_finish(const float *ws, int ksplit, int R, int ldw,
+                                                       const uint32_t *offsets, int E, void *out, int ldo, int odt) {
+  const int p = blockIdx.y;
+  if (p >= int(offsets[E])) return;
+  const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
+  const int N = MODE == MODE_GATE_UP ? ldw / 2 : ldw;
+  if (n >= N) return;
+  f32x4 a = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+  for (int s = 0; s < ksplit; ++s) {
+    const float *row = ws + (size_t(s) * R + p) * ldw;
+    a += *reinterpret_cast<const f32x4 *>(row + n);
+    if (MODE == MODE_GATE_UP) b += *reinterpret_cast<const f32x4 *>(row + N + n);
+  }
+  const size_t o = size_t(p) * ldo;
+  if (MODE == MODE_GATE_UP) {
+    const h2_t v01 = {_Float16(silu_mul(a[0], b[0])), _Float16(silu_mul(a[1], b[1]))};
+    const h2_t v23 = {_Float16(silu_mul(a[2], b[2])), _Float16(silu_mul(a[3], b[3]))};
+    *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + kperm4(n)) =
+        u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
+  } else if (odt == LMOE_F32) {
+    *reinterpret_cast<f32x4 *>(static_cast<float *>(out) + o + n) = a;
+  } else {
+    const h2_t v01 = {_Float16(a[0]), _Float16(a[1])}, v23 = {_Float16(a[2]), _Float16(a[3])};
+    *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + n) =
+        u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
+  }
 }
 
 // ---- f16 weights (the other block types, dequantized in the K order): both operands global -> LDS ---------------
@@ -665,11 +742,27 @@ extern "C" int lmoe_to_gemm_f16(const void *x, int xdtype, long long n, void *ou
   return to_f16("lmoe_to_gemm_f16", x, xdtype, n, out, stream, 1);
 }
 
-extern "C" int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, const uint32_t *order,
-                                    const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
-                                    int max_tiles, const uint8_t *wg, const uint8_t *wu, int type_g, int type_u,
-                                    int n_experts, int H, int I, void *h, void *stream) {
-  const char *fn = "lmoe_grouped_gate_up";
+// ksplit > 1: the split-K form (32-row Q4_0 tiles): ksplit workgroups a tile, fp32 slices in ws, then
+// k_splitk_finish. Checks shared by both GEMMs.
+static int check_split(const char *fn, int bm, int type, int ksplit, const float *ws, int K, int R) {
+  LMOE_REQUIRE(ksplit >= 1 && ksplit <= 8, LMOE_ESHAPE, "%s: ksplit %d (1..8)", fn, ksplit);
+  if (ksplit == 1) return 0;
+  LMOE_REQUIRE(bm == 32 && type == LMOE_Q4_0, LMOE_ESHAPE, "%s: split-K takes 32-row Q4_0 tiles", fn);
+  LMOE_REQUIRE((K / GK) % ksplit == 0, LMOE_ESHAPE, "%s: %d K steps do not split in %d", fn, K / GK, ksplit);
+  LMOE_REQUIRE(R <= 65535, LMOE_ESHAPE, "%s: %d rows is above the 65535 split-K takes", fn, R);
+  LMOE_REQUIRE(ws && aligned16(ws), LMOE_EWORKSPACE, "%s: split-K needs a 16-byte aligned workspace", fn);
+  return 0;
+}
+
+extern "C" int lmoe_grouped_gate_up_bm(const void *x, int xdtype, int T, int topk, const uint32_t *order,
+                                       const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
+                                       int max_tiles, int bm, int ksplit, float *ws, const uint8_t *wg,
+                                       const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I,
+                                       void *h, void *stream) {
+  const char *fn = "lmoe_grouped_gate_up_bm";
+  LMOE_REQUIRE(bm == GM || (bm == 32 && type_g == LMOE_Q4_0), LMOE_ESHAPE,
+               "%s: tile rows %d (128, or 32 for Q4_0)", fn, bm);
+  if (int rc = check_split(fn, bm, type_g, ksplit, ws, H, T * topk)) return rc;
   LMOE_REQUIRE(qtype_ok(type_g) && qtype_ok(type_u), LMOE_ETYPE,
                "%s: ggml types %d/%d are not supported (Q4_0 = 2, Q4_K = 12)", fn, type_g, type_u);
   LMOE_REQUIRE(type_g == type_u, LMOE_ETYPE, "%s: gate and up must share one type on this path (%d vs %d)", fn,
@@ -686,15 +779,22 @@ extern "C" int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, 
   LMOE_REQUIRE(aligned16(x) && aligned16(h) && aligned4(wg) && aligned4(wu), LMOE_EALIGN,
                "%s: x and h must be 16-byte aligned, weights 4-byte aligned", fn);
   const int n_ntile = I / (GN / 2);
-  const long long grid = (long long)n_ntile * max_tiles;
+  const long long grid = (long long)n_ntile * max_tiles * ksplit;
   LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
   hipStream_t st = (hipStream_t)stream;
   const _Float16 *a = static_cast<const _Float16 *>(x);
   if (type_g == LMOE_Q4_0) {
     LMOE_REQUIRE((long long)T * H * 2 <= 0xFFFFFFFFll && (long long)I * (H / 64) * 36 <= 0xFFFFFFFFll, LMOE_ESHAPE,
                  "%s: x or one expert's weights exceed 4 GiB", fn);
-    launch(k_grouped_q4_0<MODE_GATE_UP>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles,
-           n_tiles, n_ntile, wg, wu, H, I, h, I, int(LMOE_F16));
+    const int R = T * topk;
+    launch(bm == 32 ? k_grouped_q4_0<MODE_GATE_UP, 32, 5> : k_grouped_q4_0<MODE_GATE_UP>, dim3(unsigned(grid)),
+           dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg, wu, H, I, h, I,
+           int(LMOE_F16), ksplit, ws, R, 2 * I);
+    if (ksplit > 1) {
+      LMOE_LAUNCHED(fn);
+      launch(k_splitk_finish<MODE_GATE_UP>, dim3(unsigned((I / 4 + 255) / 256), unsigned(R)), dim3(256), 0, st,
+             static_cast<const float *>(ws), ksplit, R, 2 * I, offsets, n_experts, h, I, int(LMOE_F16));
+    }
   } else {
     launch(k_grouped_q4_k<MODE_GATE_UP>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles,
            n_tiles, n_ntile, wg, wu, H, I, h, I, int(LMOE_F16));
@@ -703,10 +803,15 @@ extern "C" int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, 
   return 0;
 }
 
-extern "C" int lmoe_grouped_down(const void *h, const uint32_t *offsets, const uint32_t *tiles,
-                                 const uint32_t *n_tiles, int max_tiles, const uint8_t *wd, int type_d, int n_experts,
-                                 int I, int H, void *y, int ydtype, void *stream) {
-  const char *fn = "lmoe_grouped_down";
+extern "C" int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offsets, const uint32_t *tiles,
+                                    const uint32_t *n_tiles, int max_tiles, int bm, int ksplit, float *ws,
+                                    const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
+                                    void *stream) {
+  const char *fn = "lmoe_grouped_down_bm";
+  LMOE_REQUIRE(bm == GM || (bm == 32 && type_d == LMOE_Q4_0), LMOE_ESHAPE,
+               "%s: tile rows %d (128, or 32 for Q4_0)", fn, bm);
+  LMOE_REQUIRE(R >= 0, LMOE_ESHAPE, "%s: bad row count", fn);
+  if (int rc = check_split(fn, bm, type_d, ksplit, ws, I, R)) return rc;
   LMOE_REQUIRE(qtype_ok(type_d), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn, type_d);
   LMOE_REQUIRE(n_experts > 0 && max_tiles >= 0, LMOE_ESHAPE, "%s: bad shape", fn);
   LMOE_REQUIRE(I > 0 && I % block_weights(type_d) == 0 && I % 64 == 0, LMOE_ESHAPE,
@@ -718,17 +823,22 @@ extern "C" int lmoe_grouped_down(const void *h, const uint32_t *offsets, const u
   LMOE_REQUIRE(aligned16(h) && aligned16(y) && aligned4(wd), LMOE_EALIGN,
                "%s: h and y must be 16-byte aligned, weights 4-byte aligned", fn);
   const int n_ntile = H / GN;
-  const long long grid = (long long)n_ntile * max_tiles;
+  const long long grid = (long long)n_ntile * max_tiles * ksplit;
   LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
   hipStream_t st = (hipStream_t)stream;
   const _Float16 *a = static_cast<const _Float16 *>(h);
   if (type_d == LMOE_Q4_0) {
     // R is not passed: offsets[E] <= max_tiles * bm rows of h can be read
-    LMOE_REQUIRE((long long)max_tiles * GM * I * 2 <= 0xFFFFFFFFll && (long long)H * (I / 64) * 36 <= 0xFFFFFFFFll,
+    LMOE_REQUIRE((long long)max_tiles * bm * I * 2 <= 0xFFFFFFFFll && (long long)H * (I / 64) * 36 <= 0xFFFFFFFFll,
                  LMOE_ESHAPE, "%s: h or one expert's weights exceed 4 GiB", fn);
-    launch(k_grouped_q4_0<MODE_DOWN>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1,
-           static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile, wd,
-           static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
+    launch(bm == 32 ? k_grouped_q4_0<MODE_DOWN, 32, 5> : k_grouped_q4_0<MODE_DOWN>, dim3(unsigned(grid)),
+           dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile,
+           wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype, ksplit, ws, R, H);
+    if (ksplit > 1) {
+      LMOE_LAUNCHED(fn);
+      launch(k_splitk_finish<MODE_DOWN>, dim3(unsigned((H / 4 + 255) / 256), unsigned(R)), dim3(256), 0, st,
+             static_cast<const float *>(ws), ksplit, R, H, offsets, n_experts, y, H, ydtype);
+    }
   } else {
     launch(k_grouped_q4_k<MODE_DOWN>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1,
            static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile, wd,
@@ -736,6 +846,21 @@ extern "C" int lmoe_grouped_down(const void *h, const uint32_t *offsets, const u
   }
   LMOE_LAUNCHED(fn);
   return 0;
+}
+
+extern "C" int lmoe_grouped_gate_up(const void *x, int xdtype, int T, int topk, const uint32_t *order,
+                                    const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
+                                    int max_tiles, const uint8_t *wg, const uint8_t *wu, int type_g, int type_u,
+                                    int n_experts, int H, int I, void *h, void *stream) {
+  return lmoe_grouped_gate_up_bm(x, xdtype, T, topk, order, offsets, tiles, n_tiles, max_tiles, GM, 1, nullptr, wg,
+                                 wu, type_g, type_u, n_experts, H, I, h, stream);
+}
+
+extern "C" int lmoe_grouped_down(const void *h, const uint32_t *offsets, const uint32_t *tiles,
+                                 const uint32_t *n_tiles, int max_tiles, const uint8_t *wd, int type_d, int n_experts,
+                                 int I, int H, void *y, int ydtype, void *stream) {
+  return lmoe_grouped_down_bm(h, 0, offsets, tiles, n_tiles, max_tiles, GM, 1, nullptr, wd, type_d, n_experts, I, H,
+                              y, ydtype, stream);
 }
 
 extern "C" int lmoe_grouped_gate_up_f16w(const void *x, int xdtype, int T, int topk, const uint32_t *order,

@@ -25,11 +25,38 @@ def tile_rows():
     return _lib.lib().lmoe_grouped_tile_rows()
 
 
-class Grouping:
-    """Device buffers of one grouping of R rows over E experts (allocated once, reusable for any ids of R rows)."""
+def pick_tile_rows(R, E, types):
+    """The GEMMs' tile rows for R rows over E experts: 32 when every projection is Q4_0 and the average expert has
+    fewer than 64 rows (the kernels then stream weights, and 32-row tiles keep more K steps of them in flight),
+    otherwise 128."""
+    return 32 if all(t == "Q4_0" for t in types) and R < 64 * E else tile_rows()
 
-    def __init__(self, R, E, device="cuda"):
-        self.R, self.E, self.bm = int(R), int(E), tile_rows()
+
+def pick_ksplit(R, E, bm, K):
+    """Split-K slices for a GEMM over K of R rows in E experts: with 32-row tiles and fewer than 16 rows an expert
+    on average, few tiles have work and each would walk every K step alone, so each tile is split over 4, 3 or 2
+    workgroups (at least 4 K steps each); otherwise 1."""
+    steps = K // 64
+    if bm != 32 or R >= 16 * E:
+        return 1
+    for s in (4, 3, 2):
+        if steps % s == 0 and steps // s >= 4:
+            return s
+    return 1
+
+
+def splitk_floats(R, E, bm, H, I):
+    """Floats of the split-K workspace that gate_up and down over this grouping need (0 without a split)."""
+    return max(pick_ksplit(R, E, bm, H) * R * 2 * I if pick_ksplit(R, E, bm, H) > 1 else 0,
+               pick_ksplit(R, E, bm, I) * R * H if pick_ksplit(R, E, bm, I) > 1 else 0)
+
+
+class Grouping:
+    """Device buffers of one grouping of R rows over E experts (allocated once, reusable for any ids of R rows),
+    in m-tiles of bm rows (128 by default; see pick_tile_rows)."""
+
+    def __init__(self, R, E, device="cuda", bm=None):
+        self.R, self.E, self.bm = int(R), int(E), int(bm) if bm else tile_rows()
         self.max_tiles = _lib.lib().lmoe_max_tiles(self.R, self.E, self.bm)
         i32 = dict(dtype=torch.int32, device=device)
         self.counts = torch.empty(E, **i32)
@@ -101,34 +128,51 @@ def gemm_weights(w, t):
     return out
 
 
-def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False):
+def _ws(n, ws, device):
+    if n == 0:
+        return None
+    if ws is not None and ws.numel() >= n:
+        return ws
+    return torch.empty(n, dtype=torch.float32, device=device)
+
+
+def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False, ws=None, ksplit=None):
     """h [R, I] f16 (grouped order, columns in the GEMMs' K order: from_kperm undoes it) = silu(x . wg) * (x . wu)
     over the grouping G of x's rows (row p reads x[order[p] // topk]); x [T, H] in natural order, any float dtype,
     meets the weights as f16 in the K order (converted into ``xh``; prepped: x already is that form). Q4_0 / Q4_K
-    weights are decoded inside the GEMM; the other types are dequantized to f16 first (gemm_weights)."""
+    weights are decoded inside the GEMM; the other types are dequantized to f16 first (gemm_weights). ksplit
+    (None: pick_ksplit) and ws (the split-K workspace, allocated when not given) drive split-K."""
     tg, tu = qcode(types[0]), qcode(types[1])
     if not prepped:
         x = as_gemm_f16(x, xh)
     T, H = x.shape
     E, I = wg.shape[0], wg.shape[1]
     if types[0] in _lib.Q4_TYPES and types[1] == types[0]:
-        call("lmoe_grouped_gate_up", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
-             ptr(G.n_tiles), G.max_tiles, ptr(wg), ptr(wu), tg, tu, E, H, I, ptr(h), stream())
+        ks = ksplit or (pick_ksplit(G.R, G.E, G.bm, H) if types[0] == "Q4_0" else 1)
+        w = _ws(ks * G.R * 2 * I if ks > 1 else 0, ws, x.device)
+        call("lmoe_grouped_gate_up_bm", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
+             ptr(G.n_tiles), G.max_tiles, G.bm, ks, ptr(w), ptr(wg), ptr(wu), tg, tu, E, H, I, ptr(h), stream())
     else:
+        if G.bm != tile_rows():
+            raise ValueError(f"the f16-weight GEMMs take {tile_rows()}-row tiles, not {G.bm}")
         wg16, wu16 = gemm_weights(wg, types[0]), gemm_weights(wu, types[1])
         call("lmoe_grouped_gate_up_f16w", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
              ptr(G.n_tiles), G.max_tiles, ptr(wg16), ptr(wu16), E, H, I, ptr(h), stream())
     return h
 
 
-def down(h, G, wd, t, y):
+def down(h, G, wd, t, y, ws=None, ksplit=None):
     """y [R, H] (f16 / f32, grouped order, natural columns) = h . wd over the grouping G; h as gate_up leaves it."""
     E, H = wd.shape[0], wd.shape[1]
     I = h.shape[1]
     if t in _lib.Q4_TYPES:
-        call("lmoe_grouped_down", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, ptr(wd),
-             qcode(t), E, I, H, ptr(y), dcode(y.dtype), stream())
+        ks = ksplit or (pick_ksplit(G.R, G.E, G.bm, I) if t == "Q4_0" else 1)
+        w = _ws(ks * G.R * H if ks > 1 else 0, ws, h.device)
+        call("lmoe_grouped_down_bm", ptr(h), G.R, ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, G.bm,
+             ks, ptr(w), ptr(wd), qcode(t), E, I, H, ptr(y), dcode(y.dtype), stream())
     else:
+        if G.bm != tile_rows():
+            raise ValueError(f"the f16-weight GEMMs take {tile_rows()}-row tiles, not {G.bm}")
         wd16 = gemm_weights(wd, t)
         call("lmoe_grouped_down_f16w", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles,
              ptr(wd16), E, I, H, ptr(y), dcode(y.dtype), stream())
@@ -144,7 +188,7 @@ def expert_rows(x, w, host, types, out_dtype):
     E, I = wg.shape[0], wg.shape[1]
     dev = x.device
     ids = torch.as_tensor(host).reshape(-1).to(device=dev, dtype=torch.int32)
-    G = Grouping(R, E, dev).run(ids)
+    G = Grouping(R, E, dev, bm=pick_tile_rows(R, E, types)).run(ids)
     h = torch.empty((R, I), dtype=torch.float16, device=dev)
     y = torch.empty((R, H), dtype=torch.float16, device=dev)
     gate_up(x.contiguous(), G, 1, wg, wu, types, h)
@@ -167,7 +211,9 @@ class PrefillBuffers:
         self.logits = torch.empty((T, L.E + (1 if L.shared is not None else 0)), **f32)
         self.ids = torch.empty((T, L.k), dtype=torch.int32, device=device)
         self.scores = torch.empty((T, L.k), **f32)
-        self.G = Grouping(R, L.E, device)
+        self.G = Grouping(R, L.E, device, bm=pick_tile_rows(R, L.E, L.types))
+        nws = splitk_floats(R, L.E, self.G.bm, L.H, L.I)
+        self.ws = torch.empty(nws, **f32) if nws else None
         self.xh = torch.empty((T, L.H), dtype=torch.float16, device=device)
         self.h = torch.empty((R, L.I), dtype=torch.float16, device=device)
         self.y = torch.empty((R, L.H), dtype=torch.float16, device=device)
@@ -201,8 +247,8 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
         sel = lg[:, :L.E].contiguous()
         call("lmoe_router_topk", ptr(sel), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
     B.G.run(B.ids.reshape(-1))
-    gate_up(x, B.G, L.k, L.wg, L.wu, L.types, B.h, B.xh)
-    down(B.h, B.G, L.wd, L.types[2], B.y)
+    gate_up(x, B.G, L.k, L.wg, L.wu, L.types, B.h, B.xh, ws=B.ws)
+    down(B.h, B.G, L.wd, L.types[2], B.y, ws=B.ws)
     shared = gate = None
     if L.shared is not None:
         sg, su, sd = L.shared

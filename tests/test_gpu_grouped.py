@@ -228,3 +228,34 @@ def test_prefill_stack_layer_major():
                                cfg["norm"], residual=host(xin))
         xr = host(xin)
         assert moe.rel_l2(host(xo) - xr, want - xr) < BAR
+
+
+@pytest.mark.parametrize("bm,ks", [(32, 1), (128, 1), (32, 4), (32, 2)])
+def test_q4_0_tile_rows_both_kernels(bm, ks):
+    """The Q4_0 GEMMs at both tile heights (32 rows with five K steps in flight, 128 with three), and split-K over
+    32-row tiles (4 and 2 slices), on the same ragged rows, gate/up and down, against the oracle: groups of 0, 1,
+    31, 32, 33, 64 and 200 rows, a slot past the experts."""
+    from larder_amd import grouped
+    types, H, I, E = ("Q4_0",) * 3, 2048, 768, 9
+    w = experts(types, H, I, E, 77)
+    rng = np.random.default_rng(bm)
+    sizes = [0, 1, 31, 32, 33, 64, 200, 5, 2]
+    slots = np.concatenate([np.full(n, e) for e, n in enumerate(sizes)]).astype(np.int32)
+    rng.shuffle(slots)
+    slots[3] = E + 1
+    R = slots.size
+    x = dev(rng.standard_normal((R, H)).astype(np.float16))
+    G = grouped.Grouping(R, E, bm=bm).run(dev(slots))
+    h = torch.empty((R, I), dtype=torch.float16, device="cuda")
+    y = torch.empty((R, H), dtype=torch.float32, device="cuda")
+    grouped.gate_up(x, G, 1, dev(w[0]), dev(w[1]), types, h, ksplit=ks)
+    grouped.down(h, G, dev(w[2]), types[2], y, ksplit=ks)
+    torch.cuda.synchronize()
+    order = host(G.order)
+    valid = slots[order] < E
+    hw, yw = moe.gemv(host(x.float()), w, slots, 1, types)
+    got_h = host(grouped.from_kperm(h).float())[valid]
+    assert moe.rel_l2(got_h, hw[order][valid]) < BAR
+    got_y = host(y)[valid]
+    assert moe.rel_l2(got_y, yw[order][valid]) < BAR
+    assert rows_ok(got_y, yw[order][valid]) < ROW_BAR
