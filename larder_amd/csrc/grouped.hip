@@ -199,8 +199,8 @@ __device__ __forceinline__ void wait_vm() {
 // 128 j .. 128 j + 127 (tile features 0..127 their gate rows, 128..255 their up rows), K = H, A rows
 // x[order[p] / topk], out h [R][I] f16. DOWN: n-tile j covers output features 256 j .., K = I, A rows h[p], out
 // y [R][H] in odt (F16 / F32). Host guarantees: K % 64 == 0, rows x K x 2 and the expert's weight block under 4 GiB.
-// GMT: tile rows (the grouping's bm): 128 with NST = 3 stages, or 32 with NST = 5 for groups of few rows, where
-// the kernel streams weights and more steps in flight matter more than A reuse.
+// GMT: tile rows (the grouping's bm): 128 with NST = 3 stages, 64 with 4, or 32 with 5 for groups of few rows,
+// where the kernel streams weights and more steps in flight matter more than A reuse.
 // ksplit > 1 (32-row tiles): workgroup kpart takes K steps [kpart nk / ksplit, +nk / ksplit) and writes its fp32
 // sums to ws[kpart][row][feature] (features: gate/up = gate 0..I-1, up I..2I-1; down = 0..H-1; ldw of them a row,
 // R rows a slice); k_splitk_finish adds the slices and applies the epilogue.
@@ -380,6 +380,11 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   };
   if constexpr (QMAX == 1) {
     run(IC<1>{});
+  } else if constexpr (QMAX == 2) {
+    if (t.rows <= 32)  // uniform across the workgroup
+      run(IC<1>{});
+    else
+      run(IC<2>{});
   } else {
     switch ((t.rows + 31) / 32) {  // uniform across the workgroup
       case 1: run(IC<1>{}); break;
@@ -584,29 +589,35 @@ __device__ __forceinline__ void pack_w_q4_k(const uint32_t *r, int kk, uint32_t 
   }
 }
 
-// Same grid and arguments as k_grouped_q4_0.
-template <int MODE>
+// Same grid and arguments as k_grouped_q4_0. GMT: tile rows (128, 64 or 32 for groups of fewer rows); D: K steps
+// held in registers ahead of the one being staged (1 at 128 rows, where the accumulators leave no room; 2 at 64
+// rows; 3 at 32 rows, so a step's loads have three steps of compute to arrive in).
+template <int MODE, int GMT = GM, int D = 1>
 __global__ void __launch_bounds__(kThreads, 2)
 k_grouped_q4_k(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
                const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
                int K, int n_rows, void *out, int ldo, int odt) {
+  constexpr int MB = GMT / 16, QMAX = GMT / 32, AQ = GMT * 8 / kThreads;  // A granules a thread a step
+  static_assert(AQ >= 1 && D >= 1 && D <= 3, "tile and prefetch shape");
   // A tile: rows of 64 halves = 8 swizzled 16-byte chunks; packed weights: kWp words a tile feature; 2 stages each
-  __shared__ __attribute__((aligned(16))) u32x4 As[2][GM * 8];
+  __shared__ __attribute__((aligned(16))) u32x4 As[2][GMT * 8];
   __shared__ __attribute__((aligned(16))) uint32_t Wp[2][GN * kWp];
   Tile t;
-  if (!tile_of(offsets, tiles, n_tiles, n_ntile, &t)) return;
+  if (!tile_of<GMT>(offsets, tiles, n_tiles, n_ntile, &t)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, g = lane >> 4;
   const size_t wrow_bytes = size_t(144) * (K / 256);
 
-  // A staging: thread -> tile row ar = tid >> 1, chunks 4 ac .. 4 ac + 3 (64 contiguous bytes of the step).
-  // Rows past the tile's end read the tile's first row instead (their results are never stored).
-  const int ar = tid >> 1, ac = tid & 1;
+  // A staging: thread -> tile row ar = tid / (256 / GMT), its AQ contiguous 16-byte chunks from c0 (128 rows: 2
+  // threads a row, 4 chunks each; 32 rows: 8 threads a row, 1 chunk each). Rows past the tile's end read the tile's
+  // first row instead (their results are never stored).
+  constexpr int TPR = kThreads / GMT;
+  const int ar = tid / TPR, c0 = (tid % TPR) * AQ;
   const u32x4 *a_ptr;
   {
     const int p = t.row0 + (ar < t.rows ? ar : 0);
     const size_t r = MODE == MODE_GATE_UP ? size_t(order[p] / uint32_t(topk)) : size_t(p);
-    a_ptr = reinterpret_cast<const u32x4 *>(a_src + r * K + 32 * ac);
+    a_ptr = reinterpret_cast<const u32x4 *>(a_src + r * K) + c0;
   }
   // weight staging: thread -> tile feature tid
   const uint8_t *w_row;
@@ -619,24 +630,26 @@ k_grouped_q4_k(const _Float16 *a_src, int topk, const uint32_t *order, const uin
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) wfeat[nb] = frag_feature<MODE>(wave, nb) + fr;
 
-  u32x4 areg[4];
-  uint32_t wraw[12];
-  f32x4 acc[4][8];
+  u32x4 areg[D][AQ];
+  uint32_t wraw[D][12];
+  f32x4 acc[4][MB];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto load = [&](int kk) {  // raw weights and A of step kk into registers
-    load_w_q4_k(w_row, kk, wraw);
+  auto load = [&](int kk, auto slot) {  // raw weights and A of step kk into register slot `slot`
+    constexpr int S = decltype(slot)::value;
+    load_w_q4_k(w_row, kk, wraw[S]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) areg[i] = a_ptr[size_t(kk) * (GK / 8) + i];
+    for (int i = 0; i < AQ; ++i) areg[S][i] = a_ptr[size_t(kk) * (GK / 8) + i];
   };
-  auto stage = [&](int l, int kk) {  // registers -> LDS stage l
+  auto stage = [&](int l, int kk, auto slot) {  // register slot -> LDS stage l
+    constexpr int S = decltype(slot)::value;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) As[l][achunk(ar, 4 * ac + j)] = areg[j];
+    for (int i = 0; i < AQ; ++i) As[l][achunk(ar, c0 + i)] = areg[S][i];
     uint32_t o[kWp];
-    pack_w_q4_k(wraw, kk, o);
+    pack_w_q4_k(wraw[S], kk, o);
 #pragma unroll
     for (int j = 0; j < kWp; ++j) Wp[l][tid * kWp + j] = o[j];
   };
@@ -659,29 +672,49 @@ k_grouped_q4_k(const _Float16 *a_src, int topk, const uint32_t *order, const uin
       }
     }
   };
-  // Step kk: issue the global loads of step kk + 1, multiply out of LDS stage kk % 2 (the loads are in flight
-  // meanwhile), then repack step kk + 1 into the other stage; one barrier a step.
+  // Step kk: issue the global loads of step kk + D into the register slot step kk left (staged one step ago),
+  // multiply out of LDS stage kk % 2 (the loads are in flight meanwhile), then stage step kk + 1 from its slot
+  // into the other LDS stage; one barrier a step. Register slots are compile-time indices, so the loop is written
+  // D steps at a time.
   const int nk = K / GK;
-  load(0);
-  stage(0, 0);
+  load(0, IC<0>{});
+  if (D > 1 && nk > 1) load(1, IC<(D > 1 ? 1 : 0)>{});
+  if (D > 2 && nk > 2) load(2, IC<(D > 2 ? 2 : 0)>{});
+  stage(0, 0, IC<0>{});
   __syncthreads();
   auto run = [&](auto qn) {
-    for (int kk = 0; kk + 1 < nk; ++kk) {
-      load(kk + 1);
+    auto step = [&](int kk, auto j) {  // j = kk % D
+      constexpr int J = decltype(j)::value, JN = (J + 1) % D;
+      if (kk + D < nk) load(kk + D, IC<J>{});
       __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs (the scheduler sinks them otherwise)
       compute(kk & 1, qn);
-      stage((kk + 1) & 1, kk + 1);
-      __syncthreads();
+      if (kk + 1 < nk) {
+        stage((kk + 1) & 1, kk + 1, IC<JN>{});
+        __syncthreads();
+      }
+    };
+    for (int base = 0; base < nk; base += D) {
+      step(base, IC<0>{});
+      if (D > 1 && base + 1 < nk) step(base + 1, IC<(D > 1 ? 1 : 0)>{});
+      if (D > 2 && base + 2 < nk) step(base + 2, IC<(D > 2 ? 2 : 0)>{});
     }
-    compute((nk - 1) & 1, qn);
   };
-  switch ((t.rows + 31) / 32) {  // uniform across the workgroup
-    case 1: run(IC<1>{}); break;
-    case 2: run(IC<2>{}); break;
-    case 3: run(IC<3>{}); break;
-    default: run(IC<4>{}); break;
+  if constexpr (QMAX == 1) {
+    run(IC<1>{});
+  } else if constexpr (QMAX == 2) {
+    if (t.rows <= 32)  // uniform across the workgroup
+      run(IC<1>{});
+    else
+      run(IC<2>{});
+  } else {
+    switch ((t.rows + 31) / 32) {  // uniform across the workgroup
+      case 1: run(IC<1>{}); break;
+      case 2: run(IC<2>{}); break;
+      case 3: run(IC<3>{}); break;
+      default: run(IC<4>{}); break;
+    }
   }
-  store_tile<MODE>(acc, t, wave, fr, g, out, ldo, odt);
+  store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
 }
 
 // x [n] in dt -> f16 (round to nearest even), 8 elements a thread (vector loads when the whole range allows).
@@ -760,8 +793,7 @@ extern "C" int lmoe_grouped_gate_up_bm(const void *x, int xdtype, int T, int top
                                        const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I,
                                        void *h, void *stream) {
   const char *fn = "lmoe_grouped_gate_up_bm";
-  LMOE_REQUIRE(bm == GM || (bm == 32 && type_g == LMOE_Q4_0), LMOE_ESHAPE,
-               "%s: tile rows %d (128, or 32 for Q4_0)", fn, bm);
+  LMOE_REQUIRE(bm == GM || bm == 64 || bm == 32, LMOE_ESHAPE, "%s: tile rows %d (128, 64 or 32)", fn, bm);
   if (int rc = check_split(fn, bm, type_g, ksplit, ws, H, T * topk)) return rc;
   LMOE_REQUIRE(qtype_ok(type_g) && qtype_ok(type_u), LMOE_ETYPE,
                "%s: ggml types %d/%d are not supported (Q4_0 = 2, Q4_K = 12)", fn, type_g, type_u);
@@ -787,7 +819,9 @@ extern "C" int lmoe_grouped_gate_up_bm(const void *x, int xdtype, int T, int top
     LMOE_REQUIRE((long long)T * H * 2 <= 0xFFFFFFFFll && (long long)I * (H / 64) * 36 <= 0xFFFFFFFFll, LMOE_ESHAPE,
                  "%s: x or one expert's weights exceed 4 GiB", fn);
     const int R = T * topk;
-    launch(bm == 32 ? k_grouped_q4_0<MODE_GATE_UP, 32, 5> : k_grouped_q4_0<MODE_GATE_UP>, dim3(unsigned(grid)),
+    launch(bm == 32 ? k_grouped_q4_0<MODE_GATE_UP, 32, 5>
+                    : bm == 64 ? k_grouped_q4_0<MODE_GATE_UP, 64, 4> : k_grouped_q4_0<MODE_GATE_UP>,
+           dim3(unsigned(grid)),
            dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg, wu, H, I, h, I,
            int(LMOE_F16), ksplit, ws, R, 2 * I);
     if (ksplit > 1) {
@@ -796,8 +830,11 @@ extern "C" int lmoe_grouped_gate_up_bm(const void *x, int xdtype, int T, int top
              static_cast<const float *>(ws), ksplit, R, 2 * I, offsets, n_experts, h, I, int(LMOE_F16));
     }
   } else {
-    launch(k_grouped_q4_k<MODE_GATE_UP>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles,
-           n_tiles, n_ntile, wg, wu, H, I, h, I, int(LMOE_F16));
+    launch(bm == 32 ? k_grouped_q4_k<MODE_GATE_UP, 32, 3>
+                    : bm == 64 ? k_grouped_q4_k<MODE_GATE_UP, 64, 2> : k_grouped_q4_k<MODE_GATE_UP>,
+           dim3(unsigned(grid)),
+           dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg, wu, H, I, h, I,
+           int(LMOE_F16));
   }
   LMOE_LAUNCHED(fn);
   return 0;
@@ -808,8 +845,7 @@ extern "C" int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offset
                                     const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
                                     void *stream) {
   const char *fn = "lmoe_grouped_down_bm";
-  LMOE_REQUIRE(bm == GM || (bm == 32 && type_d == LMOE_Q4_0), LMOE_ESHAPE,
-               "%s: tile rows %d (128, or 32 for Q4_0)", fn, bm);
+  LMOE_REQUIRE(bm == GM || bm == 64 || bm == 32, LMOE_ESHAPE, "%s: tile rows %d (128, 64 or 32)", fn, bm);
   LMOE_REQUIRE(R >= 0, LMOE_ESHAPE, "%s: bad row count", fn);
   if (int rc = check_split(fn, bm, type_d, ksplit, ws, I, R)) return rc;
   LMOE_REQUIRE(qtype_ok(type_d), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn, type_d);
@@ -831,7 +867,9 @@ extern "C" int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offset
     // R is not passed: offsets[E] <= max_tiles * bm rows of h can be read
     LMOE_REQUIRE((long long)max_tiles * bm * I * 2 <= 0xFFFFFFFFll && (long long)H * (I / 64) * 36 <= 0xFFFFFFFFll,
                  LMOE_ESHAPE, "%s: h or one expert's weights exceed 4 GiB", fn);
-    launch(bm == 32 ? k_grouped_q4_0<MODE_DOWN, 32, 5> : k_grouped_q4_0<MODE_DOWN>, dim3(unsigned(grid)),
+    launch(bm == 32 ? k_grouped_q4_0<MODE_DOWN, 32, 5>
+                    : bm == 64 ? k_grouped_q4_0<MODE_DOWN, 64, 4> : k_grouped_q4_0<MODE_DOWN>,
+           dim3(unsigned(grid)),
            dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile,
            wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype, ksplit, ws, R, H);
     if (ksplit > 1) {
@@ -840,9 +878,11 @@ extern "C" int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offset
              static_cast<const float *>(ws), ksplit, R, H, offsets, n_experts, y, H, ydtype);
     }
   } else {
-    launch(k_grouped_q4_k<MODE_DOWN>, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1,
-           static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile, wd,
-           static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
+    launch(bm == 32 ? k_grouped_q4_k<MODE_DOWN, 32, 3>
+                    : bm == 64 ? k_grouped_q4_k<MODE_DOWN, 64, 2> : k_grouped_q4_k<MODE_DOWN>,
+           dim3(unsigned(grid)),
+           dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile,
+           wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
   }
   LMOE_LAUNCHED(fn);
   return 0;

@@ -27,9 +27,11 @@ def tile_rows():
 
 def pick_tile_rows(R, E, types):
     """The GEMMs' tile rows for R rows over E experts: 32 when every projection is Q4_0 and the average expert has
-    fewer than 64 rows (the kernels then stream weights, and 32-row tiles keep more K steps of them in flight),
-    otherwise 128."""
-    return 32 if all(t == "Q4_0" for t in types) and R < 64 * E else tile_rows()
+    fewer than 16 rows (batched decode: few tiles have work, each streams its expert's weights, and 32-row tiles
+    keep five K steps in flight and allow split-K); otherwise 128. Measured on cfg4 (4 rows an expert): 116.6 ->
+    108.8 us a step; on cfg5's prefill (Q4_K, 40 rows an expert) 64-row and 32-row tiles were slower (1,367 and
+    1,546 us against 1,297), since smaller tiles read an expert's weights once a tile."""
+    return 32 if all(t == "Q4_0" for t in types) and R < 16 * E else tile_rows()
 
 
 def pick_ksplit(R, E, bm, K):

@@ -230,13 +230,15 @@ def test_prefill_stack_layer_major():
         assert moe.rel_l2(host(xo) - xr, want - xr) < BAR
 
 
-@pytest.mark.parametrize("bm,ks", [(32, 1), (128, 1), (32, 4), (32, 2)])
-def test_q4_0_tile_rows_both_kernels(bm, ks):
-    """The Q4_0 GEMMs at both tile heights (32 rows with five K steps in flight, 128 with three), and split-K over
-    32-row tiles (4 and 2 slices), on the same ragged rows, gate/up and down, against the oracle: groups of 0, 1,
-    31, 32, 33, 64 and 200 rows, a slot past the experts."""
+@pytest.mark.parametrize("t,bm,ks", [("Q4_0", 32, 1), ("Q4_0", 64, 1), ("Q4_0", 128, 1), ("Q4_0", 32, 4),
+                                     ("Q4_0", 32, 2), ("Q4_K", 32, 1), ("Q4_K", 64, 1), ("Q4_K", 128, 1)])
+def test_q4_0_tile_rows_both_kernels(t, bm, ks):
+    """The Q4_0 GEMMs at both tile heights (32 rows with five K steps in flight, 128 with three), split-K over
+    32-row tiles (4 and 2 slices), and the Q4_K GEMMs at both heights (32 rows with three steps prefetched in
+    registers), on the same ragged rows, gate/up and down, against the oracle: groups of 0, 1, 31, 32, 33, 64 and
+    200 rows, a slot past the experts."""
     from larder_amd import grouped
-    types, H, I, E = ("Q4_0",) * 3, 2048, 768, 9
+    types, H, I, E = (t,) * 3, 2048, 768, 9
     w = experts(types, H, I, E, 77)
     rng = np.random.default_rng(bm)
     sizes = [0, 1, 31, 32, 33, 64, 200, 5, 2]
