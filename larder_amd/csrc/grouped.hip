@@ -683,6 +683,17 @@ k_grouped_q4_k(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   stage(0, 0, IC<0>{});
   __syncthreads();
   auto run = [&](auto qn) {
+    if constexpr (D == 1) {  // one slot: the last step's multiply outside the loop, no branch inside it
+      for (int kk = 0; kk + 1 < nk; ++kk) {
+        load(kk + 1, IC<0>{});
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+        compute(kk & 1, qn);
+        stage((kk + 1) & 1, kk + 1, IC<0>{});
+        __syncthreads();
+      }
+      compute((nk - 1) & 1, qn);
+      return;
+    }
     auto step = [&](int kk, auto j) {  // j = kk % D
       constexpr int J = decltype(j)::value, JN = (J + 1) % D;
       if (kk + D < nk) load(kk + D, IC<J>{});
