@@ -107,6 +107,19 @@ int lmoe_moe_gate_up(const float *logits, int ld_stride, int T, int k, int norm,
                      int n_experts, int H, int I, uint32_t *ids, float *scores, uint32_t *hprep, int type_d,
                      void *stream);
 
+/* lmoe_moe_gate_up with the layer's shared expert folded in as one more slot a token (with_shared = 1; 0 is
+ * lmoe_moe_gate_up): wg / wu hold n_experts + 1 experts, the last the shared expert (same shape and type as the
+ * routed ones), logits rows hold the shared expert's gate logit at column n_experts (the router GEMV's row E), and
+ * each token gets k + 1 slots: ids / scores [T][k + 1] with slot k = (n_experts, sigmoid(gate logit)), hprep
+ * [T (k + 1)][I / 64 * 36]. lmoe_gemv_down_combine_prepped with k + 1 and wd of n_experts + 1 experts then weights
+ * the shared expert like a routed one: three launches a layer instead of five. Takes the register-resident form
+ * (H = 2048 or 4096, one type for gate and up). No counterpart in the reference (its shared expert is MLX ops,
+ * stream_fast.py:4403-4405). */
+int lmoe_moe_gate_up_ext(const float *logits, int ld_stride, int T, int k, int norm, const uint32_t *xg_prep,
+                         const uint32_t *xu_prep, const uint8_t *wg, const uint8_t *wu, int type_g, int type_u,
+                         int n_experts, int H, int I, uint32_t *ids, float *scores, uint32_t *hprep, int type_d,
+                         int with_shared, void *stream);
+
 /* Decode chain, down with the weighted combine fused:
  *   out[t][n] = sum_j scores[t][j] * (h[t * k + j] . wd[ids[t][j]][n])
  *               (+ sigmoid(gate[t * gate_stride]) * shared[t][n]) (+ residual[t][n])

@@ -301,11 +301,14 @@ __device__ __forceinline__ float group_sum(float v) {
 // (NPL a lane; softmax scores only in the one wavefront that writes ids / scores, wavefront 0 of the slot's first
 // workgroup); NPL = 0: expert ids from slots. Memory order: logits,
 // activation chunks, then (once the id is known) the weights, none predicated, so each group goes out back to back.
+// ks: slots a token, topk or, with a shared expert folded in (NPL > 0 only), topk + 1: then slot topk of a token
+// is the shared expert, stored as expert n_experts of wg / wu, and ids_out / scores_out rows hold ks entries, the
+// last (n_experts, sigmoid(logits[t][n_experts])) for the down kernel to weight it like a routed expert.
 template <int TQ, int P, int RB, int NPL>
 __global__ void __launch_bounds__(256)
     k_gate_up_xr(const uint32_t *xprep, const uint32_t *slots, int topk, const uint8_t *wg, const uint8_t *wu,
                  int n_experts, int I, float *h, uint32_t *hprep, int td, const float *logits, int ld_stride,
-                 int norm, uint32_t *ids_out, float *scores_out) {
+                 int norm, uint32_t *ids_out, float *scores_out, int ks) {
   constexpr int G = 64 / P, RG = RB / G;
   static_assert(P == 32 || P == 64, "32 or 64 units a row");
   static_assert(RB % G == 0, "rows split evenly over the lane groups");
@@ -323,7 +326,9 @@ __global__ void __launch_bounds__(256)
   u32x4 *xl = lds4;
   uint32_t *stage = reinterpret_cast<uint32_t *>(lds4 + XC) + wave * STAGE;
   uint32_t *scr = reinterpret_cast<uint32_t *>(lds4 + XC + STAGE) + wave * 64;
-  const size_t xrow = size_t(s / topk);
+  const size_t xrow = size_t(s / ks);
+  const int jslot = s % ks;
+  const bool shared_slot = NPL > 0 && jslot == topk;  // uniform across the workgroup
 
   float v[NPL > 0 ? NPL : 1];
   uint32_t e = 0;
@@ -338,9 +343,15 @@ __global__ void __launch_bounds__(256)
   u32x4 xc[XPT];
 #pragma unroll
   for (int i = 0; i < XPT; ++i) xc[i] = xg4[min(int(threadIdx.x) + 256 * i, XC - 1)];
-  if (NPL > 0) {  // each wavefront picks the slot's expert itself (no barrier before its weight loads)
+  if (NPL > 0 && shared_slot) {  // the folded shared expert: no pick; its id and sigmoid-gated weight
+    e = uint32_t(n_experts);
+    if (blockIdx.x == 0 && wave == 0 && lane == 0) {
+      ids_out[s] = e;
+      scores_out[s] = sigmoidf_(logits[xrow * ld_stride + n_experts]);
+    }
+  } else if (NPL > 0) {  // each wavefront picks the slot's expert itself (no barrier before its weight loads)
     constexpr int N = NPL > 0 ? NPL : 1;
-    const int j = s % topk;
+    const int j = jslot;
     uint32_t id;
     if (blockIdx.x == 0 && wave == 0) {  // the slot's scores: one wavefront computes and writes them
       float sc;
@@ -354,7 +365,8 @@ __global__ void __launch_bounds__(256)
     }
     e = uint32_t(__builtin_amdgcn_readlane(int(id), j));
   }
-  const bool valid = e < uint32_t(n_experts);  // no such expert: zero rows (cpu_kern.cpp:316-318)
+  // no such expert: zero rows (cpu_kern.cpp:316-318); the folded shared expert is expert n_experts
+  const bool valid = e < uint32_t(n_experts) || shared_slot;
   const size_t rsafe = size_t(valid ? e : 0u) * I + min(r0, I - RB);
   const u32x4 *gsrc = reinterpret_cast<const u32x4 *>(wg + rsafe * (36 * P));
   const u32x4 *usrc = reinterpret_cast<const u32x4 *>(wu + rsafe * (36 * P));
@@ -691,6 +703,7 @@ struct GateUpArgs {
   int ld_stride, norm;
   uint32_t *ids_out;
   float *scores_out;
+  int ks = 0;  // slots a token when a shared expert is folded in (topk + 1); 0: topk
 };
 
 template <int TG, int TU, int RB, int NC, int NW>
@@ -715,7 +728,8 @@ template <int TQ, int P, int RB, int NPL>
 static int launch_gate_up_xr(const GateUpArgs &a, hipStream_t st) {
   const dim3 grid((a.I + 4 * RB - 1) / (4 * RB), a.n_slots);
   launch(k_gate_up_xr<TQ, P, RB, NPL>, grid, dim3(256), 0, st, a.xg_prep, a.slots, a.topk, a.wg, a.wu,
-         a.n_experts, a.I, a.h, a.hprep, a.td, a.logits, a.ld_stride, a.norm, a.ids_out, a.scores_out);
+         a.n_experts, a.I, a.h, a.hprep, a.td, a.logits, a.ld_stride, a.norm, a.ids_out, a.scores_out,
+         a.ks ? a.ks : a.topk);
   LMOE_LAUNCHED("lmoe_gemv_gate_up");
   return 0;
 }
@@ -738,6 +752,7 @@ static int gate_up_p(const GateUpArgs &a, hipStream_t st) {
     if (P == 32) return gate_up_xr_npl<TG, 32, 2>(a, st);
     if (P == 64) return gate_up_xr_npl<TG, 64, 2>(a, st);
   }
+  if (a.ks) return fail(LMOE_ESHAPE, "lmoe_moe_gate_up_ext: a folded shared expert takes H = 2048 or 4096 and one type");
   if (P % 2 == 0) {
     const int nc = (2 * 9 * P / 4 + 63) / 64;
     if (nc <= 2) return launch_gate_up<TG, TU, 2, 2, 4>(a, st);
@@ -764,7 +779,7 @@ static int check_matrix(const char *fn, int type, int rows, int cols, const void
 }
 
 static int gate_up(const char *fn, const GateUpArgs &a, int type_g, int type_u, void *stream) {
-  LMOE_REQUIRE(a.n_slots >= 0 && a.topk > 0 && a.n_slots % a.topk == 0, LMOE_ESHAPE,
+  LMOE_REQUIRE(a.n_slots >= 0 && a.topk > 0 && a.n_slots % (a.ks ? a.ks : a.topk) == 0, LMOE_ESHAPE,
                "%s: %d slots is not a multiple of topk %d", fn, a.n_slots, a.topk);
   LMOE_REQUIRE(a.n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
   if (!qtype_ok(type_g) || !qtype_ok(type_u)) {  // a type beyond Q4_0 / Q4_K: the general chain
@@ -928,6 +943,27 @@ extern "C" int lmoe_moe_gate_up(const float *logits, int ld_stride, int T, int k
                n_experts);
   GateUpArgs a{xg_prep, type_g == type_u ? xg_prep : xu_prep, nullptr, 0, nullptr, T * k, k, wg, wu, n_experts,
                H, I, nullptr, hprep, type_d, logits, ld_stride, norm, ids, scores};
+  return gate_up(fn, a, type_g, type_u, stream);
+}
+
+extern "C" int lmoe_moe_gate_up_ext(const float *logits, int ld_stride, int T, int k, int norm,
+                                    const uint32_t *xg_prep, const uint32_t *xu_prep, const uint8_t *wg,
+                                    const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I,
+                                    uint32_t *ids, float *scores, uint32_t *hprep, int type_d, int with_shared,
+                                    void *stream) {
+  const char *fn = "lmoe_moe_gate_up_ext";
+  if (!with_shared)
+    return lmoe_moe_gate_up(logits, ld_stride, T, k, norm, xg_prep, xu_prep, wg, wu, type_g, type_u, n_experts, H,
+                            I, ids, scores, hprep, type_d, stream);
+  LMOE_REQUIRE(T == 0 || (logits && xg_prep && aligned16(xg_prep)), LMOE_EALIGN,
+               "%s: logits and 16-byte aligned prepared rows must be given", fn);
+  LMOE_REQUIRE(type_g == type_u, LMOE_ETYPE, "%s: a folded shared expert takes one type for gate and up", fn);
+  LMOE_REQUIRE(ld_stride >= n_experts + 1, LMOE_ESHAPE,
+               "%s: logits rows need the shared expert's gate logit at column %d (stride %d)", fn, n_experts,
+               ld_stride);
+  LMOE_REQUIRE(k >= 1 && k + 1 <= 64, LMOE_ESHAPE, "%s: k %d", fn, k);
+  GateUpArgs a{xg_prep, xg_prep, nullptr, 0, nullptr, T * (k + 1), k, wg, wu, n_experts, H, I, nullptr, hprep,
+               type_d, logits, ld_stride, norm, ids, scores, k + 1};
   return gate_up(fn, a, type_g, type_u, stream);
 }
 

@@ -28,11 +28,10 @@ class MoELayer:
     wsg      [H] shared-expert gate weight, wr's dtype, or None
     """
 
-    def __init__(self, wg, wu, wd, types, top_k, norm, wr=None, shared=None, wsg=None):
+    def __init__(self, wg, wu, wd, types, top_k, norm, wr=None, shared=None, wsg=None, fold_shared=True):
         self.types = tuple(types)
         for t in self.types:
             qcode(t)
-        self.wg, self.wu, self.wd = wg, wu, wd
         self.E, self.I = wg.shape[0], wg.shape[1]
         self.H = wd.shape[1]
         self.k, self.norm = int(top_k), bool(norm)
@@ -41,6 +40,16 @@ class MoELayer:
         self.Is = shared[0].shape[1] if shared is not None else 0
         if shared is not None and wsg is None:
             raise ValueError("a shared expert needs its gate weight wsg")
+        # A shared expert of the routed experts' shape, with a router weight, rides in the decode kernels as expert
+        # E of extended buffers [E + 1, ...] (lmoe_moe_gate_up_ext): three launches a layer instead of five. The
+        # routed buffers are then views of the extended ones (no second copy).
+        self.folded = None
+        if (fold_shared and shared is not None and wr is not None and self.Is == self.I
+                and self.types[0] == self.types[1] and self.H in (2048, 4096) and self.I % 2 == 0
+                and tuple(shared[2].shape[1:]) == tuple(wd.shape[1:])):
+            self.folded = tuple(torch.cat([w, sw], 0) for w, sw in zip((wg, wu, wd), shared))
+            wg, wu, wd = (f[:self.E] for f in self.folded)
+        self.wg, self.wu, self.wd = wg, wu, wd
 
     def nbytes_touched(self, n_unique):
         """Algorithmic HBM bytes of one decode pass touching n_unique routed experts (weights only)."""
@@ -63,13 +72,15 @@ class DecodeBuffers:
         f32 = dict(dtype=torch.float32, device=device)
         u32 = dict(dtype=torch.int32, device=device)
         self.logits = torch.empty((T, rows), **f32)
-        self.ids = torch.empty((T, L.k), **u32)
-        self.scores = torch.empty((T, L.k), **f32)
+        ks = L.k + (1 if L.folded is not None else 0)  # slots a token (the folded shared expert last)
+        self.ids_ext = torch.empty((T, ks), **u32)
+        self.scores_ext = torch.empty((T, ks), **f32)
+        self.ids, self.scores = self.ids_ext[:, :L.k], self.scores_ext[:, :L.k]
         # prepared rows (36 dwords a 64-value unit): x for the gate / up type, h for the down type
         self.xprep = torch.empty((T, L.H // 64 * 36), **u32)
         self.xprep_u = torch.empty((T, L.H // 64 * 36), **u32) if L.types[1] != L.types[0] else None
-        self.hprep = torch.empty((T * L.k, L.I // 64 * 36), **u32)
-        if L.shared is not None:
+        self.hprep = torch.empty((T * ks, L.I // 64 * 36), **u32)
+        if L.shared is not None and L.folded is None:
             self.zero_slots = torch.zeros(T, **u32)
             self.hprep_s = torch.empty((T, L.Is // 64 * 36), **u32)
             self.shared_y = torch.empty((T, L.H), **f32)
@@ -100,6 +111,14 @@ def decode(layer, x, bufs, out, residual=None, logits=None):
     if B.xprep_u is not None:
         call("lmoe_prep_x", ptr(x), xd, T, L.H, tu, ptr(B.xprep_u), st)
         xu = B.xprep_u
+    if L.folded is not None:  # the shared expert as slot k of every token: gate/up, then down + combine
+        fg, fu, fd = L.folded
+        call("lmoe_moe_gate_up_ext", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(xu), ptr(fg), ptr(fu),
+             tg, tu, L.E, L.H, L.I, ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.hprep), td, 1, st)
+        call("lmoe_gemv_down_combine_prepped", ptr(B.hprep), 0, ptr(B.ids_ext), ptr(B.scores_ext), T, L.k + 1,
+             ptr(fd), td, L.E + 1, L.I, L.H, None, None, 0, ptr(residual),
+             dcode(residual.dtype) if residual is not None else 0, ptr(out), dcode(out.dtype), st)
+        return out
     call("lmoe_moe_gate_up", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(xu), ptr(L.wg), ptr(L.wu), tg,
          tu, L.E, L.H, L.I, ptr(B.ids), ptr(B.scores), ptr(B.hprep), td, st)
     shared_y = gptr = None

@@ -100,3 +100,36 @@ def test_cfg5_prefill_T2048_sampled():
     assert moe.rel_l2(got, want) < BAR
     num = np.linalg.norm(got - want, axis=1)
     assert (num / np.linalg.norm(want, axis=1)).max() < 1e-2
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_cfg5_decode_folded_shared_matches_unfolded(T):
+    """The shared expert folded into the decode kernels as slot k (3 launches a layer) against the same layer with
+    it run apart (5 launches): ids equal, the slot's id E and score sigmoid(gate logit), outputs within the bar;
+    and the folded layer against the oracle (test_cfg5_decode_T1 above runs the folded form as well)."""
+    from larder_amd import layer as lay, workloads
+    cfg = workloads.CONFIGS[5]
+    L, g = _layer(8)
+    assert L.folded is not None
+    U = lay.MoELayer(L.wg, L.wu, L.wd, L.types, L.k, L.norm, wr=L.wr, shared=L.shared, wsg=L.wsg,
+                     fold_shared=False)
+    assert U.folded is None
+    x = torch.randn((T, cfg["H"]), generator=g, device="cuda").half()
+    res = torch.randn((T, cfg["H"]), generator=g, device="cuda").half()
+    outs = []
+    for layer in (L, U):
+        B = lay.DecodeBuffers(layer, T)
+        out = torch.empty((T, cfg["H"]), dtype=torch.float32, device="cuda")
+        lay.decode(layer, x, B, out, residual=res)
+        torch.cuda.synchronize()
+        outs.append((host(out), host(B.ids).copy(), B))
+    (of, idf, Bf), (ou, idu, _) = outs
+    assert (idf == idu).all()
+    lg = host(Bf.logits)
+    assert (host(Bf.ids_ext)[:, -1] == cfg["E"]).all()
+    assert np.allclose(host(Bf.scores_ext)[:, -1], 1 / (1 + np.exp(-lg[:, cfg["E"]])), rtol=1e-5)
+    r = host(res.float())
+    assert moe.rel_l2(of - r, ou - r) < BAR
+    xs = host(x.float())
+    ids, want = _oracle_subset(L, xs, lg[:, :cfg["E"]], cfg)
+    assert moe.rel_l2(of - r, want) < BAR
