@@ -111,11 +111,11 @@ def gpu_leg(args):
 
 
 def grouped_leg():
-    """The other configurations (BASELINE.json configs[2..4]), reported beside the decode line:
+    """The other configurations (BASELINE.json configs[0] and [2..4]), reported beside the decode line:
     cfg3 = one 8192-token bf16 prefill chunk through one cfg-2 layer with skewed router logits (MFMA roofline over
     the routed experts' 2 R 3 H I flops); cfg4 = 512 steps of 64 tokens with a fresh Zipf-prior draw each step
-    (HBM roofline over the unique experts touched); cfg5 = the 512-expert Q4_K layer at T = 1 (decode chain) and
-    T = 2048 (grouped path)."""
+    (HBM roofline over the unique experts touched); cfg1 = batch-1 decode through 8 layers with a 5,632-wide shared
+    expert; cfg5 = the 512-expert Q4_K layer at T = 1 (decode chain) and T = 2048 (grouped path)."""
     import ctypes
 
     import torch
@@ -210,9 +210,33 @@ def grouped_leg():
                            "unique_experts_per_step": round(uniq, 1),
                            "hbm_frac": round(byts / (us4 * 1e-6) / HBM_PEAK, 4)}
     del B4, xs, lgs
+    # cfg1: E 60, top-4 without renorm, I 1408, a 5,632-wide shared expert (not foldable) with a sigmoid gate, Q4_0;
+    # batch-1 decode through 8 such layers (2.5 GB: no layer stays in the 256 MB MALL), one HIP graph a step.
+    from larder_amd import layer as lay
+    cfg1 = workloads.CONFIGS[1]
+    L1s = [workloads.make_layer(cfg1, g) for _ in range(8)]
+    st1 = lay.DecodeStack(L1s, 1)
+    st1.capture()
+    n1 = 128
+    x1 = torch.randn((n1 + 16, 1, cfg1["H"]), generator=g, device="cuda").half()
+    for i in range(16):
+        st1.x_in.copy_(x1[i])
+        st1.graph.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(16, 16 + n1):
+        st1.x_in.copy_(x1[i])
+        st1.graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us1 = e0.elapsed_time(e1) / n1 * 1e3 / len(L1s)
+    b1 = workloads.decode_bytes(cfg1, cfg1["k"]) + 2 * cfg1["H"] * 2
+    out["cfg1_decode_T1"] = {"us_per_layer": round(us1, 2), "bytes_per_layer": b1,
+                             "hbm_frac": round(b1 / (us1 * 1e-6) / HBM_PEAK, 4),
+                             "note": "8-layer stack, shared expert run apart (5 launches a layer)"}
+    del st1, L1s, x1
     # cfg5: H 4096, 512 experts top-10, I 512, shared expert, Q4_K. T = 1 through the decode chain (one layer as a
     # HIP graph, a fresh x each step so the touched experts change), T = 2048 through the grouped path.
-    from larder_amd import layer as lay
     cfg5 = workloads.CONFIGS[5]
     L5 = workloads.make_layer(cfg5, g)
     st5 = lay.DecodeStack([L5], 1)
