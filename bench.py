@@ -332,10 +332,30 @@ def types_leg():
         torch.cuda.synchronize()
         us_dense = e0.elapsed_time(e1) / 5 * 1e3
         flops = 2 * T * k * 3 * H * I
+        # the layer path with the f16 K-order weights held resident (MoELayer.keep_prefill_f16): no dequant a call
+        from larder_amd import grouped, layer as lay
+        L = lay.MoELayer(*w, types, k, True)
+        L.keep_prefill_f16()
+        lg = torch.randn((T, E), generator=g, device="cuda")
+        xl = xt[:T]
+        B = grouped.PrefillBuffers(L, T)
+        yl = torch.empty((T, H), dtype=torch.float16, device="cuda")
+        for _ in range(2):
+            grouped.prefill(L, xl, B, yl, logits=lg)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(5):
+            grouped.prefill(L, xl, B, yl, logits=lg)
+        e1.record()
+        torch.cuda.synchronize()
+        us_layer = e0.elapsed_time(e1) / 5 * 1e3
+        del L, B
         out["/".join(types)] = {
             "decode_gate_up_us": round(gu, 2), "decode_down_us": round(dn, 2), "decode_bytes": byts,
             "decode_hbm_frac": round(byts / ((gu + dn) * 1e-6) / HBM_PEAK, 4),
-            "dense_2048x8_us": round(us_dense, 1), "dense_mfma_frac": round(flops / (us_dense * 1e-6) / MFMA_PEAK, 4)}
+            "dense_2048x8_us": round(us_dense, 1), "dense_mfma_frac": round(flops / (us_dense * 1e-6) / MFMA_PEAK, 4),
+            "prefill_2048_resident_f16_us": round(us_layer, 1),
+            "prefill_mfma_frac": round(flops / (us_layer * 1e-6) / MFMA_PEAK, 4)}
         del w, xt, rows
     return out
 

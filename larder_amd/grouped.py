@@ -138,7 +138,7 @@ def _ws(n, ws, device):
     return torch.empty(n, dtype=torch.float32, device=device)
 
 
-def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False, ws=None, ksplit=None):
+def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False, ws=None, ksplit=None, w16=None):
     """h [R, I] f16 (grouped order, columns in the GEMMs' K order: from_kperm undoes it) = silu(x . wg) * (x . wu)
     over the grouping G of x's rows (row p reads x[order[p] // topk]); x [T, H] in natural order, any float dtype,
     meets the weights as f16 in the K order (converted into ``xh``; prepped: x already is that form). Q4_0 / Q4_K
@@ -157,13 +157,13 @@ def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False, ws=None, kspli
     else:
         if G.bm != tile_rows():
             raise ValueError(f"the f16-weight GEMMs take {tile_rows()}-row tiles, not {G.bm}")
-        wg16, wu16 = gemm_weights(wg, types[0]), gemm_weights(wu, types[1])
+        wg16, wu16 = w16 if w16 is not None else (gemm_weights(wg, types[0]), gemm_weights(wu, types[1]))
         call("lmoe_grouped_gate_up_f16w", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
              ptr(G.n_tiles), G.max_tiles, ptr(wg16), ptr(wu16), E, H, I, ptr(h), stream())
     return h
 
 
-def down(h, G, wd, t, y, ws=None, ksplit=None):
+def down(h, G, wd, t, y, ws=None, ksplit=None, w16=None):
     """y [R, H] (f16 / f32, grouped order, natural columns) = h . wd over the grouping G; h as gate_up leaves it."""
     E, H = wd.shape[0], wd.shape[1]
     I = h.shape[1]
@@ -175,7 +175,7 @@ def down(h, G, wd, t, y, ws=None, ksplit=None):
     else:
         if G.bm != tile_rows():
             raise ValueError(f"the f16-weight GEMMs take {tile_rows()}-row tiles, not {G.bm}")
-        wd16 = gemm_weights(wd, t)
+        wd16 = w16 if w16 is not None else gemm_weights(wd, t)
         call("lmoe_grouped_down_f16w", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles,
              ptr(wd16), E, I, H, ptr(y), dcode(y.dtype), stream())
     return y
@@ -249,8 +249,9 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
         sel = lg[:, :L.E].contiguous()
         call("lmoe_router_topk", ptr(sel), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
     B.G.run(B.ids.reshape(-1))
-    gate_up(x, B.G, L.k, L.wg, L.wu, L.types, B.h, B.xh, ws=B.ws)
-    down(B.h, B.G, L.wd, L.types[2], B.y, ws=B.ws)
+    f16 = L.prefill_f16
+    gate_up(x, B.G, L.k, L.wg, L.wu, L.types, B.h, B.xh, ws=B.ws, w16=f16[:2] if f16 and f16[0] is not None else None)
+    down(B.h, B.G, L.wd, L.types[2], B.y, ws=B.ws, w16=f16[2] if f16 else None)
     shared = gate = None
     if L.shared is not None:
         sg, su, sd = L.shared

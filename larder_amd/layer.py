@@ -50,6 +50,19 @@ class MoELayer:
             self.folded = tuple(torch.cat([w, sw], 0) for w, sw in zip((wg, wu, wd), shared))
             wg, wu, wd = (f[:self.E] for f in self.folded)
         self.wg, self.wu, self.wd = wg, wu, wd
+        self.prefill_f16 = None
+
+    def keep_prefill_f16(self):
+        """Hold the f16 K-order weights the grouped path needs for projections beyond Q4_0 / Q4_K (gate/up together,
+        down alone) resident, so prefill does not dequantize them each call: 2 bytes a weight beside the packed
+        ones, a trade the 288 GB of HBM affords. Returns the bytes held."""
+        from . import grouped
+        gu = None
+        if not (self.types[0] in _lib.Q4_TYPES and self.types[1] == self.types[0]):
+            gu = (grouped.gemm_weights(self.wg, self.types[0]), grouped.gemm_weights(self.wu, self.types[1]))
+        dn = grouped.gemm_weights(self.wd, self.types[2]) if self.types[2] not in _lib.Q4_TYPES else None
+        self.prefill_f16 = (gu[0] if gu else None, gu[1] if gu else None, dn)
+        return sum(t.numel() * 2 for t in self.prefill_f16 if t is not None)
 
     def nbytes_touched(self, n_unique):
         """Algorithmic HBM bytes of one decode pass touching n_unique routed experts (weights only)."""

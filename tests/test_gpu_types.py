@@ -128,3 +128,29 @@ def test_grouped_dense(types, H, I):
     for e in (3, 5, 7):
         sel = rows == e
         assert moe.rel_l2(host(y)[sel], yw[sel]) < BAR
+
+
+def test_prefill_with_resident_f16_weights():
+    """A Q4_K / Q4_K / Q6_K layer (and an all-Q8_0 one) through grouped.prefill, dequantizing each call and with
+    keep_prefill_f16's resident weights: the same kernels on the same f16 weights, so the same bits; and against
+    the oracle."""
+    from larder_amd import grouped, layer as lay
+    rng = np.random.default_rng(41)
+    for types, H, I in ((("Q4_K", "Q4_K", "Q6_K"), 1024, 256), (("Q8_0",) * 3, 1024, 256)):
+        E, k, T = 8, 2, 96
+        w = tuple(gguf.random_experts(rng, E, r, c, t) for (r, c), t in zip(((I, H), (I, H), (H, I)), types))
+        L = lay.MoELayer(*(dev(b) for b in w), types, k, True)
+        lg = dev(rng.standard_normal((T, E)).astype(np.float32))
+        x = dev(rng.standard_normal((T, H)).astype(np.float32)).half()
+        outs = []
+        for keep in (False, True):
+            if keep:
+                assert L.keep_prefill_f16() > 0
+            B = grouped.PrefillBuffers(L, T)
+            out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+            grouped.prefill(L, x, B, out, logits=lg)
+            torch.cuda.synchronize()
+            outs.append(host(out))
+        assert (outs[0] == outs[1]).all()
+        _, _, want = moe.layer(host(x.float()), host(lg), w, types, k, True)
+        assert moe.rel_l2(outs[1], want) < BAR
