@@ -194,12 +194,14 @@ int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offsets, const ui
 /* lmoe_grouped_gate_up / lmoe_grouped_down with f16 weights in the K order (lmoe_dequant_gemm_f16's output:
  * wg16 / wu16 [n_experts][I][H], wd16 [n_experts][H][I]) instead of Q4 blocks: the grouped path of Q4_1, Q8_0,
  * Q5_K and Q6_K experts (the reference's gather_mm on dequantized f16 experts, gguf_experts.py:698-722). Same
- * grouping arguments, shapes (I % 128, H % 256 for down, K % 64) and outputs. */
+ * grouping arguments, shapes (I % 128, H % 256 for down, K % 64) and outputs; bm: the grouping's tile rows, 128
+ * or 64 (two workgroups a CU). */
 int lmoe_grouped_gate_up_f16w(const void *x, int xdtype, int T, int topk, const uint32_t *order,
                               const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles, int max_tiles,
-                              const void *wg16, const void *wu16, int n_experts, int H, int I, void *h, void *stream);
+                              int bm, const void *wg16, const void *wu16, int n_experts, int H, int I, void *h,
+                              void *stream);
 int lmoe_grouped_down_f16w(const void *h, const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
-                           int max_tiles, const void *wd16, int n_experts, int I, int H, void *y, int ydtype,
+                           int max_tiles, int bm, const void *wd16, int n_experts, int I, int H, void *y, int ydtype,
                            void *stream);
 
 /* The trunk's 4-bit affine matmul of T bf16 rows: out [T][N] bf16 = x [T][K] bf16 . W^T with W in MLX's

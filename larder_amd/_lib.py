@@ -61,8 +61,8 @@ SIGNATURES = {
     "lmoe_dequant_gemm_f16": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "lmoe_qmv_rows": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P]),
     "lmoe_swiglu_bf16": (_I, [_P, _P, _LL, _P, _P]),
-    "lmoe_grouped_gate_up_f16w": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P, _P]),
-    "lmoe_grouped_down_f16w": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _P, _I, _P]),
+    "lmoe_grouped_gate_up_f16w": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _I, _I, _I, _P, _P]),
+    "lmoe_grouped_down_f16w": (_I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P, _I, _P]),
     "lmoe_quantize_q4_0": (_I, [_P, _I, _LL, _I, _P, _P]),
     "lmoe_quantize_q4_k": (_I, [_P, _I, _LL, _I, _P, _P]),
 }

@@ -447,24 +447,24 @@ __global__ void __launch_bounds__(256) k_splitk_finish(const float *ws, int kspl
 
 // ---- f16 weights (the other block types, dequantized in the K order): both operands global -> LDS ---------------
 
-constexpr int kFwAStage = GM * 128;                  // A tile bytes a stage (16 KB)
-constexpr int kFwStage = kFwAStage + GN * 128;       // + 256 weight rows of 64 halves (32 KB)
-constexpr int kFwDmaA = GM * 128 / 1024 / 4;         // 16-byte A copies a lane a step (4)
 constexpr int kFwDmaW = GN * 128 / 1024 / 4;         // 16-byte weight copies a lane a step (8)
 
 // The grouped GEMMs over f16 weights [E][n_rows][K] already in the K order (lmoe_dequant_gemm_f16): the tiles,
 // wavefront split, MFMA fragments and epilogue of k_grouped_q4_0, with the weight tile copied like the A tile
-// (rows of 128 bytes, 16-byte chunks XOR-swizzled by the row's low 3 bits) and no decode. Two 48 KB stages, one
-// workgroup a CU: step kk + 1's copies go out while step kk multiplies. Host guarantees: K % 64 == 0, rows x K x 2
-// of A and of one expert's weights under 4 GiB.
-template <int MODE>
-__global__ void __launch_bounds__(kThreads, 1)
+// (rows of 128 bytes, 16-byte chunks XOR-swizzled by the row's low 3 bits) and no decode. Two stages of a 32 KB
+// weight tile plus the A tile: 128 rows (2 x 48 KB, one workgroup a CU) or 64 rows (2 x 40 KB, two a CU, each
+// SIMD with two wavefronts to switch between). Step kk + 1's copies go out while step kk multiplies. Host
+// guarantees: K % 64 == 0, rows x K x 2 of A and of one expert's weights under 4 GiB.
+template <int MODE, int GMT = GM>
+__global__ void __launch_bounds__(kThreads, GMT == 64 ? 2 : 1)
 k_grouped_f16w(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
                const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const _Float16 *w0, const _Float16 *w1,
                int K, int n_rows, void *out, int ldo, int odt) {
+  constexpr int kFwAStage = GMT * 128, kFwStage = kFwAStage + GN * 128, kFwDmaA = GMT * 128 / 1024 / 4;
+  constexpr int MB = GMT / 16, QMAX = GMT / 32;
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kFwStage];
   Tile t;
-  if (!tile_of(offsets, tiles, n_tiles, n_ntile, &t)) return;
+  if (!tile_of<GMT>(offsets, tiles, n_tiles, n_ntile, &t)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 15, g = lane >> 4;
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(lds));
@@ -508,11 +508,11 @@ k_grouped_f16w(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   int wfeat[4];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) wfeat[nb] = frag_feature<MODE>(wave, nb) + fr;
-  f32x4 acc[4][8];
+  f32x4 acc[4][MB];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto compute = [&](int s, auto qn) {
     constexpr int QN = decltype(qn)::value;
@@ -548,13 +548,20 @@ k_grouped_f16w(const _Float16 *a_src, int topk, const uint32_t *order, const uin
       }
     }
   };
-  switch ((t.rows + 31) / 32) {  // uniform across the workgroup
-    case 1: run(IC<1>{}); break;
-    case 2: run(IC<2>{}); break;
-    case 3: run(IC<3>{}); break;
-    default: run(IC<4>{}); break;
+  if constexpr (QMAX == 2) {
+    if (t.rows <= 32)  // uniform across the workgroup
+      run(IC<1>{});
+    else
+      run(IC<2>{});
+  } else {
+    switch ((t.rows + 31) / 32) {  // uniform across the workgroup
+      case 1: run(IC<1>{}); break;
+      case 2: run(IC<2>{}); break;
+      case 3: run(IC<3>{}); break;
+      default: run(IC<4>{}); break;
+    }
   }
-  store_tile<MODE>(acc, t, wave, fr, g, out, ldo, odt);
+  store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
 }
 
 // ---- Q4_K: register staging with repack --------------------------------------------------------------------------
@@ -916,9 +923,10 @@ extern "C" int lmoe_grouped_down(const void *h, const uint32_t *offsets, const u
 
 extern "C" int lmoe_grouped_gate_up_f16w(const void *x, int xdtype, int T, int topk, const uint32_t *order,
                                          const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
-                                         int max_tiles, const void *wg16, const void *wu16, int n_experts, int H, int I,
-                                         void *h, void *stream) {
+                                         int max_tiles, int bm, const void *wg16, const void *wu16, int n_experts,
+                                         int H, int I, void *h, void *stream) {
   const char *fn = "lmoe_grouped_gate_up_f16w";
+  LMOE_REQUIRE(bm == GM || bm == 64, LMOE_ESHAPE, "%s: tile rows %d (128 or 64)", fn, bm);
   LMOE_REQUIRE(xdtype == LMOE_F16, LMOE_EINVAL,
                "%s: x must be float16 in the GEMM K order here (convert once with lmoe_to_gemm_f16)", fn);
   LMOE_REQUIRE(T >= 0 && topk > 0 && n_experts > 0 && max_tiles >= 0, LMOE_ESHAPE, "%s: bad shape", fn);
@@ -934,7 +942,8 @@ extern "C" int lmoe_grouped_gate_up_f16w(const void *x, int xdtype, int T, int t
   const int n_ntile = I / (GN / 2);
   const long long grid = (long long)n_ntile * max_tiles;
   LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
-  launch(k_grouped_f16w<MODE_GATE_UP>, dim3(unsigned(grid)), dim3(kThreads), 0, (hipStream_t)stream,
+  launch(bm == 64 ? k_grouped_f16w<MODE_GATE_UP, 64> : k_grouped_f16w<MODE_GATE_UP>, dim3(unsigned(grid)),
+         dim3(kThreads), 0, (hipStream_t)stream,
          static_cast<const _Float16 *>(x), topk, order, offsets, tiles, n_tiles, n_ntile,
          static_cast<const _Float16 *>(wg16), static_cast<const _Float16 *>(wu16), H, I, h, I, int(LMOE_F16));
   LMOE_LAUNCHED(fn);
@@ -942,9 +951,10 @@ extern "C" int lmoe_grouped_gate_up_f16w(const void *x, int xdtype, int T, int t
 }
 
 extern "C" int lmoe_grouped_down_f16w(const void *h, const uint32_t *offsets, const uint32_t *tiles,
-                                      const uint32_t *n_tiles, int max_tiles, const void *wd16, int n_experts, int I,
-                                      int H, void *y, int ydtype, void *stream) {
+                                      const uint32_t *n_tiles, int max_tiles, int bm, const void *wd16, int n_experts,
+                                      int I, int H, void *y, int ydtype, void *stream) {
   const char *fn = "lmoe_grouped_down_f16w";
+  LMOE_REQUIRE(bm == GM || bm == 64, LMOE_ESHAPE, "%s: tile rows %d (128 or 64)", fn, bm);
   LMOE_REQUIRE(n_experts > 0 && max_tiles >= 0, LMOE_ESHAPE, "%s: bad shape", fn);
   LMOE_REQUIRE(I > 0 && I % GK == 0, LMOE_ESHAPE, "%s: intermediate size %d is not a multiple of %d", fn, I, GK);
   LMOE_REQUIRE(H > 0 && H % GN == 0, LMOE_ESHAPE, "%s: hidden size %d is not a multiple of %d", fn, H, GN);
@@ -954,12 +964,13 @@ extern "C" int lmoe_grouped_down_f16w(const void *h, const uint32_t *offsets, co
   LMOE_REQUIRE(aligned16(h) && aligned16(y) && aligned16(wd16), LMOE_EALIGN,
                "%s: h, y and the weights must be 16-byte aligned", fn);
   // R is not passed: offsets[E] <= max_tiles * bm rows of h can be read
-  LMOE_REQUIRE((long long)max_tiles * GM * I * 2 <= 0xFFFFFFFFll && (long long)H * I * 2 <= 0xFFFFFFFFll,
+  LMOE_REQUIRE((long long)max_tiles * bm * I * 2 <= 0xFFFFFFFFll && (long long)H * I * 2 <= 0xFFFFFFFFll,
                LMOE_ESHAPE, "%s: h or one expert's weights exceed 4 GiB", fn);
   const int n_ntile = H / GN;
   const long long grid = (long long)n_ntile * max_tiles;
   LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
-  launch(k_grouped_f16w<MODE_DOWN>, dim3(unsigned(grid)), dim3(kThreads), 0, (hipStream_t)stream,
+  launch(bm == 64 ? k_grouped_f16w<MODE_DOWN, 64> : k_grouped_f16w<MODE_DOWN>, dim3(unsigned(grid)), dim3(kThreads),
+         0, (hipStream_t)stream,
          static_cast<const _Float16 *>(h), 1, static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile,
          static_cast<const _Float16 *>(wd16), static_cast<const _Float16 *>(nullptr), I, H, y, H, ydtype);
   LMOE_LAUNCHED(fn);

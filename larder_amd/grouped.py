@@ -30,7 +30,13 @@ def pick_tile_rows(R, E, types):
     fewer than 16 rows (batched decode: few tiles have work, each streams its expert's weights, and 32-row tiles
     keep five K steps in flight and allow split-K); otherwise 128. Measured on cfg4 (4 rows an expert): 116.6 ->
     108.8 us a step; on cfg5's prefill (Q4_K, 40 rows an expert) 64-row and 32-row tiles were slower (1,367 and
-    1,546 us against 1,297), since smaller tiles read an expert's weights once a tile."""
+    1,546 us against 1,297), since smaller tiles read an expert's weights once a tile. When gate/up runs on
+    dequantized f16 weights (a type beyond Q4_0 / Q4_K, or gate and up of two types): 64, so the f16-weight GEMM
+    fits two workgroups a CU (2,048 x 8 rows: 405 -> 377 us); a Q4 gate/up with an f16 down keeps 128."""
+    if not (types[0] in _lib.Q4_TYPES and types[1] == types[0]):
+        return 64  # gate/up on f16 weights: 64-row tiles let that GEMM run two workgroups a CU
+    if types[2] not in _lib.Q4_TYPES:
+        return tile_rows()  # Q4 gate/up (its 128-row form is the fast one), down on f16 weights
     return 32 if all(t == "Q4_0" for t in types) and R < 16 * E else tile_rows()
 
 
@@ -155,11 +161,11 @@ def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False, ws=None, kspli
         call("lmoe_grouped_gate_up_bm", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
              ptr(G.n_tiles), G.max_tiles, G.bm, ks, ptr(w), ptr(wg), ptr(wu), tg, tu, E, H, I, ptr(h), stream())
     else:
-        if G.bm != tile_rows():
-            raise ValueError(f"the f16-weight GEMMs take {tile_rows()}-row tiles, not {G.bm}")
+        if G.bm not in (64, tile_rows()):
+            raise ValueError(f"the f16-weight GEMMs take 64- or {tile_rows()}-row tiles, not {G.bm}")
         wg16, wu16 = w16 if w16 is not None else (gemm_weights(wg, types[0]), gemm_weights(wu, types[1]))
         call("lmoe_grouped_gate_up_f16w", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
-             ptr(G.n_tiles), G.max_tiles, ptr(wg16), ptr(wu16), E, H, I, ptr(h), stream())
+             ptr(G.n_tiles), G.max_tiles, G.bm, ptr(wg16), ptr(wu16), E, H, I, ptr(h), stream())
     return h
 
 
@@ -173,10 +179,10 @@ def down(h, G, wd, t, y, ws=None, ksplit=None, w16=None):
         call("lmoe_grouped_down_bm", ptr(h), G.R, ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, G.bm,
              ks, ptr(w), ptr(wd), qcode(t), E, I, H, ptr(y), dcode(y.dtype), stream())
     else:
-        if G.bm != tile_rows():
-            raise ValueError(f"the f16-weight GEMMs take {tile_rows()}-row tiles, not {G.bm}")
+        if G.bm not in (64, tile_rows()):
+            raise ValueError(f"the f16-weight GEMMs take 64- or {tile_rows()}-row tiles, not {G.bm}")
         wd16 = w16 if w16 is not None else gemm_weights(wd, t)
-        call("lmoe_grouped_down_f16w", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles,
+        call("lmoe_grouped_down_f16w", ptr(h), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, G.bm,
              ptr(wd16), E, I, H, ptr(y), dcode(y.dtype), stream())
     return y
 

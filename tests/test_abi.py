@@ -57,11 +57,13 @@ def test_refusals_without_a_gpu(built_lib):
     assert rc == _lib.ETYPE
     rc = L.lmoe_dequant_gemm_f16(p, 8, 4, 16, 48, p, None)
     assert rc == _lib.ESHAPE
-    rc = L.lmoe_grouped_gate_up_f16w(p, _lib.F32, 64, 1, p, p, p, p, 4, p, p, 8, 2048, 768, p, None)
+    rc = L.lmoe_grouped_gate_up_f16w(p, _lib.F32, 64, 1, p, p, p, p, 4, 128, p, p, 8, 2048, 768, p, None)
     assert rc == _lib.EINVAL and b"float16" in L.lmoe_error()
-    rc = L.lmoe_grouped_gate_up_f16w(p, _lib.F16, 64, 1, p, p, p, p, 4, p, p, 8, 2048, 100, p, None)
+    rc = L.lmoe_grouped_gate_up_f16w(p, _lib.F16, 64, 1, p, p, p, p, 4, 128, p, p, 8, 2048, 100, p, None)
     assert rc == _lib.ESHAPE
-    rc = L.lmoe_grouped_down_f16w(p, p, p, p, 4, p, 8, 768, 2000, p, _lib.F16, None)
+    rc = L.lmoe_grouped_gate_up_f16w(p, _lib.F16, 64, 1, p, p, p, p, 4, 32, p, p, 8, 2048, 768, p, None)
+    assert rc == _lib.ESHAPE and b"tile rows" in L.lmoe_error()
+    rc = L.lmoe_grouped_down_f16w(p, p, p, p, 4, 128, p, 8, 768, 2000, p, _lib.F16, None)
     assert rc == _lib.ESHAPE
     rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, p, p, _lib.Q4_0, _lib.Q4_0, 128, 2000, 768, p, None)
     assert rc == _lib.ESHAPE
