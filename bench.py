@@ -37,8 +37,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-grouped", action="store_true", help="skip the cfg3 prefill / cfg4 batched lines")
     ap.add_argument("--extra-only", action="store_true",
-                    help="only the Q4_1 / Q8_0 / Q5_K / Q6_K lines (decode chain and grouped path) and the trunk's "
-                         "qmv_rows lines, one JSON line")
+                    help="only the Q4_1 / Q8_0 / Q5_K / Q6_K lines (decode chain and grouped path), the trunk's "
+                         "qmv_rows lines and the cache-biased route / GGUF loader lines, one JSON line")
     ap.add_argument("--grouped-only", action="store_true",
                     help="run only the grouped-path lines (cfg3 prefill, cfg4, cfg5) and print them: a short run to "
                          "profile the grouped GEMMs with rocprofv3 counters, not a benchmark line")
@@ -397,6 +397,85 @@ def trunk_leg():
     return out
 
 
+def route_loader_leg():
+    """The cache-biased route (lmoe_route_bias: route_cuda.route / bias_probs) at the reference's shapes, kernel-exact;
+    and the GGUF pack / loader on a synthetic ~1 GB two-layer Q4_0 GGUF file in a temporary directory: pack
+    (GGUF -> experts.bin, each chunk written, synced and read back) and load_layer (experts.bin -> HBM through pinned
+    staging) throughput."""
+    import ctypes
+    import struct
+    import tempfile
+    import time
+    from pathlib import Path
+
+    import numpy as np
+    import torch
+
+    from larder_amd import _lib, gguf_pack, route, workloads
+
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(9)
+    for E, k, T, dt in ((512, 10, 1, torch.bfloat16), (512, 10, 5, torch.bfloat16), (256, 8, 5, torch.float32)):
+        gates = torch.softmax(torch.randn((T, E), generator=g, device="cuda"), -1).to(dt)
+        slot = torch.full((E,), -1, dtype=torch.int32, device="cuda")
+        slot[:E // 3] = torch.arange(E // 3, dtype=torch.int32, device="cuda")
+        f = lambda: route.route(gates, None, slot, 0.5, 0.2, k, lim=E // 4)  # noqa: E731
+        for _ in range(5):
+            f()
+        torch.cuda.synchronize()
+        reps = 50
+        _lib.call("lmoe_profile_arm", reps)
+        for _ in range(reps):
+            f()
+        ms = (ctypes.c_float * reps)()
+        cnt = ctypes.c_int()
+        _lib.call("lmoe_profile_read", ms, reps, ctypes.byref(cnt))
+        out[f"route_bias E{E} k{k} T{T} {str(dt).split('.')[-1]}"] = {"us": round(sum(ms[:cnt.value]) / cnt.value * 1e3, 2)}
+    H, I, E = 2048, 768, 128
+    rb_gu, rb_d = workloads.row_bytes("Q4_0", H), workloads.row_bytes("Q4_0", I)
+    with tempfile.TemporaryDirectory() as d:
+        d = Path(d)
+        tensors = []
+        for L in range(2):
+            for p, (rows, rb, ne0) in (("gate", (I, rb_gu, H)), ("up", (I, rb_gu, H)), ("down", (H, rb_d, I))):
+                blocks = np.random.default_rng(L).integers(0, 256, (E, rows, rb // 18, 18), dtype=np.uint8)
+                blocks[..., 0:2] = np.frombuffer(np.float16(0.001).tobytes(), np.uint8)
+                tensors.append((f"blk.{L}.ffn_{p}_exps.weight", [ne0, rows, E], 2, blocks.tobytes()))
+        hdr = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), 0)
+        off, data = 0, []
+        for name, ne, tid, raw in tensors:
+            nb = name.encode()
+            hdr += struct.pack("<Q", len(nb)) + nb + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", x) for x in ne)
+            hdr += struct.pack("<IQ", tid, off)
+            pad = (-len(raw)) % 32
+            data.append(raw + b"\0" * pad)
+            off += len(raw) + pad
+        src = d / "m.gguf"
+        with open(src, "wb") as fh:
+            fh.write(hdr + b"\0" * ((-len(hdr)) % 32))
+            for blob in data:
+                fh.write(blob)
+        del data, tensors
+        nbytes = src.stat().st_size
+        t0 = time.perf_counter()
+        gguf_pack.pack([src], d / "experts.bin", log=None)
+        t_pack = time.perf_counter() - t0
+        packed = gguf_pack.load_packed(d)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        bufs = [gguf_pack.load_layer(packed, L)[0] for L in range(2)]
+        torch.cuda.synchronize()
+        t_load = time.perf_counter() - t0
+        packed["fd"].close()
+        loaded = sum(b.numel() for bb in bufs for b in bb)
+        out["loader"] = {"gguf_bytes": nbytes, "pack_s": round(t_pack, 3), "pack_gbps": round(nbytes / t_pack / 1e9, 2),
+                         "load_s": round(t_load, 3), "load_gbps": round(loaded / t_load / 1e9, 2),
+                         "note": "synthetic 2-layer Q4_0 GGUF (H 2048, I 768, E 128) in a temporary directory; pack "
+                                 "syncs and reads back every chunk; load = experts.bin -> HBM through pinned staging"}
+        del bufs
+    return out
+
+
 def cpu_leg(args, g):
     """The C++ restatement of the reference CPU kernel (cpu_kern gather_qmm) over the same experts, converted to
     its affine 4-bit layout, run layer after layer for about --cpu-seconds; tokens/s = 1 / (48 x mean layer time)."""
@@ -450,7 +529,7 @@ def main():
         print(json.dumps({"secondary": grouped_leg()}), flush=True)
         return
     if args.extra_only:
-        print(json.dumps({"types": types_leg(), "trunk": trunk_leg()}), flush=True)
+        print(json.dumps({"types": types_leg(), "trunk": trunk_leg(), "route_loader": route_loader_leg()}), flush=True)
         return
     g = gpu_leg(args)
     cpu = None if args.no_cpu else cpu_leg(args, g)
@@ -458,6 +537,7 @@ def main():
     if secondary is not None:
         secondary["types"] = types_leg()
         secondary["trunk"] = trunk_leg()
+        secondary["route_loader"] = route_loader_leg()
     value = args.steps / g["secs"]
     dom = g["timing"][g["dom"]]
     achieved = dom["bytes"] / (dom["us"] * 1e-6)

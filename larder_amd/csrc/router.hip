@@ -194,24 +194,61 @@ __device__ __forceinline__ float round_dt(float x, int dt) {
   return x;
 }
 
-// The k largest of v (expert lane + 64 j, j < NPL, E <= 64 NPL) by MLX's stable ascending sort read from the
-// back: equal values go to the larger index. Lanes < k get an expert in *idx and its position in the ascending
-// output (best at k - 1) in *pos. A 32-step bit search for the k-th largest key, then the keys above it and the
-// highest-index keys equal to it, compacted into lds (64 dwords), ranked by (key, index) descending.
+// The wave-uniform number of this wavefront's keys at or above c: one ballot a key slot (few slots a lane), or
+// lane-local counts summed once on DPP (many), which keeps the per-step chain off the scalar unit.
 template <int NPL>
-__device__ void select_mlx(const float (&v)[NPL], int E, int k, uint32_t *lds, uint32_t *idx, int *pos) {
-  const int lane = threadIdx.x & 63;
-  uint32_t key[NPL];
+__device__ __forceinline__ int count_ge(const uint32_t (&key)[NPL], uint32_t c) {
+  if (NPL < 4) {
+    int cnt = 0;
 #pragma unroll
-  for (int j = 0; j < NPL; ++j) key[j] = lane + 64 * j < E ? logit_key(v[j]) : 0u;
+    for (int j = 0; j < NPL; ++j) cnt += __popcll(__ballot(key[j] >= c));
+    return cnt;
+  }
+  float local = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) local += key[j] >= c ? 1.0f : 0.0f;
+  return int(wave_sum(local));  // exact: at most 1024
+}
+
+// Threshold of the k largest keys: the largest t with at least k keys >= t (a 32-step bitwise search)
+template <int NPL>
+__device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NPL], int k) {
   uint32_t thr = 0;
   for (int b = 31; b >= 0; --b) {
     const uint32_t cand = thr | (1u << b);
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) cnt += __popcll(__ballot(key[j] >= cand));
-    thr = cnt >= k ? cand : thr;
+    thr = count_ge<NPL>(key, cand) >= k ? cand : thr;
   }
+  return thr;
+}
+
+// The same for two key sets in one loop (their step chains overlap)
+template <int NPL>
+__device__ __forceinline__ void kth_key2(const uint32_t (&ka)[NPL], const uint32_t (&kb)[NPL], int k, uint32_t *ta,
+                                         uint32_t *tb) {
+  uint32_t a = 0, b2 = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t ca = a | (1u << b), cb = b2 | (1u << b);
+    const int na = count_ge<NPL>(ka, ca), nb = count_ge<NPL>(kb, cb);
+    a = na >= k ? ca : a;
+    b2 = nb >= k ? cb : b2;
+  }
+  *ta = a;
+  *tb = b2;
+}
+
+template <int NPL>
+__device__ __forceinline__ void keys_of(const float (&v)[NPL], int E, uint32_t (&key)[NPL]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) key[j] = lane + 64 * j < E ? logit_key(v[j]) : 0u;
+}
+
+// Given the threshold thr of the k largest keys: the picks (ties at thr taken from the highest index down),
+// compacted to LDS in index order, each one's rank among them by (key, index) descending, position k - 1 - rank.
+template <int NPL>
+__device__ __forceinline__ void pick_mlx(const uint32_t (&key)[NPL], uint32_t thr, int k, uint32_t *lds,
+                                         uint32_t *idx, int *pos) {
+  const int lane = threadIdx.x & 63;
   int n_gt = 0;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) n_gt += __popcll(__ballot(key[j] > thr));
@@ -252,10 +289,23 @@ __device__ void select_mlx(const float (&v)[NPL], int E, int k, uint32_t *lds, u
   __builtin_amdgcn_wave_barrier();
 }
 
+
+// The k largest of v (expert lane + 64 j, j < NPL, E <= 64 NPL) by MLX's stable ascending sort read from the
+// back: equal values go to the larger index. Lanes < k get an expert in *idx and its position in the ascending
+// output (best at k - 1) in *pos. A 32-step bit search for the k-th largest key, then the keys above it and the
+// highest-index keys equal to it, compacted into lds (64 dwords), ranked by (key, index) descending.
+template <int NPL>
+__device__ __forceinline__ void select_mlx(const float (&v)[NPL], int E, int k, uint32_t *lds, uint32_t *idx,
+                                           int *pos) {
+  uint32_t key[NPL];
+  keys_of<NPL>(v, E, key);
+  pick_mlx<NPL>(key, kth_key<NPL>(key, k), k, lds, idx, pos);
+}
+
 // The reference budget's sum of k values in T (route_cuda.py:36-37, 98-113): lane l < 32 adds positions l*N .. l*N+N-1
 // from 0 in order (N = 16 / sizeof(T)), each add rounded to T, then the 32 lanes combine by xor 16, 8, 4, 2, 1.
 // sv: the k values by position (LDS). Wave-uniform result.
-__device__ float budget_sum(const float *sv, int k, int dt) {
+__device__ __forceinline__ float budget_sum(const float *sv, int k, int dt) {
   const int lane = threadIdx.x & 63;
   const int n = dt == LMOE_F32 ? 4 : 8;
   float a = 0.0f;
@@ -269,7 +319,7 @@ __device__ float budget_sum(const float *sv, int k, int dt) {
 }
 
 template <int NPL>
-__device__ void route_row(const RouteArgs &a, int r, float *gl, uint32_t *scr, float *sv, uint32_t *okf) {
+__device__ __forceinline__ void route_row(const RouteArgs &a, int r, float *gl, uint32_t *scr, float *sv, uint32_t *okf) {
   const int lane = threadIdx.x & 63;
   const int E = a.E, k = a.k, dt = a.gdt;
   float g[NPL];
@@ -320,10 +370,14 @@ __device__ void route_row(const RouteArgs &a, int r, float *gl, uint32_t *scr, f
   for (int j = 0; j < NPL; ++j) rank[j] = g[j] + ls * m[j];  // two roundings (no contraction in this library)
   uint32_t bi = 0, hi = 0;
   int bp = 0, hp = 0;
-  select_mlx<NPL>(rank, E, k, scr, &bi, &bp);
   bool back = false;
-  if (a.tau > 0.0f) {  // the budget: honest mass against biased mass
-    select_mlx<NPL>(g, E, k, scr, &hi, &hp);
+  if (a.tau > 0.0f) {  // both selections' searches in one loop, then the budget: honest mass against biased mass
+    uint32_t kr[NPL], kg[NPL], tr, tg;
+    keys_of<NPL>(rank, E, kr);
+    keys_of<NPL>(g, E, kg);
+    kth_key2<NPL>(kr, kg, k, &tr, &tg);
+    pick_mlx<NPL>(kr, tr, k, scr, &bi, &bp);
+    pick_mlx<NPL>(kg, tg, k, scr, &hi, &hp);
     if (lane < k) {
       sv[hp] = gl[min(hi, uint32_t(E - 1))];
       sv[32 + bp] = gl[min(bi, uint32_t(E - 1))];
@@ -332,6 +386,8 @@ __device__ void route_row(const RouteArgs &a, int r, float *gl, uint32_t *scr, f
     const float mh = budget_sum(sv, k, dt), mb = budget_sum(sv + 32, k, dt);
     back = round_dt(mh - mb, dt) > round_dt(round_dt(a.tau, dt) * mh, dt);
     __builtin_amdgcn_wave_barrier();
+  } else {
+    select_mlx<NPL>(rank, E, k, scr, &bi, &bp);
   }
   const uint32_t idx = min(back ? hi : bi, uint32_t(E - 1));  // always < E for finite gates; NaN rows stay in bounds
   const int p = back ? hp : bp;
@@ -358,27 +414,18 @@ __device__ void route_row(const RouteArgs &a, int r, float *gl, uint32_t *scr, f
   }
 }
 
+// One kernel per NPL (E <= 64 NPL): each carries only its own unrolled path, which keeps the code of this
+// one-wavefront-a-row kernel small (instruction fetch is most of such a kernel's time).
+template <int NPL>
 __global__ void __launch_bounds__(1024) k_route_bias(RouteArgs a) {
-  __shared__ float gl[kRouteMaxT][kRouteMaxE];
+  __shared__ float gl[kRouteMaxT][64 * NPL];
   __shared__ __attribute__((aligned(16))) uint32_t scr[kRouteMaxT][64];
   __shared__ float sv[kRouteMaxT][64];
   __shared__ uint32_t okf;
   const int wave = threadIdx.x >> 6;
   if (threadIdx.x == 0) okf = 1u;
   __syncthreads();
-  if (wave < a.T) {
-    const int npl = (a.E + 63) / 64;
-    if (npl <= 1)
-      route_row<1>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
-    else if (npl <= 2)
-      route_row<2>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
-    else if (npl <= 4)
-      route_row<4>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
-    else if (npl <= 8)
-      route_row<8>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
-    else
-      route_row<16>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
-  }
+  if (wave < a.T) route_row<NPL>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
   __syncthreads();
   if (threadIdx.x == 0 && a.ok) a.ok[0] = okf;
 }
@@ -479,7 +526,18 @@ extern "C" int lmoe_route_bias(const void *gates, int gdtype, int T, int E, int 
   LMOE_REQUIRE(mask || slot_of, LMOE_EINVAL, "%s: give a mask or a slot table (table mode)", fn);
   LMOE_REQUIRE(slot_of || (!rhs && !ok), LMOE_EINVAL, "%s: rhs and ok need the slot table", fn);
   RouteArgs a{gates, gdtype, T, E, k, mask, slot_of, lim, lam, tau, softmax, norm, inds, ok, rhs, scores};
-  launch(k_route_bias, dim3(1), dim3(64 * T), 0, (hipStream_t)stream, a);
+  const int npl = (E + 63) / 64;
+  auto go = [&](auto kern) { launch(kern, dim3(1), dim3(64 * T), 0, (hipStream_t)stream, a); };
+  if (npl <= 1)
+    go(k_route_bias<1>);
+  else if (npl <= 2)
+    go(k_route_bias<2>);
+  else if (npl <= 4)
+    go(k_route_bias<4>);
+  else if (npl <= 8)
+    go(k_route_bias<8>);
+  else
+    go(k_route_bias<16>);
   LMOE_LAUNCHED(fn);
   return 0;
 }
