@@ -11,6 +11,8 @@
 // probabilities of the picked experts (max-subtracted, fp32), renormalised when asked.
 #include "lmoe_common.h"
 
+#include <type_traits>
+
 namespace lmoe {
 
 constexpr int kMaxNpl = 16;  // logits a lane: E <= 64 * 16
@@ -210,10 +212,12 @@ __device__ __forceinline__ int count_ge(const uint32_t (&key)[NPL], uint32_t c) 
   return int(wave_sum(local));  // exact: at most 1024
 }
 
-// Threshold of the k largest keys: the largest t with at least k keys >= t (a 32-step bitwise search)
+// Threshold of the k largest keys: the largest t with at least k keys >= t (a 32-step bitwise search, kept rolled:
+// the kernel runs once a launch, so a short loop out of the instruction cache beats 32 cold unrolled copies)
 template <int NPL>
 __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NPL], int k) {
   uint32_t thr = 0;
+#pragma unroll 1
   for (int b = 31; b >= 0; --b) {
     const uint32_t cand = thr | (1u << b);
     thr = count_ge<NPL>(key, cand) >= k ? cand : thr;
@@ -226,6 +230,7 @@ template <int NPL>
 __device__ __forceinline__ void kth_key2(const uint32_t (&ka)[NPL], const uint32_t (&kb)[NPL], int k, uint32_t *ta,
                                          uint32_t *tb) {
   uint32_t a = 0, b2 = 0;
+#pragma unroll 1
   for (int b = 31; b >= 0; --b) {
     const uint32_t ca = a | (1u << b), cb = b2 | (1u << b);
     const int na = count_ge<NPL>(ka, ca), nb = count_ge<NPL>(kb, cb);
@@ -318,10 +323,10 @@ __device__ __forceinline__ float budget_sum(const float *sv, int k, int dt) {
   return lane_value(a, 0);
 }
 
-template <int NPL>
+template <int NPL, int DT>
 __device__ __forceinline__ void route_row(const RouteArgs &a, int r, float *gl, uint32_t *scr, float *sv, uint32_t *okf) {
   const int lane = threadIdx.x & 63;
-  const int E = a.E, k = a.k, dt = a.gdt;
+  const int E = a.E, k = a.k, dt = DT;
   float g[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
@@ -414,9 +419,9 @@ __device__ __forceinline__ void route_row(const RouteArgs &a, int r, float *gl, 
   }
 }
 
-// One kernel per NPL (E <= 64 NPL): each carries only its own unrolled path, which keeps the code of this
-// one-wavefront-a-row kernel small (instruction fetch is most of such a kernel's time).
-template <int NPL>
+// One kernel per NPL (E <= 64 NPL) and gate dtype: the dtype's roundings fold to straight-line code, which keeps
+// the path this one-wavefront-a-row kernel runs once a launch short (its instruction fetch is cold).
+template <int NPL, int DT>
 __global__ void __launch_bounds__(1024) k_route_bias(RouteArgs a) {
   __shared__ float gl[kRouteMaxT][64 * NPL];
   __shared__ __attribute__((aligned(16))) uint32_t scr[kRouteMaxT][64];
@@ -425,7 +430,7 @@ __global__ void __launch_bounds__(1024) k_route_bias(RouteArgs a) {
   const int wave = threadIdx.x >> 6;
   if (threadIdx.x == 0) okf = 1u;
   __syncthreads();
-  if (wave < a.T) route_row<NPL>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
+  if (wave < a.T) route_row<NPL, DT>(a, wave, gl[wave], scr[wave], sv[wave], &okf);
   __syncthreads();
   if (threadIdx.x == 0 && a.ok) a.ok[0] = okf;
 }
@@ -528,16 +533,25 @@ extern "C" int lmoe_route_bias(const void *gates, int gdtype, int T, int E, int 
   RouteArgs a{gates, gdtype, T, E, k, mask, slot_of, lim, lam, tau, softmax, norm, inds, ok, rhs, scores};
   const int npl = (E + 63) / 64;
   auto go = [&](auto kern) { launch(kern, dim3(1), dim3(64 * T), 0, (hipStream_t)stream, a); };
-  if (npl <= 1)
-    go(k_route_bias<1>);
-  else if (npl <= 2)
-    go(k_route_bias<2>);
-  else if (npl <= 4)
-    go(k_route_bias<4>);
-  else if (npl <= 8)
-    go(k_route_bias<8>);
+  auto by_npl = [&](auto dtc) {
+    constexpr int D = decltype(dtc)::value;
+    if (npl <= 1)
+      go(k_route_bias<1, D>);
+    else if (npl <= 2)
+      go(k_route_bias<2, D>);
+    else if (npl <= 4)
+      go(k_route_bias<4, D>);
+    else if (npl <= 8)
+      go(k_route_bias<8, D>);
+    else
+      go(k_route_bias<16, D>);
+  };
+  if (a.gdt == LMOE_BF16)
+    by_npl(std::integral_constant<int, LMOE_BF16>());
+  else if (a.gdt == LMOE_F16)
+    by_npl(std::integral_constant<int, LMOE_F16>());
   else
-    go(k_route_bias<16>);
+    by_npl(std::integral_constant<int, LMOE_F32>());
   LMOE_LAUNCHED(fn);
   return 0;
 }
