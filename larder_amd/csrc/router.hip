@@ -213,7 +213,7 @@ __device__ __forceinline__ int count_ge(const uint32_t (&key)[NPL], uint32_t c) 
 }
 
 // Threshold of the k largest keys: the largest t with at least k keys >= t (a 32-step bitwise search, kept rolled:
-// the kernel runs once a launch, so a short loop out of the instruction cache beats 32 cold unrolled copies)
+// the kernel runs its path once a launch, so code length matters more than loop overhead)
 template <int NPL>
 __device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NPL], int k) {
   uint32_t thr = 0;
@@ -284,6 +284,7 @@ __device__ __forceinline__ void pick_mlx(const uint32_t (&key)[NPL], uint32_t th
   if (lane < k) {
     const uint32_t my_key = lds[lane], my_idx = lds[32 + lane];
     int rank = 0;
+#pragma unroll 1
     for (int q = 0; q < k; ++q) {
       const uint32_t kq = lds[q], iq = lds[32 + q];
       rank += (kq > my_key || (kq == my_key && iq > my_idx)) ? 1 : 0;
@@ -412,6 +413,7 @@ __device__ __forceinline__ void route_row(const RouteArgs &a, int r, float *gl, 
       if (lane < k) sv[p] = sc;
       __builtin_amdgcn_wave_barrier();
       float tot = 0.0f;
+#pragma unroll 1
       for (int j = 0; j < k; ++j) tot = round_dt(tot + sv[j], dt);
       sc = round_dt(sc / tot, dt);
     }
