@@ -154,6 +154,19 @@ int lmoe_max_tiles(int R, int E, int bm);
 /* Rows a grouped-GEMM m-tile covers: the bm that lmoe_group_rows and lmoe_max_tiles take for the grouped GEMMs. */
 int lmoe_grouped_tile_rows(void);
 
+/* The tuned launch choices for the grouped GEMMs, so every caller makes the same ones (no counterpart in the
+ * reference, whose dense path has no tile size; gguf_experts.py:698-722 is the path they serve):
+ * lmoe_grouped_pick_tile_rows: the grouping's bm for R rows over E experts with block types (type_g, type_u,
+ *   type_d): 64 when gate/up runs on f16 weights (not Q4_0 / Q4_K, or gate and up of two types), 128 for a Q4
+ *   gate/up with an f16 down, 32 when all three are Q4_0 and R < 16 E, else 128;
+ * lmoe_grouped_pick_ksplit: split-K slices for one GEMM over K at that bm (4, 3 or 2 for 32-row tiles with
+ *   R < 16 E, at least 4 K steps a slice; else 1);
+ * lmoe_grouped_workspace_bytes: bytes of the ws that lmoe_grouped_gate_up_bm / lmoe_grouped_down_bm need with
+ *   the picked ksplit of each (K = H for gate/up, I for down); 0 when neither splits. */
+int lmoe_grouped_pick_tile_rows(int R, int E, int type_g, int type_u, int type_d);
+int lmoe_grouped_pick_ksplit(int R, int E, int bm, int K);
+size_t lmoe_grouped_workspace_bytes(int R, int E, int bm, int H, int I);
+
 /* Grouped gate/up + SwiGLU on the matrix cores over rows grouped by lmoe_group_rows (bm = lmoe_grouped_tile_rows):
  *   h[p][f] = silu(x[order[p] / topk] . wg[e][f]) * (x[order[p] / topk] . wu[e][f])  for grouped row p of expert e,
  * h [R][I] float16 in grouped order (rows past offsets[E] untouched), each row in the GEMM K order (below).

@@ -49,6 +49,9 @@ SIGNATURES = {
     "lmoe_group_rows": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "lmoe_max_tiles": (_I, [_I, _I, _I]),
     "lmoe_grouped_tile_rows": (_I, []),
+    "lmoe_grouped_pick_tile_rows": (_I, [_I, _I, _I, _I, _I]),
+    "lmoe_grouped_pick_ksplit": (_I, [_I, _I, _I, _I]),
+    "lmoe_grouped_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "lmoe_to_f16": (_I, [_P, _I, _LL, _P, _P]),
     "lmoe_to_gemm_f16": (_I, [_P, _I, _LL, _P, _P]),
     "lmoe_grouped_gate_up": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),

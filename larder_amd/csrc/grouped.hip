@@ -769,6 +769,41 @@ using namespace lmoe;
 
 extern "C" int lmoe_grouped_tile_rows(void) { return GM; }
 
+// The tuned tile-row rule (measured on MI355X): 64 when gate/up runs on f16 weights (a type beyond Q4_0 / Q4_K, or
+// gate and up of two types: the f16-weight GEMM then fits two workgroups a CU; 2,048 x 8 rows 405 -> 377 us); 128
+// for a Q4 gate/up with an f16 down; 32 when every projection is Q4_0 and an expert averages fewer than 16 rows
+// (batched decode: each tile streams its expert's weights, and 32-row tiles keep five K steps in flight and allow
+// split-K; cfg4 116.6 -> 108.8 us); else 128 (Q4_K at 40 rows an expert: 64 and 32 rows were slower).
+extern "C" int lmoe_grouped_pick_tile_rows(int R, int E, int type_g, int type_u, int type_d) {
+  auto q4 = [](int t) { return t == LMOE_Q4_0 || t == LMOE_Q4_K; };
+  if (!(q4(type_g) && type_u == type_g)) return 64;
+  if (!q4(type_d)) return GM;
+  const bool all_q4_0 = type_g == LMOE_Q4_0 && type_d == LMOE_Q4_0;
+  return all_q4_0 && E > 0 && (long long)R < 16LL * E ? 32 : GM;
+}
+
+// Split-K slices for one grouped GEMM over K: with 32-row tiles and fewer than 16 rows an expert, few tiles have
+// work and each would walk every K step alone, so a tile is split over 4, 3 or 2 workgroups of at least 4 K steps
+// each; otherwise 1.
+extern "C" int lmoe_grouped_pick_ksplit(int R, int E, int bm, int K) {
+  const int steps = K / GK;
+  if (bm != 32 || E <= 0 || (long long)R >= 16LL * E) return 1;
+  for (int s = 4; s >= 2; --s)
+    if (steps % s == 0 && steps / s >= 4) return s;
+  return 1;
+}
+
+// Bytes of the split-K workspace (ws) that lmoe_grouped_gate_up_bm and lmoe_grouped_down_bm need over a grouping
+// of R rows, E experts and tile rows bm with the picked ksplit of each: ks * R * 2I floats for gate/up, ks * R * H
+// for down, the larger of the two (0 when neither splits).
+extern "C" size_t lmoe_grouped_workspace_bytes(int R, int E, int bm, int H, int I) {
+  if (R <= 0 || H <= 0 || I <= 0) return 0;
+  const int ku = lmoe_grouped_pick_ksplit(R, E, bm, H), kd = lmoe_grouped_pick_ksplit(R, E, bm, I);
+  const size_t gu = ku > 1 ? size_t(ku) * size_t(R) * 2 * size_t(I) : 0;
+  const size_t dn = kd > 1 ? size_t(kd) * size_t(R) * size_t(H) : 0;
+  return (gu > dn ? gu : dn) * sizeof(float);
+}
+
 static int to_f16(const char *fn, const void *x, int xdtype, long long n, void *out, void *stream, int kperm) {
   LMOE_REQUIRE(dtype_ok(xdtype), LMOE_EINVAL, "%s: bad dtype", fn);
   LMOE_REQUIRE(n >= 0, LMOE_ESHAPE, "%s: negative length", fn);

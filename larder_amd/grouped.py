@@ -26,37 +26,26 @@ def tile_rows():
 
 
 def pick_tile_rows(R, E, types):
-    """The GEMMs' tile rows for R rows over E experts: 32 when every projection is Q4_0 and the average expert has
-    fewer than 16 rows (batched decode: few tiles have work, each streams its expert's weights, and 32-row tiles
-    keep five K steps in flight and allow split-K); otherwise 128. Measured on cfg4 (4 rows an expert): 116.6 ->
-    108.8 us a step; on cfg5's prefill (Q4_K, 40 rows an expert) 64-row and 32-row tiles were slower (1,367 and
-    1,546 us against 1,297), since smaller tiles read an expert's weights once a tile. When gate/up runs on
-    dequantized f16 weights (a type beyond Q4_0 / Q4_K, or gate and up of two types): 64, so the f16-weight GEMM
-    fits two workgroups a CU (2,048 x 8 rows: 405 -> 377 us); a Q4 gate/up with an f16 down keeps 128."""
-    if not (types[0] in _lib.Q4_TYPES and types[1] == types[0]):
-        return 64  # gate/up on f16 weights: 64-row tiles let that GEMM run two workgroups a CU
-    if types[2] not in _lib.Q4_TYPES:
-        return tile_rows()  # Q4 gate/up (its 128-row form is the fast one), down on f16 weights
-    return 32 if all(t == "Q4_0" for t in types) and R < 16 * E else tile_rows()
+    """The GEMMs' tile rows for R rows over E experts (lmoe_grouped_pick_tile_rows, the measured rule): 32 when
+    every projection is Q4_0 and the average expert has fewer than 16 rows (batched decode: few tiles have work,
+    each streams its expert's weights, and 32-row tiles keep five K steps in flight and allow split-K; cfg4 116.6 ->
+    108.8 us a step); 64 when gate/up runs on dequantized f16 weights (a type beyond Q4_0 / Q4_K, or gate and up of
+    two types: the f16-weight GEMM then fits two workgroups a CU, 2,048 x 8 rows 405 -> 377 us); otherwise 128
+    (on cfg5's Q4_K prefill, 40 rows an expert, 64 and 32 rows were slower: 1,367 and 1,546 us against 1,297)."""
+    return _lib.lib().lmoe_grouped_pick_tile_rows(int(R), int(E), *(qcode(t) for t in types))
 
 
 def pick_ksplit(R, E, bm, K):
-    """Split-K slices for a GEMM over K of R rows in E experts: with 32-row tiles and fewer than 16 rows an expert
-    on average, few tiles have work and each would walk every K step alone, so each tile is split over 4, 3 or 2
-    workgroups (at least 4 K steps each); otherwise 1."""
-    steps = K // 64
-    if bm != 32 or R >= 16 * E:
-        return 1
-    for s in (4, 3, 2):
-        if steps % s == 0 and steps // s >= 4:
-            return s
-    return 1
+    """Split-K slices for a GEMM over K of R rows in E experts (lmoe_grouped_pick_ksplit): with 32-row tiles and
+    fewer than 16 rows an expert on average, few tiles have work and each would walk every K step alone, so each
+    tile is split over 4, 3 or 2 workgroups (at least 4 K steps each); otherwise 1."""
+    return _lib.lib().lmoe_grouped_pick_ksplit(int(R), int(E), int(bm), int(K))
 
 
 def splitk_floats(R, E, bm, H, I):
-    """Floats of the split-K workspace that gate_up and down over this grouping need (0 without a split)."""
-    return max(pick_ksplit(R, E, bm, H) * R * 2 * I if pick_ksplit(R, E, bm, H) > 1 else 0,
-               pick_ksplit(R, E, bm, I) * R * H if pick_ksplit(R, E, bm, I) > 1 else 0)
+    """Floats of the split-K workspace that gate_up and down over this grouping need (0 without a split):
+    lmoe_grouped_workspace_bytes / 4."""
+    return _lib.lib().lmoe_grouped_workspace_bytes(int(R), int(E), int(bm), int(H), int(I)) // 4
 
 
 class Grouping:

@@ -135,3 +135,34 @@ def test_gemm_k_order_index():
     for j in range(96):
         assert 32 * (j // 32) + block[pos[j] % 32] == j
     assert sorted(pos) == list(range(96))
+
+
+def test_grouped_launch_choices(built_lib):
+    """lmoe_grouped_pick_tile_rows / pick_ksplit / workspace_bytes (host functions, no GPU): the configurations'
+    choices, and split-K slices that divide K into at least 4 steps each with a workspace that holds them."""
+    from larder_amd import grouped
+    q = _lib.qcode
+    pick = lambda R, E, ts: built_lib.lmoe_grouped_pick_tile_rows(R, E, *(q(t) for t in ts))  # noqa: E731
+    assert pick(8192 * 8, 128, ("Q4_0",) * 3) == 128      # cfg3 prefill
+    assert pick(64 * 8, 128, ("Q4_0",) * 3) == 32         # cfg4 batched decode
+    assert pick(2048 * 10, 512, ("Q4_K",) * 3) == 128     # cfg5 prefill
+    assert pick(64, 512, ("Q4_K",) * 3) == 128            # few rows, Q4_K: no 32-row form
+    assert pick(64, 128, ("Q4_K", "Q4_K", "Q6_K")) == 128  # Q4 gate/up, f16 down
+    for ts in (("Q8_0",) * 3, ("Q4_0", "Q4_K", "Q4_0"), ("Q6_K", "Q6_K", "Q4_K")):
+        assert pick(2048 * 8, 128, ts) == 64              # gate/up on f16 weights
+    assert grouped.pick_tile_rows(512, 128, ("Q4_0",) * 3) == 32
+    for R, E, bm, K in ((512, 128, 32, 2048), (512, 128, 32, 768), (80, 60, 32, 5632), (512, 128, 32, 256),
+                        (512, 128, 128, 2048), (4096, 128, 32, 2048), (16, 4, 32, 192)):
+        ks = built_lib.lmoe_grouped_pick_ksplit(R, E, bm, K)
+        if bm != 32 or R >= 16 * E:
+            assert ks == 1
+        else:
+            assert ks in (1, 2, 3, 4) and (K // 64) % ks == 0 and (ks == 1 or K // 64 // ks >= 4)
+    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 2048) == 4   # 32 steps
+    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 768) == 3    # 12 steps
+    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 256) == 1    # 4 steps: no slice of 4
+    R, E, H, I = 512, 128, 2048, 768
+    ku, kd = built_lib.lmoe_grouped_pick_ksplit(R, E, 32, H), built_lib.lmoe_grouped_pick_ksplit(R, E, 32, I)
+    assert built_lib.lmoe_grouped_workspace_bytes(R, E, 32, H, I) == 4 * max(ku * R * 2 * I, kd * R * H)
+    assert built_lib.lmoe_grouped_workspace_bytes(R, E, 128, H, I) == 0
+    assert grouped.splitk_floats(R, E, 32, H, I) * 4 == built_lib.lmoe_grouped_workspace_bytes(R, E, 32, H, I)
