@@ -196,20 +196,15 @@ __device__ __forceinline__ float round_dt(float x, int dt) {
   return x;
 }
 
-// The wave-uniform number of this wavefront's keys at or above c: one ballot a key slot (few slots a lane), or
-// lane-local counts summed once on DPP (many), which keeps the per-step chain off the scalar unit.
+// The wave-uniform number of this wavefront's keys at or above c: one ballot (v_cmp into a scalar pair) and one
+// scalar popcount a key slot. A lone wavefront issues a vector instruction every ~4 cycles, so the scalar unit's
+// counts are the short form; lane-local counts summed on DPP took twice the instructions.
 template <int NPL>
 __device__ __forceinline__ int count_ge(const uint32_t (&key)[NPL], uint32_t c) {
-  if (NPL < 4) {
-    int cnt = 0;
+  int cnt = 0;
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) cnt += __popcll(__ballot(key[j] >= c));
-    return cnt;
-  }
-  float local = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NPL; ++j) local += key[j] >= c ? 1.0f : 0.0f;
-  return int(wave_sum(local));  // exact: at most 1024
+  for (int j = 0; j < NPL; ++j) cnt += __popcll(__ballot(key[j] >= c));
+  return cnt;
 }
 
 // Threshold of the k largest keys: the largest t with at least k keys >= t (a 32-step bitwise search, kept rolled:
@@ -284,10 +279,14 @@ __device__ __forceinline__ void pick_mlx(const uint32_t (&key)[NPL], uint32_t th
   if (lane < k) {
     const uint32_t my_key = lds[lane], my_idx = lds[32 + lane];
     int rank = 0;
+    // four picks a step from 16-byte reads (lds is 16-byte aligned; entries past k are masked off)
 #pragma unroll 1
-    for (int q = 0; q < k; ++q) {
-      const uint32_t kq = lds[q], iq = lds[32 + q];
-      rank += (kq > my_key || (kq == my_key && iq > my_idx)) ? 1 : 0;
+    for (int q0 = 0; q0 < k; q0 += 4) {
+      const u32x4 kq = *reinterpret_cast<const u32x4 *>(lds + q0);
+      const u32x4 iq = *reinterpret_cast<const u32x4 *>(lds + 32 + q0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        rank += (q0 + c < k && (kq[c] > my_key || (kq[c] == my_key && iq[c] > my_idx))) ? 1 : 0;
     }
     *idx = my_idx;
     *pos = k - 1 - rank;
