@@ -207,33 +207,65 @@ __device__ __forceinline__ int count_ge(const uint32_t (&key)[NPL], uint32_t c) 
   return cnt;
 }
 
-// Threshold of the k largest keys: the largest t with at least k keys >= t (a 32-step bitwise search, kept rolled:
-// the kernel runs its path once a launch, so code length matters more than loop overhead)
+// OR and AND of every key of the wavefront (lanes past E hold key 0 and take part), as wave-uniform scalars
 template <int NPL>
-__device__ __forceinline__ uint32_t kth_key(const uint32_t (&key)[NPL], int k) {
-  uint32_t thr = 0;
-#pragma unroll 1
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t cand = thr | (1u << b);
-    thr = count_ge<NPL>(key, cand) >= k ? cand : thr;
+__device__ __forceinline__ void key_bits(const uint32_t (&key)[NPL], uint32_t *o, uint32_t *a) {
+  uint32_t vo = 0u, va = ~0u;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    vo |= key[j];
+    va &= key[j];
   }
-  return thr;
+#define LMOE_OR_AND(ctrl)                                                          \
+  vo |= uint32_t(__builtin_amdgcn_update_dpp(0, int(vo), ctrl, 0xF, 0xF, false)); \
+  va &= uint32_t(__builtin_amdgcn_update_dpp(0, int(va), ctrl, 0xF, 0xF, false))
+  LMOE_OR_AND(kDppXor1);
+  LMOE_OR_AND(kDppXor2);
+  LMOE_OR_AND(kDppHalfMirror);
+  LMOE_OR_AND(kDppMirror);
+#undef LMOE_OR_AND
+  vo |= __builtin_bit_cast(uint32_t, lane_xor16(__builtin_bit_cast(float, vo)));
+  va &= __builtin_bit_cast(uint32_t, lane_xor16(__builtin_bit_cast(float, va)));
+  vo |= __builtin_bit_cast(uint32_t, lane_xor32(__builtin_bit_cast(float, vo)));
+  va &= __builtin_bit_cast(uint32_t, lane_xor32(__builtin_bit_cast(float, va)));
+  *o = __builtin_amdgcn_readfirstlane(vo);
+  *a = __builtin_amdgcn_readfirstlane(va);
 }
 
-// The same for two key sets in one loop (their step chains overlap)
-template <int NPL>
-__device__ __forceinline__ void kth_key2(const uint32_t (&ka)[NPL], const uint32_t (&kb)[NPL], int k, uint32_t *ta,
-                                         uint32_t *tb) {
-  uint32_t a = 0, b2 = 0;
-#pragma unroll 1
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t ca = a | (1u << b), cb = b2 | (1u << b);
-    const int na = count_ge<NPL>(ka, ca), nb = count_ge<NPL>(kb, cb);
-    a = na >= k ? ca : a;
-    b2 = nb >= k ? cb : b2;
+// Thresholds of the k largest keys of NS key sets: for each, the largest t with at least k keys >= t, by a bitwise
+// search. Every key of a set agrees on the bits where OR == AND, and so does its k-th largest key; the search runs
+// only over bits lo..hi, the lowest and highest bits where some set's keys differ (bf16 gates have 16 trailing zero
+// bits), starting from AND's bits above hi and taking AND's bits below lo. A step outside a set's own range leaves
+// its threshold as it is: the candidate equals it (a bit every key has) or exceeds every key (a bit none has), and
+// a bit below the set's range is one every key has or none has. Kept rolled: the kernel runs its path once a
+// launch, so code length matters more than loop overhead.
+template <int NPL, int NS>
+__device__ __forceinline__ void kth_keys(const uint32_t (*keys)[NPL], int k, uint32_t *thr) {
+  uint32_t o[NS], an[NS], diff = 0u;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    key_bits<NPL>(keys[s], &o[s], &an[s]);
+    diff |= o[s] ^ an[s];
   }
-  *ta = a;
-  *tb = b2;
+  if (diff == 0u) {  // every set's keys are all equal
+#pragma unroll
+    for (int s = 0; s < NS; ++s) thr[s] = an[s];
+    return;
+  }
+  const int hi = 31 - __builtin_clz(diff), lo = __builtin_ctz(diff);
+  const uint32_t upto_hi = (2u << hi) - 1u;  // bits 0..hi (hi = 31: all of them)
+#pragma unroll
+  for (int s = 0; s < NS; ++s) thr[s] = an[s] & ~upto_hi;
+#pragma unroll 1
+  for (int b = hi; b >= lo; --b) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const uint32_t cand = thr[s] | (1u << b);
+      thr[s] = count_ge<NPL>(keys[s], cand) >= k ? cand : thr[s];
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < NS; ++s) thr[s] |= an[s] & ((1u << lo) - 1u);
 }
 
 template <int NPL>
@@ -304,7 +336,9 @@ __device__ __forceinline__ void select_mlx(const float (&v)[NPL], int E, int k, 
                                            int *pos) {
   uint32_t key[NPL];
   keys_of<NPL>(v, E, key);
-  pick_mlx<NPL>(key, kth_key<NPL>(key, k), k, lds, idx, pos);
+  uint32_t thr;
+  kth_keys<NPL, 1>(&key, k, &thr);
+  pick_mlx<NPL>(key, thr, k, lds, idx, pos);
 }
 
 // The reference budget's sum of k values in T (route_cuda.py:36-37, 98-113): lane l < 32 adds positions l*N .. l*N+N-1
@@ -377,12 +411,12 @@ __device__ __forceinline__ void route_row(const RouteArgs &a, int r, float *gl, 
   int bp = 0, hp = 0;
   bool back = false;
   if (a.tau > 0.0f) {  // both selections' searches in one loop, then the budget: honest mass against biased mass
-    uint32_t kr[NPL], kg[NPL], tr, tg;
-    keys_of<NPL>(rank, E, kr);
-    keys_of<NPL>(g, E, kg);
-    kth_key2<NPL>(kr, kg, k, &tr, &tg);
-    pick_mlx<NPL>(kr, tr, k, scr, &bi, &bp);
-    pick_mlx<NPL>(kg, tg, k, scr, &hi, &hp);
+    uint32_t ks[2][NPL], th[2];  // 0: the biased ranking's keys, 1: the honest gates'
+    keys_of<NPL>(rank, E, ks[0]);
+    keys_of<NPL>(g, E, ks[1]);
+    kth_keys<NPL, 2>(ks, k, th);
+    pick_mlx<NPL>(ks[0], th[0], k, scr, &bi, &bp);
+    pick_mlx<NPL>(ks[1], th[1], k, scr, &hi, &hp);
     if (lane < k) {
       sv[hp] = gl[min(hi, uint32_t(E - 1))];
       sv[32 + bp] = gl[min(bi, uint32_t(E - 1))];

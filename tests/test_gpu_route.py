@@ -148,3 +148,24 @@ def test_bias_probs_matches_oracle(dt, norm):
                 if (inds[r] == w_inds[r]).all():
                     tol = 1e-6 if dt == "f32" else 2.0 ** -7
                     assert np.allclose(sc[r], w_sc[r], rtol=2 * tol, atol=1e-30), (dt, norm, i, r)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("e,k", [(512, 10), (60, 5)])
+def test_route_search_range_edges(dt, e, k):
+    """The threshold search runs only over the bits where the keys differ: rows whose gates are all equal (no
+    bit differs), take two or three values (a narrow range), or spread over one dt ulp, with and without the bias,
+    against the oracle."""
+    rng = np.random.default_rng(e + k)
+    rows = [np.full(e, 1.0 / e), np.where(np.arange(e) % 3 == 0, 0.02, 0.001),
+            np.choose(np.arange(e) % 3, [0.25, 0.125, 0.0625]), 0.01 * (1 + np.arange(e) % 2 * 2.0 ** -7)]
+    for r in rows:
+        g = np.asarray(torch.from_numpy(r[None].astype(np.float32)).to(TD[dt]).float().numpy())
+        for lam, tau in ((0.0, 0.0), (0.5, 0.2), (2.0, 0.01)):
+            slot, lim = residency(rng, e)
+            m = np.zeros(e, np.float32)
+            m[rng.choice(e, e // 4, replace=False)] = 1.0
+            w_inds, w_ok, w_rhs = rb.route(g, dt, m, slot, lam, tau, k)
+            inds, ok, rhs = run_route(g, dt, m, slot, lam, tau, k)
+            assert (inds.astype(np.uint32) == w_inds).all(), (dt, e, k, lam, tau, r[:4])
+            assert bool(ok[0]) == w_ok and (rhs == w_rhs).all()
