@@ -275,32 +275,45 @@ __device__ __forceinline__ void keys_of(const float (&v)[NPL], int E, uint32_t (
   for (int j = 0; j < NPL; ++j) key[j] = lane + 64 * j < E ? logit_key(v[j]) : 0u;
 }
 
+// Set bits of the wave mask m in lanes below this one (v_mbcnt_lo / v_mbcnt_hi)
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+}
+
 // Given the threshold thr of the k largest keys: the picks (ties at thr taken from the highest index down),
 // compacted to LDS in index order, each one's rank among them by (key, index) descending, position k - 1 - rank.
 template <int NPL>
 __device__ __forceinline__ void pick_mlx(const uint32_t (&key)[NPL], uint32_t thr, int k, uint32_t *lds,
                                          uint32_t *idx, int *pos) {
   const int lane = threadIdx.x & 63;
-  int n_gt = 0;
+  int n_gt = 0, n_eq = 0;
+  uint64_t eqm[NPL];
 #pragma unroll
-  for (int j = 0; j < NPL; ++j) n_gt += __popcll(__ballot(key[j] > thr));
-  const int need = k - n_gt;  // >= 1 ties at thr are taken, highest index first
-  const uint64_t above = lane == 63 ? 0ull : (~0ull << (lane + 1));
-  bool sel[NPL];
-  int eq_after = 0;  // ties at thr with a higher j
-#pragma unroll
-  for (int j = NPL - 1; j >= 0; --j) {
-    const uint64_t eq = __ballot(key[j] == thr);
-    const bool tie = (eq >> lane) & 1u;
-    sel[j] = key[j] > thr || (tie && eq_after + __popcll(eq & above) < need);
-    eq_after += __popcll(eq);
+  for (int j = 0; j < NPL; ++j) {
+    n_gt += __popcll(__ballot(key[j] > thr));
+    eqm[j] = __ballot(key[j] == thr);
+    n_eq += __popcll(eqm[j]);
   }
-  const uint64_t below = (uint64_t(1) << lane) - 1;
+  const int need = k - n_gt;  // >= 1 ties at thr are taken, highest index first
+  bool sel[NPL];
+  if (n_eq == need) {  // the usual case: no surplus ties, every key >= thr is picked
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) sel[j] = key[j] >= thr;
+  } else {
+    int eq_after = 0;  // ties at thr with a higher j
+#pragma unroll
+    for (int j = NPL - 1; j >= 0; --j) {
+      const int tie = int((eqm[j] >> lane) & 1u);
+      const int higher = __popcll(eqm[j]) - lanes_below(eqm[j]) - tie;  // ties in this slot at higher lanes
+      sel[j] = key[j] > thr || (tie && eq_after + higher < need);
+      eq_after += __popcll(eqm[j]);
+    }
+  }
   int sel_before = 0;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     const uint64_t selm = __ballot(sel[j]);
-    const int p = sel_before + __popcll(selm & below);
+    const int p = sel_before + lanes_below(selm);
     if (sel[j] && p < 32) {  // k <= 32 picks; the bound keeps every write inside this wavefront's 64 dwords
       lds[p] = key[j];
       lds[32 + p] = uint32_t(lane + 64 * j);
