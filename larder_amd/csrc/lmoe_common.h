@@ -178,6 +178,8 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8
 constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16
+constexpr int kDppRor8 = 0x128;        // row_ror:8, lane i reads lane (i + 8) mod 16 within 16: lane i ^ 8
+constexpr int kDppRor4 = 0x124;        // row_ror:4, lane i reads lane (i - 4) mod 16 within 16
 
 // the value of lane ^ 16 / lane ^ 32
 // (the swapped pair's elements are copied out as values before the cast: a bit cast of a vector element lvalue is

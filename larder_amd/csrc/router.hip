@@ -365,8 +365,14 @@ __device__ __forceinline__ float budget_sum(const float *sv, int k, int dt) {
     const int j = (lane & 31) * n + i;
     a = round_dt(a + (j < k ? sv[j] : 0.0f), dt);
   }
-#pragma unroll
-  for (int m = 16; m > 0; m >>= 1) a = round_dt(a + __shfl_xor(a, m, 32), dt);
+  // the xor 16, 8, 4, 2, 1 partners without an LDS round trip, each the partner's exact value: permlane16 swap
+  // (lane l ^ 16), row rotate by 8 (l ^ 8), then row rotate by 4 (lane l -/+ 4 mod 16 holds the value of l ^ 4,
+  // since lanes l and l ^ 8 agree after the first two steps), quad permutes (l ^ 2, l ^ 1)
+  a = round_dt(a + lane_xor16(a), dt);
+  a = round_dt(a + LMOE_DPP(a, kDppRor8), dt);
+  a = round_dt(a + LMOE_DPP(a, kDppRor4), dt);
+  a = round_dt(a + LMOE_DPP(a, kDppXor2), dt);
+  a = round_dt(a + LMOE_DPP(a, kDppXor1), dt);
   return lane_value(a, 0);
 }
 
