@@ -139,6 +139,29 @@ int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sums, const ui
                                    const float *shared, const float *gate, int gate_stride, const void *residual,
                                    int rdtype, void *out, int odtype, void *stream);
 
+/* Batch-1 decode through a stack of L MoE layers of one shape in ONE kernel launch: x_{l+1} = x_l + moe_l(x_l),
+ * moe_l = router logits (f16 router weight, plus the shared gate row when Is > 0), softmax top-k (ties to the
+ * lowest index), the k experts' gate/up + SwiGLU and down read from GGUF blocks, weighted by the softmax scores
+ * (renormalised when norm), plus sigmoid(x . wsg) times the shared expert when Is > 0. This is the decode loop of
+ * the reference's layer stack (stream_fast.py:4352-4377 over gguf_experts.experts, gguf_experts.py:803-819) with
+ * the layer boundary moved inside the kernel; it has no single counterpart in the reference. One cooperative launch
+ * of one workgroup a CU; the layers' hand-offs go through the workspace. x and out: [H] f16 (one token).
+ * wg / wu / wd / wr / wsg / sg / su / sd: DEVICE arrays of L device pointers: wg[l], wu[l] [E][I][36 H / 64],
+ * wd[l] [E][H][36 I / 64], wr[l] [E][H] f16, and (Is > 0) wsg[l] [H] f16, sg[l], su[l] [Is][36 H / 64],
+ * sd[l] [H][36 Is / 64], all Q4_0 or all Q4_K (qtype). H 2048 or 4096, E <= 512, k <= 16, I and Is multiples of
+ * 128 (256 for Q4_K). y [L][H] f32 (each layer's MoE output before the residual), ids [L][k], scores [L][k]:
+ * optional (NULL). The workspace (lmoe_stack_workspace_bytes) must be zeroed once before its first use and keeps
+ * state between calls (a launch epoch); calls sharing one workspace must be ordered on one stream. Each internal
+ * wait is bounded (0.2 s); a launch whose wait ran out sets a status word that lmoe_stack_status reads, and the
+ * workspace must then be zeroed again before it is reused (launches on it do nothing until then). */
+size_t lmoe_stack_workspace_bytes(int L, int H, int E, int k, int I, int Is);
+int lmoe_stack_decode(int L, int H, int E, int k, int I, int Is, int qtype, int norm, const void *const *wg,
+                      const void *const *wu, const void *const *wd, const void *const *wr, const void *const *wsg,
+                      const void *const *sg, const void *const *su, const void *const *sd, const void *x, void *out,
+                      void *workspace, float *y, uint32_t *ids, float *scores, void *stream);
+/* The status word of a stack workspace (0: every wait of every launch ended in time); synchronises the stream. */
+int lmoe_stack_status(const void *workspace, uint32_t *status, void *stream);
+
 /* Device-side ragged grouping: the stable counting sort of the flattened (token, k) expert ids, the device
  * form of stream_fast.py:5466-5471 (argsort of the flat ids and its inverse) and gguf_experts.py:702-713.
  * ids [R] -> counts [E], offsets [E + 1], order [R] (rows of expert 0 in flat order, then expert 1, ...; ids >= E

@@ -68,6 +68,9 @@ SIGNATURES = {
     "lmoe_grouped_down_f16w": (_I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P, _I, _P]),
     "lmoe_quantize_q4_0": (_I, [_P, _I, _LL, _I, _P, _P]),
     "lmoe_quantize_q4_k": (_I, [_P, _I, _LL, _I, _P, _P]),
+    "lmoe_stack_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "lmoe_stack_decode": (_I, [_I] * 8 + [_P] * 8 + [_P] * 7),
+    "lmoe_stack_status": (_I, [_P, _P, _P]),
 }
 
 _LIB = None

@@ -261,34 +261,6 @@ __global__ void __launch_bounds__(64 * NW, 3)
   }
 }
 
-// The dot of unit p of a staged row (9 P dwords) with an activation unit held in registers (pairs xv, sums sx0 / sx1).
-template <int TQ>
-__device__ __forceinline__ float row_unit_dot_r(const uint32_t *row, int p, const uint32_t *xv, float sx0, float sx1) {
-  if (TQ == LMOE_Q4_0) {
-    uint32_t u[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) u[i] = row[9 * p + i];
-    return unit_dot_q4_0(u, xv, sx0, sx1);
-  } else {
-    const uint32_t *sb = row + 36 * (p >> 2);
-    const int c = p & 3;
-    uint32_t hdr[4], q[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hdr[i] = sb[i];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[i] = sb[4 + 8 * c + i];
-    return unit_dot_q4_k(hdr, q, c, xv, sx0, sx1);
-  }
-}
-
-// sum over the aligned group of P lanes (P = 32 or 64), the result in every lane of the group
-template <int P>
-__device__ __forceinline__ float group_sum(float v) {
-  if (P == 64) return wave_sum(v);
-  v = sum16(v);
-  const float g0 = lane_value(v, 0) + lane_value(v, 16), g1 = lane_value(v, 32) + lane_value(v, 48);
-  return (threadIdx.x & 32) ? g1 : g0;
-}
 
 // ---- gate/up with the activation unit in registers (H = 64 P, P = 32 or 64; one block type for gate and up) ----
 //

@@ -450,6 +450,109 @@ __device__ __forceinline__ float unit_dot_q4_k(const uint32_t *hdr, const uint32
   return ra + rb;
 }
 
+// The dot of unit p of a staged row (9 P dwords) with an activation unit held in registers (pairs xv, sums sx0 / sx1).
+template <int TQ>
+__device__ __forceinline__ float row_unit_dot_r(const uint32_t *row, int p, const uint32_t *xv, float sx0, float sx1) {
+  if (TQ == LMOE_Q4_0) {
+    uint32_t u[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) u[i] = row[9 * p + i];
+    return unit_dot_q4_0(u, xv, sx0, sx1);
+  } else {
+    const uint32_t *sb = row + 36 * (p >> 2);
+    const int c = p & 3;
+    uint32_t hdr[4], q[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hdr[i] = sb[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = sb[4 + 8 * c + i];
+    return unit_dot_q4_k(hdr, q, c, xv, sx0, sx1);
+  }
+}
+
+// sum over the aligned group of P lanes (P = 32 or 64), the result in every lane of the group
+template <int P>
+__device__ __forceinline__ float group_sum(float v) {
+  if (P == 64) return wave_sum(v);
+  v = sum16(v);
+  const float g0 = lane_value(v, 0) + lane_value(v, 16), g1 = lane_value(v, 32) + lane_value(v, 48);
+  return (threadIdx.x & 32) ? g1 : g0;
+}
+
+// ---- a cheaper nibble decode (the fused decode stack) ----------------------------------------------------------------
+//
+// A nibble q at bits [0, 4) of a 16-bit half under exponent 0x6400 is the f16 value 1024 + q; at bits [4, 8) under
+// 0x5400 it is 64 + q. So a qs word's four nibble pairs become f16 pairs with one and-or each, plus one shift for the
+// upper byte of each half: 5 operations a word instead of 12. The offsets come back out through sums of x: for a
+// Q4_0 block the low nibbles (offset 1024) are its first 16 weights and the high nibbles (offset 64) its last 16, so
+// sum(q x) = acc - 1024 lo16 - 64 (s32 - lo16) with lo16 the sum of the block's first 16 x values and s32 of all 32.
+// Products of f16 values are exact in fp32; the offsets make the fp32 accumulator larger than the 16 + q form's, which
+// costs about 1e-5 relative on a block's dot (measured against the fp32 reference in the stack's parity tests).
+__device__ __forceinline__ float word_dot_f(uint32_t w, const uint32_t *xp, float acc) {
+  const uint32_t ws = w >> 8;
+  acc = dot2((w & 0x000F000Fu) | 0x64006400u, xp[0], acc);
+  acc = dot2((w & 0x00F000F0u) | 0x54005400u, xp[1], acc);
+  acc = dot2((ws & 0x000F000Fu) | 0x64006400u, xp[2], acc);
+  acc = dot2((ws & 0x00F000F0u) | 0x54005400u, xp[3], acc);
+  return acc;
+}
+
+// unit_dot_q4_0 in the cheaper decode; lo0 / lo1: sums of x over the unit's weights [0, 16) and [32, 48)
+__device__ __forceinline__ float unit_dot_q4_0_f(const uint32_t *u, const uint32_t *xp, float sx0, float sx1,
+                                                 float lo0, float lo1) {
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a = word_dot_f(__builtin_amdgcn_alignbyte(u[i + 1], u[i], 2), xp + 4 * i, a);
+  float b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b = word_dot_f(u[5 + i], xp + 16 + 4 * i, b);
+  const float dA = half_lo(u[0]), dB = half_hi(u[4]);
+  // sum((q - 8) x) = acc - 1024 lo - 64 (s - lo) - 8 s = acc - 960 lo - 72 s
+  return dA * fmaf(-960.0f, lo0, fmaf(-72.0f, sx0, a)) + dB * fmaf(-960.0f, lo1, fmaf(-72.0f, sx1, b));
+}
+
+// unit_dot_q4_k in the cheaper decode: the low nibbles (offset 1024) are sub-block 2c, the high ones (64) 2c + 1
+__device__ __forceinline__ float unit_dot_q4_k_f(const uint32_t *hdr, const uint32_t *q, int c, const uint32_t *xp,
+                                                 float sx0, float sx1) {
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t w = q[i], ws = w >> 8;
+    a = dot2((w & 0x000F000Fu) | 0x64006400u, xp[4 * i + 0], a);
+    b = dot2((w & 0x00F000F0u) | 0x54005400u, xp[4 * i + 1], b);
+    a = dot2((ws & 0x000F000Fu) | 0x64006400u, xp[4 * i + 2], a);
+    b = dot2((ws & 0x00F000F0u) | 0x54005400u, xp[4 * i + 3], b);
+  }
+  const float d = half_lo(hdr[0]), dmin = half_hi(hdr[0]);
+  float sc0, m0, sc1, m1;
+  k4_scale_min(hdr[1], hdr[2], hdr[3], 2 * c, &sc0, &m0);
+  k4_scale_min(hdr[1], hdr[2], hdr[3], 2 * c + 1, &sc1, &m1);
+  const float ra = (d * sc0) * fmaf(-1024.0f, sx0, a) - (dmin * m0) * sx0;
+  const float rb = (d * sc1) * fmaf(-64.0f, sx1, b) - (dmin * m1) * sx1;
+  return ra + rb;
+}
+
+// row_unit_dot_r in the cheaper decode (lo0 / lo1 used by Q4_0 only)
+template <int TQ>
+__device__ __forceinline__ float row_unit_dot_f(const uint32_t *row, int p, const uint32_t *xv, float sx0, float sx1,
+                                                float lo0, float lo1) {
+  if (TQ == LMOE_Q4_0) {
+    uint32_t u[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) u[i] = row[9 * p + i];
+    return unit_dot_q4_0_f(u, xv, sx0, sx1, lo0, lo1);
+  } else {
+    const uint32_t *sb = row + 36 * (p >> 2);
+    const int c = p & 3;
+    uint32_t hdr[4], q[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hdr[i] = sb[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = sb[4 + 8 * c + i];
+    return unit_dot_q4_k_f(hdr, q, c, xv, sx0, sx1);
+  }
+}
+
 // ---- preparing activation rows -----------------------------------------------------------------------------------
 
 // Unit dword (p, dw) of a prepared row for block type TQ, from an element reader ld(i) over the row's 64 P values.

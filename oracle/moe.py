@@ -46,6 +46,61 @@ def router(logits, k, norm):
     return ids, s
 
 
+def _tree(s):
+    """Balanced binary tree sum over the last axis (a power of two long), neighbours first, in float32."""
+    s = np.asarray(s, np.float32)
+    while s.shape[-1] > 1:
+        s = (s[..., 0::2] + s[..., 1::2]).astype(np.float32)
+    return s[..., 0]
+
+
+def _exact_products(x, w, H):
+    x = np.asarray(x, np.float32).reshape(-1, H)
+    w = np.asarray(w, np.float32).reshape(-1, H)
+    return (w[None, :, :] * x[:, None, :]).astype(np.float32)  # [T, E, H]; f16 / bf16 products are exact in fp32
+
+
+def router_logits_stack(x, w, lanes=512):
+    """Router logits [T, E] of x [T, H] and w [E, H] in the fused decode stack's order (larder_amd/csrc/stack.hip,
+    phase A): lane t of ``lanes`` sums the products of elements [C t, C t + C) (C = H / lanes) in element order, the
+    first product alone, then the lanes' partials are added as a balanced binary tree in lane order. Exact for f16
+    or bf16 x and w, whose products float32 holds without rounding (each step then rounds once, as the GPU's fused
+    multiply-add does). This is this build's reduction order, not the reference's: its router is an MLX matmul
+    (stream_fast.py:4352-4356) whose order MLX does not fix."""
+    H = np.asarray(x).shape[-1]
+    C = H // lanes
+    p = _exact_products(x, w, H).reshape(-1, np.asarray(w).reshape(-1, H).shape[0], lanes, C)
+    s = p[..., 0]
+    for j in range(1, C):
+        s = (s + p[..., j]).astype(np.float32)
+    return _tree(s)
+
+
+def router_logits_gemv(x, w):
+    """Router logits [T, E] in the order of the per-layer router GEMV (larder_amd/csrc/router.hip k_router_gemv):
+    thread i of 256 sums, in order, the products of its 8-element items i, i + 256, ... (item j covers elements
+    [8 j, 8 j + 8)), starting from zero; each wavefront's 64 partials are added as a balanced binary tree in lane
+    order; the four wavefronts' totals are added left to right. Exact for f16 / bf16 inputs (see
+    router_logits_stack)."""
+    H = np.asarray(x).shape[-1]
+    E = np.asarray(w).reshape(-1, H).shape[0]
+    nit = H // 8
+    ni = -(-nit // 256)
+    p = _exact_products(x, w, H)
+    T = p.shape[0]
+    acc = np.zeros((T, E, 256), np.float32)
+    for i in range(ni):
+        for t in range(256):
+            it = t + 256 * i
+            if it >= nit:
+                continue
+            for e in range(8):
+                acc[:, :, t] = (acc[:, :, t] + p[:, :, 8 * it + e]).astype(np.float32)
+    waves = _tree(acc.reshape(T, E, 4, 64))
+    return (((waves[..., 0] + waves[..., 1]).astype(np.float32) + waves[..., 2]).astype(np.float32)
+            + waves[..., 3]).astype(np.float32)
+
+
 def group_rows(ids, n_experts):
     """Flattened (token, k) rows bucketed by expert id: (counts [E], offsets [E + 1], order [R], inv [R]) with
     ``order`` the stable argsort of the flat ids (rows of one expert in flat order, experts ascending),

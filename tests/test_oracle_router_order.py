@@ -1,0 +1,90 @@
+"""Pins of the oracle's two router-logit restatements (oracle.moe.router_logits_stack / router_logits_gemv).
+
+The GPU kernels sum x . w in a fixed order, and the oracle restates that order so that the expert ids can be
+checked bit for bit from x and the router weight. These cases are built so that the order decides the result
+(2^24 + 1 rounds back to 2^24 in float32, 2^24 + 2 does not), with the expected values derived by hand below;
+a restatement that chunks, trees or orders the partials differently gets a different number.
+"""
+import numpy as np
+
+from oracle import moe
+
+BIG = np.float32(2.0 ** 24)
+
+
+def _one_hot_products(H, placements):
+    """x, w (f16, [1, H] / [1, H]) with product x_i w_i = v at each (i, v) and 0 elsewhere; v in {2^24, 1, 2, 4}."""
+    x = np.zeros((1, H), np.float16)
+    w = np.zeros((1, H), np.float16)
+    for i, v in placements:
+        if v == BIG:
+            x[0, i], w[0, i] = 2048.0, 8192.0
+        else:
+            x[0, i], w[0, i] = float(v), 1.0
+    return x, w
+
+
+def test_stack_order_small_integers_equal_exact_dot():
+    rng = np.random.default_rng(0)
+    for H in (2048, 4096):
+        x = rng.integers(-3, 4, (3, H)).astype(np.float16)
+        w = rng.integers(-3, 4, (5, H)).astype(np.float16)
+        want = x.astype(np.float64) @ w.astype(np.float64).T
+        assert np.array_equal(moe.router_logits_stack(x, w), want.astype(np.float32))
+        assert np.array_equal(moe.router_logits_gemv(x, w), want.astype(np.float32))
+
+
+def test_stack_order_chunk_then_tree():
+    # H 2048, 512 lanes of C = 4. Lane 0: 2^24 then three 1s -> each +1 rounds back: 2^24. Lane 1: 1,1,1,1 -> 4.
+    # Tree: ((2^24 + 4) + 0 ...) = 2^24 + 4 exactly. Sequential over all elements would lose lane 1's ones too
+    # (2^24); a tree over single elements would give 2^24 + 2 + 2 + ... = 2^24 + 6 + ... paths.
+    x, w = _one_hot_products(2048, [(0, BIG), (1, 1), (2, 1), (3, 1), (4, 1), (5, 1), (6, 1), (7, 1)])
+    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24 + 4)
+    # the same products with lane 1's ones moved to lane 256 (the other half of the tree): still 2^24 + 4
+    x, w = _one_hot_products(2048, [(0, BIG), (1, 1), (2, 1), (3, 1), (1024, 1), (1025, 1), (1026, 1), (1027, 1)])
+    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24 + 4)
+    # H 4096: C = 8. Lane 0 holds elements 0..7: 2^24 + seven 1s -> 2^24; lane 1 (elements 8..15) eight 1s -> 8
+    x, w = _one_hot_products(4096, [(0, BIG)] + [(i, 1) for i in range(1, 16)])
+    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24 + 8)
+
+
+def test_stack_order_tree_pairs_neighbours():
+    # partials: lane 0 = 2^24, lanes 1 and 2 = 1 each (others 0). Tree: (2^24 + 1) + (1 + 0) -> 2^24 + 1 = 2^24 at
+    # the first level (round to even), then 2^24 + 1 -> 2^24. Result 2^24. If the tree paired lane 0 with lane 256
+    # first, the ones would meet each other first and give 2^24 + 2.
+    x, w = _one_hot_products(2048, [(0, BIG), (4, 1), (8, 1)])
+    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24)
+    # lanes 2 and 3 = 1 each: (2^24 + 0) + (1 + 1) = 2^24 + 2
+    x, w = _one_hot_products(2048, [(0, BIG), (8, 1), (12, 1)])
+    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24 + 2)
+
+
+def test_gemv_order_waves_left_to_right():
+    # H 2048: 256 threads of one 8-element item. Wave 0 (threads 0..63, elements 0..511) totals 2^24; waves 1, 2,
+    # 3 total 1 each. Left to right: ((2^24 + 1) + 1) + 1 = 2^24 (each +1 lost). A tree over the waves would give
+    # (2^24 + 1) + (1 + 1) = 2^24 + 2.
+    x, w = _one_hot_products(2048, [(0, BIG), (512, 1), (1024, 1), (1536, 1)])
+    assert moe.router_logits_gemv(x, w)[0, 0] == np.float32(2.0 ** 24)
+    # wave 0 = 2^24, wave 1 = 2: (2^24 + 2) + 0 + 0 = 2^24 + 2
+    x, w = _one_hot_products(2048, [(0, BIG), (512, 2)])
+    assert moe.router_logits_gemv(x, w)[0, 0] == np.float32(2.0 ** 24 + 2)
+
+
+def test_gemv_order_items_of_a_thread():
+    # H 4096: thread 0 holds items 0 and 256 (elements 0..7, then 2048..2055), summed in that order from zero:
+    # 2^24 + 1 + 1 -> 2^24; thread 1 (elements 8..15) holds 2 -> wave tree (2^24 + 2) = 2^24 + 2.
+    x, w = _one_hot_products(4096, [(0, BIG), (2048, 1), (2049, 1), (8, 2)])
+    assert moe.router_logits_gemv(x, w)[0, 0] == np.float32(2.0 ** 24 + 2)
+    # inside a wave the tree pairs neighbours: threads 0 (2^24) and 1 (1) -> 2^24, thread 2 (1) + thread 3 (0) = 1,
+    # then 2^24 + 1 -> 2^24
+    x, w = _one_hot_products(2048, [(0, BIG), (8, 1), (16, 1)])
+    assert moe.router_logits_gemv(x, w)[0, 0] == np.float32(2.0 ** 24)
+
+
+def test_planted_order_mistake_is_caught():
+    """A restatement that sums a lane's chunk as a tree instead of in element order gives a different value on the
+    case above: the pins would catch that mistake."""
+    x, w = _one_hot_products(2048, [(0, BIG), (1, 1), (2, 1), (3, 1), (4, 1), (5, 1), (6, 1), (7, 1)])
+    p = (x.astype(np.float32) * w.astype(np.float32)).reshape(512, 4)
+    wrong = moe._tree(moe._tree(p))   # tree inside the chunk: (2^24 + 1) + (1 + 1) = 2^24 + 2 for lane 0
+    assert wrong != moe.router_logits_stack(x, w)[0, 0]
