@@ -171,6 +171,14 @@ int lmoe_stack_status(const void *workspace, uint32_t *status, void *stream);
 size_t lmoe_group_workspace_bytes(int R, int E);
 int lmoe_group_rows(const uint32_t *ids, int R, int E, int bm, uint32_t *counts, uint32_t *offsets,
                     uint32_t *order, uint32_t *inv, uint32_t *tiles, uint32_t *n_tiles, void *ws, void *stream);
+/* lmoe_group_rows with no workspace argument, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); no counterpart in the reference. The histograms
+ * live in a file-scope device array of 1 MiB (lmoe_group_workspace_bytes(R, E) must not exceed it: R <= 519,936 at
+ * E = 128, R <= 65,024 at E = 1024; larger requests are refused with LMOE_EWORKSPACE). The call
+ * allocates nothing. Every call on one GPU shares that array, so calls that overlap on one GPU (two streams) race;
+ * order them on one stream. Same arguments and results as lmoe_group_rows otherwise. */
+int lmoe_group_rows_noalloc(const uint32_t *ids, int R, int E, int bm, uint32_t *counts, uint32_t *offsets,
+                            uint32_t *order, uint32_t *inv, uint32_t *tiles, uint32_t *n_tiles, void *stream);
 /* Upper bound on the grouped GEMM tiles for R rows over E experts at bm rows a tile. */
 int lmoe_max_tiles(int R, int E, int bm);
 

@@ -47,6 +47,7 @@ SIGNATURES = {
                                             _P]),
     "lmoe_group_workspace_bytes": (_SZ, [_I, _I]),
     "lmoe_group_rows": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "lmoe_group_rows_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "lmoe_max_tiles": (_I, [_I, _I, _I]),
     "lmoe_grouped_tile_rows": (_I, []),
     "lmoe_grouped_pick_tile_rows": (_I, [_I, _I, _I, _I, _I]),

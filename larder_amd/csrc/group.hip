@@ -12,6 +12,8 @@
 //      by comparing against the chunk's keys in LDS), so rows keep flat order within an expert. Workgroup 0 also
 //      writes counts, offsets and the grouped GEMM's work list.
 // Bucket E collects ids >= E, which therefore sort after every expert.
+#include <mutex>
+
 #include "lmoe_common.h"
 
 namespace lmoe {
@@ -173,4 +175,53 @@ extern "C" int lmoe_group_rows(const uint32_t *ids, int R, int E, int bm, uint32
          static_cast<const uint32_t *>(totals), nchunk, counts, offsets, order, inv, tiles, n_tiles);
   LMOE_LAUNCHED(fn);
   return 0;
+}
+
+// ---- the same grouping with no caller workspace ------------------------------------------------------------------
+//
+// For callers that cannot allocate device memory (code under graph capture, serving loops, harnesses that forbid
+// it): the histograms and totals live in a file-scope device array. Each GPU holds its own copy until the process
+// ends; its address is taken once per device (hipGetSymbolAddress) and kept, and host code passes only that address
+// to kernels. Every call on one GPU shares the array, so calls that overlap on one GPU race. The count and scan
+// kernels write every entry they later read, so nothing needs clearing between calls.
+namespace lmoe {
+constexpr size_t kGroupScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) uint8_t scratch[kGroupScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void **out, const char *fn) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, fn);
+  LMOE_REQUIRE(dev >= 0 && dev < kMaxDevices, LMOE_EINVAL, "%s: device %d is past %d", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, fn);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+}  // namespace
+}  // namespace lmoe
+
+extern "C" int lmoe_group_rows_noalloc(const uint32_t *ids, int R, int E, int bm, uint32_t *counts,
+                                       uint32_t *offsets, uint32_t *order, uint32_t *inv, uint32_t *tiles,
+                                       uint32_t *n_tiles, void *stream) {
+  const char *fn = "lmoe_group_rows_noalloc";
+  LMOE_REQUIRE(R >= 0 && R <= (1 << 24), LMOE_ESHAPE, "%s: %d rows is outside 0..2^24", fn, R);
+  LMOE_REQUIRE(E > 0 && E <= kGroupMaxE, LMOE_ESHAPE, "%s: %d experts is outside 1..%d", fn, E, kGroupMaxE);
+  const size_t need = lmoe_group_workspace_bytes(R, E);
+  LMOE_REQUIRE(need <= kGroupScratchBytes, LMOE_EWORKSPACE,
+               "%s: %d rows over %d experts need %zu bytes of scratch, more than the %zu this entry point holds", fn,
+               R, E, need, kGroupScratchBytes);
+  void *ws = nullptr;
+  if (int rc = scratch_for_current_device(&ws, fn)) return rc;
+  return lmoe_group_rows(ids, R, E, bm, counts, offsets, order, inv, tiles, n_tiles, ws, stream);
 }
