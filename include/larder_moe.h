@@ -69,6 +69,18 @@ int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, const void 
                           int E, int k, int norm, float *logits, uint32_t *ids, float *scores, uint32_t *xprep,
                           int qtype, void *stream);
 
+/* Router GEMV and top-k in ONE launch: the logits of lmoe_router_gemv (the same bits: every row summed in its order),
+ * then the ids / scores of lmoe_router_topk (ties to the lowest index, best first), plus the prepared activation rows
+ * when xprep is given. The workgroup that finishes its rows last ranks every token, so no gate/up wavefront has to
+ * rank (the fused form lmoe_moe_gate_up ranks in each of them). ks: slots a token in ids / scores, k or (with wsg)
+ * k + 1, slot k then holding id E and weight sigmoid(x . wsg): the folded shared expert of lmoe_moe_gate_up_ext.
+ * sync: one uint32 of device memory, zero before the first call, left zero by each call; one per stream (two calls
+ * in flight on one counter race). E <= 512, k <= 16, T <= 16. Replaces the reference's gate linear + moe_probs
+ * (route_cuda.py:193-254, 280-288, 433-444). */
+int lmoe_router_gemv_rank(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T, int H, int E,
+                          int k, int norm, int ks, float *logits, uint32_t *ids, float *scores, uint32_t *xprep,
+                          int qtype, uint32_t *sync, void *stream);
+
 /* The cache-biased route of route_cuda.route / route_cuda.bias_probs (route_cuda.py:42-121, 158-178, 306-417), which
  * reproduce CacheBiasedMoE._select: per row of gates g [E] in gdtype T (softmax: the row holds logits and
  * g = T(softmax)), spread = T(max g - min g), rank = float(g) + float(T(T(lam) * spread)) * m with m = mask[e]

@@ -37,6 +37,7 @@ SIGNATURES = {
     "lmoe_prep_x": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "lmoe_router_gemv": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
     "lmoe_router_gemv_topk": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P]),
+    "lmoe_router_gemv_rank": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P]),
     "lmoe_route_bias": (_I, [_P, _I, _I, _I, _I, _P, _P, _I, _F, _F, _I, _I, _P, _P, _P, _P, _P]),
     "lmoe_gemv_gate_up": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "lmoe_gemv_gate_up_prepped": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P]),

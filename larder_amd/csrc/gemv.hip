@@ -15,6 +15,7 @@
 //   * down adds the k experts of a token, weighted by the router scores, plus the shared expert and a residual,
 //     in the same kernel, so no [T * k, H] intermediate is written.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "lmoe_common.h"
@@ -276,7 +277,7 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // ks: slots a token, topk or, with a shared expert folded in (NPL > 0 only), topk + 1: then slot topk of a token
 // is the shared expert, stored as expert n_experts of wg / wu, and ids_out / scores_out rows hold ks entries, the
 // last (n_experts, sigmoid(logits[t][n_experts])) for the down kernel to weight it like a routed expert.
-template <int TQ, int P, int RB, int NPL>
+template <int TQ, int P, int RB, int NPL, bool RANKWG>
 __global__ void __launch_bounds__(256)
     k_gate_up_xr(const uint32_t *xprep, const uint32_t *slots, int topk, const uint8_t *wg, const uint8_t *wu,
                  int n_experts, int I, float *h, uint32_t *hprep, int td, const float *logits, int ld_stride,
@@ -302,9 +303,18 @@ __global__ void __launch_bounds__(256)
   const int jslot = s % ks;
   const bool shared_slot = NPL > 0 && jslot == topk;  // uniform across the workgroup
 
+  // RANKWG and E <= 512: the workgroup ranks its token's logits once (rank256: the four wavefronts share the
+  // comparisons); otherwise each wavefront ranks them itself (topk_wave)
+  constexpr bool RANK = RANKWG && NPL > 0 && NPL <= 8;
+  __shared__ __attribute__((aligned(16))) RankScratch rs;
   float v[NPL > 0 ? NPL : 1];
+  float lv[2];
   uint32_t e = 0;
-  if (NPL > 0) {
+  if (RANK) {
+    const float *row = logits + xrow * ld_stride;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) lv[j] = row[min(int(threadIdx.x) + 256 * j, n_experts - 1)];
+  } else if (NPL > 0) {
     const float *row = logits + xrow * ld_stride;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) v[j] = row[min(lane + 64 * j, n_experts - 1)];  // lanes past E: masked by topk_wave
@@ -320,6 +330,17 @@ __global__ void __launch_bounds__(256)
     if (blockIdx.x == 0 && wave == 0 && lane == 0) {
       ids_out[s] = e;
       scores_out[s] = sigmoidf_(logits[xrow * ld_stride + n_experts]);
+    }
+  } else if (RANK) {  // uniform across the workgroup (the slot is blockIdx.y)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (int(threadIdx.x) + 256 * j < n_experts) rs.vals[threadIdx.x + 256 * j] = lv[j];
+    __syncthreads();
+    const float p = rank256(rs, n_experts, topk, norm, int(threadIdx.x));
+    e = rs.pick[jslot];
+    if (blockIdx.x == 0 && int(threadIdx.x) == jslot) {
+      ids_out[s] = e;
+      scores_out[s] = p;
     }
   } else if (NPL > 0) {  // each wavefront picks the slot's expert itself (no barrier before its weight loads)
     constexpr int N = NPL > 0 ? NPL : 1;
@@ -696,10 +717,21 @@ static int launch_gate_up(const GateUpArgs &a, hipStream_t st) {
 }
 
 // 2 rows a task when the row chunks split evenly (P even), else 4; NC covers a task's 16-byte chunks a lane.
+// Where the fused top-k ranks: in each wavefront (the default: cfg2 in a HIP graph, 15.65 against 15.84 us a layer
+// on one box), or with LMOE_GATE_UP_RANK=1 once a workgroup (rank256, one barrier before every weight load).
+static bool gate_up_rank_wg() {
+  static const bool wg = [] {
+    const char *v = getenv("LMOE_GATE_UP_RANK");
+    return v && v[0] == '1';
+  }();
+  return wg;
+}
+
 template <int TQ, int P, int RB, int NPL>
 static int launch_gate_up_xr(const GateUpArgs &a, hipStream_t st) {
   const dim3 grid((a.I + 4 * RB - 1) / (4 * RB), a.n_slots);
-  launch(k_gate_up_xr<TQ, P, RB, NPL>, grid, dim3(256), 0, st, a.xg_prep, a.slots, a.topk, a.wg, a.wu,
+  auto kern = gate_up_rank_wg() ? k_gate_up_xr<TQ, P, RB, NPL, true> : k_gate_up_xr<TQ, P, RB, NPL, false>;
+  launch(kern, grid, dim3(256), 0, st, a.xg_prep, a.slots, a.topk, a.wg, a.wu,
          a.n_experts, a.I, a.h, a.hprep, a.td, a.logits, a.ld_stride, a.norm, a.ids_out, a.scores_out,
          a.ks ? a.ks : a.topk);
   LMOE_LAUNCHED("lmoe_gemv_gate_up");

@@ -6,10 +6,11 @@
 // nibbles). Row bytes are 36 * (cols / 64) for both, so one staging scheme serves both types.
 //
 // Dot products run on v_dot2_f32_f16: x is held as f16 pairs arranged in the order the nibbles sit in a 32-bit
-// word, and a nibble q becomes the f16 value 16 + q by masking it into mantissa bits 6..9 under the exponent of
-// 16 (0x4C00). Then sum((16 + q) x) = 16 sum(x) + sum(q x): the block's exact sum(q x) follows from one fused
-// multiply-add with the block's precomputed sum(x). Products of f16 values are exact in fp32, so the dot is an
-// fp32-accumulated dot of the exact integer nibbles with the f16 activations.
+// word, and a nibble q becomes the f16 value 64 + q by moving it to mantissa bits 4..7 (one shift, none for the
+// nibble already there) and masking it under the exponent of 64 (0x5400): 7 operations a word of 8 nibbles. Then
+// sum((64 + q) x) = 64 sum(x) + sum(q x): the block's exact sum(q x) follows from one fused multiply-add with the
+// block's precomputed sum(x). Products of f16 values are exact in fp32, so the dot is an fp32-accumulated dot of
+// the exact integer nibbles with the f16 activations.
 //
 // Prepared activations ("prep" rows): an activation row of 64 P values is kept as P units of 36 dwords, the
 // layout the kernels use in LDS: dwords 0..31 the unit's f16 pairs in nibble order (xelem below), dwords 32 and 33
@@ -339,20 +340,140 @@ __device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm
   *score_out = mine;
 }
 
+// Entries of ck[f0, f0 + 2 N) (composite keys, 16-byte aligned) above `me`. Composite key: order-preserving logit
+// key in the high half, 0xFFFFFFFF - expert in the low half, so a larger composite is the better pick (larger logit,
+// or equal logit and lower index) and no two experts tie; 0 pads an empty slot below every expert.
+template <int N>
+__device__ __forceinline__ int count_above(const uint64_t *ck, int f0, uint64_t me) {
+  typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+  const u64x2 *p = reinterpret_cast<const u64x2 *>(ck + f0);
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const u64x2 v = p[j];
+    const uint64_t v0 = v.x, v1 = v.y;
+    c += (v0 > me ? 1 : 0) + (v1 > me ? 1 : 0);
+  }
+  return c;
+}
+
+// ---- top-k of one token by a 256-thread workgroup ------------------------------------------------------------
+
+constexpr int kRankMaxE = 512;
+constexpr int kRankMaxK = 16;
+
+struct RankScratch {
+  float vals[kRankMaxE + 16];
+  uint64_t ck[kRankMaxE];
+  uint64_t surv[8 * kRankMaxK];
+  uint32_t cnt[128 * 8];
+  uint32_t pick[kRankMaxK];
+  float praw[kRankMaxK];
+  float red[4];
+};
+
+// The top k of vals[0, E) (LDS) by the 256 threads of the workgroup: composite keys (logit key above, 0xFFFFFFFF -
+// expert below: no ties, lower index first among equal logits); E > 128: the best k of each 64-candidate chunk
+// survive; the survivors' ranks are the sums of counts over 8 groups of 16. Leaves ids in s.pick, and returns in
+// threads r < k the softmax probability of pick r (max subtracted, fp32; renormalised in rank order when norm).
+__device__ __forceinline__ float rank256(RankScratch &s, int E, int k, int norm, int tid) {
+  typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+  uint64_t mine[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = tid + 256 * j;
+    mine[j] = e < E ? (uint64_t(logit_key(s.vals[e])) << 32) | (0xFFFFFFFFu - uint32_t(e)) : 0u;
+    s.ck[e] = mine[j];
+  }
+  if (tid < 8 * kRankMaxK) s.surv[tid] = 0u;
+  __syncthreads();
+  const uint64_t *set = s.ck;
+  if (E > 128) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = tid + 256 * j;
+      const int c = count_above<32>(s.ck, e & ~63, mine[j]);
+      if (e < E && c < k) s.surv[(e >> 6) * k + c] = mine[j];
+    }
+    __syncthreads();
+    set = s.surv;
+  }
+  {
+    const int g = tid & 31, q = tid >> 5;
+    const u64x2 *p16 = reinterpret_cast<const u64x2 *>(set + 16 * q);
+    uint64_t o[16];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u64x2 v = p16[j];
+      o[2 * j] = v.x;
+      o[2 * j + 1] = v.y;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint64_t me = set[g + 32 * i];
+      int c = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) c += o[j] > me ? 1 : 0;
+      s.cnt[(g + 32 * i) * 8 + q] = uint32_t(c);
+    }
+  }
+  __syncthreads();
+  if (tid < 128 && set[tid] != 0u) {
+    const u32x4 *c4 = reinterpret_cast<const u32x4 *>(s.cnt + 8 * tid);
+    const u32x4 a = c4[0], b = c4[1];
+    const uint32_t r = a.x + a.y + a.z + a.w + b.x + b.y + b.z + b.w;
+    if (r < uint32_t(k)) s.pick[r] = 0xFFFFFFFFu - uint32_t(set[tid]);
+  }
+  __syncthreads();
+  // softmax denominator: this thread's two terms, a wavefront tree, the four wavefronts left to right
+  const float m = s.vals[s.pick[0]];
+  float term = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = tid + 256 * j;
+    if (e < E) term += __expf(s.vals[e] - m);
+  }
+  term = wave_sum(term);
+  if ((tid & 63) == 0) s.red[tid >> 6] = term;
+  __syncthreads();
+  const float tot = ((s.red[0] + s.red[1]) + s.red[2]) + s.red[3];
+  float p = 0.0f;
+  if (tid < k) {
+    p = __expf(s.vals[s.pick[tid]] - m) / tot;
+    s.praw[tid] = p;
+  }
+  __syncthreads();
+  if (tid < k && norm) {
+    float sum = 0.0f;  // the k probabilities in rank order
+    for (int r = 0; r < k; ++r) sum += s.praw[r];
+    p = p / sum;
+  }
+  return p;
+}
+
 // ---- nibble words -> f16 pairs ----------------------------------------------------------------------------------
 
-// The f16 pair (16 + a, 16 + b) from nibbles a, b sitting at bits [s, s+4) and [s+16, s+20) of w (0 <= s <= 12).
+// (t & 0x00F000F0) | 0x54005400 in one v_and_or_b32. The compiler splits it into an and and an or (the fused form
+// takes at most one scalar operand on gfx9 and both constants are literals); here the mask rides in a vector
+// register, the exponent constant in a scalar one.
+__device__ __forceinline__ uint32_t and_or_nib(uint32_t t) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(t), "v"(0x00F000F0u), "s"(0x54005400u));
+  return r;
+}
+
+// The f16 pair (64 + a, 64 + b) from nibbles a, b sitting at bits [s, s+4) and [s+16, s+20) of w (0 <= s <= 12).
 template <int S>
 __device__ __forceinline__ uint32_t nib_pair(uint32_t w) {
-  const uint32_t t = S <= 6 ? (w << (6 - S)) : (w >> (S - 6));
-  return (t & 0x03C003C0u) | 0x4C004C00u;
+  const uint32_t t = S == 4 ? w : (S < 4 ? (w << (4 - S)) : (w >> (S - 4)));
+  return and_or_nib(t);
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a), __builtin_bit_cast(h2_t, b), c, false);
 }
 
-// sum((16 + q) x) over the 8 nibbles of qs word w against x pairs xp[0..3] =
+// sum((64 + q) x) over the 8 nibbles of qs word w against x pairs xp[0..3] =
 // (x[j], x[j+2]), (x[j+H], x[j+H+2]), (x[j+1], x[j+3]), (x[j+H+1], x[j+H+3]) where the word's low nibbles are
 // weights j..j+3 and its high nibbles weights j+H..j+H+3 (H = 16 for Q4_0, 32 for Q4_K).
 __device__ __forceinline__ float word_dot(uint32_t w, const uint32_t *xp, float acc) {
@@ -423,8 +544,8 @@ __device__ __forceinline__ float unit_dot_q4_0(const uint32_t *u, const uint32_t
 #pragma unroll
   for (int i = 0; i < 4; ++i) b = word_dot(u[5 + i], xp + 16 + 4 * i, b);
   const float dA = half_lo(u[0]), dB = half_hi(u[4]);
-  // sum((q - 8) x) = sum((16 + q) x) - 24 sum(x)
-  return dA * fmaf(-24.0f, sx0, a) + dB * fmaf(-24.0f, sx1, b);
+  // sum((q - 8) x) = sum((64 + q) x) - 72 sum(x)
+  return dA * fmaf(-72.0f, sx0, a) + dB * fmaf(-72.0f, sx1, b);
 }
 
 __device__ __forceinline__ float unit_dot_q4_k(const uint32_t *hdr, const uint32_t *q, int c, const uint32_t *xp,
@@ -444,9 +565,9 @@ __device__ __forceinline__ float unit_dot_q4_k(const uint32_t *hdr, const uint32
   float sc0, m0, sc1, m1;
   k4_scale_min(hdr[1], hdr[2], hdr[3], 2 * c, &sc0, &m0);
   k4_scale_min(hdr[1], hdr[2], hdr[3], 2 * c + 1, &sc1, &m1);
-  // w = (d sc) q - (dmin m): sum(w x) = (d sc) (sum((16 + q) x) - 16 sum(x)) - (dmin m) sum(x)
-  const float ra = (d * sc0) * fmaf(-16.0f, sx0, a) - (dmin * m0) * sx0;
-  const float rb = (d * sc1) * fmaf(-16.0f, sx1, b) - (dmin * m1) * sx1;
+  // w = (d sc) q - (dmin m): sum(w x) = (d sc) (sum((64 + q) x) - 64 sum(x)) - (dmin m) sum(x)
+  const float ra = (d * sc0) * fmaf(-64.0f, sx0, a) - (dmin * m0) * sx0;
+  const float rb = (d * sc1) * fmaf(-64.0f, sx1, b) - (dmin * m1) * sx1;
   return ra + rb;
 }
 
@@ -477,80 +598,6 @@ __device__ __forceinline__ float group_sum(float v) {
   v = sum16(v);
   const float g0 = lane_value(v, 0) + lane_value(v, 16), g1 = lane_value(v, 32) + lane_value(v, 48);
   return (threadIdx.x & 32) ? g1 : g0;
-}
-
-// ---- a cheaper nibble decode (the fused decode stack) ----------------------------------------------------------------
-//
-// A nibble q at bits [0, 4) of a 16-bit half under exponent 0x6400 is the f16 value 1024 + q; at bits [4, 8) under
-// 0x5400 it is 64 + q. So a qs word's four nibble pairs become f16 pairs with one and-or each, plus one shift for the
-// upper byte of each half: 5 operations a word instead of 12. The offsets come back out through sums of x: for a
-// Q4_0 block the low nibbles (offset 1024) are its first 16 weights and the high nibbles (offset 64) its last 16, so
-// sum(q x) = acc - 1024 lo16 - 64 (s32 - lo16) with lo16 the sum of the block's first 16 x values and s32 of all 32.
-// Products of f16 values are exact in fp32; the offsets make the fp32 accumulator larger than the 16 + q form's, which
-// costs about 1e-5 relative on a block's dot (measured against the fp32 reference in the stack's parity tests).
-__device__ __forceinline__ float word_dot_f(uint32_t w, const uint32_t *xp, float acc) {
-  const uint32_t ws = w >> 8;
-  acc = dot2((w & 0x000F000Fu) | 0x64006400u, xp[0], acc);
-  acc = dot2((w & 0x00F000F0u) | 0x54005400u, xp[1], acc);
-  acc = dot2((ws & 0x000F000Fu) | 0x64006400u, xp[2], acc);
-  acc = dot2((ws & 0x00F000F0u) | 0x54005400u, xp[3], acc);
-  return acc;
-}
-
-// unit_dot_q4_0 in the cheaper decode; lo0 / lo1: sums of x over the unit's weights [0, 16) and [32, 48)
-__device__ __forceinline__ float unit_dot_q4_0_f(const uint32_t *u, const uint32_t *xp, float sx0, float sx1,
-                                                 float lo0, float lo1) {
-  float a = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a = word_dot_f(__builtin_amdgcn_alignbyte(u[i + 1], u[i], 2), xp + 4 * i, a);
-  float b = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) b = word_dot_f(u[5 + i], xp + 16 + 4 * i, b);
-  const float dA = half_lo(u[0]), dB = half_hi(u[4]);
-  // sum((q - 8) x) = acc - 1024 lo - 64 (s - lo) - 8 s = acc - 960 lo - 72 s
-  return dA * fmaf(-960.0f, lo0, fmaf(-72.0f, sx0, a)) + dB * fmaf(-960.0f, lo1, fmaf(-72.0f, sx1, b));
-}
-
-// unit_dot_q4_k in the cheaper decode: the low nibbles (offset 1024) are sub-block 2c, the high ones (64) 2c + 1
-__device__ __forceinline__ float unit_dot_q4_k_f(const uint32_t *hdr, const uint32_t *q, int c, const uint32_t *xp,
-                                                 float sx0, float sx1) {
-  float a = 0.0f, b = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t w = q[i], ws = w >> 8;
-    a = dot2((w & 0x000F000Fu) | 0x64006400u, xp[4 * i + 0], a);
-    b = dot2((w & 0x00F000F0u) | 0x54005400u, xp[4 * i + 1], b);
-    a = dot2((ws & 0x000F000Fu) | 0x64006400u, xp[4 * i + 2], a);
-    b = dot2((ws & 0x00F000F0u) | 0x54005400u, xp[4 * i + 3], b);
-  }
-  const float d = half_lo(hdr[0]), dmin = half_hi(hdr[0]);
-  float sc0, m0, sc1, m1;
-  k4_scale_min(hdr[1], hdr[2], hdr[3], 2 * c, &sc0, &m0);
-  k4_scale_min(hdr[1], hdr[2], hdr[3], 2 * c + 1, &sc1, &m1);
-  const float ra = (d * sc0) * fmaf(-1024.0f, sx0, a) - (dmin * m0) * sx0;
-  const float rb = (d * sc1) * fmaf(-64.0f, sx1, b) - (dmin * m1) * sx1;
-  return ra + rb;
-}
-
-// row_unit_dot_r in the cheaper decode (lo0 / lo1 used by Q4_0 only)
-template <int TQ>
-__device__ __forceinline__ float row_unit_dot_f(const uint32_t *row, int p, const uint32_t *xv, float sx0, float sx1,
-                                                float lo0, float lo1) {
-  if (TQ == LMOE_Q4_0) {
-    uint32_t u[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) u[i] = row[9 * p + i];
-    return unit_dot_q4_0_f(u, xv, sx0, sx1, lo0, lo1);
-  } else {
-    const uint32_t *sb = row + 36 * (p >> 2);
-    const int c = p & 3;
-    uint32_t hdr[4], q[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hdr[i] = sb[i];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[i] = sb[4 + 8 * c + i];
-    return unit_dot_q4_k_f(hdr, q, c, xv, sx0, sx1);
-  }
 }
 
 // ---- preparing activation rows -----------------------------------------------------------------------------------

@@ -11,6 +11,7 @@
 // probabilities of the picked experts (max-subtracted, fp32), renormalised when asked.
 #include "lmoe_common.h"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace lmoe {
@@ -159,6 +160,109 @@ static void launch_router(int qt, dim3 grid, dim3 block, hipStream_t st, const v
     launch_router_q<WDT, LMOE_Q4_0>(grid, block, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
 }
 
+
+// ---- router GEMV and top-k in one launch ------------------------------------------------------------------------
+//
+// Workgroup g < NR computes router rows [8 g, 8 g + 8) (row E: the shared-expert gate) for every token, each row in
+// exactly k_router_gemv's order (thread i holds items i, i + 256, ...; a wavefront tree; the four wavefronts' totals
+// left to right), so the logits are bit-for-bit those of lmoe_router_gemv. It then counts itself in on a device
+// counter (release); the workgroup that arrives last (acquire) ranks each token's logits, writes ids / scores, and
+// resets the counter for the next launch. Nobody waits on anybody: with NR = ceil((E + 1) / 8) workgroups the
+// counter sees ~17 arrivals for E 128 instead of a kernel boundary and a top-k in every gate/up wavefront.
+// Workgroups past NR write the prepared activation rows, as in k_router_gemv.
+// ks: slots a token in ids / scores (k, or k + 1 with a shared expert folded in as slot k: id E, weight
+// sigmoid(gate logit)). sync: a device counter, zero before the first launch, left zero by every launch.
+template <int WDT, int TQ, int NI, int kRankRows>
+__global__ void __launch_bounds__(256)
+    k_router_rank(const void *x, int xdt, const void *wr, const void *wsg, int T, int H, int E, int k, int norm,
+                  int ks, float *logits, uint32_t *ids, float *scores, uint32_t *xprep, uint32_t *sync, int nr) {
+  constexpr int WQ = WDT == LMOE_F32 ? 2 : 1;
+  __shared__ float part[kRankRows][4];
+  __shared__ float xu[4][64];
+  __shared__ int last;
+  __shared__ __attribute__((aligned(16))) RankScratch rs;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rows = E + (wsg != nullptr ? 1 : 0);
+  const int nit = H / 8;
+  if (int(blockIdx.x) >= nr) {  // a prepared-activation workgroup: one unit a wavefront
+    const int P = H / 64;
+    const int u = (blockIdx.x - nr) * 4 + wave;
+    if (u >= T * P) return;
+    const int t = u / P, p = u - t * P;
+    xu[wave][lane] = load_elt(x, size_t(t) * H + 64 * p + lane, xdt);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < XS) xprep[size_t(u) * XS + lane] = prep_dword<TQ>([&](int i) { return xu[wave][i]; }, 0, lane);
+    return;
+  }
+  const int r0 = blockIdx.x * kRankRows;
+  float wv[kRankRows][NI][8];
+#pragma unroll
+  for (int r = 0; r < kRankRows; ++r) {
+    const int row = min(r0 + r, rows - 1);
+    const u32x4 *w4 = reinterpret_cast<const u32x4 *>(
+        row < E ? static_cast<const char *>(wr) + size_t(row) * H * (WDT == LMOE_F32 ? 4 : 2)
+                : static_cast<const char *>(wsg));
+    u32x4 wq[NI][2];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int it = min(tid + 256 * i, nit - 1);
+#pragma unroll
+      for (int q = 0; q < WQ; ++q) wq[i][q] = __builtin_nontemporal_load(w4 + it * WQ + q);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) unpack8(wq[i][0], wq[i][WQ - 1], WDT, wv[r][i]);
+  }
+  const int xq = xdt == LMOE_F32 ? 2 : 1;
+  for (int t = 0; t < T; ++t) {
+    const u32x4 *x4 = reinterpret_cast<const u32x4 *>(static_cast<const char *>(x) +
+                                                      size_t(t) * H * (xdt == LMOE_F32 ? 4 : 2));
+    float xv[NI][8];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int it = min(tid + 256 * i, nit - 1);
+      unpack8(x4[it * xq], x4[it * xq + xq - 1], xdt, xv[i]);
+    }
+#pragma unroll
+    for (int r = 0; r < kRankRows; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        if (tid + 256 * i >= nit) continue;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf(xv[i][e], wv[r][i][e], acc);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) part[r][wave] = acc;
+    }
+    __syncthreads();
+    if (tid < kRankRows && r0 + tid < rows)
+      logits[size_t(t) * rows + r0 + tid] = ((part[tid][0] + part[tid][1]) + part[tid][2]) + part[tid][3];
+    __syncthreads();
+  }
+  // count in; the last workgroup ranks
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(sync, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == uint32_t(nr - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (tid == 0) __hip_atomic_store(sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int t = 0; t < T; ++t) {
+    for (int e = tid; e < rows; e += 256) rs.vals[e] = logits[size_t(t) * rows + e];
+    __syncthreads();
+    const float p = rank256(rs, E, k, norm, tid);
+    if (tid < k) {
+      ids[size_t(t) * ks + tid] = rs.pick[tid];
+      scores[size_t(t) * ks + tid] = p;
+    }
+    if (tid == 0 && ks > k) {
+      ids[size_t(t) * ks + k] = uint32_t(E);
+      scores[size_t(t) * ks + k] = sigmoidf_(rs.vals[E]);
+    }
+    __syncthreads();
+  }
+}
 
 // ---- cache-biased route (route_cuda.route / bias_probs) -------------------------------------------------------
 //
@@ -606,6 +710,79 @@ extern "C" int lmoe_route_bias(const void *gates, int gdtype, int T, int E, int 
     by_npl(std::integral_constant<int, LMOE_F16>());
   else
     by_npl(std::integral_constant<int, LMOE_F32>());
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+// Router rows a workgroup of k_router_rank: 1, 2, 4 or 8. More rows a workgroup mean fewer arrivals on the counter
+// but less memory parallelism for the GEMV. LMOE_RANK_ROWS overrides the choice.
+static int rank_rows(int rows) {
+  static const int forced = [] {
+    const char *v = getenv("LMOE_RANK_ROWS");
+    const int n = v ? atoi(v) : 0;
+    return (n == 1 || n == 2 || n == 4 || n == 8) ? n : 0;
+  }();
+  if (forced) return forced;
+  return rows <= 160 ? 2 : 4;
+}
+
+extern "C" int lmoe_router_gemv_rank(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T,
+                                     int H, int E, int k, int norm, int ks, float *logits, uint32_t *ids,
+                                     float *scores, uint32_t *xprep, int qtype, uint32_t *sync, void *stream) {
+  const char *fn = "lmoe_router_gemv_rank";
+  LMOE_REQUIRE(dtype_ok(xdtype) && dtype_ok(wdtype), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(T > 0 && T <= kRouterMaxT, LMOE_ESHAPE, "%s: %d tokens is outside 1..%d", fn, T, kRouterMaxT);
+  LMOE_REQUIRE(H > 0 && H % 64 == 0 && H <= 8 * 256 * kRouterMaxNi, LMOE_ESHAPE, "%s: hidden %d", fn, H);
+  LMOE_REQUIRE(E > 0 && E <= kRankMaxE && k > 0 && k <= kRankMaxK && k <= E, LMOE_ESHAPE,
+               "%s: top-%d of %d experts (E <= %d, k <= %d)", fn, k, E, kRankMaxE, kRankMaxK);
+  LMOE_REQUIRE(ks == k || (ks == k + 1 && wsg), LMOE_EINVAL, "%s: %d slots a token for top-%d", fn, ks, k);
+  LMOE_REQUIRE(!xprep || qtype_ok(qtype), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn,
+               qtype);
+  LMOE_REQUIRE(x && wr && logits && ids && scores && sync, LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(aligned16(x) && aligned16(wr) && (!wsg || aligned16(wsg)), LMOE_EALIGN,
+               "%s: x, wr and wsg must be 16-byte aligned", fn);
+  const int rows = E + (wsg ? 1 : 0);
+  const int rr = rank_rows(rows);
+  const int nr = (rows + rr - 1) / rr;
+  const dim3 grid(nr + (xprep ? (T * (H / 64) + 3) / 4 : 0)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  const int ni = (H / 8 + 255) / 256;
+  auto go = [&](auto wdc, auto tqc) {
+    constexpr int WD = decltype(wdc)::value, TQ = decltype(tqc)::value;
+    auto by_rr = [&](auto nic) {
+      constexpr int NI = decltype(nic)::value;
+      auto run = [&](auto kern) {
+        launch(kern, grid, block, 0, st, x, xdtype, wr, wsg, T, H, E, k, norm, ks, logits, ids, scores, xprep, sync,
+               nr);
+      };
+      if (rr == 1)
+        run(k_router_rank<WD, TQ, NI, 1>);
+      else if (rr == 2)
+        run(k_router_rank<WD, TQ, NI, 2>);
+      else if (rr == 4)
+        run(k_router_rank<WD, TQ, NI, 4>);
+      else
+        run(k_router_rank<WD, TQ, NI, 8>);
+    };
+    if (ni <= 1)
+      by_rr(std::integral_constant<int, 1>());
+    else if (ni <= 2)
+      by_rr(std::integral_constant<int, 2>());
+    else
+      by_rr(std::integral_constant<int, 4>());
+  };
+  auto by_q = [&](auto wdc) {
+    if (qtype == LMOE_Q4_K)
+      go(wdc, std::integral_constant<int, LMOE_Q4_K>());
+    else
+      go(wdc, std::integral_constant<int, LMOE_Q4_0>());
+  };
+  if (wdtype == LMOE_F16)
+    by_q(std::integral_constant<int, LMOE_F16>());
+  else if (wdtype == LMOE_BF16)
+    by_q(std::integral_constant<int, LMOE_BF16>());
+  else
+    by_q(std::integral_constant<int, LMOE_F32>());
   LMOE_LAUNCHED(fn);
   return 0;
 }

@@ -160,23 +160,6 @@ __device__ __forceinline__ float f16f(uint32_t bits16) {
   return float(__builtin_bit_cast(_Float16, uint16_t(bits16)));
 }
 
-// Entries of ck[f0, f0 + 2 N) (composite keys, 16-byte aligned) above `me`. Composite key: order-preserving logit
-// key in the high half, 0xFFFFFFFF - expert in the low half, so a larger composite is the better pick (larger logit,
-// or equal logit and lower index) and no two experts tie; 0 pads an empty slot below every expert.
-template <int N>
-__device__ __forceinline__ int count_above(const uint64_t *ck, int f0, uint64_t me) {
-  typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
-  const u64x2 *p = reinterpret_cast<const u64x2 *>(ck + f0);
-  int c = 0;
-#pragma unroll
-  for (int j = 0; j < N; ++j) {
-    const u64x2 v = p[j];
-    const uint64_t v0 = v.x, v1 = v.y;
-    c += (v0 > me ? 1 : 0) + (v1 > me ? 1 : 0);
-  }
-  return c;
-}
-
 // (ids, scores) of the top k of the E logits in LDS (vals), into pick / psc (k entries, best first).
 // ck: 512 u64, cnt: 2048 u32, surv: 128 u64, praw: KMAX floats, red: 8 floats of LDS scratch. All threads; ends
 // with a barrier. E <= 128: each of the 512 threads counts, for candidate t % 128, the candidates above it among one
@@ -457,13 +440,7 @@ __global__ void __launch_bounds__(stk::NT, 1) k_stack(stk::Args a) {
     // prepared x units (pairs in nibble order + half sums), then this lane's unit into registers
     for (int idx = tid; idx < 36 * P; idx += NT) {
       const int p = idx / 36, dw = idx - p * 36;
-      if (TQ == LMOE_Q4_0 && dw >= 34) {  // the sums over the unit's values [0, 16) and [32, 48)
-        float sm = 0.0f;
-        for (int i = 0; i < 16; ++i) sm += f16f(xraw[64 * p + 32 * (dw - 34) + i]);
-        xprep[idx] = __float_as_uint(sm);
-      } else {
-        xprep[idx] = prep_dword<TQ>([&](int i) { return f16f(xraw[i]); }, p, dw);
-      }
+      xprep[idx] = prep_dword<TQ>([&](int i) { return f16f(xraw[i]); }, p, dw);
     }
 
     // ---- B. logits -> top-k ------------------------------------------------------------------------------
@@ -524,7 +501,6 @@ __global__ void __launch_bounds__(stk::NT, 1) k_stack(stk::Args a) {
       }
       const u32x4 sv = reinterpret_cast<const u32x4 *>(xprep)[9 * p + 8];
       const float sx0 = __uint_as_float(sv.x), sx1 = __uint_as_float(sv.y);
-      const float lo0 = __uint_as_float(sv.z), lo1 = __uint_as_float(sv.w);
       const uint32_t *st = reinterpret_cast<const uint32_t *>(stage);
       u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
       const int R2 = 2 * np;
@@ -539,7 +515,7 @@ __global__ void __launch_bounds__(stk::NT, 1) k_stack(stk::Args a) {
         have = lim;
         __syncthreads();
         const int r = min(r0 + g, R2 - 1);
-        const float d = group_sum<P>(row_unit_dot_f<TQ>(st + r * (RBH / 4), p, xu, sx0, sx1, lo0, lo1));
+        const float d = group_sum<P>(row_unit_dot_r<TQ>(st + r * (RBH / 4), p, xu, sx0, sx1));
         if (p == 0 && r0 + g < R2) rowdot[r0 + g] = d;
       }
     }
@@ -565,26 +541,17 @@ __global__ void __launch_bounds__(stk::NT, 1) k_stack(stk::Args a) {
       }
     }
     __syncthreads();
-    // a unit's sums: over its first / last 32 values (dwords 32, 33) and, for Q4_0, over values [0, 16) and [32, 48)
-    // (the even dwords of each 16-dword half: dwords 34, 35)
-    for (int hu = tid; hu < 4 * Utot; hu += NT) {
-      const int U = hu >> 2, which = hu & 3;
+    // a unit's sums over its first / last 32 values (dwords 32, 33)
+    for (int hu = tid; hu < 2 * Utot; hu += NT) {
+      const int U = hu >> 1, half = hu & 1;
       const uint32_t *u = hprep + U * XS;
       float s = 0.0f;
-      if (which < 2) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const uint32_t w = TQ == LMOE_Q4_K ? u[2 * i + which] : u[16 * which + i];
-          s += half_lo(w) + half_hi(w);
-        }
-      } else if (TQ == LMOE_Q4_0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t w = u[16 * (which - 2) + 2 * i];
-          s += half_lo(w) + half_hi(w);
-        }
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t w = TQ == LMOE_Q4_K ? u[2 * i + half] : u[16 * half + i];
+        s += half_lo(w) + half_hi(w);
       }
-      hprep[U * XS + 32 + which] = __builtin_bit_cast(uint32_t, s);
+      hprep[U * XS + 32 + half] = __builtin_bit_cast(uint32_t, s);
     }
     // the down weights into the stage (gate/up's reads of it ended at the barrier above)
     {
@@ -627,8 +594,7 @@ __global__ void __launch_bounds__(stk::NT, 1) k_stack(stk::Args a) {
             hv[4 * i + 3] = v.w;
           }
           const u32x4 sv = reinterpret_cast<const u32x4 *>(hu)[8];
-          const float d = row_unit_dot_f<TQ>(row, j, hv, __uint_as_float(sv.x), __uint_as_float(sv.y),
-                                             __uint_as_float(sv.z), __uint_as_float(sv.w));
+          const float d = row_unit_dot_r<TQ>(row, j, hv, __uint_as_float(sv.x), __uint_as_float(sv.y));
           const float wt = s < k ? psc[s] : gsh;
           acc = (u0 + lane < Utot) ? fmaf(wt, d, acc) : acc;
         }

@@ -4,10 +4,11 @@ The layer is the reference block's sequence (stream_fast.py:4352-4377 over gguf_
 gguf_experts.py:803-819): router logits x . Wr, softmax top-k, the k experts' SwiGLU chains read straight from
 GGUF blocks, the weighted combine, and a sigmoid-gated shared expert when the model has one. Two drivers:
 
-  * decode (T <= 16 tokens): router GEMV (which also writes x prepared for the expert kernels) -> top-k fused
-    into gate/up + SwiGLU (writing h prepared for down) [-> the shared expert's gate/up and down] -> down +
-    weighted combine + shared expert + residual in one kernel; 3 launches a layer without a shared expert, no
-    host synchronisation, every buffer preallocated so a whole step can be captured in a HIP graph;
+  * decode (T <= 16 tokens): router GEMV + top-k in one kernel (which also writes x prepared for the expert
+    kernels; its last workgroup ranks the logits) -> gate/up + SwiGLU on the picked experts (writing h prepared for
+    down) [-> the shared expert's gate/up and down] -> down + weighted combine + shared expert + residual in one
+    kernel; 3 launches a layer without a shared expert, no host synchronisation, every buffer preallocated so a
+    whole step can be captured in a HIP graph;
   * prefill / batched decode (any T): the device grouping and the grouped MFMA GEMMs (larder_amd.grouped).
 """
 import ctypes
@@ -16,6 +17,13 @@ import torch
 
 from . import _lib
 from ._lib import call, dcode, ptr, qcode, stream
+
+# Where a decode layer ranks its router logits. False (the default): inside gate/up, one rank a workgroup (the router
+# GEMV keeps one router row a workgroup, its widest form). True: in the router kernel's last workgroup
+# (lmoe_router_gemv_rank), which needs fewer, wider router workgroups; measured on cfg2 in a HIP graph it is the
+# slower of the two (17.1 against 15.7 us a layer), so it stays off.
+RANKED_ROUTER = False
+RANK_MAX_E, RANK_MAX_K = 512, 16  # the router-and-rank kernel's limits
 
 
 class MoELayer:
@@ -89,6 +97,8 @@ class DecodeBuffers:
         self.ids_ext = torch.empty((T, ks), **u32)
         self.scores_ext = torch.empty((T, ks), **f32)
         self.ids, self.scores = self.ids_ext[:, :L.k], self.scores_ext[:, :L.k]
+        # the router-and-rank kernel's arrival counter (zero between launches; one a stream)
+        self.sync = torch.zeros(1, **u32)
         # prepared rows (36 dwords a 64-value unit): x for the gate / up type, h for the down type
         self.xprep = torch.empty((T, L.H // 64 * 36), **u32)
         self.xprep_u = torch.empty((T, L.H // 64 * 36), **u32) if L.types[1] != L.types[0] else None
@@ -109,11 +119,19 @@ def decode(layer, x, bufs, out, residual=None, logits=None):
     st = stream()
     tg, tu, td = (qcode(t) for t in L.types)
     xd = dcode(x.dtype)
+    ranked = False
     if logits is None:
         if L.wr is None:
             raise ValueError("this layer has no router weight: pass logits")
-        call("lmoe_router_gemv", ptr(x), xd, ptr(L.wr), ptr(L.wsg), dcode(L.wr.dtype), T, L.H, L.E, ptr(B.logits),
-             ptr(B.xprep), tg, st)
+        if RANKED_ROUTER and L.E <= RANK_MAX_E and L.k <= RANK_MAX_K:
+            # router GEMV and top-k in one launch: ids / scores (with the folded shared expert's slot) come out of it
+            call("lmoe_router_gemv_rank", ptr(x), xd, ptr(L.wr), ptr(L.wsg), dcode(L.wr.dtype), T, L.H, L.E, L.k,
+                 int(L.norm), B.ids_ext.shape[1], ptr(B.logits), ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.xprep), tg,
+                 ptr(B.sync), st)
+            ranked = True
+        else:
+            call("lmoe_router_gemv", ptr(x), xd, ptr(L.wr), ptr(L.wsg), dcode(L.wr.dtype), T, L.H, L.E,
+                 ptr(B.logits), ptr(B.xprep), tg, st)
         lg, stride = B.logits, B.logits.shape[1]
     else:
         if L.shared is not None:
@@ -126,14 +144,22 @@ def decode(layer, x, bufs, out, residual=None, logits=None):
         xu = B.xprep_u
     if L.folded is not None:  # the shared expert as slot k of every token: gate/up, then down + combine
         fg, fu, fd = L.folded
-        call("lmoe_moe_gate_up_ext", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(xu), ptr(fg), ptr(fu),
-             tg, tu, L.E, L.H, L.I, ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.hprep), td, 1, st)
+        if ranked:
+            call("lmoe_gemv_gate_up_prepped", ptr(B.xprep), ptr(xu), ptr(B.ids_ext), T * (L.k + 1), L.k + 1,
+                 ptr(fg), ptr(fu), tg, tu, L.E + 1, L.H, L.I, None, ptr(B.hprep), td, st)
+        else:
+            call("lmoe_moe_gate_up_ext", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(xu), ptr(fg),
+                 ptr(fu), tg, tu, L.E, L.H, L.I, ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.hprep), td, 1, st)
         call("lmoe_gemv_down_combine_prepped", ptr(B.hprep), 0, ptr(B.ids_ext), ptr(B.scores_ext), T, L.k + 1,
              ptr(fd), td, L.E + 1, L.I, L.H, None, None, 0, ptr(residual),
              dcode(residual.dtype) if residual is not None else 0, ptr(out), dcode(out.dtype), st)
         return out
-    call("lmoe_moe_gate_up", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(xu), ptr(L.wg), ptr(L.wu), tg,
-         tu, L.E, L.H, L.I, ptr(B.ids), ptr(B.scores), ptr(B.hprep), td, st)
+    if ranked:
+        call("lmoe_gemv_gate_up_prepped", ptr(B.xprep), ptr(xu), ptr(B.ids_ext), T * L.k, L.k, ptr(L.wg),
+             ptr(L.wu), tg, tu, L.E, L.H, L.I, None, ptr(B.hprep), td, st)
+    else:
+        call("lmoe_moe_gate_up", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(xu), ptr(L.wg), ptr(L.wu),
+             tg, tu, L.E, L.H, L.I, ptr(B.ids), ptr(B.scores), ptr(B.hprep), td, st)
     shared_y = gptr = None
     gate_stride = 0
     if L.shared is not None:

@@ -72,9 +72,13 @@ def test_cfg5_decode_T1():
     lay.decode(L, x, B, out)
     torch.cuda.synchronize()
     xs = host(x.float())
-    lg = host(B.logits)[:, :cfg["E"]]
-    assert moe.rel_l2(lg, xs @ host(L.wr.float()).T) < 1e-5
-    ids, want = _oracle_subset(L, xs, lg, cfg)
+    # routing pinned from x: the router GEMV's fixed order restated, bit for bit, then the oracle's own top-k
+    want_lg = moe.router_logits_gemv(host(x), host(L.wr))
+    lg = host(B.logits)
+    assert np.array_equal(lg[:, :cfg["E"]].view(np.uint32), want_lg.view(np.uint32))
+    want_gate = moe.router_logits_gemv(host(x), host(L.wsg).reshape(1, -1))
+    assert np.array_equal(lg[:, cfg["E"]:].view(np.uint32), want_gate.view(np.uint32))
+    ids, want = _oracle_subset(L, xs, want_lg, cfg)
     assert (host(B.ids).astype(np.uint32) == ids).all()
     assert moe.rel_l2(host(out), want) < BAR
 

@@ -193,10 +193,12 @@ def test_decode_layer_cfg1_vs_oracle(T):
     torch.cuda.synchronize()
     xs = host(x.float())
     lg_gpu = host(B.logits)
-    lg_ref = xs @ host(L.wr.float()).T
-    assert moe.rel_l2(lg_gpu[:, :cfg["E"]], lg_ref) < 1e-5
-    assert moe.rel_l2(lg_gpu[:, cfg["E"]], xs @ host(L.wsg.float())) < 1e-5
-    ids, _, want = moe.layer(xs, lg_gpu[:, :cfg["E"]], tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"],
+    # routing pinned from x: the router GEMV's fixed order restated bit for bit, ids from the oracle's own logits
+    lg_ref = moe.router_logits_gemv(host(x), host(L.wr))
+    assert np.array_equal(lg_gpu[:, :cfg["E"]].view(np.uint32), lg_ref.view(np.uint32))
+    gate_ref = moe.router_logits_gemv(host(x), host(L.wsg).reshape(1, -1))
+    assert np.array_equal(lg_gpu[:, cfg["E"]:].view(np.uint32), gate_ref.view(np.uint32))
+    ids, _, want = moe.layer(xs, lg_ref, tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"],
                              cfg["k"], cfg["norm"], shared=tuple(host(b[0]) for b in L.shared),
                              shared_gate_w=host(L.wsg.float()))
     assert (host(B.ids).astype(np.uint32) == ids).all()
@@ -214,7 +216,8 @@ def test_decode_layer_cfg2_residual():
     lay.decode(L, x, B, out, residual=x)
     torch.cuda.synchronize()
     xs = host(x.float())
-    lg = host(B.logits)
+    lg = moe.router_logits_gemv(host(x), host(L.wr))  # routing pinned from x, bit for bit
+    assert np.array_equal(host(B.logits).view(np.uint32), lg.view(np.uint32))
     ids, _, want = moe.layer(xs, lg, tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"], cfg["k"],
                              cfg["norm"], residual=xs)
     assert (host(B.ids).astype(np.uint32) == ids).all()
@@ -283,3 +286,51 @@ def test_tail_combine_vs_oracle():
     got = route.tail(dev(y), dev(sc), dev(sh), dev(gt))
     want = moe.combine(y[0], sc[0], sh[0], gt[0, :, 0])
     assert moe.rel_l2(host(got)[0], want) < 1e-6
+
+
+@pytest.mark.parametrize("E,k,norm,T,shared,H", [(60, 4, False, 1, True, 2048), (128, 8, True, 1, False, 2048),
+                                                  (128, 8, True, 5, False, 2048), (512, 10, True, 1, True, 4096),
+                                                  (512, 16, False, 3, False, 2048), (9, 9, True, 2, False, 2048),
+                                                  (256, 8, True, 16, True, 4096), (129, 7, True, 4, False, 2048)])
+def test_router_gemv_rank_vs_oracle(E, k, norm, T, shared, H):
+    """lmoe_router_gemv_rank (GEMV + top-k in one launch, the last workgroup ranking): logits bit-exact against the
+    router GEMV's restated order, ids bit-exact against the oracle's top-k of those logits (planted equal rows: ties
+    to the lowest index), scores to 2e-6, the folded shared expert's slot, and a second launch on the same arrival
+    counter giving the same bits."""
+    from larder_amd import _lib
+    rng = np.random.default_rng(E * 31 + k * 7 + T)
+    wr = (rng.standard_normal((E, H)) * 0.02).astype(np.float16)
+    for grp in (rng.choice(E, min(4, E), replace=False), rng.choice(E, min(3, E), replace=False)):
+        wr[grp] = wr[grp[0]] * np.float16(3)              # equal rows: exactly equal logits
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    wsg = (rng.standard_normal(H) * 0.02).astype(np.float16) if shared else None
+    ks = k + 1 if shared else k
+    rows = E + (1 if shared else 0)
+    dx, dwr = dev(x), dev(wr)
+    dwsg = dev(wsg) if shared else None
+    sync = torch.zeros(1, dtype=torch.int32, device="cuda")
+    outs = []
+    for _ in range(2):
+        lg = torch.full((T, rows), float("nan"), device="cuda")
+        ids = torch.full((T, ks), -1, dtype=torch.int32, device="cuda")
+        sc = torch.full((T, ks), float("nan"), device="cuda")
+        xp = torch.empty((T, H // 64 * 36), dtype=torch.int32, device="cuda")
+        _lib.call("lmoe_router_gemv_rank", _lib.ptr(dx), _lib.F16, _lib.ptr(dwr), _lib.ptr(dwsg), _lib.F16, T, H, E, k,
+                  int(norm), ks, _lib.ptr(lg), _lib.ptr(ids), _lib.ptr(sc), _lib.ptr(xp), _lib.Q4_0, _lib.ptr(sync),
+                  _lib.stream())
+        torch.cuda.synchronize()
+        outs.append((host(lg), host(ids), host(sc)))
+    assert int(sync.item()) == 0
+    lg, ids, sc = outs[0]
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    want_lg = moe.router_logits_gemv(x, wr)
+    assert np.array_equal(lg[:, :E].view(np.uint32), want_lg.view(np.uint32))
+    want_ids, want_sc = moe.router(want_lg, k, norm)
+    assert (ids[:, :k].astype(np.uint32) == want_ids).all()
+    assert np.allclose(sc[:, :k], want_sc, rtol=2e-6, atol=1e-7)
+    if shared:
+        gate = moe.router_logits_gemv(x, wsg.reshape(1, -1))
+        assert np.array_equal(lg[:, E:].view(np.uint32), gate.view(np.uint32))
+        assert (ids[:, k] == E).all()
+        assert np.allclose(sc[:, k], moe.sigmoid(gate[:, 0]), rtol=1e-6)
