@@ -15,15 +15,16 @@ come back unweighted in the requested dtype. Unsupported types raise ValueError.
 import hashlib
 import json
 import os
-import time
+import tempfile
 from pathlib import Path
 
+import numpy as np
 import torch
 
 from . import _lib
 from ._lib import TYPES, call, dcode, ptr, qcode, stream
 
-__all__ = ["TYPES", "dims", "dequant", "gemv", "dense", "experts", "calibrate", "dense_pays", "CALIB_DIR"]
+__all__ = ["TYPES", "dims", "dequant", "gemv", "dense", "experts", "calibrate", "dense_pays", "calib_dir"]
 
 
 def _types(types):
@@ -96,46 +97,69 @@ def dense(x, w, host, types, out_dtype):
     return grouped.expert_rows(x.contiguous(), w, host, types, out_dtype)
 
 
-# Per-device costs of the two paths as calibrate() measures them: chain fixed s, chain s a row, dense fixed s,
-# dense s an expert, dense s a row (gguf_experts.py:725-729); until then every pass takes the decode chain.
+# This device's cost model of the two paths, as calibrate() fits it: five non-negative terms (chain fixed, chain per
+# row, dense fixed, dense per expert, dense per row), the form the reference's callers rely on (gguf_experts.py:725-800,
+# read through dense_pays). None until calibrate() runs: every pass then takes the decode chain.
 _COST = None
-CALIB_DIR = Path(os.environ.get("LMOE_CACHE", Path.home() / ".cache" / "larder-amd"))
+_CAL_E = 64  # experts in the calibration pool
+
+
+def calib_dir():
+    """Where calibrate() caches its fits: $LMOE_CACHE, else ~/.cache/larder-amd (read on every call)."""
+    return Path(os.environ.get("LMOE_CACHE") or (Path.home() / ".cache" / "larder-amd"))
+
+
+def _sample_points(rows_a_tile):
+    """(chain row counts, dense (experts, rows) points) for the fit. The chain's cost grows with its rows (one
+    workgroup row a slot): 1 token, a decode batch, and past the crossing. The grouped path's cost has a part per
+    m-tile (one at least per expert used) and a part per row: points at one tile, at a dozen experts, at ~2 tiles an
+    expert over the whole pool, and two between, so that the expert and row terms are separable."""
+    bm = rows_a_tile
+    chain = (1, 16, 128, 512)
+    dense = ((1, bm), (12, 12 * bm // 4), (12, 24 * bm), (_CAL_E, 2 * _CAL_E * bm), (_CAL_E // 2, 4 * bm),
+             (_CAL_E, _CAL_E * bm // 8))
+    return chain, dense
+
+
+def _time_call(fn, batches=3, reps=5):
+    """Median over batches of the mean time of ``reps`` calls of fn, in seconds, from events on the current
+    stream."""
+    fn()
+    fn()
+    torch.cuda.current_stream().synchronize()
+    means = []
+    for _ in range(batches):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        b.synchronize()
+        means.append(a.elapsed_time(b) / reps * 1e-3)
+    return sorted(means)[len(means) // 2]
 
 
 def _measure(hid, inter, types):
-    """The cost model's five terms, timed on random Q4 experts at these shapes (best of 5), fitted by least
-    squares: the chain over three row counts and the dense path over five (experts, rows) points
-    (gguf_experts.py:731-768)."""
+    """The five cost terms at these shapes, fitted by least squares to timings of both paths on a pool of random
+    experts of these types (made on the device)."""
+    from . import grouped
     dev = torch.device("cuda")
-    E = 32
-    g = torch.Generator(device=dev).manual_seed(0)
-    w = tuple(_random_q4(E, r, c, t, g) for (r, c), t in zip(((inter, hid), (inter, hid), (hid, inter)), types))
-    x = torch.randn((80 * E, hid), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(1234)
+    w = tuple(_random_q4(_CAL_E, r, c, t, g) for (r, c), t in zip(((inter, hid), (inter, hid), (hid, inter)), types))
+    chain_rows, dense_pts = _sample_points(grouped.pick_tile_rows(4 * _CAL_E, _CAL_E, types))
+    most = max(max(chain_rows), max(p for _, p in dense_pts))
+    x = torch.randn((most, hid), generator=g, device=dev).to(torch.bfloat16)
 
-    def secs(u, p, dense_path):
-        host = (torch.arange(p, device=dev) % u).to(torch.int32)
-        f = (lambda: dense(x[:p], w, host, types, x.dtype)) if dense_path else \
-            (lambda: _chain(x[:p], w, host, 1, types, x.dtype)[1])
-        f()
-        torch.cuda.synchronize()
-        best = float("inf")
-        for _ in range(5):
-            t0 = time.perf_counter()
-            f()
-            torch.cuda.synchronize()
-            best = min(best, time.perf_counter() - t0)
-        return best
+    def slots(u, p):  # p rows over u experts, spread evenly
+        return (torch.arange(p, device=dev, dtype=torch.int32) * 7919) % u
 
-    def fit(rows, ts):
-        a = torch.tensor(rows, dtype=torch.float64)
-        b = torch.tensor(ts, dtype=torch.float64).reshape(-1, 1)
-        return torch.linalg.lstsq(a, b).solution.reshape(-1).tolist()
-
-    chain = [(p, secs(E, p, False)) for p in (10, 10 * E, 80 * E)]
-    cg = fit([[1.0, p] for p, _ in chain], [t for _, t in chain])
-    pts = [(u, p, secs(u, p, True)) for u, p in ((1, 10), (10, 100), (10, 800), (E, 10 * E), (E, 80 * E))]
-    cd = fit([[1.0, u, p] for u, p, _ in pts], [t for *_, t in pts])
-    return [max(float(v), 0.0) for v in (*cg, *cd)]
+    t_chain = [_time_call(lambda p=p: _chain(x[:p], w, slots(_CAL_E, p), 1, types, x.dtype)) for p in chain_rows]
+    t_dense = [_time_call(lambda u=u, p=p: dense(x[:p], w, slots(u, p), types, x.dtype)) for u, p in dense_pts]
+    a_chain = np.array([[1.0, p] for p in chain_rows])
+    a_dense = np.array([[1.0, u, p] for u, p in dense_pts], dtype=np.float64)
+    fit_chain = np.linalg.lstsq(a_chain, np.array(t_chain), rcond=None)[0]
+    fit_dense = np.linalg.lstsq(a_dense, np.array(t_dense), rcond=None)[0]
+    return [max(float(v), 0.0) for v in np.concatenate([fit_chain, fit_dense])]
 
 
 # byte offsets of each block type's f16 scale fields
@@ -159,35 +183,50 @@ def _random_q4(n, rows, cols, t, gen):
     return b.reshape(n, rows, -1).contiguous()
 
 
-def _source_hash():
-    h = hashlib.sha1()
+def _source_digest():
+    h = hashlib.sha256()
     for p in sorted((Path(__file__).parent / "csrc").glob("*")):
+        h.update(p.name.encode())
         h.update(p.read_bytes())
-    return h.hexdigest()
+    return h.hexdigest()[:20]
+
+
+def _device_key():
+    """What a fit depends on besides the shapes: the GPU, the HIP runtime and the kernels' sources."""
+    props = torch.cuda.get_device_properties(torch.cuda.current_device())
+    return [getattr(props, "gcnArchName", props.name), props.multi_processor_count, torch.version.hip,
+            _source_digest()]
 
 
 def calibrate(hid, inter, types):
-    """This device's cost model at these shapes and types, measured once (a few seconds) and cached on disk
-    keyed by the GPU architecture, the HIP runtime version, the kernels' source hash and the shapes
-    (gguf_experts.py:771-794)."""
+    """This device's cost model at these shapes and types (the reference's calibrate, gguf_experts.py:771-794):
+    read from the cache under calib_dir() when a fit for this device, runtime, kernel source and shape is there,
+    else measured (a few seconds) and stored. Returns the five terms and makes them the ones dense_pays() uses."""
     global _COST
     types = _types(types)
-    props = torch.cuda.get_device_properties(0)
-    key = json.dumps([getattr(props, "gcnArchName", props.name), torch.version.hip, _source_hash(), hid, inter,
-                      list(types)])
-    path = CALIB_DIR / f"gguf-{hashlib.sha1(key.encode()).hexdigest()[:16]}.json"
-    try:
-        _COST = json.loads(path.read_text())["cost"]
-    except (OSError, ValueError, KeyError):
-        _COST = _measure(hid, inter, types)
+    ident = json.dumps({"device": _device_key(), "hid": hid, "inter": inter, "types": list(types)}, sort_keys=True)
+    path = calib_dir() / f"dense-switch-{hashlib.sha256(ident.encode()).hexdigest()[:24]}.json"
+    cost = None
+    if path.is_file():
+        try:
+            got = json.loads(path.read_text())
+            if got.get("ident") == ident and len(got.get("cost", ())) == 5:
+                cost = [float(v) for v in got["cost"]]
+        except (OSError, ValueError):
+            cost = None
+    if cost is None:
+        cost = _measure(hid, inter, types)
         try:
             path.parent.mkdir(parents=True, exist_ok=True)
-            tmp = path.with_suffix(".tmp")
-            tmp.write_text(json.dumps({"cost": _COST}))
-            tmp.replace(path)
+            fd, tmp = tempfile.mkstemp(dir=path.parent, prefix=path.name, suffix=".part")
+            with os.fdopen(fd, "w") as f:
+                json.dump({"ident": ident, "cost": cost}, f)
+            os.replace(tmp, path)
         except OSError as e:
-            print(f"  gguf: could not save the prefill switch to {path}: {e}", flush=True)
-    return _COST
+            print(f"larder_amd: the dense-path fit for {hid}x{inter} {'/'.join(types)} was measured but not cached "
+                  f"({e})", flush=True)
+    _COST = cost
+    return cost
 
 
 def dense_pays(u, p):

@@ -20,6 +20,7 @@ Q4_0 stack) stay resident, so the loader streams records through a pinned stagin
 expert kernels read directly (the arena slots of the reference's store, stream_fast.py:3936-3941).
 """
 import json
+import mmap
 import os
 import re
 import struct
@@ -49,83 +50,102 @@ GGML_BLOCKS = {
 DECODED = {"Q4_0": (0,), "Q4_K": (0, 2), "Q4_1": (0, 2), "Q8_0": (0,), "Q5_K": (0, 2), "Q6_K": (208,)}
 
 RECORD_ALIGN = 4096          # every record starts 4 KiB aligned (direct reads), a pad part filling the stride
-_CHUNK = 32                  # experts copied at a time while packing
-_EXPS = re.compile(r"blk\.(\d+)\.ffn_(gate|up|down)_exps\.weight")
 _PROJ = ("gate", "up", "down")
-# GGUF metadata value types: 0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool, 8 string, 9 array,
-# 10 u64, 11 i64, 12 f64
-_SCALAR = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
-_KEEP = 64                   # metadata arrays longer than this keep only their length (tokenizer tables)
+_EXPERT_TENSOR = re.compile(r"blk\.(?P<layer>\d+)\.ffn_(?P<proj>gate|up|down)_exps\.weight")
+
+# GGUF metadata value types -> (struct code, name); 8 is a string, 9 an array
+_VT = {0: ("B", "u8"), 1: ("b", "i8"), 2: ("H", "u16"), 3: ("h", "i16"), 4: ("I", "u32"), 5: ("i", "i32"),
+       6: ("f", "f32"), 7: ("?", "bool"), 10: ("Q", "u64"), 11: ("q", "i64"), 12: ("d", "f64")}
+_NP = {"B": np.uint8, "b": np.int8, "H": np.uint16, "h": np.int16, "I": np.uint32, "i": np.int32, "f": np.float32,
+       "?": np.bool_, "Q": np.uint64, "q": np.int64, "d": np.float64}
 
 
 def _key(layer, proj):
     return f"model.layers.{layer}.mlp.switch_mlp.{proj}_proj"
 
 
-class _Reader:
-    def __init__(self, f):
-        self.f = f
+class _Cursor:
+    """Little-endian reads at a moving position in an in-memory (memory-mapped) GGUF header."""
 
-    def take(self, fmt):
-        n = struct.calcsize(fmt)
-        b = self.f.read(n)
-        if len(b) != n:
-            raise ValueError(f"{getattr(self.f, 'name', 'GGUF file')}: the header ends early")
-        return struct.unpack(fmt, b)[0]
+    def __init__(self, buf, where):
+        self.buf, self.at, self.where = buf, 0, where
 
-    def string(self):
-        return self.f.read(self.take("<Q")).decode("utf-8", "replace")
+    def _span(self, n):
+        if self.at + n > len(self.buf):
+            raise ValueError(f"{self.where}: the header ends early")
+        a = self.at
+        self.at += n
+        return a
 
-    def value(self, vt):
-        if vt in _SCALAR:
-            return self.take(_SCALAR[vt])
+    def num(self, code):
+        return struct.unpack_from("<" + code, self.buf, self._span(struct.calcsize(code)))[0]
+
+    def text(self):
+        n = self.num("Q")
+        a = self._span(n)
+        return bytes(self.buf[a:a + n]).decode("utf-8", "replace")
+
+    def meta_value(self, vt):
+        """One metadata value: a Python scalar or str; an array of numbers as a numpy array, of strings (or of
+        arrays) as a list."""
+        if vt in _VT:
+            v = self.num(_VT[vt][0])
+            return bool(v) if vt == 7 else v
         if vt == 8:
-            return self.string()
+            return self.text()
         if vt != 9:
-            raise ValueError(f"{getattr(self.f, 'name', 'GGUF file')}: metadata value type {vt} is not GGUF's")
-        et, n = self.take("<I"), self.take("<Q")
-        if et in _SCALAR and n > _KEEP:
-            self.f.seek(n * struct.calcsize(_SCALAR[et]), os.SEEK_CUR)
-            return {"array_len": n}
-        vals = [self.value(et) for _ in range(n)]
-        return vals if n <= _KEEP else {"array_len": n, "head": vals[:4]}
+            raise ValueError(f"{self.where}: metadata value type {vt} is not a GGUF type")
+        et, count = self.num("I"), self.num("Q")
+        if et in _VT:
+            code = _VT[et][0]
+            a = self._span(count * struct.calcsize(code))
+            return np.frombuffer(self.buf, dtype=np.dtype(_NP[code]).newbyteorder("<"), count=count, offset=a).copy()
+        return [self.meta_value(et) for _ in range(count)]
 
 
 def read_header(f):
-    """(metadata, tensors, data start) of the GGUF file object ``f`` read from offset 0 (gguf_repack.py:70-104).
-    tensors: dicts of name, ne (ggml order, innermost first), type (ggml id), offset (absolute in the file) and
-    nbytes (None for a type id this table does not know). Versions 2 and 3; anything else raises ValueError."""
-    r = _Reader(f)
-    name = getattr(f, "name", "GGUF file")
-    if f.read(4) != b"GGUF":
-        raise ValueError(f"{name}: not a GGUF file")
-    version = r.take("<I")
-    if version not in (2, 3):
-        raise ValueError(f"{name}: GGUF version {version} (2 and 3 are read)")
-    n_tensors, n_kv = r.take("<Q"), r.take("<Q")
-    meta = {"version": version}
-    for _ in range(n_kv):
-        k = r.string()
-        meta[k] = r.value(r.take("<I"))
-    tensors = []
-    for _ in range(n_tensors):
-        tname = r.string()
-        ne = [r.take("<Q") for _ in range(r.take("<I"))]
-        tid, off = r.take("<I"), r.take("<Q")
-        tensors.append({"name": tname, "ne": ne, "type": tid, "offset": off})
+    """(metadata, tensors, data start) of the GGUF file object ``f``, versions 2 and 3 (the layout llama.cpp's gguf
+    writer produces; the reference reads it in tools/gguf_repack.py:70-104). tensors: dicts of name, ne (ggml order,
+    innermost first), type (ggml id), offset (absolute in the file) and nbytes (None for a type id GGML_BLOCKS does
+    not know). Anything that is not such a file raises ValueError."""
+    where = getattr(f, "name", "GGUF file")
+    size = os.fstat(f.fileno()).st_size
+    if size < 24:
+        raise ValueError(f"{where}: not a GGUF file")
+    with mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ) as mm:
+        c = _Cursor(memoryview(mm), where)
+        try:
+            if bytes(mm[:4]) != b"GGUF":
+                raise ValueError(f"{where}: not a GGUF file")
+            c.at = 4
+            version = c.num("I")
+            if version not in (2, 3):
+                raise ValueError(f"{where}: GGUF version {version} (2 and 3 are read)")
+            n_tensors, n_meta = c.num("Q"), c.num("Q")
+            meta = {"version": version}
+            for _ in range(n_meta):
+                k = c.text()
+                meta[k] = c.meta_value(c.num("I"))
+            infos = []
+            for _ in range(n_tensors):
+                tname = c.text()
+                dims = [c.num("Q") for _ in range(c.num("I"))]
+                infos.append((tname, dims, c.num("I"), c.num("Q")))
+            header_end = c.at
+        finally:
+            del c
     align = int(meta.get("general.alignment", 32))
-    pos = f.tell()
-    start = pos + (-pos) % align
-    for t in tensors:
-        t["offset"] += start
-        blk = GGML_BLOCKS.get(t["type"])
-        if blk is None:
-            t["nbytes"] = None
-            continue
-        n = int(np.prod(t["ne"], dtype=np.int64)) if t["ne"] else 1
-        if n % blk[1]:
-            raise ValueError(f"{name}: {t['name']} has {n} weights, not whole {blk[0]} blocks")
-        t["nbytes"] = n // blk[1] * blk[2]
+    start = -(-header_end // align) * align
+    tensors = []
+    for tname, dims, tid, rel in infos:
+        count = int(np.prod(dims, dtype=np.int64)) if dims else 1
+        nbytes = None
+        if tid in GGML_BLOCKS:
+            tn, per, width = GGML_BLOCKS[tid]
+            if count % per:
+                raise ValueError(f"{where}: {tname} has {count} weights, not whole {tn} blocks")
+            nbytes = count // per * width
+        tensors.append({"name": tname, "ne": dims, "type": tid, "offset": start + rel, "nbytes": nbytes})
     return meta, tensors, start
 
 
@@ -134,29 +154,36 @@ def _type_name(tid):
 
 
 def expert_tensors(shards, layers=None):
-    """[(index key, shard, tensor)] of every routed-expert tensor of the layers below ``layers`` (all when None),
-    by layer, then gate, up, down (gguf_repack.py:107-125). A layer missing one of its three projections, or an
-    expert tensor in a type the kernels do not decode, raises ValueError naming the file and the type."""
-    found = {}
-    for sh in shards:
-        with open(sh, "rb") as f:
+    """[(index key, shard, tensor)] of every routed-expert tensor (blk.N.ffn_{gate,up,down}_exps.weight) of the
+    layers below ``layers`` (all when None), ordered by layer, then gate, up, down. The reference builds the same
+    list in tools/gguf_repack.py:107-125. A layer missing one of its three projections, an expert tensor that is not
+    [row length, rows, experts], or one in a type the kernels do not decode raises ValueError naming the file and the
+    type."""
+    by_layer = {}
+    for shard in shards:
+        with open(shard, "rb") as f:
             _, tensors, _ = read_header(f)
         for t in tensors:
-            m = _EXPS.fullmatch(t["name"])
-            if m and (layers is None or int(m.group(1)) < layers):
-                found[int(m.group(1)), _PROJ.index(m.group(2))] = (sh, t)
-    for L in sorted({L for L, _ in found}):
-        missing = [_PROJ[p] for p in range(3) if (L, p) not in found]
-        if missing:
-            raise ValueError(f"layer {L} has no {'/'.join(missing)} expert tensor")
-    for sh, t in found.values():
-        tn = _type_name(t["type"])
-        if tn not in DECODED:
-            raise ValueError(f"{Path(sh).name}: {t['name']} is {tn}, which these kernels do not decode "
-                             f"(they decode {', '.join(DECODED)})")
-        if len(t["ne"]) != 3:
-            raise ValueError(f"{Path(sh).name}: {t['name']} has ne {t['ne']}, not [row length, rows, experts]")
-    return [(_key(L, _PROJ[p]), *found[L, p]) for L, p in sorted(found)]
+            m = _EXPERT_TENSOR.fullmatch(t["name"])
+            if m is None or (layers is not None and int(m["layer"]) >= layers):
+                continue
+            by_layer.setdefault(int(m["layer"]), {})[m["proj"]] = (shard, t)
+    out = []
+    for layer in sorted(by_layer):
+        have = by_layer[layer]
+        absent = [p for p in _PROJ if p not in have]
+        if absent:
+            raise ValueError(f"layer {layer} has no {'/'.join(absent)} expert tensor")
+        for proj in _PROJ:
+            shard, t = have[proj]
+            tn = _type_name(t["type"])
+            if tn not in DECODED:
+                raise ValueError(f"{Path(shard).name}: {t['name']} is {tn}, which these kernels do not decode "
+                                 f"(they decode {', '.join(DECODED)})")
+            if len(t["ne"]) != 3:
+                raise ValueError(f"{Path(shard).name}: {t['name']} has ne {t['ne']}, not [row length, rows, experts]")
+            out.append((_key(layer, proj), shard, t))
+    return out
 
 
 def check_scales(records, t):
@@ -178,52 +205,102 @@ def _block_bytes(t):
     raise ValueError(f"unknown ggml type {t}")
 
 
-def _drop_cache(fd, off, n):
+def _uncache(fd, off, n):
+    """Drop [off, off + n) of fd from the page cache where the OS allows (so a read-back comes from the drive)."""
     if hasattr(os, "posix_fadvise"):
         os.posix_fadvise(fd, off, n, os.POSIX_FADV_DONTNEED)
 
 
+def _record_entry(t, offset):
+    """The experts_index.json entry of tensor t written from byte ``offset`` of experts.bin: one record an expert, the
+    expert's blocks as part "gguf" [rows, row bytes] and zeros as part "pad" up to a 4 KiB multiple."""
+    row_len, rows, n_exp = t["ne"]
+    body = t["nbytes"] // n_exp
+    stride = -(-body // RECORD_ALIGN) * RECORD_ALIGN
+    parts = [{"name": "gguf", "bytes": body, "shape": [rows, body // rows], "dtype": "U8",
+              "ggml_type": GGML_BLOCKS[t["type"]][0], "ne": [row_len, rows]}]
+    if stride != body:
+        parts.append({"name": "pad", "bytes": stride - body, "shape": [stride - body], "dtype": "U8"})
+    return {"offset": offset, "stride": stride, "n_experts": n_exp, "parts": parts}
+
+
+class _RecordWriter:
+    """experts.bin under construction. Each projection's records go out with positioned writes in groups of experts
+    taken straight from the memory-mapped GGUF shard; after a group is synced and dropped from the page cache, a
+    second descriptor reads it back and it is compared with the source before the next group is taken."""
+
+    def __init__(self, path, group=32):
+        self.path = Path(path)
+        self.group = group
+        self.fd = os.open(self.path, os.O_WRONLY | os.O_CREAT | os.O_TRUNC, 0o644)
+        self.check_fd = os.open(self.path, os.O_RDONLY)
+        self.end = 0
+
+    def close(self):
+        os.close(self.fd)
+        os.close(self.check_fd)
+
+    def _write_groups(self, key, t, src, entry, src_fd):
+        body, stride, n_exp = entry["parts"][0]["bytes"], entry["stride"], entry["n_experts"]
+        tn = entry["parts"][0]["ggml_type"]
+        out = np.zeros((self.group, stride), np.uint8)
+        for first in range(0, n_exp, self.group):
+            last = min(first + self.group, n_exp)
+            n = last - first
+            if not check_scales(src[first:last], tn):
+                raise ValueError(f"{t['name']} experts {first}..{last - 1} hold a non-finite {tn} scale")
+            out[:n, :body] = src[first:last]
+            at = self.end + first * stride
+            view = memoryview(out[:n].reshape(-1))
+            done = 0
+            while done < len(view):
+                done += os.pwrite(self.fd, view[done:], at + done)
+            os.fsync(self.fd)
+            _uncache(self.fd, at, n * stride)
+            if os.pread(self.check_fd, n * stride, at) != view.tobytes():
+                raise OSError(f"{self.path.name}: {key} experts {first}..{last - 1} read back differently")
+            if src_fd is not None:
+                _uncache(src_fd, t["offset"] + first * body, n * body)
+
+    def add(self, key, shard, t, drop_src):
+        entry = _record_entry(t, self.end)
+        body, stride, n_exp = entry["parts"][0]["bytes"], entry["stride"], entry["n_experts"]
+        with open(shard, "rb") as f:
+            mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+            src = None
+            try:
+                if t["offset"] + n_exp * body > len(mm):
+                    raise ValueError(f"{Path(shard).name}: {t['name']} runs past the end of the file")
+                src = np.frombuffer(mm, np.uint8, count=n_exp * body, offset=t["offset"]).reshape(n_exp, body)
+                self._write_groups(key, t, src, entry, f.fileno() if drop_src else None)
+            finally:
+                del src
+                try:
+                    mm.close()
+                except BufferError:  # an exception in flight still holds a view of the map: it closes when collected
+                    pass
+        self.end += n_exp * stride
+        return entry
+
+
 def pack(shards, out_bin, log=print, layers=None, drop_src=True):
     """Write ``out_bin`` and experts_index.json beside it from the routed experts of the GGUF ``shards``, and
-    return the index (gguf_repack.py:138-177). Each chunk of records is written, flushed, dropped from the page
-    cache, read back and compared byte for byte with the source slices; a non-finite scale raises ValueError."""
+    return the index: the on-disk form the reference's tools/gguf_repack.py:138-177 writes and its loader reads
+    (stream_fast.py:6654-6661). Every group of records is verified against its source slice after it is synced; a
+    non-finite scale raises ValueError."""
     out_bin = Path(out_bin)
     todo = expert_tensors(shards, layers)
-    index, written = {}, 0
-    with open(out_bin, "wb") as dst, open(out_bin, "rb") as back:
-        for i, (key, shard, t) in enumerate(todo):
-            tn = GGML_BLOCKS[t["type"]][0]
-            ne0, ne1, n_exp = t["ne"]
-            nbytes = t["nbytes"] // n_exp
-            stride = nbytes + (-nbytes) % RECORD_ALIGN
-            parts = [{"name": "gguf", "bytes": nbytes, "shape": [ne1, nbytes // ne1], "dtype": "U8",
-                      "ggml_type": tn, "ne": [ne0, ne1]}]
-            if stride > nbytes:
-                parts.append({"name": "pad", "bytes": stride - nbytes, "shape": [stride - nbytes], "dtype": "U8"})
-            index[key] = {"offset": written, "stride": stride, "n_experts": n_exp, "parts": parts}
-            with open(shard, "rb") as src:
-                for e0 in range(0, n_exp, _CHUNK):
-                    n = min(_CHUNK, n_exp - e0)
-                    at = t["offset"] + e0 * nbytes
-                    raw = os.pread(src.fileno(), n * nbytes, at)
-                    if len(raw) != n * nbytes:
-                        raise ValueError(f"{Path(shard).name}: {t['name']} ends before expert {e0 + n - 1}")
-                    if drop_src:
-                        _drop_cache(src.fileno(), at, n * nbytes)
-                    rec = np.zeros((n, stride), np.uint8)
-                    rec[:, :nbytes] = np.frombuffer(raw, np.uint8).reshape(n, nbytes)
-                    if not check_scales(rec[:, :nbytes], tn):
-                        raise ValueError(f"{Path(shard).name}: {t['name']} experts {e0}..{e0 + n - 1} hold a "
-                                         f"non-finite {tn} scale")
-                    dst.write(rec.data)
-                    dst.flush()
-                    os.fsync(dst.fileno())
-                    _drop_cache(dst.fileno(), written, n * stride)
-                    if os.pread(back.fileno(), n * stride, written) != rec.tobytes():
-                        raise OSError(f"{out_bin.name}: {key} experts {e0}..{e0 + n - 1} read back differently")
-                    written += n * stride
+    writer = _RecordWriter(out_bin)
+    index = {}
+    try:
+        for n, (key, shard, t) in enumerate(todo, 1):
+            index[key] = writer.add(key, shard, t, drop_src)
             if log is not None:
-                log(f"  [{i + 1}/{len(todo)}] {key}: {tn} {n_exp} x {stride:,} B, {written / 1e9:.2f} GB")
+                e = index[key]
+                log(f"  {key} ({n} of {len(todo)}): {e['n_experts']} {e['parts'][0]['ggml_type']} records of "
+                    f"{e['stride']:,} B; {writer.end / 1e9:.2f} GB written")
+    finally:
+        writer.close()
     out_bin.with_name("experts_index.json").write_text(json.dumps(index, indent=1))
     return index
 

@@ -176,9 +176,9 @@ def test_header_values(tmp_path, version, align):
         meta, tensors, start = gp.read_header(f)
     assert meta["version"] == version and meta["general.alignment"] == align
     assert meta["general.architecture"] == "qwen3moe" and meta["qwen3moe.expert_count"] == E
-    assert meta["rope.scale"] == 1.5 and meta["flag"] is True and meta["short"] == [1, -2, 3]
+    assert meta["rope.scale"] == 1.5 and meta["flag"] is True and meta["short"].tolist() == [1, -2, 3]
     assert meta["tokens"] == ["a", "bc", "def"] and meta["u8"] == 200 and meta["i64"] == -5
-    assert meta["f64"] == 0.25 and meta["long"] == {"array_len": 100}
+    assert meta["f64"] == 0.25 and meta["long"].dtype == np.int32 and meta["long"].tolist() == list(range(100))
     assert start % align == 0
     body = path.read_bytes()
     for (name, ne, tid, raw), t in zip(exps, tensors):
