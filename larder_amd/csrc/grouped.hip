@@ -123,39 +123,54 @@ __device__ __forceinline__ int frag_feature(int wave, int nb) {
                               : 64 * wave + 16 * nb;
 }
 
-// acc[nb][mb][r] = D[tile feature frag_feature(nb) + 4 g + r][tile row 16 mb + fr]. Gate/up: h (f16, K order) =
-// silu(gate) * up; down: y (F32 / F16, natural order).
+// Two f16 of a, b packed in one word
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, h2_t{_Float16(a), _Float16(b)});
+}
+
+// acc[nb][mb][r] = D[tile feature frag_feature(nb) + 4 g + r][tile row 16 mb + fr]. Every store is 16 bytes:
+//   * gate/up: h (f16, K order) = silu(gate) * up. A lane's features 4g..4g+3 of fragments 0 and 1 (32 w + 4g.. and
+//     32 w + 16 + 4g.. of the n-tile) sit at K-order positions 8g..8g+3 and 8g+4..8g+7 of their 32-block: one store;
+//   * down, f16: fragments nb and nb + 1 meet through one permlane16 swap a word: lane group g then holds 8
+//     consecutive features, of fragment nb + (g & 1), from 8 (g >> 1) on, so a row's 32 features of the pair go out
+//     as one 64-byte run; f32: each fragment's 4 features as they are.
+// Called by every lane of the workgroup (the swaps read the lanes 16 away); rows past the tile's end store nothing.
 template <int MODE, int MB = 8>
 __device__ __forceinline__ void store_tile(f32x4 (&acc)[4][MB], const Tile &t, int wave, int fr, int g, void *out,
                                            int ldo, int odt) {
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = 16 * mb + fr;
-    if (m >= t.rows) continue;
-    const size_t o = size_t(t.row0 + m) * ldo;
+    const bool ok = m < t.rows;
+    const size_t o = size_t(t.row0 + (ok ? m : 0)) * ldo;
     if (MODE == MODE_GATE_UP) {
+      uint32_t v[4];
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        h2_t v01 = {_Float16(silu_mul(acc[nb][mb][0], acc[nb + 2][mb][0])),
-                    _Float16(silu_mul(acc[nb][mb][1], acc[nb + 2][mb][1]))};
-        h2_t v23 = {_Float16(silu_mul(acc[nb][mb][2], acc[nb + 2][mb][2])),
-                    _Float16(silu_mul(acc[nb][mb][3], acc[nb + 2][mb][3]))};
-        const int n = t.nt * (GN / 2) + frag_feature<MODE>(wave, nb) + 4 * g;
-        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + kperm4(n)) =
-            u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
-      }
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+          v[2 * nb + r] = pack_h2(silu_mul_h(acc[nb][mb][2 * r], acc[nb + 2][mb][2 * r]),
+                                  silu_mul_h(acc[nb][mb][2 * r + 1], acc[nb + 2][mb][2 * r + 1]));
+      const int n0 = t.nt * (GN / 2) + frag_feature<MODE>(wave, 0);  // a multiple of 32
+      if (ok) *reinterpret_cast<u32x4 *>(static_cast<_Float16 *>(out) + o + n0 + 8 * g) = u32x4{v[0], v[1], v[2], v[3]};
     } else if (odt == LMOE_F32) {
+      if (ok) {
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        *reinterpret_cast<f32x4 *>(static_cast<float *>(out) + o + t.nt * GN + frag_feature<MODE>(wave, nb) +
-                                   4 * g) = acc[nb][mb];
+        for (int nb = 0; nb < 4; ++nb)
+          *reinterpret_cast<f32x4 *>(static_cast<float *>(out) + o + t.nt * GN + frag_feature<MODE>(wave, nb) +
+                                     4 * g) = acc[nb][mb];
+      }
     } else {
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        h2_t v01 = {_Float16(acc[nb][mb][0]), _Float16(acc[nb][mb][1])};
-        h2_t v23 = {_Float16(acc[nb][mb][2]), _Float16(acc[nb][mb][3])};
-        *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + t.nt * GN + frag_feature<MODE>(wave, nb) +
-                                   4 * g) = u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
+      for (int pr = 0; pr < 2; ++pr) {
+        const int nb = 2 * pr;
+        const auto s0 = __builtin_amdgcn_permlane16_swap(pack_h2(acc[nb][mb][0], acc[nb][mb][1]),
+                                                         pack_h2(acc[nb + 1][mb][0], acc[nb + 1][mb][1]), false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(pack_h2(acc[nb][mb][2], acc[nb][mb][3]),
+                                                         pack_h2(acc[nb + 1][mb][2], acc[nb + 1][mb][3]), false, false);
+        const uint32_t a0 = s0[0], b0 = s0[1], a1 = s1[0], b1 = s1[1];
+        const int n = t.nt * GN + frag_feature<MODE>(wave, nb + (g & 1)) + 8 * (g >> 1);
+        if (ok) *reinterpret_cast<u32x4 *>(static_cast<_Float16 *>(out) + o + n) = u32x4{a0, a1, b0, b1};
       }
     }
   }
@@ -170,11 +185,20 @@ template <int GMT> constexpr int q0_stage() { return q0_astage<GMT>() + GN * 36;
 template <int GMT> constexpr int q0_dma_a() { return GMT * 128 / 1024 / 4; }      // 16-byte A copies a lane a step
 constexpr int kQ0DmaW = GN * 32 / 1024 / 4;     // 16-byte unit-head copies a lane a step (2), plus one 4-byte copy
 
+// A wavefront-uniform pointer held in scalar registers (the copy instructions take their base there)
+template <typename P>
+__device__ __forceinline__ P *uniform(P *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v)), hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+  return reinterpret_cast<P *>((uint64_t(hi) << 32) | lo);
+}
+
 // One wavefront-wide global -> LDS copy: lane l's `BYTES` (4 or 16) at base + voff land at LDS address
 // lds + l * BYTES (global_load_lds_dwordx3 would also step 16 bytes a lane). M0 carries the LDS address; nothing
 // else in these kernels uses M0.
 template <int BYTES>
-__device__ __forceinline__ void dma(const void *base, uint32_t voff, uint32_t lds) {
+__device__ __forceinline__ void dma(const void *base_any, uint32_t voff, uint32_t lds) {
+  const void *base = uniform(base_any);
   if (BYTES == 16)
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "memory");
   else
@@ -193,6 +217,94 @@ __device__ __forceinline__ void barrier_lds() {
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Where lane (fr, g) of a wavefront finds its 4 weight fragments in a Q4_0 stage (the same for every tile). Lane
+// (fr, g) of fragment nb decodes tile feature f = frag_feature(nb) + fr's unit: block 0 qs bytes 4g..+3 (unit bytes
+// 2 + 4g.., straddling words g and g + 1), block 1 qs bytes 4g..+3 (word 5 + g; word 8 sits in the tail area),
+// d0 / d1 in the low half of word 0 / the high half of word 4. Byte offsets in a stage: the feature's first half at
+// head[nb], its second half 256 bytes on; word g + 1 at head[nb] + w1_of; block 1's word at blk1[nb].
+struct Q0Lane {
+  int head[4], blk1[4], w1_of;
+};
+
+template <int MODE, int GMT>
+__device__ __forceinline__ Q0Lane q0_lane(int wave, int fr, int g) {
+  Q0Lane L;
+  L.w1_of = g < 3 ? 4 * g + 4 : 256;
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int f = frag_feature<MODE>(wave, nb) + fr;
+    L.head[nb] = q0_astage<GMT>() + 512 * (f >> 4) + 16 * (f & 15);
+    L.blk1[nb] = g < 3 ? L.head[nb] + 256 + 4 * (1 + g) : q0_astage<GMT>() + kQ0WHead + 4 * f;
+  }
+  return L;
+}
+
+// One K step of a wavefront out of the Q4_0 stage at st into acc. The MFMA order is written out by hand. The
+// step's 8 weight fragments (K slice ks = i / 4, fragment nb = i % 4) go in turn; fragment i's 8 MFMAs issue in
+// pairs with a quarter of fragment i + 1's decode (4 VALU) between pairs, so the decode issues while the matrix
+// core works; fragment i + 2's weight word is read from LDS one fragment ahead of its decode and the second K
+// slice's A fragments two fragments ahead of their use. sched_barrier keeps the compiler from regrouping them.
+// QN: the 32-row pairs of fragments the tile has rows in (a tile's last m-tile is often short): the MFMAs and A
+// reads of empty pairs are left out.
+template <int QN, int MB>
+__device__ __forceinline__ void q0_step(const uint8_t *st, const Q0Lane &L, int fr, int g, f32x4 (&acc)[4][MB]) {
+  __builtin_amdgcn_s_setprio(1);  // the other workgroup's wavefront on this SIMD yields while this one multiplies
+  const u32x4 *as = reinterpret_cast<const u32x4 *>(st);
+  auto at = [&](int byte) -> uint32_t { return *reinterpret_cast<const uint32_t *>(st + byte); };
+  auto word = [&](int i) -> uint32_t {
+    const int ks = i / 4, nb = i % 4;
+    return ks == 0 ? __builtin_amdgcn_alignbyte(at(L.head[nb] + L.w1_of), at(L.head[nb] + 4 * g), 2) : at(L.blk1[nb]);
+  };
+  auto scale = [&](int i) -> uint32_t { return at(L.head[i % 4] + 256 * (i / 4)); };
+  const h2_t bias = {_Float16(1032.0f), _Float16(1032.0f)};
+  half8 xf[2][8];
+#pragma unroll
+  for (int mb = 0; mb < 2 * QN; ++mb) xf[0][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, g)]);
+  uint32_t xw[8], sw[8];  // fully unrolled: each element lives in its own registers
+  xw[0] = word(0);
+  sw[0] = scale(0);
+  xw[1] = word(1);
+  sw[1] = scale(1);
+  u32x4 wcur = __builtin_bit_cast(u32x4, decode8<LMOE_Q4_0>(xw[0], sw[0], 0));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int ks = i / 4, nb = i % 4;
+    if (i + 2 < 8) {
+      xw[i + 2] = word(i + 2);
+      sw[i + 2] = scale(i + 2);
+    }
+    if (i == 2) {
+#pragma unroll
+      for (int mb = 0; mb < 2 * QN; ++mb) xf[1][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 + g)]);
+    }
+    const int n = i + 1 < 8 ? i + 1 : 7;  // the next fragment (a repeat of the last, unused, after it)
+    const _Float16 d = __builtin_bit_cast(h2_t, sw[n])[n / 4];
+    const h2_t dd = {d, d};
+    uint32_t lo = 0, hi = 0;
+    u32x4 wnext;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q < QN) {
+        acc[nb][2 * q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur), xf[ks][2 * q],
+                                                                 acc[nb][2 * q], 0, 0, 0);
+        acc[nb][2 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur),
+                                                                     xf[ks][2 * q + 1], acc[nb][2 * q + 1], 0, 0, 0);
+      }
+      if (i + 1 < 8) {
+        if (q == 0) {
+          lo = xw[n] & 0x0F0F0F0Fu;
+          hi = (xw[n] >> 4) & 0x0F0F0F0Fu;
+        }
+        const uint32_t p = magic_pair(q < 2 ? lo : hi, q % 2 == 0 ? kSel01 : kSel23);
+        wnext[q] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2_t, p) - bias) * dd);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i + 1 < 8) wcur = wnext;
+  }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // Grid: n_ntile * max_tiles workgroups of 256 threads, two a CU. GATE_UP: n-tile j covers intermediate features
@@ -264,89 +376,13 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
     dma<4>(wb, w_off[kQ0DmaW], __builtin_amdgcn_readfirstlane(st + kQ0AStage + kQ0WHead + 256u * uint32_t(wave)));
   };
 
-  int wfeat[4];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) wfeat[nb] = frag_feature<MODE>(wave, nb) + fr;
   f32x4 acc[4][MB];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // Lane (fr, g) of fragment nb decodes feature wfeat[nb]'s unit: block 0 qs bytes 4g..+3 (unit bytes 2 + 4g..,
-  // straddling words g and g + 1), block 1 qs bytes 4g..+3 (word 5 + g; word 8 sits in the tail area), d0 / d1 in
-  // the low half of word 0 / the high half of word 4. Byte offsets in a stage: the feature's first half at
-  // head[nb], its second half 256 bytes on; word g + 1 at head[nb] + w1_of; block 1's word at blk1[nb].
-  int head[4], blk1[4];
-  const int w1_of = g < 3 ? 4 * g + 4 : 256;
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    head[nb] = kQ0AStage + 512 * (wfeat[nb] >> 4) + 16 * (wfeat[nb] & 15);
-    blk1[nb] = g < 3 ? head[nb] + 256 + 4 * (1 + g) : kQ0AStage + kQ0WHead + 4 * wfeat[nb];
-  }
-  // The MFMA order is written out by hand. The step's 8 weight fragments (K slice ks = i / 4, fragment nb = i % 4)
-  // go in turn; fragment i's 8 MFMAs issue in pairs with a quarter of fragment i + 1's decode (4 VALU) between
-  // pairs, so the decode issues while the matrix core works; fragment i + 2's weight word is read from LDS one
-  // fragment ahead of its decode and the second K slice's A fragments two fragments ahead of their use.
-  // sched_barrier keeps the compiler from regrouping them. QN: the 32-row pairs of fragments the tile has rows
-  // in (a tile's last m-tile is often short): the MFMAs and A reads of empty pairs are left out.
-  auto compute = [&](int s, auto qn) {
-    constexpr int QN = decltype(qn)::value;
-    const uint8_t *st = lds + s * kQ0Stage;
-    const u32x4 *as = reinterpret_cast<const u32x4 *>(st);
-    auto at = [&](int byte) -> uint32_t { return *reinterpret_cast<const uint32_t *>(st + byte); };
-    auto word = [&](int i) -> uint32_t {
-      const int ks = i / 4, nb = i % 4;
-      return ks == 0 ? __builtin_amdgcn_alignbyte(at(head[nb] + w1_of), at(head[nb] + 4 * g), 2) : at(blk1[nb]);
-    };
-    auto scale = [&](int i) -> uint32_t { return at(head[i % 4] + 256 * (i / 4)); };
-    const h2_t bias = {_Float16(1032.0f), _Float16(1032.0f)};
-    half8 xf[2][8];
-#pragma unroll
-    for (int mb = 0; mb < 2 * QN; ++mb) xf[0][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, g)]);
-    uint32_t xw[8], sw[8];  // fully unrolled: each element lives in its own registers
-    xw[0] = word(0);
-    sw[0] = scale(0);
-    xw[1] = word(1);
-    sw[1] = scale(1);
-    u32x4 wcur = __builtin_bit_cast(u32x4, decode8<LMOE_Q4_0>(xw[0], sw[0], 0));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int ks = i / 4, nb = i % 4;
-      if (i + 2 < 8) {
-        xw[i + 2] = word(i + 2);
-        sw[i + 2] = scale(i + 2);
-      }
-      if (i == 2) {
-#pragma unroll
-        for (int mb = 0; mb < 2 * QN; ++mb) xf[1][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 + g)]);
-      }
-      const int n = i + 1 < 8 ? i + 1 : 7;  // the next fragment (a repeat of the last, unused, after it)
-      const _Float16 d = __builtin_bit_cast(h2_t, sw[n])[n / 4];
-      const h2_t dd = {d, d};
-      uint32_t lo = 0, hi = 0;
-      u32x4 wnext;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q < QN) {
-          acc[nb][2 * q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur), xf[ks][2 * q],
-                                                                   acc[nb][2 * q], 0, 0, 0);
-          acc[nb][2 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wcur),
-                                                                       xf[ks][2 * q + 1], acc[nb][2 * q + 1], 0, 0, 0);
-        }
-        if (i + 1 < 8) {
-          if (q == 0) {
-            lo = xw[n] & 0x0F0F0F0Fu;
-            hi = (xw[n] >> 4) & 0x0F0F0F0Fu;
-          }
-          const uint32_t p = magic_pair(q < 2 ? lo : hi, q % 2 == 0 ? kSel01 : kSel23);
-          wnext[q] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(h2_t, p) - bias) * dd);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (i + 1 < 8) wcur = wnext;
-    }
-  };
+  const Q0Lane ql = q0_lane<MODE, GMT>(wave, fr, g);
+  auto compute = [&](int s, auto qn) { q0_step<decltype(qn)::value, MB>(lds + s * kQ0Stage, ql, fr, g, acc); };
 
   // Step kk: the copies of step kk + NST - 1 go out, step kk multiplies out of its stage, then each wavefront waits
   // for its own copies of step kk + 1 (the counter counts in issue order: the copies of the steps after kk + 1 may
@@ -432,8 +468,8 @@ __global__ void __launch_bounds__(256) k_splitk_finish(const float *ws, int kspl
   }
   const size_t o = size_t(p) * ldo;
   if (MODE == MODE_GATE_UP) {
-    const h2_t v01 = {_Float16(silu_mul(a[0], b[0])), _Float16(silu_mul(a[1], b[1]))};
-    const h2_t v23 = {_Float16(silu_mul(a[2], b[2])), _Float16(silu_mul(a[3], b[3]))};
+    const h2_t v01 = {_Float16(silu_mul_h(a[0], b[0])), _Float16(silu_mul_h(a[1], b[1]))};
+    const h2_t v23 = {_Float16(silu_mul_h(a[2], b[2])), _Float16(silu_mul_h(a[3], b[3]))};
     *reinterpret_cast<u32x2 *>(static_cast<_Float16 *>(out) + o + kperm4(n)) =
         u32x2{__builtin_bit_cast(uint32_t, v01), __builtin_bit_cast(uint32_t, v23)};
   } else if (odt == LMOE_F32) {

@@ -31,6 +31,17 @@ namespace lmoe {
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// The value unchanged, opaque to the optimiser: per-thread arithmetic on it is redone in each iteration of an outer
+// loop (a layer, a tile) instead of being hoisted out of the loop and kept live, in registers, for the whole kernel
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 constexpr int XS = 36;  // dwords a prepared unit takes (32 pairs, 2 sums, 2 pad)
 
 // ---- host-side error plumbing ----------------------------------------------------------------------------------
@@ -166,6 +177,14 @@ __device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + __ex
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float e = __expf(-fabsf(g));
   const float s = g >= 0.0f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+  return g * s * u;
+}
+// The same for a result rounded to f16 right after: the hardware reciprocal (1 ulp in fp32, far below f16's
+// rounding) in place of the correctly rounded division's ten-instruction sequence
+__device__ __forceinline__ float silu_mul_h(float g, float u) {
+  const float e = __expf(-fabsf(g));
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);
+  const float s = g >= 0.0f ? r : e * r;
   return g * s * u;
 }
 

@@ -145,16 +145,6 @@ __device__ __forceinline__ const uint8_t *table_at(const void *const *tab, int l
   return reinterpret_cast<const uint8_t *>(uintptr_t(t[l]));
 }
 
-// the value unchanged, opaque to the optimiser: per-thread arithmetic on it is redone each layer instead of being
-// hoisted out of the layer loop and kept live (register pressure) for the whole kernel
-__device__ __forceinline__ int opaque(int v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
-__device__ __forceinline__ uint32_t opaque(uint32_t v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
 
 __device__ __forceinline__ float f16f(uint32_t bits16) {
   return float(__builtin_bit_cast(_Float16, uint16_t(bits16)));
