@@ -283,6 +283,18 @@ int lmoe_to_f16(const void *x, int xdtype, long long n, void *out, void *stream)
  * 8 weights are the low and high nibbles of one 4-byte word of a Q4 block. No counterpart in the reference. */
 int lmoe_to_gemm_f16(const void *x, int xdtype, long long n, void *out, void *stream);
 
+/* Router logits of a prefill chunk on the matrix cores, replacing the reference's gate matmul before top-k
+ * (stream_fast.py:4352-4360; route_cuda.py:433-444 on CUDA): xh [T][H] float16 in the GEMM K order (the activation
+ * operand the grouped GEMMs read, lmoe_to_gemm_f16), wk [E + n_gate][H] float16 in the same order (the router
+ * weight, plus the shared expert's gate row when n_gate == 1, converted once with lmoe_to_gemm_f16); exact f16
+ * products, fp32 sums. logits [T][E] float32, gate [T] float32 (logit row E; null when n_gate == 0). H % 64 == 0.
+ * lmoe_router_gemm_ksplit picks the K split (at least ~512 workgroups); with a split the partial sums go to ws
+ * (lmoe_router_gemm_workspace_bytes, 16-byte aligned) and a second launch adds them in slice order. */
+int lmoe_router_gemm_ksplit(int T, int H, int En);
+size_t lmoe_router_gemm_workspace_bytes(int T, int H, int En);
+int lmoe_router_gemm(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws, float *logits,
+                     float *gate, void *stream);
+
 /* Weighted combine of rows kept in grouped (expert-sorted) order:
  *   out[t][n] = sum_j scores[t][j] * y[inv[t * k + j]][n] (+ sigmoid(gate) * shared) (+ residual)
  * y [R][H] in ydtype. Replaces the unsort plus combine of stream_fast.py:5525 and 4372-4376. */

@@ -56,6 +56,9 @@ SIGNATURES = {
     "lmoe_grouped_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "lmoe_to_f16": (_I, [_P, _I, _LL, _P, _P]),
     "lmoe_to_gemm_f16": (_I, [_P, _I, _LL, _P, _P]),
+    "lmoe_router_gemm_ksplit": (_I, [_I, _I, _I]),
+    "lmoe_router_gemm_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "lmoe_router_gemm": (_I, [_P, _I, _I, _P, _I, _I, _P, _P, _P, _P]),
     "lmoe_grouped_gate_up": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "lmoe_grouped_down": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_grouped_gate_up_bm": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P,

@@ -64,7 +64,7 @@ constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
 
 // An MFMA lane's 8 f16 weights from its nibble word x (low nibbles: K positions 0-3 of the lane group, high
 // nibbles: 4-7). Q4_0: w = ((1024 + q) - 1032) d, d = the selected half of sw. Q4_K: sw = {f16(d sc), f16(dmin m)},
-// w = ((1024 + q) - 1024) (d sc) - dmin m.
+// w = fma((1024 + q) - 1024, d sc, -dmin m) (q exact, one rounding).
 template <int TB>
 __device__ __forceinline__ half8 decode8(uint32_t x, uint32_t sw, int half) {
   const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
@@ -84,7 +84,9 @@ __device__ __forceinline__ half8 decode8(uint32_t x, uint32_t sw, int half) {
   }
   uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = __builtin_bit_cast(uint32_t, (p[i] - bias) * scale - sub);
+  for (int i = 0; i < 4; ++i)
+    o[i] = TB == LMOE_Q4_0 ? __builtin_bit_cast(uint32_t, (p[i] - bias) * scale)
+                           : __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p[i] - bias, scale, -sub));
   return __builtin_bit_cast(half8, u32x4{o[0], o[1], o[2], o[3]});
 }
 
@@ -771,6 +773,189 @@ k_grouped_q4_k(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
 }
 
+// ---- Q4_K: global -> LDS directly, four stages of 64-row tiles --------------------------------------------------
+
+// LDS: NST stages of the A tile (GMT rows x 64 K, f16, swizzled rows of 128 bytes as in the Q4_0 kernel) and the
+// step's 32 qs bytes of every tile feature (two 16-byte halves: each group of 16 features keeps its first halves in
+// one 256-byte row and its second halves in the next, as the Q4_0 unit heads); one buffer of super-block headers
+// (d, dmin, 12 scale bytes: 16 bytes a feature), copied with the first step of each super-block; and the table of
+// the current super-block's 8 (f16(d sc), f16(dmin m)) pairs of every feature, 40 bytes a feature so that the 16
+// features of an MFMA fragment read 16 different bank pairs.
+constexpr int kKQs = GN * 32, kKHd = GN * 16, kKTabRow = 40, kKTab = GN * kKTabRow;
+template <int GMT> constexpr int qk_astage() { return GMT * 128; }
+template <int GMT> constexpr int qk_stage() { return qk_astage<GMT>() + kKQs; }
+
+// The Q4_K grouped GEMMs on the copy ring of k_grouped_q4_0: A and the step's raw qs bytes go global -> LDS directly
+// (global_load_lds, no registers), NST - 1 K steps ahead, one barrier a step; each super-block's header goes with
+// its first step. When a super-block starts, thread t turns feature t's header into the table of its 8 sub-block
+// scale pairs (get_scale_min_k4, gguf_ref.py:253-258; one more barrier every 4 steps). Each MFMA lane then builds
+// its nibble word from qs words g and g + 4 of its feature (the low nibbles for the step's first sub-block, the
+// high nibbles for its second: ggml's Q4_K packs sub-blocks 2s and 2s + 1 of pair s in one 32-byte run) and
+// decodes it with its pair from the table. 64-row tiles: a 16 KB stage, four stages, two workgroups a CU, three
+// steps in flight: streaming a different expert's weights through every tile (prefill over many experts with few
+// rows each). Grid and arguments as k_grouped_q4_0; host guarantees: K % 256 == 0, rows x K x 2 of A and one
+// expert's weight block under 4 GiB.
+template <int MODE, int GMT = 64, int NST = 4>
+__global__ void __launch_bounds__(kThreads, 2)
+k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
+                   const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
+                   int K, int n_rows, void *out, int ldo, int odt) {
+  constexpr int kAStage = qk_astage<GMT>(), kStage = qk_stage<GMT>(), kDmaA = GMT * 128 / 1024 / 4;
+  constexpr int kHd = NST * kStage, kTab = kHd + kKHd;
+  constexpr int MB = GMT / 16, QMAX = GMT / 32;
+  static_assert(kDmaA >= 1 && NST >= 3 && kTab + kKTab <= 81920, "tile and pipeline shape");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kTab + kKTab];
+  Tile t;
+  if (!tile_of<GMT>(offsets, tiles, n_tiles, n_ntile, &t)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, g = lane >> 4;
+  const uint32_t wrow = 144u * uint32_t(K / 256);
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(lds));
+
+  // A: as in k_grouped_q4_0
+  uint32_t a_off[kDmaA];
+#pragma unroll
+  for (int i = 0; i < kDmaA; ++i) {
+    const int q = 64 * (kDmaA * wave + i) + lane, r = q >> 3, c = (q & 7) ^ (r & 7);
+    const int p = t.row0 + (r < t.rows ? r : 0);
+    const uint32_t row = MODE == MODE_GATE_UP ? order[p] / uint32_t(topk) : uint32_t(p);
+    a_off[i] = row * uint32_t(K) * 2u + 16u * uint32_t(c);
+  }
+  // weights: wavefront w copies tile features 64 w .. 64 w + 63 (gate/up: waves 0-1 gate rows, 2-3 up rows).
+  // qs copy i: granule q = 64 (2 w + i) + lane is half h = (q / 16) % 2 of feature f = 16 (q / 32) + q % 16, from
+  // super-block byte 16 + 16 h (+ 32 s of step pair s). Header copy: feature 64 w + lane's first 16 bytes.
+  const uint8_t *wbase;
+  uint32_t q_off[2], h_off;
+  {
+    const uint8_t *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
+    const int row_base = MODE == MODE_GATE_UP ? t.nt * (GN / 2) - (wave >= 2 ? GN / 2 : 0) : t.nt * GN;
+    wbase = m + (size_t(t.e) * n_rows) * wrow;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = 64 * (2 * wave + i) + lane;
+      q_off[i] = uint32_t(row_base + 16 * (q >> 5) + (q & 15)) * wrow + 16u + 16u * uint32_t((q >> 4) & 1);
+    }
+    h_off = uint32_t(row_base + 64 * wave + lane) * wrow;
+  }
+  const int nk = K / GK;
+  auto issue = [&](int kk) {  // step kk into stage kk % NST (its super-block's header too when kk % 4 == 0)
+    const uint32_t st = lds0 + uint32_t(kk % NST) * kStage;
+    const _Float16 *ab = a_src + size_t(kk) * GK;
+#pragma unroll
+    for (int i = 0; i < kDmaA; ++i)
+      dma<16>(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kDmaA * wave + i)));
+    const uint8_t *sb = wbase + size_t(kk >> 2) * 144;
+    const uint8_t *qb = sb + 32 * (kk & 3);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      dma<16>(qb, q_off[i], __builtin_amdgcn_readfirstlane(st + kAStage + 1024u * uint32_t(2 * wave + i)));
+    if ((kk & 3) == 0) dma<16>(sb, h_off, __builtin_amdgcn_readfirstlane(lds0 + kHd + 1024u * uint32_t(wave)));
+  };
+  // the scale pairs of feature tid's current super-block, from its header: table row tid, pair j at 4 j
+  auto fill_table = [&] {
+    const u32x4 h = *reinterpret_cast<const u32x4 *>(lds + kHd + 16 * tid);
+    const uint32_t h0 = h[0], h1 = h[1], h2 = h[2], h3 = h[3];
+    const float d = half_lo(h0), dmin = half_hi(h0);
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float sc, mn;
+      k4_scale_min(h1, h2, h3, j, &sc, &mn);
+      v[j] = __builtin_bit_cast(uint32_t, h2_t{_Float16(d * sc), _Float16(dmin * mn)});
+    }
+    uint32_t *row = reinterpret_cast<uint32_t *>(lds + kTab + kKTabRow * tid);
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) *reinterpret_cast<u32x2 *>(row + j) = u32x2{v[j], v[j + 1]};
+  };
+
+  f32x4 acc[4][MB];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // lane (fr, g) of fragment nb: feature f = frag_feature(nb) + fr; its qs words g and g + 4 sit at qlo[nb] and
+  // qlo[nb] + 256 of a stage, its scale pairs in table row f
+  int qlo[4], tab[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int f = frag_feature<MODE>(wave, nb) + fr;
+    qlo[nb] = kAStage + 512 * (f >> 4) + 16 * (f & 15) + 4 * g;
+    tab[nb] = kTab + kKTabRow * f;
+  }
+  // Step kk out of stage s: per fragment the two qs words and the step's two scale pairs, both K slices' weights
+  // decoded, each meeting the tile's A fragments (QN pairs of 16-row blocks)
+  auto compute = [&](int s, int kk, auto qn) {
+    constexpr int QN = decltype(qn)::value;
+    const uint8_t *st = lds + s * kStage;
+    const u32x4 *as = reinterpret_cast<const u32x4 *>(st);
+    const int pr = kk & 3;  // the step's sub-block pair: sub-blocks 2 pr (low nibbles) and 2 pr + 1 (high)
+    half8 xf[2][2 * QMAX];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int mb = 0; mb < 2 * QN; ++mb) xf[ks][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 * ks + g)]);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const uint32_t lo = *reinterpret_cast<const uint32_t *>(st + qlo[nb]);
+      const uint32_t hi = *reinterpret_cast<const uint32_t *>(st + qlo[nb] + 256);
+      const u32x2 sp = *reinterpret_cast<const u32x2 *>(lds + tab[nb] + 8 * pr);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint32_t x = ks == 0 ? (lo & 0x0F0F0F0Fu) | ((hi & 0x0F0F0F0Fu) << 4)
+                                   : ((lo >> 4) & 0x0F0F0F0Fu) | (hi & 0xF0F0F0F0u);
+        const half8 wf = decode8<LMOE_Q4_K>(x, ks == 0 ? uint32_t(sp[0]) : uint32_t(sp[1]), 0);
+#pragma unroll
+        for (int mb = 0; mb < 2 * QN; ++mb)
+          acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, xf[ks][mb], acc[nb][mb], 0, 0, 0);
+      }
+    }
+  };
+
+  // the ring of k_grouped_q4_0: step kk + NST - 1's copies go out, step kk multiplies, each wavefront waits for its
+  // own copies of step kk + 1 and the barrier publishes that stage (and frees stage kk for the refill after it).
+  // A step makes C copies a lane, C + 1 when it starts a super-block; the waits count C a step, so they may also
+  // wait for one copy of the step after (never less than they must).
+  constexpr int C = kDmaA + 2;
+  static_assert(NST <= 5 && 3 * C + 3 <= 63, "the wait counts below");
+  auto wait_steps = [&](int later) {
+    if (later <= 0)
+      wait_vm<0>();
+    else if (later == 1)
+      wait_vm<C>();
+    else if (later == 2)
+      wait_vm<2 * C>();
+    else
+      wait_vm<3 * C>();
+  };
+  const int pre = min(NST - 1, nk);
+  for (int j = 0; j < pre; ++j) issue(j);
+  wait_steps(pre - 1);
+  barrier_lds();
+  auto run = [&](auto qn) {
+    for (int kk = 0; kk < nk; ++kk) {
+      if ((kk & 3) == 0) {  // the super-block's header landed with this step: its scale table, then a barrier
+        fill_table();
+        barrier_lds();
+      }
+      if (kk + NST - 1 < nk) issue(kk + NST - 1);
+      compute(kk % NST, kk, qn);
+      if (kk + 1 < nk) {
+        wait_steps(min(kk + NST - 1, nk - 1) - (kk + 1));
+        barrier_lds();
+      }
+    }
+  };
+  if constexpr (QMAX == 1) {
+    run(IC<1>{});
+  } else {
+    if (t.rows <= 32)  // uniform across the workgroup
+      run(IC<1>{});
+    else
+      run(IC<2>{});
+  }
+  store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
+}
+
 // x [n] in dt -> f16 (round to nearest even), 8 elements a thread (vector loads when the whole range allows).
 // kperm: element i lands at its position in the grouped GEMMs' K order (n % 32 == 0, vector path only).
 __global__ void __launch_bounds__(256) k_to_f16(const void *x, int dt, long long n, _Float16 *out, int vec,
@@ -799,6 +984,133 @@ __global__ void __launch_bounds__(256) k_to_f16(const void *x, int dt, long long
     if (i < cnt) out[i0 + i] = _Float16(load_elt(x, size_t(i0 + i), dt));
 }
 
+// ---- the prefill router: logits = x . wr^T on the matrix cores ------------------------------------------------
+
+constexpr int kRgM = 64, kRgN = 128;  // tokens and logit rows a tile
+constexpr int kRgAStage = kRgM * 128, kRgStage = kRgAStage + kRgN * 128, kRgNst = 3;
+
+// Router logits for a prefill chunk: x [T][K] and w [E + n_gate][K] both f16 in the grouped GEMMs' K order (the
+// x the experts read, and the router weight converted once), fp32 accumulation of exact f16 products. A tile is
+// 64 tokens x 128 logit rows, four wavefronts of 64 tokens x 32 rows (2 x 4 accumulators of
+// v_mfma_f32_16x16x32_f16, the weight rows as the first operand); both operands go global -> LDS directly, three
+// stages, as in the grouped GEMMs. ksplit > 1: workgroup kpart takes K steps [kpart nk, (kpart + 1) nk) and writes
+// its sums to part[kpart][t][ldp] (k_router_finish adds the slices in slice order); ksplit == 1: logits straight
+// out. Rows past T read token T - 1 and logit rows past E read row E - 1; neither is stored. Logit row E (the
+// shared expert's gate, n_gate == 1) goes to gate[t].
+__global__ void __launch_bounds__(kThreads, 2)
+k_router_gemm(const _Float16 *x, int T, const _Float16 *w, int En, int K, int n_ntile, int ksplit, float *part,
+              int ldp, float *logits, int E, float *gate) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kRgNst * kRgStage];
+  const int b = blockIdx.x;
+  const int kpart = b % ksplit, tile = b / ksplit;
+  const int nt = tile % n_ntile, mt = tile / n_ntile;
+  const int row0 = mt * kRgM, col0 = nt * kRgN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, g = lane >> 4;
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(lds));
+  // x: copy i carries granule q = 64 (2 w + i) + lane = chunk (q % 8) ^ (r % 8) of token row r = q / 8;
+  // w: copy i carries granule q = 64 (4 w + i) + lane of logit row f = q / 8
+  uint32_t a_off[2], w_off[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = 64 * (2 * wave + i) + lane, r = q >> 3, c = (q & 7) ^ (r & 7);
+    a_off[i] = uint32_t(min(row0 + r, T - 1)) * uint32_t(K) * 2u + 16u * uint32_t(c);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = 64 * (4 * wave + i) + lane, f = q >> 3, c = (q & 7) ^ (f & 7);
+    w_off[i] = uint32_t(min(col0 + f, En - 1)) * uint32_t(K) * 2u + 16u * uint32_t(c);
+  }
+  const int nk = K / GK / ksplit, k0 = kpart * nk;
+  auto issue = [&](int kk) {
+    const uint32_t st = lds0 + uint32_t(kk % kRgNst) * kRgStage;
+    const _Float16 *ab = x + size_t(k0 + kk) * GK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      dma<16>(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(2 * wave + i)));
+    const _Float16 *wb = w + size_t(k0 + kk) * GK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma<16>(wb, w_off[i], __builtin_amdgcn_readfirstlane(st + kRgAStage + 1024u * uint32_t(4 * wave + i)));
+  };
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int s) {
+    const u32x4 *as = reinterpret_cast<const u32x4 *>(lds + s * kRgStage);
+    const u32x4 *ws = reinterpret_cast<const u32x4 *>(lds + s * kRgStage + kRgAStage);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      half8 xf[4];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) xf[mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 * ks + g)]);
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const half8 wf = __builtin_bit_cast(half8, ws[achunk(32 * wave + 16 * nb + fr, 4 * ks + g)]);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+          acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, xf[mb], acc[nb][mb], 0, 0, 0);
+      }
+    }
+  };
+  constexpr int C = 6;  // copies a lane a step
+  issue(0);
+  if (nk > 1) issue(1);
+  if (nk > 1)
+    wait_vm<C>();
+  else
+    wait_vm<0>();
+  barrier_lds();
+  for (int kk = 0; kk < nk; ++kk) {
+    if (kk + 2 < nk) issue(kk + 2);
+    compute(kk % kRgNst);
+    if (kk + 1 < nk) {
+      if (kk + 2 < nk)
+        wait_vm<C>();
+      else
+        wait_vm<0>();
+      barrier_lds();
+    }
+  }
+  // acc[nb][mb][r] = sum over this slice for logit row col0 + 32 w + 16 nb + 4 g + r, token row0 + 16 mb + fr
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int t = row0 + 16 * mb + fr;
+    if (t >= T) continue;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int e = col0 + 32 * wave + 16 * nb + 4 * g;
+      if (ksplit > 1) {
+        *reinterpret_cast<f32x4 *>(part + (size_t(kpart) * T + t) * ldp + e) = acc[nb][mb];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (e + r < E)
+            logits[size_t(t) * E + e + r] = acc[nb][mb][r];
+          else if (e + r < En)
+            gate[t] = acc[nb][mb][r];
+        }
+      }
+    }
+  }
+}
+
+// Adds the ksplit slices of k_router_gemm in slice order: logits[t][e] (e < E), gate[t] (e == E < En).
+// Grid (ceil(En / 256), T).
+__global__ void __launch_bounds__(256) k_router_finish(const float *part, int ksplit, int T, int ldp, int En, int E,
+                                                       float *logits, float *gate) {
+  const int t = blockIdx.y, e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= En) return;
+  float v = 0.0f;
+  for (int s = 0; s < ksplit; ++s) v += part[(size_t(s) * T + t) * ldp + e];
+  if (e < E)
+    logits[size_t(t) * E + e] = v;
+  else
+    gate[t] = v;
+}
+
 }  // namespace lmoe
 
 using namespace lmoe;
@@ -813,6 +1125,7 @@ extern "C" int lmoe_grouped_tile_rows(void) { return GM; }
 extern "C" int lmoe_grouped_pick_tile_rows(int R, int E, int type_g, int type_u, int type_d) {
   auto q4 = [](int t) { return t == LMOE_Q4_0 || t == LMOE_Q4_K; };
   if (!(q4(type_g) && type_u == type_g)) return 64;
+  if (type_g == LMOE_Q4_K) return 64;
   if (!q4(type_d)) return GM;
   const bool all_q4_0 = type_g == LMOE_Q4_0 && type_d == LMOE_Q4_0;
   return all_q4_0 && E > 0 && (long long)R < 16LL * E ? 32 : GM;
@@ -920,7 +1233,7 @@ extern "C" int lmoe_grouped_gate_up_bm(const void *x, int xdtype, int T, int top
     }
   } else {
     launch(bm == 32 ? k_grouped_q4_k<MODE_GATE_UP, 32, 3>
-                    : bm == 64 ? k_grouped_q4_k<MODE_GATE_UP, 64, 2> : k_grouped_q4_k<MODE_GATE_UP>,
+                    : bm == 64 ? k_grouped_q4_k_dma<MODE_GATE_UP> : k_grouped_q4_k<MODE_GATE_UP>,
            dim3(unsigned(grid)),
            dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg, wu, H, I, h, I,
            int(LMOE_F16));
@@ -968,7 +1281,7 @@ extern "C" int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offset
     }
   } else {
     launch(bm == 32 ? k_grouped_q4_k<MODE_DOWN, 32, 3>
-                    : bm == 64 ? k_grouped_q4_k<MODE_DOWN, 64, 2> : k_grouped_q4_k<MODE_DOWN>,
+                    : bm == 64 ? k_grouped_q4_k_dma<MODE_DOWN> : k_grouped_q4_k<MODE_DOWN>,
            dim3(unsigned(grid)),
            dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile,
            wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
@@ -1044,6 +1357,52 @@ extern "C" int lmoe_grouped_down_f16w(const void *h, const uint32_t *offsets, co
          0, (hipStream_t)stream,
          static_cast<const _Float16 *>(h), 1, static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile,
          static_cast<const _Float16 *>(wd16), static_cast<const _Float16 *>(nullptr), I, H, y, H, ydtype);
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+// The prefill router's split: K slices so that at least ~512 workgroups run, each slice at least 4 K steps, the
+// slice count a power of two dividing the K steps
+extern "C" int lmoe_router_gemm_ksplit(int T, int H, int En) {
+  if (T <= 0 || H <= 0 || En <= 0) return 1;
+  const long long tiles = (long long)((T + kRgM - 1) / kRgM) * ((En + kRgN - 1) / kRgN);
+  const int steps = H / GK;
+  int s = 1;
+  while (tiles * s < 512 && s < 8 && steps % (2 * s) == 0 && steps / (2 * s) >= 4) s *= 2;
+  return s;
+}
+
+extern "C" size_t lmoe_router_gemm_workspace_bytes(int T, int H, int En) {
+  const int s = lmoe_router_gemm_ksplit(T, H, En);
+  if (s <= 1) return 0;
+  return size_t(s) * size_t(T) * size_t((En + kRgN - 1) / kRgN * kRgN) * sizeof(float);
+}
+
+extern "C" int lmoe_router_gemm(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws,
+                                float *logits, float *gate, void *stream) {
+  const char *fn = "lmoe_router_gemm";
+  LMOE_REQUIRE(T >= 0 && E > 0 && (n_gate == 0 || n_gate == 1), LMOE_ESHAPE, "%s: bad shape", fn);
+  LMOE_REQUIRE(H > 0 && H % GK == 0, LMOE_ESHAPE, "%s: hidden size %d is not a multiple of %d", fn, H, GK);
+  if (T == 0) return 0;
+  LMOE_REQUIRE(xh && wk && logits && (n_gate == 0 || gate), LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(aligned16(xh) && aligned16(wk), LMOE_EALIGN, "%s: x and the weight must be 16-byte aligned", fn);
+  const int En = E + n_gate;
+  LMOE_REQUIRE((long long)T * H * 2 <= 0xFFFFFFFFll && (long long)En * H * 2 <= 0xFFFFFFFFll, LMOE_ESHAPE,
+               "%s: x or the weight exceeds 4 GiB", fn);
+  const int ks = lmoe_router_gemm_ksplit(T, H, En);
+  const int n_ntile = (En + kRgN - 1) / kRgN, ldp = n_ntile * kRgN;
+  LMOE_REQUIRE(ks == 1 || (ws && aligned16(ws)), LMOE_EWORKSPACE,
+               "%s: needs a 16-byte aligned workspace of lmoe_router_gemm_workspace_bytes", fn);
+  const long long grid = (long long)((T + kRgM - 1) / kRgM) * n_ntile * ks;
+  LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
+  hipStream_t st = (hipStream_t)stream;
+  launch(k_router_gemm, dim3(unsigned(grid)), dim3(kThreads), 0, st, static_cast<const _Float16 *>(xh), T,
+         static_cast<const _Float16 *>(wk), En, H, n_ntile, ks, ws, ldp, logits, E, gate);
+  if (ks > 1) {
+    LMOE_LAUNCHED(fn);
+    launch(k_router_finish, dim3(unsigned((En + 255) / 256), unsigned(T)), dim3(256), 0, st,
+           static_cast<const float *>(ws), ks, T, ldp, En, E, logits, gate);
+  }
   LMOE_LAUNCHED(fn);
   return 0;
 }

@@ -74,11 +74,11 @@ class Grouping:
         return self
 
     @classmethod
-    def identity(cls, R, device="cuda"):
-        """All R rows on expert 0 in their own order (a dense FFN, such as the shared expert, on the same kernels);
-        built on the host once."""
+    def identity(cls, R, device="cuda", bm=None):
+        """All R rows on expert 0 in their own order (a dense FFN, such as the shared expert, on the same kernels),
+        in m-tiles of bm rows (128 by default); built on the host once."""
         g = cls.__new__(cls)
-        g.R, g.E, g.bm = int(R), 1, tile_rows()
+        g.R, g.E, g.bm = int(R), 1, int(bm) if bm else tile_rows()
         nt = -(-g.R // g.bm)
         g.max_tiles = nt
         i32 = dict(dtype=torch.int32)
@@ -205,7 +205,12 @@ class PrefillBuffers:
         self.T = T
         R = T * L.k
         f32 = dict(dtype=torch.float32, device=device)
-        self.logits = torch.empty((T, L.E + (1 if L.shared is not None else 0)), **f32)
+        self.logits = torch.empty((T, L.E), **f32)
+        self.gate = torch.empty(T, **f32) if L.shared is not None else None   # the shared expert's gate logit
+        self.rws = None
+        if L.wr is not None:
+            nrw = _lib.lib().lmoe_router_gemm_workspace_bytes(T, L.H, L.E + (1 if L.shared is not None else 0))
+            self.rws = torch.empty(max(nrw // 4, 1), **f32)
         self.ids = torch.empty((T, L.k), dtype=torch.int32, device=device)
         self.scores = torch.empty((T, L.k), **f32)
         self.G = Grouping(R, L.E, device, bm=pick_tile_rows(R, L.E, L.types))
@@ -215,47 +220,60 @@ class PrefillBuffers:
         self.h = torch.empty((R, L.I), dtype=torch.float16, device=device)
         self.y = torch.empty((R, L.H), dtype=torch.float16, device=device)
         if L.shared is not None:
-            self.Gs = Grouping.identity(T, device)
+            self.Gs = Grouping.identity(T, device, bm=pick_tile_rows(T, 1, L.types))
             self.hs = torch.empty((T, L.Is), dtype=torch.float16, device=device)
             self.ys = torch.empty((T, L.H), **f32)
+            # the shared expert runs on a second stream (default priority) beside the routed experts: its dense
+            # GEMMs fill the units the routed, weight-streaming ones leave idle
+            self.side = torch.cuda.Stream(device=device)
+            self.x_ready = torch.cuda.Event()
+            self.shared_done = torch.cuda.Event()
 
 
 def prefill(layer, x, bufs, out, residual=None, logits=None):
-    """out [T, H] = layer(x) (+ residual) for x [T, H] through the grouped path: router logits (given, or x . Wr as
-    one library GEMM), top-k, device grouping, grouped gate/up + SwiGLU, grouped down, [the shared expert on the
-    same kernels], weighted combine (+ sigmoid-gated shared) (+ residual). No host synchronisation."""
+    """out [T, H] = layer(x) (+ residual) for x [T, H] through the grouped path: x once to f16 in the GEMM K order,
+    router logits (given, or lmoe_router_gemm on that x), top-k, device grouping, grouped gate/up + SwiGLU, grouped
+    down, [the shared expert on the same kernels, on a side stream that joins before the combine], weighted
+    combine (+ sigmoid-gated shared) (+ residual). No host synchronisation and no allocation."""
     L, B = layer, bufs
     T, H = x.shape
     st = stream()
     x = x.contiguous()
+    call("lmoe_to_gemm_f16", ptr(x), dcode(x.dtype), x.numel(), ptr(B.xh), st)
     if logits is None:
         if L.wr is None:
             raise ValueError("this layer has no router weight: pass logits")
-        w = L.wr if L.shared is None else torch.cat([L.wr, L.wsg.reshape(1, -1)], 0)
-        torch.matmul(x.float(), w.float().t(), out=B.logits)
-        lg, stride = B.logits, B.logits.shape[1]
+        ng = 1 if L.shared is not None else 0
+        call("lmoe_router_gemm", ptr(B.xh), T, H, ptr(L.router_gemm_weight()), L.E, ng, ptr(B.rws), ptr(B.logits),
+             ptr(B.gate) if ng else None, st)
+        lg = B.logits
     else:
         if L.shared is not None:
             raise ValueError("a shared expert's gate logit comes from the router: use the router weight")
-        lg, stride = logits.to(torch.float32).contiguous(), L.E
-    if stride == L.E:
-        call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
-    else:
-        sel = lg[:, :L.E].contiguous()
-        call("lmoe_router_topk", ptr(sel), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
+        if logits.dtype != torch.float32 or not logits.is_contiguous() or tuple(logits.shape) != (T, L.E):
+            raise ValueError(f"logits must be float32 [{T}, {L.E}] and contiguous")
+        lg = logits
+    shared = gate = None
+    if L.shared is not None:  # x is ready: the shared expert starts on the side stream
+        main = torch.cuda.current_stream()
+        B.x_ready.record(main)
+        B.side.wait_event(B.x_ready)
+        with torch.cuda.stream(B.side):
+            sg, su, sd = L.shared
+            gate_up(B.xh, B.Gs, 1, sg, su, L.types, B.hs, prepped=True)
+            down(B.hs, B.Gs, sd, L.types[2], B.ys)
+            B.shared_done.record(B.side)
+        shared, gate = ptr(B.ys), ptr(B.gate)
+    call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
     B.G.run(B.ids.reshape(-1))
     f16 = L.prefill_f16
-    gate_up(x, B.G, L.k, L.wg, L.wu, L.types, B.h, B.xh, ws=B.ws, w16=f16[:2] if f16 and f16[0] is not None else None)
+    gate_up(B.xh, B.G, L.k, L.wg, L.wu, L.types, B.h, prepped=True, ws=B.ws,
+            w16=f16[:2] if f16 and f16[0] is not None else None)
     down(B.h, B.G, L.wd, L.types[2], B.y, ws=B.ws, w16=f16[2] if f16 else None)
-    shared = gate = None
     if L.shared is not None:
-        sg, su, sd = L.shared
-        gate_up(B.xh, B.Gs, 1, sg, su, L.types, B.hs, prepped=True)
-        down(B.hs, B.Gs, sd, L.types[2], B.ys)
-        shared = ptr(B.ys)
-        gate = ctypes.c_void_p(B.logits.data_ptr() + L.E * B.logits.element_size())
+        torch.cuda.current_stream().wait_event(B.shared_done)
     call("lmoe_combine_sorted", ptr(B.y), _lib.F16, ptr(B.G.inv), ptr(B.scores), T, L.k, H, shared, gate,
-         stride if shared is not None else 0, ptr(residual), dcode(residual.dtype) if residual is not None else 0,
+         1 if shared is not None else 0, ptr(residual), dcode(residual.dtype) if residual is not None else 0,
          ptr(out), dcode(out.dtype), st)
     return out
 

@@ -59,6 +59,24 @@ class MoELayer:
             wg, wu, wd = (f[:self.E] for f in self.folded)
         self.wg, self.wu, self.wd = wg, wu, wd
         self.prefill_f16 = None
+        self._router_k = None
+
+    def router_gemm_weight(self):
+        """The router weight, with the shared expert's gate row after it when there is a shared expert, as float16
+        [E (+ 1), H] in the grouped GEMMs' K order: the weight operand of the prefill router (lmoe_router_gemm),
+        converted on the first call and kept (f16 and bf16 weights convert exactly)."""
+        if self._router_k is None:
+            if self.wr is None:
+                raise ValueError("this layer has no router weight")
+            n = self.E + (1 if self.shared is not None else 0)
+            w = torch.empty((n, self.H), dtype=torch.float16, device=self.wr.device)
+            wr = self.wr.contiguous()
+            call("lmoe_to_gemm_f16", ptr(wr), dcode(wr.dtype), self.E * self.H, ptr(w), stream())
+            if self.shared is not None:
+                sg = self.wsg.contiguous()
+                call("lmoe_to_gemm_f16", ptr(sg), dcode(sg.dtype), self.H, ptr(w[self.E]), stream())
+            self._router_k = w
+        return self._router_k
 
     def keep_prefill_f16(self):
         """Hold the f16 K-order weights the grouped path needs for projections beyond Q4_0 / Q4_K (gate/up together,
