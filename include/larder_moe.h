@@ -200,8 +200,8 @@ int lmoe_grouped_tile_rows(void);
 /* The tuned launch choices for the grouped GEMMs, so every caller makes the same ones (no counterpart in the
  * reference, whose dense path has no tile size; gguf_experts.py:698-722 is the path they serve):
  * lmoe_grouped_pick_tile_rows: the grouping's bm for R rows over E experts with block types (type_g, type_u,
- *   type_d): 64 when gate/up runs on f16 weights (not Q4_0 / Q4_K, or gate and up of two types), 128 for a Q4
- *   gate/up with an f16 down, 32 when all three are Q4_0 and R < 16 E, else 128;
+ *   type_d): 64 when gate/up runs on f16 weights (not Q4_0 / Q4_K, or gate and up of two types) or is Q4_K, 128
+ *   for a Q4_0 gate/up with an f16 down, 32 when all three are Q4_0 and R < 16 E, else 128;
  * lmoe_grouped_pick_ksplit: split-K slices for one GEMM over K at that bm (4, 3 or 2 for 32-row tiles with
  *   R < 16 E, at least 4 K steps a slice; else 1);
  * lmoe_grouped_workspace_bytes: bytes of the ws that lmoe_grouped_gate_up_bm / lmoe_grouped_down_bm need with

@@ -1118,10 +1118,11 @@ using namespace lmoe;
 extern "C" int lmoe_grouped_tile_rows(void) { return GM; }
 
 // The tuned tile-row rule (measured on MI355X): 64 when gate/up runs on f16 weights (a type beyond Q4_0 / Q4_K, or
-// gate and up of two types: the f16-weight GEMM then fits two workgroups a CU; 2,048 x 8 rows 405 -> 377 us); 128
-// for a Q4 gate/up with an f16 down; 32 when every projection is Q4_0 and an expert averages fewer than 16 rows
-// (batched decode: each tile streams its expert's weights, and 32-row tiles keep five K steps in flight and allow
-// split-K; cfg4 116.6 -> 108.8 us); else 128 (Q4_K at 40 rows an expert: 64 and 32 rows were slower).
+// gate and up of two types: the f16-weight GEMM then fits two workgroups a CU; 2,048 x 8 rows 405 -> 377 us); 64
+// for a Q4_K gate/up (the direct-copy kernel k_grouped_q4_k_dma: cfg5 gate/up 545 -> 387 us, and as fast as 128
+// rows at 1,000 rows an expert); 128 for a Q4_0 gate/up with an f16 down; 32 when every projection is Q4_0 and an
+// expert averages fewer than 16 rows (batched decode: each tile streams its expert's weights, and 32-row tiles keep
+// five K steps in flight and allow split-K; cfg4 116.6 -> 108.8 us); else 128.
 extern "C" int lmoe_grouped_pick_tile_rows(int R, int E, int type_g, int type_u, int type_d) {
   auto q4 = [](int t) { return t == LMOE_Q4_0 || t == LMOE_Q4_K; };
   if (!(q4(type_g) && type_u == type_g)) return 64;

@@ -30,8 +30,8 @@ def pick_tile_rows(R, E, types):
     every projection is Q4_0 and the average expert has fewer than 16 rows (batched decode: few tiles have work,
     each streams its expert's weights, and 32-row tiles keep five K steps in flight and allow split-K; cfg4 116.6 ->
     108.8 us a step); 64 when gate/up runs on dequantized f16 weights (a type beyond Q4_0 / Q4_K, or gate and up of
-    two types: the f16-weight GEMM then fits two workgroups a CU, 2,048 x 8 rows 405 -> 377 us); otherwise 128
-    (on cfg5's Q4_K prefill, 40 rows an expert, 64 and 32 rows were slower: 1,367 and 1,546 us against 1,297)."""
+    two types: the f16-weight GEMM then fits two workgroups a CU, 2,048 x 8 rows 405 -> 377 us) and for Q4_K (the
+    direct-copy kernel: cfg5's gate/up 545 -> 387 us); otherwise 128."""
     return _lib.lib().lmoe_grouped_pick_tile_rows(int(R), int(E), *(qcode(t) for t in types))
 
 

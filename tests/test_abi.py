@@ -145,9 +145,10 @@ def test_grouped_launch_choices(built_lib):
     pick = lambda R, E, ts: built_lib.lmoe_grouped_pick_tile_rows(R, E, *(q(t) for t in ts))  # noqa: E731
     assert pick(8192 * 8, 128, ("Q4_0",) * 3) == 128      # cfg3 prefill
     assert pick(64 * 8, 128, ("Q4_0",) * 3) == 32         # cfg4 batched decode
-    assert pick(2048 * 10, 512, ("Q4_K",) * 3) == 128     # cfg5 prefill
-    assert pick(64, 512, ("Q4_K",) * 3) == 128            # few rows, Q4_K: no 32-row form
-    assert pick(64, 128, ("Q4_K", "Q4_K", "Q6_K")) == 128  # Q4 gate/up, f16 down
+    assert pick(2048 * 10, 512, ("Q4_K",) * 3) == 64      # cfg5 prefill: the direct-copy Q4_K kernel
+    assert pick(64, 512, ("Q4_K",) * 3) == 64             # few rows, Q4_K
+    assert pick(64, 128, ("Q4_K", "Q4_K", "Q6_K")) == 64   # Q4_K gate/up, f16 down
+    assert pick(64, 128, ("Q4_0", "Q4_0", "Q6_K")) == 128  # Q4_0 gate/up, f16 down
     for ts in (("Q8_0",) * 3, ("Q4_0", "Q4_K", "Q4_0"), ("Q6_K", "Q6_K", "Q4_K")):
         assert pick(2048 * 8, 128, ts) == 64              # gate/up on f16 weights
     assert grouped.pick_tile_rows(512, 128, ("Q4_0",) * 3) == 32
