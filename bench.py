@@ -144,9 +144,9 @@ def grouped_leg():
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) / n * 1e3
     flops = workloads.expert_flops(cfg, T * cfg["k"])
-    # per-kernel, kernel-exact, over 5 more passes (8 launches a pass: top-k, 3 grouping, f16 copy, gate/up,
-    # down, combine)
-    names = ["k_router_topk", "k_group_count", "k_group_scan", "k_group_scatter", "k_to_f16", "k_grouped<gate_up>",
+    # per-kernel, kernel-exact, over 5 more passes (8 launches a pass, in launch order: x to f16 in the K order,
+    # top-k, 3 grouping, gate/up, down, combine)
+    names = ["k_to_f16", "k_router_topk", "k_group_count", "k_group_scan", "k_group_scatter", "k_grouped<gate_up>",
              "k_grouped<down>", "k_combine_sorted"]
     M = 5 * len(names)
     _lib.call("lmoe_profile_arm", M)
