@@ -40,7 +40,9 @@ def tie_logits(rng, T, E):
 def test_router_topk_bit_exact(E, k, norm, dtype):
     from larder_amd import route
     rng = np.random.default_rng(E * 7 + k)
-    lg = tie_logits(rng, 67, E)
+    # tie-heavy rows, then all-negative rows in steps of 0.5 (the k-th key negative and tied)
+    neg = (-np.round(np.abs(rng.normal(0, 2.0, (16, E))) * 2) / 2 - 0.5).astype(np.float32)
+    lg = np.concatenate([tie_logits(rng, 67, E), neg])
     x = dev(lg).to(dtype)
     ids, sc = route.topk(x, k, norm)
     lg32 = host(x.float())
