@@ -273,7 +273,7 @@ __device__ __forceinline__ float key_logit(uint32_t key) {
 //   1. thr = the k-th largest key, by a 32-step bitwise search on the scalar unit: bit b stays set when at least k
 //      keys are >= the prefix (one compare a value and a ballot popcount a step);
 //   2. the picks are the keys above thr, then the lowest-index keys equal to thr up to k, compacted into LDS in
-//      index order;
+//      index order (a count other than k, impossible with the right threshold, sets every id to 0xFFFFFFFF);
 //   3. each pick's rank is the number of picks ahead of it, then a lane permute puts rank r in lane r.
 template <int NPL, bool SCORES = true>
 __device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm, uint32_t *lds, uint32_t *id_out,
@@ -325,6 +325,10 @@ __device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm
     eq_before += __popcll(eq);
     sel_before += __popcll(selm);
   }
+  // exactly k picks by construction (emulated on the CPU in tests/emul/topk_wave.cpp); any other count would mean a
+  // wrong threshold, and then every id of the token is 0xFFFFFFFF (no expert: zero rows downstream, and a mismatch
+  // in every parity test) instead of a silently truncated pick list
+  const bool bad = sel_before != k;
   __builtin_amdgcn_wave_barrier();
   // 3. ranks, then rank order
   uint32_t my_key = 0, my_idx = 0;
@@ -346,7 +350,7 @@ __device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm
   __builtin_amdgcn_wave_barrier();
   const int dst = (rank & 63) * 4;
   const uint32_t id = uint32_t(__builtin_amdgcn_ds_permute(dst, int(my_idx)));
-  *id_out = id;
+  *id_out = bad ? 0xFFFFFFFFu : id;
   if (!SCORES) return;
   const uint32_t kr = uint32_t(__builtin_amdgcn_ds_permute(dst, int(my_key)));
   float mine = lane < k ? __expf(key_logit(kr) - m) / s : 0.0f;

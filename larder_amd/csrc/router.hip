@@ -424,6 +424,7 @@ __device__ __forceinline__ void pick_mlx(const uint32_t (&key)[NPL], uint32_t th
     }
     sel_before += __popcll(selm);
   }
+  const bool bad = sel_before != k;  // exactly k by construction; otherwise every id is 0xFFFFFFFF (no expert)
   __builtin_amdgcn_wave_barrier();
   if (lane < k) {
     const uint32_t my_key = lds[lane], my_idx = lds[32 + lane];
@@ -437,8 +438,8 @@ __device__ __forceinline__ void pick_mlx(const uint32_t (&key)[NPL], uint32_t th
       for (int c = 0; c < 4; ++c)
         rank += (q0 + c < k && (kq[c] > my_key || (kq[c] == my_key && iq[c] > my_idx))) ? 1 : 0;
     }
-    *idx = my_idx;
-    *pos = k - 1 - rank;
+    *idx = bad ? 0xFFFFFFFFu : my_idx;
+    *pos = bad ? lane : k - 1 - rank;
   }
   __builtin_amdgcn_wave_barrier();
 }
