@@ -144,6 +144,20 @@ int lmoe_gemv_down_combine(const float *h, const uint32_t *ids, const float *sco
                            const float *gate, int gate_stride, const void *residual, int rdtype, void *out,
                            int odtype, void *stream);
 
+/* The decode chain on rows of one slot each (topk 1), with weight reuse: rows go in windows of up to run_rows
+ * (lowered to fit LDS), and a weight row is read once a run of equal consecutive slots in a window, so rows sorted
+ * by slot read each expert once a window instead of once a row. Per row the arithmetic is the chain's (same
+ * prepared units, unit dots and reduction tree), so h and out are meant to be bit-equal to lmoe_gemv_gate_up /
+ * lmoe_gemv_down_combine (k 1, no scores); the Python layer checks that once a shape before using them. Replace
+ * gguf_experts kernels gguf_gate_up_runs / gguf_down_runs (gguf_cuda.py:33-152) as driven by _gemv_runs
+ * (gguf_experts.py:632-658). Q4_0 / Q4_K only; slots >= n_experts give zero rows.
+ *   gate/up: x [n][H] in xdtype -> h [n][I] fp32;   down: h [n][I] fp32 -> out [n][H] in odtype, unweighted. */
+int lmoe_gemv_gate_up_runs(const void *x, int xdtype, const uint32_t *slots, int n, int run_rows, const uint8_t *wg,
+                           const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I, float *h,
+                           void *stream);
+int lmoe_gemv_down_runs(const float *h, const uint32_t *slots, int n, int run_rows, const uint8_t *wd, int type_d,
+                        int n_experts, int I, int H, void *out, int odtype, void *stream);
+
 /* lmoe_gemv_down_combine on h's prepared rows [T * k][I / 64 * 36] (has_sums 0: their half sums are derived from
  * the pairs, as lmoe_gemv_gate_up_prepped leaves them). */
 int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sums, const uint32_t *ids, const float *scores,

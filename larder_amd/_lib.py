@@ -46,6 +46,8 @@ SIGNATURES = {
     "lmoe_gemv_down_combine": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_gemv_down_combine_prepped": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I,
                                             _P]),
+    "lmoe_gemv_gate_up_runs": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
+    "lmoe_gemv_down_runs": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_group_workspace_bytes": (_SZ, [_I, _I]),
     "lmoe_group_rows": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "lmoe_group_rows_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),

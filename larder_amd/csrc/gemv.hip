@@ -681,6 +681,245 @@ __global__ void __launch_bounds__(256)
 
 // ---- host dispatch ----------------------------------------------------------------------------------------------
 
+// ---- the decode chain on runs of equal slots (one slot a row) ----------------------------------------------------
+//
+// The reference's run kernels (gguf_experts.py:600-607, gguf_cuda.py:33-152): rows of one slot each, best sorted by
+// slot, go through windows of up to TR rows; a wavefront loads its weight rows once a run of equal slots in the
+// window and reuses them for every row of the run. Per row the arithmetic is the chain's own (the same prepared
+// activation units, unit dots, partial layout and reduction tree as k_gate_up / k_down_combine at the same RB), so
+// the outputs are meant to be bit-equal to the chain's; the host checks that once a shape before using them.
+// Latency is what bounds both kernels (a few KB of weights a wavefront a run), so every round trip is overlapped:
+// the window's slot ids are read once, the first run's weights are in flight while the window's rows are prepared,
+// and each run's successor is fetched into registers while the run computes.
+
+// Rows [row0, row0 + nr) of x (64 P elements each, dtype dt, 16-byte aligned) as prepared units of block type TQ
+// into dst [nr][P XS]: the f16 values go straight from 16-byte global loads to their (dword, half) places, then the
+// half sums are read back from them in element order, which gives prep_dword's bits without staging the raw rows.
+// Ends with a workgroup barrier.
+template <int TQ>
+__device__ __forceinline__ void prep_rows(const void *x, int dt, size_t row0, int nr, int P, uint32_t *dst, int tid,
+                                          int nthr) {
+  constexpr int HS = TQ == LMOE_Q4_K ? 32 : 16;
+  const int esz = dt == LMOE_F32 ? 4 : 2, per = 16 / esz;  // elements a 16-byte chunk
+  const int cpr = 64 * P / per;                              // chunks a row
+  const int n = nr * cpr;
+  const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const char *>(x) + row0 * 64 * P * esz);
+  for (int b = tid; b < n; b += 8 * nthr) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = src[min(b + j * nthr, n - 1)];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = b + j * nthr;
+      if (c < n) {
+        const int r = c / cpr, i0 = (c - r * cpr) * per;
+        _Float16 *row = reinterpret_cast<_Float16 *>(dst + r * P * XS);
+        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        for (int k = 0; k < per; ++k) {
+          float f;
+          if (dt == LMOE_F32) {
+            f = __uint_as_float(w[k]);
+          } else {
+            const uint16_t bits = uint16_t(w[k >> 1] >> (16 * (k & 1)));
+            f = dt == LMOE_F16 ? float(__builtin_bit_cast(_Float16, bits)) : bf16_to_f32(bits);
+          }
+          const int i = i0 + k;
+          int dw, half;
+          xslot(i & 63, HS, &dw, &half);
+          row[2 * ((i >> 6) * XS + dw) + half] = _Float16(f);
+        }
+      }
+    }
+  }
+  for (int q = tid; q < nr * P; q += nthr) {
+    dst[q * XS + 34] = 0u;
+    dst[q * XS + 35] = 0u;
+  }
+  __syncthreads();
+  for (int hu = tid; hu < nr * P * 2; hu += nthr) {
+    const int q = hu >> 1, half = hu & 1;
+    const _Float16 *u = reinterpret_cast<const _Float16 *>(dst + q * XS);
+    float s = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      int dw, hf;
+      xslot(32 * half + j, HS, &dw, &hf);
+      s += float(u[2 * dw + hf]);
+    }
+    dst[q * XS + 32 + half] = __builtin_bit_cast(uint32_t, s);
+  }
+  __syncthreads();
+}
+
+constexpr int kRunQ = 4;  // rows of a run whose unit dots go out in one loop
+
+// Gate/up: grid (ceil(I / (RB NW)), ceil(n / TR)); wavefront w of block (bx, y) takes gate and up rows
+// [(bx NW + w) RB, +RB) for rows [y TR, +TR) of x. LDS: the window's prepared rows (gate's, then up's when the types
+// differ), its slot ids, each wavefront's 2 RB staged weight rows, then each wavefront's partials of kRunQ rows.
+// NC >= ceil(RB 9 P / 4 / 64) 16-byte chunks a lane a matrix.
+template <int TG, int TU, int RB, int NW, int NC>
+__global__ void __launch_bounds__(64 * NW)
+    k_gate_up_runs(const void *x, int xdt, const uint32_t *slots, int n, int tr, const uint8_t *wg,
+                   const uint8_t *wu, int n_experts, int I, int P, float *h) {
+  constexpr bool SAME = TG == TU;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r0 = (blockIdx.x * NW + wave) * RB;
+  const int e0 = blockIdx.y * tr, ne = min(tr, n - e0);
+  const int stage_dw = 2 * RB * 9 * P, U = 2 * RB * P, RL = 2 * RB * (P + 1);
+  extern __shared__ u32x4 lds4[];
+  uint32_t *xg = reinterpret_cast<uint32_t *>(lds4);
+  uint32_t *xu = SAME ? xg : xg + tr * P * XS;
+  uint32_t *sl = xu + tr * P * XS;
+  uint32_t *stage = sl + ((tr + 3) & ~3) + wave * stage_dw;
+  float *red = reinterpret_cast<float *>(sl + ((tr + 3) & ~3) + NW * stage_dw) + wave * kRunQ * RL;
+
+  // the first run's rows into registers, unpredicated (a wavefront past the rows reads the last row block, an id
+  // past the experts expert 0's), while the window is prepared
+  const int C = RB * 9 * P / 4;
+  const size_t rowb = size_t(36) * P;
+  const int rs = min(r0, I - RB);
+  u32x4 vg[NC], vu[NC];
+  auto fetch = [&](uint32_t e) {
+    const size_t base = (size_t(e < uint32_t(n_experts) ? e : 0u) * I + rs) * rowb;
+    const u32x4 *gs = reinterpret_cast<const u32x4 *>(wg + base);
+    const u32x4 *us = reinterpret_cast<const u32x4 *>(wu + base);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = min(lane + 64 * i, C - 1);
+      vg[i] = __builtin_nontemporal_load(gs + c);
+      vu[i] = __builtin_nontemporal_load(us + c);
+    }
+  };
+  fetch(slots[e0]);
+  if (int(threadIdx.x) < ne) sl[threadIdx.x] = slots[e0 + threadIdx.x];
+  prep_rows<TG>(x, xdt, e0, ne, P, xg, threadIdx.x, 64 * NW);
+  if (!SAME) prep_rows<TU>(x, xdt, e0, ne, P, xu, threadIdx.x, 64 * NW);
+  if (r0 >= I) return;
+
+  u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
+  constexpr int LPR = 64 / (2 * RB);
+  const int rr = lane / LPR, sub = lane % LPR;
+  for (int r = 0; r < ne;) {
+    const uint32_t e = sl[r];
+    int r1 = r + 1;  // the run: rows [r, r1) of slot e
+    while (r1 < ne && sl[r1] == e) ++r1;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = lane + 64 * i;
+      if (c < C) {
+        st4[c] = vg[i];
+        st4[C + c] = vu[i];
+      }
+    }
+    if (r1 < ne) fetch(sl[r1]);  // the next run's rows, in flight during this one
+    __builtin_amdgcn_wave_barrier();
+    if (e >= uint32_t(n_experts)) {  // no such expert: zero rows (cpu_kern.cpp:316-318)
+      for (int q = r; q < r1; ++q)
+        if (lane < RB) h[size_t(e0 + q) * I + r0 + lane] = 0.0f;
+      r = r1;
+      continue;
+    }
+    for (int q0 = r; q0 < r1; q0 += kRunQ) {
+      const int nq = min(kRunQ, r1 - q0);
+#pragma unroll 2
+      for (int v = lane; v < nq * U; v += 64) {
+        const int q = v / U, u = v - q * U;
+        const int row = u / P, p = u - row * P;
+        float part;
+        if (row < RB)
+          part = row_unit_dot<TG>(stage + row * 9 * P, p, xg + ((q0 + q) * P + p) * XS);
+        else
+          part = row_unit_dot<TU>(stage + row * 9 * P, p, xu + ((q0 + q) * P + p) * XS);
+        red[q * RL + row * (P + 1) + p] = part;
+      }
+      __builtin_amdgcn_wave_barrier();
+      for (int q = 0; q < nq; ++q) {
+        float acc = 0.0f;
+        for (int p = sub; p < P; p += LPR) acc += red[q * RL + rr * (P + 1) + p];
+        acc = LPR == 8 ? sum8(acc) : sum16(acc);
+        const float up = lane_xor32(acc);
+        if (rr < RB && sub == 0) h[size_t(e0 + q0 + q) * I + r0 + rr] = silu_mul(acc, up);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    r = r1;
+  }
+}
+
+// Down of the same windows, unweighted: grid (ceil(H / (RB NW)), ceil(n / TR)); wavefront w of block (bx, y) takes
+// output rows [(bx NW + w) RB, +RB) for h rows [y TR, +TR). LDS: the window's prepared h rows, its slot ids, each
+// wavefront's RB staged weight rows, then each wavefront's partials of kRunQ rows.
+template <int TD, int RB, int NW, int NC>
+__global__ void __launch_bounds__(64 * NW)
+    k_down_runs(const float *h, const uint32_t *slots, int n, int tr, const uint8_t *wd, int n_experts, int I, int H,
+                void *out, int odt) {
+  const int P = I / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * NW + wave) * RB;
+  const int e0 = blockIdx.y * tr, ne = min(tr, n - e0);
+  const int stage_dw = RB * 9 * P, red_ld = P + 1, U = RB * P, RL = RB * red_ld;
+  extern __shared__ u32x4 lds4[];
+  uint32_t *hx = reinterpret_cast<uint32_t *>(lds4);
+  uint32_t *sl = hx + tr * P * XS;
+  uint32_t *stage = sl + ((tr + 3) & ~3) + wave * stage_dw;
+  float *red = reinterpret_cast<float *>(sl + ((tr + 3) & ~3) + NW * stage_dw) + wave * kRunQ * RL;
+
+  const size_t rowb = size_t(36) * P;
+  const int C = RB * 9 * P / 4;
+  const int ns = min(n0, H - RB);
+  u32x4 v[NC];
+  auto fetch = [&](uint32_t e) {
+    const u32x4 *src =
+        reinterpret_cast<const u32x4 *>(wd + (size_t(e < uint32_t(n_experts) ? e : 0u) * H + ns) * rowb);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) v[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, C - 1));
+  };
+  fetch(slots[e0]);
+  if (int(threadIdx.x) < ne) sl[threadIdx.x] = slots[e0 + threadIdx.x];
+  prep_rows<TD>(h, LMOE_F32, e0, ne, P, hx, threadIdx.x, 64 * NW);
+  if (n0 >= H) return;
+
+  u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
+  constexpr int LPR = 64 / RB;
+  const int rr = lane / LPR, sub = lane % LPR;
+  for (int r = 0; r < ne;) {
+    const uint32_t e = sl[r];
+    int r1 = r + 1;
+    while (r1 < ne && sl[r1] == e) ++r1;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+      if (lane + 64 * i < C) st4[lane + 64 * i] = v[i];
+    if (r1 < ne) fetch(sl[r1]);
+    __builtin_amdgcn_wave_barrier();
+    if (e >= uint32_t(n_experts)) {
+      for (int q = r; q < r1; ++q)
+        if (sub == 0) store_elt(out, size_t(e0 + q) * H + n0 + rr, 0.0f, odt);
+      r = r1;
+      continue;
+    }
+    for (int q0 = r; q0 < r1; q0 += kRunQ) {
+      const int nq = min(kRunQ, r1 - q0);
+#pragma unroll 2
+      for (int w = lane; w < nq * U; w += 64) {
+        const int q = w / U, u = w - q * U;
+        const int row = u / P, p = u - row * P;
+        red[q * RL + row * red_ld + p] = row_unit_dot<TD>(stage + row * 9 * P, p, hx + ((q0 + q) * P + p) * XS);
+      }
+      __builtin_amdgcn_wave_barrier();
+      for (int q = 0; q < nq; ++q) {
+        float acc = 0.0f;
+        for (int i = sub; i < P; i += LPR) acc += red[q * RL + rr * red_ld + i];
+        acc = sum16(acc);
+        if (LPR == 32) acc += lane_xor16(acc);
+        if (sub == 0) store_elt(out, size_t(e0 + q0 + q) * H + n0 + rr, acc, odt);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    r = r1;
+  }
+}
+
 struct GateUpArgs {
   const uint32_t *xg_prep, *xu_prep;
   const void *x;
@@ -909,6 +1148,123 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   return 0;
 }
 
+// Rows a window of the run kernels: `want` (1..64), lowered until the window's LDS fits `cap` bytes.
+static int runs_window(int want, size_t fixed, size_t per_row, size_t cap) {
+  int tr = std::min(std::max(want, 1), 64);
+  while (tr > 1 && fixed + per_row * tr > cap) --tr;
+  return tr;
+}
+
+// 16-byte chunks a lane a matrix the run kernels hold for c chunks a wavefront: a compiled count at or above it
+static int runs_nc(int c) {
+  const int nc = (c + 63) / 64;
+  return nc <= 1 ? 1 : nc <= 2 ? 2 : nc <= 3 ? 3 : nc <= 5 ? 5 : nc <= 6 ? 6 : nc <= 9 ? 9 : 0;
+}
+
+template <int TG, int TU, int RB, int NW>
+static int launch_gate_up_runs(int nc, dim3 grid, size_t lds, hipStream_t st, const void *x, int xdt,
+                               const uint32_t *slots, int n, int tr, const uint8_t *wg, const uint8_t *wu,
+                               int n_experts, int I, int P, float *h) {
+  const char *fn = "lmoe_gemv_gate_up_runs";
+  auto go = [&](auto kern) {
+    if (int rc = allow_lds(kern, lds, fn)) return rc;
+    launch(kern, grid, dim3(64 * NW), lds, st, x, xdt, slots, n, tr, wg, wu, n_experts, I, P, h);
+    LMOE_LAUNCHED(fn);
+    return 0;
+  };
+  switch (nc) {
+    case 1: return go(k_gate_up_runs<TG, TU, RB, NW, 1>);
+    case 2: return go(k_gate_up_runs<TG, TU, RB, NW, 2>);
+    case 3: return go(k_gate_up_runs<TG, TU, RB, NW, 3>);
+    case 5: return go(k_gate_up_runs<TG, TU, RB, NW, 5>);
+    case 6: return go(k_gate_up_runs<TG, TU, RB, NW, 6>);
+    default: return go(k_gate_up_runs<TG, TU, RB, NW, 9>);
+  }
+}
+
+static int gate_up_runs(const void *x, int xdt, const uint32_t *slots, int n, int tr_want, const uint8_t *wg,
+                        const uint8_t *wu, int tg, int tu, int n_experts, int H, int I, float *h, hipStream_t st) {
+  const char *fn = "lmoe_gemv_gate_up_runs";
+  LMOE_REQUIRE(dtype_ok(xdt), LMOE_EINVAL, "%s: x dtype %d is not F32, F16 or BF16", fn, xdt);
+  LMOE_REQUIRE(qtype_ok(tg) && qtype_ok(tu), LMOE_ETYPE, "%s: the run kernels take Q4_0 / Q4_K (got %d/%d)", fn, tg,
+               tu);
+  LMOE_REQUIRE(n_experts > 0 && n >= 0 && tr_want >= 1, LMOE_ESHAPE, "%s: %d experts, %d rows, window %d", fn,
+               n_experts, n, tr_want);
+  if (int rc = check_matrix(fn, tg, I, H, wg)) return rc;
+  if (int rc = check_matrix(fn, tu, I, H, wu)) return rc;
+  constexpr int NW = 4;
+  const int P = H / 64, RB = P % 2 == 0 ? 2 : 4;
+  const int nc = runs_nc(RB * 9 * P / 4);
+  LMOE_REQUIRE(nc > 0, LMOE_ESHAPE, "%s: hidden %d needs more weight chunks a lane than the run kernels hold", fn, H);
+  if (n == 0) return 0;
+  LMOE_REQUIRE(x && slots && h && aligned16(x), LMOE_EALIGN, "%s: null or unaligned pointer", fn);
+  const size_t prow = size_t(P) * XS * (tg == tu ? 1 : 2), stage = size_t(NW) * 2 * RB * 9 * P;
+  const size_t red = size_t(NW) * kRunQ * 2 * RB * (P + 1);
+  const int tr = runs_window(tr_want, 4 * (stage + red + 64), 4 * prow, 80 * 1024);
+  const size_t lds = 4 * (tr * prow + ((tr + 3) & ~3) + stage + red);
+  LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "%s: hidden %d needs %zu bytes of LDS", fn, H, lds);
+  const dim3 grid((I + RB * NW - 1) / (RB * NW), (n + tr - 1) / tr);
+  constexpr int Q0 = LMOE_Q4_0, QK = LMOE_Q4_K;
+  auto go = [&](auto g, auto u, auto rb) {
+    constexpr int G = decltype(g)::value, UU = decltype(u)::value, R = decltype(rb)::value;
+    return launch_gate_up_runs<G, UU, R, NW>(nc, grid, lds, st, x, xdt, slots, n, tr, wg, wu, n_experts, I, P, h);
+  };
+  using T0 = std::integral_constant<int, Q0>;
+  using TK = std::integral_constant<int, QK>;
+  using R2 = std::integral_constant<int, 2>;
+  using R4 = std::integral_constant<int, 4>;
+  if (RB == 2) {
+    if (tg == Q0) return tu == Q0 ? go(T0(), T0(), R2()) : go(T0(), TK(), R2());
+    return tu == Q0 ? go(TK(), T0(), R2()) : go(TK(), TK(), R2());
+  }
+  if (tg == Q0) return tu == Q0 ? go(T0(), T0(), R4()) : go(T0(), TK(), R4());
+  return tu == Q0 ? go(TK(), T0(), R4()) : go(TK(), TK(), R4());
+}
+
+static int down_runs(const float *h, const uint32_t *slots, int n, int tr_want, const uint8_t *wd, int td,
+                     int n_experts, int I, int H, void *out, int odt, hipStream_t st) {
+  const char *fn = "lmoe_gemv_down_runs";
+  LMOE_REQUIRE(dtype_ok(odt), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(qtype_ok(td), LMOE_ETYPE, "%s: the run kernels take Q4_0 / Q4_K (got %d)", fn, td);
+  LMOE_REQUIRE(n_experts > 0 && n >= 0 && tr_want >= 1, LMOE_ESHAPE, "%s: %d experts, %d rows, window %d", fn,
+               n_experts, n, tr_want);
+  if (int rc = check_matrix(fn, td, H, I, wd)) return rc;
+  constexpr int NW = 4;
+  const int P = I / 64, RB = P % 2 == 0 ? 2 : 4;
+  const int nc = runs_nc(RB * 9 * P / 4);
+  LMOE_REQUIRE(nc > 0, LMOE_ESHAPE, "%s: width %d needs more weight chunks a lane than the run kernels hold", fn, I);
+  if (n == 0) return 0;
+  LMOE_REQUIRE(h && slots && out && aligned16(h), LMOE_EALIGN, "%s: null or unaligned pointer", fn);
+  const size_t prow = size_t(P) * XS, stage = size_t(NW) * RB * 9 * P, red = size_t(NW) * kRunQ * RB * (P + 1);
+  const int tr = runs_window(tr_want, 4 * (stage + red + 64), 4 * prow, 80 * 1024);
+  const size_t lds = 4 * (tr * prow + ((tr + 3) & ~3) + stage + red);
+  LMOE_REQUIRE(lds <= 160 * 1024, LMOE_ESHAPE, "%s: width %d needs %zu bytes of LDS", fn, I, lds);
+  const dim3 grid((H + RB * NW - 1) / (RB * NW), (n + tr - 1) / tr);
+  auto go = [&](auto kern) {
+    if (int rc = allow_lds(kern, lds, fn)) return rc;
+    launch(kern, grid, dim3(64 * NW), lds, st, h, slots, n, tr, wd, n_experts, I, H, out, odt);
+    LMOE_LAUNCHED(fn);
+    return 0;
+  };
+  auto by_nc = [&](auto td_, auto rb) {
+    constexpr int D = decltype(td_)::value, R = decltype(rb)::value;
+    switch (nc) {
+      case 1: return go(k_down_runs<D, R, NW, 1>);
+      case 2: return go(k_down_runs<D, R, NW, 2>);
+      case 3: return go(k_down_runs<D, R, NW, 3>);
+      case 5: return go(k_down_runs<D, R, NW, 5>);
+      case 6: return go(k_down_runs<D, R, NW, 6>);
+      default: return go(k_down_runs<D, R, NW, 9>);
+    }
+  };
+  using T0 = std::integral_constant<int, LMOE_Q4_0>;
+  using TK = std::integral_constant<int, LMOE_Q4_K>;
+  using R2 = std::integral_constant<int, 2>;
+  using R4 = std::integral_constant<int, 4>;
+  if (td == LMOE_Q4_0) return RB == 2 ? by_nc(T0(), R2()) : by_nc(T0(), R4());
+  return RB == 2 ? by_nc(TK(), R2()) : by_nc(TK(), R4());
+}
+
 }  // namespace lmoe
 
 using namespace lmoe;
@@ -989,4 +1345,16 @@ extern "C" int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sum
   DownArgs a{hprep, has_sums, nullptr, ids, scores, T, k, wd, type_d, n_experts, I, H, shared, gate, gate_stride,
              residual, rdtype, out, odtype};
   return down("lmoe_gemv_down_combine_prepped", a, stream);
+}
+
+extern "C" int lmoe_gemv_gate_up_runs(const void *x, int xdtype, const uint32_t *slots, int n, int run_rows,
+                                      const uint8_t *wg, const uint8_t *wu, int type_g, int type_u, int n_experts,
+                                      int H, int I, float *h, void *stream) {
+  return gate_up_runs(x, xdtype, slots, n, run_rows, wg, wu, type_g, type_u, n_experts, H, I, h,
+                      (hipStream_t)stream);
+}
+
+extern "C" int lmoe_gemv_down_runs(const float *h, const uint32_t *slots, int n, int run_rows, const uint8_t *wd,
+                                   int type_d, int n_experts, int I, int H, void *out, int odtype, void *stream) {
+  return down_runs(h, slots, n, run_rows, wd, type_d, n_experts, I, H, out, odtype, (hipStream_t)stream);
 }

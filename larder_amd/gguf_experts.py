@@ -3,7 +3,7 @@ surface of the reference's gguf_experts module (gguf_experts.py:573-819) over to
 liblarder_moe.so.
 
     experts(x, bufs, rhs, types, host=None)    gguf_experts.py:803-819
-    gemv(x, w, slots, topk, types, out_dtype)  gguf_experts.py:600-607  (the decode chain)
+    gemv(x, w, slots, topk, types, out_dtype)  gguf_experts.py:600-607  (the decode chain, or the run kernels)
     dense(x, w, host, types, out_dtype)        gguf_experts.py:698-722  (the grouped path)
     dequant(buf, slots, t, dtype), dims(buf, t) gguf_experts.py:573-586
     calibrate(hid, inter, types), dense_pays(u, p) gguf_experts.py:771-800
@@ -24,7 +24,8 @@ import torch
 from . import _lib
 from ._lib import TYPES, call, dcode, ptr, qcode, stream
 
-__all__ = ["TYPES", "dims", "dequant", "gemv", "dense", "experts", "calibrate", "dense_pays", "calib_dir"]
+__all__ = ["TYPES", "dims", "dequant", "gemv", "dense", "experts", "calibrate", "dense_pays", "calib_dir", "runs_on",
+           "run_rows"]
 
 
 def _types(types):
@@ -81,11 +82,93 @@ def _chain(x, w, slots, topk, types, out_dtype):
     return h, y
 
 
+def runs_on():
+    """LMOE_GGUF_RUNS, read on every call (the reference's MOE_GGUF_RUNS, gguf_experts.py:590-596): on unless "0".
+    When on, gemv() on rows of one slot each goes through the run kernels, once _runs_ok() has found them bit-equal
+    to the chain at that shape."""
+    return os.environ.get("LMOE_GGUF_RUNS", "1") != "0"
+
+
+def run_rows():
+    """LMOE_GGUF_RUN_ROWS: rows a window of the run kernels (the reference's MOE_GGUF_RUN_TILE window, default 4, the
+    fastest measured on sorted and unsorted rows; the library lowers it to fit LDS). No bit depends on it."""
+    return max(1, int(os.environ.get("LMOE_GGUF_RUN_ROWS", "4")))
+
+
+def _gemv_runs(x, w, slots, types, out_dtype):
+    """gemv() on rows of one slot each (best sorted by slot) through the run kernels: a window of rows reads a weight
+    row once a run of equal slots; returns (h float32 [n, I], y [n, H] in out_dtype) (gguf_experts.py:632-658)."""
+    bg, bu, bd = w
+    tg, tu, td = types
+    inter, hid = dims(bg, tg)
+    s = _slots_u32(slots)
+    n = s.numel()
+    x = x.contiguous()
+    h = torch.empty((n, inter), dtype=torch.float32, device=x.device)
+    y = torch.empty((n, hid), dtype=out_dtype, device=x.device)
+    tr = run_rows()
+    call("lmoe_gemv_gate_up_runs", ptr(x), dcode(x.dtype), ptr(s), n, tr, ptr(bg), ptr(bu), qcode(tg), qcode(tu),
+         bg.shape[0], hid, inter, ptr(h), stream())
+    call("lmoe_gemv_down_runs", ptr(h), ptr(s), n, tr, ptr(bd), qcode(td), bd.shape[0], inter, hid, ptr(y),
+         dcode(out_dtype), stream())
+    return h, y
+
+
+# (hid, inter, types, x dtype, out dtype) -> whether the run kernels passed their check there
+_RUNS_OK = {}
+
+
+def _same_bits(a, b):
+    if a.shape != b.shape or a.dtype != b.dtype:
+        return False
+    u = {4: torch.int32, 2: torch.int16}[a.element_size()]
+    return bool(torch.equal(a.contiguous().view(u), b.contiguous().view(u)))
+
+
+def _runs_ok(hid, inter, types, x_dtype, out_dtype):
+    """Whether the run kernels may stand in for the chain at these shapes and dtypes: checked once (the reference's
+    _runs_ok, gguf_experts.py:661-680), on random experts of these types and rows in runs of 1 to 16 equal slots,
+    some past the experts; on only if h and the outputs are bit-equal to the chain's. Types beyond Q4_0 / Q4_K have
+    no run kernels and always take the chain."""
+    key = (hid, inter, tuple(types), x_dtype, out_dtype)
+    if key in _RUNS_OK:
+        return _RUNS_OK[key]
+    if any(t not in _lib.Q4_TYPES for t in types):
+        _RUNS_OK[key] = False
+        return False
+    _RUNS_OK[key] = False
+    try:
+        g = torch.Generator(device="cuda").manual_seed(hid * 7 + inter)
+        n_exp = 6
+        w = tuple(_random_q4(n_exp, r, c, t, g)
+                  for (r, c), t in zip(((inter, hid), (inter, hid), (hid, inter)), types))
+        lens = torch.randperm(16, generator=g, device="cuda").cpu() + 1
+        ids = torch.randint(0, n_exp + 1, (16,), generator=g, device="cuda").cpu()  # id n_exp: no such expert
+        slots = torch.repeat_interleave(ids, lens).to(device="cuda", dtype=torch.int32)
+        x = torch.randn((slots.numel(), hid), generator=g, device="cuda").to(x_dtype)
+        want = _chain(x, w, slots, 1, types, out_dtype)
+        got = _gemv_runs(x, w, slots, types, out_dtype)
+        ok = all(map(_same_bits, want, got))
+        why = "" if ok else "they differ from the decode chain"
+    except (RuntimeError, ValueError) as e:  # a refusal at this shape
+        ok, why = False, f"{type(e).__name__}: {str(e)[:200]}"
+    _RUNS_OK[key] = ok
+    print(f"larder_amd: run kernels at {hid}x{inter} {'/'.join(types)} "
+          f"{'on, bit-equal to the decode chain' if ok else 'off: ' + why}", flush=True)
+    return ok
+
+
 def gemv(x, w, slots, topk, types, out_dtype):
     """Every slot's expert output, unweighted: x (rows, hidden), slots (rows * topk,) with slot s on row s // topk,
-    w the gate, up and down buffers [S, rows, row bytes] in ``types``; returns (rows * topk, hidden) in out_dtype
-    (gguf_experts.py:600-607)."""
-    return _chain(x, w, slots, topk, _types(types), out_dtype)[1]
+    w the gate, up and down buffers [S, rows, row bytes] in ``types``; returns (rows * topk, hidden) in out_dtype,
+    through the run kernels at one slot a row when runs_on() and they passed their check (gguf_experts.py:600-607)."""
+    types = _types(types)
+    n = slots.numel()
+    if topk == 1 and n > 1 and runs_on():
+        inter, hid = dims(w[0], types[0])
+        if _runs_ok(hid, inter, types, x.dtype, out_dtype):
+            return _gemv_runs(x, w, slots, types, out_dtype)[1]
+    return _chain(x, w, slots, topk, types, out_dtype)[1]
 
 
 def dense(x, w, host, types, out_dtype):

@@ -82,6 +82,22 @@ def test_refusals_without_a_gpu(built_lib):
     rc = L.lmoe_quantize_q4_0(p, _lib.F32, 4, 33, p, None)
     assert rc == _lib.ESHAPE
     assert L.lmoe_max_tiles(65536, 128, 128) == 512 + 128
+    # the run kernels: Q4_0 / Q4_K only, a window of at least one row, aligned rows
+    rc = L.lmoe_gemv_gate_up_runs(p, _lib.F16, p, 8, 8, p, p, 14, 14, 128, 2048, 768, p, None)
+    assert rc == _lib.ETYPE and b"run kernels" in L.lmoe_error()
+    rc = L.lmoe_gemv_gate_up_runs(p, _lib.F16, p, 8, 0, p, p, _lib.Q4_0, _lib.Q4_0, 128, 2048, 768, p, None)
+    assert rc == _lib.ESHAPE and b"window 0" in L.lmoe_error()
+    rc = L.lmoe_gemv_gate_up_runs(ctypes.c_void_p(18), _lib.F16, p, 8, 8, p, p, _lib.Q4_0, _lib.Q4_0, 128, 2048, 768,
+                                  p, None)
+    assert rc == _lib.EALIGN
+    rc = L.lmoe_gemv_gate_up_runs(p, _lib.F16, p, 0, 8, p, p, _lib.Q4_0, _lib.Q4_0, 128, 2048, 768, p, None)
+    assert rc == 0   # no rows: nothing to launch
+    rc = L.lmoe_gemv_down_runs(p, p, 8, 8, p, 8, 128, 768, 2048, p, _lib.F16, None)
+    assert rc == _lib.ETYPE and b"run kernels" in L.lmoe_error()
+    rc = L.lmoe_gemv_down_runs(p, p, 8, 8, p, _lib.Q4_K, 128, 640, 2048, p, _lib.F16, None)
+    assert rc == _lib.ESHAPE and b"256" in L.lmoe_error()
+    rc = L.lmoe_gemv_down_runs(p, p, 8, 8, p, _lib.Q4_0, 128, 768, 2048, p, 9, None)
+    assert rc == _lib.EINVAL
 
 
 def test_grouped_refusals_without_a_gpu(built_lib):
