@@ -25,6 +25,7 @@
 //     registers and h leaves as f16 in grouped row order. Down writes y [R][H] (f16 or f32) in grouped order.
 // Operands are f16 with fp32 accumulation. A single rounding of (q - 8) d to f16 keeps the layer well inside the
 // 2e-3 relative L2 bar; bf16 operands would not.
+#include <cstdlib>
 #include <type_traits>
 
 #include "lmoe_common.h"
@@ -1123,8 +1124,20 @@ extern "C" int lmoe_grouped_tile_rows(void) { return GM; }
 // rows at 1,000 rows an expert); 128 for a Q4_0 gate/up with an f16 down; 32 when every projection is Q4_0 and an
 // expert averages fewer than 16 rows (batched decode: each tile streams its expert's weights, and 32-row tiles keep
 // five K steps in flight and allow split-K; cfg4 116.6 -> 108.8 us); else 128.
+// LMOE_TILE_ROWS and LMOE_KSPLIT override the two rules below (knobs of the kind of the reference's MOE_GGUF_RUN_TILE,
+// gguf_experts.py:590-596, for measuring other tilings). They are read on every call and ignored when the value is
+// not one the GEMMs take for these types: tile rows 32 (Q4 projections only), 64 or 128; split-K 1 to 8 slices that
+// divide the K steps, on 32-row tiles of at most 65,535 rows.
+static int env_knob(const char *name) {
+  const char *v = getenv(name);
+  return v && *v ? atoi(v) : 0;
+}
+
 extern "C" int lmoe_grouped_pick_tile_rows(int R, int E, int type_g, int type_u, int type_d) {
   auto q4 = [](int t) { return t == LMOE_Q4_0 || t == LMOE_Q4_K; };
+  const int want = env_knob("LMOE_TILE_ROWS");
+  const bool f16w = !(q4(type_g) && type_u == type_g) || !q4(type_d);  // a GEMM on dequantized f16 weights
+  if (want == GM || want == 64 || (want == 32 && !f16w)) return want;
   if (!(q4(type_g) && type_u == type_g)) return 64;
   if (type_g == LMOE_Q4_K) return 64;
   if (!q4(type_d)) return GM;
@@ -1137,6 +1150,8 @@ extern "C" int lmoe_grouped_pick_tile_rows(int R, int E, int type_g, int type_u,
 // each; otherwise 1.
 extern "C" int lmoe_grouped_pick_ksplit(int R, int E, int bm, int K) {
   const int steps = K / GK;
+  const int want = env_knob("LMOE_KSPLIT");
+  if (want == 1 || (want > 1 && want <= 8 && bm == 32 && steps % want == 0 && R <= 65535)) return want;
   if (bm != 32 || E <= 0 || (long long)R >= 16LL * E) return 1;
   for (int s = 4; s >= 2; --s)
     if (steps % s == 0 && steps / s >= 4) return s;

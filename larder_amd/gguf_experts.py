@@ -318,11 +318,18 @@ def dense_pays(u, p):
     return c is not None and c[2] + c[3] * u + c[4] * p < c[0] + c[1] * p
 
 
+def _dense_knob(rule):
+    """LMOE_DENSE, read on every call: "1" sends every call with ``host`` to dense(), "0" none, unset (or anything
+    else) leaves it to rule() (dense_pays)."""
+    v = os.environ.get("LMOE_DENSE", "")
+    return True if v == "1" else False if v == "0" else rule()
+
+
 def experts(x, bufs, rhs, types, host=None):
     """The routed experts' outputs, x (..., 1, hidden) broadcast against rhs (...) slot ids, bufs the
     (gguf part, [pad part]) buffers of gate, up and down, types their ggml types; returns rhs.shape + (1, hidden)
-    in x's dtype. With ``host`` (the slots, one row of x a slot) dense_pays() may pick the grouped path
-    (gguf_experts.py:803-819)."""
+    in x's dtype. With ``host`` (the slots, one row of x a slot) dense_pays() may pick the grouped path, or
+    LMOE_DENSE forces the choice (gguf_experts.py:803-819)."""
     types = _types(types)
     hid = x.shape[-1]
     x2 = x.reshape(-1, hid)
@@ -331,7 +338,7 @@ def experts(x, bufs, rhs, types, host=None):
         host = torch.as_tensor(host).reshape(-1)
         if not (host.numel() == x2.shape[0] == rhs.numel()):
             raise ValueError("dense: one row of x per slot")
-        if dense_pays(int(torch.unique(host).numel()), host.numel()):
+        if _dense_knob(lambda: dense_pays(int(torch.unique(host).numel()), host.numel())):
             return dense(x2, w, host, types, x.dtype).reshape(tuple(rhs.shape) + (1, hid))
     y = gemv(x2, w, rhs.reshape(-1), rhs.numel() // x2.shape[0], types, x.dtype)
     return y.reshape(tuple(rhs.shape) + (1, hid))

@@ -31,14 +31,16 @@ def pick_tile_rows(R, E, types):
     each streams its expert's weights, and 32-row tiles keep five K steps in flight and allow split-K; cfg4 116.6 ->
     108.8 us a step); 64 when gate/up runs on dequantized f16 weights (a type beyond Q4_0 / Q4_K, or gate and up of
     two types: the f16-weight GEMM then fits two workgroups a CU, 2,048 x 8 rows 405 -> 377 us) and for Q4_K (the
-    direct-copy kernel: cfg5's gate/up 545 -> 387 us); otherwise 128."""
+    direct-copy kernel: cfg5's gate/up 545 -> 387 us); otherwise 128. LMOE_TILE_ROWS (32, 64 or 128, read on every
+    call) overrides the rule where the types' GEMMs take that height."""
     return _lib.lib().lmoe_grouped_pick_tile_rows(int(R), int(E), *(qcode(t) for t in types))
 
 
 def pick_ksplit(R, E, bm, K):
     """Split-K slices for a GEMM over K of R rows in E experts (lmoe_grouped_pick_ksplit): with 32-row tiles and
     fewer than 16 rows an expert on average, few tiles have work and each would walk every K step alone, so each
-    tile is split over 4, 3 or 2 workgroups (at least 4 K steps each); otherwise 1."""
+    tile is split over 4, 3 or 2 workgroups (at least 4 K steps each); otherwise 1. LMOE_KSPLIT (1-8, read on every
+    call) overrides the rule on 32-row tiles when it divides the K steps."""
     return _lib.lib().lmoe_grouped_pick_ksplit(int(R), int(E), int(bm), int(K))
 
 

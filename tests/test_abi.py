@@ -183,3 +183,42 @@ def test_grouped_launch_choices(built_lib):
     assert built_lib.lmoe_grouped_workspace_bytes(R, E, 32, H, I) == 4 * max(ku * R * 2 * I, kd * R * H)
     assert built_lib.lmoe_grouped_workspace_bytes(R, E, 128, H, I) == 0
     assert grouped.splitk_floats(R, E, 32, H, I) * 4 == built_lib.lmoe_grouped_workspace_bytes(R, E, 32, H, I)
+
+
+def test_tile_and_split_knobs(built_lib, monkeypatch):
+    """LMOE_TILE_ROWS / LMOE_KSPLIT override the pickers on every call when the value is one the GEMMs take for the
+    types, and are ignored otherwise; the split-K workspace follows the forced split."""
+    q = _lib.qcode
+    pick = lambda R, E, ts: built_lib.lmoe_grouped_pick_tile_rows(R, E, *(q(t) for t in ts))  # noqa: E731
+    q40, q4k, mix = ("Q4_0",) * 3, ("Q4_K",) * 3, ("Q4_K", "Q4_K", "Q6_K")
+    for v, want in (("64", 64), ("128", 128), ("32", 32), ("48", 128), ("", 128)):
+        monkeypatch.setenv("LMOE_TILE_ROWS", v)
+        assert pick(8192 * 8, 128, q40) == want, v
+    monkeypatch.setenv("LMOE_TILE_ROWS", "32")
+    assert pick(2048 * 10, 512, q4k) == 32                  # Q4_K has 32-row tiles too
+    assert pick(64, 128, mix) == 64                          # an f16-weight down has none: the rule
+    monkeypatch.setenv("LMOE_TILE_ROWS", "128")
+    assert pick(64, 128, mix) == 128
+    monkeypatch.delenv("LMOE_TILE_ROWS")
+    ks = built_lib.lmoe_grouped_pick_ksplit
+    assert ks(8192 * 8, 128, 32, 2048) == 1                 # the rule: enough rows an expert
+    monkeypatch.setenv("LMOE_KSPLIT", "2")
+    assert ks(8192 * 8, 128, 32, 2048) == 1                 # more than 65,535 rows: not taken
+    assert ks(4096, 128, 32, 2048) == 2
+    assert ks(4096, 128, 128, 2048) == 1                    # split-K only on 32-row tiles
+    # both GEMMs split in 2 (gate/up over H = 2048, down over I = 768): the larger slice set, down's
+    assert built_lib.lmoe_grouped_workspace_bytes(4096, 128, 32, 2048, 768) == 2 * 4096 * max(2 * 768, 2048) * 4
+    monkeypatch.setenv("LMOE_KSPLIT", "3")
+    assert ks(4096, 128, 32, 2048) == 1                     # 32 K steps do not split in 3: the rule
+    assert ks(512, 128, 32, 768) == 3                       # 12 K steps split in 3
+    monkeypatch.setenv("LMOE_KSPLIT", "1")
+    assert ks(512, 128, 32, 2048) == 1                      # the rule would split in 4
+
+
+def test_dense_knob(monkeypatch):
+    """LMOE_DENSE forces experts()'s switch either way, else dense_pays decides."""
+    from larder_amd import gguf_experts as ge
+    for v, rule, want in (("1", False, True), ("0", True, False), ("", True, True), ("", False, False),
+                          ("2", True, True)):
+        monkeypatch.setenv("LMOE_DENSE", v)
+        assert ge._dense_knob(lambda r=rule: r) is want

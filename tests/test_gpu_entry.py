@@ -111,6 +111,15 @@ def test_experts_host_form_takes_the_path_dense_pays_picks(arena, monkeypatch):
     ran.clear()
     ge.experts(x, bufs, rhs, types)
     assert ran == ["gemv"]
+    # LMOE_DENSE overrides the fit either way
+    for env, cost, path in (("0", [1.0, 1.0, 0.0, 0.0, 0.0], "gemv"), ("1", [0.0, 0.0, 1.0, 1.0, 1.0], "dense")):
+        monkeypatch.setenv("LMOE_DENSE", env)
+        monkeypatch.setattr(ge, "_COST", cost)
+        ran.clear()
+        y = ge.experts(x, bufs, rhs, types, host=host_slots)
+        assert ran == [path], (env, ran)
+        assert moe.rel_l2(host(y.float()), want) < BAR
+    monkeypatch.delenv("LMOE_DENSE")
     with pytest.raises(ValueError, match="one row of x per slot"):
         ge.experts(x[:5], bufs, rhs, types, host=host_slots)
 

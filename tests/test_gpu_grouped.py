@@ -73,6 +73,29 @@ def test_expert_rows_vs_oracle(types, H, I, E, xdt):
     assert rows_ok(got[keep], want[keep]) < ROW_BAR
 
 
+@pytest.mark.parametrize("types,tile,ks", [(("Q4_0",) * 3, "32", "2"), (("Q4_0",) * 3, "64", ""),
+                                           (("Q4_K",) * 3, "128", ""), (("Q4_K",) * 3, "32", "")])
+def test_knobs_force_tiling(types, tile, ks, monkeypatch):
+    """LMOE_TILE_ROWS / LMOE_KSPLIT force the grouped path's tiling (here against the rule's choice for 40 rows over
+    6 experts), and the result stays within the bar."""
+    from larder_amd import grouped
+    H, I, E = (2048, 768, 6) if types[0] == "Q4_0" else (1024, 512, 6)
+    w = experts(types, H, I, E, 77)
+    rng = np.random.default_rng(78)
+    R = 40
+    slots = rng.integers(0, E, R).astype(np.int32)
+    monkeypatch.setenv("LMOE_TILE_ROWS", tile)
+    monkeypatch.setenv("LMOE_KSPLIT", ks)
+    assert grouped.pick_tile_rows(R, E, types) == int(tile)
+    if ks:
+        assert grouped.pick_ksplit(R, E, int(tile), H) == int(ks)
+    x = dev(rng.standard_normal((R, H)).astype(np.float32)).half()
+    y = grouped.expert_rows(x, tuple(dev(b) for b in w), dev(slots), types, torch.float32)
+    _, want = moe.gemv(host(x.float()), w, slots, 1, types)
+    assert moe.rel_l2(host(y), want) < BAR
+    assert rows_ok(host(y), want) < ROW_BAR
+
+
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32, torch.float16])
 def test_to_gemm_f16_k_order(xdt):
     """lmoe_to_gemm_f16: every element rounded to f16 once and placed at its K-order position."""
