@@ -7,6 +7,7 @@ read from ``lmoe_error()``; a refused ggml type raises ValueError (the reference
 stream_fast.py:8058-8061), any other refusal or HIP failure raises RuntimeError.
 """
 import ctypes
+import os
 from pathlib import Path
 
 import torch
@@ -136,8 +137,31 @@ def qcode(t):
     return TYPES[t][0]
 
 
+# device index -> True once the known-answer self-check (larder_amd.selfcheck) passed there; False while it runs
+_CHECKED = {}
+
+
 def stream():
+    """The current torch stream as a hipStream_t, for a call that launches work. The first such call on a device
+    first runs the library's known-answer self-check there (and raises if it fails), unless LMOE_SELF_CHECK=0 or a
+    graph is being captured (then the next eager call checks)."""
+    dev = torch.cuda.current_device()
+    if dev not in _CHECKED:
+        _self_check(dev)
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _self_check(dev):
+    if os.environ.get("LMOE_SELF_CHECK", "1") == "0" or torch.cuda.is_current_stream_capturing():
+        return
+    _CHECKED[dev] = False  # the check's own calls pass through
+    try:
+        from . import selfcheck
+        selfcheck.run(dev)
+    except BaseException:
+        del _CHECKED[dev]
+        raise
+    _CHECKED[dev] = True
 
 
 def row_bytes(t, n):
