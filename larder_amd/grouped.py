@@ -189,20 +189,26 @@ def expert_rows(x, w, host, types, out_dtype):
     ids = torch.as_tensor(host).reshape(-1).to(device=dev, dtype=torch.int32)
     G = Grouping(R, E, dev, bm=pick_tile_rows(R, E, types)).run(ids)
     h = torch.empty((R, I), dtype=torch.float16, device=dev)
-    y = torch.empty((R, H), dtype=torch.float16, device=dev)
+    # the down GEMM's f32 result goes to out_dtype with one rounding: an f16 y only when out is f16 itself
+    y = torch.empty((R, H), dtype=torch.float16 if out_dtype == torch.float16 else torch.float32, device=dev)
     gate_up(x.contiguous(), G, 1, wg, wu, types, h)
     down(h, G, wd, types[2], y)
     out = torch.empty((R, H), dtype=out_dtype, device=dev)
-    call("lmoe_combine_sorted", ptr(y), _lib.F16, ptr(G.inv), None, R, 1, H, None, None, 0, None, 0, ptr(out),
+    call("lmoe_combine_sorted", ptr(y), dcode(y.dtype), ptr(G.inv), None, R, 1, H, None, None, 0, None, 0, ptr(out),
          dcode(out_dtype), stream())
     bad = (ids < 0) | (ids >= E)
     return out.masked_fill_(bad[:, None], 0)
 
 
 class PrefillBuffers:
-    """Every intermediate of a prefill pass of T tokens through layers of one shape, allocated once."""
+    """Every intermediate of a prefill pass of T tokens through layers of one shape, allocated once. y_dtype is the
+    dtype of the routed experts' unweighted outputs between the down GEMM and the combine: float16 (the default,
+    half the traffic; an output row entry above 65504 in magnitude becomes inf) or float32 (finite wherever the
+    layer's output is, the reference dense path's f32 until the output dtype, gguf_experts.py:698-722)."""
 
-    def __init__(self, layer, T, device="cuda"):
+    def __init__(self, layer, T, device="cuda", y_dtype=torch.float16):
+        if y_dtype not in (torch.float16, torch.float32):
+            raise ValueError(f"y_dtype must be float16 or float32, not {y_dtype}")
         L = layer
         self.T = T
         R = T * L.k
@@ -220,7 +226,7 @@ class PrefillBuffers:
         self.ws = torch.empty(nws, **f32) if nws else None
         self.xh = torch.empty((T, L.H), dtype=torch.float16, device=device)
         self.h = torch.empty((R, L.I), dtype=torch.float16, device=device)
-        self.y = torch.empty((R, L.H), dtype=torch.float16, device=device)
+        self.y = torch.empty((R, L.H), dtype=y_dtype, device=device)
         if L.shared is not None:
             self.Gs = Grouping.identity(T, device, bm=pick_tile_rows(T, 1, L.types))
             self.hs = torch.empty((T, L.Is), dtype=torch.float16, device=device)
@@ -274,7 +280,7 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
     down(B.h, B.G, L.wd, L.types[2], B.y, ws=B.ws, w16=f16[2] if f16 else None)
     if L.shared is not None:
         torch.cuda.current_stream().wait_event(B.shared_done)
-    call("lmoe_combine_sorted", ptr(B.y), _lib.F16, ptr(B.G.inv), ptr(B.scores), T, L.k, H, shared, gate,
+    call("lmoe_combine_sorted", ptr(B.y), dcode(B.y.dtype), ptr(B.G.inv), ptr(B.scores), T, L.k, H, shared, gate,
          1 if shared is not None else 0, ptr(residual), dcode(residual.dtype) if residual is not None else 0,
          ptr(out), dcode(out.dtype), st)
     return out

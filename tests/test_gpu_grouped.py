@@ -96,6 +96,44 @@ def test_knobs_force_tiling(types, tile, ks, monkeypatch):
     assert rows_ok(host(y), want) < ROW_BAR
 
 
+def test_large_outputs_f16_limit_and_f32_y():
+    """Expert outputs past f16's range (down scales multiplied by a power of two): the default f16 y turns them into
+    inf, the documented limit; PrefillBuffers(y_dtype=float32) and expert_rows with a bf16 / f32 out keep them
+    finite and within the bar."""
+    from larder_amd import grouped
+    from larder_amd.layer import MoELayer
+    types, H, I, E, T, k = ("Q4_0",) * 3, 2048, 768, 8, 32, 2
+    rng = np.random.default_rng(90)
+    wg, wu, wd = (gguf.random_experts(rng, E, r, c, "Q4_0") for r, c in ((I, H), (I, H), (H, I)))
+    x = rng.standard_normal((T, H)).astype(np.float16)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    _, _, base = moe.layer(x.astype(np.float32), lg, (wg, wu, wd), types, k, True)
+    f = 2.0 ** int(np.ceil(np.log2(2e5 / np.abs(base).max())))
+    d = wd.reshape(-1, 18)[:, :2].copy().view(np.float16)
+    assert np.isfinite(d.astype(np.float32) * f).all() and (np.abs(d.astype(np.float32) * f) < 65504).all()
+    wd.reshape(-1, 18)[:, :2] = (d.astype(np.float32) * f).astype(np.float16).view(np.uint8)
+    _, _, want = moe.layer(x.astype(np.float32), lg, (wg, wu, wd), types, k, True)
+    assert np.abs(want).max() > 65504
+    L = MoELayer(dev(wg), dev(wu), dev(wd), types, k, True)
+    for y_dtype in (torch.float16, torch.float32):
+        B = grouped.PrefillBuffers(L, T, y_dtype=y_dtype)
+        out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+        grouped.prefill(L, dev(x), B, out, logits=dev(lg))
+        got = host(out)
+        if y_dtype == torch.float16:
+            assert not np.isfinite(got).all()              # the f16 y's limit
+        else:
+            assert np.isfinite(got).all() and moe.rel_l2(got, want) < BAR
+    slots = rng.integers(0, E, 40).astype(np.int32)
+    xr = dev(rng.standard_normal((40, H)).astype(np.float16))
+    _, yw = moe.gemv(host(xr.float()), (wg, wu, wd), slots, 1, types)
+    assert np.abs(yw).max() > 65504
+    for odt in (torch.float32, torch.bfloat16):
+        y = host(grouped.expert_rows(xr, (dev(wg), dev(wu), dev(wd)), dev(slots), types, odt).float())
+        ref = yw if odt == torch.float32 else host(torch.from_numpy(yw).bfloat16().float())   # out rounding
+        assert np.isfinite(y).all() and moe.rel_l2(y, ref) < BAR
+
+
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32, torch.float16])
 def test_to_gemm_f16_k_order(xdt):
     """lmoe_to_gemm_f16: every element rounded to f16 once and placed at its K-order position."""
