@@ -34,6 +34,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-config-seconds", type=float, default=4.0,
+                    help="seconds of CPU baseline at each of the other configurations")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-grouped", action="store_true", help="skip the cfg3 prefill / cfg4 batched lines")
     ap.add_argument("--extra-only", action="store_true",
@@ -482,12 +484,14 @@ def route_loader_leg():
 
 def cpu_leg(args, g):
     """The C++ restatement of the reference CPU kernel (cpu_kern gather_qmm) over the same experts, converted to
-    its affine 4-bit layout, run layer after layer for about --cpu-seconds; tokens/s = 1 / (48 x mean layer time)."""
+    its affine 4-bit layout, run layer after layer for about --cpu-seconds; tokens/s = 1 / (48 x mean layer time).
+    Threads follow the reference's rule (MOE_CPU_THREADS, else the physical cores of a socket), and every other
+    configuration gets a bounded sample of its own (cpu_configs)."""
     import numpy as np
 
     from oracle import cpu_baseline as cb
 
-    cores = cb.usable_cores()
+    cores = cb.threads()
     cb.lib().ckp_set_threads(cores)
     cfg = g["cfg"]
     nl = min(8, len(g["layers"]))
@@ -509,10 +513,80 @@ def cpu_leg(args, g):
         done += 1
     secs = time.perf_counter() - t0
     per_layer = secs / done
+    hw = cb.host()
+    from larder_amd import workloads
     return dict(value=1.0 / (per_layer * args.layers), unit="tokens/s", cores=cores, kind="port",
                 sample=f"{done} layer passes (batch 1, cfg-2 layer shape) over {nl} of the stack's layers in "
-                       f"{secs:.1f} s, {'AVX-512' if cb.lib().ckp_has_avx512() else 'scalar'} f32 path, "
-                       f"{cb.cpu_model()}; tokens/s = 1 / ({len(g['layers'])} x mean layer time)")
+                       f"{secs:.1f} s, {hw['isa']}, {hw['model']}; tokens/s = 1 / ({len(g['layers'])} x mean "
+                       f"layer time)",
+                gb_s=round(workloads.decode_bytes(cfg, cfg["k"]) / per_layer / 1e9, 2),
+                host=hw, configs=cpu_configs(cb, args.cpu_config_seconds))
+
+
+def cpu_configs(cb, secs):
+    """The CPU baseline at the other configurations, each a bounded sample of about ``secs`` seconds on the same
+    restated kernel: synthetic experts in the affine layout at the configuration's shapes (the kernel's time does
+    not depend on the values), routing by the layer's own router on random weights. gb_s is the GGUF algorithmic
+    bytes over the time, the GPU lines' measure (the affine layout the kernel reads is 0.75 B a weight, Q4_0 0.5625,
+    Q4_K 0.5625)."""
+    import numpy as np
+
+    from larder_amd import workloads
+    rng = np.random.default_rng(2)
+
+    def timed(fn):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < secs or n < 2:
+            fn()
+            n += 1
+        return (time.perf_counter() - t0) / n, n
+
+    def layer(cfg):
+        E, H, I, Is = cfg["E"], cfg["H"], cfg["I"], cfg["Is"]
+        ex = (cb.synthetic(E, I, H, 1), cb.synthetic(E, I, H, 2), cb.synthetic(E, H, I, 3))
+        wr = (rng.standard_normal((E, H)) * 0.02).astype(np.float16)
+        sh = (cb.synthetic(1, Is, H, 4), cb.synthetic(1, Is, H, 5), cb.synthetic(1, H, Is, 6)) if Is else None
+        wsg = (rng.standard_normal(H) * 0.02).astype(np.float32)
+
+        def run(x):
+            y = cb.moe_layer(x, wr, cfg["k"], cfg["norm"], *ex)
+            if sh is not None:   # the shared expert through the same kernel, gated by sigmoid(x . wsg)
+                z = np.zeros(x.shape[0], np.uint32)
+                gg, uu = cb.gather_qmm(x, sh[0], z), cb.gather_qmm(x, sh[1], z)
+                hh = gg / (1.0 + np.exp(-gg)) * uu
+                y = y + cb.gather_qmm(hh.astype(np.float32), sh[2], z) / (1.0 + np.exp(-(x @ wsg)))[:, None]
+            return y
+        return run
+
+    out = {}
+    runs = {}  # one layer a shape: cfg3 and cfg4 share cfg2's, cfg5's two lines share one
+    for name, cid, T, unit in (("cfg1_decode_T1", 1, 1, "layer"), ("cfg3_prefill", 3, 256, "chunk"),
+                               ("cfg4_batched", 4, 64, "step"), ("cfg5_decode_T1", 5, 1, "token"),
+                               ("cfg5_prefill_T2048", 5, 128, "chunk")):
+        cfg = workloads.CONFIGS[cid]
+        key = tuple(cfg[f] for f in ("H", "E", "k", "I", "Is", "norm"))
+        if key not in runs:
+            runs.clear()
+            runs[key] = layer(cfg)
+        run = runs[key]
+        x = rng.standard_normal((T, cfg["H"])).astype(np.float32)
+        per, n = timed(lambda: run(x))
+        line = {"tokens_per_s": round(T / per, 2), "passes": n, "tokens_a_pass": T}
+        if T == 1:
+            line["us_per_" + unit] = round(per * 1e6, 1)
+            line["gb_s"] = round(workloads.decode_bytes(cfg, cfg["k"]) / per / 1e9, 2)
+        else:
+            rows = T * cfg["k"]
+            line["tflops"] = round((workloads.expert_flops(cfg, rows) + 2 * T * 3 * cfg["H"] * cfg["Is"]) / per / 1e12,
+                                   3)
+            full = cfg.get("T", 2048 if cid == 5 else T)
+            if full != T:
+                line["sample"] = f"{T} of the {full}-token {unit}; tokens/s scales with rows"
+            if cid == 4:
+                line["us_per_step"] = round(per * 1e6, 1)
+        out[name] = line
+    return out
 
 
 def main():

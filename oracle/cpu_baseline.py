@@ -39,7 +39,7 @@ def _p(a):
 
 
 def usable_cores():
-    """Host cores this process may run on (the GPU box gives a share of its cores)."""
+    """Logical cores this process may run on (the GPU box gives a share of its cores)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -48,14 +48,66 @@ def usable_cores():
     return max(1, min(n, cap) if cap > 0 else n)
 
 
-def cpu_model():
+def _cpuinfo():
+    """/proc/cpuinfo as a list of {field: value} dicts, one a logical core (empty when unreadable)."""
+    cores, cur = [], {}
     try:
         for ln in open("/proc/cpuinfo"):
-            if ln.startswith("model name"):
-                return ln.split(":", 1)[1].strip()
+            if not ln.strip():
+                if cur:
+                    cores.append(cur)
+                cur = {}
+                continue
+            if ":" in ln:
+                k, v = ln.split(":", 1)
+                cur[k.strip()] = v.strip()
     except OSError:
-        pass
-    return "unknown"
+        return []
+    if cur:
+        cores.append(cur)
+    return cores
+
+
+def host():
+    """The host as the CPU baseline reports it: model, sockets, physical cores (distinct (physical id, core id)
+    pairs), physical cores a socket (the "cpu cores" field), logical cores, the cores this process may use, and the
+    ISA path the restated kernel takes."""
+    info = _cpuinfo()
+    model = info[0].get("model name", "unknown") if info else "unknown"
+    sockets = len({c.get("physical id", "0") for c in info}) or 1
+    physical = len({(c.get("physical id", "0"), c.get("core id", str(i))) for i, c in enumerate(info)}) or 1
+    per_socket = int(info[0].get("cpu cores", physical)) if info else physical
+    return {"model": model, "sockets": sockets, "physical_cores": physical, "cores_per_socket": per_socket,
+            "logical_cores": os.cpu_count() or len(info) or 1, "usable_logical_cores": usable_cores(),
+            "isa": "AVX-512 F/BW f32 FMA (group size 32 takes the f32 path)" if lib().ckp_has_avx512()
+                   else "scalar f32"}
+
+
+def threads():
+    """Threads the baseline runs, by the reference's rule (cpu_kernels.py:14-22, 91): MOE_CPU_THREADS when set,
+    else physical_cores(), which reads /proc/cpuinfo's "cpu cores" (the cores of one socket); capped at the cores
+    this process may run on."""
+    want = int(os.environ.get("MOE_CPU_THREADS", "0") or 0) or host()["cores_per_socket"]
+    return max(1, min(want, usable_cores()))
+
+
+def cpu_model():
+    return host()["model"]
+
+
+def synthetic(E, N, K, seed=0):
+    """An Affine-shaped expert set of E experts [N, K] with fixed pseudo-random nibbles and small scales, for timing
+    shapes whose experts are not on the host (the kernel's time does not depend on the values)."""
+    a = Affine.__new__(Affine)
+    a.E, a.N, a.K = E, N, K
+    rng = np.random.default_rng(seed)
+    a.w = np.empty((E, N, K // 2), np.uint8)
+    a.w.reshape(-1, K // 2)[:] = rng.integers(0, 256, K // 2, dtype=np.uint8)
+    a.sc = np.empty((E, N, K // 32), np.float32)
+    a.sc.reshape(-1).fill(1e-3)
+    a.bi = np.empty((E, N, K // 32), np.float32)
+    a.bi.reshape(-1).fill(-8e-3)
+    return a
 
 
 class Affine:
