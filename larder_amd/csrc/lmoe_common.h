@@ -476,13 +476,15 @@ __device__ __forceinline__ float rank256(RankScratch &s, int E, int k, int norm,
 
 // ---- nibble words -> f16 pairs ----------------------------------------------------------------------------------
 
-// (t & 0x00F000F0) | 0x54005400 in one v_and_or_b32. The compiler splits it into an and and an or (the fused form
-// takes at most one scalar operand on gfx9 and both constants are literals); here the mask rides in a vector
-// register, the exponent constant in a scalar one.
+// (t & 0x00F000F0) | 0x54005400 in one v_and_or_b32. With both constants as literals the compiler splits it into an
+// and and an or (the fused form takes at most one literal or scalar operand on gfx9), so the mask comes from a
+// vector register: a one-instruction asm moves it there (not volatile, so every call shares one), and the and-or
+// stays plain code the scheduler sees through. Writing the whole v_and_or_b32 as asm instead cost 190 VGPRs
+// against 111 in the Q4_K gate/up kernel at H = 4096 (occupancy 2 waves a SIMD instead of 3).
 __device__ __forceinline__ uint32_t and_or_nib(uint32_t t) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(t), "v"(0x00F000F0u), "s"(0x54005400u));
-  return r;
+  uint32_t m;
+  asm("v_mov_b32 %0, 0xf000f0" : "=v"(m));
+  return (t & m) | 0x54005400u;
 }
 
 // The f16 pair (64 + a, 64 + b) from nibbles a, b sitting at bits [s, s+4) and [s+16, s+20) of w (0 <= s <= 12).
