@@ -129,6 +129,9 @@ def grouped_leg():
     cfg = workloads.CONFIGS[3]
     T = cfg["T"]
     L = workloads.make_layer(cfg, g, with_router=False)
+    # the layer holds stream-layout copies of its experts for the grouped GEMMs (MoELayer.keep_stream: 2x the Q4
+    # bytes in HBM; the decode kernels read the GGUF copies), as a resident prefill layer would
+    stream_bytes = L.keep_stream()
     lg = workloads.skewed_logits(T, cfg["E"], g)
     x = torch.randn((T, cfg["H"]), generator=g, device="cuda").bfloat16()
     B = grouped.PrefillBuffers(L, T)
@@ -166,7 +169,8 @@ def grouped_leg():
         "kernels_us": kern,
         "gate_up_mfma_frac": round(gu / (kern["k_grouped<gate_up>"] * 1e-6) / MFMA_PEAK, 4),
         "down_mfma_frac": round(dn / (kern["k_grouped<down>"] * 1e-6) / MFMA_PEAK, 4),
-        "rows_per_expert_max": int(B.G.counts.max().item()), "experts_empty": int((B.G.counts == 0).sum().item())}
+        "rows_per_expert_max": int(B.G.counts.max().item()), "experts_empty": int((B.G.counts == 0).sum().item()),
+        "weights": f"GGUF Q4_0 plus a stream-layout copy ({stream_bytes / 1e6:.0f} MB) for the grouped GEMMs"}
     del B, x, y, lg
     # cfg4: 64 sequences x 1 token a step, 512 steps, a fresh draw of logits and x each step
     cfg4 = workloads.CONFIGS[4]
@@ -211,7 +215,8 @@ def grouped_leg():
     byts = uniq * (2 * cfg4["I"] * workloads.row_bytes("Q4_0", cfg4["H"]) +
                    cfg4["H"] * workloads.row_bytes("Q4_0", cfg4["I"])) + T4 * cfg4["H"] * 2 * 2
     out["cfg4_batched"] = {"us_per_step": round(us4, 1), "tokens_per_s": round(T4 / (us4 * 1e-6), 1),
-                           "note": "one HIP graph a step; input copies of x and logits inside the timed loop",
+                           "note": "one HIP graph a step; input copies of x and logits inside the timed loop; the "
+                                   "grouped GEMMs read stream-layout copies of the experts",
                            "unique_experts_per_step": round(uniq, 1), "rows_per_expert_max": round(rmax, 1),
                            "hbm_frac": round(byts / (us4 * 1e-6) / HBM_PEAK, 4)}
     del B4, xs, lgs
@@ -244,6 +249,7 @@ def grouped_leg():
     # HIP graph, a fresh x each step so the touched experts change), T = 2048 through the grouped path.
     cfg5 = workloads.CONFIGS[5]
     L5 = workloads.make_layer(cfg5, g)
+    L5.keep_stream()
     st5 = lay.DecodeStack([L5], 1)
     st5.capture()
     n5 = 256
@@ -282,7 +288,7 @@ def grouped_leg():
                                  "mfma_frac": round(f5 / (us5p * 1e-6) / MFMA_PEAK, 4),
                                  "hbm_frac": round(by5 / (us5p * 1e-6) / HBM_PEAK, 4), "experts_touched": u5,
                                  "note": "router logits by lmoe_router_gemm inside the timing; the shared expert on a "
-                                         "side stream"}
+                                         "side stream; the grouped GEMMs read stream-layout copies of the experts"}
     return out
 
 

@@ -261,6 +261,26 @@ int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offsets, const ui
                          const uint32_t *n_tiles, int max_tiles, int bm, int ksplit, float *ws, const uint8_t *wd,
                          int type_d, int n_experts, int I, int H, void *y, int ydtype, void *stream);
 
+/* The stream layout of a Q4_0 / Q4_K expert matrix [n_experts][rows][row bytes] (no counterpart in the reference,
+ * whose dense path reads the GGUF rows; it serves the same gather_mm, gguf_experts.py:698-722): the same bytes
+ * ordered [expert][block of 128 features][K block] so that each grouped-GEMM step copies one contiguous run a block
+ * of features. A K block is one 64-weight step for Q4_0 (4,608 bytes: the 128 features' 16-byte unit halves in the
+ * GEMM's LDS order, then their 4-byte tails) and one super-block for Q4_K (18,432 bytes: the 128 headers, then four
+ * steps of the features' 32-byte qs runs as 16-byte halves in the GEMM's LDS order). rows % 128 == 0.
+ * lmoe_stream_bytes: its size (the GGUF matrix's), 0 for a type or shape without one; lmoe_stream_repack: writes
+ * dst from the GGUF src (a one-time copy for a resident layer). */
+size_t lmoe_stream_bytes(int type, int n_experts, int rows, int cols);
+int lmoe_stream_repack(const uint8_t *src, int type, int n_experts, int rows, int cols, uint8_t *dst, void *stream);
+/* lmoe_grouped_gate_up_bm / lmoe_grouped_down_bm on stream-layout weights (wg, wu, wd from lmoe_stream_repack),
+ * bit-equal results; Q4_K at bm = 64 only. */
+int lmoe_grouped_gate_up_sl(const void *x, int xdtype, int T, int topk, const uint32_t *order,
+                            const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles, int max_tiles,
+                            int bm, int ksplit, float *ws, const uint8_t *wg, const uint8_t *wu, int type_g,
+                            int type_u, int n_experts, int H, int I, void *h, void *stream);
+int lmoe_grouped_down_sl(const void *h, int R, const uint32_t *offsets, const uint32_t *tiles,
+                         const uint32_t *n_tiles, int max_tiles, int bm, int ksplit, float *ws, const uint8_t *wd,
+                         int type_d, int n_experts, int I, int H, void *y, int ydtype, void *stream);
+
 /* lmoe_grouped_gate_up / lmoe_grouped_down with f16 weights in the K order (lmoe_dequant_gemm_f16's output:
  * wg16 / wu16 [n_experts][I][H], wd16 [n_experts][H][I]) instead of Q4 blocks: the grouped path of Q4_1, Q8_0,
  * Q5_K and Q6_K experts (the reference's gather_mm on dequantized f16 experts, gguf_experts.py:698-722). Same

@@ -67,6 +67,11 @@ SIGNATURES = {
     "lmoe_grouped_gate_up_bm": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P,
                                      _P]),
     "lmoe_grouped_down_bm": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P]),
+    "lmoe_grouped_gate_up_sl": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P,
+                                     _P]),
+    "lmoe_grouped_down_sl": (_I, [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P]),
+    "lmoe_stream_bytes": (_SZ, [_I, _I, _I, _I]),
+    "lmoe_stream_repack": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "lmoe_combine_sorted": (_I, [_P, _I, _P, _P, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_dequant": (_I, [_P, _I, _I, _I, _I, _P, _I, _P, _I, _P]),
     "lmoe_dequant_gemm_f16": (_I, [_P, _I, _I, _I, _I, _P, _P]),

@@ -179,6 +179,57 @@ __device__ __forceinline__ void store_tile(f32x4 (&acc)[4][MB], const Tile &t, i
   }
 }
 
+// ---- the stream layout -----------------------------------------------------------------------------------------
+//
+// A second copy of a Q4 expert matrix [E][rows][row bytes] (rows % 128 == 0), for the grouped GEMMs of resident
+// layers: the same bytes, ordered so that what a GEMM step copies for a block of 128 features is contiguous (in the
+// GGUF order each feature's 32 or 36 bytes of a step sit a row apart, and copies of such pieces run at ~4.9 TB/s
+// against ~6.2 for contiguous ones). Blocks in the order [expert][feature block fb of 128][K block]:
+//   Q4_0, a K block = one 64-weight step (two GGUF blocks, 36 bytes a feature), 4,608 bytes: granule q (16 bytes,
+//     q < 256) = half (q / 16) % 2 (bytes 16 h .. 16 h + 15 of the 36) of block feature 16 (q / 32) + q % 16, then
+//     the 128 features' bytes 32..35, 4 a feature;
+//   Q4_K, a K block = one super-block (256 weights, 4 steps), 18,432 bytes: the 128 features' 16-byte headers, then
+//     for each of the 4 steps pr, granule q = half (q / 16) % 2 of block feature 16 (q / 32) + q % 16's step bytes
+//     (super-block bytes 16 + 32 pr + 16 h .. + 15).
+// The granule order is the LDS order of a GEMM stage, so a wavefront's copies of a step read one kilobyte each.
+constexpr int kSlQ0 = 4608, kSlQK = 18432;
+
+// One thread a dword of the stream copy: where it comes from in the GGUF matrix.
+template <int TQ>
+__global__ void __launch_bounds__(256) k_stream_repack(const uint32_t *src, int rows, int row_dw, int nkb,
+                                                       long long n_dw, uint32_t *dst) {
+  const long long d = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (d >= n_dw) return;
+  constexpr int BDW = (TQ == LMOE_Q4_K ? kSlQK : kSlQ0) / 4;
+  const long long blk = d / BDW;
+  const int o = int(d - blk * BDW);
+  const int kb = int(blk % nkb);
+  const long long efb = blk / nkb;  // expert * (rows / 128) + fb
+  const int fb = int(efb % (rows / 128));
+  const long long e = efb / (rows / 128);
+  int feature, byte;
+  if (TQ == LMOE_Q4_0) {
+    if (o < 1024) {
+      const int q = o >> 2, w = o & 3;
+      feature = 16 * (q >> 5) + (q & 15);
+      byte = 36 * kb + 16 * ((q >> 4) & 1) + 4 * w;
+    } else {
+      feature = o - 1024;
+      byte = 36 * kb + 32;
+    }
+  } else {
+    if (o < 512) {
+      feature = o >> 2;
+      byte = 144 * kb + 4 * (o & 3);
+    } else {
+      const int o2 = o - 512, pr = o2 >> 10, r = o2 & 1023, q = r >> 2, w = r & 3;
+      feature = 16 * (q >> 5) + (q & 15);
+      byte = 144 * kb + 16 + 32 * pr + 16 * ((q >> 4) & 1) + 4 * w;
+    }
+  }
+  dst[d] = src[(e * rows + fb * 128 + feature) * row_dw + byte / 4];
+}
+
 // ---- Q4_0: global -> LDS directly, three stages ------------------------------------------------------------------
 
 // Per tile-row count GMT (128, or 32 for groups of few rows): A tile bytes a stage, the stage, A copies a lane.
@@ -206,6 +257,26 @@ __device__ __forceinline__ void dma(const void *base_any, uint32_t voff, uint32_
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "memory");
   else
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "memory");
+}
+
+// The A copies of a tile whose rows end early: copy i of wavefront w (D copies a wavefront a step) moves tile rows
+// [8 (D w + i), +8); bit i of the mask says whether any of them is a row of the tile. A copy of rows past the end
+// becomes a 4-byte copy of one address into the same place (the rows' LDS bytes are never stored: their output
+// rows are masked), so every wavefront still issues the same number of copies a step and the counted waits hold,
+// while the padding rows of a short group (~40 rows in a 64-row tile, ~5 in a 32-row one) cost no A bytes.
+template <int D>
+__device__ __forceinline__ uint32_t a_live_mask(int wave, int rows) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < D; ++i) m |= (8 * (D * wave + i) < rows ? 1u : 0u) << i;
+  return __builtin_amdgcn_readfirstlane(m);
+}
+
+__device__ __forceinline__ void dma_a(const _Float16 *ab, uint32_t off, uint32_t lds, uint32_t live) {
+  if (live)
+    dma<16>(ab, off, lds);
+  else
+    dma<4>(ab, 0u, lds);
 }
 
 // s_barrier with compiler memory fences on both sides: the intrinsic alone does not order memory accesses, and
@@ -319,7 +390,7 @@ __device__ __forceinline__ void q0_step(const uint8_t *st, const Q0Lane &L, int 
 // ksplit > 1 (32-row tiles): workgroup kpart takes K steps [kpart nk / ksplit, +nk / ksplit) and writes its fp32
 // sums to ws[kpart][row][feature] (features: gate/up = gate 0..I-1, up I..2I-1; down = 0..H-1; ldw of them a row,
 // R rows a slice); k_splitk_finish adds the slices and applies the epilogue.
-template <int MODE, int GMT = GM, int NST = 3>
+template <int MODE, int GMT = GM, int NST = 3, bool SL = false>
 __global__ void __launch_bounds__(kThreads, 2)
 k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
                const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
@@ -346,6 +417,7 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
     const uint32_t row = MODE == MODE_GATE_UP ? order[p] / uint32_t(topk) : uint32_t(p);
     a_off[i] = row * uint32_t(K) * 2u + 16u * uint32_t(c);
   }
+  const uint32_t a_live = a_live_mask<kQ0DmaA>(wave, t.rows);
   // weights: wavefront w covers tile features 64 w .. 64 w + 63 (gate/up: waves 0-1 gate rows, 2-3 up rows).
   // Its 16-byte copy i fills bytes [1024 (2 w + i), +1024) of the stage's head area: granule q = 64 (2 w + i) +
   // lane is half h = (q / 16) % 2 (words 4h .. 4h + 3) of tile feature f = 16 (q / 32) + q % 16. So each group of
@@ -354,7 +426,16 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   // Its 4-byte copy puts word 8 of tile feature 64 w + lane at 4 f of the tail area.
   const uint8_t *wbase;
   uint32_t w_off[kQ0DmaW + 1];
-  {
+  if constexpr (SL) {
+    // the stream layout (k_stream_repack): wavefront w's 128-feature block fb, one 4,608-byte block a K step: the
+    // granules and tail words this wavefront copies are one contiguous run of each
+    const uint8_t *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
+    const int fb = MODE == MODE_GATE_UP ? t.nt : 2 * t.nt + (wave >> 1);
+    wbase = m + (size_t(t.e) * (n_rows / 128) + fb) * size_t(K / GK) * kSlQ0;
+#pragma unroll
+    for (int i = 0; i < kQ0DmaW; ++i) w_off[i] = 16u * uint32_t(64 * (kQ0DmaW * (wave & 1) + i) + lane);
+    w_off[kQ0DmaW] = 4096u + 4u * uint32_t(64 * (wave & 1) + lane);
+  } else {
     const uint8_t *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
     const int row_base = MODE == MODE_GATE_UP ? t.nt * (GN / 2) - (wave >= 2 ? GN / 2 : 0) : t.nt * GN;
     wbase = m + (size_t(t.e) * n_rows) * wrow;
@@ -371,8 +452,8 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
     const _Float16 *ab = a_src + size_t(k0 + kk) * GK;
 #pragma unroll
     for (int i = 0; i < kQ0DmaA; ++i)
-      dma<16>(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kQ0DmaA * wave + i)));
-    const uint8_t *wb = wbase + size_t(k0 + kk) * 36;
+      dma_a(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kQ0DmaA * wave + i)), a_live >> i & 1u);
+    const uint8_t *wb = wbase + size_t(k0 + kk) * (SL ? kSlQ0 : 36);
 #pragma unroll
     for (int i = 0; i < kQ0DmaW; ++i)
       dma<16>(wb, w_off[i], __builtin_amdgcn_readfirstlane(st + kQ0AStage + 1024u * uint32_t(kQ0DmaW * wave + i)));
@@ -796,7 +877,7 @@ template <int GMT> constexpr int qk_stage() { return qk_astage<GMT>() + kKQs; }
 // steps in flight: streaming a different expert's weights through every tile (prefill over many experts with few
 // rows each). Grid and arguments as k_grouped_q4_0; host guarantees: K % 256 == 0, rows x K x 2 of A and one
 // expert's weight block under 4 GiB.
-template <int MODE, int GMT = 64, int NST = 4>
+template <int MODE, int GMT = 64, int NST = 4, bool SL = false>
 __global__ void __launch_bounds__(kThreads, 2)
 k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
                    const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
@@ -822,12 +903,22 @@ k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const
     const uint32_t row = MODE == MODE_GATE_UP ? order[p] / uint32_t(topk) : uint32_t(p);
     a_off[i] = row * uint32_t(K) * 2u + 16u * uint32_t(c);
   }
+  const uint32_t a_live = a_live_mask<kDmaA>(wave, t.rows);
   // weights: wavefront w copies tile features 64 w .. 64 w + 63 (gate/up: waves 0-1 gate rows, 2-3 up rows).
   // qs copy i: granule q = 64 (2 w + i) + lane is half h = (q / 16) % 2 of feature f = 16 (q / 32) + q % 16, from
   // super-block byte 16 + 16 h (+ 32 s of step pair s). Header copy: feature 64 w + lane's first 16 bytes.
   const uint8_t *wbase;
   uint32_t q_off[2], h_off;
-  {
+  if constexpr (SL) {
+    // the stream layout (k_stream_repack): wavefront w's 128-feature block fb, one 18,432-byte block a super-block
+    // (the headers, then the 4 steps' qs): each copy reads one contiguous kilobyte
+    const uint8_t *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
+    const int fb = MODE == MODE_GATE_UP ? t.nt : 2 * t.nt + (wave >> 1);
+    wbase = m + (size_t(t.e) * (n_rows / 128) + fb) * size_t(K / 256) * kSlQK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) q_off[i] = 2048u + 16u * uint32_t(64 * (2 * (wave & 1) + i) + lane);
+    h_off = 16u * uint32_t(64 * (wave & 1) + lane);
+  } else {
     const uint8_t *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
     const int row_base = MODE == MODE_GATE_UP ? t.nt * (GN / 2) - (wave >= 2 ? GN / 2 : 0) : t.nt * GN;
     wbase = m + (size_t(t.e) * n_rows) * wrow;
@@ -844,9 +935,9 @@ k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const
     const _Float16 *ab = a_src + size_t(kk) * GK;
 #pragma unroll
     for (int i = 0; i < kDmaA; ++i)
-      dma<16>(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kDmaA * wave + i)));
-    const uint8_t *sb = wbase + size_t(kk >> 2) * 144;
-    const uint8_t *qb = sb + 32 * (kk & 3);
+      dma_a(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kDmaA * wave + i)), a_live >> i & 1u);
+    const uint8_t *sb = wbase + size_t(kk >> 2) * (SL ? kSlQK : 144);
+    const uint8_t *qb = sb + (SL ? 4096 : 32) * (kk & 3);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       dma<16>(qb, q_off[i], __builtin_amdgcn_readfirstlane(st + kAStage + 1024u * uint32_t(2 * wave + i)));
@@ -1205,18 +1296,20 @@ static int check_split(const char *fn, int bm, int type, int ksplit, const float
   return 0;
 }
 
-extern "C" int lmoe_grouped_gate_up_bm(const void *x, int xdtype, int T, int topk, const uint32_t *order,
-                                       const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
-                                       int max_tiles, int bm, int ksplit, float *ws, const uint8_t *wg,
-                                       const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I,
-                                       void *h, void *stream) {
-  const char *fn = "lmoe_grouped_gate_up_bm";
+// The grouped GEMMs' launches. sl: the weights are stream-layout copies (k_stream_repack), which the Q4_0 kernels
+// take at every tile height and the Q4_K kernel at 64 rows.
+static int grouped_gate_up(const char *fn, bool sl, const void *x, int xdtype, int T, int topk, const uint32_t *order,
+                           const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles, int max_tiles,
+                           int bm, int ksplit, float *ws, const uint8_t *wg, const uint8_t *wu, int type_g,
+                           int type_u, int n_experts, int H, int I, void *h, void *stream) {
   LMOE_REQUIRE(bm == GM || bm == 64 || bm == 32, LMOE_ESHAPE, "%s: tile rows %d (128, 64 or 32)", fn, bm);
   if (int rc = check_split(fn, bm, type_g, ksplit, ws, H, T * topk)) return rc;
   LMOE_REQUIRE(qtype_ok(type_g) && qtype_ok(type_u), LMOE_ETYPE,
                "%s: ggml types %d/%d are not supported (Q4_0 = 2, Q4_K = 12)", fn, type_g, type_u);
   LMOE_REQUIRE(type_g == type_u, LMOE_ETYPE, "%s: gate and up must share one type on this path (%d vs %d)", fn,
                type_g, type_u);
+  LMOE_REQUIRE(!sl || type_g == LMOE_Q4_0 || bm == 64, LMOE_ESHAPE,
+               "%s: stream-layout Q4_K weights take 64-row tiles (not %d)", fn, bm);
   LMOE_REQUIRE(xdtype == LMOE_F16, LMOE_EINVAL,
                "%s: x must be float16 in the GEMM K order here (convert once with lmoe_to_gemm_f16)", fn);
   LMOE_REQUIRE(T >= 0 && topk > 0 && n_experts > 0 && max_tiles >= 0, LMOE_ESHAPE, "%s: bad shape", fn);
@@ -1237,36 +1330,41 @@ extern "C" int lmoe_grouped_gate_up_bm(const void *x, int xdtype, int T, int top
     LMOE_REQUIRE((long long)T * H * 2 <= 0xFFFFFFFFll && (long long)I * (H / 64) * 36 <= 0xFFFFFFFFll, LMOE_ESHAPE,
                  "%s: x or one expert's weights exceed 4 GiB", fn);
     const int R = T * topk;
-    launch(bm == 32 ? k_grouped_q4_0<MODE_GATE_UP, 32, 5>
-                    : bm == 64 ? k_grouped_q4_0<MODE_GATE_UP, 64, 4> : k_grouped_q4_0<MODE_GATE_UP>,
-           dim3(unsigned(grid)),
-           dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg, wu, H, I, h, I,
-           int(LMOE_F16), ksplit, ws, R, 2 * I);
+    auto kern = sl ? (bm == 32   ? k_grouped_q4_0<MODE_GATE_UP, 32, 5, true>
+                      : bm == 64 ? k_grouped_q4_0<MODE_GATE_UP, 64, 4, true>
+                                 : k_grouped_q4_0<MODE_GATE_UP, GM, 3, true>)
+                   : (bm == 32   ? k_grouped_q4_0<MODE_GATE_UP, 32, 5>
+                      : bm == 64 ? k_grouped_q4_0<MODE_GATE_UP, 64, 4>
+                                 : k_grouped_q4_0<MODE_GATE_UP>);
+    launch(kern, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg,
+           wu, H, I, h, I, int(LMOE_F16), ksplit, ws, R, 2 * I);
     if (ksplit > 1) {
       LMOE_LAUNCHED(fn);
       launch(k_splitk_finish<MODE_GATE_UP>, dim3(unsigned((I / 4 + 255) / 256), unsigned(R)), dim3(256), 0, st,
              static_cast<const float *>(ws), ksplit, R, 2 * I, offsets, n_experts, h, I, int(LMOE_F16));
     }
   } else {
-    launch(bm == 32 ? k_grouped_q4_k<MODE_GATE_UP, 32, 3>
-                    : bm == 64 ? k_grouped_q4_k_dma<MODE_GATE_UP> : k_grouped_q4_k<MODE_GATE_UP>,
-           dim3(unsigned(grid)),
-           dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg, wu, H, I, h, I,
-           int(LMOE_F16));
+    launch(sl           ? k_grouped_q4_k_dma<MODE_GATE_UP, 64, 4, true>
+           : bm == 32   ? k_grouped_q4_k<MODE_GATE_UP, 32, 3>
+           : bm == 64   ? k_grouped_q4_k_dma<MODE_GATE_UP>
+                        : k_grouped_q4_k<MODE_GATE_UP>,
+           dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg, wu, H,
+           I, h, I, int(LMOE_F16));
   }
   LMOE_LAUNCHED(fn);
   return 0;
 }
 
-extern "C" int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offsets, const uint32_t *tiles,
-                                    const uint32_t *n_tiles, int max_tiles, int bm, int ksplit, float *ws,
-                                    const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
-                                    void *stream) {
-  const char *fn = "lmoe_grouped_down_bm";
+static int grouped_down(const char *fn, bool sl, const void *h, int R, const uint32_t *offsets,
+                        const uint32_t *tiles, const uint32_t *n_tiles, int max_tiles, int bm, int ksplit, float *ws,
+                        const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
+                        void *stream) {
   LMOE_REQUIRE(bm == GM || bm == 64 || bm == 32, LMOE_ESHAPE, "%s: tile rows %d (128, 64 or 32)", fn, bm);
   LMOE_REQUIRE(R >= 0, LMOE_ESHAPE, "%s: bad row count", fn);
   if (int rc = check_split(fn, bm, type_d, ksplit, ws, I, R)) return rc;
   LMOE_REQUIRE(qtype_ok(type_d), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn, type_d);
+  LMOE_REQUIRE(!sl || type_d == LMOE_Q4_0 || bm == 64, LMOE_ESHAPE,
+               "%s: stream-layout Q4_K weights take 64-row tiles (not %d)", fn, bm);
   LMOE_REQUIRE(n_experts > 0 && max_tiles >= 0, LMOE_ESHAPE, "%s: bad shape", fn);
   LMOE_REQUIRE(I > 0 && I % block_weights(type_d) == 0 && I % 64 == 0, LMOE_ESHAPE,
                "%s: intermediate size %d is not a multiple of %d", fn, I, type_d == LMOE_Q4_K ? 256 : 64);
@@ -1285,23 +1383,91 @@ extern "C" int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offset
     // R is not passed: offsets[E] <= max_tiles * bm rows of h can be read
     LMOE_REQUIRE((long long)max_tiles * bm * I * 2 <= 0xFFFFFFFFll && (long long)H * (I / 64) * 36 <= 0xFFFFFFFFll,
                  LMOE_ESHAPE, "%s: h or one expert's weights exceed 4 GiB", fn);
-    launch(bm == 32 ? k_grouped_q4_0<MODE_DOWN, 32, 5>
-                    : bm == 64 ? k_grouped_q4_0<MODE_DOWN, 64, 4> : k_grouped_q4_0<MODE_DOWN>,
-           dim3(unsigned(grid)),
-           dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile,
-           wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype, ksplit, ws, R, H);
+    auto kern = sl ? (bm == 32   ? k_grouped_q4_0<MODE_DOWN, 32, 5, true>
+                      : bm == 64 ? k_grouped_q4_0<MODE_DOWN, 64, 4, true>
+                                 : k_grouped_q4_0<MODE_DOWN, GM, 3, true>)
+                   : (bm == 32   ? k_grouped_q4_0<MODE_DOWN, 32, 5>
+                      : bm == 64 ? k_grouped_q4_0<MODE_DOWN, 64, 4>
+                                 : k_grouped_q4_0<MODE_DOWN>);
+    launch(kern, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets,
+           tiles, n_tiles, n_ntile, wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype, ksplit, ws, R,
+           H);
     if (ksplit > 1) {
       LMOE_LAUNCHED(fn);
       launch(k_splitk_finish<MODE_DOWN>, dim3(unsigned((H / 4 + 255) / 256), unsigned(R)), dim3(256), 0, st,
              static_cast<const float *>(ws), ksplit, R, H, offsets, n_experts, y, H, ydtype);
     }
   } else {
-    launch(bm == 32 ? k_grouped_q4_k<MODE_DOWN, 32, 3>
-                    : bm == 64 ? k_grouped_q4_k_dma<MODE_DOWN> : k_grouped_q4_k<MODE_DOWN>,
-           dim3(unsigned(grid)),
-           dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets, tiles, n_tiles, n_ntile,
-           wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
+    launch(sl           ? k_grouped_q4_k_dma<MODE_DOWN, 64, 4, true>
+           : bm == 32   ? k_grouped_q4_k<MODE_DOWN, 32, 3>
+           : bm == 64   ? k_grouped_q4_k_dma<MODE_DOWN>
+                        : k_grouped_q4_k<MODE_DOWN>,
+           dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets, tiles,
+           n_tiles, n_ntile, wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);
   }
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+extern "C" int lmoe_grouped_gate_up_bm(const void *x, int xdtype, int T, int topk, const uint32_t *order,
+                                       const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
+                                       int max_tiles, int bm, int ksplit, float *ws, const uint8_t *wg,
+                                       const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I,
+                                       void *h, void *stream) {
+  return grouped_gate_up("lmoe_grouped_gate_up_bm", false, x, xdtype, T, topk, order, offsets, tiles, n_tiles,
+                         max_tiles, bm, ksplit, ws, wg, wu, type_g, type_u, n_experts, H, I, h, stream);
+}
+
+extern "C" int lmoe_grouped_gate_up_sl(const void *x, int xdtype, int T, int topk, const uint32_t *order,
+                                       const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles,
+                                       int max_tiles, int bm, int ksplit, float *ws, const uint8_t *wg,
+                                       const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I,
+                                       void *h, void *stream) {
+  return grouped_gate_up("lmoe_grouped_gate_up_sl", true, x, xdtype, T, topk, order, offsets, tiles, n_tiles,
+                         max_tiles, bm, ksplit, ws, wg, wu, type_g, type_u, n_experts, H, I, h, stream);
+}
+
+extern "C" int lmoe_grouped_down_bm(const void *h, int R, const uint32_t *offsets, const uint32_t *tiles,
+                                    const uint32_t *n_tiles, int max_tiles, int bm, int ksplit, float *ws,
+                                    const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
+                                    void *stream) {
+  return grouped_down("lmoe_grouped_down_bm", false, h, R, offsets, tiles, n_tiles, max_tiles, bm, ksplit, ws, wd,
+                      type_d, n_experts, I, H, y, ydtype, stream);
+}
+
+extern "C" int lmoe_grouped_down_sl(const void *h, int R, const uint32_t *offsets, const uint32_t *tiles,
+                                    const uint32_t *n_tiles, int max_tiles, int bm, int ksplit, float *ws,
+                                    const uint8_t *wd, int type_d, int n_experts, int I, int H, void *y, int ydtype,
+                                    void *stream) {
+  return grouped_down("lmoe_grouped_down_sl", true, h, R, offsets, tiles, n_tiles, max_tiles, bm, ksplit, ws, wd,
+                      type_d, n_experts, I, H, y, ydtype, stream);
+}
+
+// Bytes of the stream-layout copy of an expert matrix (the GGUF matrix's own size), or 0 when the shape has no
+// stream layout: Q4_0 / Q4_K, rows % 128 == 0, row length a multiple of 64 (Q4_0) or 256 (Q4_K).
+extern "C" size_t lmoe_stream_bytes(int type, int n_experts, int rows, int cols) {
+  if (!qtype_ok(type) || n_experts <= 0 || rows <= 0 || rows % 128 || cols <= 0 || cols % 64 ||
+      cols % block_weights(type))
+    return 0;
+  return size_t(n_experts) * size_t(rows) * size_t(cols / block_weights(type)) * size_t(type == LMOE_Q4_K ? 144 : 18);
+}
+
+extern "C" int lmoe_stream_repack(const uint8_t *src, int type, int n_experts, int rows, int cols, uint8_t *dst,
+                                  void *stream) {
+  const char *fn = "lmoe_stream_repack";
+  LMOE_REQUIRE(qtype_ok(type), LMOE_ETYPE, "%s: ggml type %d has no stream layout (Q4_0 = 2, Q4_K = 12)", fn, type);
+  const size_t n = lmoe_stream_bytes(type, n_experts, rows, cols);
+  LMOE_REQUIRE(n > 0, LMOE_ESHAPE, "%s: %d experts of %d x %d have no stream layout (rows %% 128, row length %% %d)",
+               fn, n_experts, rows, cols, type == LMOE_Q4_K ? 256 : 64);
+  LMOE_REQUIRE(src && dst && aligned4(src) && aligned4(dst), LMOE_EALIGN, "%s: 4-byte aligned buffers", fn);
+  const long long n_dw = (long long)(n / 4);
+  const int row_dw = int(size_t(cols / block_weights(type)) * (type == LMOE_Q4_K ? 144 : 18) / 4);
+  const int nkb = type == LMOE_Q4_K ? cols / 256 : cols / 64;
+  const long long blocks = (n_dw + 255) / 256;
+  LMOE_REQUIRE(blocks < (1ll << 31), LMOE_ESHAPE, "%s: %zu bytes", fn, n);
+  auto kern = type == LMOE_Q4_K ? k_stream_repack<LMOE_Q4_K> : k_stream_repack<LMOE_Q4_0>;
+  launch(kern, dim3(unsigned(blocks)), dim3(256), 0, (hipStream_t)stream, reinterpret_cast<const uint32_t *>(src),
+         rows, row_dw, nkb, n_dw, reinterpret_cast<uint32_t *>(dst));
   LMOE_LAUNCHED(fn);
   return 0;
 }

@@ -135,12 +135,27 @@ def _ws(n, ws, device):
     return torch.empty(n, dtype=torch.float32, device=device)
 
 
-def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False, ws=None, ksplit=None, w16=None):
+def stream_copy(w, t):
+    """The stream-layout copy of a Q4_0 / Q4_K expert matrix w uint8 [E, rows, row bytes] (lmoe_stream_repack): the
+    same bytes, ordered so that each grouped-GEMM step reads one contiguous run for a block of 128 features instead
+    of a 32- or 36-byte piece of every row. rows must be a multiple of 128. For resident layers (MoELayer.keep_stream);
+    the decode kernels keep reading the GGUF copy."""
+    E, rows = w.shape[0], w.shape[1]
+    cols = w.shape[2] // _lib.TYPES[t][2] * _lib.TYPES[t][1]
+    if t not in _lib.Q4_TYPES or _lib.lib().lmoe_stream_bytes(qcode(t), E, rows, cols) == 0:
+        raise ValueError(f"{t} experts of {rows} x {cols} have no stream layout (Q4_0 / Q4_K, rows a multiple of 128)")
+    out = torch.empty_like(w)
+    call("lmoe_stream_repack", ptr(w.contiguous()), qcode(t), E, rows, cols, ptr(out), stream())
+    return out
+
+
+def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False, ws=None, ksplit=None, w16=None, sl=None):
     """h [R, I] f16 (grouped order, columns in the GEMMs' K order: from_kperm undoes it) = silu(x . wg) * (x . wu)
     over the grouping G of x's rows (row p reads x[order[p] // topk]); x [T, H] in natural order, any float dtype,
     meets the weights as f16 in the K order (converted into ``xh``; prepped: x already is that form). Q4_0 / Q4_K
     weights are decoded inside the GEMM; the other types are dequantized to f16 first (gemm_weights). ksplit
-    (None: pick_ksplit) and ws (the split-K workspace, allocated when not given) drive split-K."""
+    (None: pick_ksplit) and ws (the split-K workspace, allocated when not given) drive split-K. sl: (gate, up) in the
+    stream layout (stream_copy) to read instead of wg / wu, same results bit for bit."""
     tg, tu = qcode(types[0]), qcode(types[1])
     if not prepped:
         x = as_gemm_f16(x, xh)
@@ -149,8 +164,9 @@ def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False, ws=None, kspli
     if types[0] in _lib.Q4_TYPES and types[1] == types[0]:
         ks = ksplit or (pick_ksplit(G.R, G.E, G.bm, H) if types[0] == "Q4_0" else 1)
         w = _ws(ks * G.R * 2 * I if ks > 1 else 0, ws, x.device)
-        call("lmoe_grouped_gate_up_bm", ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles),
-             ptr(G.n_tiles), G.max_tiles, G.bm, ks, ptr(w), ptr(wg), ptr(wu), tg, tu, E, H, I, ptr(h), stream())
+        entry, (wg_, wu_) = ("lmoe_grouped_gate_up_sl", sl) if sl is not None else ("lmoe_grouped_gate_up_bm", (wg, wu))
+        call(entry, ptr(x), _lib.F16, T, topk, ptr(G.order), ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles),
+             G.max_tiles, G.bm, ks, ptr(w), ptr(wg_), ptr(wu_), tg, tu, E, H, I, ptr(h), stream())
     else:
         if G.bm not in (64, tile_rows()):
             raise ValueError(f"the f16-weight GEMMs take 64- or {tile_rows()}-row tiles, not {G.bm}")
@@ -160,15 +176,17 @@ def gate_up(x, G, topk, wg, wu, types, h, xh=None, prepped=False, ws=None, kspli
     return h
 
 
-def down(h, G, wd, t, y, ws=None, ksplit=None, w16=None):
-    """y [R, H] (f16 / f32, grouped order, natural columns) = h . wd over the grouping G; h as gate_up leaves it."""
+def down(h, G, wd, t, y, ws=None, ksplit=None, w16=None, sl=None):
+    """y [R, H] (f16 / f32, grouped order, natural columns) = h . wd over the grouping G; h as gate_up leaves it.
+    sl: wd in the stream layout (stream_copy) to read instead, same results bit for bit."""
     E, H = wd.shape[0], wd.shape[1]
     I = h.shape[1]
     if t in _lib.Q4_TYPES:
         ks = ksplit or (pick_ksplit(G.R, G.E, G.bm, I) if t == "Q4_0" else 1)
         w = _ws(ks * G.R * H if ks > 1 else 0, ws, h.device)
-        call("lmoe_grouped_down_bm", ptr(h), G.R, ptr(G.offsets), ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, G.bm,
-             ks, ptr(w), ptr(wd), qcode(t), E, I, H, ptr(y), dcode(y.dtype), stream())
+        call("lmoe_grouped_down_sl" if sl is not None else "lmoe_grouped_down_bm", ptr(h), G.R, ptr(G.offsets),
+             ptr(G.tiles), ptr(G.n_tiles), G.max_tiles, G.bm, ks, ptr(w), ptr(sl if sl is not None else wd), qcode(t),
+             E, I, H, ptr(y), dcode(y.dtype), stream())
     else:
         if G.bm not in (64, tile_rows()):
             raise ValueError(f"the f16-weight GEMMs take 64- or {tile_rows()}-row tiles, not {G.bm}")
@@ -268,16 +286,22 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
         B.side.wait_event(B.x_ready)
         with torch.cuda.stream(B.side):
             sg, su, sd = L.shared
-            gate_up(B.xh, B.Gs, 1, sg, su, L.types, B.hs, prepped=True)
-            down(B.hs, B.Gs, sd, L.types[2], B.ys)
+            ss = L.shared_stream or (None, None, None)
+            s_ok = lambda t: t == "Q4_0" or B.Gs.bm == 64  # noqa: E731
+            gate_up(B.xh, B.Gs, 1, sg, su, L.types, B.hs, prepped=True,
+                    sl=ss[:2] if ss[0] is not None and s_ok(L.types[0]) else None)
+            down(B.hs, B.Gs, sd, L.types[2], B.ys, sl=ss[2] if s_ok(L.types[2]) else None)
             B.shared_done.record(B.side)
         shared, gate = ptr(B.ys), ptr(B.gate)
     call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
     B.G.run(B.ids.reshape(-1))
-    f16 = L.prefill_f16
+    f16, sl = L.prefill_f16, L.stream_w or (None, None, None)
+    sl_ok = lambda t: t == "Q4_0" or B.G.bm == 64  # noqa: E731  (stream-layout Q4_K: the 64-row kernel)
     gate_up(B.xh, B.G, L.k, L.wg, L.wu, L.types, B.h, prepped=True, ws=B.ws,
-            w16=f16[:2] if f16 and f16[0] is not None else None)
-    down(B.h, B.G, L.wd, L.types[2], B.y, ws=B.ws, w16=f16[2] if f16 else None)
+            w16=f16[:2] if f16 and f16[0] is not None else None,
+            sl=sl[:2] if sl[0] is not None and sl_ok(L.types[0]) else None)
+    down(B.h, B.G, L.wd, L.types[2], B.y, ws=B.ws, w16=f16[2] if f16 else None,
+         sl=sl[2] if sl_ok(L.types[2]) else None)
     if L.shared is not None:
         torch.cuda.current_stream().wait_event(B.shared_done)
     call("lmoe_combine_sorted", ptr(B.y), dcode(B.y.dtype), ptr(B.G.inv), ptr(B.scores), T, L.k, H, shared, gate,

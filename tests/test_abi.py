@@ -98,6 +98,20 @@ def test_refusals_without_a_gpu(built_lib):
     assert rc == _lib.ESHAPE and b"256" in L.lmoe_error()
     rc = L.lmoe_gemv_down_runs(p, p, 8, 8, p, _lib.Q4_0, 128, 768, 2048, p, 9, None)
     assert rc == _lib.EINVAL
+    # the stream layout: Q4 only, rows a multiple of 128; the Q4_K GEMM on it only at 64-row tiles
+    assert L.lmoe_stream_bytes(_lib.Q4_0, 4, 256, 512) == 4 * 256 * 16 * 18
+    assert L.lmoe_stream_bytes(_lib.Q4_K, 4, 256, 512) == 4 * 256 * 2 * 144
+    assert L.lmoe_stream_bytes(_lib.Q4_0, 4, 200, 512) == 0 and L.lmoe_stream_bytes(14, 4, 256, 512) == 0
+    assert L.lmoe_stream_bytes(_lib.Q4_K, 4, 256, 320) == 0
+    rc = L.lmoe_stream_repack(p, 14, 4, 256, 512, p, None)
+    assert rc == _lib.ETYPE
+    rc = L.lmoe_stream_repack(p, _lib.Q4_0, 4, 200, 512, p, None)
+    assert rc == _lib.ESHAPE and b"128" in L.lmoe_error()
+    rc = L.lmoe_grouped_gate_up_sl(p, _lib.F16, 64, 1, p, p, p, p, 4, 128, 1, None, p, p, _lib.Q4_K, _lib.Q4_K, 8,
+                                   1024, 512, p, None)
+    assert rc == _lib.ESHAPE and b"64-row" in L.lmoe_error()
+    rc = L.lmoe_grouped_down_sl(p, 64, p, p, p, 4, 32, 1, None, p, _lib.Q4_K, 8, 512, 1024, p, _lib.F16, None)
+    assert rc == _lib.ESHAPE and b"64-row" in L.lmoe_error()
 
 
 def test_grouped_refusals_without_a_gpu(built_lib):
