@@ -94,10 +94,13 @@ def test_stream_gemms_bit_equal(t, bm, ks):
 
 
 @pytest.mark.parametrize("cfgid,T", [(4, 64), (5, 300), (1, 40)])
-def test_prefill_with_stream_copies(cfgid, T):
-    """cfg4 (Q4_0, 32-row tiles, split-K), cfg5's Q4_K layer (64 experts, no shared expert) and cfg1 (Q4_0 with its
-    5,632-wide shared expert, router logits from the router weight): bit-equal with and without the copies."""
+def test_prefill_with_stream_copies(cfgid, T, monkeypatch):
+    """cfg4 (Q4_0, 32-row tiles), cfg5's Q4_K layer (64 experts, no shared expert) and cfg1 (Q4_0 with its 5,632-wide
+    shared expert, router logits from the router weight): bit-equal with and without the copies at one K split
+    (on stream copies the path takes no split-K, where the GGUF layout's rule splits cfg4's tiles), and within the
+    bar of the oracle either way."""
     from larder_amd import grouped, workloads
+    monkeypatch.setenv("LMOE_KSPLIT", "1")
     cfg = dict(workloads.CONFIGS[cfgid])
     if cfgid == 5:
         cfg.update(E=64, Is=0)          # the Q4_K layer at cfg5's shapes, fewer experts
