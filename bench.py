@@ -243,7 +243,7 @@ def grouped_leg():
     b1 = workloads.decode_bytes(cfg1, cfg1["k"]) + 2 * cfg1["H"] * 2
     out["cfg1_decode_T1"] = {"us_per_layer": round(us1, 2), "bytes_per_layer": b1,
                              "hbm_frac": round(b1 / (us1 * 1e-6) / HBM_PEAK, 4),
-                             "note": "8-layer stack, shared expert run apart (5 launches a layer)"}
+                             "note": "8-layer stack; the 5,632-wide shared expert folded into the decode kernels as four slices of the routed width (3 launches a layer)"}
     del st1, L1s, x1
     # cfg5: H 4096, 512 experts top-10, I 512, shared expert, Q4_K. T = 1 through the decode chain (one layer as a
     # HIP graph, a fresh x each step so the touched experts change), T = 2048 through the grouped path.

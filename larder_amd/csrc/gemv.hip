@@ -274,9 +274,11 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // (NPL a lane; softmax scores only in the one wavefront that writes ids / scores, wavefront 0 of the slot's first
 // workgroup); NPL = 0: expert ids from slots. Memory order: logits,
 // activation chunks, then (once the id is known) the weights, none predicated, so each group goes out back to back.
-// ks: slots a token, topk or, with a shared expert folded in (NPL > 0 only), topk + 1: then slot topk of a token
-// is the shared expert, stored as expert n_experts of wg / wu, and ids_out / scores_out rows hold ks entries, the
-// last (n_experts, sigmoid(logits[t][n_experts])) for the down kernel to weight it like a routed expert.
+// ks: slots a token, topk or, with a shared expert folded in (NPL > 0 only), topk + m: then slot topk + j of a token
+// is slice j of the shared expert (its intermediate features [j I, (j + 1) I), the whole expert when m = 1), stored
+// as expert n_experts + j of wg / wu, and ids_out / scores_out rows hold ks entries, the last m
+// (n_experts + j, sigmoid(logits[t][n_experts])) for the down kernel to weight them like routed experts: the shared
+// expert's down is linear in its intermediate features, so the m weighted slices sum to the gated shared row.
 template <int TQ, int P, int RB, int NPL, bool RANKWG>
 __global__ void __launch_bounds__(256)
     k_gate_up_xr(const uint32_t *xprep, const uint32_t *slots, int topk, const uint8_t *wg, const uint8_t *wu,
@@ -301,7 +303,7 @@ __global__ void __launch_bounds__(256)
   uint32_t *scr = reinterpret_cast<uint32_t *>(lds4 + XC + STAGE) + wave * 64;
   const size_t xrow = size_t(s / ks);
   const int jslot = s % ks;
-  const bool shared_slot = NPL > 0 && jslot == topk;  // uniform across the workgroup
+  const bool shared_slot = NPL > 0 && jslot >= topk;  // uniform across the workgroup
 
   // RANKWG and E <= 512: the workgroup ranks its token's logits once (rank256: the four wavefronts share the
   // comparisons); otherwise each wavefront ranks them itself (topk_wave)
@@ -325,8 +327,8 @@ __global__ void __launch_bounds__(256)
   u32x4 xc[XPT];
 #pragma unroll
   for (int i = 0; i < XPT; ++i) xc[i] = xg4[min(int(threadIdx.x) + 256 * i, XC - 1)];
-  if (NPL > 0 && shared_slot) {  // the folded shared expert: no pick; its id and sigmoid-gated weight
-    e = uint32_t(n_experts);
+  if (NPL > 0 && shared_slot) {  // a slice of the folded shared expert: no pick; its id and sigmoid-gated weight
+    e = uint32_t(n_experts + jslot - topk);
     if (blockIdx.x == 0 && wave == 0 && lane == 0) {
       ids_out[s] = e;
       scores_out[s] = sigmoidf_(logits[xrow * ld_stride + n_experts]);
@@ -577,19 +579,24 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // wavefront finish on DPP / permlane swaps, then the gated shared-expert row and the residual are added. Memory order:
 // h units, ids and scores (one a lane), then the weights, whose addresses need only the ids; no load is predicated
 // (clamped indices; expert 0 stands in for an id past the experts, with a zero weight).
-template <int TD, int NU, int NCW>
+template <int TD, int NU, int NCW, int KS = 1>
 __global__ void __launch_bounds__(256)
     k_down_xr(const uint32_t *hprep, const uint32_t *ids, const float *scores, int k, const uint8_t *wd,
               int n_experts, int I, int H, const float *shared, const float *gate, int gate_stride,
               const void *residual, int rdt, void *out, int odt) {
   constexpr int RB = 2;
-  const int P = I / 64, U = k * P;
-  const int CJ = RB * 9 * P / 4, CW = k * CJ;  // 16-byte chunks of one expert's RB rows, of all k
+  // KS = 2 (a token's units past 128): wavefronts 2 q and 2 q + 1 share rows [(2 bx + q) RB, +RB), each over half of
+  // the experts (the first ceil(k / 2), the rest), and add their two row sums through LDS
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = KS == 2 ? (wave & 1) : 0;
+  const int kh = KS == 2 ? (k + 1) / 2 : k;
+  const int j0 = half * kh, kj = KS == 2 ? (half ? k - kh : kh) : k;  // this wavefront's experts [j0, j0 + kj)
+  const int P = I / 64, U = kj * P;
+  const int CJ = RB * 9 * P / 4, CW = kj * CJ;  // 16-byte chunks of one expert's RB rows, of this wavefront's
   const int t = blockIdx.y;
-  const int n0 = (blockIdx.x * 4 + wave) * RB;
+  const int n0 = KS == 2 ? (blockIdx.x * 2 + (wave >> 1)) * RB : (blockIdx.x * 4 + wave) * RB;
   extern __shared__ u32x4 lds4[];
-  uint32_t *stage = reinterpret_cast<uint32_t *>(lds4) + wave * (CW * 4);
+  uint32_t *stage = reinterpret_cast<uint32_t *>(lds4) + wave * (kh * CJ * 4);
 
   // 1. the token's ids and scores (lane j < k holds expert j's), then the h units. The empty asm with a memory
   // clobber keeps the compiler from sinking these loads below the weights' (the count of outstanding loads is in
@@ -598,7 +605,7 @@ __global__ void __launch_bounds__(256)
   const uint32_t my_id = ids[size_t(t) * k + kl];
   const float sc_ld = (scores ? scores + size_t(t) * k : reinterpret_cast<const float *>(ids))[kl];
   const float my_sc = scores ? sc_ld : 1.0f;
-  const u32x4 *hb = reinterpret_cast<const u32x4 *>(hprep + size_t(t) * U * XS);
+  const u32x4 *hb = reinterpret_cast<const u32x4 *>(hprep + (size_t(t) * k + j0) * P * XS);
   u32x4 hq[NU][9];
 #pragma unroll
   for (int a = 0; a < NU; ++a) {
@@ -607,14 +614,14 @@ __global__ void __launch_bounds__(256)
     for (int i = 0; i < 9; ++i) hq[a][i] = hb[u * 9 + i];
   }
   asm volatile("" ::: "memory");
-  // 2. the weights: chunk c of expert j's block at rows [n0, n0 + RB)
+  // 2. the weights: chunk c of expert j0 + j's block at rows [n0, n0 + RB)
   const size_t rowb = size_t(36) * P, nsafe = size_t(min(n0, H - RB));
   u32x4 w[NCW];
 #pragma unroll
   for (int i = 0; i < NCW; ++i) {
     const int c = min(lane + 64 * i, CW - 1);
     const int j = c / CJ, cc = c - j * CJ;
-    uint32_t e = uint32_t(__shfl(int(my_id), j, 64));
+    uint32_t e = uint32_t(__shfl(int(my_id), j0 + j, 64));
     e = e < uint32_t(n_experts) ? e : 0u;
     w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wd + (size_t(e) * H + nsafe) * rowb) + cc);
   }
@@ -629,8 +636,8 @@ __global__ void __launch_bounds__(256)
     const int u = lane + 64 * a, uc = min(u, U - 1);
     ja[a] = uc / P;
     pa[a] = uc - ja[a] * P;
-    const uint32_t e = uint32_t(__shfl(int(my_id), ja[a], 64));
-    const float sj = __shfl(my_sc, ja[a], 64);
+    const uint32_t e = uint32_t(__shfl(int(my_id), j0 + ja[a], 64));
+    const float sj = __shfl(my_sc, j0 + ja[a], 64);
     fa[a] = (u < U && e < uint32_t(n_experts)) ? sj : 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -655,7 +662,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int i = 0; i < NCW; ++i) st4[min(lane + 64 * i, CW - 1)] = w[i];
   __builtin_amdgcn_wave_barrier();
-  if (n0 >= H) return;
+  if (KS == 1 && n0 >= H) return;  // (KS == 2: the host launches exactly H / 4 workgroups, every row in range)
   // 5. dots
   float acc[RB];
 #pragma unroll
@@ -665,9 +672,17 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int r = 0; r < RB; ++r)
       acc[r] = fmaf(fa[a], row_unit_dot_r<TD>(stage + (ja[a] * RB + r) * 9 * P, pa[a], xv[a], s0[a], s1[a]), acc[r]);
-  // 6. the rows' sums, then shared expert and residual
+  // 6. the rows' sums (KS = 2: the second half's through LDS into the first's), then shared expert and residual
 #pragma unroll
   for (int r = 0; r < RB; ++r) acc[r] = wave_sum(acc[r]);
+  if (KS == 2) {
+    __shared__ float part[2 * RB];
+    if (half == 1 && lane < RB) part[(wave >> 1) * RB + lane] = lane == 0 ? acc[0] : acc[1];
+    __syncthreads();
+    if (half == 1) return;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) acc[r] += part[(wave >> 1) * RB + r];
+  }
   if (lane < RB) {
     float v = acc[0];
 #pragma unroll
@@ -1089,6 +1104,38 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   hipStream_t st = (hipStream_t)stream;
   {  // prepared h, at most 128 units a token, P even, H a multiple of 8: the register-resident kernel
     const int P = a.I / 64, U = a.k * P, CW = a.k * 9 * P / 2;
+    const int kh = (a.k + 1) / 2, Uh = kh * P, CWh = kh * 9 * P / 2;
+    if (a.hprep && !(U <= 128 && CW <= 64 * 9) && Uh <= 128 && P % 2 == 0 && a.H % 4 == 0 && CWh <= 64 * 9) {
+      // up to 256 units: two wavefronts a row pair, half of the experts each (config 1 with its shared expert
+      // folded in as four slices: 8 experts of 22 units)
+      const int NU = Uh <= 64 ? 1 : 2, ncw = (CWh + 63) / 64;
+      auto go = [&](auto td, auto nu, auto nc) {
+        constexpr int TD = decltype(td)::value, N = decltype(nu)::value, C = decltype(nc)::value;
+        launch(k_down_xr<TD, N, C, 2>, dim3(a.H / 4, a.T), dim3(256), size_t(4) * 4 * CWh * 4, st, a.hprep, a.ids,
+               a.scores, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt,
+               a.out, a.odt);
+      };
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using C5 = std::integral_constant<int, 5>;
+      using C7 = std::integral_constant<int, 7>;
+      using C9 = std::integral_constant<int, 9>;
+      auto by_c = [&](auto td, auto nu) {
+        if (ncw <= 5) go(td, nu, C5());
+        else if (ncw <= 7) go(td, nu, C7());
+        else go(td, nu, C9());
+      };
+      auto by_nu = [&](auto td) {
+        if (NU == 1) by_c(td, I1());
+        else by_c(td, I2());
+      };
+      if (a.type_d == LMOE_Q4_0)
+        by_nu(std::integral_constant<int, LMOE_Q4_0>());
+      else
+        by_nu(std::integral_constant<int, LMOE_Q4_K>());
+      LMOE_LAUNCHED(fn);
+      return 0;
+    }
     if (a.hprep && U <= 128 && P % 2 == 0 && a.H % 8 == 0 && CW <= 64 * 9) {
       const int NU = U <= 64 ? 1 : 2, ncw = (CW + 63) / 64;
       auto go = [&](auto td, auto nu, auto nc) {
@@ -1312,6 +1359,7 @@ extern "C" int lmoe_moe_gate_up_ext(const float *logits, int ld_stride, int T, i
                                     uint32_t *ids, float *scores, uint32_t *hprep, int type_d, int with_shared,
                                     void *stream) {
   const char *fn = "lmoe_moe_gate_up_ext";
+  LMOE_REQUIRE(with_shared >= 0, LMOE_EINVAL, "%s: %d shared slices", fn, with_shared);
   if (!with_shared)
     return lmoe_moe_gate_up(logits, ld_stride, T, k, norm, xg_prep, xu_prep, wg, wu, type_g, type_u, n_experts, H,
                             I, ids, scores, hprep, type_d, stream);
@@ -1321,9 +1369,10 @@ extern "C" int lmoe_moe_gate_up_ext(const float *logits, int ld_stride, int T, i
   LMOE_REQUIRE(ld_stride >= n_experts + 1, LMOE_ESHAPE,
                "%s: logits rows need the shared expert's gate logit at column %d (stride %d)", fn, n_experts,
                ld_stride);
-  LMOE_REQUIRE(k >= 1 && k + 1 <= 64, LMOE_ESHAPE, "%s: k %d", fn, k);
-  GateUpArgs a{xg_prep, xg_prep, nullptr, 0, nullptr, T * (k + 1), k, wg, wu, n_experts, H, I, nullptr, hprep,
-               type_d, logits, ld_stride, norm, ids, scores, k + 1};
+  const int ks = k + with_shared;
+  LMOE_REQUIRE(k >= 1 && ks <= 64, LMOE_ESHAPE, "%s: k %d with %d shared slices", fn, k, with_shared);
+  GateUpArgs a{xg_prep, xg_prep, nullptr, 0, nullptr, T * ks, k, wg, wu, n_experts, H, I, nullptr, hprep,
+               type_d, logits, ld_stride, norm, ids, scores, ks};
   return gate_up(fn, a, type_g, type_u, stream);
 }
 

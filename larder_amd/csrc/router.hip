@@ -170,7 +170,7 @@ static void launch_router(int qt, dim3 grid, dim3 block, hipStream_t st, const v
 // resets the counter for the next launch. Nobody waits on anybody: with NR = ceil((E + 1) / 8) workgroups the
 // counter sees ~17 arrivals for E 128 instead of a kernel boundary and a top-k in every gate/up wavefront.
 // Workgroups past NR write the prepared activation rows, as in k_router_gemv.
-// ks: slots a token in ids / scores (k, or k + 1 with a shared expert folded in as slot k: id E, weight
+// ks: slots a token in ids / scores (k, or k + m with a shared expert folded in as slots k..k+m-1: ids E.., weight
 // sigmoid(gate logit)). sync: a device counter, zero before the first launch, left zero by every launch.
 template <int WDT, int TQ, int NI, int kRankRows>
 __global__ void __launch_bounds__(256)
@@ -256,9 +256,9 @@ __global__ void __launch_bounds__(256)
       ids[size_t(t) * ks + tid] = rs.pick[tid];
       scores[size_t(t) * ks + tid] = p;
     }
-    if (tid == 0 && ks > k) {
-      ids[size_t(t) * ks + k] = uint32_t(E);
-      scores[size_t(t) * ks + k] = sigmoidf_(rs.vals[E]);
+    if (tid >= k && tid < ks) {  // the folded shared expert's slices: ids E.., one sigmoid-gated weight
+      ids[size_t(t) * ks + tid] = uint32_t(E + tid - k);
+      scores[size_t(t) * ks + tid] = sigmoidf_(rs.vals[E]);
     }
     __syncthreads();
   }
@@ -736,7 +736,7 @@ extern "C" int lmoe_router_gemv_rank(const void *x, int xdtype, const void *wr, 
   LMOE_REQUIRE(H > 0 && H % 64 == 0 && H <= 8 * 256 * kRouterMaxNi, LMOE_ESHAPE, "%s: hidden %d", fn, H);
   LMOE_REQUIRE(E > 0 && E <= kRankMaxE && k > 0 && k <= kRankMaxK && k <= E, LMOE_ESHAPE,
                "%s: top-%d of %d experts (E <= %d, k <= %d)", fn, k, E, kRankMaxE, kRankMaxK);
-  LMOE_REQUIRE(ks == k || (ks == k + 1 && wsg), LMOE_EINVAL, "%s: %d slots a token for top-%d", fn, ks, k);
+  LMOE_REQUIRE(ks == k || (ks > k && ks <= 64 && wsg), LMOE_EINVAL, "%s: %d slots a token for top-%d", fn, ks, k);
   LMOE_REQUIRE(!xprep || qtype_ok(qtype), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn,
                qtype);
   LMOE_REQUIRE(x && wr && logits && ids && scores && sync, LMOE_EINVAL, "%s: null pointer", fn);

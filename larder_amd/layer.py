@@ -48,14 +48,22 @@ class MoELayer:
         self.Is = shared[0].shape[1] if shared is not None else 0
         if shared is not None and wsg is None:
             raise ValueError("a shared expert needs its gate weight wsg")
-        # A shared expert of the routed experts' shape, with a router weight, rides in the decode kernels as expert
-        # E of extended buffers [E + 1, ...] (lmoe_moe_gate_up_ext): three launches a layer instead of five. The
-        # routed buffers are then views of the extended ones (no second copy).
-        self.folded = None
-        if (fold_shared and shared is not None and wr is not None and self.Is == self.I
+        # A shared expert m times the routed width (m >= 1), with a router weight, rides in the decode kernels as m
+        # experts E .. E + m - 1 of extended buffers [E + m, ...] (lmoe_moe_gate_up_ext): slice j is its intermediate
+        # features [j I, (j + 1) I), i.e. gate / up rows j I .. and down columns j I .. (whole GGUF blocks, since I is
+        # a multiple of the block length), and the m slices' down outputs, each weighted by the gate's sigmoid, add
+        # up to the gated shared row. Three launches a layer instead of five. The routed buffers are then views of
+        # the extended ones (no second copy of them).
+        self.folded, self.n_shared = None, 0
+        m = self.Is // self.I if shared is not None and self.Is % self.I == 0 else 0
+        if (fold_shared and m >= 1 and wr is not None and self.k + m <= 64
                 and self.types[0] == self.types[1] and self.H in (2048, 4096) and self.I % 2 == 0
-                and tuple(shared[2].shape[1:]) == tuple(wd.shape[1:])):
-            self.folded = tuple(torch.cat([w, sw], 0) for w, sw in zip((wg, wu, wd), shared))
+                and shared[2].shape[1] == wd.shape[1] and shared[2].shape[2] == m * wd.shape[2]):
+            sg, su, sd = shared
+            slices = (sg.reshape(m, self.I, sg.shape[2]), su.reshape(m, self.I, su.shape[2]),
+                      sd.reshape(self.H, m, wd.shape[2]).permute(1, 0, 2))
+            self.folded = tuple(torch.cat([w, sw], 0).contiguous() for w, sw in zip((wg, wu, wd), slices))
+            self.n_shared = m
             wg, wu, wd = (f[:self.E] for f in self.folded)
         self.wg, self.wu, self.wd = wg, wu, wd
         self.prefill_f16 = None
@@ -136,7 +144,7 @@ class DecodeBuffers:
         f32 = dict(dtype=torch.float32, device=device)
         u32 = dict(dtype=torch.int32, device=device)
         self.logits = torch.empty((T, rows), **f32)
-        ks = L.k + (1 if L.folded is not None else 0)  # slots a token (the folded shared expert last)
+        ks = L.k + L.n_shared  # slots a token (the folded shared expert's slices last)
         self.ids_ext = torch.empty((T, ks), **u32)
         self.scores_ext = torch.empty((T, ks), **f32)
         self.ids, self.scores = self.ids_ext[:, :L.k], self.scores_ext[:, :L.k]
@@ -185,16 +193,18 @@ def decode(layer, x, bufs, out, residual=None, logits=None):
     if B.xprep_u is not None:
         call("lmoe_prep_x", ptr(x), xd, T, L.H, tu, ptr(B.xprep_u), st)
         xu = B.xprep_u
-    if L.folded is not None:  # the shared expert as slot k of every token: gate/up, then down + combine
+    if L.folded is not None:  # the shared expert's m slices as slots k .. k + m - 1: gate/up, then down + combine
         fg, fu, fd = L.folded
+        ks = L.k + L.n_shared
         if ranked:
-            call("lmoe_gemv_gate_up_prepped", ptr(B.xprep), ptr(xu), ptr(B.ids_ext), T * (L.k + 1), L.k + 1,
-                 ptr(fg), ptr(fu), tg, tu, L.E + 1, L.H, L.I, None, ptr(B.hprep), td, st)
+            call("lmoe_gemv_gate_up_prepped", ptr(B.xprep), ptr(xu), ptr(B.ids_ext), T * ks, ks,
+                 ptr(fg), ptr(fu), tg, tu, L.E + L.n_shared, L.H, L.I, None, ptr(B.hprep), td, st)
         else:
             call("lmoe_moe_gate_up_ext", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(xu), ptr(fg),
-                 ptr(fu), tg, tu, L.E, L.H, L.I, ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.hprep), td, 1, st)
-        call("lmoe_gemv_down_combine_prepped", ptr(B.hprep), 0, ptr(B.ids_ext), ptr(B.scores_ext), T, L.k + 1,
-             ptr(fd), td, L.E + 1, L.I, L.H, None, None, 0, ptr(residual),
+                 ptr(fu), tg, tu, L.E, L.H, L.I, ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.hprep), td, L.n_shared,
+                 st)
+        call("lmoe_gemv_down_combine_prepped", ptr(B.hprep), 0, ptr(B.ids_ext), ptr(B.scores_ext), T, ks,
+             ptr(fd), td, L.E + L.n_shared, L.I, L.H, None, None, 0, ptr(residual),
              dcode(residual.dtype) if residual is not None else 0, ptr(out), dcode(out.dtype), st)
         return out
     if ranked:

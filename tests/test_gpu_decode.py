@@ -207,6 +207,40 @@ def test_decode_layer_cfg1_vs_oracle(T):
     assert moe.rel_l2(host(out), want) < BAR
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_cfg1_shared_slices_folded_match_apart(T):
+    """Config 1's 5,632-wide shared expert folded into the decode kernels as four slices of the routed width (slots
+    k .. k + 3, ids E .. E + 3, each weighted by the gate's sigmoid: three launches a layer) against the same layer
+    with the shared expert run apart (five launches): equal ids, outputs within the bar of each other and of the
+    oracle."""
+    from larder_amd import layer as lay, workloads
+    cfg = workloads.CONFIGS[1]
+    L = _layer_from_device(cfg, 12)
+    assert L.folded is not None and L.n_shared == 4
+    U = lay.MoELayer(L.wg, L.wu, L.wd, L.types, L.k, L.norm, wr=L.wr, shared=L.shared, wsg=L.wsg,
+                     fold_shared=False)
+    assert U.folded is None
+    rng = np.random.default_rng(T + 40)
+    x = dev(rng.standard_normal((T, cfg["H"])).astype(np.float16))
+    outs = []
+    for layer in (L, U):
+        B = lay.DecodeBuffers(layer, T)
+        out = torch.empty((T, cfg["H"]), dtype=torch.float32, device="cuda")
+        lay.decode(layer, x, B, out)
+        torch.cuda.synchronize()
+        outs.append((host(out), host(B.ids).copy(), B))
+    (of, idf, Bf), (ou, idu, _) = outs
+    assert (idf == idu).all()
+    lg = host(Bf.logits)
+    assert (host(Bf.ids_ext)[:, cfg["k"]:] == cfg["E"] + np.arange(4)).all()
+    assert np.allclose(host(Bf.scores_ext)[:, cfg["k"]:], 1 / (1 + np.exp(-lg[:, cfg["E"]:cfg["E"] + 1])), rtol=1e-5)
+    assert moe.rel_l2(of, ou) < BAR
+    _, _, want = moe.layer(host(x.float()), lg[:, :cfg["E"]], tuple(host(b) for b in (L.wg, L.wu, L.wd)),
+                           cfg["types"], cfg["k"], cfg["norm"], shared=tuple(host(b[0]) for b in L.shared),
+                           shared_gate_w=host(L.wsg.float()))
+    assert moe.rel_l2(of, want) < BAR
+
+
 def test_decode_layer_cfg2_residual():
     from larder_amd import layer as lay, workloads
     cfg = workloads.CONFIGS[2]
@@ -290,15 +324,16 @@ def test_tail_combine_vs_oracle():
     assert moe.rel_l2(host(got)[0], want) < 1e-6
 
 
-@pytest.mark.parametrize("E,k,norm,T,shared,H", [(60, 4, False, 1, True, 2048), (128, 8, True, 1, False, 2048),
-                                                  (128, 8, True, 5, False, 2048), (512, 10, True, 1, True, 4096),
-                                                  (512, 16, False, 3, False, 2048), (9, 9, True, 2, False, 2048),
-                                                  (256, 8, True, 16, True, 4096), (129, 7, True, 4, False, 2048)])
+@pytest.mark.parametrize("E,k,norm,T,shared,H", [(60, 4, False, 1, 1, 2048), (128, 8, True, 1, 0, 2048),
+                                                  (128, 8, True, 5, 0, 2048), (512, 10, True, 1, 1, 4096),
+                                                  (512, 16, False, 3, 0, 2048), (9, 9, True, 2, 0, 2048),
+                                                  (256, 8, True, 16, 1, 4096), (129, 7, True, 4, 0, 2048),
+                                                  (60, 4, False, 3, 4, 2048)])
 def test_router_gemv_rank_vs_oracle(E, k, norm, T, shared, H):
     """lmoe_router_gemv_rank (GEMV + top-k in one launch, the last workgroup ranking): logits bit-exact against the
     router GEMV's restated order, ids bit-exact against the oracle's top-k of those logits (planted equal rows: ties
     to the lowest index), scores to 2e-6, the folded shared expert's slot, and a second launch on the same arrival
-    counter giving the same bits."""
+    counter giving the same bits. shared: the folded shared expert's slices a token (0: none)."""
     from larder_amd import _lib
     rng = np.random.default_rng(E * 31 + k * 7 + T)
     wr = (rng.standard_normal((E, H)) * 0.02).astype(np.float16)
@@ -306,7 +341,7 @@ def test_router_gemv_rank_vs_oracle(E, k, norm, T, shared, H):
         wr[grp] = wr[grp[0]] * np.float16(3)              # equal rows: exactly equal logits
     x = rng.standard_normal((T, H)).astype(np.float16)
     wsg = (rng.standard_normal(H) * 0.02).astype(np.float16) if shared else None
-    ks = k + 1 if shared else k
+    ks = k + shared
     rows = E + (1 if shared else 0)
     dx, dwr = dev(x), dev(wr)
     dwsg = dev(wsg) if shared else None
@@ -334,5 +369,5 @@ def test_router_gemv_rank_vs_oracle(E, k, norm, T, shared, H):
     if shared:
         gate = moe.router_logits_gemv(x, wsg.reshape(1, -1))
         assert np.array_equal(lg[:, E:].view(np.uint32), gate.view(np.uint32))
-        assert (ids[:, k] == E).all()
-        assert np.allclose(sc[:, k], moe.sigmoid(gate[:, 0]), rtol=1e-6)
+        assert (ids[:, k:] == E + np.arange(shared)).all()
+        assert np.allclose(sc[:, k:], moe.sigmoid(gate[:, :1]), rtol=1e-6)
