@@ -73,7 +73,8 @@ int lmoe_router_gemv_topk(const void *x, int xdtype, const void *wr, const void 
  * then the ids / scores of lmoe_router_topk (ties to the lowest index, best first), plus the prepared activation rows
  * when xprep is given. The workgroup that finishes its rows last ranks every token, so no gate/up wavefront has to
  * rank (the fused form lmoe_moe_gate_up ranks in each of them). ks: slots a token in ids / scores, k or (with wsg)
- * k + 1, slot k then holding id E and weight sigmoid(x . wsg): the folded shared expert of lmoe_moe_gate_up_ext.
+ * k + m, slots k + j then holding id E + j and weight sigmoid(x . wsg): the folded shared expert's slices of
+ * lmoe_moe_gate_up_ext.
  * sync: one uint32 of device memory, zero before the first call, left zero by each call; one per stream (two calls
  * in flight on one counter race). E <= 512, k <= 16, T <= 16. Replaces the reference's gate linear + moe_probs
  * (route_cuda.py:193-254, 280-288, 433-444). */
@@ -119,13 +120,15 @@ int lmoe_moe_gate_up(const float *logits, int ld_stride, int T, int k, int norm,
                      int n_experts, int H, int I, uint32_t *ids, float *scores, uint32_t *hprep, int type_d,
                      void *stream);
 
-/* lmoe_moe_gate_up with the layer's shared expert folded in as one more slot a token (with_shared = 1; 0 is
- * lmoe_moe_gate_up): wg / wu hold n_experts + 1 experts, the last the shared expert (same shape and type as the
- * routed ones), logits rows hold the shared expert's gate logit at column n_experts (the router GEMV's row E), and
- * each token gets k + 1 slots: ids / scores [T][k + 1] with slot k = (n_experts, sigmoid(gate logit)), hprep
- * [T (k + 1)][I / 64 * 36]. lmoe_gemv_down_combine_prepped with k + 1 and wd of n_experts + 1 experts then weights
- * the shared expert like a routed one: three launches a layer instead of five. Takes the register-resident form
- * (H = 2048 or 4096, one type for gate and up). No counterpart in the reference (its shared expert is MLX ops,
+/* lmoe_moe_gate_up with the layer's shared expert folded in as m = with_shared more slots a token (0 is
+ * lmoe_moe_gate_up): a shared expert m times the routed width, cut into m slices of its intermediate features
+ * (slice j: gate / up rows [j I, (j + 1) I), down columns likewise), stored as experts n_experts .. n_experts + m - 1
+ * of wg / wu (same shape and type as the routed ones); logits rows hold the shared expert's gate logit at column
+ * n_experts (the router GEMV's row E), and each token gets k + m slots: ids / scores [T][k + m] with slot k + j =
+ * (n_experts + j, sigmoid(gate logit)), hprep [T (k + m)][I / 64 * 36]. lmoe_gemv_down_combine_prepped with k + m
+ * and wd of n_experts + m experts then weights the slices like routed experts, and their sum is the gated shared
+ * row: three launches a layer instead of five. Takes the register-resident form (H = 2048 or 4096, one type for
+ * gate and up), k + m <= 64. No counterpart in the reference (its shared expert is MLX ops,
  * stream_fast.py:4403-4405). */
 int lmoe_moe_gate_up_ext(const float *logits, int ld_stride, int T, int k, int norm, const uint32_t *xg_prep,
                          const uint32_t *xu_prep, const uint8_t *wg, const uint8_t *wu, int type_g, int type_u,
