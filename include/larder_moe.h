@@ -51,6 +51,13 @@ int lmoe_profile_read(float *ms, int cap, int *count);
 int lmoe_router_topk(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids, float *scores,
                      void *stream);
 
+/* lmoe_router_topk on fp32 logits [T][E] with a folded shared expert's m slices appended to every token (no
+ * counterpart in the reference; the prefill form of lmoe_moe_gate_up_ext's slots): ids / scores [T][k + m], slot
+ * k + j = (E + j, sigmoid(gate[t])), gate [T] the shared expert's gate logits (lmoe_router_gemm's gate output). The
+ * grouped GEMMs then run the slices as experts E .. E + m - 1 of the extended weight buffers. k + m <= 64. */
+int lmoe_router_topk_shared(const float *logits, int T, int E, int k, int norm, const float *gate, int m,
+                            uint32_t *ids, float *scores, void *stream);
+
 /* Prepared activation rows: an activation row of 64 P values as P units of 36 dwords (32 dwords of f16 pairs in
  * the nibble order of block type qtype, the sums of the unit's two 32-value halves as fp32, two zero dwords), the
  * form the expert kernels read. x [rows][H] in xdtype -> xprep [rows][H / 64 * 36] uint32. */

@@ -35,6 +35,7 @@ SIGNATURES = {
     "lmoe_profile_arm": (_I, [_I]),
     "lmoe_profile_read": (_I, [_P, _I, _P]),
     "lmoe_router_topk": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "lmoe_router_topk_shared": (_I, [_P, _I, _I, _I, _I, _P, _I, _P, _P, _P]),
     "lmoe_prep_x": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "lmoe_router_gemv": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
     "lmoe_router_gemv_topk": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P]),

@@ -19,9 +19,12 @@ namespace lmoe {
 constexpr int kMaxNpl = 16;  // logits a lane: E <= 64 * 16
 
 // Four tokens a workgroup, one wavefront each.
+// m > 0: each token's ids / scores rows hold k + m entries, the last m the folded shared expert's slices
+// (E + j, sigmoid(gate[t])).
 template <int NPL>
 __global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt, int ld_stride, int T, int E,
-                                                     int k, int norm, uint32_t *ids, float *scores) {
+                                                     int k, int norm, uint32_t *ids, float *scores,
+                                                     const float *gate = nullptr, int m = 0) {
   __shared__ __attribute__((aligned(16))) uint32_t scr[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
@@ -36,9 +39,13 @@ __global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt
   uint32_t id;
   float sc;
   topk_wave<NPL>(v, E, k, norm, scr[wave], &id, &sc);
+  const int ks = k + m;
   if (lane < k) {
-    ids[size_t(t) * k + lane] = id;
-    scores[size_t(t) * k + lane] = sc;
+    ids[size_t(t) * ks + lane] = id;
+    scores[size_t(t) * ks + lane] = sc;
+  } else if (lane < ks) {
+    ids[size_t(t) * ks + lane] = uint32_t(E + lane - k);
+    scores[size_t(t) * ks + lane] = sigmoidf_(gate[t]);
   }
 }
 
@@ -599,7 +606,7 @@ __global__ void __launch_bounds__(1024) k_route_bias(RouteArgs a) {
 using namespace lmoe;
 
 static int topk_launch(const void *logits, int ldtype, int stride, int T, int E, int k, int norm, uint32_t *ids,
-                       float *scores, hipStream_t st, const char *fn) {
+                       float *scores, hipStream_t st, const char *fn, const float *gate = nullptr, int m = 0) {
   LMOE_REQUIRE(dtype_ok(ldtype), LMOE_EINVAL, "%s: logits dtype %d is not F32, F16 or BF16", fn, ldtype);
   LMOE_REQUIRE(T >= 0 && E > 0 && E <= 64 * kMaxNpl, LMOE_ESHAPE, "%s: %d experts is outside 1..%d", fn, E,
                64 * kMaxNpl);
@@ -608,15 +615,15 @@ static int topk_launch(const void *logits, int ldtype, int stride, int T, int E,
   LMOE_REQUIRE(logits && ids && scores, LMOE_EINVAL, "%s: null pointer", fn);
   const dim3 grid((T + 3) / 4), block(256);
   if (E <= 64)
-    launch(k_router_topk<1>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<1>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores, gate, m);
   else if (E <= 128)
-    launch(k_router_topk<2>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<2>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores, gate, m);
   else if (E <= 256)
-    launch(k_router_topk<4>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<4>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores, gate, m);
   else if (E <= 512)
-    launch(k_router_topk<8>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<8>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores, gate, m);
   else
-    launch(k_router_topk<16>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores);
+    launch(k_router_topk<16>, grid, block, 0, st, logits, ldtype, stride, T, E, k, norm, ids, scores, gate, m);
   LMOE_LAUNCHED(fn);
   return 0;
 }
@@ -624,6 +631,14 @@ static int topk_launch(const void *logits, int ldtype, int stride, int T, int E,
 extern "C" int lmoe_router_topk(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids,
                                 float *scores, void *stream) {
   return topk_launch(logits, ldtype, E, T, E, k, norm, ids, scores, (hipStream_t)stream, "lmoe_router_topk");
+}
+
+extern "C" int lmoe_router_topk_shared(const float *logits, int T, int E, int k, int norm, const float *gate, int m,
+                                       uint32_t *ids, float *scores, void *stream) {
+  const char *fn = "lmoe_router_topk_shared";
+  LMOE_REQUIRE(m >= 1 && k + m <= 64, LMOE_ESHAPE, "%s: %d shared slices with top-%d", fn, m, k);
+  LMOE_REQUIRE(T == 0 || gate, LMOE_EINVAL, "%s: null gate", fn);
+  return topk_launch(logits, LMOE_F32, E, T, E, k, norm, ids, scores, (hipStream_t)stream, fn, gate, m);
 }
 
 extern "C" int lmoe_prep_x(const void *x, int xdtype, int rows, int H, int qtype, uint32_t *xprep, void *stream) {

@@ -230,7 +230,6 @@ class PrefillBuffers:
             raise ValueError(f"y_dtype must be float16 or float32, not {y_dtype}")
         L = layer
         self.T = T
-        R = T * L.k
         f32 = dict(dtype=torch.float32, device=device)
         self.logits = torch.empty((T, L.E), **f32)
         self.gate = torch.empty(T, **f32) if L.shared is not None else None   # the shared expert's gate logit
@@ -238,15 +237,21 @@ class PrefillBuffers:
         if L.wr is not None:
             nrw = _lib.lib().lmoe_router_gemm_workspace_bytes(T, L.H, L.E + (1 if L.shared is not None else 0))
             self.rws = torch.empty(max(nrw // 4, 1), **f32)
-        self.ids = torch.empty((T, L.k), dtype=torch.int32, device=device)
-        self.scores = torch.empty((T, L.k), **f32)
-        self.G = Grouping(R, L.E, device, bm=pick_tile_rows(R, L.E, L.types))
-        nws = splitk_floats(R, L.E, self.G.bm, L.H, L.I)
+        # a folded shared expert (MoELayer.folded, m slices) rides in the routed GEMMs as experts E .. E + m - 1,
+        # slots k .. k + m - 1 of every token, when the router weight gives its gate logit
+        self.fold = L.folded is not None and L.wr is not None
+        ks, ne = (L.k + L.n_shared, L.E + L.n_shared) if self.fold else (L.k, L.E)
+        R = T * ks
+        self.ids_ext = torch.empty((T, ks), dtype=torch.int32, device=device)
+        self.scores_ext = torch.empty((T, ks), **f32)
+        self.ids, self.scores = self.ids_ext[:, :L.k], self.scores_ext[:, :L.k]  # the routed picks
+        self.G = Grouping(R, ne, device, bm=pick_tile_rows(R, ne, L.types))
+        nws = splitk_floats(R, ne, self.G.bm, L.H, L.I)
         self.ws = torch.empty(nws, **f32) if nws else None
         self.xh = torch.empty((T, L.H), dtype=torch.float16, device=device)
         self.h = torch.empty((R, L.I), dtype=torch.float16, device=device)
         self.y = torch.empty((R, L.H), dtype=y_dtype, device=device)
-        if L.shared is not None:
+        if L.shared is not None and not self.fold:
             self.Gs = Grouping.identity(T, device, bm=pick_tile_rows(T, 1, L.types))
             self.hs = torch.empty((T, L.Is), dtype=torch.float16, device=device)
             self.ys = torch.empty((T, L.H), **f32)
@@ -280,6 +285,22 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
         if logits.dtype != torch.float32 or not logits.is_contiguous() or tuple(logits.shape) != (T, L.E):
             raise ValueError(f"logits must be float32 [{T}, {L.E}] and contiguous")
         lg = logits
+    if B.fold:  # the shared expert's slices as experts E .. E + m - 1 in the routed GEMMs: no side stream
+        m = L.n_shared
+        ks = L.k + m
+        call("lmoe_router_topk_shared", ptr(lg), T, L.E, L.k, int(L.norm), ptr(B.gate), m, ptr(B.ids_ext),
+             ptr(B.scores_ext), st)
+        B.G.run(B.ids_ext.reshape(-1))
+        fs = L.folded_stream or (None, None, None)
+        sl_ok = lambda t: t == "Q4_0" or B.G.bm == 64  # noqa: E731
+        fg, fu, fd = L.folded
+        gate_up(B.xh, B.G, ks, fg, fu, L.types, B.h, prepped=True, ws=B.ws,
+                sl=fs[:2] if fs[0] is not None and sl_ok(L.types[0]) else None)
+        down(B.h, B.G, fd, L.types[2], B.y, ws=B.ws, sl=fs[2] if sl_ok(L.types[2]) else None)
+        call("lmoe_combine_sorted", ptr(B.y), dcode(B.y.dtype), ptr(B.G.inv), ptr(B.scores_ext), T, ks, H, None,
+             None, 0, ptr(residual), dcode(residual.dtype) if residual is not None else 0, ptr(out), dcode(out.dtype),
+             st)
+        return out
     shared = gate = None
     if L.shared is not None:  # x is ready: the shared expert starts on the side stream
         main = torch.cuda.current_stream()
@@ -294,8 +315,8 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
             down(B.hs, B.Gs, sd, L.types[2], B.ys, sl=ss[2] if s_ok(L.types[2]) else None)
             B.shared_done.record(B.side)
         shared, gate = ptr(B.ys), ptr(B.gate)
-    call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids), ptr(B.scores), st)
-    B.G.run(B.ids.reshape(-1))
+    call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids_ext), ptr(B.scores_ext), st)
+    B.G.run(B.ids_ext.reshape(-1))
     f16, sl = L.prefill_f16, L.stream_w or (None, None, None)
     sl_ok = lambda t: t == "Q4_0" or B.G.bm == 64  # noqa: E731  (stream-layout Q4_K: the 64-row kernel)
     gate_up(B.xh, B.G, L.k, L.wg, L.wu, L.types, B.h, prepped=True, ws=B.ws,
@@ -305,7 +326,7 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
          sl=sl[2] if sl_ok(L.types[2]) else None)
     if L.shared is not None:
         torch.cuda.current_stream().wait_event(B.shared_done)
-    call("lmoe_combine_sorted", ptr(B.y), dcode(B.y.dtype), ptr(B.G.inv), ptr(B.scores), T, L.k, H, shared, gate,
+    call("lmoe_combine_sorted", ptr(B.y), dcode(B.y.dtype), ptr(B.G.inv), ptr(B.scores_ext), T, L.k, H, shared, gate,
          1 if shared is not None else 0, ptr(residual), dcode(residual.dtype) if residual is not None else 0,
          ptr(out), dcode(out.dtype), st)
     return out

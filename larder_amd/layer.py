@@ -69,6 +69,7 @@ class MoELayer:
         self.prefill_f16 = None
         self.stream_w = None
         self.shared_stream = None
+        self.folded_stream = None
         self._router_k = None
 
     def router_gemm_weight(self):
@@ -108,13 +109,19 @@ class MoELayer:
         expert's likewise; a projection that has no stream layout keeps None. Returns the bytes held."""
         from . import grouped
         tg, tu, td = self.types
+        # a folded layer's copies cover its extended buffers (the shared slices too); the routed ones are prefixes
+        src = self.folded if self.folded is not None else (self.wg, self.wu, self.wd)
         gu = None
         if tg == tu and tg in _lib.Q4_TYPES and self.I % 128 == 0:
-            gu = (grouped.stream_copy(self.wg, tg), grouped.stream_copy(self.wu, tu))
-        dn = grouped.stream_copy(self.wd, td) if td in _lib.Q4_TYPES and self.H % 128 == 0 else None
-        self.stream_w = (gu[0] if gu else None, gu[1] if gu else None, dn)
-        held = [t for t in self.stream_w if t is not None]
-        if self.shared is not None:  # the shared expert's GEMMs on the same kernels
+            gu = (grouped.stream_copy(src[0], tg), grouped.stream_copy(src[1], tu))
+        dn = grouped.stream_copy(src[2], td) if td in _lib.Q4_TYPES and self.H % 128 == 0 else None
+        full = (gu[0] if gu else None, gu[1] if gu else None, dn)
+        held = [t for t in full if t is not None]
+        if self.folded is not None:
+            self.folded_stream = full
+            full = tuple(t[:self.E] if t is not None else None for t in full)
+        self.stream_w = full
+        if self.shared is not None and self.folded is None:  # the shared expert's GEMMs on the same kernels
             sg, su, sd = self.shared
             sgu = ((grouped.stream_copy(sg, tg), grouped.stream_copy(su, tu))
                    if tg == tu and tg in _lib.Q4_TYPES and self.Is % 128 == 0 else None)

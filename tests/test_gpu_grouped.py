@@ -216,6 +216,42 @@ def test_prefill_layer_cfg1_shared_expert():
     assert rows_ok(host(out), want) < ROW_BAR
 
 
+@pytest.mark.parametrize("cfgid,T", [(1, 150), (5, 96)])
+def test_prefill_folded_shared_matches_apart(cfgid, T):
+    """A shared expert folded into the grouped GEMMs (cfg1: four slices of the routed width, cfg5: one; slots
+    k .. k + m - 1 of every token from lmoe_router_topk_shared) against the same layer with the shared expert run
+    apart on a side stream: equal routed ids, the slots' ids E + j and sigmoid weights, outputs within the bar."""
+    from larder_amd import grouped, workloads
+    from larder_amd.layer import MoELayer
+    cfg = dict(workloads.CONFIGS[cfgid])
+    if cfgid == 5:
+        cfg.update(E=64)
+    L, g = _device_layer(cfg, 21)
+    assert L.folded is not None and L.n_shared == cfg["Is"] // cfg["I"]
+    U = MoELayer(L.wg, L.wu, L.wd, L.types, L.k, L.norm, wr=L.wr, shared=L.shared, wsg=L.wsg, fold_shared=False)
+    x = torch.randn((T, cfg["H"]), generator=g, device="cuda").half()
+    outs = []
+    for layer in (L, U):
+        B = grouped.PrefillBuffers(layer, T)
+        assert B.fold == (layer is L)
+        out = torch.empty((T, cfg["H"]), dtype=torch.float32, device="cuda")
+        grouped.prefill(layer, x, B, out)
+        torch.cuda.synchronize()
+        outs.append((host(out), host(B.ids).copy(), B))
+    (of, idf, Bf), (ou, idu, _) = outs
+    assert (idf == idu).all()
+    m = L.n_shared
+    assert (host(Bf.ids_ext)[:, cfg["k"]:] == cfg["E"] + np.arange(m)).all()
+    gate = host(Bf.gate)
+    assert np.allclose(host(Bf.scores_ext)[:, cfg["k"]:], 1 / (1 + np.exp(-gate[:, None])), rtol=1e-5)
+    assert moe.rel_l2(of, ou) < BAR
+    lg = host(Bf.logits)
+    _, _, want = moe.layer(host(x.float()), lg, tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"], cfg["k"],
+                           cfg["norm"], shared=tuple(host(b[0]) for b in L.shared), shared_gate_w=host(L.wsg.float()))
+    assert moe.rel_l2(of, want) < BAR
+    assert rows_ok(of, want) < ROW_BAR
+
+
 def test_prefill_matches_decode_chain():
     """The grouped path and the decode chain (separately checked against the oracle) agree on the same tokens."""
     from larder_amd import grouped, layer as lay, workloads
