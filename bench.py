@@ -282,13 +282,14 @@ def grouped_leg():
     torch.cuda.synchronize()
     us5p = e0.elapsed_time(e1) / 10 * 1e3
     f5 = workloads.expert_flops(cfg5, T5 * cfg5["k"]) + 2 * T5 * 3 * cfg5["H"] * cfg5["Is"]
-    u5 = int((B5.G.counts > 0).sum().item())
+    u5 = int((B5.G.counts[:cfg5["E"]] > 0).sum().item())  # routed experts (the folded shared one is counted apart)
     by5 = workloads.decode_bytes(cfg5, u5) + T5 * cfg5["H"] * 2 * 2
     out["cfg5_prefill_T2048"] = {"us": round(us5p, 1), "tokens_per_s": round(T5 / (us5p * 1e-6), 1),
                                  "mfma_frac": round(f5 / (us5p * 1e-6) / MFMA_PEAK, 4),
                                  "hbm_frac": round(by5 / (us5p * 1e-6) / HBM_PEAK, 4), "experts_touched": u5,
-                                 "note": "router logits by lmoe_router_gemm inside the timing; the shared expert on a "
-                                         "side stream; the grouped GEMMs read stream-layout copies of the experts"}
+                                 "note": "router logits by lmoe_router_gemm inside the timing; the shared expert folded "
+                                         "into the routed GEMMs as expert E (slot k of every token); the grouped GEMMs "
+                                         "read stream-layout copies of the experts"}
     return out
 
 
