@@ -175,6 +175,34 @@ int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sums, const ui
                                    const float *shared, const float *gate, int gate_stride, const void *residual,
                                    int rdtype, void *out, int odtype, void *stream);
 
+/* The decode chain with the router GEMV folded into its neighbours (a stack of layers: two launches a layer instead
+ * of three). The router's logits are sums over 8-element items of x: lmoe_router_gemv forms each item's products as
+ * one fma chain from zero and adds the chains in a fixed tree (per wavefront a balanced tree over 64 items, then the
+ * four wavefronts in order). At H = 2048 each of its threads holds exactly one item, so those item chains, the
+ * router partials part [T][256][R] (R = E rows, plus the shared gate row last when wsg is given), rebuild the
+ * logits bit for bit. Replaces the block's gate linear and top-k as in lmoe_router_gemv / lmoe_moe_gate_up
+ * (stream_fast.py:4358-4370, route_cuda.py:433-444); the split into partials has no counterpart in the reference.
+ *   lmoe_router_part: the partials of x [T][H] against wr [E][H] (+ wsg [H]), for the first layer of a stack.
+ *   lmoe_moe_gate_up_part: lmoe_moe_gate_up_ext's work (ids / scores [T][k + m], hprep [T (k + m)][I / 64 * 36])
+ *     with the logits summed from part and x [T][H] raw in xdtype (prepared in-kernel); the ids are those
+ *     lmoe_router_gemv + lmoe_moe_gate_up give, bit for bit. m = shared_slices (0: none; else the router's R
+ *     includes the gate row). H = 2048, E + (m > 0) <= 256, one type for gate and up.
+ *   lmoe_gemv_down_combine_part: lmoe_gemv_down_combine_prepped (no separate shared row) whose output rows, as
+ *     stored in odtype, also give the NEXT layer's partials against wr_next [e_next][H] (+ wsg_next) into part. It
+ *     takes the one-wavefront-a-row-pair form: at most 128 h units a token (k I / 64), I / 64 even.
+ * Measured on MI355X at cfg2's shape (48 layers, E 128, k 8, one token) the three entries run a layer in 22.2 us
+ * against 15.0 for the three-launch chain: every gate/up workgroup (16 wavefronts) reads all 256 x R partials, and
+ * the wider workgroups with their in-kernel x preparation cost more than the router launch they remove. */
+int lmoe_router_part(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T, int H, int E,
+                     float *part, void *stream);
+int lmoe_moe_gate_up_part(const float *part, const void *x, int xdtype, int T, int k, int norm, const uint8_t *wg,
+                          const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I, uint32_t *ids,
+                          float *scores, uint32_t *hprep, int type_d, int shared_slices, void *stream);
+int lmoe_gemv_down_combine_part(const uint32_t *hprep, const uint32_t *ids, const float *scores, int T, int k,
+                                const uint8_t *wd, int type_d, int n_experts, int I, int H, const void *residual,
+                                int rdtype, void *out, int odtype, const void *wr_next, const void *wsg_next,
+                                int wdtype_next, int e_next, float *part, void *stream);
+
 /* Batch-1 decode through a stack of L MoE layers of one shape in ONE kernel launch: x_{l+1} = x_l + moe_l(x_l),
  * moe_l = router logits (f16 router weight, plus the shared gate row when Is > 0), softmax top-k (ties to the
  * lowest index), the k experts' gate/up + SwiGLU and down read from GGUF blocks, weighted by the softmax scores

@@ -48,6 +48,10 @@ SIGNATURES = {
     "lmoe_gemv_down_combine": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_gemv_down_combine_prepped": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I,
                                             _P]),
+    "lmoe_router_part": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P]),
+    "lmoe_moe_gate_up_part": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
+    "lmoe_gemv_down_combine_part": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I, _P,
+                                         _P]),
     "lmoe_gemv_gate_up_runs": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "lmoe_gemv_down_runs": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_group_workspace_bytes": (_SZ, [_I, _I]),

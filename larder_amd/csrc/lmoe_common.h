@@ -512,6 +512,50 @@ __device__ __forceinline__ float word_dot(uint32_t w, const uint32_t *xp, float 
 __device__ __forceinline__ float half_lo(uint32_t w) { return float(__builtin_bit_cast(h2_t, w)[0]); }
 __device__ __forceinline__ float half_hi(uint32_t w) { return float(__builtin_bit_cast(h2_t, w)[1]); }
 
+// 8 values at element index i of a row of dtype dt, from one or two 16-byte chunks already loaded
+__device__ __forceinline__ void unpack8(const u32x4 &a, const u32x4 &b, int dt, float *v) {
+  const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  if (dt == LMOE_F32) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(u[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = dt == LMOE_F16 ? half_lo(u[e]) : __uint_as_float(u[e] << 16);
+      v[2 * e + 1] = dt == LMOE_F16 ? half_hi(u[e]) : __uint_as_float(u[e] & 0xFFFF0000u);
+    }
+  }
+}
+
+// v as the element it becomes when stored as dtype dt and read back (the value a later kernel reads)
+__device__ __forceinline__ float round_elt(float v, int dt) {
+  if (dt == LMOE_F32) return v;
+  if (dt == LMOE_F16) return float(_Float16(v));
+  return bf16_to_f32(f32_to_bf16(v));
+}
+
+// ---- router partials -------------------------------------------------------------------------------------------
+//
+// The decode router's logits are sums over 8-element items of x (item i: elements [8 i, 8 i + 8)). k_router_gemv
+// (router.hip) forms each item's products as one fma chain from zero, adds the chains of its 256 threads as a
+// balanced tree over each wavefront's 64 items, then the four wavefront totals left to right. When H / 8 <= 256 each
+// thread holds exactly one item, so the logits can be rebuilt bit for bit from the item chains alone: partials
+// [T][H / 8][R] (R router rows, the shared expert's gate row last) written by whoever owns the item's 8 values, then
+// summed in that same tree (items past H / 8 add a +0). That lets the kernel that produces x (the previous layer's
+// down) emit the next router's partials, and the kernel that consumes the logits (gate/up) finish them.
+constexpr int kPartItems = 256;  // items a token at most: H <= 2048
+constexpr int kPartRows = 256;   // router rows at most (experts + the shared expert's gate)
+
+// item i's fma chain against router row r (8 weights of element type wdt: one 16-byte chunk, two for f32)
+__device__ __forceinline__ float part_chain(const float *x8, const u32x4 &w0, const u32x4 &w1, int wdt) {
+  float w[8];
+  unpack8(w0, w1, wdt, w);
+  float acc = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = fmaf(x8[e], w[e], acc);
+  return acc;
+}
+
 // ---- x arrangement ----------------------------------------------------------------------------------------------
 //
 // A unit of 64 weights takes 32 dwords of x pairs, arranged so that word i of a block's (or sub-block pair's)

@@ -12,6 +12,7 @@ GGUF blocks, the weighted combine, and a sigmoid-gated shared expert when the mo
   * prefill / batched decode (any T): the device grouping and the grouped MFMA GEMMs (larder_amd.grouped).
 """
 import ctypes
+import os
 
 import torch
 
@@ -236,6 +237,59 @@ def decode(layer, x, bufs, out, residual=None, logits=None):
     return out
 
 
+# Router partials (lmoe_router_part / lmoe_moe_gate_up_part / lmoe_gemv_down_combine_part): hidden 2048 (one 8-value
+# item a router thread), at most 256 router rows, and the down kernel that takes a row pair a wavefront.
+PART_ITEMS, PART_ROWS = 256, 256
+# Whether a DecodeStack whose layers all allow it folds each router GEMV into its neighbours: the previous layer's
+# down writes the item partials of the next router, gate/up sums them (two launches a layer instead of three, the
+# same bits). Off unless LMOE_ROUTER_PARTS=1: on cfg2's 48-layer graph it measured 22.2 us a layer against 15.0
+# for the three-launch chain (every 16-wavefront gate/up workgroup reads all 256 x E partials, written by other
+# XCDs, and the wider workgroups, the in-kernel x preparation and the extra barriers cost more than the launch).
+ROUTER_PARTS = os.environ.get("LMOE_ROUTER_PARTS", "0") == "1"
+
+
+def part_ok(layer):
+    """Whether ``layer`` can take its logits as router partials (and its down can emit the next layer's)."""
+    L = layer
+    if L.wr is None or (L.shared is not None and L.folded is None) or L.H != 8 * PART_ITEMS:
+        return False
+    if (L.wsg is not None) != (L.folded is not None):  # the gate row travels with the folded shared expert only
+        return False
+    if L.E + (1 if L.wsg is not None else 0) > PART_ROWS or L.types[0] != L.types[1]:
+        return False
+    if any(t not in ("Q4_0", "Q4_K") for t in L.types) or L.I % 64 or (L.types[2] == "Q4_K" and L.I % 256):
+        return False
+    ks, P = L.k + L.n_shared, L.I // 64
+    return P % 2 == 0 and ks * P <= 128 and ks * 9 * P // 2 <= 576 and ks <= 64 and L.k <= 32
+
+
+def decode_part(layer, x, bufs, out, part, nxt=None):
+    """out = x + layer(x) with the router logits summed from ``part`` (the item partials of x against this layer's
+    router, written by lmoe_router_part or the previous layer's down), gate/up then down; when ``nxt`` is given the
+    down also writes x_out's partials against nxt's router into ``part`` (after gate/up has read them, in stream
+    order). Same bits as ``decode(layer, x, bufs, out, residual=x)``."""
+    L, B = layer, bufs
+    T = x.shape[0]
+    st = stream()
+    tg, tu, td = (qcode(t) for t in L.types)
+    xd = dcode(x.dtype)
+    if L.folded is not None:
+        (wg, wu, wd), m = L.folded, L.n_shared
+    else:
+        wg, wu, wd, m = L.wg, L.wu, L.wd, 0
+    ks = L.k + m
+    call("lmoe_moe_gate_up_part", ptr(part), ptr(x), xd, T, L.k, int(L.norm), ptr(wg), ptr(wu), tg, tu, L.E, L.H,
+         L.I, ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.hprep), td, m, st)
+    if nxt is None:
+        call("lmoe_gemv_down_combine_prepped", ptr(B.hprep), 0, ptr(B.ids_ext), ptr(B.scores_ext), T, ks, ptr(wd), td,
+             L.E + m, L.I, L.H, None, None, 0, ptr(x), xd, ptr(out), dcode(out.dtype), st)
+    else:
+        call("lmoe_gemv_down_combine_part", ptr(B.hprep), ptr(B.ids_ext), ptr(B.scores_ext), T, ks, ptr(wd), td,
+             L.E + m, L.I, L.H, ptr(x), xd, ptr(out), dcode(out.dtype), ptr(nxt.wr), ptr(nxt.wsg),
+             dcode(nxt.wr.dtype), nxt.E, ptr(part), st)
+    return out
+
+
 def _ptr_offset(t, elems):
     """Device pointer ``elems`` elements into tensor t."""
     return ctypes.c_void_p(t.data_ptr() + elems * t.element_size())
@@ -246,7 +300,7 @@ class DecodeStack:
     fused into each layer's combine. ``step`` runs eagerly; ``capture`` records one step as a HIP graph reading
     ``self.x_in`` and leaving the result in ``self.x_out``."""
 
-    def __init__(self, layers, T, dtype=torch.float16, device="cuda"):
+    def __init__(self, layers, T, dtype=torch.float16, device="cuda", parts=None):
         self.layers = layers
         self.T = T
         self.bufs = DecodeBuffers(layers[0], T, device)
@@ -255,12 +309,28 @@ class DecodeStack:
         self.ping = torch.empty((T, H), dtype=dtype, device=device)
         self.pong = torch.empty((T, H), dtype=dtype, device=device)
         self.graph = None
+        # the router folded into its neighbours (decode_part) when every layer allows it
+        self.parts = (ROUTER_PARTS if parts is None else parts) and all(part_ok(L) for L in layers)
+        if parts and not self.parts:
+            raise ValueError("router partials need hidden 2048, at most 256 router rows, one gate/up type and at "
+                             "most 128 h units a token in every layer")
+        if self.parts:
+            rows = max(L.E + (1 if L.wsg is not None else 0) for L in layers)
+            self.part = torch.empty(T * PART_ITEMS * rows, dtype=torch.float32, device=device)
 
     def step(self):
         cur = self.x_in
+        if self.parts:
+            L0 = self.layers[0]
+            call("lmoe_router_part", ptr(cur), dcode(cur.dtype), ptr(L0.wr), ptr(L0.wsg), dcode(L0.wr.dtype), self.T,
+                 L0.H, L0.E, ptr(self.part), stream())
         for i, L in enumerate(self.layers):
             nxt = self.ping if i % 2 == 0 else self.pong
-            decode(L, cur, self.bufs, nxt, residual=cur)
+            if self.parts:
+                decode_part(L, cur, self.bufs, nxt, self.part,
+                            self.layers[i + 1] if i + 1 < len(self.layers) else None)
+            else:
+                decode(L, cur, self.bufs, nxt, residual=cur)
             cur = nxt
         self.x_out = cur
         return cur

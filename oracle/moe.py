@@ -101,6 +101,35 @@ def router_logits_gemv(x, w):
             + waves[..., 3]).astype(np.float32)
 
 
+def router_partials(x, w):
+    """Item chains [T, H / 8, R] of the router GEMV's order (larder_amd/csrc/router.hip k_router_gemv with one item
+    a thread, H <= 2048; emitted by lmoe_router_part and by the down kernel for the next layer): item i of token t
+    against row r adds the products x[t, 8 i + j] w[r, 8 i + j], j = 0..7, in order from zero in float32. Exact
+    products for f16 / bf16 inputs, so these are the fma chain's bits."""
+    x = np.asarray(x, np.float32)
+    H = x.shape[-1]
+    p = _exact_products(x, w, H)
+    T, R = p.shape[:2]
+    p = p.reshape(T, R, H // 8, 8)
+    acc = np.zeros((T, R, H // 8), np.float32)
+    for j in range(8):
+        acc = (acc + p[..., j]).astype(np.float32)
+    return np.ascontiguousarray(acc.transpose(0, 2, 1))
+
+
+def router_logits_from_partials(part):
+    """Logits [T, R] from item chains [T, n, R] (n <= 256 items; the rest count as +0) in k_router_gemv's tree:
+    a balanced tree over each wavefront's 64 items, then the four wavefront totals left to right (the sum that
+    lmoe_moe_gate_up_part forms before its top-k)."""
+    part = np.asarray(part, np.float32)
+    T, n, R = part.shape
+    acc = np.zeros((T, R, 256), np.float32)
+    acc[:, :, :n] = part.transpose(0, 2, 1)
+    waves = _tree(acc.reshape(T, R, 4, 64))
+    return (((waves[..., 0] + waves[..., 1]).astype(np.float32) + waves[..., 2]).astype(np.float32)
+            + waves[..., 3]).astype(np.float32)
+
+
 def group_rows(ids, n_experts):
     """Flattened (token, k) rows bucketed by expert id: (counts [E], offsets [E + 1], order [R], inv [R]) with
     ``order`` the stable argsort of the flat ids (rows of one expert in flat order, experts ascending),

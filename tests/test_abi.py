@@ -112,6 +112,32 @@ def test_refusals_without_a_gpu(built_lib):
     assert rc == _lib.ESHAPE and b"64-row" in L.lmoe_error()
     rc = L.lmoe_grouped_down_sl(p, 64, p, p, p, 4, 32, 1, None, p, _lib.Q4_K, 8, 512, 1024, p, _lib.F16, None)
     assert rc == _lib.ESHAPE and b"64-row" in L.lmoe_error()
+    # router partials: hidden 2048 (one item a router thread), at most 256 router rows, the row-pair down kernel
+    rc = L.lmoe_router_part(p, _lib.F16, p, None, _lib.F16, 1, 4096, 128, p, None)
+    assert rc == _lib.ESHAPE and b"one 8-element item" in L.lmoe_error()
+    rc = L.lmoe_router_part(p, _lib.F16, p, p, _lib.F16, 1, 2048, 256, p, None)
+    assert rc == _lib.ESHAPE and b"257 router rows" in L.lmoe_error()
+    rc = L.lmoe_router_part(ctypes.c_void_p(18), _lib.F16, p, None, _lib.F16, 1, 2048, 128, p, None)
+    assert rc == _lib.EALIGN
+    rc = L.lmoe_moe_gate_up_part(p, p, _lib.F16, 1, 8, 1, p, p, _lib.Q4_K, _lib.Q4_K, 512, 4096, 512, p, p, p,
+                                 _lib.Q4_K, 1, None)
+    assert rc == _lib.ESHAPE and b"hidden 2048" in L.lmoe_error()
+    rc = L.lmoe_moe_gate_up_part(p, p, _lib.F16, 1, 8, 1, p, p, _lib.Q4_0, _lib.Q4_0, 256, 2048, 768, p, p, p,
+                                 _lib.Q4_0, 1, None)
+    assert rc == _lib.ESHAPE and b"257 router rows" in L.lmoe_error()
+    rc = L.lmoe_moe_gate_up_part(p, p, _lib.F16, 1, 8, 1, p, p, _lib.Q4_0, _lib.Q4_K, 128, 2048, 768, p, p, p,
+                                 _lib.Q4_0, 0, None)
+    assert rc == _lib.ESHAPE and b"one type" in L.lmoe_error()
+    # 8 slots of 22 units (cfg1's folded shape) need two wavefronts a row pair: no partials there
+    rc = L.lmoe_gemv_down_combine_part(p, p, p, 1, 8, p, _lib.Q4_0, 64, 1408, 2048, p, _lib.F16, p, _lib.F16, p,
+                                       p, _lib.F16, 60, p, None)
+    assert rc == _lib.ESHAPE and b"128 h units" in L.lmoe_error()
+    rc = L.lmoe_gemv_down_combine_part(p, p, p, 1, 8, p, _lib.Q4_0, 128, 768, 2048, p, _lib.F16, p, _lib.F16, p,
+                                       None, _lib.F16, 300, p, None)
+    assert rc == _lib.ESHAPE and b"router rows" in L.lmoe_error()
+    rc = L.lmoe_gemv_down_combine_part(p, p, p, 1, 8, p, _lib.Q4_0, 128, 768, 2048, p, _lib.F16, p, _lib.F16,
+                                       ctypes.c_void_p(18), None, _lib.F16, 128, p, None)
+    assert rc == _lib.EALIGN
 
 
 def test_grouped_refusals_without_a_gpu(built_lib):

@@ -88,3 +88,35 @@ def test_planted_order_mistake_is_caught():
     p = (x.astype(np.float32) * w.astype(np.float32)).reshape(512, 4)
     wrong = moe._tree(moe._tree(p))   # tree inside the chunk: (2^24 + 1) + (1 + 1) = 2^24 + 2 for lane 0
     assert wrong != moe.router_logits_stack(x, w)[0, 0]
+
+
+def test_partials_rebuild_the_gemv_order():
+    """The item chains (oracle.moe.router_partials, the decode stack's router partials) summed in the router's tree
+    give router_logits_gemv's bits: on random f16 rows (H 2048: 256 items; H 1024: items past 128 count as +0) and
+    on the order-deciding one-hot cases above."""
+    rng = np.random.default_rng(7)
+    for H in (2048, 1024):
+        x = (rng.standard_normal((3, H)) * 4).astype(np.float16)
+        w = (rng.standard_normal((9, H)) * 4).astype(np.float16)
+        part = moe.router_partials(x, w)
+        assert part.shape == (3, H // 8, 9)
+        assert np.array_equal(moe.router_logits_from_partials(part), moe.router_logits_gemv(x, w))
+    for placements in ([(0, BIG), (512, 1), (1024, 1), (1536, 1)], [(0, BIG), (8, 1), (16, 1)],
+                       [(0, BIG), (512, 2)]):
+        x, w = _one_hot_products(2048, placements)
+        assert np.array_equal(moe.router_logits_from_partials(moe.router_partials(x, w)),
+                              moe.router_logits_gemv(x, w))
+
+
+def test_partials_chain_in_element_order():
+    # item 0 = elements 0..7 with products 2^24, 1, 1, 1, 1, 1, 1, 1: added in order from zero every +1 rounds back
+    # (2^24 + 1 -> 2^24, ties to even), so the chain is 2^24; a tree over the item would keep the ones (2^24 + 6)
+    x, w = _one_hot_products(2048, [(0, BIG)] + [(i, 1) for i in range(1, 8)])
+    part = moe.router_partials(x, w)
+    assert part[0, 0, 0] == BIG and part[0, 1, 0] == 0
+    p = (x.astype(np.float32) * w.astype(np.float32))[0, :8]
+    assert moe._tree(p) == np.float32(2.0 ** 24 + 6) != part[0, 0, 0]
+    # the ones of item 1 (elements 8..15) stay in their own chain: 8, and the tree then gives (2^24 + 8)
+    x, w = _one_hot_products(2048, [(0, BIG)] + [(i, 1) for i in range(8, 16)])
+    part = moe.router_partials(x, w)
+    assert part[0, 1, 0] == 8 and moe.router_logits_from_partials(part)[0, 0] == np.float32(2.0 ** 24 + 8)
