@@ -385,8 +385,8 @@ __device__ __forceinline__ void q0_step(const uint8_t *st, const Q0Lane &L, int 
 // 128 j .. 128 j + 127 (tile features 0..127 their gate rows, 128..255 their up rows), K = H, A rows
 // x[order[p] / topk], out h [R][I] f16. DOWN: n-tile j covers output features 256 j .., K = I, A rows h[p], out
 // y [R][H] in odt (F16 / F32). Host guarantees: K % 64 == 0, rows x K x 2 and the expert's weight block under 4 GiB.
-// GMT: tile rows (the grouping's bm): 128 with NST = 3 stages, 64 with 4, or 32 with 5 for groups of few rows,
-// where the kernel streams weights and more steps in flight matter more than A reuse.
+// GMT: tile rows (the grouping's bm): 128 with NST = 3 stages, 64 with 4, or 32 with 3 or 5 for groups of few rows,
+// where the kernel streams weights (5: more steps in flight; 3: four workgroups a CU instead of two).
 // ksplit > 1 (32-row tiles): workgroup kpart takes K steps [kpart nk / ksplit, +nk / ksplit) and writes its fp32
 // sums to ws[kpart][row][feature] (features: gate/up = gate 0..I-1, up I..2I-1; down = 0..H-1; ldw of them a row,
 // R rows a slice); k_splitk_finish adds the slices and applies the epilogue.
@@ -1298,6 +1298,16 @@ static int check_split(const char *fn, int bm, int type, int ksplit, const float
 
 // The grouped GEMMs' launches. sl: the weights are stream-layout copies (k_stream_repack), which the Q4_0 kernels
 // take at every tile height and the Q4_K kernel at 64 rows.
+// LDS stages of the 32-row Q4_0 tiles (batched decode: each tile streams one expert's weights): 3 (40 KB, four
+// workgroups a CU, two steps in flight) by default; LMOE_Q0_STAGES=4 or 5 trades workgroups for steps in flight
+// (53 KB: three a CU; 66 KB: two, four steps ahead). At 3, cfg4's ~620 gate/up tiles run in one wave of workgroups
+// instead of a full wave and a ragged second one: 120.4 -> 101.8 us a step on stream copies, 152.2 -> 147.7 on the
+// GGUF layout with split-K, the same bits.
+static int q0_stages32() {
+  const int v = env_knob("LMOE_Q0_STAGES");
+  return v == 4 || v == 5 ? v : 3;
+}
+
 static int grouped_gate_up(const char *fn, bool sl, const void *x, int xdtype, int T, int topk, const uint32_t *order,
                            const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles, int max_tiles,
                            int bm, int ksplit, float *ws, const uint8_t *wg, const uint8_t *wu, int type_g,
@@ -1330,10 +1340,15 @@ static int grouped_gate_up(const char *fn, bool sl, const void *x, int xdtype, i
     LMOE_REQUIRE((long long)T * H * 2 <= 0xFFFFFFFFll && (long long)I * (H / 64) * 36 <= 0xFFFFFFFFll, LMOE_ESHAPE,
                  "%s: x or one expert's weights exceed 4 GiB", fn);
     const int R = T * topk;
-    auto kern = sl ? (bm == 32   ? k_grouped_q4_0<MODE_GATE_UP, 32, 5, true>
+    const int nst = q0_stages32();
+    auto kern = sl ? (bm == 32   ? (nst == 3   ? k_grouped_q4_0<MODE_GATE_UP, 32, 3, true>
+                                   : nst == 4 ? k_grouped_q4_0<MODE_GATE_UP, 32, 4, true>
+                                              : k_grouped_q4_0<MODE_GATE_UP, 32, 5, true>)
                       : bm == 64 ? k_grouped_q4_0<MODE_GATE_UP, 64, 4, true>
                                  : k_grouped_q4_0<MODE_GATE_UP, GM, 3, true>)
-                   : (bm == 32   ? k_grouped_q4_0<MODE_GATE_UP, 32, 5>
+                   : (bm == 32   ? (nst == 3   ? k_grouped_q4_0<MODE_GATE_UP, 32, 3>
+                                   : nst == 4 ? k_grouped_q4_0<MODE_GATE_UP, 32, 4>
+                                              : k_grouped_q4_0<MODE_GATE_UP, 32, 5>)
                       : bm == 64 ? k_grouped_q4_0<MODE_GATE_UP, 64, 4>
                                  : k_grouped_q4_0<MODE_GATE_UP>);
     launch(kern, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg,
@@ -1383,10 +1398,15 @@ static int grouped_down(const char *fn, bool sl, const void *h, int R, const uin
     // R is not passed: offsets[E] <= max_tiles * bm rows of h can be read
     LMOE_REQUIRE((long long)max_tiles * bm * I * 2 <= 0xFFFFFFFFll && (long long)H * (I / 64) * 36 <= 0xFFFFFFFFll,
                  LMOE_ESHAPE, "%s: h or one expert's weights exceed 4 GiB", fn);
-    auto kern = sl ? (bm == 32   ? k_grouped_q4_0<MODE_DOWN, 32, 5, true>
+    const int nst = q0_stages32();
+    auto kern = sl ? (bm == 32   ? (nst == 3   ? k_grouped_q4_0<MODE_DOWN, 32, 3, true>
+                                   : nst == 4 ? k_grouped_q4_0<MODE_DOWN, 32, 4, true>
+                                              : k_grouped_q4_0<MODE_DOWN, 32, 5, true>)
                       : bm == 64 ? k_grouped_q4_0<MODE_DOWN, 64, 4, true>
                                  : k_grouped_q4_0<MODE_DOWN, GM, 3, true>)
-                   : (bm == 32   ? k_grouped_q4_0<MODE_DOWN, 32, 5>
+                   : (bm == 32   ? (nst == 3   ? k_grouped_q4_0<MODE_DOWN, 32, 3>
+                                   : nst == 4 ? k_grouped_q4_0<MODE_DOWN, 32, 4>
+                                              : k_grouped_q4_0<MODE_DOWN, 32, 5>)
                       : bm == 64 ? k_grouped_q4_0<MODE_DOWN, 64, 4>
                                  : k_grouped_q4_0<MODE_DOWN>);
     launch(kern, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets,
