@@ -295,21 +295,26 @@ __device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm
       if (lane + 64 * j < E) s += __expf(v[j] - m);
     s = wave_sum(s);
   }
-  // 1. the k-th largest key
+  // 1. the k-th largest key, or a threshold with the same picks: bit b stays set while at least k keys are at or
+  // above the prefix; once exactly k are, no lower bit changes which keys those are (every later threshold lies
+  // between the prefix and the k-th key), so the search stops there. Ties at the k-th key run all 32 steps.
   uint32_t thr = 0;
   for (int b = 31; b >= 0; --b) {
     const uint32_t cand = thr | (1u << b);
     int cnt = 0;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) cnt += __popcll(__ballot(key[j] >= cand));
-    thr = cnt >= k ? cand : thr;
+    if (cnt >= k) {  // cnt is wavefront-uniform: a scalar branch
+      thr = cand;
+      if (cnt == k) break;
+    }
   }
   // 2. the picks, compacted in index order (expert lane + 64 j: j major, then lane)
   const uint64_t below = (uint64_t(1) << lane) - 1;
   int n_gt = 0;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) n_gt += __popcll(__ballot(key[j] > thr));
-  const int need = k - n_gt;  // >= 1 ties at thr are picked, lowest index first
+  const int need = k - n_gt;  // ties at thr picked, lowest index first (none when the search stopped early)
   int eq_before = 0, sel_before = 0;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {

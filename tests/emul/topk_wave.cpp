@@ -1,11 +1,12 @@
 // Host emulation of the wavefront top-k (larder_amd/csrc/lmoe_common.h, topk_wave): 64 lanes as loops, a ballot
 // as a 64-bit mask, the LDS pick area as an array of 64 words. Two threshold searches: the kernel's, one bit a
-// step (32 steps), and a two-bits-a-step form (16 steps, three candidates a step). Used by
+// step (up to 32 steps, stopping once exactly k keys are at or above the prefix), and a two-bits-a-step form (16
+// steps, three candidates a step). Used by
 // tests/test_topk_emulation.py to check, on the CPU, that both give the oracle's picks on tie-heavy rows and that
 // the compaction never writes more than k picks.
 //
 // stdin: "rows E k" then rows lines of E float32 bit patterns (hex); stdout per row: "ok|BAD n_picks ids..." for
-// each search. argv[1]: a slip planted in the two-bit search (0: none).
+// each search. argv[1]: a slip planted in a search (0: none; 1-3 the two-bit one, 4 the one-bit one).
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -21,14 +22,21 @@ static uint32_t logit_key(float f) {
 
 static int popc(uint64_t m) { return __builtin_popcountll(m); }
 
-// the k-th largest key: bit b stays set when at least k keys are >= the prefix
+static int g_slip = 0;
+
+// the k-th largest key: bit b stays set when at least k keys are >= the prefix; the search stops at a prefix with
+// exactly k keys at or above it (the same picks). slip 4 (planted on the CPU only): it stops at the first prefix with
+// at least k, a threshold too low whenever more than k keys are above it
 static uint32_t thr_one_bit(const std::vector<uint32_t> &key, int k) {
   uint32_t thr = 0;
   for (int b = 31; b >= 0; --b) {
     const uint32_t cand = thr | (1u << b);
     int cnt = 0;
     for (uint32_t v : key) cnt += v >= cand;
-    thr = cnt >= k ? cand : thr;
+    if (cnt >= k) {
+      thr = cand;
+      if (cnt == k || g_slip == 4) break;
+    }
   }
   return thr;
 }
@@ -37,7 +45,6 @@ static uint32_t thr_one_bit(const std::vector<uint32_t> &key, int k) {
 // slip (planted on the CPU only, to show the check has teeth): 1 = a candidate kept when more than k keys are above
 // it (> for >=); 2 = the candidates tried low to high, the first with enough keys kept; 3 = the loop stopping one
 // step early (b > 1), so the threshold's two lowest bits stay clear
-static int g_slip = 0;
 static uint32_t thr_two_bit(const std::vector<uint32_t> &key, int k) {
   uint32_t thr = 0;
   for (int b = 31; g_slip == 3 ? b > 1 : b >= 1; b -= 2) {

@@ -1,6 +1,6 @@
 """The wavefront top-k's algorithm (larder_amd/csrc/lmoe_common.h, topk_wave) emulated on the CPU
-(tests/emul/topk_wave.cpp: 64 lanes as loops, ballots as masks): its one-bit threshold search and a two-bits-a-step
-form both give the oracle's picks (lowest index first among equal logits) on the tie-heavy rows the GPU tests use
+(tests/emul/topk_wave.cpp: 64 lanes as loops, ballots as masks): its one-bit threshold search (which stops once
+exactly k keys are at or above the prefix) and a two-bits-a-step form both give the oracle's picks (lowest index first among equal logits) on the tie-heavy rows the GPU tests use
 (test_gpu_decode.tie_logits), in float32, float16 and bfloat16, and the compaction writes exactly k picks, so it
 never reaches past the 32-pick LDS area. This is the CPU check a faster top-k must pass before it runs on a GPU."""
 import shutil
@@ -84,4 +84,18 @@ def test_emulation_catches_planted_slips(emul, slip):
                 f = forms[1]
                 wrong += f[0] != "ok" or [int(v) for v in f[2:]] != [int(v) for v in want[r]]
                 over += int(f[1]) > k
+    assert wrong > 0 and over > 0
+
+
+def test_emulation_catches_an_early_stop_slip(emul):
+    """The one-bit search stops only at a prefix with exactly k keys at or above it. Stopping at the first prefix
+    with at least k (slip 4, planted on the CPU) keeps a threshold too low: more than k picks and wrong ids."""
+    wrong = over = 0
+    for E, k in [(128, 8), (512, 10)]:
+        lg = rows_for(E, k, torch.float32)
+        want, _ = moe.router(lg, k, False)
+        for r, forms in enumerate(run_emul(emul, lg, k, 4)):
+            f = forms[0]
+            wrong += f[0] != "ok" or [int(v) for v in f[2:]] != [int(v) for v in want[r]]
+            over += int(f[1]) > k
     assert wrong > 0 and over > 0
