@@ -416,10 +416,11 @@ __global__ void __launch_bounds__(64 * NW)
         ids_out[s] = id;
         scores_out[s] = sc;
       }
-    } else {
-      topk_wave<N, false>(v, n_experts, topk, norm, scr, &id, nullptr);
+      id = uint32_t(__builtin_amdgcn_readlane(int(id), j));
+    } else {  // only the slot's own pick
+      topk_wave<N, false>(v, n_experts, topk, norm, scr, &id, nullptr, j);
     }
-    e = uint32_t(__builtin_amdgcn_readlane(int(id), j));
+    e = id;
   }
   // no such expert: zero rows (cpu_kern.cpp:316-318); the folded shared expert is expert n_experts
   const bool valid = e < uint32_t(n_experts) || shared_slot;

@@ -275,9 +275,11 @@ __device__ __forceinline__ float key_logit(uint32_t key) {
 //   2. the picks are the keys above thr, then the lowest-index keys equal to thr up to k, compacted into LDS in
 //      index order (a count other than k, impossible with the right threshold, sets every id to 0xFFFFFFFF);
 //   3. each pick's rank is the number of picks ahead of it, then a lane permute puts rank r in lane r.
+// SCORES false: only the pick of rank `want` (wavefront-uniform) is wanted; *id_out is that id in every lane, found
+// by a ballot over the ranks instead of the permute to rank order.
 template <int NPL, bool SCORES = true>
 __device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm, uint32_t *lds, uint32_t *id_out,
-                                          float *score_out) {
+                                          float *score_out, int want = 0) {
   const int lane = threadIdx.x & 63;
   uint32_t key[NPL];
   float m = -INFINITY;
@@ -352,11 +354,16 @@ __device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm
         rank += (o + q < k && (ko[q] > my_key || (ko[q] == my_key && io[q] < my_idx))) ? 1 : 0;
     }
   }
+  if (!SCORES) {  // the lane holding rank `want` (one of the first k: ranks are distinct)
+    const uint64_t hit = __ballot(lane < k && rank == want);
+    const uint32_t id = uint32_t(__builtin_amdgcn_readlane(int(my_idx), hit ? __builtin_ctzll(hit) : 0));
+    *id_out = bad || !hit ? 0xFFFFFFFFu : id;
+    return;
+  }
   __builtin_amdgcn_wave_barrier();
   const int dst = (rank & 63) * 4;
   const uint32_t id = uint32_t(__builtin_amdgcn_ds_permute(dst, int(my_idx)));
   *id_out = bad ? 0xFFFFFFFFu : id;
-  if (!SCORES) return;
   const uint32_t kr = uint32_t(__builtin_amdgcn_ds_permute(dst, int(my_key)));
   float mine = lane < k ? __expf(key_logit(kr) - m) / s : 0.0f;
   if (norm) {
