@@ -149,10 +149,10 @@ def grouped_leg():
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) / n * 1e3
     flops = workloads.expert_flops(cfg, T * cfg["k"])
-    # per-kernel, kernel-exact, over 5 more passes (8 launches a pass, in launch order: x to f16 in the K order,
-    # top-k, 3 grouping, gate/up, down, combine)
-    names = ["k_to_f16", "k_router_topk", "k_group_count", "k_group_scan", "k_group_scatter", "k_grouped<gate_up>",
-             "k_grouped<down>", "k_combine_sorted"]
+    # per-kernel, kernel-exact, over 5 more passes (7 launches a pass, in launch order: top-k and x to f16 in the K
+    # order in one launch, 3 grouping, gate/up, down, combine; 8 with LMOE_FUSED_TOPK=0: the first two apart)
+    names = (["k_to_f16", "k_router_topk"] if os.environ.get("LMOE_FUSED_TOPK", "1") == "0" else ["k_topk_and_f16"]) + \
+        ["k_group_count", "k_group_scan", "k_group_scatter", "k_grouped<gate_up>", "k_grouped<down>", "k_combine_sorted"]
     M = 5 * len(names)
     _lib.call("lmoe_profile_arm", M)
     for _ in range(5):

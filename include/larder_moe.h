@@ -51,6 +51,13 @@ int lmoe_profile_read(float *ms, int cap, int *count);
 int lmoe_router_topk(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids, float *scores,
                      void *stream);
 
+/* lmoe_router_topk and lmoe_to_gemm_f16 in ONE launch (no counterpart in the reference; the prefill chain's two steps
+ * before the grouping when the logits are given, stream_fast.py:4352-4370 / gguf_experts.py:698-722): ids / scores
+ * [T][k] from logits [T][E] as lmoe_router_topk gives them, and x [n] (n % 32 == 0, 16-byte aligned) to xh [n] in f16
+ * in the grouped GEMMs' K order as lmoe_to_gemm_f16 gives it, bit for bit. One kernel boundary fewer. */
+int lmoe_topk_and_gemm_f16(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids,
+                           float *scores, const void *x, int xdtype, long long n, void *xh, void *stream);
+
 /* lmoe_router_topk on fp32 logits [T][E] with a folded shared expert's m slices appended to every token (no
  * counterpart in the reference; the prefill form of lmoe_moe_gate_up_ext's slots): ids / scores [T][k + m], slot
  * k + j = (E + j, sigmoid(gate[t])), gate [T] the shared expert's gate logits (lmoe_router_gemm's gate output). The

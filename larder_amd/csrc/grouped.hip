@@ -37,7 +37,6 @@ using IC = std::integral_constant<int, N>;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int GM = 128;  // rows a tile (the grouping kernel's bm)
 constexpr int GN = 256;  // weight rows a tile (gate/up: 128 gate + 128 up features; down: 256 outputs)
@@ -50,12 +49,6 @@ enum { MODE_GATE_UP = 0, MODE_DOWN = 1 };
 // 16-byte chunk c (0..7) of A row r in a stage: rows are 128 bytes, chunks XOR-swizzled by the row's low 3 bits
 __device__ __forceinline__ int achunk(int r, int c) { return r * 8 + (c ^ (r & 7)); }
 
-// Position of natural element n (a multiple of 4) of a row in the GEMMs' K order: within each 32-wide block,
-// group n4 = (n % 32) / 4 sits at 8 n4 (n4 < 4) or 8 (n4 - 4) + 4
-__device__ __forceinline__ int kperm4(int n) {
-  const int n4 = (n & 31) >> 2;
-  return (n & ~31) | (n4 < 4 ? 8 * n4 : 8 * (n4 - 4) + 4);
-}
 
 // two f16 (1024 + q) from a byte-wise masked word: {q0, q1} or {q2, q3}
 __device__ __forceinline__ uint32_t magic_pair(uint32_t nib, uint32_t sel) {
@@ -1052,22 +1045,16 @@ k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const
 // kperm: element i lands at its position in the grouped GEMMs' K order (n % 32 == 0, vector path only).
 __global__ void __launch_bounds__(256) k_to_f16(const void *x, int dt, long long n, _Float16 *out, int vec,
                                                 int kperm) {
+  if (vec && kperm) {
+    to_f16_kperm(blockIdx.x, x, dt, n, out);
+    return;
+  }
   const long long i0 = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 8;
   if (i0 >= n) return;
   if (vec) {
     float v[8];
     load8(x, size_t(i0), dt, v);
-    if (kperm) {
-      const long long b = i0 & ~31ll;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const h2_t p0 = {_Float16(v[4 * h]), _Float16(v[4 * h + 1])}, p1 = {_Float16(v[4 * h + 2]), _Float16(v[4 * h + 3])};
-        *reinterpret_cast<u32x2 *>(out + b + kperm4(int(i0 & 31) + 4 * h)) =
-            u32x2{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1)};
-      }
-    } else {
-      store8(out, size_t(i0), LMOE_F16, v);
-    }
+    store8(out, size_t(i0), LMOE_F16, v);
     return;
   }
   const int cnt = int(min(8ll, n - i0));

@@ -30,6 +30,7 @@ namespace lmoe {
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // The value unchanged, opaque to the optimiser: per-thread arithmetic on it is redone in each iteration of an outer
 // loop (a layer, a tile) instead of being hoisted out of the loop and kept live, in registers, for the whole kernel
@@ -544,6 +545,29 @@ __device__ __forceinline__ float round_elt(float v, int dt) {
   if (dt == LMOE_F32) return v;
   if (dt == LMOE_F16) return float(_Float16(v));
   return bf16_to_f32(f32_to_bf16(v));
+}
+
+// Position of natural element n (a multiple of 4) of a row in the GEMMs' K order: within each 32-wide block,
+// group n4 = (n % 32) / 4 sits at 8 n4 (n4 < 4) or 8 (n4 - 4) + 4
+__device__ __forceinline__ int kperm4(int n) {
+  const int n4 = (n & 31) >> 2;
+  return (n & ~31) | (n4 < 4 ? 8 * n4 : 8 * (n4 - 4) + 4);
+}
+
+// Elements [2048 block, +2048) of x (n of them, dtype dt, n % 32 == 0, 16-byte aligned) to f16 in the K order: 8 a
+// thread, one 16-byte load and two 8-byte stores (a 4-element group keeps its neighbours within the 32-block).
+__device__ __forceinline__ void to_f16_kperm(int block, const void *x, int dt, long long n, _Float16 *out) {
+  const long long i0 = (static_cast<long long>(block) * 256 + threadIdx.x) * 8;
+  if (i0 >= n) return;
+  float v[8];
+  load8(x, size_t(i0), dt, v);
+  const long long b = i0 & ~31ll;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const h2_t p0 = {_Float16(v[4 * h]), _Float16(v[4 * h + 1])}, p1 = {_Float16(v[4 * h + 2]), _Float16(v[4 * h + 3])};
+    *reinterpret_cast<u32x2 *>(out + b + kperm4(int(i0 & 31) + 4 * h)) =
+        u32x2{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1)};
+  }
 }
 
 // ---- router partials -------------------------------------------------------------------------------------------

@@ -18,16 +18,13 @@ namespace lmoe {
 
 constexpr int kMaxNpl = 16;  // logits a lane: E <= 64 * 16
 
-// Four tokens a workgroup, one wavefront each.
-// m > 0: each token's ids / scores rows hold k + m entries, the last m the folded shared expert's slices
-// (E + j, sigmoid(gate[t])).
+// Four tokens a workgroup, one wavefront each (k_router_topk's body).
 template <int NPL>
-__global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt, int ld_stride, int T, int E,
-                                                     int k, int norm, uint32_t *ids, float *scores,
-                                                     const float *gate = nullptr, int m = 0) {
+__device__ __forceinline__ void topk_rows(int block, const void *logits, int ldt, int ld_stride, int T, int E,
+                                          int k, int norm, uint32_t *ids, float *scores, const float *gate, int m) {
   __shared__ __attribute__((aligned(16))) uint32_t scr[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + wave;
+  const int t = block * 4 + wave;
   if (t >= T) return;
   const size_t base = size_t(t) * ld_stride;
   float v[NPL];
@@ -47,6 +44,29 @@ __global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt
     ids[size_t(t) * ks + lane] = uint32_t(E + lane - k);
     scores[size_t(t) * ks + lane] = sigmoidf_(gate[t]);
   }
+}
+
+// Four tokens a workgroup, one wavefront each.
+// m > 0: each token's ids / scores rows hold k + m entries, the last m the folded shared expert's slices
+// (E + j, sigmoid(gate[t])).
+template <int NPL>
+__global__ void __launch_bounds__(256) k_router_topk(const void *logits, int ldt, int ld_stride, int T, int E,
+                                                     int k, int norm, uint32_t *ids, float *scores,
+                                                     const float *gate = nullptr, int m = 0) {
+  topk_rows<NPL>(blockIdx.x, logits, ldt, ld_stride, T, E, k, norm, ids, scores, gate, m);
+}
+
+// The prefill's top-k and x's conversion to f16 in the GEMM K order (the two steps before the grouping that do not
+// depend on each other, when the logits are given) as one launch: workgroups [0, nb_topk) rank four tokens each,
+// the rest convert 2,048 elements each. One kernel boundary fewer, and the two overlap on the chip.
+template <int NPL>
+__global__ void __launch_bounds__(256) k_topk_and_f16(const void *logits, int ldt, int T, int E, int k, int norm,
+                                                      uint32_t *ids, float *scores, int nb_topk, const void *x,
+                                                      int xdt, long long n, _Float16 *xh) {
+  if (int(blockIdx.x) < nb_topk)
+    topk_rows<NPL>(blockIdx.x, logits, ldt, E, T, E, k, norm, ids, scores, nullptr, 0);
+  else
+    to_f16_kperm(blockIdx.x - nb_topk, x, xdt, n, xh);
 }
 
 constexpr int kRouterMaxT = 16;
@@ -636,6 +656,39 @@ static int topk_launch(const void *logits, int ldtype, int stride, int T, int E,
 extern "C" int lmoe_router_topk(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids,
                                 float *scores, void *stream) {
   return topk_launch(logits, ldtype, E, T, E, k, norm, ids, scores, (hipStream_t)stream, "lmoe_router_topk");
+}
+
+extern "C" int lmoe_topk_and_gemm_f16(const void *logits, int ldtype, int T, int E, int k, int norm, uint32_t *ids,
+                                      float *scores, const void *x, int xdtype, long long n, void *xh, void *stream) {
+  const char *fn = "lmoe_topk_and_gemm_f16";
+  LMOE_REQUIRE(dtype_ok(ldtype) && dtype_ok(xdtype), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(T >= 0 && E > 0 && E <= 64 * kMaxNpl, LMOE_ESHAPE, "%s: %d experts is outside 1..%d", fn, E,
+               64 * kMaxNpl);
+  LMOE_REQUIRE(k > 0 && k <= E && k <= 32, LMOE_ESHAPE, "%s: top-k %d is outside 1..min(E, 32)", fn, k);
+  LMOE_REQUIRE(n >= 0 && n % 32 == 0, LMOE_ESHAPE, "%s: length %lld is not a multiple of 32", fn, n);
+  LMOE_REQUIRE(T == 0 || (logits && ids && scores), LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(n == 0 || (x && xh && aligned16(x) && aligned16(xh)), LMOE_EALIGN,
+               "%s: x and xh must be given and 16-byte aligned", fn);
+  const long long nb_conv = (n + 2047) / 2048, nb_topk = (T + 3) / 4;
+  LMOE_REQUIRE(nb_conv + nb_topk < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, nb_conv + nb_topk);
+  if (nb_conv + nb_topk == 0) return 0;
+  const dim3 grid(unsigned(nb_conv + nb_topk)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  _Float16 *out = static_cast<_Float16 *>(xh);
+  const int nt = int(nb_topk);
+  if (E <= 64)
+    launch(k_topk_and_f16<1>, grid, block, 0, st, logits, ldtype, T, E, k, norm, ids, scores, nt, x, xdtype, n, out);
+  else if (E <= 128)
+    launch(k_topk_and_f16<2>, grid, block, 0, st, logits, ldtype, T, E, k, norm, ids, scores, nt, x, xdtype, n, out);
+  else if (E <= 256)
+    launch(k_topk_and_f16<4>, grid, block, 0, st, logits, ldtype, T, E, k, norm, ids, scores, nt, x, xdtype, n, out);
+  else if (E <= 512)
+    launch(k_topk_and_f16<8>, grid, block, 0, st, logits, ldtype, T, E, k, norm, ids, scores, nt, x, xdtype, n, out);
+  else
+    launch(k_topk_and_f16<16>, grid, block, 0, st, logits, ldtype, T, E, k, norm, ids, scores, nt, x, xdtype, n,
+           out);
+  LMOE_LAUNCHED(fn);
+  return 0;
 }
 
 extern "C" int lmoe_router_topk_shared(const float *logits, int T, int E, int k, int norm, const float *gate, int m,

@@ -127,7 +127,6 @@ __device__ __forceinline__ float block_tree(float v, float *red, int tid) {
 
 // 16 / 8 bytes from global memory with the nontemporal hint; the address-space cast keeps the compiler from
 // falling back to flat loads for pointers picked from tables
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u32x4 ldg_nt4(const void *p) {
   return __builtin_nontemporal_load(
       (const __attribute__((address_space(1))) u32x4 *)(reinterpret_cast<uintptr_t>(p)));

@@ -13,6 +13,7 @@ chunks. Here every step stays on the device with no host round trip:
 whole layer over T tokens from router logits.
 """
 import ctypes
+import os
 
 import torch
 
@@ -271,7 +272,11 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
     T, H = x.shape
     st = stream()
     x = x.contiguous()
-    call("lmoe_to_gemm_f16", ptr(x), dcode(x.dtype), x.numel(), ptr(B.xh), st)
+    # with the logits given and no shared expert, the top-k and x's conversion go out as one launch
+    # (LMOE_FUSED_TOPK=0: two)
+    fused = logits is not None and L.shared is None and os.environ.get("LMOE_FUSED_TOPK", "1") != "0"
+    if not fused:
+        call("lmoe_to_gemm_f16", ptr(x), dcode(x.dtype), x.numel(), ptr(B.xh), st)
     if logits is None:
         if L.wr is None:
             raise ValueError("this layer has no router weight: pass logits")
@@ -315,7 +320,12 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
             down(B.hs, B.Gs, sd, L.types[2], B.ys, sl=ss[2] if s_ok(L.types[2]) else None)
             B.shared_done.record(B.side)
         shared, gate = ptr(B.ys), ptr(B.gate)
-    call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids_ext), ptr(B.scores_ext), st)
+    if fused:
+        call("lmoe_topk_and_gemm_f16", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids_ext), ptr(B.scores_ext),
+             ptr(x), dcode(x.dtype), x.numel(), ptr(B.xh), st)
+    else:
+        call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids_ext), ptr(B.scores_ext),
+             st)
     B.G.run(B.ids_ext.reshape(-1))
     f16, sl = L.prefill_f16, L.stream_w or (None, None, None)
     sl_ok = lambda t: t == "Q4_0" or B.G.bm == 64  # noqa: E731  (stream-layout Q4_K: the 64-row kernel)

@@ -112,6 +112,13 @@ def test_refusals_without_a_gpu(built_lib):
     assert rc == _lib.ESHAPE and b"64-row" in L.lmoe_error()
     rc = L.lmoe_grouped_down_sl(p, 64, p, p, p, 4, 32, 1, None, p, _lib.Q4_K, 8, 512, 1024, p, _lib.F16, None)
     assert rc == _lib.ESHAPE and b"64-row" in L.lmoe_error()
+    # the top-k and the K-order conversion in one launch: the top-k's limits and the conversion's
+    rc = L.lmoe_topk_and_gemm_f16(p, _lib.F32, 4, 2000, 8, 1, p, p, p, _lib.F16, 4096, p, None)
+    assert rc == _lib.ESHAPE and b"experts" in L.lmoe_error()
+    rc = L.lmoe_topk_and_gemm_f16(p, _lib.F32, 4, 128, 8, 1, p, p, p, _lib.F16, 4016, p, None)
+    assert rc == _lib.ESHAPE and b"multiple of 32" in L.lmoe_error()
+    rc = L.lmoe_topk_and_gemm_f16(p, _lib.F32, 4, 128, 8, 1, p, p, ctypes.c_void_p(18), _lib.F16, 4096, p, None)
+    assert rc == _lib.EALIGN
     # router partials: hidden 2048 (one item a router thread), at most 256 router rows, the row-pair down kernel
     rc = L.lmoe_router_part(p, _lib.F16, p, None, _lib.F16, 1, 4096, 128, p, None)
     assert rc == _lib.ESHAPE and b"one 8-element item" in L.lmoe_error()

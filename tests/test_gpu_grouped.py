@@ -144,6 +144,32 @@ def test_to_gemm_f16_k_order(xdt):
     assert torch.equal(got[:, grouped.kperm_index(160)], x.half())
 
 
+@pytest.mark.parametrize("T,E,k,xdt", [(1, 60, 4, torch.bfloat16), (37, 128, 8, torch.float16),
+                                        (513, 512, 10, torch.float32), (2048, 128, 8, torch.bfloat16)])
+def test_topk_and_gemm_f16_equals_the_two_launches(T, E, k, xdt):
+    """lmoe_topk_and_gemm_f16 against lmoe_router_topk + lmoe_to_gemm_f16: ids, scores and xh bit for bit (with tied
+    rows), and the ids are the oracle's."""
+    from larder_amd import _lib
+    g = torch.Generator(device="cuda").manual_seed(T + E)
+    lg = torch.randn((T, E), generator=g, device="cuda")
+    lg[::3, : E // 2] = lg[::3, :1]                      # ties on every third row
+    H = 2048
+    x = torch.randn((T, H), generator=g, device="cuda").to(xdt)
+    i32, f32 = dict(dtype=torch.int32, device="cuda"), dict(dtype=torch.float32, device="cuda")
+    ids_a, sc_a, ids_b, sc_b = torch.empty((T, k), **i32), torch.empty((T, k), **f32), torch.empty((T, k), **i32), \
+        torch.empty((T, k), **f32)
+    xa, xb = (torch.empty((T, H), dtype=torch.float16, device="cuda") for _ in range(2))
+    st = _lib.stream()
+    _lib.call("lmoe_router_topk", _lib.ptr(lg), _lib.F32, T, E, k, 1, _lib.ptr(ids_a), _lib.ptr(sc_a), st)
+    _lib.call("lmoe_to_gemm_f16", _lib.ptr(x), _lib.dcode(xdt), x.numel(), _lib.ptr(xa), st)
+    _lib.call("lmoe_topk_and_gemm_f16", _lib.ptr(lg), _lib.F32, T, E, k, 1, _lib.ptr(ids_b), _lib.ptr(sc_b),
+              _lib.ptr(x), _lib.dcode(xdt), x.numel(), _lib.ptr(xb), st)
+    torch.cuda.synchronize()
+    assert torch.equal(ids_a, ids_b) and torch.equal(sc_a.view(torch.int32), sc_b.view(torch.int32))
+    assert torch.equal(xa.view(torch.int16), xb.view(torch.int16))
+    assert np.array_equal(host(ids_b).astype(np.uint32), moe.topk_ids(host(lg), k))
+
+
 @pytest.mark.parametrize("types,H,I,E", MIXES[:2])
 def test_gate_up_h_matches_oracle(types, H, I, E):
     """h in grouped order against the oracle's h, element by element (f16 output rounding plus f16 weights)."""
