@@ -12,6 +12,7 @@
 //      by comparing against the chunk's keys in LDS), so rows keep flat order within an expert. Workgroup 0 also
 //      writes counts, offsets and the grouped GEMM's work list.
 // Bucket E collects ids >= E, which therefore sort after every expert.
+#include <cstdlib>
 #include <mutex>
 
 #include "lmoe_common.h"
@@ -143,6 +144,91 @@ __global__ void __launch_bounds__(256)
   inv[r] = pos;
 }
 
+// ---- the same sort for R <= 1024 rows in one workgroup -----------------------------------------------------------
+//
+// One row a thread, 16 wavefronts: the histogram and its exclusive scan in LDS; each row's rank among the earlier
+// rows of its bucket is its rank inside its wavefront (a ballot for each distinct key of the wavefront, lowest lane
+// first) plus the rows of that bucket in the earlier wavefronts (per-wavefront bucket counts in LDS, 16 x 1025
+// bytes). The same positions as the three kernels (a stable sort), in one launch and with no serial loop over rows.
+constexpr int kGroupSmallR = 1024;
+
+__global__ void __launch_bounds__(1024)
+    k_group_small(const uint32_t *ids, int R, int E, int bm, uint32_t *counts, uint32_t *offsets, uint32_t *order,
+                  uint32_t *inv, uint32_t *tiles, uint32_t *n_tiles) {
+  __shared__ uint32_t cnt[kGroupMaxE + 1];  // bucket counts, then their exclusive prefix
+  __shared__ uint8_t wc[16][kGroupMaxE + 4];  // rows of bucket e in wavefront w (<= 64)
+  __shared__ uint32_t wsum[16], wsum2[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e <= E; e += 1024) cnt[e] = 0;
+  for (int i = tid; i < 16 * (kGroupMaxE + 4) / 4; i += 1024) reinterpret_cast<uint32_t *>(wc)[i] = 0;
+  __syncthreads();
+  const bool act = tid < R;
+  uint32_t key = uint32_t(E);
+  if (act) {
+    const uint32_t v = ids[tid];
+    key = v < uint32_t(E) ? v : uint32_t(E);
+    atomicAdd(&cnt[key], 1u);
+  }
+  // rank inside the wavefront and the wavefront's count of each key: one ballot a distinct key
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  uint32_t wrank = 0;
+  uint64_t rem = __ballot(act);
+  while (rem) {
+    const uint32_t lk = uint32_t(__builtin_amdgcn_readlane(int(key), __builtin_ctzll(rem)));
+    const uint64_t m = __ballot(act && key == lk);
+    if (act && key == lk) {
+      wrank = uint32_t(__popcll(m & below));
+      if (wrank == 0) wc[wave][lk] = uint8_t(__popcll(m));
+    }
+    rem &= ~m;
+  }
+  __syncthreads();
+  // exclusive scan of the bucket counts: bucket tid (bucket 1024, when E == 1024, added after)
+  uint32_t c = tid <= E ? cnt[tid] : 0u, x = c;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wave] = x;
+  // experts' m-tiles for the work list: the same scan over ceil(count / bm)
+  const uint32_t nt = tiles && tid < E ? (c + uint32_t(bm) - 1) / uint32_t(bm) : 0u;
+  uint32_t xt = nt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(xt, o, 64);
+    if (lane >= o) xt += y;
+  }
+  if (lane == 63) wsum2[wave] = xt;
+  __syncthreads();
+  uint32_t base = 0, tbase = 0, ttot = 0;
+  for (int w = 0; w < 16; ++w) {
+    base += w < wave ? wsum[w] : 0u;
+    tbase += w < wave ? wsum2[w] : 0u;
+    ttot += wsum2[w];
+  }
+  const uint32_t off = base + x - c;  // bucket tid's first position
+  if (tid <= E) {
+    if (tid < E) counts[tid] = c;
+    offsets[tid] = off;
+  }
+  if (E == kGroupMaxE && tid == 1023) offsets[kGroupMaxE] = off + c;  // bucket 1024 starts after bucket 1023
+  if (tiles) {
+    uint32_t run = tbase + xt - nt;
+    for (uint32_t m = 0; m < nt; ++m) tiles[run + m] = (uint32_t(tid) << 20) | m;
+    if (tid == 0) *n_tiles = ttot;
+  }
+  __syncthreads();  // every thread has read cnt: it becomes the offsets
+  if (tid <= E) cnt[tid] = off;
+  if (E == kGroupMaxE && tid == 1023) cnt[kGroupMaxE] = off + c;
+  __syncthreads();
+  if (!act) return;
+  uint32_t pos = cnt[key] + wrank;
+  for (int w = 0; w < wave; ++w) pos += wc[w][key];
+  order[pos] = uint32_t(tid);
+  inv[tid] = pos;
+}
+
 }  // namespace lmoe
 
 using namespace lmoe;
@@ -154,6 +240,15 @@ extern "C" size_t lmoe_group_workspace_bytes(int R, int E) {
 
 extern "C" int lmoe_max_tiles(int R, int E, int bm) { return bm > 0 ? (R + bm - 1) / bm + E : 0; }
 
+// R <= 1024 rows go through k_group_small unless LMOE_GROUP_SMALL=0
+static bool small_grouping() {
+  static const bool on = [] {
+    const char *v = getenv("LMOE_GROUP_SMALL");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 extern "C" int lmoe_group_rows(const uint32_t *ids, int R, int E, int bm, uint32_t *counts, uint32_t *offsets,
                                uint32_t *order, uint32_t *inv, uint32_t *tiles, uint32_t *n_tiles, void *ws,
                                void *stream) {
@@ -164,6 +259,11 @@ extern "C" int lmoe_group_rows(const uint32_t *ids, int R, int E, int bm, uint32
   LMOE_REQUIRE(counts && offsets && ws, LMOE_EINVAL, "%s: null pointer", fn);
   LMOE_REQUIRE(R == 0 || (ids && order && inv), LMOE_EINVAL, "%s: null pointer", fn);
   hipStream_t st = (hipStream_t)stream;
+  if (R <= kGroupSmallR && small_grouping()) {  // one launch
+    launch(k_group_small, dim3(1), dim3(1024), 0, st, ids, R, E, bm, counts, offsets, order, inv, tiles, n_tiles);
+    LMOE_LAUNCHED(fn);
+    return 0;
+  }
   const int nchunk = R > 0 ? (R + kGroupChunk - 1) / kGroupChunk : 1;
   uint32_t *hist = static_cast<uint32_t *>(ws);
   uint32_t *totals = hist + size_t(nchunk) * (E + 1);

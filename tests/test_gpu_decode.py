@@ -282,7 +282,10 @@ def test_graph_replay_matches_eager():
 
 
 @pytest.mark.parametrize("R,E,bm", [(1, 4, 16), (8, 128, 16), (512, 128, 32), (65536, 128, 128), (5000, 60, 64),
-                                    (3000, 1024, 16)])
+                                    (3000, 1024, 16),
+                                    # one workgroup (R <= 1024): the E = 1024 edge (ids past it in bucket 1024), a
+                                    # handful of experts, one expert, and the first size past it
+                                    (1024, 1024, 16), (777, 1024, 32), (1024, 3, 128), (64, 1, 16), (1025, 60, 32)])
 def test_group_rows_bit_exact(R, E, bm):
     from larder_amd import _lib
     rng = np.random.default_rng(R + E)
