@@ -8,8 +8,9 @@
 //   2. k_group_scan: one workgroup a bucket turns its row of hist into the exclusive prefix over chunks (the
 //      bucket's rows in earlier chunks) and writes the bucket total;
 //   3. k_group_scatter: each workgroup scans the totals into bucket offsets, and every row goes to
-//      offset[bucket] + rows of its bucket in earlier chunks + rows of its bucket earlier in its own chunk (found
-//      by comparing against the chunk's keys in LDS), so rows keep flat order within an expert. Workgroup 0 also
+//      offset[bucket] + rows of its bucket in earlier chunks + rows of its bucket earlier in its own chunk (its rank
+//      inside its wavefront by ballots, plus the bucket's rows in the chunk's earlier wavefronts), so rows keep flat
+//      order within an expert. Workgroup 0 also
 //      writes counts, offsets and the grouped GEMM's work list.
 // Bucket E collects ids >= E, which therefore sort after every expert.
 #include <cstdlib>
@@ -80,9 +81,9 @@ __global__ void __launch_bounds__(256)
                     int nchunk, uint32_t *counts, uint32_t *offsets, uint32_t *order, uint32_t *inv, uint32_t *tiles,
                     uint32_t *n_tiles) {
   __shared__ uint32_t off[kGroupMaxE + 1];
-  __shared__ uint32_t keys[kGroupChunk];
+  __shared__ uint8_t wc[4][kGroupMaxE + 4];  // rows of bucket e in wavefront w of the chunk (<= 64)
   __shared__ uint32_t tmp[4];
-  const int c = blockIdx.x, tid = threadIdx.x;
+  const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // bucket offsets: exclusive scan of the totals, 4 consecutive buckets a thread (E + 1 <= 1025 < 1028)
   {
     uint32_t t[4], sum = 0;
@@ -134,11 +135,25 @@ __global__ void __launch_bounds__(256)
     const uint32_t v = ids[r];
     key = v < uint32_t(E) ? v : uint32_t(E);
   }
-  keys[tid] = act ? key : 0xFFFFFFFFu;
+  // rows of this bucket earlier in the chunk: the row's rank inside its wavefront (a ballot for each distinct key
+  // of the wavefront) plus the bucket's rows in the chunk's earlier wavefronts
+  for (int i = tid; i < 4 * (kGroupMaxE + 4) / 4; i += 256) reinterpret_cast<uint32_t *>(wc)[i] = 0;
+  __syncthreads();
+  const uint64_t below = (uint64_t(1) << lane) - 1;
+  uint32_t rank = 0;
+  uint64_t rem = __ballot(act);
+  while (rem) {
+    const uint32_t lk = uint32_t(__builtin_amdgcn_readlane(int(key), __builtin_ctzll(rem)));
+    const uint64_t m = __ballot(act && key == lk);
+    if (act && key == lk) {
+      rank = uint32_t(__popcll(m & below));
+      if (rank == 0) wc[wave][lk] = uint8_t(__popcll(m));
+    }
+    rem &= ~m;
+  }
   __syncthreads();
   if (!act) return;
-  uint32_t rank = 0;  // rows of this bucket earlier in the chunk
-  for (int j = 0; j < tid; ++j) rank += keys[j] == key ? 1u : 0u;
+  for (int w = 0; w < wave; ++w) rank += wc[w][key];
   const uint32_t pos = off[key] + hist[size_t(key) * nchunk + c] + rank;
   order[pos] = uint32_t(r);
   inv[r] = pos;
