@@ -374,6 +374,14 @@ size_t lmoe_router_gemm_workspace_bytes(int T, int H, int En);
 int lmoe_router_gemm(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws, float *logits,
                      float *gate, void *stream);
 
+/* lmoe_router_gemm, then the top-k of its logits in the same pass over them (no counterpart in the reference; the
+ * prefill router of stream_fast.py:4358-4370): ids / scores [T][k + m] as lmoe_router_topk (m == 0) or
+ * lmoe_router_topk_shared (m > 0, n_gate == 1: slot k + j = (E + j, sigmoid(gate logit))) give them on the logits
+ * lmoe_router_gemm writes, which are also written (logits, gate). With a K split, the top-k kernel adds the slices
+ * itself, in lmoe_router_gemm's order: one launch fewer. E <= 1024, k <= 32, k + m <= 64. */
+int lmoe_router_gemm_topk(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws, float *logits,
+                          float *gate, int k, int norm, int m, uint32_t *ids, float *scores, void *stream);
+
 /* Weighted combine of rows kept in grouped (expert-sorted) order:
  *   out[t][n] = sum_j scores[t][j] * y[inv[t * k + j]][n] (+ sigmoid(gate) * shared) (+ residual)
  * y [R][H] in ydtype. Replaces the unsort plus combine of stream_fast.py:5525 and 4372-4376. */

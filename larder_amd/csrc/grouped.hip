@@ -1190,6 +1190,45 @@ __global__ void __launch_bounds__(256) k_router_finish(const float *part, int ks
     gate[t] = v;
 }
 
+// The split-K finish and the top-k in one launch, four tokens a workgroup, one wavefront each: each logit is its
+// slices added in slice order from zero (k_router_finish's sums, written to logits / gate as it would), then
+// topk_wave; with m > 0 slots k .. k + m - 1 are the folded shared expert's slices (E + j, sigmoid(gate logit)), as
+// in k_router_topk.
+template <int NPL>
+__global__ void __launch_bounds__(256) k_topk_from_parts(const float *part, int ksplit, int T, int ldp, int E,
+                                                         int n_gate, int k, int norm, int m, float *logits,
+                                                         float *gate, uint32_t *ids, float *scores) {
+  __shared__ __attribute__((aligned(16))) uint32_t scr[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  float v[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int e = min(lane + 64 * j, E - 1);
+    float a = 0.0f;
+    for (int q = 0; q < ksplit; ++q) a += part[(size_t(q) * T + t) * ldp + e];
+    if (lane + 64 * j < E) logits[size_t(t) * E + e] = a;
+    v[j] = lane + 64 * j < E ? a : -INFINITY;
+  }
+  float gl = 0.0f;
+  if (n_gate) {
+    for (int q = 0; q < ksplit; ++q) gl += part[(size_t(q) * T + t) * ldp + E];
+    if (lane == 0) gate[t] = gl;
+  }
+  uint32_t id;
+  float sc;
+  topk_wave<NPL>(v, E, k, norm, scr[wave], &id, &sc);
+  const int ks = k + m;
+  if (lane < k) {
+    ids[size_t(t) * ks + lane] = id;
+    scores[size_t(t) * ks + lane] = sc;
+  } else if (lane < ks) {
+    ids[size_t(t) * ks + lane] = uint32_t(E + lane - k);
+    scores[size_t(t) * ks + lane] = sigmoidf_(gl);
+  }
+}
+
 }  // namespace lmoe
 
 using namespace lmoe;
@@ -1567,9 +1606,9 @@ extern "C" size_t lmoe_router_gemm_workspace_bytes(int T, int H, int En) {
   return size_t(s) * size_t(T) * size_t((En + kRgN - 1) / kRgN * kRgN) * sizeof(float);
 }
 
-extern "C" int lmoe_router_gemm(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws,
-                                float *logits, float *gate, void *stream) {
-  const char *fn = "lmoe_router_gemm";
+// The router GEMM's launch; with finish false and a K split, the slices stay in ws for the caller (*ks_out, *ldp_out)
+static int router_gemm(const char *fn, const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws,
+                       float *logits, float *gate, bool finish, int *ks_out, int *ldp_out, hipStream_t st) {
   LMOE_REQUIRE(T >= 0 && E > 0 && (n_gate == 0 || n_gate == 1), LMOE_ESHAPE, "%s: bad shape", fn);
   LMOE_REQUIRE(H > 0 && H % GK == 0, LMOE_ESHAPE, "%s: hidden size %d is not a multiple of %d", fn, H, GK);
   if (T == 0) return 0;
@@ -1584,14 +1623,54 @@ extern "C" int lmoe_router_gemm(const void *xh, int T, int H, const void *wk, in
                "%s: needs a 16-byte aligned workspace of lmoe_router_gemm_workspace_bytes", fn);
   const long long grid = (long long)((T + kRgM - 1) / kRgM) * n_ntile * ks;
   LMOE_REQUIRE(grid < (1ll << 31), LMOE_ESHAPE, "%s: %lld workgroups", fn, grid);
-  hipStream_t st = (hipStream_t)stream;
   launch(k_router_gemm, dim3(unsigned(grid)), dim3(kThreads), 0, st, static_cast<const _Float16 *>(xh), T,
          static_cast<const _Float16 *>(wk), En, H, n_ntile, ks, ws, ldp, logits, E, gate);
-  if (ks > 1) {
+  if (ks > 1 && finish) {
     LMOE_LAUNCHED(fn);
     launch(k_router_finish, dim3(unsigned((En + 255) / 256), unsigned(T)), dim3(256), 0, st,
            static_cast<const float *>(ws), ks, T, ldp, En, E, logits, gate);
   }
+  LMOE_LAUNCHED(fn);
+  *ks_out = ks;
+  *ldp_out = ldp;
+  return 0;
+}
+
+extern "C" int lmoe_router_gemm(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws,
+                                float *logits, float *gate, void *stream) {
+  int ks, ldp;
+  return router_gemm("lmoe_router_gemm", xh, T, H, wk, E, n_gate, ws, logits, gate, true, &ks, &ldp,
+                     (hipStream_t)stream);
+}
+
+extern "C" int lmoe_router_gemm_topk(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws,
+                                     float *logits, float *gate, int k, int norm, int m, uint32_t *ids,
+                                     float *scores, void *stream) {
+  const char *fn = "lmoe_router_gemm_topk";
+  LMOE_REQUIRE(E > 0 && E <= 1024, LMOE_ESHAPE, "%s: %d experts is outside 1..1024", fn, E);
+  LMOE_REQUIRE(k > 0 && k <= E && k <= 32 && m >= 0 && k + m <= 64, LMOE_ESHAPE,
+               "%s: top-k %d with %d shared slices is outside what the top-k takes", fn, k, m);
+  LMOE_REQUIRE(m == 0 || n_gate == 1, LMOE_EINVAL, "%s: shared slices need the gate row", fn);
+  LMOE_REQUIRE(T == 0 || (ids && scores), LMOE_EINVAL, "%s: null pointer", fn);
+  hipStream_t st = (hipStream_t)stream;
+  int ks = 1, ldp = 0;
+  if (int rc = router_gemm(fn, xh, T, H, wk, E, n_gate, ws, logits, gate, false, &ks, &ldp, st)) return rc;
+  if (T == 0) return 0;
+  if (ks == 1)  // the GEMM wrote the logits (and the gate logit) itself: the plain top-k on them
+    return m > 0 ? lmoe_router_topk_shared(logits, T, E, k, norm, gate, m, ids, scores, stream)
+                 : lmoe_router_topk(logits, LMOE_F32, T, E, k, norm, ids, scores, stream);
+  const dim3 grid((T + 3) / 4), block(256);
+  const float *pw = static_cast<const float *>(ws);
+  auto go = [&](auto npl) {
+    constexpr int N = decltype(npl)::value;
+    launch(k_topk_from_parts<N>, grid, block, 0, st, pw, ks, T, ldp, E, n_gate, k, norm, m, logits, gate, ids,
+           scores);
+  };
+  if (E <= 64) go(IC<1>{});
+  else if (E <= 128) go(IC<2>{});
+  else if (E <= 256) go(IC<4>{});
+  else if (E <= 512) go(IC<8>{});
+  else go(IC<16>{});
   LMOE_LAUNCHED(fn);
   return 0;
 }

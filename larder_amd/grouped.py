@@ -275,14 +275,22 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
     # with the logits given and no shared expert, the top-k and x's conversion go out as one launch
     # (LMOE_FUSED_TOPK=0: two)
     fused = logits is not None and L.shared is None and os.environ.get("LMOE_FUSED_TOPK", "1") != "0"
+    ranked = fused  # ids / scores already out of the launch that made them
     if not fused:
         call("lmoe_to_gemm_f16", ptr(x), dcode(x.dtype), x.numel(), ptr(B.xh), st)
     if logits is None:
         if L.wr is None:
             raise ValueError("this layer has no router weight: pass logits")
         ng = 1 if L.shared is not None else 0
-        call("lmoe_router_gemm", ptr(B.xh), T, H, ptr(L.router_gemm_weight()), L.E, ng, ptr(B.rws), ptr(B.logits),
-             ptr(B.gate) if ng else None, st)
+        # the router GEMM and the top-k (its split-K finish folded in); LMOE_FUSED_TOPK=0: apart
+        if (L.shared is None or B.fold) and os.environ.get("LMOE_FUSED_TOPK", "1") != "0":
+            call("lmoe_router_gemm_topk", ptr(B.xh), T, H, ptr(L.router_gemm_weight()), L.E, ng, ptr(B.rws),
+                 ptr(B.logits), ptr(B.gate) if ng else None, L.k, int(L.norm), L.n_shared if B.fold else 0,
+                 ptr(B.ids_ext), ptr(B.scores_ext), st)
+            ranked = True
+        else:
+            call("lmoe_router_gemm", ptr(B.xh), T, H, ptr(L.router_gemm_weight()), L.E, ng, ptr(B.rws),
+                 ptr(B.logits), ptr(B.gate) if ng else None, st)
         lg = B.logits
     else:
         if L.shared is not None:
@@ -293,8 +301,9 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
     if B.fold:  # the shared expert's slices as experts E .. E + m - 1 in the routed GEMMs: no side stream
         m = L.n_shared
         ks = L.k + m
-        call("lmoe_router_topk_shared", ptr(lg), T, L.E, L.k, int(L.norm), ptr(B.gate), m, ptr(B.ids_ext),
-             ptr(B.scores_ext), st)
+        if not ranked:
+            call("lmoe_router_topk_shared", ptr(lg), T, L.E, L.k, int(L.norm), ptr(B.gate), m, ptr(B.ids_ext),
+                 ptr(B.scores_ext), st)
         B.G.run(B.ids_ext.reshape(-1))
         fs = L.folded_stream or (None, None, None)
         sl_ok = lambda t: t == "Q4_0" or B.G.bm == 64  # noqa: E731
@@ -323,7 +332,7 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
     if fused:
         call("lmoe_topk_and_gemm_f16", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids_ext), ptr(B.scores_ext),
              ptr(x), dcode(x.dtype), x.numel(), ptr(B.xh), st)
-    else:
+    elif not ranked:
         call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids_ext), ptr(B.scores_ext),
              st)
     B.G.run(B.ids_ext.reshape(-1))

@@ -119,6 +119,11 @@ def test_refusals_without_a_gpu(built_lib):
     assert rc == _lib.ESHAPE and b"multiple of 32" in L.lmoe_error()
     rc = L.lmoe_topk_and_gemm_f16(p, _lib.F32, 4, 128, 8, 1, p, p, ctypes.c_void_p(18), _lib.F16, 4096, p, None)
     assert rc == _lib.EALIGN
+    # the prefill router GEMM with its top-k: the top-k's limits, and shared slices only with the gate row
+    rc = L.lmoe_router_gemm_topk(p, 64, 2048, p, 128, 0, p, p, None, 33, 1, 0, p, p, None)
+    assert rc == _lib.ESHAPE and b"top-k 33" in L.lmoe_error()
+    rc = L.lmoe_router_gemm_topk(p, 64, 2048, p, 128, 0, p, p, None, 8, 1, 1, p, p, None)
+    assert rc == _lib.EINVAL and b"gate row" in L.lmoe_error()
     # router partials: hidden 2048 (one item a router thread), at most 256 router rows, the row-pair down kernel
     rc = L.lmoe_router_part(p, _lib.F16, p, None, _lib.F16, 1, 4096, 128, p, None)
     assert rc == _lib.ESHAPE and b"one 8-element item" in L.lmoe_error()

@@ -144,6 +144,49 @@ def test_to_gemm_f16_k_order(xdt):
     assert torch.equal(got[:, grouped.kperm_index(160)], x.half())
 
 
+@pytest.mark.parametrize("cfgid,T,fold", [(5, 2048, True), (5, 300, True), (2, 8192, False), (2, 64, False),
+                                         (1, 5, False)])
+def test_router_gemm_topk_equals_the_two_steps(cfgid, T, fold):
+    """lmoe_router_gemm_topk against lmoe_router_gemm + lmoe_router_topk(_shared): logits, gate logit, ids and scores
+    bit for bit (split-K and not), and the ids are the oracle's top-k of those logits."""
+    from larder_amd import _lib, grouped, workloads
+    cfg = dict(workloads.CONFIGS[cfgid])
+    if not fold:
+        cfg["Is"] = 0
+    g = torch.Generator(device="cuda").manual_seed(T + cfgid)
+    L = workloads.make_layer(cfg, g)
+    x = torch.randn((T, cfg["H"]), generator=g, device="cuda").bfloat16()
+    xh = grouped.as_gemm_f16(x)
+    E, k, ng = cfg["E"], cfg["k"], 1 if fold else 0
+    m = L.n_shared if fold else 0
+    ks = k + m
+    f32, i32 = dict(dtype=torch.float32, device="cuda"), dict(dtype=torch.int32, device="cuda")
+    nws = _lib.lib().lmoe_router_gemm_workspace_bytes(T, cfg["H"], E + ng)
+    ws = torch.empty(max(nws // 4, 1), **f32)
+    out = [[torch.empty((T, E), **f32), torch.empty(T, **f32), torch.empty((T, ks), **i32), torch.empty((T, ks), **f32)]
+           for _ in range(2)]
+    w = L.router_gemm_weight()
+    st = _lib.stream()
+    lg, gt, ids, sc = out[0]
+    _lib.call("lmoe_router_gemm", _lib.ptr(xh), T, cfg["H"], _lib.ptr(w), E, ng, _lib.ptr(ws), _lib.ptr(lg),
+              _lib.ptr(gt) if ng else None, st)
+    if fold:
+        _lib.call("lmoe_router_topk_shared", _lib.ptr(lg), T, E, k, int(cfg["norm"]), _lib.ptr(gt), m, _lib.ptr(ids),
+                  _lib.ptr(sc), st)
+    else:
+        _lib.call("lmoe_router_topk", _lib.ptr(lg), _lib.F32, T, E, k, int(cfg["norm"]), _lib.ptr(ids), _lib.ptr(sc),
+                  st)
+    lg2, gt2, ids2, sc2 = out[1]
+    _lib.call("lmoe_router_gemm_topk", _lib.ptr(xh), T, cfg["H"], _lib.ptr(w), E, ng, _lib.ptr(ws), _lib.ptr(lg2),
+              _lib.ptr(gt2) if ng else None, k, int(cfg["norm"]), m, _lib.ptr(ids2), _lib.ptr(sc2), st)
+    torch.cuda.synchronize()
+    bits = lambda t: t.view(torch.int32)  # noqa: E731
+    assert torch.equal(bits(lg), bits(lg2)) and torch.equal(ids, ids2) and torch.equal(bits(sc), bits(sc2))
+    if ng:
+        assert torch.equal(bits(gt), bits(gt2))
+    assert np.array_equal(host(ids2)[:, :k].astype(np.uint32), moe.topk_ids(host(lg2), k))
+
+
 @pytest.mark.parametrize("T,E,k,xdt", [(1, 60, 4, torch.bfloat16), (37, 128, 8, torch.float16),
                                         (513, 512, 10, torch.float32), (2048, 128, 8, torch.bfloat16)])
 def test_topk_and_gemm_f16_equals_the_two_launches(T, E, k, xdt):
