@@ -1194,26 +1194,36 @@ __global__ void __launch_bounds__(256) k_router_finish(const float *part, int ks
 // slices added in slice order from zero (k_router_finish's sums, written to logits / gate as it would), then
 // topk_wave; with m > 0 slots k .. k + m - 1 are the folded shared expert's slices (E + j, sigmoid(gate logit)), as
 // in k_router_topk.
-template <int NPL>
-__global__ void __launch_bounds__(256) k_topk_from_parts(const float *part, int ksplit, int T, int ldp, int E,
-                                                         int n_gate, int k, int norm, int m, float *logits,
-                                                         float *gate, uint32_t *ids, float *scores) {
+// KS: the K split (2, 4 or 8), so that every slice's loads go out before the first add.
+template <int NPL, int KS>
+__global__ void __launch_bounds__(256) k_topk_from_parts(const float *part, int T, int ldp, int E, int n_gate, int k,
+                                                         int norm, int m, float *logits, float *gate, uint32_t *ids,
+                                                         float *scores) {
   __shared__ __attribute__((aligned(16))) uint32_t scr[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
+  float p[KS][NPL], pg[KS];
+#pragma unroll
+  for (int q = 0; q < KS; ++q) {
+    const float *row = part + (size_t(q) * T + t) * ldp;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) p[q][j] = row[min(lane + 64 * j, E - 1)];
+    pg[q] = row[n_gate ? E : 0];
+  }
   float v[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const int e = min(lane + 64 * j, E - 1);
     float a = 0.0f;
-    for (int q = 0; q < ksplit; ++q) a += part[(size_t(q) * T + t) * ldp + e];
-    if (lane + 64 * j < E) logits[size_t(t) * E + e] = a;
+#pragma unroll
+    for (int q = 0; q < KS; ++q) a += p[q][j];  // slice order, from zero: k_router_finish's sum
+    if (lane + 64 * j < E) logits[size_t(t) * E + lane + 64 * j] = a;
     v[j] = lane + 64 * j < E ? a : -INFINITY;
   }
   float gl = 0.0f;
   if (n_gate) {
-    for (int q = 0; q < ksplit; ++q) gl += part[(size_t(q) * T + t) * ldp + E];
+#pragma unroll
+    for (int q = 0; q < KS; ++q) gl += pg[q];
     if (lane == 0) gate[t] = gl;
   }
   uint32_t id;
@@ -1661,11 +1671,17 @@ extern "C" int lmoe_router_gemm_topk(const void *xh, int T, int H, const void *w
                  : lmoe_router_topk(logits, LMOE_F32, T, E, k, norm, ids, scores, stream);
   const dim3 grid((T + 3) / 4), block(256);
   const float *pw = static_cast<const float *>(ws);
-  auto go = [&](auto npl) {
-    constexpr int N = decltype(npl)::value;
-    launch(k_topk_from_parts<N>, grid, block, 0, st, pw, ks, T, ldp, E, n_gate, k, norm, m, logits, gate, ids,
+  auto by_ks = [&](auto npl, auto ksc) {
+    constexpr int N = decltype(npl)::value, K = decltype(ksc)::value;
+    launch(k_topk_from_parts<N, K>, grid, block, 0, st, pw, T, ldp, E, n_gate, k, norm, m, logits, gate, ids,
            scores);
   };
+  auto go = [&](auto npl) {
+    if (ks == 2) by_ks(npl, IC<2>{});
+    else if (ks == 4) by_ks(npl, IC<4>{});
+    else by_ks(npl, IC<8>{});
+  };
+  LMOE_REQUIRE(ks == 2 || ks == 4 || ks == 8, LMOE_ESHAPE, "%s: K split %d", fn, ks);
   if (E <= 64) go(IC<1>{});
   else if (E <= 128) go(IC<2>{});
   else if (E <= 256) go(IC<4>{});
