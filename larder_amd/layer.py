@@ -166,14 +166,91 @@ class DecodeBuffers:
             self.zero_slots = torch.zeros(T, **u32)
             self.hprep_s = torch.empty((T, L.Is // 64 * 36), **u32)
             self.shared_y = torch.empty((T, L.H), **f32)
+        # a layer off the prepared chain (a projection beyond Q4_0 / Q4_K) passes h between gate/up and down as fp32
+        self.h32 = self.h32_s = None
+        if not prepared_chain(L):
+            self.h32 = torch.empty((T * ks, L.I), **f32)
+            if L.shared is not None and L.folded is None:
+                self.h32_s = torch.empty((T, L.Is), **f32)
+
+
+def prepared_chain(layer):
+    """Whether ``layer`` decodes on the prepared chain (every projection Q4_0 / Q4_K: h passed prepared for the
+    register-resident down kernel); other layers take decode_general."""
+    return all(t in _lib.Q4_TYPES for t in layer.types)
+
+
+def decode_general(layer, x, bufs, out, residual=None, logits=None):
+    """decode() for a layer with a projection beyond Q4_0 / Q4_K, such as the 35B's Q4_K / Q4_K / Q6_K (the
+    reference runs every type through gguf_experts.gemv's chain, gguf_experts.py:600-653, with f32 h):
+      * the router GEMV ranks in its last workgroup (lmoe_router_gemv_rank: ids / scores with a folded shared
+        expert's slots, and x prepared when gate/up take the register-resident form), or lmoe_router_topk on
+        given logits;
+      * gate/up + SwiGLU into fp32 h: on the prepared rows when gate and up share one Q4 type at hidden 2048 or
+        4096 (lmoe_gemv_gate_up_prepped), else from raw x (lmoe_gemv_gate_up);
+      * [an unfolded shared expert's gate/up and down into an fp32 row;]
+      * the general down + weighted combine + shared + residual (lmoe_gemv_down_combine).
+    Four launches a layer (six with an unfolded shared expert), all preallocated, so a stack still captures as one
+    HIP graph."""
+    L, B = layer, bufs
+    T = x.shape[0]
+    st = stream()
+    tg, tu, td = (qcode(t) for t in L.types)
+    xd = dcode(x.dtype)
+    ks = L.k + L.n_shared
+    xr = L.types[0] == L.types[1] and L.types[0] in _lib.Q4_TYPES and L.H in (2048, 4096) and L.I % 2 == 0
+    if logits is None:
+        if L.wr is None:
+            raise ValueError("this layer has no router weight: pass logits")
+        if L.E > RANK_MAX_E or L.k > RANK_MAX_K:
+            raise ValueError(f"decode takes at most {RANK_MAX_E} experts and top-{RANK_MAX_K} when a projection is "
+                             f"beyond Q4_0 / Q4_K (got {L.E}, top-{L.k})")
+        call("lmoe_router_gemv_rank", ptr(x), xd, ptr(L.wr), ptr(L.wsg), dcode(L.wr.dtype), T, L.H, L.E, L.k,
+             int(L.norm), ks, ptr(B.logits), ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.xprep) if xr else None, tg,
+             ptr(B.sync), st)
+    else:
+        if L.shared is not None:
+            raise ValueError("a shared expert's gate logit comes from the router GEMV: use the router weight")
+        lg = logits.to(torch.float32).contiguous()
+        call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids_ext), ptr(B.scores_ext), st)
+        if xr:
+            call("lmoe_prep_x", ptr(x), xd, T, L.H, tg, ptr(B.xprep), st)
+    wg, wu, wd = L.folded if L.folded is not None else (L.wg, L.wu, L.wd)
+    ne = L.E + L.n_shared
+
+    def gate_up(slots, n, topk, g, u, n_exp, width, h):
+        if xr:
+            call("lmoe_gemv_gate_up_prepped", ptr(B.xprep), ptr(B.xprep), ptr(slots), n, topk, ptr(g), ptr(u), tg,
+                 tu, n_exp, L.H, width, ptr(h), None, 0, st)
+        else:
+            call("lmoe_gemv_gate_up", ptr(x), xd, ptr(slots), n, topk, ptr(g), ptr(u), tg, tu, n_exp, L.H, width,
+                 ptr(h), st)
+
+    gate_up(B.ids_ext, T * ks, ks, wg, wu, ne, L.I, B.h32)
+    shared_y = gptr = None
+    gate_stride = 0
+    if L.shared is not None and L.folded is None:
+        sg, su, sd = L.shared
+        gate_up(B.zero_slots, T, 1, sg, su, 1, L.Is, B.h32_s)
+        call("lmoe_gemv_down_combine", ptr(B.h32_s), ptr(B.zero_slots), None, T, 1, ptr(sd), td, 1, L.Is, L.H, None,
+             None, 0, None, 0, ptr(B.shared_y), _lib.F32, st)
+        shared_y = B.shared_y
+        gptr, gate_stride = _ptr_offset(B.logits, L.E), L.E + 1
+    call("lmoe_gemv_down_combine", ptr(B.h32), ptr(B.ids_ext), ptr(B.scores_ext), T, ks, ptr(wd), td, ne, L.I, L.H,
+         ptr(shared_y), gptr, gate_stride, ptr(residual), dcode(residual.dtype) if residual is not None else 0,
+         ptr(out), dcode(out.dtype), st)
+    return out
 
 
 def decode(layer, x, bufs, out, residual=None, logits=None):
     """out [T, H] = layer(x) (+ residual) for x [T, H] (float16 / bfloat16 / float32) through the decode chain:
     router GEMV (+ x prepared for the experts) and top-k, gate/up + SwiGLU (writing h prepared for down),
     [the shared expert's gate/up and down], then down + weighted combine + shared + residual. ``logits`` [T, E]
-    replaces the router GEMV when the layer has no router weight."""
+    replaces the router GEMV when the layer has no router weight. A layer with a projection beyond Q4_0 / Q4_K
+    goes through decode_general."""
     L, B = layer, bufs
+    if not prepared_chain(L):
+        return decode_general(L, x, B, out, residual, logits)
     T = x.shape[0]
     st = stream()
     tg, tu, td = (qcode(t) for t in L.types)
