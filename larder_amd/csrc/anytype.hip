@@ -43,6 +43,22 @@ __device__ __forceinline__ uint32_t ld32h(const uint8_t *p) { return ld16(p) | (
 __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 __device__ __forceinline__ float f16at(const uint8_t *p) { return float(__builtin_bit_cast(_Float16, uint16_t(ld16(p)))); }
 
+// 32 bytes at a 2-byte aligned address as 8 dwords: the 9 dwords from the 4-byte aligned address at or below it
+// (two 16-byte loads, which need only dword alignment, and a dword), realigned by the address's low 2 bits. The
+// window reaches 2 bytes below p when p is 2 mod 4 (never the start of an allocation) and up to p + 36: callers keep
+// p + 36 inside the block.
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ void load_window8(const uint8_t *p, uint32_t (&o)[8]) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t *base = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+  const u32x4a4 v0 = *reinterpret_cast<const u32x4a4 *>(base), v1 = *reinterpret_cast<const u32x4a4 *>(base + 4);
+  const uint32_t v8 = base[8];
+  const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v8};
+  const uint32_t sh = uint32_t(a & 3);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+}
+
 // The 32 weights of chunk c (weights 32 c .. 32 c + 31) of a row of type T, in natural order.
 template <int T>
 __device__ __forceinline__ void decode32(const uint8_t *row, int c, float *w) {
@@ -97,15 +113,19 @@ __device__ __forceinline__ void decode32(const uint8_t *row, int c, float *w) {
   } else {  // Q6_K: chunk j = 4 h + g of the super-block
     const uint8_t *b = row + size_t(c >> 3) * 210;
     const int j = c & 7, h = j >> 2, g = j & 3;
+    // the super-block is 2-byte aligned: its 32 ql and 32 qh bytes come as 9-dword windows from the 4-byte
+    // aligned address below them (two 16-byte loads and one dword each, instead of 16 halfword pairs; the windows
+    // end by byte 196 of the 210) and are realigned by the 0 or 2 byte offset
+    uint32_t lq[8], hq[8];
+    load_window8(b + 64 * h + 32 * (g & 1), lq);
+    load_window8(b + 128 + 32 * h, hq);
     const float d = f16at(b + 208);
     const uint32_t scw = ld16(b + 192 + 8 * h + 2 * g);
     const float ds0 = d * float(int(int8_t(uint8_t(scw)))), ds1 = d * float(int(int8_t(uint8_t(scw >> 8))));
-    const uint8_t *ql = b + 64 * h + 32 * (g & 1);
-    const uint8_t *qh = b + 128 + 32 * h;
     const int sl = 4 * (g >> 1), shh = 2 * g;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t lw = ld32h(ql + 4 * i), hw = ld32h(qh + 4 * i);
+      const uint32_t lw = lq[i], hw = hq[i];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int v = int(((lw >> (8 * k + sl)) & 15u) | (((hw >> (8 * k + shh)) & 3u) << 4)) - 32;
@@ -207,17 +227,46 @@ __global__ void __launch_bounds__(256) k_gate_up_any(const void *x, int xdt, con
 
 // One token's weighted sum over its k experts of rows o0, o0 + 1 of down (type T), every expert's loads issued
 // before the sums: acc[rr] = sum_j s_j (h_j . wd[e_j][o0 + rr]) as this lane's part.
+// The token's k experts x I / 32 chunks are one list of (expert j, chunk c) items, item u = j (I / 32) + c; lane
+// takes u = lane, lane + 64, ... two a pass, so that at decode width (k 8, I 768: 192 items) every lane has work and
+// both items' loads are out before either's arithmetic (a loop over the experts kept 40 of 64 lanes idle at I 768
+// and paid one memory round trip an expert). A lane's clamped repeat of the last item takes weight 0.
 template <int T>
 __device__ __forceinline__ void down_rows(const uint8_t *wd, size_t rb, int H, int I, int k, int n_experts,
                                           const uint32_t *eid, const float *esc, const float *hs, int lane,
                                           float *acc) {
-  for (int j = 0; j < k; ++j) {
-    const uint32_t e = eid[j];
-    const float sc = e < uint32_t(n_experts) ? esc[j] : 0.0f;
-    const uint8_t *row = wd + (size_t(e < uint32_t(n_experts) ? e : 0u) * H) * rb;
+  const int nch = I / 32, n = k * nch;
+  for (int u0 = lane; u0 < n; u0 += 128) {
+    float w[2][kAnyRows][32];
+    float sc[2];
+    int hj[2];
 #pragma unroll
-    for (int rr = 0; rr < kAnyRows; ++rr)
-      acc[rr] = fmaf(sc, chunks_dot<T>(row + rr * rb, I / 32, hs + size_t(j) * I, lane), acc[rr]);
+    for (int q = 0; q < 2; ++q) {
+      const int u = min(u0 + 64 * q, n - 1), j = u / nch, c = u - j * nch;
+      const uint32_t e = eid[j];
+      sc[q] = u0 + 64 * q < n && e < uint32_t(n_experts) ? esc[j] : 0.0f;
+      hj[q] = j * I + 32 * c;
+      const uint8_t *row = wd + (size_t(e < uint32_t(n_experts) ? e : 0u) * H) * rb;
+#pragma unroll
+      for (int rr = 0; rr < kAnyRows; ++rr) decode32<T>(row + rr * rb, c, w[q][rr]);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float4 *xv = reinterpret_cast<const float4 *>(hs + hj[q]);
+#pragma unroll
+      for (int rr = 0; rr < kAnyRows; ++rr) {
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float4 v = xv[i];
+          d = fmaf(w[q][rr][4 * i], v.x, d);
+          d = fmaf(w[q][rr][4 * i + 1], v.y, d);
+          d = fmaf(w[q][rr][4 * i + 2], v.z, d);
+          d = fmaf(w[q][rr][4 * i + 3], v.w, d);
+        }
+        acc[rr] = fmaf(sc[q], d, acc[rr]);
+      }
+    }
   }
 }
 
@@ -262,6 +311,112 @@ __global__ void __launch_bounds__(256)
       if (residual) v += load_elt(residual, oi, rdt);
       store_elt(out, oi, v, odt);
     }
+  }
+}
+
+// k_down_any for Q6_K down matrices (the 35B's down projections), on the packed-f16 dot instead of a decode to f32.
+// Grid (ceil(H / 4), T), 256 threads, one output row a wavefront (twice k_down_any's wavefronts: the kernel is
+// latency-bound at decode width). The token's k x I / 32 (expert, chunk) items go four a lane, every weight load
+// issued before h is staged, so the weights' round trip overlaps the staging: h into LDS as f16 pairs [k][I / 2],
+// then the sums of its f16 values over each 16-weight scale group [k][I / 16] from LDS. A chunk's 6-bit q
+// (ql nibble | qh bits << 4) go four to a dword; v_perm spreads two of them to the low byte of each half and one
+// shift-or makes the f16 pair (64 + q_a, 64 + q_b) exact, so that v_dot2 forms sum h (64 + q) in fp32 and a
+// group's dot is (d sc) (that - 96 sum h) = sum h (d sc) (q - 32). About 11 VALU for 4 weights against ~30 for
+// the f32 decode; results are within rounding of k_down_any's (h is rounded to f16 once, as the Q4 down kernels
+// take it). Items past 256 a row take further passes.
+constexpr int kQ6Slots = 4;
+__global__ void __launch_bounds__(256)
+    k_down_q6k(const float *h, const uint32_t *ids, const float *scores, int k, const uint8_t *wd, int n_experts,
+               int I, int H, size_t rbd, const float *shared, const float *gate, int gate_stride,
+               const void *residual, int rdt, void *out, int odt) {
+  extern __shared__ uint32_t hl[];
+  __shared__ uint32_t eid[32];
+  __shared__ float esc[32];
+  const int t = blockIdx.y;
+  const int nh = k * I / 2, ng = k * I / 16;
+  uint32_t *h16 = hl;
+  float *hsum = reinterpret_cast<float *>(hl + nh);
+  if (threadIdx.x < k) {
+    eid[threadIdx.x] = ids[size_t(t) * k + threadIdx.x];
+    esc[threadIdx.x] = scores ? scores[size_t(t) * k + threadIdx.x] : 1.0f;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int o0 = blockIdx.x * 4 + wave;  // this wavefront's output row (past H: row H - 1 again, not stored)
+  const int o = min(o0, H - 1);
+  const int nch = I / 32, n = k * nch;
+  uint32_t lq[kQ6Slots][8], hq[kQ6Slots][8], scw[kQ6Slots];
+  float dd[kQ6Slots], sc[kQ6Slots];
+  int jj[kQ6Slots], cc[kQ6Slots];
+  // item u = j (I / 32) + c: chunk c of expert j; slot q holds u0 + 64 q (clamped repeats weigh 0)
+  auto load = [&](int u0) {
+#pragma unroll
+    for (int q = 0; q < kQ6Slots; ++q) {
+      const int u = min(u0 + 64 * q, n - 1), j = u / nch, c = u - j * nch;
+      const uint32_t e = eid[j];
+      sc[q] = u0 + 64 * q < n && e < uint32_t(n_experts) ? esc[j] : 0.0f;
+      jj[q] = j;
+      cc[q] = c;
+      const int js = c & 7, hh = js >> 2, g = js & 3;
+      const uint8_t *b = wd + (size_t(e < uint32_t(n_experts) ? e : 0u) * H + o) * rbd + size_t(c >> 3) * 210;
+      load_window8(b + 64 * hh + 32 * (g & 1), lq[q]);
+      load_window8(b + 128 + 32 * hh, hq[q]);
+      dd[q] = f16at(b + 208);
+      scw[q] = ld16(b + 192 + 8 * hh + 2 * g);
+    }
+  };
+  float acc = 0.0f;
+  auto compute = [&]() {
+#pragma unroll
+    for (int q = 0; q < kQ6Slots; ++q) {
+      const int g = (cc[q] & 7) & 3, sl = 4 * (g >> 1), shh = 2 * g;
+      const uint32_t *hp = h16 + jj[q] * (I / 2) + 16 * cc[q];
+      const float s0 = hsum[jj[q] * (I / 16) + 2 * cc[q]], s1 = hsum[jj[q] * (I / 16) + 2 * cc[q] + 1];
+      float g0 = 0.0f, g1 = 0.0f;  // sum h (64 + q) over the chunk's two scale groups (weights 0-15, 16-31)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t q6 = ((lq[q][i] >> sl) & 0x0F0F0F0Fu) | (((hq[q][i] >> shh) & 0x03030303u) << 4);
+        const uint32_t p01 = (__builtin_amdgcn_perm(0u, q6, 0x0C010C00u) << 4) | 0x54005400u;
+        const uint32_t p23 = (__builtin_amdgcn_perm(0u, q6, 0x0C030C02u) << 4) | 0x54005400u;
+        float &gi = i < 4 ? g0 : g1;
+        gi = dot2(p01, hp[2 * i], gi);
+        gi = dot2(p23, hp[2 * i + 1], gi);
+      }
+      const float d = dd[q];
+      const float ds0 = d * float(int(int8_t(uint8_t(scw[q])))), ds1 = d * float(int(int8_t(uint8_t(scw[q] >> 8))));
+      acc = fmaf(sc[q], ds0 * fmaf(-96.0f, s0, g0) + ds1 * fmaf(-96.0f, s1, g1), acc);
+    }
+  };
+  load(lane);  // the first four items' weights go out before h is staged
+  const float *ht = h + size_t(t) * k * I;
+  for (int i = threadIdx.x; i < nh; i += 256) {
+    const float2 v = reinterpret_cast<const float2 *>(ht)[i];
+    const h2_t p = {_Float16(v.x), _Float16(v.y)};
+    h16[i] = __builtin_bit_cast(uint32_t, p);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < ng; i += 256) {
+    float sm = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const h2_t p = __builtin_bit_cast(h2_t, h16[8 * i + q]);
+      sm += float(p[0]);
+      sm += float(p[1]);
+    }
+    hsum[i] = sm;
+  }
+  __syncthreads();
+  compute();
+  for (int u0 = lane + 64 * kQ6Slots; u0 < n; u0 += 64 * kQ6Slots) {
+    load(u0);
+    compute();
+  }
+  float v = wave_sum(acc);
+  if (lane == 0 && o0 < H) {
+    const size_t oi = size_t(t) * H + o0;
+    if (shared) v += sigmoidf_(gate[size_t(t) * gate_stride]) * shared[oi];
+    if (residual) v += load_elt(residual, oi, rdt);
+    store_elt(out, oi, v, odt);
   }
 }
 
@@ -358,9 +513,18 @@ int down_any(const char *fn, const float *h, const uint32_t *ids, const float *s
   if (T == 0) return 0;
   LMOE_REQUIRE(T <= 65535, LMOE_ESHAPE, "%s: %d tokens a call is above the 65535 this kernel takes", fn, T);
   LMOE_REQUIRE(h && ids && out, LMOE_EINVAL, "%s: null pointer", fn);
+  const dim3 grid((H + 4 * kAnyRows - 1) / (4 * kAnyRows), T);
+  if (td == LMOE_Q6_K) {  // f16 pairs of h and the 16-weight group sums: k I (2 + 1 / 4) bytes
+    const size_t lq6 = size_t(k) * I / 2 * 4 + size_t(k) * I / 16 * 4;
+    if (int rc = allow_lds(k_down_q6k, lq6, fn)) return rc;
+    launch(k_down_q6k, dim3((H + 3) / 4, T), dim3(256), lq6, st, h, ids, scores, k, wd, n_experts, I, H,
+           row_bytes_any(td, I), shared, gate, gate_stride, residual, rdt, out, odt);
+    LMOE_LAUNCHED(fn);
+    return 0;
+  }
   if (int rc = allow_lds(k_down_any, lds, fn)) return rc;
-  launch(k_down_any, dim3((H + 4 * kAnyRows - 1) / (4 * kAnyRows), T), dim3(256), lds, st, h, ids, scores, k, wd,
-         td, n_experts, I, H, row_bytes_any(td, I), shared, gate, gate_stride, residual, rdt, out, odt);
+  launch(k_down_any, grid, dim3(256), lds, st, h, ids, scores, k, wd, td, n_experts, I, H, row_bytes_any(td, I),
+         shared, gate, gate_stride, residual, rdt, out, odt);
   LMOE_LAUNCHED(fn);
   return 0;
 }

@@ -81,7 +81,9 @@ def test_gemv_chain(types, H, I, xdt):
 
 @pytest.mark.parametrize("t", NEW)
 def test_down_combine_epilogue(t):
-    """out[t] = sum_j s_j h[t k + j] . wd[ids] + sigmoid(gate) shared + residual on the general kernel."""
+    """out[t] = sum_j s_j h[t k + j] . wd[ids] + sigmoid(gate) shared + residual on the general kernel. The Q6_K
+    kernel takes h as f16 (v_dot2 on (64 + q) pairs), so its reference rounds h to f16 first; the others read fp32
+    h. Either way only the summation order is left, held to 1e-5."""
     from larder_amd import _lib
     from larder_amd._lib import call, ptr, qcode, stream
     rng = np.random.default_rng(31)
@@ -99,12 +101,13 @@ def test_down_combine_epilogue(t):
     call("lmoe_gemv_down_combine", ptr(dh), ptr(did), ptr(dsc), T, k, ptr(dev(wd)), qcode(t), E, I, H, ptr(dsh),
          ptr(dg), 1, ptr(dr), _lib.F32, ptr(out), _lib.F32, stream())
     W = moe.dequant_experts(wd, t).astype(np.float64)
+    hw = h.astype(np.float16).astype(np.float64) if t == "Q6_K" else h.astype(np.float64)
     want = np.zeros((T, H))
     for r in range(T):
         for j in range(k):
             e = ids[r * k + j]
             if e < E:
-                want[r] += sc[r, j] * (W[e] @ h[r * k + j].astype(np.float64))
+                want[r] += sc[r, j] * (W[e] @ hw[r * k + j])
         want[r] += shared[r] / (1.0 + np.exp(-float(gate[r]))) + res[r]
     assert moe.rel_l2(host(out), want) < 1e-5
 
