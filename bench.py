@@ -388,7 +388,29 @@ def types_leg():
         torch.cuda.synchronize()
         us_layer = e0.elapsed_time(e1) / 5 * 1e3
         del L, B
+        # batch-1 decode through a stack of 8 such layers (own experts and router each) as one HIP graph a token,
+        # the route layer.decode takes for these types (decode_general: fp32 h, the general or Q6_K down)
+        shapes = ((I, H), (I, H), (H, I))
+        Ls = [lay.MoELayer(*(workloads.random_blocks(t, E, r, c, g) for (r, c), t in zip(shapes, types)), types, k,
+                           True, wr=workloads.router_weight(E, H, g)) for _ in range(8)]
+        st = lay.DecodeStack(Ls, 1)
+        st.capture()
+        xs = torch.randn((80, 1, H), generator=g, device="cuda").half()
+        for i in range(40):
+            st.x_in.copy_(xs[i % 16])
+            st.graph.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for i in range(16, 80):
+            st.x_in.copy_(xs[i])
+            st.graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us_stack = e0.elapsed_time(e1) / 64 * 1e3 / len(Ls)
+        del st, Ls
         out["/".join(types)] = {
+            "decode_stack_us_per_layer": round(us_stack, 2),
+            "decode_stack_hbm_frac": round(wbytes / (us_stack * 1e-6) / HBM_PEAK, 4),
             "decode_gate_up_us": round(gu, 2), "decode_down_us": round(dn, 2), "decode_bytes": byts,
             "decode_hbm_frac": round(byts / ((gu + dn) * 1e-6) / HBM_PEAK, 4),
             "dense_2048x8_us": round(us_dense, 1), "dense_mfma_frac": round(flops / (us_dense * 1e-6) / MFMA_PEAK, 4),

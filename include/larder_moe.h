@@ -149,6 +149,15 @@ int lmoe_moe_gate_up_ext(const float *logits, int ld_stride, int T, int k, int n
                          int n_experts, int H, int I, uint32_t *ids, float *scores, uint32_t *hprep, int type_d,
                          int with_shared, void *stream);
 
+/* lmoe_moe_gate_up (with_shared = 0) or lmoe_moe_gate_up_ext (with_shared = m slices) writing h as fp32
+ * [T (k + m)][I] instead of prepared rows, for a layer whose down matrix is a type beyond Q4_0 / Q4_K (the 35B's
+ * Q6_K down): lmoe_gemv_down_combine then takes h. One Q4 type for gate and up, hidden 2048 or 4096, I even (the
+ * register-resident form). Replaces route_cuda.probs plus gguf_gate_up on decode rows with f32 h out, as the
+ * reference's chain passes it (route_cuda.py:433-444; gguf_experts.py:452-495, 600-653). */
+int lmoe_moe_gate_up_h(const float *logits, int ld_stride, int T, int k, int norm, const uint32_t *x_prep,
+                       const uint8_t *wg, const uint8_t *wu, int type, int n_experts, int H, int I, uint32_t *ids,
+                       float *scores, float *h, int with_shared, void *stream);
+
 /* Decode chain, down with the weighted combine fused:
  *   out[t][n] = sum_j scores[t][j] * (h[t * k + j] . wd[ids[t][j]][n])
  *               (+ sigmoid(gate[t * gate_stride]) * shared[t][n]) (+ residual[t][n])

@@ -45,6 +45,7 @@ SIGNATURES = {
     "lmoe_gemv_gate_up_prepped": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _P]),
     "lmoe_moe_gate_up": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P]),
     "lmoe_moe_gate_up_ext": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
+    "lmoe_moe_gate_up_h": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P]),
     "lmoe_gemv_down_combine": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_gemv_down_combine_prepped": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I,
                                             _P]),

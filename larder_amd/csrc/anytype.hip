@@ -231,17 +231,32 @@ __global__ void __launch_bounds__(256) k_gate_up_any(const void *x, int xdt, con
 // takes u = lane, lane + 64, ... two a pass, so that at decode width (k 8, I 768: 192 items) every lane has work and
 // both items' loads are out before either's arithmetic (a loop over the experts kept 40 of 64 lanes idle at I 768
 // and paid one memory round trip an expert). A lane's clamped repeat of the last item takes weight 0.
-template <int T>
+template <int T, bool FLAT>
 __device__ __forceinline__ void down_rows(const uint8_t *wd, size_t rb, int H, int I, int k, int n_experts,
                                           const uint32_t *eid, const float *esc, const float *hs, int lane,
                                           float *acc) {
+  if (!FLAT) {  // a row's items fit one pass (k I / 32 <= 64): chunks over lanes, one expert after another
+    for (int j = 0; j < k; ++j) {
+      const uint32_t e = eid[j];
+      const float sc = e < uint32_t(n_experts) ? esc[j] : 0.0f;
+      const uint8_t *row = wd + (size_t(e < uint32_t(n_experts) ? e : 0u) * H) * rb;
+#pragma unroll
+      for (int rr = 0; rr < kAnyRows; ++rr)
+        acc[rr] = fmaf(sc, chunks_dot<T>(row + rr * rb, I / 32, hs + size_t(j) * I, lane), acc[rr]);
+    }
+    return;
+  }
   const int nch = I / 32, n = k * nch;
-  for (int u0 = lane; u0 < n; u0 += 128) {
+  for (int u0 = lane; u0 - lane < n; u0 += 128) {
+    // the pass's second item only when a lane of the wavefront has one (uniform: u0 - lane is); otherwise it would
+    // be a whole wavefront of repeats (k 1, I 768: 24 items a row)
+    const int nq = u0 - lane + 64 < n ? 2 : 1;
     float w[2][kAnyRows][32];
-    float sc[2];
-    int hj[2];
+    float sc[2] = {0.0f, 0.0f};
+    int hj[2] = {0, 0};
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
+      if (q >= nq) break;
       const int u = min(u0 + 64 * q, n - 1), j = u / nch, c = u - j * nch;
       const uint32_t e = eid[j];
       sc[q] = u0 + 64 * q < n && e < uint32_t(n_experts) ? esc[j] : 0.0f;
@@ -252,6 +267,7 @@ __device__ __forceinline__ void down_rows(const uint8_t *wd, size_t rb, int H, i
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
+      if (q >= nq) break;
       const float4 *xv = reinterpret_cast<const float4 *>(hs + hj[q]);
 #pragma unroll
       for (int rr = 0; rr < kAnyRows; ++rr) {
@@ -273,6 +289,7 @@ __device__ __forceinline__ void down_rows(const uint8_t *wd, size_t rb, int H, i
 // Grid (ceil(H / 8), T), 256 threads: token t's k h rows staged as float32 in LDS; wavefront w takes output rows
 // 8 bx + 2 w, +1: out[t][o] = sum_j s_j (h[t k + j] . wd[ids[t k + j]][o]) (+ sigmoid(gate) shared) (+ residual),
 // s_j = scores[t k + j] (1 without scores), ids past the experts adding nothing (expert 0's row read, weight 0).
+template <bool FLAT>
 __global__ void __launch_bounds__(256)
     k_down_any(const float *h, const uint32_t *ids, const float *scores, int k, const uint8_t *wd, int td,
                int n_experts, int I, int H, size_t rbd, const float *shared, const float *gate, int gate_stride,
@@ -294,12 +311,12 @@ __global__ void __launch_bounds__(256)
   const uint8_t *w0 = wd + size_t(ob) * rbd;
   float acc[kAnyRows] = {0.0f, 0.0f};
   switch (td) {
-    case LMOE_Q4_0: down_rows<LMOE_Q4_0>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
-    case LMOE_Q4_1: down_rows<LMOE_Q4_1>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
-    case LMOE_Q8_0: down_rows<LMOE_Q8_0>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
-    case LMOE_Q4_K: down_rows<LMOE_Q4_K>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
-    case LMOE_Q5_K: down_rows<LMOE_Q5_K>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
-    default: down_rows<LMOE_Q6_K>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
+    case LMOE_Q4_0: down_rows<LMOE_Q4_0, FLAT>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
+    case LMOE_Q4_1: down_rows<LMOE_Q4_1, FLAT>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
+    case LMOE_Q8_0: down_rows<LMOE_Q8_0, FLAT>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
+    case LMOE_Q4_K: down_rows<LMOE_Q4_K, FLAT>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
+    case LMOE_Q5_K: down_rows<LMOE_Q5_K, FLAT>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
+    default: down_rows<LMOE_Q6_K, FLAT>(w0, rbd, H, I, k, n_experts, eid, esc, hs, lane, acc); break;
   }
 #pragma unroll
   for (int rr = 0; rr < kAnyRows; ++rr) {
@@ -315,8 +332,8 @@ __global__ void __launch_bounds__(256)
 }
 
 // k_down_any for Q6_K down matrices (the 35B's down projections), on the packed-f16 dot instead of a decode to f32.
-// Grid (ceil(H / 4), T), 256 threads, one output row a wavefront (twice k_down_any's wavefronts: the kernel is
-// latency-bound at decode width). The token's k x I / 32 (expert, chunk) items go four a lane, every weight load
+// Grid (ceil(H / 8), T), 512 threads, one output row a wavefront: eight rows share one staging of the token's h (a
+// four-row workgroup read more h than weights at decode width, 12.6 MB against 10.3 at k 8, I 768, H 2048). The token's k x I / 32 (expert, chunk) items go four a lane, every weight load
 // issued before h is staged, so the weights' round trip overlaps the staging: h into LDS as f16 pairs [k][I / 2],
 // then the sums of its f16 values over each 16-weight scale group [k][I / 16] from LDS. A chunk's 6-bit q
 // (ql nibble | qh bits << 4) go four to a dword; v_perm spreads two of them to the low byte of each half and one
@@ -325,7 +342,7 @@ __global__ void __launch_bounds__(256)
 // the f32 decode; results are within rounding of k_down_any's (h is rounded to f16 once, as the Q4 down kernels
 // take it). Items past 256 a row take further passes.
 constexpr int kQ6Slots = 4;
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
     k_down_q6k(const float *h, const uint32_t *ids, const float *scores, int k, const uint8_t *wd, int n_experts,
                int I, int H, size_t rbd, const float *shared, const float *gate, int gate_stride,
                const void *residual, int rdt, void *out, int odt) {
@@ -342,16 +359,21 @@ __global__ void __launch_bounds__(256)
   }
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int o0 = blockIdx.x * 4 + wave;  // this wavefront's output row (past H: row H - 1 again, not stored)
+  const int o0 = blockIdx.x * 8 + wave;  // this wavefront's output row (past H: row H - 1 again, not stored)
   const int o = min(o0, H - 1);
   const int nch = I / 32, n = k * nch;
   uint32_t lq[kQ6Slots][8], hq[kQ6Slots][8], scw[kQ6Slots];
   float dd[kQ6Slots], sc[kQ6Slots];
   int jj[kQ6Slots], cc[kQ6Slots];
   // item u = j (I / 32) + c: chunk c of expert j; slot q holds u0 + 64 q (clamped repeats weigh 0)
+  // slots a pass: only as many as a lane of the wavefront has items for (uniform), so that short rows (the
+  // decode chain's one slot a row: 24 items at I 768) do not decode whole wavefronts of repeats
+  int ns = kQ6Slots;
   auto load = [&](int u0) {
+    ns = min(kQ6Slots, (n - (u0 - lane) + 63) / 64);
 #pragma unroll
     for (int q = 0; q < kQ6Slots; ++q) {
+      if (q >= ns) break;
       const int u = min(u0 + 64 * q, n - 1), j = u / nch, c = u - j * nch;
       const uint32_t e = eid[j];
       sc[q] = u0 + 64 * q < n && e < uint32_t(n_experts) ? esc[j] : 0.0f;
@@ -369,6 +391,7 @@ __global__ void __launch_bounds__(256)
   auto compute = [&]() {
 #pragma unroll
     for (int q = 0; q < kQ6Slots; ++q) {
+      if (q >= ns) break;
       const int g = (cc[q] & 7) & 3, sl = 4 * (g >> 1), shh = 2 * g;
       const uint32_t *hp = h16 + jj[q] * (I / 2) + 16 * cc[q];
       const float s0 = hsum[jj[q] * (I / 16) + 2 * cc[q]], s1 = hsum[jj[q] * (I / 16) + 2 * cc[q] + 1];
@@ -389,13 +412,13 @@ __global__ void __launch_bounds__(256)
   };
   load(lane);  // the first four items' weights go out before h is staged
   const float *ht = h + size_t(t) * k * I;
-  for (int i = threadIdx.x; i < nh; i += 256) {
+  for (int i = threadIdx.x; i < nh; i += 512) {
     const float2 v = reinterpret_cast<const float2 *>(ht)[i];
     const h2_t p = {_Float16(v.x), _Float16(v.y)};
     h16[i] = __builtin_bit_cast(uint32_t, p);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < ng; i += 256) {
+  for (int i = threadIdx.x; i < ng; i += 512) {
     float sm = 0.0f;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -407,7 +430,7 @@ __global__ void __launch_bounds__(256)
   }
   __syncthreads();
   compute();
-  for (int u0 = lane + 64 * kQ6Slots; u0 < n; u0 += 64 * kQ6Slots) {
+  for (int u0 = lane + 64 * kQ6Slots; u0 - lane < n; u0 += 64 * kQ6Slots) {
     load(u0);
     compute();
   }
@@ -514,17 +537,21 @@ int down_any(const char *fn, const float *h, const uint32_t *ids, const float *s
   LMOE_REQUIRE(T <= 65535, LMOE_ESHAPE, "%s: %d tokens a call is above the 65535 this kernel takes", fn, T);
   LMOE_REQUIRE(h && ids && out, LMOE_EINVAL, "%s: null pointer", fn);
   const dim3 grid((H + 4 * kAnyRows - 1) / (4 * kAnyRows), T);
-  if (td == LMOE_Q6_K) {  // f16 pairs of h and the 16-weight group sums: k I (2 + 1 / 4) bytes
+  // a row of more than 64 (expert, chunk) items (the decode layer's k slots a token) takes the flattened forms; the
+  // decode chain's one slot a row keeps the serial one
+  const bool flat = k * (I / 32) > 64;
+  if (flat && td == LMOE_Q6_K) {  // f16 pairs of h and the 16-weight group sums: k I (2 + 1 / 4) bytes
     const size_t lq6 = size_t(k) * I / 2 * 4 + size_t(k) * I / 16 * 4;
     if (int rc = allow_lds(k_down_q6k, lq6, fn)) return rc;
-    launch(k_down_q6k, dim3((H + 3) / 4, T), dim3(256), lq6, st, h, ids, scores, k, wd, n_experts, I, H,
+    launch(k_down_q6k, dim3((H + 7) / 8, T), dim3(512), lq6, st, h, ids, scores, k, wd, n_experts, I, H,
            row_bytes_any(td, I), shared, gate, gate_stride, residual, rdt, out, odt);
     LMOE_LAUNCHED(fn);
     return 0;
   }
-  if (int rc = allow_lds(k_down_any, lds, fn)) return rc;
-  launch(k_down_any, grid, dim3(256), lds, st, h, ids, scores, k, wd, td, n_experts, I, H, row_bytes_any(td, I),
-         shared, gate, gate_stride, residual, rdt, out, odt);
+  auto kern = flat ? k_down_any<true> : k_down_any<false>;
+  if (int rc = allow_lds(kern, lds, fn)) return rc;
+  launch(kern, grid, dim3(256), lds, st, h, ids, scores, k, wd, td, n_experts, I, H, row_bytes_any(td, I), shared,
+         gate, gate_stride, residual, rdt, out, odt);
   LMOE_LAUNCHED(fn);
   return 0;
 }

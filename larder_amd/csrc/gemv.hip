@@ -1528,6 +1528,25 @@ extern "C" int lmoe_moe_gate_up_ext(const float *logits, int ld_stride, int T, i
   return gate_up(fn, a, type_g, type_u, stream);
 }
 
+extern "C" int lmoe_moe_gate_up_h(const float *logits, int ld_stride, int T, int k, int norm, const uint32_t *x_prep,
+                                  const uint8_t *wg, const uint8_t *wu, int type, int n_experts, int H, int I,
+                                  uint32_t *ids, float *scores, float *h, int with_shared, void *stream) {
+  const char *fn = "lmoe_moe_gate_up_h";
+  LMOE_REQUIRE(with_shared >= 0, LMOE_EINVAL, "%s: %d shared slices", fn, with_shared);
+  LMOE_REQUIRE(T == 0 || (logits && x_prep && aligned16(x_prep) && h), LMOE_EALIGN,
+               "%s: logits, 16-byte aligned prepared rows and h must be given", fn);
+  LMOE_REQUIRE((H == 2048 || H == 4096) && I % 2 == 0, LMOE_ESHAPE,
+               "%s: takes the register-resident form, hidden 2048 or 4096 and an even width (got %d, %d)", fn, H, I);
+  LMOE_REQUIRE(ld_stride >= n_experts + (with_shared ? 1 : 0), LMOE_ESHAPE,
+               "%s: logits row stride %d is below %d experts%s", fn, ld_stride, n_experts,
+               with_shared ? " and the shared gate logit" : "");
+  const int ks = k + with_shared;
+  LMOE_REQUIRE(k >= 1 && ks <= 64, LMOE_ESHAPE, "%s: k %d with %d shared slices", fn, k, with_shared);
+  GateUpArgs a{x_prep, x_prep, nullptr, 0, nullptr, T * ks, k, wg, wu, n_experts, H, I, h, nullptr, 0, logits,
+               ld_stride, norm, ids, scores, with_shared ? ks : 0};
+  return gate_up(fn, a, type, type, stream);
+}
+
 extern "C" int lmoe_moe_gate_up_part(const float *part, const void *x, int xdtype, int T, int k, int norm,
                                      const uint8_t *wg, const uint8_t *wu, int type_g, int type_u, int n_experts,
                                      int H, int I, uint32_t *ids, float *scores, uint32_t *hprep, int type_d,

@@ -183,15 +183,16 @@ def prepared_chain(layer):
 def decode_general(layer, x, bufs, out, residual=None, logits=None):
     """decode() for a layer with a projection beyond Q4_0 / Q4_K, such as the 35B's Q4_K / Q4_K / Q6_K (the
     reference runs every type through gguf_experts.gemv's chain, gguf_experts.py:600-653, with f32 h):
-      * the router GEMV ranks in its last workgroup (lmoe_router_gemv_rank: ids / scores with a folded shared
-        expert's slots, and x prepared when gate/up take the register-resident form), or lmoe_router_topk on
-        given logits;
-      * gate/up + SwiGLU into fp32 h: on the prepared rows when gate and up share one Q4 type at hidden 2048 or
-        4096 (lmoe_gemv_gate_up_prepped), else from raw x (lmoe_gemv_gate_up);
+      * when gate and up share one Q4 type at hidden 2048 or 4096: the router GEMV (x prepared), then gate/up +
+        SwiGLU with the top-k fused in (lmoe_moe_gate_up_h: ids / scores with a folded shared expert's slots, h as
+        fp32), as the prepared chain does;
+      * otherwise the router GEMV ranks in its last workgroup (lmoe_router_gemv_rank), or lmoe_router_topk takes
+        given logits, and gate/up + SwiGLU run from raw x (lmoe_gemv_gate_up) into fp32 h;
       * [an unfolded shared expert's gate/up and down into an fp32 row;]
-      * the general down + weighted combine + shared + residual (lmoe_gemv_down_combine).
-    Four launches a layer (six with an unfolded shared expert), all preallocated, so a stack still captures as one
-    HIP graph."""
+      * the general down + weighted combine + shared + residual (lmoe_gemv_down_combine; Q6_K on its packed-f16
+        kernel).
+    Three launches a layer (five with an unfolded shared expert), all preallocated, so a stack still captures as
+    one HIP graph."""
     L, B = layer, bufs
     T = x.shape[0]
     st = stream()
@@ -199,24 +200,31 @@ def decode_general(layer, x, bufs, out, residual=None, logits=None):
     xd = dcode(x.dtype)
     ks = L.k + L.n_shared
     xr = L.types[0] == L.types[1] and L.types[0] in _lib.Q4_TYPES and L.H in (2048, 4096) and L.I % 2 == 0
-    if logits is None:
-        if L.wr is None:
-            raise ValueError("this layer has no router weight: pass logits")
-        if L.E > RANK_MAX_E or L.k > RANK_MAX_K:
-            raise ValueError(f"decode takes at most {RANK_MAX_E} experts and top-{RANK_MAX_K} when a projection is "
-                             f"beyond Q4_0 / Q4_K (got {L.E}, top-{L.k})")
-        call("lmoe_router_gemv_rank", ptr(x), xd, ptr(L.wr), ptr(L.wsg), dcode(L.wr.dtype), T, L.H, L.E, L.k,
-             int(L.norm), ks, ptr(B.logits), ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.xprep) if xr else None, tg,
-             ptr(B.sync), st)
-    else:
-        if L.shared is not None:
-            raise ValueError("a shared expert's gate logit comes from the router GEMV: use the router weight")
-        lg = logits.to(torch.float32).contiguous()
-        call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids_ext), ptr(B.scores_ext), st)
-        if xr:
-            call("lmoe_prep_x", ptr(x), xd, T, L.H, tg, ptr(B.xprep), st)
+    if logits is not None and L.shared is not None:
+        raise ValueError("a shared expert's gate logit comes from the router GEMV: use the router weight")
+    if logits is None and L.wr is None:
+        raise ValueError("this layer has no router weight: pass logits")
     wg, wu, wd = L.folded if L.folded is not None else (L.wg, L.wu, L.wd)
     ne = L.E + L.n_shared
+    if xr:  # the prepared chain's router and fused top-k, h out as fp32
+        if logits is None:
+            call("lmoe_router_gemv", ptr(x), xd, ptr(L.wr), ptr(L.wsg), dcode(L.wr.dtype), T, L.H, L.E,
+                 ptr(B.logits), ptr(B.xprep), tg, st)
+            lg, stride = B.logits, B.logits.shape[1]
+        else:
+            lg, stride = logits.to(torch.float32).contiguous(), L.E
+            call("lmoe_prep_x", ptr(x), xd, T, L.H, tg, ptr(B.xprep), st)
+        call("lmoe_moe_gate_up_h", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(wg), ptr(wu), tg, L.E,
+             L.H, L.I, ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.h32), L.n_shared, st)
+    elif logits is None:
+        if L.E > RANK_MAX_E or L.k > RANK_MAX_K:
+            raise ValueError(f"decode takes at most {RANK_MAX_E} experts and top-{RANK_MAX_K} when gate/up are "
+                             f"beyond Q4_0 / Q4_K (got {L.E}, top-{L.k})")
+        call("lmoe_router_gemv_rank", ptr(x), xd, ptr(L.wr), ptr(L.wsg), dcode(L.wr.dtype), T, L.H, L.E, L.k,
+             int(L.norm), ks, ptr(B.logits), ptr(B.ids_ext), ptr(B.scores_ext), None, tg, ptr(B.sync), st)
+    else:
+        lg = logits.to(torch.float32).contiguous()
+        call("lmoe_router_topk", ptr(lg), _lib.F32, T, L.E, L.k, int(L.norm), ptr(B.ids_ext), ptr(B.scores_ext), st)
 
     def gate_up(slots, n, topk, g, u, n_exp, width, h):
         if xr:
@@ -226,7 +234,8 @@ def decode_general(layer, x, bufs, out, residual=None, logits=None):
             call("lmoe_gemv_gate_up", ptr(x), xd, ptr(slots), n, topk, ptr(g), ptr(u), tg, tu, n_exp, L.H, width,
                  ptr(h), st)
 
-    gate_up(B.ids_ext, T * ks, ks, wg, wu, ne, L.I, B.h32)
+    if not xr:
+        gate_up(B.ids_ext, T * ks, ks, wg, wu, ne, L.I, B.h32)
     shared_y = gptr = None
     gate_stride = 0
     if L.shared is not None and L.folded is None:

@@ -79,15 +79,17 @@ def test_gemv_chain(types, H, I, xdt):
     assert moe.rel_l2(host(y16.float()), yw) < BAR
 
 
+@pytest.mark.parametrize("k", [4, 8])
 @pytest.mark.parametrize("t", NEW)
-def test_down_combine_epilogue(t):
-    """out[t] = sum_j s_j h[t k + j] . wd[ids] + sigmoid(gate) shared + residual on the general kernel. The Q6_K
-    kernel takes h as f16 (v_dot2 on (64 + q) pairs), so its reference rounds h to f16 first; the others read fp32
-    h. Either way only the summation order is left, held to 1e-5."""
+def test_down_combine_epilogue(t, k):
+    """out[t] = sum_j s_j h[t k + j] . wd[ids] + sigmoid(gate) shared + residual on the general kernels: k 4 at I 512
+    is 64 (expert, chunk) items a row, the serial form; k 8 is 128, the flattened forms, where Q6_K takes h as f16
+    (v_dot2 on (64 + q) pairs), so its reference rounds h to f16 first. Either way only the summation order is
+    left, held to 1e-5."""
     from larder_amd import _lib
     from larder_amd._lib import call, ptr, qcode, stream
-    rng = np.random.default_rng(31)
-    E, I, H, T, k = 10, 512, 1024, 3, 4
+    rng = np.random.default_rng(31 + k)
+    E, I, H, T = 10, 512, 1024, 3
     wd = gguf.random_experts(rng, E, H, I, t)
     h = rng.standard_normal((T * k, I)).astype(np.float32)
     ids = rng.integers(0, E, T * k).astype(np.int32)
@@ -101,7 +103,7 @@ def test_down_combine_epilogue(t):
     call("lmoe_gemv_down_combine", ptr(dh), ptr(did), ptr(dsc), T, k, ptr(dev(wd)), qcode(t), E, I, H, ptr(dsh),
          ptr(dg), 1, ptr(dr), _lib.F32, ptr(out), _lib.F32, stream())
     W = moe.dequant_experts(wd, t).astype(np.float64)
-    hw = h.astype(np.float16).astype(np.float64) if t == "Q6_K" else h.astype(np.float64)
+    hw = h.astype(np.float16).astype(np.float64) if t == "Q6_K" and k * I // 32 > 64 else h.astype(np.float64)
     want = np.zeros((T, H))
     for r in range(T):
         for j in range(k):
