@@ -4,11 +4,11 @@ The layer is the reference block's sequence (stream_fast.py:4352-4377 over gguf_
 gguf_experts.py:803-819): router logits x . Wr, softmax top-k, the k experts' SwiGLU chains read straight from
 GGUF blocks, the weighted combine, and a sigmoid-gated shared expert when the model has one. Two drivers:
 
-  * decode (T <= 16 tokens): router GEMV + top-k in one kernel (which also writes x prepared for the expert
-    kernels; its last workgroup ranks the logits) -> gate/up + SwiGLU on the picked experts (writing h prepared for
-    down) [-> the shared expert's gate/up and down] -> down + weighted combine + shared expert + residual in one
-    kernel; 3 launches a layer without a shared expert, no host synchronisation, every buffer preallocated so a
-    whole step can be captured in a HIP graph;
+  * decode (T <= 16 tokens): router GEMV (which also writes x prepared for the expert kernels) -> top-k fused
+    into gate/up + SwiGLU on the picked experts (writing h prepared for down) [-> the shared expert's gate/up and
+    down] -> down + weighted combine + shared expert + residual in one kernel; 3 launches a layer without a shared
+    expert, no host synchronisation, every buffer preallocated so a whole step can be captured in a HIP graph. A
+    layer with a projection beyond Q4_0 / Q4_K passes h as fp32 to the general down (decode_general);
   * prefill / batched decode (any T): the device grouping and the grouped MFMA GEMMs (larder_amd.grouped).
 """
 import ctypes
