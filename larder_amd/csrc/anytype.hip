@@ -333,26 +333,29 @@ __global__ void __launch_bounds__(256)
 
 // k_down_any for Q6_K down matrices (the 35B's down projections), on the packed-f16 dot instead of a decode to f32.
 // Grid (ceil(H / 8), T), 512 threads, one output row a wavefront: eight rows share one staging of the token's h (a
-// four-row workgroup read more h than weights at decode width, 12.6 MB against 10.3 at k 8, I 768, H 2048). The token's k x I / 32 (expert, chunk) items go four a lane, every weight load
-// issued before h is staged, so the weights' round trip overlaps the staging: h into LDS as f16 pairs [k][I / 2],
-// then the sums of its f16 values over each 16-weight scale group [k][I / 16] from LDS. A chunk's 6-bit q
-// (ql nibble | qh bits << 4) go four to a dword; v_perm spreads two of them to the low byte of each half and one
-// shift-or makes the f16 pair (64 + q_a, 64 + q_b) exact, so that v_dot2 forms sum h (64 + q) in fp32 and a
-// group's dot is (d sc) (that - 96 sum h) = sum h (d sc) (q - 32). About 11 VALU for 4 weights against ~30 for
-// the f32 decode; results are within rounding of k_down_any's (h is rounded to f16 once, as the Q4 down kernels
-// take it). Items past 256 a row take further passes.
+// four-row workgroup read more h than weights at decode width, 12.6 MB against 10.3 at k 8, I 768, H 2048). The
+// token's k x I / 32 (expert, chunk) items go up to four a lane, every weight load issued before h is staged, so the
+// weights' round trip overlaps the staging. h comes in one of two forms:
+//   PREP = false: fp32 [T k][I], staged as f16 pairs in natural order (weights 2m, 2m + 1);
+//   PREP = true: prepared rows [T k][I / 64 * 36] in the Q4_K order (lmoe_moe_gate_up with a Q6_K down: dword
+//     4 i + s of a 64-value unit holds values (4 i, 4 i + 2) + 32 (s & 1) for s < 2, (4 i + 1, 4 i + 3) + 32 (s & 1)
+//     for s >= 2), copied as they are with 16-byte loads: 2.25 bytes a value against 4.
+// A chunk's 6-bit q (ql nibble | qh bits << 4) go four to a dword; v_perm spreads two of them to the low byte of each
+// half and one shift-or makes the f16 pair (64 + q_a, 64 + q_b), from which one packed subtraction of 96 leaves
+// q - 32 exact; v_dot2 then forms sum h (q - 32) over each 16-weight scale group, times (d sc). About 13 VALU for 4
+// weights against ~30 for the f32 decode; results are within rounding of k_down_any's (h rounded to f16 once, as
+// the Q4 down kernels take it). Items past 256 a row take further passes.
 constexpr int kQ6Slots = 4;
+template <bool PREP>
 __global__ void __launch_bounds__(512)
-    k_down_q6k(const float *h, const uint32_t *ids, const float *scores, int k, const uint8_t *wd, int n_experts,
+    k_down_q6k(const void *hin, const uint32_t *ids, const float *scores, int k, const uint8_t *wd, int n_experts,
                int I, int H, size_t rbd, const float *shared, const float *gate, int gate_stride,
                const void *residual, int rdt, void *out, int odt) {
-  extern __shared__ uint32_t hl[];
+  extern __shared__ uint32_t hl[];  // the token's h: k rows of I / 2 dwords (natural) or I / 64 * 36 (prepared)
   __shared__ uint32_t eid[32];
   __shared__ float esc[32];
   const int t = blockIdx.y;
-  const int nh = k * I / 2, ng = k * I / 16;
-  uint32_t *h16 = hl;
-  float *hsum = reinterpret_cast<float *>(hl + nh);
+  const int rowd = PREP ? I / 64 * 36 : I / 2;  // dwords a staged h row
   if (threadIdx.x < k) {
     eid[threadIdx.x] = ids[size_t(t) * k + threadIdx.x];
     esc[threadIdx.x] = scores ? scores[size_t(t) * k + threadIdx.x] : 1.0f;
@@ -365,10 +368,10 @@ __global__ void __launch_bounds__(512)
   uint32_t lq[kQ6Slots][8], hq[kQ6Slots][8], scw[kQ6Slots];
   float dd[kQ6Slots], sc[kQ6Slots];
   int jj[kQ6Slots], cc[kQ6Slots];
-  // item u = j (I / 32) + c: chunk c of expert j; slot q holds u0 + 64 q (clamped repeats weigh 0)
   // slots a pass: only as many as a lane of the wavefront has items for (uniform), so that short rows (the
   // decode chain's one slot a row: 24 items at I 768) do not decode whole wavefronts of repeats
   int ns = kQ6Slots;
+  // item u = j (I / 32) + c: chunk c of expert j; slot q holds u0 + 64 q (clamped repeats weigh 0)
   auto load = [&](int u0) {
     ns = min(kQ6Slots, (n - (u0 - lane) + 63) / 64);
 #pragma unroll
@@ -388,45 +391,44 @@ __global__ void __launch_bounds__(512)
     }
   };
   float acc = 0.0f;
+  const h2_t k96 = {_Float16(96.0f), _Float16(96.0f)};
   auto compute = [&]() {
 #pragma unroll
     for (int q = 0; q < kQ6Slots; ++q) {
       if (q >= ns) break;
-      const int g = (cc[q] & 7) & 3, sl = 4 * (g >> 1), shh = 2 * g;
-      const uint32_t *hp = h16 + jj[q] * (I / 2) + 16 * cc[q];
-      const float s0 = hsum[jj[q] * (I / 16) + 2 * cc[q]], s1 = hsum[jj[q] * (I / 16) + 2 * cc[q] + 1];
-      float g0 = 0.0f, g1 = 0.0f;  // sum h (64 + q) over the chunk's two scale groups (weights 0-15, 16-31)
+      const int c = cc[q], g = (c & 7) & 3, sl = 4 * (g >> 1), shh = 2 * g;
+      // the chunk's h pairs: natural, 16 dwords from 16 c; prepared, unit c / 2's dwords, half c & 1
+      const uint32_t *hp = hl + jj[q] * rowd + (PREP ? 36 * (c >> 1) + (c & 1) : 16 * c);
+      float g0 = 0.0f, g1 = 0.0f;  // sum h (q - 32) over the chunk's two scale groups (weights 0-15, 16-31)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const uint32_t q6 = ((lq[q][i] >> sl) & 0x0F0F0F0Fu) | (((hq[q][i] >> shh) & 0x03030303u) << 4);
-        const uint32_t p01 = (__builtin_amdgcn_perm(0u, q6, 0x0C010C00u) << 4) | 0x54005400u;
-        const uint32_t p23 = (__builtin_amdgcn_perm(0u, q6, 0x0C030C02u) << 4) | 0x54005400u;
+        // weights 4 i .. 4 i + 3: natural pairs (0, 1), (2, 3); prepared pairs (0, 2), (1, 3)
+        const uint32_t pa = (__builtin_amdgcn_perm(0u, q6, PREP ? 0x0C020C00u : 0x0C010C00u) << 4) | 0x54005400u;
+        const uint32_t pb = (__builtin_amdgcn_perm(0u, q6, PREP ? 0x0C030C01u : 0x0C030C02u) << 4) | 0x54005400u;
+        const uint32_t wa = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, pa) - k96);
+        const uint32_t wb = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, pb) - k96);
         float &gi = i < 4 ? g0 : g1;
-        gi = dot2(p01, hp[2 * i], gi);
-        gi = dot2(p23, hp[2 * i + 1], gi);
+        gi = dot2(wa, PREP ? hp[4 * i] : hp[2 * i], gi);
+        gi = dot2(wb, PREP ? hp[4 * i + 2] : hp[2 * i + 1], gi);
       }
       const float d = dd[q];
       const float ds0 = d * float(int(int8_t(uint8_t(scw[q])))), ds1 = d * float(int(int8_t(uint8_t(scw[q] >> 8))));
-      acc = fmaf(sc[q], ds0 * fmaf(-96.0f, s0, g0) + ds1 * fmaf(-96.0f, s1, g1), acc);
+      acc = fmaf(sc[q], ds0 * g0 + ds1 * g1, acc);
     }
   };
   load(lane);  // the first four items' weights go out before h is staged
-  const float *ht = h + size_t(t) * k * I;
-  for (int i = threadIdx.x; i < nh; i += 512) {
-    const float2 v = reinterpret_cast<const float2 *>(ht)[i];
-    const h2_t p = {_Float16(v.x), _Float16(v.y)};
-    h16[i] = __builtin_bit_cast(uint32_t, p);
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < ng; i += 512) {
-    float sm = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const h2_t p = __builtin_bit_cast(h2_t, h16[8 * i + q]);
-      sm += float(p[0]);
-      sm += float(p[1]);
+  if (PREP) {  // k prepared rows, contiguous, copied as they are
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(static_cast<const uint32_t *>(hin) + size_t(t) * k * rowd);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(hl);
+    for (int i = threadIdx.x; i < k * rowd / 4; i += 512) dst[i] = src[i];
+  } else {
+    const float2 *src = reinterpret_cast<const float2 *>(static_cast<const float *>(hin) + size_t(t) * k * I);
+    for (int i = threadIdx.x; i < k * I / 2; i += 512) {
+      const float2 v = src[i];
+      const h2_t p = {_Float16(v.x), _Float16(v.y)};
+      hl[i] = __builtin_bit_cast(uint32_t, p);
     }
-    hsum[i] = sm;
   }
   __syncthreads();
   compute();
@@ -540,11 +542,11 @@ int down_any(const char *fn, const float *h, const uint32_t *ids, const float *s
   // a row of more than 64 (expert, chunk) items (the decode layer's k slots a token) takes the flattened forms; the
   // decode chain's one slot a row keeps the serial one
   const bool flat = k * (I / 32) > 64;
-  if (flat && td == LMOE_Q6_K) {  // f16 pairs of h and the 16-weight group sums: k I (2 + 1 / 4) bytes
-    const size_t lq6 = size_t(k) * I / 2 * 4 + size_t(k) * I / 16 * 4;
-    if (int rc = allow_lds(k_down_q6k, lq6, fn)) return rc;
-    launch(k_down_q6k, dim3((H + 7) / 8, T), dim3(512), lq6, st, h, ids, scores, k, wd, n_experts, I, H,
-           row_bytes_any(td, I), shared, gate, gate_stride, residual, rdt, out, odt);
+  if (flat && td == LMOE_Q6_K) {  // h as f16 pairs: k I 2 bytes
+    const size_t lq6 = size_t(k) * I / 2 * 4;
+    if (int rc = allow_lds(k_down_q6k<false>, lq6, fn)) return rc;
+    launch(k_down_q6k<false>, dim3((H + 7) / 8, T), dim3(512), lq6, st, static_cast<const void *>(h), ids, scores, k,
+           wd, n_experts, I, H, row_bytes_any(td, I), shared, gate, gate_stride, residual, rdt, out, odt);
     LMOE_LAUNCHED(fn);
     return 0;
   }
@@ -552,6 +554,29 @@ int down_any(const char *fn, const float *h, const uint32_t *ids, const float *s
   if (int rc = allow_lds(kern, lds, fn)) return rc;
   launch(kern, grid, dim3(256), lds, st, h, ids, scores, k, wd, td, n_experts, I, H, row_bytes_any(td, I), shared,
          gate, gate_stride, residual, rdt, out, odt);
+  LMOE_LAUNCHED(fn);
+  return 0;
+}
+
+// The Q6_K down + combine on prepared h rows [T k][I / 64 * 36] in the Q4_K order (lmoe_gemv_down_combine_prepped
+// with a Q6_K down matrix; the rows' sum dwords are not read).
+int down_q6k_prepped(const char *fn, const uint32_t *hprep, const uint32_t *ids, const float *scores, int T, int k,
+                     const uint8_t *wd, int n_experts, int I, int H, const float *shared, const float *gate,
+                     int gate_stride, const void *residual, int rdt, void *out, int odt, hipStream_t st) {
+  if (int rc = check_any(fn, LMOE_Q6_K, H, I, wd)) return rc;
+  LMOE_REQUIRE(dtype_ok(odt) && (!residual || dtype_ok(rdt)), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(k > 0 && k <= 32 && n_experts > 0, LMOE_ESHAPE, "%s: k %d of %d experts", fn, k, n_experts);
+  LMOE_REQUIRE(!shared == !gate, LMOE_EINVAL, "%s: shared and gate go together", fn);
+  const size_t lds = size_t(k) * (I / 64) * 36 * 4;
+  LMOE_REQUIRE(lds <= 150 * 1024, LMOE_ESHAPE, "%s: k %d rows of width %d exceed the LDS this kernel stages", fn, k,
+               I);
+  if (T == 0) return 0;
+  LMOE_REQUIRE(T <= 65535, LMOE_ESHAPE, "%s: %d tokens a call is above the 65535 this kernel takes", fn, T);
+  LMOE_REQUIRE(hprep && ids && out, LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(aligned16(hprep), LMOE_EALIGN, "%s: prepared h must be 16-byte aligned", fn);
+  if (int rc = allow_lds(k_down_q6k<true>, lds, fn)) return rc;
+  launch(k_down_q6k<true>, dim3((H + 7) / 8, T), dim3(512), lds, st, static_cast<const void *>(hprep), ids, scores,
+         k, wd, n_experts, I, H, row_bytes_any(LMOE_Q6_K, I), shared, gate, gate_stride, residual, rdt, out, odt);
   LMOE_LAUNCHED(fn);
   return 0;
 }

@@ -1,7 +1,8 @@
 """GPU parity of the decode layer (larder_amd.layer.decode, DecodeStack) on layers with a projection beyond
 Q4_0 / Q4_K, the route every block type takes in the reference (gguf_experts.py:600-653 over stream_fast.py:4352-4377):
-the 35B's Q4_K / Q4_K / Q6_K mix (gate/up on the register-resident kernel, Q6_K down on the general one), a Q8_0
-down with an unfolded shared expert, all-Q6_K and Q8_0 gate/up layers (the general gate/up), and given logits.
+the 35B's Q4_K / Q4_K / Q6_K mix (the prepared chain: gate/up on the register-resident kernel writing h in the Q4_K
+order, the Q6_K down reading it), a Q8_0 down with an unfolded shared expert (fp32 h, the general down), all-Q6_K
+and Q8_0 gate/up layers (the general gate/up), and given logits.
 Routing is pinned from x (the router GEMV's fixed order restated in the oracle, bit for bit) and the outputs are
 held to the north star's 2e-3 relative L2 against the fp32 dequant-then-matmul oracle."""
 import numpy as np
@@ -67,7 +68,8 @@ def test_decode_general_layer_vs_oracle(types, H, I, E, k, norm, Is, T):
     from larder_amd import layer as lay
     rng = np.random.default_rng(H + I + E + T + len(types[2]))
     L = make_layer(rng, types, H, I, E, k, norm, Is)
-    assert not lay.prepared_chain(L)
+    # a Q6_K down under one Q4 gate/up type stays on the prepared chain (h in the Q4_K order); the rest go general
+    assert lay.prepared_chain(L) == (types[2] == "Q6_K" and types[0] == types[1] and types[0] in ("Q4_0", "Q4_K"))
     if Is and Is % I == 0:
         assert L.folded is not None
     x = dev(rng.standard_normal((T, H)).astype(np.float16))
