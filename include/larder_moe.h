@@ -119,7 +119,8 @@ int lmoe_gemv_gate_up(const void *x, int xdtype, const uint32_t *slots, int n_sl
 
 /* lmoe_gemv_gate_up on prepared rows: xg_prep (and xu_prep when type_u differs from type_g) [n_slots / topk][...];
  * writes h (fp32, may be NULL) and / or hprep, h's prepared rows for the down matrix's type_d without their sums
- * ([n_slots][I / 64 * 36], may be NULL; type_d Q4_0, Q4_K, or Q6_K, which takes the Q4_K order). */
+ * ([n_slots][I / 64 * 36], may be NULL; type_d Q4_0, Q4_K, Q6_K (which takes the Q4_K order) or Q8_0 (the Q4_0
+ * order)). */
 int lmoe_gemv_gate_up_prepped(const uint32_t *xg_prep, const uint32_t *xu_prep, const uint32_t *slots, int n_slots,
                               int topk, const uint8_t *wg, const uint8_t *wu, int type_g, int type_u, int n_experts,
                               int H, int I, float *h, uint32_t *hprep, int type_d, void *stream);
@@ -185,8 +186,9 @@ int lmoe_gemv_down_runs(const float *h, const uint32_t *slots, int n, int run_ro
                         int n_experts, int I, int H, void *out, int odtype, void *stream);
 
 /* lmoe_gemv_down_combine on h's prepared rows [T * k][I / 64 * 36] (has_sums 0: their half sums are derived from
- * the pairs, as lmoe_gemv_gate_up_prepped leaves them). type_d Q4_0 / Q4_K, or Q6_K on rows prepared in the Q4_K
- * order (the 35B's down: one f16 rounding of h, v_dot2 on exact (q - 32) pairs). */
+ * the pairs, as lmoe_gemv_gate_up_prepped leaves them). type_d Q4_0 / Q4_K, Q6_K on rows prepared in the Q4_K
+ * order (the 35B's down: one f16 rounding of h, v_dot2 on exact (q - 32) pairs) or Q8_0 on rows in the Q4_0 order
+ * (v_dot2 on exact int8 pairs; experts 4-byte aligned). */
 int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sums, const uint32_t *ids, const float *scores,
                                    int T, int k, const uint8_t *wd, int type_d, int n_experts, int I, int H,
                                    const float *shared, const float *gate, int gate_stride, const void *residual,

@@ -445,6 +445,101 @@ __global__ void __launch_bounds__(512)
   }
 }
 
+// The Q8_0 down on h prepared in the Q4_0 order (lmoe_moe_gate_up with a Q8_0 down; values (4 i, 4 i + 2) + 16 (s & 1)
+// of a 32-value span in dword 4 i + s for s < 2, (4 i + 1, 4 i + 3) + 16 (s & 1) for s >= 2), in k_down_q6k's shape:
+// one output row a wavefront, 8 a workgroup, up to four (expert, block) items a lane with every weight load out
+// before h is staged. A block's 34 bytes are 2-byte aligned: 9 dwords from the 4-byte aligned address at or below
+// it (with K a multiple of 64 a row holds an even number of blocks, so a row's last block starts 2 mod 4 and the
+// window ends inside the row). Each int8 q becomes the exact f16 1024 + (q + 128) through one xor and the 0x64
+// byte of v_perm, one packed subtraction of 1152 leaves q, and v_dot2 forms sum h q over the block, times d.
+constexpr int kQ8Slots = 4;
+__global__ void __launch_bounds__(512)
+    k_down_q8p(const uint32_t *hprep, const uint32_t *ids, const float *scores, int k, const uint8_t *wd,
+               int n_experts, int I, int H, size_t rbd, const float *shared, const float *gate, int gate_stride,
+               const void *residual, int rdt, void *out, int odt) {
+  extern __shared__ uint32_t hl[];  // the token's k prepared h rows, I / 64 * 36 dwords each
+  __shared__ uint32_t eid[32];
+  __shared__ float esc[32];
+  const int t = blockIdx.y;
+  const int rowd = I / 64 * 36;
+  if (threadIdx.x < k) {
+    eid[threadIdx.x] = ids[size_t(t) * k + threadIdx.x];
+    esc[threadIdx.x] = scores ? scores[size_t(t) * k + threadIdx.x] : 1.0f;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int o0 = blockIdx.x * 8 + wave;  // this wavefront's output row (past H: row H - 1 again, not stored)
+  const int o = min(o0, H - 1);
+  const int nch = I / 32, n = k * nch;
+  uint32_t qw[kQ8Slots][8];
+  float dd[kQ8Slots], sc[kQ8Slots];
+  int jj[kQ8Slots], cc[kQ8Slots];
+  int ns = kQ8Slots;
+  auto load = [&](int u0) {
+    ns = min(kQ8Slots, (n - (u0 - lane) + 63) / 64);
+#pragma unroll
+    for (int q = 0; q < kQ8Slots; ++q) {
+      if (q >= ns) break;
+      const int u = min(u0 + 64 * q, n - 1), j = u / nch, c = u - j * nch;
+      const uint32_t e = eid[j];
+      sc[q] = u0 + 64 * q < n && e < uint32_t(n_experts) ? esc[j] : 0.0f;
+      jj[q] = j;
+      cc[q] = c;
+      const uintptr_t a = reinterpret_cast<uintptr_t>(
+          wd + (size_t(e < uint32_t(n_experts) ? e : 0u) * H + o) * rbd + size_t(c) * 34);
+      const uint32_t *base = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+      const u32x4a4 v0 = *reinterpret_cast<const u32x4a4 *>(base), v1 = *reinterpret_cast<const u32x4a4 *>(base + 4);
+      const uint32_t w[9] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, base[8]};
+      const bool odd = (a & 2) != 0;  // the block starts 2 mod 4: d in the high half of w[0], qs from w[1]
+      dd[q] = float(__builtin_bit_cast(_Float16, uint16_t(odd ? w[0] >> 16 : w[0] & 0xFFFFu)));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qw[q][i] = odd ? w[i + 1] : __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+    }
+  };
+  float acc = 0.0f;
+  const h2_t k1152 = {_Float16(1152.0f), _Float16(1152.0f)};
+  auto pair = [&](uint32_t x, uint32_t sel) {  // two bytes of x ^ 0x80.. as f16 1024 + u, less 1152: the int8 q
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, x, sel)) - k1152);
+  };
+  auto compute = [&]() {
+#pragma unroll
+    for (int q = 0; q < kQ8Slots; ++q) {
+      if (q >= ns) break;
+      const int c = cc[q];
+      const uint32_t *hp = hl + jj[q] * rowd + 36 * (c >> 1) + 16 * (c & 1);
+      float sm = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // weights 4 i .. 4 i + 3 (word i) and 16 + 4 i .. (word 4 + i)
+        const uint32_t lo = qw[q][i] ^ 0x80808080u, hi = qw[q][4 + i] ^ 0x80808080u;
+        sm = dot2(pair(lo, 0x04020400u), hp[4 * i], sm);
+        sm = dot2(pair(hi, 0x04020400u), hp[4 * i + 1], sm);
+        sm = dot2(pair(lo, 0x04030401u), hp[4 * i + 2], sm);
+        sm = dot2(pair(hi, 0x04030401u), hp[4 * i + 3], sm);
+      }
+      acc = fmaf(sc[q], dd[q] * sm, acc);
+    }
+  };
+  load(lane);  // the first four items' weights go out before h is staged
+  {
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(hprep + size_t(t) * k * rowd);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(hl);
+    for (int i = threadIdx.x; i < k * rowd / 4; i += 512) dst[i] = src[i];
+  }
+  __syncthreads();
+  compute();
+  for (int u0 = lane + 64 * kQ8Slots; u0 - lane < n; u0 += 64 * kQ8Slots) {
+    load(u0);
+    compute();
+  }
+  float v = wave_sum(acc);
+  if (lane == 0 && o0 < H) {
+    const size_t oi = size_t(t) * H + o0;
+    if (shared) v += sigmoidf_(gate[size_t(t) * gate_stride]) * shared[oi];
+    if (residual) v += load_elt(residual, oi, rdt);
+    store_elt(out, oi, v, odt);
+  }
+}
+
 // One thread a 32-weight chunk: q[c][r][32 u .. 32 u + 31] of the expert at slots[c] (identity when slots is
 // null), in natural order or, with kperm, in the grouped GEMMs' K order (4-element groups 0-3, 16-19, 4-7, 20-23,
 // 8-11, 24-27, 12-15, 28-31 of every 32). Slots past the experts give zeros.
@@ -558,12 +653,18 @@ int down_any(const char *fn, const float *h, const uint32_t *ids, const float *s
   return 0;
 }
 
-// The Q6_K down + combine on prepared h rows [T k][I / 64 * 36] in the Q4_K order (lmoe_gemv_down_combine_prepped
-// with a Q6_K down matrix; the rows' sum dwords are not read).
-int down_q6k_prepped(const char *fn, const uint32_t *hprep, const uint32_t *ids, const float *scores, int T, int k,
-                     const uint8_t *wd, int n_experts, int I, int H, const float *shared, const float *gate,
-                     int gate_stride, const void *residual, int rdt, void *out, int odt, hipStream_t st) {
-  if (int rc = check_any(fn, LMOE_Q6_K, H, I, wd)) return rc;
+// The Q6_K / Q8_0 down + combine on prepared h rows [T k][I / 64 * 36] in the Q4_K / Q4_0 order
+// (lmoe_gemv_down_combine_prepped with such a down matrix; the rows' sum dwords are not read).
+int down_packed_prepped(const char *fn, int td, const uint32_t *hprep, const uint32_t *ids, const float *scores,
+                        int T, int k, const uint8_t *wd, int n_experts, int I, int H, const float *shared,
+                        const float *gate, int gate_stride, const void *residual, int rdt, void *out, int odt,
+                        hipStream_t st) {
+  LMOE_REQUIRE(td == LMOE_Q6_K || td == LMOE_Q8_0, LMOE_ETYPE, "%s: prepared h takes a Q4_0 / Q4_K / Q6_K / Q8_0 "
+               "down (got ggml type %d)", fn, td);
+  if (int rc = check_any(fn, td, H, I, wd)) return rc;
+  LMOE_REQUIRE(I % 64 == 0, LMOE_ESHAPE, "%s: width %d is not a multiple of 64", fn, I);
+  LMOE_REQUIRE(td != LMOE_Q8_0 || (reinterpret_cast<uintptr_t>(wd) & 3) == 0, LMOE_EALIGN,
+               "%s: Q8_0 experts must be 4-byte aligned here", fn);
   LMOE_REQUIRE(dtype_ok(odt) && (!residual || dtype_ok(rdt)), LMOE_EINVAL, "%s: bad dtype", fn);
   LMOE_REQUIRE(k > 0 && k <= 32 && n_experts > 0, LMOE_ESHAPE, "%s: k %d of %d experts", fn, k, n_experts);
   LMOE_REQUIRE(!shared == !gate, LMOE_EINVAL, "%s: shared and gate go together", fn);
@@ -574,6 +675,13 @@ int down_q6k_prepped(const char *fn, const uint32_t *hprep, const uint32_t *ids,
   LMOE_REQUIRE(T <= 65535, LMOE_ESHAPE, "%s: %d tokens a call is above the 65535 this kernel takes", fn, T);
   LMOE_REQUIRE(hprep && ids && out, LMOE_EINVAL, "%s: null pointer", fn);
   LMOE_REQUIRE(aligned16(hprep), LMOE_EALIGN, "%s: prepared h must be 16-byte aligned", fn);
+  if (td == LMOE_Q8_0) {
+    if (int rc = allow_lds(k_down_q8p, lds, fn)) return rc;
+    launch(k_down_q8p, dim3((H + 7) / 8, T), dim3(512), lds, st, hprep, ids, scores, k, wd, n_experts, I, H,
+           row_bytes_any(td, I), shared, gate, gate_stride, residual, rdt, out, odt);
+    LMOE_LAUNCHED(fn);
+    return 0;
+  }
   if (int rc = allow_lds(k_down_q6k<true>, lds, fn)) return rc;
   launch(k_down_q6k<true>, dim3((H + 7) / 8, T), dim3(512), lds, st, static_cast<const void *>(hprep), ids, scores,
          k, wd, n_experts, I, H, row_bytes_any(LMOE_Q6_K, I), shared, gate, gate_stride, residual, rdt, out, odt);

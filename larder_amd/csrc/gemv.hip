@@ -1170,9 +1170,11 @@ static int check_matrix(const char *fn, int type, int rows, int cols, const void
 }
 
 static int gate_up(const char *fn, const GateUpArgs &a_in, int type_g, int type_u, void *stream) {
-  // a Q6_K down takes h prepared in the Q4_K order (its kernel pairs the 6-bit values as the Q4_K nibble words do)
+  // a Q6_K down takes h prepared in the Q4_K order, a Q8_0 down in the Q4_0 order (their kernels pair the values as
+  // those types' nibble words do)
   GateUpArgs a = a_in;
   if (a.hprep && a.td == LMOE_Q6_K) a.td = LMOE_Q4_K;
+  if (a.hprep && a.td == LMOE_Q8_0) a.td = LMOE_Q4_0;
   LMOE_REQUIRE(a.n_slots >= 0 && a.topk > 0 && a.n_slots % (a.ks ? a.ks : a.topk) == 0, LMOE_ESHAPE,
                "%s: %d slots is not a multiple of topk %d", fn, a.n_slots, a.topk);
   LMOE_REQUIRE(a.n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
@@ -1231,9 +1233,11 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   LMOE_REQUIRE(a.n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
   LMOE_REQUIRE(!a.shared == !a.gate, LMOE_EINVAL, "%s: shared and gate go together", fn);
   if (!qtype_ok(a.type_d)) {  // a type beyond Q4_0 / Q4_K: the general chain
-    if (a.hprep && a.type_d == LMOE_Q6_K && !a.part)  // Q6_K also reads h prepared in the Q4_K order
-      return down_q6k_prepped(fn, a.hprep, a.ids, a.scores, a.T, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate,
-                              a.gate_stride, a.residual, a.rdt, a.out, a.odt, (hipStream_t)stream);
+    // Q6_K and Q8_0 also read h prepared in the Q4_K / Q4_0 order
+    if (a.hprep && (a.type_d == LMOE_Q6_K || a.type_d == LMOE_Q8_0) && !a.part)
+      return down_packed_prepped(fn, a.type_d, a.hprep, a.ids, a.scores, a.T, a.k, a.wd, a.n_experts, a.I, a.H,
+                                 a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt,
+                                 (hipStream_t)stream);
     LMOE_REQUIRE(!a.hprep, LMOE_ETYPE, "%s: ggml type %d runs on the general chain only (float32 h in)", fn,
                  a.type_d);
     LMOE_REQUIRE(a.T == 0 || aligned16(a.h), LMOE_EALIGN, "%s: h must be 16-byte aligned", fn);

@@ -100,9 +100,10 @@ int gate_up_any(const char *fn, const void *x, int xdt, const uint32_t *slots, i
 int down_any(const char *fn, const float *h, const uint32_t *ids, const float *scores, int T, int k,
              const uint8_t *wd, int td, int n_experts, int I, int H, const float *shared, const float *gate,
              int gate_stride, const void *residual, int rdt, void *out, int odt, hipStream_t st);
-int down_q6k_prepped(const char *fn, const uint32_t *hprep, const uint32_t *ids, const float *scores, int T, int k,
-                     const uint8_t *wd, int n_experts, int I, int H, const float *shared, const float *gate,
-                     int gate_stride, const void *residual, int rdt, void *out, int odt, hipStream_t st);
+int down_packed_prepped(const char *fn, int td, const uint32_t *hprep, const uint32_t *ids, const float *scores,
+                        int T, int k, const uint8_t *wd, int n_experts, int I, int H, const float *shared,
+                        const float *gate, int gate_stride, const void *residual, int rdt, void *out, int odt,
+                        hipStream_t st);
 int dequant_any(const char *fn, const uint8_t *buf, int type, int n_experts, int rows, int cols,
                 const uint32_t *slots, int n, void *q, int odt, int kperm, hipStream_t st);
 

@@ -176,13 +176,14 @@ class DecodeBuffers:
 
 def prepared_chain(layer):
     """Whether ``layer`` decodes on the prepared chain (h passed prepared from gate/up to down): every projection
-    Q4_0 / Q4_K, or a Q6_K down (the 35B's mix) under gate and up of one Q4 type in the register-resident form
-    (hidden 2048 or 4096), whose kernel reads h prepared in the Q4_K order. Other layers take decode_general."""
+    Q4_0 / Q4_K, or a Q6_K down (the 35B's mix) or a Q8_0 down under gate and up of one Q4 type in the
+    register-resident form (hidden 2048 or 4096), whose kernels read h prepared in the Q4_K / Q4_0 order. Other
+    layers take decode_general."""
     t = layer.types
     if all(x in _lib.Q4_TYPES for x in t):
         return True
-    return (t[2] == "Q6_K" and t[0] == t[1] and t[0] in _lib.Q4_TYPES and layer.H in (2048, 4096)
-            and layer.I % 2 == 0)
+    return (t[2] in ("Q6_K", "Q8_0") and t[0] == t[1] and t[0] in _lib.Q4_TYPES and layer.H in (2048, 4096)
+            and layer.I % 64 == 0)
 
 
 def decode_general(layer, x, bufs, out, residual=None, logits=None):

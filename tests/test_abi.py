@@ -50,7 +50,8 @@ def test_refusals_without_a_gpu(built_lib):
     assert rc == _lib.ESHAPE and b"256" in L.lmoe_error()
     rc = L.lmoe_gemv_gate_up(p, _lib.F16, p, 8, 8, ctypes.c_void_p(18), p, 13, 13, 128, 2048, 768, p, None)
     assert rc == _lib.EALIGN and b"16-byte" in L.lmoe_error()
-    rc = L.lmoe_gemv_down_combine_prepped(p, 0, p, p, 1, 8, p, 8, 128, 768, 2048, None, None, 0, None, 0, p,
+    # prepared h feeds Q4_0 / Q4_K / Q6_K / Q8_0 downs only: a Q5_K down (13) is refused before any launch
+    rc = L.lmoe_gemv_down_combine_prepped(p, 0, p, p, 1, 8, p, 13, 128, 768, 2048, None, None, 0, None, 0, p,
                                           _lib.F16, None)
     assert rc == _lib.ETYPE and b"general chain" in L.lmoe_error()
     rc = L.lmoe_dequant_gemm_f16(p, 9, 4, 16, 64, p, None)

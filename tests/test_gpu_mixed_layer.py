@@ -1,8 +1,8 @@
 """GPU parity of the decode layer (larder_amd.layer.decode, DecodeStack) on layers with a projection beyond
 Q4_0 / Q4_K, the route every block type takes in the reference (gguf_experts.py:600-653 over stream_fast.py:4352-4377):
-the 35B's Q4_K / Q4_K / Q6_K mix (the prepared chain: gate/up on the register-resident kernel writing h in the Q4_K
-order, the Q6_K down reading it), a Q8_0 down with an unfolded shared expert (fp32 h, the general down), all-Q6_K
-and Q8_0 gate/up layers (the general gate/up), and given logits.
+the 35B's Q4_K / Q4_K / Q6_K mix and a Q8_0 down (the prepared chain: gate/up on the register-resident kernel
+writing h in the Q4_K / Q4_0 order, the Q6_K / Q8_0 down reading it), a Q5_K down (fp32 h, the general down),
+all-Q6_K and Q8_0 gate/up layers (the general gate/up), and given logits.
 Routing is pinned from x (the router GEMV's fixed order restated in the oracle, bit for bit) and the outputs are
 held to the north star's 2e-3 relative L2 against the fp32 dequant-then-matmul oracle."""
 import numpy as np
@@ -53,8 +53,12 @@ CASES = [
     (("Q4_K", "Q4_K", "Q6_K"), 2048, 768, 16, 4, True, 0),
     (("Q4_K", "Q4_K", "Q6_K"), 2048, 512, 12, 4, True, 512),
     (("Q4_K", "Q4_K", "Q6_K"), 4096, 256, 8, 2, False, 512),
-    # a Q8_0 down with a shared expert that does not fold (1024 is not a multiple of 768)
+    # a Q8_0 down (h prepared in the Q4_0 order) with a shared expert that does not fold (1024 is not a multiple of
+    # 768), and with one that folds
     (("Q4_0", "Q4_0", "Q8_0"), 2048, 768, 12, 4, False, 1024),
+    (("Q4_0", "Q4_0", "Q8_0"), 4096, 512, 10, 3, True, 1024),
+    # a Q5_K down under Q4_K gate/up: fp32 h (lmoe_moe_gate_up_h), the general down
+    (("Q4_K", "Q4_K", "Q5_K"), 2048, 512, 12, 4, True, 0),
     # gate/up beyond Q4 (the general gate/up from raw x), down Q6_K or Q4_0
     (("Q6_K", "Q6_K", "Q6_K"), 1024, 512, 8, 2, True, 0),
     (("Q8_0", "Q8_0", "Q4_0"), 2048, 768, 10, 3, True, 0),
@@ -68,8 +72,10 @@ def test_decode_general_layer_vs_oracle(types, H, I, E, k, norm, Is, T):
     from larder_amd import layer as lay
     rng = np.random.default_rng(H + I + E + T + len(types[2]))
     L = make_layer(rng, types, H, I, E, k, norm, Is)
-    # a Q6_K down under one Q4 gate/up type stays on the prepared chain (h in the Q4_K order); the rest go general
-    assert lay.prepared_chain(L) == (types[2] == "Q6_K" and types[0] == types[1] and types[0] in ("Q4_0", "Q4_K"))
+    # a Q6_K / Q8_0 down under one Q4 gate/up type stays on the prepared chain (h in the Q4_K / Q4_0 order); the
+    # rest go general
+    assert lay.prepared_chain(L) == (types[2] in ("Q6_K", "Q8_0") and types[0] == types[1]
+                                     and types[0] in ("Q4_0", "Q4_K"))
     if Is and Is % I == 0:
         assert L.folded is not None
     x = dev(rng.standard_normal((T, H)).astype(np.float16))
