@@ -230,7 +230,9 @@ __global__ void __launch_bounds__(256) k_gate_up_any(const void *x, int xdt, con
 // The token's k experts x I / 32 chunks are one list of (expert j, chunk c) items, item u = j (I / 32) + c; lane
 // takes u = lane, lane + 64, ... two a pass, so that at decode width (k 8, I 768: 192 items) every lane has work and
 // both items' loads are out before either's arithmetic (a loop over the experts kept 40 of 64 lanes idle at I 768
-// and paid one memory round trip an expert). A lane's clamped repeat of the last item takes weight 0.
+// and paid one memory round trip an expert). A lane's clamped repeat of the last item takes weight 0. FLAT = false,
+// for rows of at most 64 items (the decode chain's one slot a row, k 1), keeps that loop: it needs neither the second
+// item's registers nor its pass.
 template <int T, bool FLAT>
 __device__ __forceinline__ void down_rows(const uint8_t *wd, size_t rb, int H, int I, int k, int n_experts,
                                           const uint32_t *eid, const float *esc, const float *hs, int lane,
