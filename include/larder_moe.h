@@ -194,6 +194,31 @@ int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sums, const ui
                                    const float *shared, const float *gate, int gate_stride, const void *residual,
                                    int rdtype, void *out, int odtype, void *stream);
 
+/* The decode layer's gate/up + SwiGLU and down + weighted combine (+ residual) in ONE launch: the work of
+ * lmoe_moe_gate_up_ext (m = n_shared folded shared-expert slices, 0 for none) followed by
+ * lmoe_gemv_down_combine_prepped, with the same ids [T][k + m], scores [T][k + m] and out [T][H] bit for bit. The down
+ * workgroups rank the logits themselves and request their weights at once; h passes between the two kinds of
+ * workgroup inside the launch as epoch-tagged words in the workspace. Replaces route_cuda.probs plus gguf_gate_up and
+ * gguf_down with the block's combine on decode rows (route_cuda.py:433-444; gguf_experts.py:452-526;
+ * stream_fast.py:4372-4376); the single launch has no counterpart in the reference.
+ * logits [T][ld_stride] (E routed, then the shared gate's logit when n_shared > 0), x_prep [T][H / 64 * 36] prepared
+ * for type_gu (lmoe_router_gemv / lmoe_prep_x), wg / wu [E + m][I][.] of type_gu, wd [E + m][H][.] of type_d (the
+ * same type: all three Q4_0 or all Q4_K), hprep [T (k + m)][I / 64 * 36] (NULL: not written). H 2048 or 4096, T <= 16, k <= 32, E <= 1024,
+ * (k + m) I / 64 <= 128. The workspace (lmoe_moe_fused_workspace_bytes) is zeroed once before its first use and keeps
+ * per-workgroup launch counts between calls: every call on one workspace must have the same T, k, m, H and I, and the
+ * calls must be ordered (one stream). Each wait for h is bounded (0.2 s); a launch whose wait ran out writes NaN
+ * output rows and leaves its epoch in the status word (lmoe_moe_fused_status); later launches run normally.
+ * Measured on MI355X it is slower than the two launches it replaces (cfg2: 16.2 against 14.7 us a layer: the in-grid
+ * hand-off of h costs as much as the kernel boundary), so the Python decode uses it only with LMOE_FUSED=1. */
+size_t lmoe_moe_fused_workspace_bytes(int T, int k, int n_shared, int H, int I);
+int lmoe_moe_fused(const float *logits, int ld_stride, int T, int k, int norm, const uint32_t *x_prep,
+                   const uint8_t *wg, const uint8_t *wu, const uint8_t *wd, int type_gu, int type_d, int n_experts,
+                   int H, int I, int n_shared, uint32_t *ids, float *scores, uint32_t *hprep, const void *residual,
+                   int rdtype, void *out, int odtype, void *workspace, size_t workspace_bytes, void *stream);
+/* The status word of a fused-decode workspace: 0, or the epoch of the last launch whose wait ran out. Synchronises
+ * the stream. */
+int lmoe_moe_fused_status(const void *workspace, uint32_t *status, void *stream);
+
 /* The decode chain with the router GEMV folded into its neighbours (a stack of layers: two launches a layer instead
  * of three). The router's logits are sums over 8-element items of x: lmoe_router_gemv forms each item's products as
  * one fma chain from zero and adds the chains in a fixed tree (per wavefront a balanced tree over 64 items, then the

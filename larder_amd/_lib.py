@@ -49,6 +49,10 @@ SIGNATURES = {
     "lmoe_gemv_down_combine": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_gemv_down_combine_prepped": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I,
                                             _P]),
+    "lmoe_moe_fused_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "lmoe_moe_fused": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _I, _P,
+                            _SZ, _P]),
+    "lmoe_moe_fused_status": (_I, [_P, _P, _P]),
     "lmoe_topk_and_gemm_f16": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _LL, _P, _P]),
     "lmoe_router_part": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P]),
     "lmoe_moe_gate_up_part": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P]),

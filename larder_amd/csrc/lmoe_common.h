@@ -42,6 +42,12 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   asm volatile("" : "+v"(v));
   return v;
 }
+// A float materialised as the fp32 value it is: a conversion that follows rounds that value, instead of the compiler
+// merging the multiply that produced it with the conversion (v_fma_mix*_f16: one rounding in place of two)
+__device__ __forceinline__ float opaque(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
 
 constexpr int XS = 36;  // dwords a prepared unit takes (32 pairs, 2 sums, 2 pad)
 

@@ -320,9 +320,10 @@ struct RouteArgs {
   void *scores;    // [T][k] in gdt, or nullptr
 };
 
-// x rounded to nearest even in dtype dt (the value as a float)
+// x rounded to nearest even in dtype dt (the value as a float). x is the fp32 result of the step before; opaque()
+// keeps the compiler from merging that step's multiply into the f16 conversion (one rounding in place of two)
 __device__ __forceinline__ float round_dt(float x, int dt) {
-  if (dt == LMOE_F16) return float(_Float16(x));
+  if (dt == LMOE_F16) return float(_Float16(opaque(x)));
   if (dt == LMOE_BF16) {
     uint32_t u = __float_as_uint(x);
     if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return x;  // NaN stays

@@ -133,6 +133,9 @@ def read_header(f):
                 infos.append((tname, dims, c.num("I"), c.num("Q")))
             header_end = c.at
         finally:
+            # release the view before the mmap closes: a raised error's traceback frames still hold the cursor, and
+            # an unreleased view of the map would make mmap's close raise BufferError in place of that error
+            c.buf.release()
             del c
     align = int(meta.get("general.alignment", 32))
     start = -(-header_end // align) * align

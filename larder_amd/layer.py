@@ -26,6 +26,29 @@ from ._lib import call, dcode, ptr, qcode, stream
 RANKED_ROUTER = False
 RANK_MAX_E, RANK_MAX_K = 512, 16  # the router-and-rank kernel's limits
 
+# Whether a decode layer on the prepared chain runs gate/up and down as one launch (lmoe_moe_fused: the down
+# workgroups rank the logits themselves and wait for h in the same grid) instead of two. Off unless LMOE_FUSED=1: on
+# cfg2's 48-layer graph it measured 16.2 us a layer (down's weights requested early; 20.5 requested once h is complete)
+# against 14.7 for the two launches. A workgroup's stamps put the loss in the hand-off: a device-coherent store seen by
+# a poller on another XCD takes 1.5-3 us while the weights stream, as long as the kernel boundary it replaces. Tests
+# switch it through this flag.
+FUSED = os.environ.get("LMOE_FUSED", "0") == "1"
+
+
+def fused_ok(layer, T):
+    """Whether ``layer`` at T tokens fits the one-launch gate/up + down (lmoe_moe_fused): all three projections of
+    one Q4 type, hidden 2048 or 4096, any shared expert folded in, at most 128 h units a token."""
+    L = layer
+    t = L.types
+    if not (t[0] == t[1] == t[2] and t[0] in _lib.Q4_TYPES):
+        return False
+    if L.H not in (2048, 4096) or L.I % 64 or (t[2] == "Q4_K" and L.I % 256) or L.I % 16:
+        return False
+    if L.shared is not None and L.folded is None:
+        return False
+    ks = L.k + L.n_shared
+    return 1 <= T <= 16 and ks * (L.I // 64) <= 128 and L.k <= 32 and ks <= 64 and L.E <= 1024
+
 
 class MoELayer:
     """A layer's weights (all on the GPU):
@@ -172,6 +195,21 @@ class DecodeBuffers:
             self.h32 = torch.empty((T * ks, L.I), **f32)
             if L.shared is not None and L.folded is None:
                 self.h32_s = torch.empty((T, L.Is), **f32)
+        # the one-launch gate/up + down's workspace (status, per-workgroup launch counts, epoch-tagged h words),
+        # zeroed once; its grid is this buffer's T and the layer shape, which every call over it keeps
+        self.fused_ws = None
+        if fused_ok(L, T):
+            n = _lib.lib().lmoe_moe_fused_workspace_bytes(T, L.k, L.n_shared, L.H, L.I)
+            self.fused_ws = torch.zeros(n // 4, dtype=torch.int32, device=device)
+
+    def fused_status(self):
+        """0, or the epoch of the last one-launch gate/up + down whose wait for h ran out (its output rows are NaN).
+        Synchronises the current stream."""
+        if self.fused_ws is None:
+            return 0
+        v = ctypes.c_uint32(0)
+        call("lmoe_moe_fused_status", ptr(self.fused_ws), ctypes.byref(v), stream())
+        return int(v.value)
 
 
 def prepared_chain(layer):
@@ -293,6 +331,13 @@ def decode(layer, x, bufs, out, residual=None, logits=None):
     if B.xprep_u is not None:
         call("lmoe_prep_x", ptr(x), xd, T, L.H, tu, ptr(B.xprep_u), st)
         xu = B.xprep_u
+    if FUSED and not ranked and B.fused_ws is not None and T == B.T:
+        wg, wu, wd = L.folded if L.folded is not None else (L.wg, L.wu, L.wd)
+        call("lmoe_moe_fused", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(wg), ptr(wu), ptr(wd), tg,
+             td, L.E, L.H, L.I, L.n_shared, ptr(B.ids_ext), ptr(B.scores_ext), None, ptr(residual),
+             dcode(residual.dtype) if residual is not None else 0, ptr(out), dcode(out.dtype), ptr(B.fused_ws),
+             B.fused_ws.numel() * 4, st)
+        return out
     if L.folded is not None:  # the shared expert's m slices as slots k .. k + m - 1: gate/up, then down + combine
         fg, fu, fd = L.folded
         ks = L.k + L.n_shared

@@ -184,3 +184,38 @@ def test_header_values(tmp_path, version, align):
     for (name, ne, tid, raw), t in zip(exps, tensors):
         assert t["name"] == name and t["ne"] == ne and t["type"] == tid and t["nbytes"] == len(raw)
         assert body[t["offset"]:t["offset"] + len(raw)] == raw
+
+
+def test_malformed_headers_raise_value_error(tmp_path):
+    """A header cut short anywhere, or holding a metadata value type GGUF does not define, raises ValueError (not
+    the BufferError an unreleased view of the mapped file would leave behind when the map closes)."""
+    rng = np.random.default_rng(4)
+    exps = expert_tensors(rng)[:3]
+    good = tmp_path / "g.gguf"
+    write_gguf(good, KV, exps)
+    body = good.read_bytes()
+    with open(good, "rb") as f:
+        _, _, start = gp.read_header(f)
+    # every cut inside the metadata and tensor infos (the header ends at most align - 1 = 31 bytes before the data):
+    # a key length running past the end, a value cut short, ...
+    cuts = sorted(set(range(24, 64)) | set(range(24, start - 32, 37)) | {start - 40, start - 33})
+    for cut in cuts:
+        p = tmp_path / f"cut{cut}.gguf"
+        p.write_bytes(body[:cut])
+        with open(p, "rb") as f, pytest.raises(ValueError):
+            gp.read_header(f)
+    # a metadata key whose length field claims more bytes than the file holds
+    h = b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + struct.pack("<Q", 1 << 40) + b"abc"
+    (tmp_path / "long.gguf").write_bytes(h + bytes(32))
+    with open(tmp_path / "long.gguf", "rb") as f, pytest.raises(ValueError, match="ends early"):
+        gp.read_header(f)
+    # an unknown metadata value type (13), and an array of an unknown element type
+    for raw in (_s("k") + struct.pack("<I", 13) + bytes(8),
+                _s("k") + struct.pack("<IIQ", 9, 13, 2) + bytes(16)):
+        p = tmp_path / "vt.gguf"
+        p.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + raw + bytes(32))
+        with open(p, "rb") as f, pytest.raises(ValueError, match="not a GGUF type"):
+            gp.read_header(f)
+    # the reader stays usable on the good file afterwards
+    with open(good, "rb") as f:
+        assert gp.read_header(f)[2] == start
