@@ -419,6 +419,30 @@ int lmoe_router_gemm(const void *xh, int T, int H, const void *wk, int E, int n_
 int lmoe_router_gemm_topk(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws, float *logits,
                           float *gate, int k, int norm, int m, uint32_t *ids, float *scores, void *stream);
 
+/* The prefill router's picks made exact (the prefill form of route_cuda.probs on the block's gate matmul,
+ * stream_fast.py:4352-4370; the decode router's order, k_router_gemv, restated by the test oracle, fixes the bits).
+ * lmoe_router_norms: norms [E (+1)][4] float32 of the router rows wr [E][H] (and the shared gate row wsg [H], when
+ * given) in wdtype: |f16(w)|, |w|, |f16(w) - w|, |f16(w) restricted to f16 subnormals|, rounded up; once a layer.
+ * lmoe_router_refine: from the router GEMM's logits M (part: its ksplit slices [ksplit][T][ldp], or the logits
+ * [T][ldp] when ksplit == 1) and the raw x [T][H] in xdtype, each token's candidates are the experts whose M lies
+ * within a proven bound of the k-th largest (the bound covers any summation order of the matrix cores, f16 rounding
+ * of bf16 / f32 operands and flushed f16 subnormals); their logits are recomputed in the decode router's fixed order
+ * (lmoe_router_gemv's bits), and ids / scores [T][k + m] are the top-k of those (ties to the lower index; slot k + j =
+ * (E + j, sigmoid(gate logit)) when m > 0): the ids equal the decode router's on the same x, bit for bit. logits
+ * [T][E] (optional, may alias part when ksplit == 1) receive the candidates' fixed-order logits and M elsewhere; gate
+ * [T] (optional) the gate row's fixed-order logit; n_cand [T] (optional) the candidate counts. H % 8 == 0, H <= 8192,
+ * E <= 1024, k <= 32, k + m <= 64, wr / wsg / norms 16-byte aligned. No counterpart in the reference.
+ * lmoe_router_gemm_refine: lmoe_router_gemm (without its finish) then lmoe_router_refine on its slices; n_gate == 1
+ * exactly when wsg is given. */
+int lmoe_router_norms(const void *wr, const void *wsg, int wdtype, int E, int H, float *norms, void *stream);
+int lmoe_router_refine(const float *part, int ksplit, int ldp, const void *x, int xdtype, int T, int H, const void *wr,
+                       const void *wsg, int wdtype, int E, const float *norms, int k, int norm, int m, uint32_t *ids,
+                       float *scores, float *logits, float *gate, int *n_cand, void *stream);
+int lmoe_router_gemm_refine(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws, const void *x,
+                            int xdtype, const void *wr, const void *wsg, int wdtype, const float *norms, int k,
+                            int norm, int m, uint32_t *ids, float *scores, float *logits, float *gate, int *n_cand,
+                            void *stream);
+
 /* Weighted combine of rows kept in grouped (expert-sorted) order:
  *   out[t][n] = sum_j scores[t][j] * y[inv[t * k + j]][n] (+ sigmoid(gate) * shared) (+ residual)
  * y [R][H] in ydtype. Replaces the unsort plus combine of stream_fast.py:5525 and 4372-4376. */

@@ -74,6 +74,10 @@ SIGNATURES = {
     "lmoe_router_gemm_workspace_bytes": (_SZ, [_I, _I, _I]),
     "lmoe_router_gemm": (_I, [_P, _I, _I, _P, _I, _I, _P, _P, _P, _P]),
     "lmoe_router_gemm_topk": (_I, [_P, _I, _I, _P, _I, _I, _P, _P, _P, _I, _I, _I, _P, _P, _P]),
+    "lmoe_router_norms": (_I, [_P, _P, _I, _I, _I, _P, _P]),
+    "lmoe_router_refine": (_I, [_P, _I, _I, _P, _I, _I, _I, _P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "lmoe_router_gemm_refine": (_I, [_P, _I, _I, _P, _I, _I, _P, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P, _P, _P, _P,
+                                     _P, _P]),
     "lmoe_grouped_gate_up": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "lmoe_grouped_down": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_grouped_gate_up_bm": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P,

@@ -1653,6 +1653,27 @@ extern "C" int lmoe_router_gemm(const void *xh, int T, int H, const void *wk, in
                      (hipStream_t)stream);
 }
 
+extern "C" int lmoe_router_refine(const float *part, int ksplit, int ldp, const void *x, int xdtype, int T, int H,
+                                  const void *wr, const void *wsg, int wdtype, int E, const float *norms, int k,
+                                  int norm, int m, uint32_t *ids, float *scores, float *logits, float *gate,
+                                  int *n_cand, void *stream);
+
+// The router GEMM, then its picks made exact by lmoe_router_refine (refine.hip) straight from the K slices (or the
+// logits, unsplit): ids equal to the top-k of the decode router's fixed-order logits on the same x.
+extern "C" int lmoe_router_gemm_refine(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws,
+                                       const void *x, int xdtype, const void *wr, const void *wsg, int wdtype,
+                                       const float *norms, int k, int norm, int m, uint32_t *ids, float *scores,
+                                       float *logits, float *gate, int *n_cand, void *stream) {
+  const char *fn = "lmoe_router_gemm_refine";
+  LMOE_REQUIRE((n_gate == 1) == (wsg != nullptr), LMOE_EINVAL, "%s: the gate row and wsg go together", fn);
+  hipStream_t st = (hipStream_t)stream;
+  int ks = 1, ldp = 0;
+  if (int rc = router_gemm(fn, xh, T, H, wk, E, n_gate, ws, logits, gate, false, &ks, &ldp, st)) return rc;
+  if (T == 0) return 0;
+  return lmoe_router_refine(ks > 1 ? ws : logits, ks, ks > 1 ? ldp : E, x, xdtype, T, H, wr, wsg, wdtype, E, norms,
+                            k, norm, m, ids, scores, logits, gate, n_cand, stream);
+}
+
 extern "C" int lmoe_router_gemm_topk(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws,
                                      float *logits, float *gate, int k, int norm, int m, uint32_t *ids,
                                      float *scores, void *stream) {

@@ -234,6 +234,8 @@ class PrefillBuffers:
         f32 = dict(dtype=torch.float32, device=device)
         self.logits = torch.empty((T, L.E), **f32)
         self.gate = torch.empty(T, **f32) if L.shared is not None else None   # the shared expert's gate logit
+        # candidates a token the exact pick recomputed in the decode router's order (lmoe_router_gemm_refine)
+        self.n_cand = torch.zeros(T, dtype=torch.int32, device=device)
         self.rws = None
         if L.wr is not None:
             nrw = _lib.lib().lmoe_router_gemm_workspace_bytes(T, L.H, L.E + (1 if L.shared is not None else 0))
@@ -282,15 +284,14 @@ def prefill(layer, x, bufs, out, residual=None, logits=None):
         if L.wr is None:
             raise ValueError("this layer has no router weight: pass logits")
         ng = 1 if L.shared is not None else 0
-        # the router GEMM and the top-k (its split-K finish folded in); LMOE_FUSED_TOPK=0: apart
-        if (L.shared is None or B.fold) and os.environ.get("LMOE_FUSED_TOPK", "1") != "0":
-            call("lmoe_router_gemm_topk", ptr(B.xh), T, H, ptr(L.router_gemm_weight()), L.E, ng, ptr(B.rws),
-                 ptr(B.logits), ptr(B.gate) if ng else None, L.k, int(L.norm), L.n_shared if B.fold else 0,
-                 ptr(B.ids_ext), ptr(B.scores_ext), st)
-            ranked = True
-        else:
-            call("lmoe_router_gemm", ptr(B.xh), T, H, ptr(L.router_gemm_weight()), L.E, ng, ptr(B.rws),
-                 ptr(B.logits), ptr(B.gate) if ng else None, st)
+        # the router GEMM, then its picks made exact: the candidates its error bound leaves are recomputed in the
+        # decode router's fixed order, so the ids are the top-k of the decode router's logits on the same x
+        norms = L.router_norms()
+        call("lmoe_router_gemm_refine", ptr(B.xh), T, H, ptr(L.router_gemm_weight()), L.E, ng, ptr(B.rws), ptr(x),
+             dcode(x.dtype), ptr(L.wr), ptr(L._router_wsg), dcode(L.wr.dtype), ptr(norms), L.k, int(L.norm),
+             L.n_shared if B.fold else 0, ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.logits),
+             ptr(B.gate) if ng else None, ptr(B.n_cand), st)
+        ranked = True
         lg = B.logits
     else:
         if L.shared is not None:

@@ -95,6 +95,8 @@ class MoELayer:
         self.shared_stream = None
         self.folded_stream = None
         self._router_k = None
+        self._router_norms = None
+        self._router_wsg = None
 
     def router_gemm_weight(self):
         """The router weight, with the shared expert's gate row after it when there is a shared expert, as float16
@@ -112,6 +114,24 @@ class MoELayer:
                 call("lmoe_to_gemm_f16", ptr(sg), dcode(sg.dtype), self.H, ptr(w[self.E]), stream())
             self._router_k = w
         return self._router_k
+
+    def router_norms(self):
+        """float32 [E (+ 1)][4] norms of the router rows (and the shared gate row) as the prefill router's exact picks
+        need them (lmoe_router_norms: |f16(w)|, |w|, |f16(w) - w|, |f16(w) restricted to f16 subnormals|), computed
+        on the first call and kept."""
+        if self._router_norms is None:
+            if self.wr is None:
+                raise ValueError("this layer has no router weight")
+            n = self.E + (1 if self.shared is not None else 0)
+            out = torch.empty((n, 4), dtype=torch.float32, device=self.wr.device)
+            wr = self.wr.contiguous()
+            wsg = self.wsg.contiguous() if self.shared is not None else None
+            if wsg is not None and wsg.dtype != wr.dtype:
+                wsg = wsg.to(wr.dtype)
+            self._router_wsg = wsg
+            call("lmoe_router_norms", ptr(wr), ptr(wsg), dcode(wr.dtype), self.E, self.H, ptr(out), stream())
+            self._router_norms = out
+        return self._router_norms
 
     def keep_prefill_f16(self):
         """Hold the f16 K-order weights the grouped path needs for projections beyond Q4_0 / Q4_K (gate/up together,

@@ -93,12 +93,15 @@ def test_cfg5_prefill_T2048_sampled():
     out = torch.empty((T, cfg["H"]), dtype=torch.float32, device="cuda")
     grouped.prefill(L, x, B, out)
     torch.cuda.synchronize()
-    lg = host(B.logits)[:, :cfg["E"]]
+    # routing pinned from x and Wr: the oracle's fixed-order logits (the decode router's order, which the prefill's
+    # exact pick reproduces), their top-k against every token's ids
+    xs_all = host(x.float())
+    lg = moe.router_logits_gemv(xs_all, host(L.wr.float()))
     ids_all, _ = moe.router(lg, cfg["k"], cfg["norm"])
     assert (host(B.ids).astype(np.uint32) == ids_all).all()
     rng = np.random.default_rng(1)
     sample = np.sort(rng.choice(T, 24, replace=False))
-    xs = host(x.float())[sample]
+    xs = xs_all[sample]
     _, want = _oracle_subset(L, xs, lg[sample], cfg)
     got = host(out)[sample]
     assert moe.rel_l2(got, want) < BAR

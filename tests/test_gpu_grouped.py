@@ -275,9 +275,11 @@ def test_prefill_layer_cfg1_shared_expert():
     grouped.prefill(L, x, B, out)
     torch.cuda.synchronize()
     xs = host(x.float())
-    lg = host(B.logits)
-    assert moe.rel_l2(lg[:, :cfg["E"]], xs @ host(L.wr.float()).T) < 1e-5
-    ids, _, want = moe.layer(xs, lg[:, :cfg["E"]], tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"],
+    # routing pinned from x and Wr: the oracle's fixed-order logits (the decode router's order, which the prefill's
+    # exact pick reproduces), not the GPU's
+    lg = moe.router_logits_gemv(xs, host(L.wr.float()))
+    assert moe.rel_l2(host(B.logits), xs @ host(L.wr.float()).T) < 1e-5
+    ids, _, want = moe.layer(xs, lg, tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"],
                              cfg["k"], cfg["norm"], shared=tuple(host(b[0]) for b in L.shared),
                              shared_gate_w=host(L.wsg.float()))
     assert (host(B.ids).astype(np.uint32) == ids).all()
@@ -314,7 +316,8 @@ def test_prefill_folded_shared_matches_apart(cfgid, T):
     gate = host(Bf.gate)
     assert np.allclose(host(Bf.scores_ext)[:, cfg["k"]:], 1 / (1 + np.exp(-gate[:, None])), rtol=1e-5)
     assert moe.rel_l2(of, ou) < BAR
-    lg = host(Bf.logits)
+    lg = moe.router_logits_gemv(host(x.float()), host(L.wr.float()))  # routing pinned from x
+    assert (host(Bf.ids).astype(np.uint32) == moe.topk_ids(lg, cfg["k"])).all()
     _, _, want = moe.layer(host(x.float()), lg, tuple(host(b) for b in (L.wg, L.wu, L.wd)), cfg["types"], cfg["k"],
                            cfg["norm"], shared=tuple(host(b[0]) for b in L.shared), shared_gate_w=host(L.wsg.float()))
     assert moe.rel_l2(of, want) < BAR

@@ -120,3 +120,44 @@ def test_partials_chain_in_element_order():
     x, w = _one_hot_products(2048, [(0, BIG)] + [(i, 1) for i in range(8, 16)])
     part = moe.router_partials(x, w)
     assert part[0, 1, 0] == 8 and moe.router_logits_from_partials(part)[0, 0] == np.float32(2.0 ** 24 + 8)
+
+
+def _gemv_order_loops(x, w):
+    """k_router_gemv's order written out thread by thread (256 threads, items i, i + 256, ..., 8 products a step,
+    wave trees, waves left to right), for tiny shapes only: the chunked, vectorised oracle must give its bits."""
+    x = np.asarray(x, np.float32)
+    H = x.shape[-1]
+    w = np.asarray(w, np.float32).reshape(-1, H)
+    nit = H // 8
+    out = np.zeros((x.shape[0], w.shape[0]), np.float32)
+    for t in range(x.shape[0]):
+        for r in range(w.shape[0]):
+            chains = np.zeros(256, np.float32)
+            for th in range(256):
+                a = np.float32(0)
+                for it in range(th, nit, 256):
+                    for e in range(8):
+                        a = np.float32(a + np.float32(x[t, 8 * it + e] * w[r, 8 * it + e]))
+                chains[th] = a
+            wv = []
+            for q in range(4):
+                v = chains[64 * q:64 * q + 64]
+                while v.size > 1:
+                    v = (v[0::2] + v[1::2]).astype(np.float32)
+                wv.append(v[0])
+            out[t, r] = np.float32(np.float32(np.float32(wv[0] + wv[1]) + wv[2]) + wv[3])
+    return out
+
+
+def test_gemv_order_vectorised_equals_thread_loops():
+    """The chunked oracle against the thread-by-thread loops on random f16 / bf16 rows whose sums round differently
+    in different orders (values spanning 2^-8 .. 2^8), at hidden sizes with one, two and a partial second item a
+    thread."""
+    import torch
+    rng = np.random.default_rng(7)
+    for H in (2048, 2560, 4096):
+        x = (rng.standard_normal((2, H)) * np.exp2(rng.integers(-8, 9, (2, H)))).astype(np.float16)
+        w = torch.from_numpy(rng.standard_normal((3, H)).astype(np.float32) * 0.02).bfloat16().float().numpy()
+        got = moe.router_logits_gemv(x, w)
+        want = _gemv_order_loops(x, w)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), H
