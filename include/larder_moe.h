@@ -185,6 +185,35 @@ int lmoe_gemv_gate_up_runs(const void *x, int xdtype, const uint32_t *slots, int
 int lmoe_gemv_down_runs(const float *h, const uint32_t *slots, int n, int run_rows, const uint8_t *wd, int type_d,
                         int n_experts, int I, int H, void *out, int odtype, void *stream);
 
+/* The drop-in decode chain in its register-resident form (gguf_experts.gemv at one Q4 type for gate and up, a Q4
+ * down, hidden 2048 or 4096, I a multiple of 128 up to 8192). Replace gguf_experts kernels gguf_gate_up and gguf_down
+ * (gguf_experts.py:452-526) as driven by _chain (gguf_experts.py:610-629).
+ *   gate/up: h[s] = silu(x[s / topk] . wg[slots[s]]) * (x[s / topk] . wu[slots[s]]) with x raw [n_slots / topk][H] in
+ *            xdtype, prepared inside the launch (lmoe_prep_x's bits), the arithmetic of lmoe_gemv_gate_up_prepped;
+ *            h [n_slots][I] fp32 and / or hprep [n_slots][I / 64 * 36] prepared for type_d without sums (either may
+ *            be NULL);
+ *   down:    out[s] = hprep[s] . wd[slots[s]], unweighted, [n][H] in odtype; each slot's units on an aligned group of
+ *            16, 32 or 64 lanes with its own sum, so a slot's bits do not depend on the other slots of its call.
+ * Slots >= n_experts give zero rows. */
+int lmoe_gemv_chain_gate_up(const void *x, int xdtype, const uint32_t *slots, int n_slots, int topk, const uint8_t *wg,
+                            const uint8_t *wu, int type, int n_experts, int H, int I, float *h, uint32_t *hprep,
+                            int type_d, void *stream);
+int lmoe_gemv_chain_down(const uint32_t *hprep, const uint32_t *slots, int n, const uint8_t *wd, int type_d,
+                         int n_experts, int I, int H, void *out, int odtype, void *stream);
+
+/* The run kernels for that chain: per row the arithmetic of lmoe_gemv_chain_gate_up / lmoe_gemv_chain_down (the same
+ * staged rows, unit dots and cross-lane sums), so h, hprep and out are meant to be bit-equal to the chain's; the
+ * Python layer checks that once a shape before using them. Replace gguf_gate_up_runs / gguf_down_runs
+ * (gguf_cuda.py:33-152) as driven by _gemv_runs (gguf_experts.py:632-658).
+ *   gate/up: x_prep [n][H / 64 * 36] (lmoe_prep_x for type) -> h [n][I] fp32 and / or hprep [n][I / 64 * 36];
+ *   down:    hprep [n][I / 64 * 36] -> out [n][H] in odtype, unweighted.
+ * Shapes and types as the chain's. Slots >= n_experts give zero rows. */
+int lmoe_gemv_gate_up_runs_prepped(const uint32_t *x_prep, const uint32_t *slots, int n, int run_rows,
+                                   const uint8_t *wg, const uint8_t *wu, int type, int n_experts, int H, int I,
+                                   float *h, uint32_t *hprep, int type_d, void *stream);
+int lmoe_gemv_down_runs_prepped(const uint32_t *hprep, const uint32_t *slots, int n, int run_rows, const uint8_t *wd,
+                                int type_d, int n_experts, int I, int H, void *out, int odtype, void *stream);
+
 /* lmoe_gemv_down_combine on h's prepared rows [T * k][I / 64 * 36] (has_sums 0: their half sums are derived from
  * the pairs, as lmoe_gemv_gate_up_prepped leaves them). type_d Q4_0 / Q4_K, Q6_K on rows prepared in the Q4_K
  * order (the 35B's down: one f16 rounding of h, v_dot2 on exact (q - 32) pairs) or Q8_0 on rows in the Q4_0 order

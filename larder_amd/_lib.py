@@ -60,6 +60,10 @@ SIGNATURES = {
                                          _P]),
     "lmoe_gemv_gate_up_runs": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "lmoe_gemv_down_runs": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
+    "lmoe_gemv_chain_gate_up": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
+    "lmoe_gemv_chain_down": (_I, [_P, _P, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
+    "lmoe_gemv_gate_up_runs_prepped": (_I, [_P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
+    "lmoe_gemv_down_runs_prepped": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_group_workspace_bytes": (_SZ, [_I, _I]),
     "lmoe_group_rows": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "lmoe_group_rows_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),

@@ -285,7 +285,10 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // is prepared here: one workgroup barrier after the partials' first tree level, one after the logits, one after the
 // prepared row (the three share LDS with the wavefronts' stages, which are written only after the last barrier).
 // Wavefront w takes the first-level tasks (item row r of 16 items, block of 64 router rows) w, w + NW, ...
-template <int TQ, int P, int RB, int NPL, bool RANKWG, int NW = 4, bool RP = false>
+//
+// RAW (slots given, NPL = 0): x comes raw (dtype xdt) and each workgroup prepares its row in LDS with prep_dword,
+// the bits lmoe_prep_x writes, so the launch before it is saved: the drop-in chain's form.
+template <int TQ, int P, int RB, int NPL, bool RANKWG, int NW = 4, bool RP = false, bool RAW = false>
 __global__ void __launch_bounds__(64 * NW)
     k_gate_up_xr(const uint32_t *xprep, const uint32_t *slots, int topk, const uint8_t *wg, const uint8_t *wu,
                  int n_experts, int I, float *h, uint32_t *hprep, int td, const float *logits, int ld_stride,
@@ -294,6 +297,8 @@ __global__ void __launch_bounds__(64 * NW)
   static_assert(P == 32 || P == 64, "32 or 64 units a row");
   static_assert(RB % G == 0, "rows split evenly over the lane groups");
   static_assert(!RP || (NW >= 8 && P == 32 && NPL > 0 && NPL <= 4 && !RANKWG), "partials: H 2048, 8+ wavefronts");
+  static_assert(!RAW || (!RP && NPL == 0), "raw x: slots given");
+  static_assert(!RAW || NW * 2 * RB * 9 * P >= 64 * P, "the stages hold the raw row (f32 at most)");
   constexpr int C = RB * 9 * P / 4;  // 16-byte chunks of RB rows of one matrix
   constexpr int NC = (C + 63) / 64;
   constexpr int STAGE = 2 * RB * 9 * P;  // dwords a wavefront
@@ -323,7 +328,9 @@ __global__ void __launch_bounds__(64 * NW)
   // RP's LDS, over the stages: first-level sums [16][256], logits [256], the raw x row (H = 2048, <= 8 KB)
   float *red = reinterpret_cast<float *>(lds4 + XC);
   float *lgl = red + 16 * kPartRows;
-  u32x4 *xraw = reinterpret_cast<u32x4 *>(lgl + kPartRows);
+  u32x4 *xraw = RAW ? lds4 + XC : reinterpret_cast<u32x4 *>(lgl + kPartRows);
+  constexpr int XRR = RAW ? (16 * P + NT - 1) / NT : 1;  // raw 16-byte chunks a thread (f32 at most)
+  u32x4 xr4[XRR];
   static_assert(!RP || NW * STAGE >= 17 * kPartRows + 2048, "the stages hold RP's scratch");
   if (RP) {
     const int rows = n_experts + (ks > topk ? 1 : 0), nb = (rows + 63) / 64;
@@ -371,6 +378,12 @@ __global__ void __launch_bounds__(64 * NW)
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < NPL; ++j) v[j] = lgl[min(lane + 64 * j, n_experts - 1)];
+  } else if (RAW) {  // the raw row's chunks first, then the slot's expert
+    const int xch = xdt == LMOE_F32 ? 16 * P : 8 * P;
+    const u32x4 *xs4 = reinterpret_cast<const u32x4 *>(static_cast<const char *>(x) + xrow * (size_t(xch) * 16));
+#pragma unroll
+    for (int i = 0; i < XRR; ++i) xr4[i] = xs4[min(int(threadIdx.x) + NT * i, xch - 1)];
+    e = slots[s];
   } else if (RANK) {
     const float *row = logits + xrow * ld_stride;
 #pragma unroll
@@ -383,8 +396,8 @@ __global__ void __launch_bounds__(64 * NW)
     e = slots[s];
   }
   const u32x4 *xg4 = reinterpret_cast<const u32x4 *>(xprep + xrow * P * XS);
-  u32x4 xc[RP ? 1 : XPT];
-  if (!RP) {
+  u32x4 xc[RP || RAW ? 1 : XPT];
+  if (!RP && !RAW) {
 #pragma unroll
     for (int i = 0; i < XPT; ++i) xc[i] = xg4[min(int(threadIdx.x) + NT * i, XC - 1)];
   }
@@ -437,6 +450,13 @@ __global__ void __launch_bounds__(64 * NW)
   // the activation row into LDS (a thread past the end rewrites the last chunk with its own value; RP: prepared
   // here from the raw row), then the weights into the wavefront's stage, with no branch between loads and stores so
   // that no load is sunk into a conditional block behind the others' wait
+  if (RAW) {
+    const int xch = xdt == LMOE_F32 ? 16 * P : 8 * P;
+#pragma unroll
+    for (int i = 0; i < XRR; ++i)
+      if (int(threadIdx.x) + NT * i < xch) xraw[threadIdx.x + NT * i] = xr4[i];
+    __syncthreads();
+  }
   if (RP) {
     const _Float16 *xh = reinterpret_cast<const _Float16 *>(xraw);
     const uint16_t *xb = reinterpret_cast<const uint16_t *>(xraw);
@@ -448,6 +468,27 @@ __global__ void __launch_bounds__(64 * NW)
           [&](int i) { return xdt == LMOE_F16 ? float(xh[i]) : xdt == LMOE_BF16 ? bf16_to_f32(xb[i]) : xf[i]; }, pu,
           dw);
     }
+  } else if (RAW) {  // the pair dwords, then each unit's two sums and two pads (no thread mixes the two kinds)
+    const _Float16 *xh = reinterpret_cast<const _Float16 *>(xraw);
+    const uint16_t *xb = reinterpret_cast<const uint16_t *>(xraw);
+    const float *xf = reinterpret_cast<const float *>(xraw);
+    uint32_t *xd = reinterpret_cast<uint32_t *>(xl);
+    auto go = [&](auto ld) {
+      for (int idx = threadIdx.x; idx < P * 32; idx += NT) {
+        const int pu = idx >> 5, dw = idx & 31;
+        xd[pu * XS + dw] = prep_dword<TQ>(ld, pu, dw);
+      }
+      for (int idx = threadIdx.x; idx < P * 4; idx += NT) {
+        const int pu = idx >> 2, dw = 32 + (idx & 3);
+        xd[pu * XS + dw] = prep_dword<TQ>(ld, pu, dw);
+      }
+    };
+    if (xdt == LMOE_F16)
+      go([&](int i) { return float(xh[i]); });
+    else if (xdt == LMOE_BF16)
+      go([&](int i) { return bf16_to_f32(xb[i]); });
+    else
+      go([&](int i) { return xf[i]; });
   } else {
 #pragma unroll
     for (int i = 0; i < XPT; ++i) xl[min(int(threadIdx.x) + NT * i, XC - 1)] = xc[i];
@@ -1032,6 +1073,315 @@ __global__ void __launch_bounds__(64 * NW)
   }
 }
 
+// ---- run kernels on prepared rows: per row the register-resident chain's arithmetic ------------------------------
+//
+// The run kernels above follow k_gate_up / k_down_combine. These two follow the kernels the drop-in chain takes when
+// the shapes allow it: k_gate_up_xr with slots given, and k_down_xr at one slot a row, unweighted. Per row they use
+// the same staged weight rows, the same activation unit in the same lane, the same unit dots and the same cross-lane
+// sums, so h, its prepared rows and the outputs are meant to be bit-equal to that chain's; the host checks that once
+// a shape before it uses them.
+//
+// Gate/up: grid (ceil(I / 8), ceil(n / tr)), 256 threads; wavefront w of block (bx, y) takes gate and up rows
+// [(4 bx + w) 2, +2) for the prepared rows [y tr, +tr) of x, lane (g, p) unit p of row g as in k_gate_up_xr. LDS:
+// the window's prepared rows (copied as they are), its slot ids, each wavefront's 2 gate + 2 up staged rows.
+template <int TQ, int P>
+__global__ void __launch_bounds__(256)
+    k_gate_up_runs_xr(const uint32_t *xprep, const uint32_t *slots, int n, int tr, const uint8_t *wg,
+                      const uint8_t *wu, int n_experts, int I, float *h, uint32_t *hprep, int td) {
+  static_assert(P == 32 || P == 64, "32 or 64 units a row");
+  constexpr int RB = 2, G = 64 / P, RG = RB / G;
+  constexpr int C = RB * 9 * P / 4;  // 16-byte chunks of RB rows of one matrix
+  constexpr int NC = (C + 63) / 64;
+  constexpr int STAGE = 2 * RB * 9 * P;  // dwords a wavefront
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r0 = (blockIdx.x * 4 + wave) * RB;
+  const int e0 = blockIdx.y * tr, ne = min(tr, n - e0);
+  const int g = lane / P, p = lane % P;
+  extern __shared__ u32x4 lds4[];
+  u32x4 *xw = lds4;  // 9 P chunks a row
+  uint32_t *sl = reinterpret_cast<uint32_t *>(lds4 + size_t(tr) * 9 * P);
+  u32x4 *st4 = reinterpret_cast<u32x4 *>(sl + ((tr + 3) & ~3) + wave * STAGE);
+  const uint32_t *stage = reinterpret_cast<const uint32_t *>(st4);
+
+  // the first run's rows into registers (clamped, unpredicated) while the window is copied
+  const int rs = min(r0, I - RB);
+  u32x4 vg[NC], vu[NC];
+  auto fetch = [&](uint32_t e) {
+    const size_t base = (size_t(e < uint32_t(n_experts) ? e : 0u) * I + rs) * (36 * P);
+    const u32x4 *gs = reinterpret_cast<const u32x4 *>(wg + base);
+    const u32x4 *us = reinterpret_cast<const u32x4 *>(wu + base);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = min(lane + 64 * i, C - 1);
+      vg[i] = __builtin_nontemporal_load(gs + c);
+      vu[i] = __builtin_nontemporal_load(us + c);
+    }
+  };
+  fetch(slots[e0]);
+  if (int(threadIdx.x) < ne) sl[threadIdx.x] = slots[e0 + threadIdx.x];
+  {
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(xprep + size_t(e0) * P * XS);
+    for (int c = threadIdx.x; c < ne * 9 * P; c += 256) xw[c] = src[c];
+  }
+  __syncthreads();
+  if (r0 >= I) return;
+
+  const int hs = td == LMOE_Q4_K ? 32 : 16;
+  for (int r = 0; r < ne;) {
+    const uint32_t e = sl[r];
+    int r1 = r + 1;  // the run: rows [r, r1) of slot e
+    while (r1 < ne && sl[r1] == e) ++r1;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = min(lane + 64 * i, C - 1);
+      st4[c] = vg[i];
+      st4[C + c] = vu[i];
+    }
+    if (r1 < ne) fetch(sl[r1]);  // the next run's rows, in flight during this one
+    __builtin_amdgcn_wave_barrier();
+    const bool valid = e < uint32_t(n_experts);
+    for (int q = r; q < r1; ++q) {
+      const size_t row = size_t(e0 + q);
+      if (!valid) {  // no such expert: zero rows, as k_gate_up_xr writes them
+        if (lane < RB) {
+          const int nn = r0 + lane;
+          if (h) h[row * I + nn] = 0.0f;
+          if (hprep) {
+            int dw, half;
+            xslot(nn & 63, hs, &dw, &half);
+            reinterpret_cast<_Float16 *>(hprep + (row * (I / 64) + (nn >> 6)) * XS + dw)[half] = _Float16(0.0f);
+          }
+        }
+        continue;
+      }
+      const u32x4 *xu4 = xw + size_t(q) * 9 * P;
+      uint32_t xv[32];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const u32x4 v = xu4[9 * p + i];
+        xv[4 * i] = v.x;
+        xv[4 * i + 1] = v.y;
+        xv[4 * i + 2] = v.z;
+        xv[4 * i + 3] = v.w;
+      }
+      const u32x4 qs = xu4[9 * p + 8];
+      const float sx0 = __uint_as_float(qs.x), sx1 = __uint_as_float(qs.y);
+      float pg[RG], pu[RG];
+#pragma unroll
+      for (int i = 0; i < RG; ++i) {
+        const int rr = g + G * i;
+        pg[i] = row_unit_dot_r<TQ>(stage + rr * 9 * P, p, xv, sx0, sx1);
+        pu[i] = row_unit_dot_r<TQ>(stage + (RB + rr) * 9 * P, p, xv, sx0, sx1);
+      }
+#pragma unroll
+      for (int i = 0; i < RG; ++i) {
+        pg[i] = group_sum<P>(pg[i]);
+        pu[i] = group_sum<P>(pu[i]);
+      }
+      if (p == 0) {
+#pragma unroll
+        for (int i = 0; i < RG; ++i) {
+          const int nn = r0 + g + G * i;
+          const float hv = silu_mul(pg[i], pu[i]);
+          if (h) h[row * I + nn] = hv;
+          if (hprep) {
+            int dw, half;
+            xslot(nn & 63, hs, &dw, &half);
+            reinterpret_cast<_Float16 *>(hprep + (row * (I / 64) + (nn >> 6)) * XS + dw)[half] = _Float16(hv);
+          }
+        }
+      }
+    }
+    r = r1;
+  }
+}
+
+// The drop-in chain's down: every slot's unweighted output from its prepared h row (without sums, as gate/up leaves
+// them). A slot's P units sit on an aligned group of G lanes (G = 16, 32 or 64, at least P; two units a lane past 64),
+// so SPW = 64 / G slots share a wavefront and each slot's row sums are a sum over its own group only: a slot's
+// output does not depend on which slots share its wavefront, and the run kernel below repeats it bit for bit.
+template <int G>
+__device__ __forceinline__ float slot_sum(float v) {
+  static_assert(G == 16 || G == 32 || G == 64, "a group of 16, 32 or 64 lanes");
+  if (G == 64) return wave_sum(v);
+  v = sum16(v);
+  return G == 32 ? v + lane_xor16(v) : v;
+}
+
+// k_down_xr's half sums of an h unit held as 32 f16 pair dwords: dwords 0..15 / 16..31 (Q4_0), even / odd (Q4_K)
+template <int TD>
+__device__ __forceinline__ void h_unit_sums(const uint32_t *xv, float *x0, float *x1) {
+  const h2_t one2 = {_Float16(1.0f), _Float16(1.0f)};
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t d0 = TD == LMOE_Q4_K ? xv[2 * i] : xv[i];
+    const uint32_t d1 = TD == LMOE_Q4_K ? xv[2 * i + 1] : xv[16 + i];
+    a = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, d0), one2, a, false);
+    b = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, d1), one2, b, false);
+  }
+  *x0 = a;
+  *x1 = b;
+}
+
+__device__ __forceinline__ void unpack_unit(const u32x4 *q, uint32_t *xv) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const u32x4 v = q[i];
+    xv[4 * i] = v.x;
+    xv[4 * i + 1] = v.y;
+    xv[4 * i + 2] = v.z;
+    xv[4 * i + 3] = v.w;
+  }
+}
+
+// Grid (H / 8, ceil(n / SPW)), 256 threads; wavefront w of block (bx, y) takes output rows [(4 bx + w) 2, +2) of
+// slots [y SPW, +SPW). Memory order as k_down_xr's: the slot ids and h units, then the weights (their addresses need
+// only the ids), the half sums while they are in flight; no load is predicated (clamped indices; expert 0 stands in
+// for an id past the experts, whose output is written as 0).
+template <int TD, int G, int NU, int NCW>
+__global__ void __launch_bounds__(256)
+    k_down_slots(const uint32_t *hprep, const uint32_t *slots, int n, const uint8_t *wd, int n_experts, int I, int H,
+                 void *out, int odt) {
+  constexpr int RB = 2, SPW = 64 / G;
+  static_assert(NU == 1 || G == 64, "two units a lane only at one slot a wavefront");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int P = I / 64, CJ = RB * 9 * P / 4, CW = SPW * CJ;
+  const int n0 = (blockIdx.x * 4 + wave) * RB;
+  const int s0 = blockIdx.y * SPW, js = lane / G, p = lane % G;
+  extern __shared__ u32x4 lds4[];
+  u32x4 *st4 = lds4 + wave * CW;
+  const uint32_t *stage = reinterpret_cast<const uint32_t *>(st4);
+
+  const uint32_t id_l = slots[min(s0 + min(lane, SPW - 1), n - 1)];  // lane j < SPW: slot s0 + j's id
+  const u32x4 *hb = reinterpret_cast<const u32x4 *>(hprep + size_t(min(s0 + js, n - 1)) * P * XS);
+  u32x4 hq[NU][9];
+#pragma unroll
+  for (int a = 0; a < NU; ++a) {
+    const int u = min(p + 64 * a, P - 1);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) hq[a][i] = hb[u * 9 + i];
+  }
+  asm volatile("" ::: "memory");
+  const size_t rowb = size_t(36) * P, nsafe = size_t(min(n0, H - RB));
+  u32x4 w[NCW];
+#pragma unroll
+  for (int i = 0; i < NCW; ++i) {
+    const int c = min(lane + 64 * i, CW - 1);
+    const int j = c / CJ, cc = c - j * CJ;
+    uint32_t e = uint32_t(__shfl(int(id_l), j, 64));
+    e = e < uint32_t(n_experts) ? e : 0u;
+    w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wd + (size_t(e) * H + nsafe) * rowb) + cc);
+  }
+  asm volatile("" ::: "memory");
+  uint32_t xv[NU][32];
+  float fa[NU], hs0[NU], hs1[NU];
+  int uc[NU];
+#pragma unroll
+  for (int a = 0; a < NU; ++a) {
+    const int u = p + 64 * a;
+    uc[a] = min(u, P - 1);
+    fa[a] = u < P ? 1.0f : 0.0f;
+    unpack_unit(hq[a], xv[a]);
+    h_unit_sums<TD>(xv[a], &hs0[a], &hs1[a]);
+  }
+#pragma unroll
+  for (int i = 0; i < NCW; ++i) st4[min(lane + 64 * i, CW - 1)] = w[i];
+  __builtin_amdgcn_wave_barrier();
+  float acc[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int a = 0; a < NU; ++a)
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      acc[r] = fmaf(fa[a], row_unit_dot_r<TD>(stage + (js * RB + r) * 9 * P, uc[a], xv[a], hs0[a], hs1[a]), acc[r]);
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r] = slot_sum<G>(acc[r]);
+  const uint32_t e = uint32_t(__shfl(int(id_l), js, 64));
+  if (p < RB && s0 + js < n)
+    store_elt(out, size_t(s0 + js) * H + n0 + p, e < uint32_t(n_experts) ? (p == 0 ? acc[0] : acc[1]) : 0.0f, odt);
+}
+
+// Down of the same windows, unweighted: grid (H / 8, ceil(n / tr)), 256 threads; wavefront w of block (bx, y) takes
+// output rows [(4 bx + w) 2, +2) for the prepared h rows [y tr, +tr), SPW rows of a run a pass on k_down_slots'
+// lanes and arithmetic (the same staged rows, unit dots, weights and group sums). LDS: the window's h rows, its slot
+// ids, each wavefront's 2 staged rows.
+template <int TD, int G, int NU, int NCW>
+__global__ void __launch_bounds__(256)
+    k_down_runs_xr(const uint32_t *hprep, const uint32_t *slots, int n, int tr, const uint8_t *wd, int n_experts,
+                   int I, int H, void *out, int odt) {
+  constexpr int RB = 2, SPW = 64 / G;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int P = I / 64, CW = RB * 9 * P / 4;
+  const int n0 = (blockIdx.x * 4 + wave) * RB;
+  const int e0 = blockIdx.y * tr, ne = min(tr, n - e0);
+  const int js = lane / G, p = lane % G;
+  extern __shared__ u32x4 lds4[];
+  u32x4 *hw = lds4;  // 9 P chunks a row
+  uint32_t *sl = reinterpret_cast<uint32_t *>(lds4 + size_t(tr) * 9 * P);
+  u32x4 *st4 = reinterpret_cast<u32x4 *>(sl + ((tr + 3) & ~3)) + wave * CW;
+  const uint32_t *stage = reinterpret_cast<const uint32_t *>(st4);
+
+  const size_t rowb = size_t(36) * P, nsafe = size_t(min(n0, H - RB));
+  u32x4 w[NCW];
+  auto fetch = [&](uint32_t e) {
+    const u32x4 *src =
+        reinterpret_cast<const u32x4 *>(wd + (size_t(e < uint32_t(n_experts) ? e : 0u) * H + nsafe) * rowb);
+#pragma unroll
+    for (int i = 0; i < NCW; ++i) w[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, CW - 1));
+  };
+  fetch(slots[e0]);
+  if (int(threadIdx.x) < ne) sl[threadIdx.x] = slots[e0 + threadIdx.x];
+  {
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(hprep + size_t(e0) * P * XS);
+    for (int c = threadIdx.x; c < ne * 9 * P; c += 256) hw[c] = src[c];
+  }
+  __syncthreads();
+  if (n0 >= H) return;
+
+  for (int r = 0; r < ne;) {
+    const uint32_t e = sl[r];
+    int r1 = r + 1;
+    while (r1 < ne && sl[r1] == e) ++r1;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < NCW; ++i) st4[min(lane + 64 * i, CW - 1)] = w[i];
+    if (r1 < ne) fetch(sl[r1]);
+    __builtin_amdgcn_wave_barrier();
+    const bool valid = e < uint32_t(n_experts);
+    for (int q0 = r; q0 < r1; q0 += SPW) {
+      const bool mine = q0 + js < r1;
+      const size_t o = size_t(e0 + q0 + js) * H + n0 + p;
+      if (!valid) {  // k_down_slots writes 0 for such an id
+        if (p < RB && mine) store_elt(out, o, 0.0f, odt);
+        continue;
+      }
+      const u32x4 *hb = hw + size_t(min(q0 + js, r1 - 1)) * 9 * P;
+      float acc[RB];
+#pragma unroll
+      for (int rr = 0; rr < RB; ++rr) acc[rr] = 0.0f;
+#pragma unroll
+      for (int a = 0; a < NU; ++a) {
+        const int u = p + 64 * a, uc = min(u, P - 1);
+        const float fa = u < P ? 1.0f : 0.0f;
+        uint32_t xv[32];
+        unpack_unit(hb + uc * 9, xv);
+        float x0, x1;
+        h_unit_sums<TD>(xv, &x0, &x1);
+#pragma unroll
+        for (int rr = 0; rr < RB; ++rr)
+          acc[rr] = fmaf(fa, row_unit_dot_r<TD>(stage + rr * 9 * P, uc, xv, x0, x1), acc[rr]);
+      }
+#pragma unroll
+      for (int rr = 0; rr < RB; ++rr) acc[rr] = slot_sum<G>(acc[rr]);
+      if (p < RB && mine) store_elt(out, o, p == 0 ? acc[0] : acc[1], odt);
+    }
+    r = r1;
+  }
+}
+
 struct GateUpArgs {
   const uint32_t *xg_prep, *xu_prep;
   const void *x;
@@ -1087,6 +1437,17 @@ static int launch_gate_up_xr(const GateUpArgs &a, hipStream_t st) {
          a.n_experts, a.I, a.h, a.hprep, a.td, a.logits, a.ld_stride, a.norm, a.ids_out, a.scores_out,
          a.ks ? a.ks : a.topk, nullptr, nullptr, 0);
   LMOE_LAUNCHED("lmoe_gemv_gate_up");
+  return 0;
+}
+
+// The drop-in chain's gate/up: raw x prepared in each workgroup, slots given (k_gate_up_xr's RAW form).
+template <int TQ, int P>
+static int launch_gate_up_xr_raw(const GateUpArgs &a, hipStream_t st) {
+  constexpr int RB = 2;
+  const dim3 grid((a.I + 4 * RB - 1) / (4 * RB), a.n_slots);
+  launch(k_gate_up_xr<TQ, P, RB, 0, false, 4, false, true>, grid, dim3(256), 0, st, nullptr, a.slots, a.topk, a.wg,
+         a.wu, a.n_experts, a.I, a.h, a.hprep, a.td, nullptr, 0, 0, nullptr, nullptr, a.topk, nullptr, a.x, a.xdt);
+  LMOE_LAUNCHED("lmoe_gemv_chain_gate_up");
   return 0;
 }
 
@@ -1474,6 +1835,148 @@ static int down_runs(const float *h, const uint32_t *slots, int n, int tr_want, 
   return RB == 2 ? by_nc(TK(), R2()) : by_nc(TK(), R4());
 }
 
+static int gate_up_runs_prepped(const uint32_t *xprep, const uint32_t *slots, int n, int tr_want, const uint8_t *wg,
+                                const uint8_t *wu, int type, int n_experts, int H, int I, float *h, uint32_t *hprep,
+                                int td, hipStream_t st) {
+  const char *fn = "lmoe_gemv_gate_up_runs_prepped";
+  LMOE_REQUIRE(qtype_ok(type), LMOE_ETYPE, "%s: the run kernels take Q4_0 / Q4_K (got %d)", fn, type);
+  LMOE_REQUIRE(n_experts > 0 && n >= 0 && tr_want >= 1, LMOE_ESHAPE, "%s: %d experts, %d rows, window %d", fn,
+               n_experts, n, tr_want);
+  LMOE_REQUIRE((H == 2048 || H == 4096) && I % 2 == 0, LMOE_ESHAPE,
+               "%s: takes the register-resident form, hidden 2048 or 4096 and an even width (got %d, %d)", fn, H, I);
+  if (int rc = check_matrix(fn, type, I, H, wg)) return rc;
+  if (int rc = check_matrix(fn, type, I, H, wu)) return rc;
+  if (hprep && td == LMOE_Q6_K) td = LMOE_Q4_K;  // the orders lmoe_gemv_gate_up_prepped writes for these downs
+  if (hprep && td == LMOE_Q8_0) td = LMOE_Q4_0;
+  LMOE_REQUIRE(!hprep || (qtype_ok(td) && I % 64 == 0 && (td != LMOE_Q4_K || I % 256 == 0)), LMOE_ESHAPE,
+               "%s: width %d cannot be prepared for ggml type %d", fn, I, td);
+  LMOE_REQUIRE(h || hprep, LMOE_EINVAL, "%s: neither h nor its prepared rows asked for", fn);
+  if (n == 0) return 0;
+  LMOE_REQUIRE(xprep && slots && aligned16(xprep), LMOE_EALIGN, "%s: null or unaligned pointer", fn);
+  const int P = H / 64;
+  const size_t prow = size_t(P) * XS, stage = size_t(4) * 2 * 2 * 9 * P;
+  const int tr = runs_window(tr_want, 4 * (stage + 64), 4 * prow, 80 * 1024);
+  const size_t lds = 4 * (tr * prow + ((tr + 3) & ~3) + stage);
+  const dim3 grid((I + 7) / 8, (n + tr - 1) / tr);
+  auto go = [&](auto kern) {
+    if (int rc = allow_lds(kern, lds, fn)) return rc;
+    launch(kern, grid, dim3(256), lds, st, xprep, slots, n, tr, wg, wu, n_experts, I, h, hprep, td);
+    LMOE_LAUNCHED(fn);
+    return 0;
+  };
+  if (type == LMOE_Q4_0) return P == 32 ? go(k_gate_up_runs_xr<LMOE_Q4_0, 32>) : go(k_gate_up_runs_xr<LMOE_Q4_0, 64>);
+  return P == 32 ? go(k_gate_up_runs_xr<LMOE_Q4_K, 32>) : go(k_gate_up_runs_xr<LMOE_Q4_K, 64>);
+}
+
+// Lanes a slot's units take in k_down_slots / k_down_runs_xr (a power of two, 16 at least, 64 at most) and units a
+// lane (2 past 64 units)
+static int slot_group(int P) { return P <= 16 ? 16 : P <= 32 ? 32 : 64; }
+
+static int check_down_slots(const char *fn, int td, int n_experts, int I, int H, const uint8_t *wd, int odt) {
+  LMOE_REQUIRE(dtype_ok(odt), LMOE_EINVAL, "%s: bad dtype", fn);
+  LMOE_REQUIRE(qtype_ok(td), LMOE_ETYPE, "%s: takes Q4_0 / Q4_K (got %d)", fn, td);
+  LMOE_REQUIRE(n_experts > 0, LMOE_ESHAPE, "%s: no experts", fn);
+  if (int rc = check_matrix(fn, td, H, I, wd)) return rc;
+  const int P = I / 64;
+  LMOE_REQUIRE(P % 2 == 0 && P <= 128 && H % 8 == 0, LMOE_ESHAPE,
+               "%s: takes a width that is a multiple of 128 up to 8192 and a hidden size that is a multiple of 8 "
+               "(got %d, %d)", fn, I, H);
+  return 0;
+}
+
+static int down_slots(const uint32_t *hprep, const uint32_t *slots, int n, const uint8_t *wd, int td, int n_experts,
+                      int I, int H, void *out, int odt, hipStream_t st) {
+  const char *fn = "lmoe_gemv_chain_down";
+  if (int rc = check_down_slots(fn, td, n_experts, I, H, wd, odt)) return rc;
+  if (n == 0) return 0;
+  LMOE_REQUIRE(hprep && slots && out && aligned16(hprep), LMOE_EALIGN, "%s: null or unaligned pointer", fn);
+  const int P = I / 64, G = slot_group(P), spw = 64 / G, cw = spw * 9 * P / 2, ncw = (cw + 63) / 64;
+  const size_t lds = size_t(16) * 4 * cw;
+  const dim3 grid(H / 8, (n + spw - 1) / spw);
+  auto go = [&](auto kern) {
+    if (int rc = allow_lds(kern, lds, fn)) return rc;
+    launch(kern, grid, dim3(256), lds, st, hprep, slots, n, wd, n_experts, I, H, out, odt);
+    LMOE_LAUNCHED(fn);
+    return 0;
+  };
+  auto by_nc = [&](auto td_, auto g_, auto nu_) {
+    constexpr int D = decltype(td_)::value, GG = decltype(g_)::value, N = decltype(nu_)::value;
+    if (ncw <= 2) return go(k_down_slots<D, GG, N, 2>);
+    if (ncw <= 3) return go(k_down_slots<D, GG, N, 3>);
+    if (ncw <= 4) return go(k_down_slots<D, GG, N, 4>);
+    if (ncw <= 5) return go(k_down_slots<D, GG, N, 5>);
+    return go(k_down_slots<D, GG, N, 9>);
+  };
+  auto by_g = [&](auto td_) {
+    if (G == 16) return by_nc(td_, std::integral_constant<int, 16>(), std::integral_constant<int, 1>());
+    if (G == 32) return by_nc(td_, std::integral_constant<int, 32>(), std::integral_constant<int, 1>());
+    if (P <= 64) return by_nc(td_, std::integral_constant<int, 64>(), std::integral_constant<int, 1>());
+    return by_nc(td_, std::integral_constant<int, 64>(), std::integral_constant<int, 2>());
+  };
+  return td == LMOE_Q4_0 ? by_g(std::integral_constant<int, LMOE_Q4_0>())
+                         : by_g(std::integral_constant<int, LMOE_Q4_K>());
+}
+
+static int down_runs_prepped(const uint32_t *hprep, const uint32_t *slots, int n, int tr_want, const uint8_t *wd,
+                             int td, int n_experts, int I, int H, void *out, int odt, hipStream_t st) {
+  const char *fn = "lmoe_gemv_down_runs_prepped";
+  LMOE_REQUIRE(tr_want >= 1 && n >= 0, LMOE_ESHAPE, "%s: %d rows, window %d", fn, n, tr_want);
+  if (int rc = check_down_slots(fn, td, n_experts, I, H, wd, odt)) return rc;
+  if (n == 0) return 0;
+  LMOE_REQUIRE(hprep && slots && out && aligned16(hprep), LMOE_EALIGN, "%s: null or unaligned pointer", fn);
+  const int P = I / 64, G = slot_group(P), cw = 9 * P / 2, ncw = (cw + 63) / 64;
+  const size_t prow = size_t(P) * XS, stage = size_t(4) * 4 * cw;
+  const int tr = runs_window(tr_want, 4 * (stage + 64), 4 * prow, 80 * 1024);
+  const size_t lds = 4 * (tr * prow + ((tr + 3) & ~3) + stage);
+  const dim3 grid(H / 8, (n + tr - 1) / tr);
+  auto go = [&](auto kern) {
+    if (int rc = allow_lds(kern, lds, fn)) return rc;
+    launch(kern, grid, dim3(256), lds, st, hprep, slots, n, tr, wd, n_experts, I, H, out, odt);
+    LMOE_LAUNCHED(fn);
+    return 0;
+  };
+  auto by_nc = [&](auto td_, auto g_, auto nu_) {
+    constexpr int D = decltype(td_)::value, GG = decltype(g_)::value, N = decltype(nu_)::value;
+    if (ncw <= 1) return go(k_down_runs_xr<D, GG, N, 1>);
+    if (ncw <= 2) return go(k_down_runs_xr<D, GG, N, 2>);
+    if (ncw <= 3) return go(k_down_runs_xr<D, GG, N, 3>);
+    if (ncw <= 5) return go(k_down_runs_xr<D, GG, N, 5>);
+    return go(k_down_runs_xr<D, GG, N, 9>);
+  };
+  auto by_g = [&](auto td_) {
+    if (G == 16) return by_nc(td_, std::integral_constant<int, 16>(), std::integral_constant<int, 1>());
+    if (G == 32) return by_nc(td_, std::integral_constant<int, 32>(), std::integral_constant<int, 1>());
+    if (P <= 64) return by_nc(td_, std::integral_constant<int, 64>(), std::integral_constant<int, 1>());
+    return by_nc(td_, std::integral_constant<int, 64>(), std::integral_constant<int, 2>());
+  };
+  return td == LMOE_Q4_0 ? by_g(std::integral_constant<int, LMOE_Q4_0>())
+                         : by_g(std::integral_constant<int, LMOE_Q4_K>());
+}
+
+static int chain_gate_up(const void *x, int xdt, const uint32_t *slots, int n, int topk, const uint8_t *wg,
+                         const uint8_t *wu, int type, int n_experts, int H, int I, float *h, uint32_t *hprep, int td,
+                         hipStream_t st) {
+  const char *fn = "lmoe_gemv_chain_gate_up";
+  LMOE_REQUIRE(dtype_ok(xdt), LMOE_EINVAL, "%s: x dtype %d is not F32, F16 or BF16", fn, xdt);
+  LMOE_REQUIRE(qtype_ok(type), LMOE_ETYPE, "%s: takes Q4_0 / Q4_K (got %d)", fn, type);
+  LMOE_REQUIRE(n_experts > 0 && n >= 0 && topk > 0 && n % topk == 0, LMOE_ESHAPE,
+               "%s: %d experts, %d slots, topk %d", fn, n_experts, n, topk);
+  LMOE_REQUIRE((H == 2048 || H == 4096) && I % 2 == 0, LMOE_ESHAPE,
+               "%s: takes hidden 2048 or 4096 and an even width (got %d, %d)", fn, H, I);
+  if (int rc = check_matrix(fn, type, I, H, wg)) return rc;
+  if (int rc = check_matrix(fn, type, I, H, wu)) return rc;
+  LMOE_REQUIRE(!hprep || (qtype_ok(td) && I % 64 == 0 && (td != LMOE_Q4_K || I % 256 == 0)), LMOE_ESHAPE,
+               "%s: width %d cannot be prepared for ggml type %d", fn, I, td);
+  LMOE_REQUIRE(h || hprep, LMOE_EINVAL, "%s: neither h nor its prepared rows asked for", fn);
+  if (n == 0) return 0;
+  LMOE_REQUIRE(x && slots && aligned16(x), LMOE_EALIGN, "%s: null or unaligned pointer", fn);
+  GateUpArgs a{nullptr, nullptr, x, xdt, slots, n, topk, wg, wu, n_experts, H, I, h, hprep, td, nullptr, 0, 0,
+               nullptr, nullptr};
+  if (type == LMOE_Q4_0) return H == 2048 ? launch_gate_up_xr_raw<LMOE_Q4_0, 32>(a, st)
+                                          : launch_gate_up_xr_raw<LMOE_Q4_0, 64>(a, st);
+  return H == 2048 ? launch_gate_up_xr_raw<LMOE_Q4_K, 32>(a, st) : launch_gate_up_xr_raw<LMOE_Q4_K, 64>(a, st);
+}
+
 }  // namespace lmoe
 
 using namespace lmoe;
@@ -1621,4 +2124,29 @@ extern "C" int lmoe_gemv_gate_up_runs(const void *x, int xdtype, const uint32_t 
 extern "C" int lmoe_gemv_down_runs(const float *h, const uint32_t *slots, int n, int run_rows, const uint8_t *wd,
                                    int type_d, int n_experts, int I, int H, void *out, int odtype, void *stream) {
   return down_runs(h, slots, n, run_rows, wd, type_d, n_experts, I, H, out, odtype, (hipStream_t)stream);
+}
+
+extern "C" int lmoe_gemv_gate_up_runs_prepped(const uint32_t *x_prep, const uint32_t *slots, int n, int run_rows,
+                                              const uint8_t *wg, const uint8_t *wu, int type, int n_experts, int H,
+                                              int I, float *h, uint32_t *hprep, int type_d, void *stream) {
+  return gate_up_runs_prepped(x_prep, slots, n, run_rows, wg, wu, type, n_experts, H, I, h, hprep, type_d,
+                              (hipStream_t)stream);
+}
+
+extern "C" int lmoe_gemv_down_runs_prepped(const uint32_t *hprep, const uint32_t *slots, int n, int run_rows,
+                                           const uint8_t *wd, int type_d, int n_experts, int I, int H, void *out,
+                                           int odtype, void *stream) {
+  return down_runs_prepped(hprep, slots, n, run_rows, wd, type_d, n_experts, I, H, out, odtype, (hipStream_t)stream);
+}
+
+extern "C" int lmoe_gemv_chain_gate_up(const void *x, int xdtype, const uint32_t *slots, int n_slots, int topk,
+                                       const uint8_t *wg, const uint8_t *wu, int type, int n_experts, int H, int I,
+                                       float *h, uint32_t *hprep, int type_d, void *stream) {
+  return chain_gate_up(x, xdtype, slots, n_slots, topk, wg, wu, type, n_experts, H, I, h, hprep, type_d,
+                       (hipStream_t)stream);
+}
+
+extern "C" int lmoe_gemv_chain_down(const uint32_t *hprep, const uint32_t *slots, int n, const uint8_t *wd,
+                                    int type_d, int n_experts, int I, int H, void *out, int odtype, void *stream) {
+  return down_slots(hprep, slots, n, wd, type_d, n_experts, I, H, out, odtype, (hipStream_t)stream);
 }

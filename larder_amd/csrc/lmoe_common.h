@@ -725,9 +725,13 @@ __device__ __forceinline__ uint32_t prep_dword(Ld ld, int p, int dw) {
     const h2_t v = {_Float16(ld(64 * p + xelem(dw, 0, H))), _Float16(ld(64 * p + xelem(dw, 1, H)))};
     return __builtin_bit_cast(uint32_t, v);
   }
-  if (dw < 34) {
+  if (dw < 34) {  // the 32 values read first, then added in element order
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = float(_Float16(ld(64 * p + 32 * (dw - 32) + j)));
     float s = 0.0f;
-    for (int j = 0; j < 32; ++j) s += float(_Float16(ld(64 * p + 32 * (dw - 32) + j)));
+#pragma unroll
+    for (int j = 0; j < 32; ++j) s += v[j];
     return __builtin_bit_cast(uint32_t, s);
   }
   return 0u;

@@ -709,9 +709,9 @@ extern "C" int lmoe_prep_x(const void *x, int xdtype, int rows, int H, int qtype
   LMOE_REQUIRE(x && xprep, LMOE_EINVAL, "%s: null pointer", fn);
   const dim3 grid(((H / 64) * XS + 255) / 256, rows);
   if (qtype == LMOE_Q4_K)
-    hipLaunchKernelGGL(k_prep_x<LMOE_Q4_K>, grid, dim3(256), 0, (hipStream_t)stream, x, xdtype, H, xprep);
+    launch(k_prep_x<LMOE_Q4_K>, grid, dim3(256), 0, (hipStream_t)stream, x, xdtype, H, xprep);
   else
-    hipLaunchKernelGGL(k_prep_x<LMOE_Q4_0>, grid, dim3(256), 0, (hipStream_t)stream, x, xdtype, H, xprep);
+    launch(k_prep_x<LMOE_Q4_0>, grid, dim3(256), 0, (hipStream_t)stream, x, xdtype, H, xprep);
   LMOE_LAUNCHED(fn);
   return 0;
 }

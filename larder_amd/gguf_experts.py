@@ -65,16 +65,43 @@ def dequant(buf, slots, t, dtype):
     return q
 
 
-def _chain(x, w, slots, topk, types, out_dtype):
-    """gemv() through the decode chain: (h float32 [n, I], y [n, H] in out_dtype)."""
+def fast_form(hid, inter, types):
+    """Whether gemv() at these shapes and types runs the register-resident kernels (lmoe_gemv_chain_gate_up: x
+    prepared inside the launch, h kept as f16 prepared rows; lmoe_gemv_chain_down). They take one Q4 type for gate and
+    up, a Q4 down, hidden 2048 or 4096 and a width that is a multiple of 128 up to 8192; everything else runs the
+    raw-activation kernels with fp32 h between them."""
+    tg, tu, td = types
+    return (tg == tu and tg in _lib.Q4_TYPES and td in _lib.Q4_TYPES and hid in (2048, 4096)
+            and inter % 128 == 0 and inter // 64 <= 128)
+
+
+def _prepared(x, t):
+    """x's rows as prepared units for block type t (lmoe_prep_x): int32 [rows, hidden / 64 * 36]."""
+    rows, hid = x.shape
+    xp = torch.empty((rows, hid // 64 * 36), dtype=torch.int32, device=x.device)
+    call("lmoe_prep_x", ptr(x), dcode(x.dtype), rows, hid, qcode(t), ptr(xp), stream())
+    return xp
+
+
+def _chain(x, w, slots, topk, types, out_dtype, want_h=True):
+    """gemv() through the decode chain, a workgroup row a slot: (h float32 [n, I] or None when not wanted,
+    y [n, H] in out_dtype) (gguf_experts.py:610-629)."""
     bg, bu, bd = w
     tg, tu, td = types
     inter, hid = dims(bg, tg)
     s = _slots_u32(slots)
     n = s.numel()
     x = x.contiguous()
-    h = torch.empty((n, inter), dtype=torch.float32, device=x.device)
+    h = torch.empty((n, inter), dtype=torch.float32, device=x.device) if want_h or not fast_form(hid, inter, types) \
+        else None
     y = torch.empty((n, hid), dtype=out_dtype, device=x.device)
+    if fast_form(hid, inter, types):
+        hp = torch.empty((n, inter // 64 * 36), dtype=torch.int32, device=x.device)
+        call("lmoe_gemv_chain_gate_up", ptr(x), dcode(x.dtype), ptr(s), n, topk, ptr(bg), ptr(bu), qcode(tg),
+             bg.shape[0], hid, inter, ptr(h), ptr(hp), qcode(td), stream())
+        call("lmoe_gemv_chain_down", ptr(hp), ptr(s), n, ptr(bd), qcode(td), bd.shape[0], inter, hid, ptr(y),
+             dcode(out_dtype), stream())
+        return h, y
     call("lmoe_gemv_gate_up", ptr(x), dcode(x.dtype), ptr(s), n, topk, ptr(bg), ptr(bu), qcode(tg), qcode(tu),
          bg.shape[0], hid, inter, ptr(h), stream())
     call("lmoe_gemv_down_combine", ptr(h), ptr(s), None, n, 1, ptr(bd), qcode(td), bd.shape[0], inter, hid, None,
@@ -95,18 +122,28 @@ def run_rows():
     return max(1, int(os.environ.get("LMOE_GGUF_RUN_ROWS", "4")))
 
 
-def _gemv_runs(x, w, slots, types, out_dtype):
+def _gemv_runs(x, w, slots, types, out_dtype, want_h=True):
     """gemv() on rows of one slot each (best sorted by slot) through the run kernels: a window of rows reads a weight
-    row once a run of equal slots; returns (h float32 [n, I], y [n, H] in out_dtype) (gguf_experts.py:632-658)."""
+    row once a run of equal slots; returns (h float32 [n, I] or None, y [n, H] in out_dtype), the kernels matching
+    the chain's form at these shapes (gguf_experts.py:632-658)."""
     bg, bu, bd = w
     tg, tu, td = types
     inter, hid = dims(bg, tg)
     s = _slots_u32(slots)
     n = s.numel()
     x = x.contiguous()
-    h = torch.empty((n, inter), dtype=torch.float32, device=x.device)
+    fast = fast_form(hid, inter, types)
+    h = torch.empty((n, inter), dtype=torch.float32, device=x.device) if want_h or not fast else None
     y = torch.empty((n, hid), dtype=out_dtype, device=x.device)
     tr = run_rows()
+    if fast:
+        xp = _prepared(x, tg)
+        hp = torch.empty((n, inter // 64 * 36), dtype=torch.int32, device=x.device)
+        call("lmoe_gemv_gate_up_runs_prepped", ptr(xp), ptr(s), n, tr, ptr(bg), ptr(bu), qcode(tg), bg.shape[0], hid,
+             inter, ptr(h), ptr(hp), qcode(td), stream())
+        call("lmoe_gemv_down_runs_prepped", ptr(hp), ptr(s), n, tr, ptr(bd), qcode(td), bd.shape[0], inter, hid,
+             ptr(y), dcode(out_dtype), stream())
+        return h, y
     call("lmoe_gemv_gate_up_runs", ptr(x), dcode(x.dtype), ptr(s), n, tr, ptr(bg), ptr(bu), qcode(tg), qcode(tu),
          bg.shape[0], hid, inter, ptr(h), stream())
     call("lmoe_gemv_down_runs", ptr(h), ptr(s), n, tr, ptr(bd), qcode(td), bd.shape[0], inter, hid, ptr(y),
@@ -114,48 +151,61 @@ def _gemv_runs(x, w, slots, types, out_dtype):
     return h, y
 
 
-# (hid, inter, types, x dtype, out dtype) -> whether the run kernels passed their check there
+def _bits(t):
+    """t's raw bits as an integer tensor of its element size (so -0 / +0 and NaN payloads compare as bits)."""
+    return t.contiguous().view({4: torch.int32, 2: torch.int16}[t.element_size()])
+
+
+def _identical(a, b):
+    return a.dtype == b.dtype and a.shape == b.shape and bool(torch.equal(_bits(a), _bits(b)))
+
+
+# (hid, inter, types, x dtype, out dtype) -> whether the run kernels stand in for the chain there. An entry is
+# written False before its check runs, so anything gemv() is asked during the check takes the chain.
 _RUNS_OK = {}
 
 
-def _same_bits(a, b):
-    if a.shape != b.shape or a.dtype != b.dtype:
-        return False
-    u = {4: torch.int32, 2: torch.int16}[a.element_size()]
-    return bool(torch.equal(a.contiguous().view(u), b.contiguous().view(u)))
+def _run_check_case(hid, inter, types, x_dtype):
+    """The check's input: six random experts of these types, 16 runs of distinct lengths 1..16 (120 rows) over
+    slots 0..6 (slot 6 is past the experts: zero rows), and x random in x_dtype; seeded by the shape."""
+    g = torch.Generator(device="cuda").manual_seed(7 * hid + inter)
+    shapes = ((inter, hid), (inter, hid), (hid, inter))
+    w = tuple(_random_q4(6, r, c, t, g) for (r, c), t in zip(shapes, types))
+    run_len = torch.randperm(16, generator=g, device="cuda") + 1
+    run_id = torch.randint(0, 7, (16,), generator=g, device="cuda")
+    slots = torch.repeat_interleave(run_id.cpu(), run_len.cpu()).to(device="cuda", dtype=torch.int32)
+    x = torch.randn((slots.numel(), hid), generator=g, device="cuda").to(x_dtype)
+    return x, w, slots
+
+
+def _check_runs(hid, inter, types, x_dtype, out_dtype):
+    """(verdict, reason): the run kernels against the chain on _run_check_case, both outputs bit for bit."""
+    if not all(t in _lib.Q4_TYPES for t in types):
+        return False, f"no run kernels for {'/'.join(types)} (Q4_0 and Q4_K only)"
+    try:
+        x, w, slots = _run_check_case(hid, inter, types, x_dtype)
+        chain = _chain(x, w, slots, 1, types, out_dtype)
+        runs = _gemv_runs(x, w, slots, types, out_dtype)
+    except (RuntimeError, ValueError) as e:  # refused at this shape
+        return False, f"refused: {type(e).__name__}: {str(e)[:200]}"
+    for name, a, b in zip(("h", "output"), chain, runs):
+        if not _identical(a, b):
+            return False, f"their {name} is not bit-identical to the chain's"
+    return True, "bit-identical to the chain"
 
 
 def _runs_ok(hid, inter, types, x_dtype, out_dtype):
-    """Whether the run kernels may stand in for the chain at these shapes and dtypes: checked once (the reference's
-    _runs_ok, gguf_experts.py:661-680), on random experts of these types and rows in runs of 1 to 16 equal slots,
-    some past the experts; on only if h and the outputs are bit-equal to the chain's. Types beyond Q4_0 / Q4_K have
-    no run kernels and always take the chain."""
+    """Whether gemv() may take the run kernels at these shapes and dtypes (the reference's _runs_ok contract,
+    gguf_experts.py:661-680): decided once a key by _check_runs, logged once, False on any difference or refusal."""
     key = (hid, inter, tuple(types), x_dtype, out_dtype)
-    if key in _RUNS_OK:
-        return _RUNS_OK[key]
-    if any(t not in _lib.Q4_TYPES for t in types):
+    if key not in _RUNS_OK:
         _RUNS_OK[key] = False
-        return False
-    _RUNS_OK[key] = False
-    try:
-        g = torch.Generator(device="cuda").manual_seed(hid * 7 + inter)
-        n_exp = 6
-        w = tuple(_random_q4(n_exp, r, c, t, g)
-                  for (r, c), t in zip(((inter, hid), (inter, hid), (hid, inter)), types))
-        lens = torch.randperm(16, generator=g, device="cuda").cpu() + 1
-        ids = torch.randint(0, n_exp + 1, (16,), generator=g, device="cuda").cpu()  # id n_exp: no such expert
-        slots = torch.repeat_interleave(ids, lens).to(device="cuda", dtype=torch.int32)
-        x = torch.randn((slots.numel(), hid), generator=g, device="cuda").to(x_dtype)
-        want = _chain(x, w, slots, 1, types, out_dtype)
-        got = _gemv_runs(x, w, slots, types, out_dtype)
-        ok = all(map(_same_bits, want, got))
-        why = "" if ok else "they differ from the decode chain"
-    except (RuntimeError, ValueError) as e:  # a refusal at this shape
-        ok, why = False, f"{type(e).__name__}: {str(e)[:200]}"
-    _RUNS_OK[key] = ok
-    print(f"larder_amd: run kernels at {hid}x{inter} {'/'.join(types)} "
-          f"{'on, bit-equal to the decode chain' if ok else 'off: ' + why}", flush=True)
-    return ok
+        ok, reason = _check_runs(hid, inter, tuple(types), x_dtype, out_dtype)
+        _RUNS_OK[key] = ok
+        state = "in use" if ok else "not used"
+        print(f"larder_amd: run kernels {state} at {hid}x{inter} {'/'.join(types)} "
+              f"({str(x_dtype).split('.')[-1]} -> {str(out_dtype).split('.')[-1]}): {reason}", flush=True)
+    return _RUNS_OK[key]
 
 
 def gemv(x, w, slots, topk, types, out_dtype):
@@ -167,8 +217,8 @@ def gemv(x, w, slots, topk, types, out_dtype):
     if topk == 1 and n > 1 and runs_on():
         inter, hid = dims(w[0], types[0])
         if _runs_ok(hid, inter, types, x.dtype, out_dtype):
-            return _gemv_runs(x, w, slots, types, out_dtype)[1]
-    return _chain(x, w, slots, topk, types, out_dtype)[1]
+            return _gemv_runs(x, w, slots, types, out_dtype, want_h=False)[1]
+    return _chain(x, w, slots, topk, types, out_dtype, want_h=False)[1]
 
 
 def dense(x, w, host, types, out_dtype):
@@ -309,6 +359,8 @@ def calibrate(hid, inter, types):
             print(f"larder_amd: the dense-path fit for {hid}x{inter} {'/'.join(types)} was measured but not cached "
                   f"({e})", flush=True)
     _COST = cost
+    if runs_on():  # the run kernels are checked here, at load, not in the middle of the first prompt
+        _runs_ok(hid, inter, types, torch.bfloat16, torch.bfloat16)
     return cost
 
 

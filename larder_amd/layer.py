@@ -174,6 +174,10 @@ class MoELayer:
             held += [t for t in self.shared_stream if t is not None]
         return sum(t.numel() for t in held)
 
+    def drop_stream(self):
+        """Release the stream-layout copies: the grouped path reads the GGUF blocks as stored again."""
+        self.stream_w = self.folded_stream = self.shared_stream = None
+
     def nbytes_touched(self, n_unique):
         """Algorithmic HBM bytes of one decode pass touching n_unique routed experts (weights only)."""
         per = self.wg[0].numel() + self.wu[0].numel() + self.wd[0].numel()

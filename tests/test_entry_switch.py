@@ -31,8 +31,13 @@ def test_calibrate_caches_by_device_and_shape(monkeypatch, tmp_path):
         return [1e-5, 2e-6, 4e-5, 1e-6, 1e-7]
 
     monkeypatch.setattr(ge, "_measure", fake_measure)
+    checked = []
+    monkeypatch.setattr(ge, "_runs_ok", lambda *a: checked.append(a) or True)
     cost = ge.calibrate(2048, 768, "Q4_0/Q4_0/Q4_0")
     assert cost == [1e-5, 2e-6, 4e-5, 1e-6, 1e-7] and ge._COST == cost and len(calls) == 1
+    # the run kernels are checked at load (gguf_experts.py:791-792), at the reference's bf16 -> bf16
+    import torch
+    assert checked == [(2048, 768, ("Q4_0",) * 3, torch.bfloat16, torch.bfloat16)]
     files = list(tmp_path.glob("dense-switch-*.json"))
     assert len(files) == 1 and json.loads(files[0].read_text())["cost"] == cost
     # the second call reads the cache
@@ -47,6 +52,11 @@ def test_calibrate_caches_by_device_and_shape(monkeypatch, tmp_path):
         f.write_text("{")
     ge.calibrate(2048, 768, "Q4_0/Q4_0/Q4_0")
     assert len(calls) == 4
+    # every load asks (the check itself runs once a key); LMOE_GGUF_RUNS=0 skips it
+    assert len(checked) == 5
+    monkeypatch.setenv("LMOE_GGUF_RUNS", "0")
+    ge.calibrate(2048, 768, "Q4_0/Q4_0/Q4_0")
+    assert len(checked) == 5
 
 
 def test_calibrate_unwritable_cache_still_fits(monkeypatch, tmp_path, capsys):
@@ -55,6 +65,7 @@ def test_calibrate_unwritable_cache_still_fits(monkeypatch, tmp_path, capsys):
     monkeypatch.setenv("LMOE_CACHE", str(blocker / "sub"))      # a directory under a file: cannot be created
     monkeypatch.setattr(ge, "_device_key", lambda: ["gfx950", 256, "7.0", "src"])
     monkeypatch.setattr(ge, "_measure", lambda h, i, t: [0.0, 1e-6, 0.0, 0.0, 0.0])
+    monkeypatch.setattr(ge, "_runs_ok", lambda *a: True)
     assert ge.calibrate(1024, 256, "Q4_K/Q4_K/Q4_K") == [0.0, 1e-6, 0.0, 0.0, 0.0]
     assert "not cached" in capsys.readouterr().out
 

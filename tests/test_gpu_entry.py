@@ -28,7 +28,9 @@ def _bf16_round(a):
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).float().numpy()
 
 
-@pytest.fixture(scope="module", params=[(("Q4_0", "Q4_0", "Q4_0"), 1024, 256), (("Q4_K", "Q4_K", "Q6_K"), 1024, 512)])
+# the first two run the raw-activation chain, the third (cfg2's shape) the register-resident one
+@pytest.fixture(scope="module", params=[(("Q4_0", "Q4_0", "Q4_0"), 1024, 256), (("Q4_K", "Q4_K", "Q6_K"), 1024, 512),
+                                        (("Q4_0", "Q4_0", "Q4_0"), 2048, 768)])
 def arena(request, tmp_path_factory):
     """(src experts per projection, bufs as (gguf, pad) tuples over arena slots, slot_of[expert], types, H)."""
     from larder_amd import gguf_pack as gp

@@ -32,8 +32,12 @@ def same_bits(a, b):
                                                                        torch.int16)))
 
 
+# the first four and the last two run the register-resident chain and the run kernels that follow it
+# (gguf_experts.fast_form: one Q4 type for gate and up, hidden 2048 / 4096, a width that is a multiple of 128 up to
+# 8192; 4608 puts 72 units a row on the lanes, past one a lane); the rest the raw-activation chain and its run kernels
 MIXES = [(("Q4_0",) * 3, 2048, 768), (("Q4_0",) * 3, 1344, 448), (("Q4_K",) * 3, 1024, 512),
-         (("Q4_K",) * 3, 4096, 256), (("Q4_0", "Q4_K", "Q4_0"), 1024, 512), (("Q4_K", "Q4_0", "Q4_K"), 512, 512)]
+         (("Q4_K",) * 3, 4096, 256), (("Q4_0", "Q4_K", "Q4_0"), 1024, 512), (("Q4_K", "Q4_0", "Q4_K"), 512, 512),
+         (("Q4_K",) * 3, 2048, 512), (("Q4_0",) * 3, 4096, 1408), (("Q4_0",) * 3, 2048, 4608)]
 
 
 def sorted_runs(rng, E, n_runs, longest):
@@ -93,13 +97,13 @@ def test_gemv_dispatch(monkeypatch, capsys):
     x = dev(rng.standard_normal((24, H)).astype(np.float32)).half()
     ran = []
     runs0, chain0 = ge._gemv_runs, ge._chain
-    monkeypatch.setattr(ge, "_gemv_runs", lambda *a: ran.append("runs") or runs0(*a))
-    monkeypatch.setattr(ge, "_chain", lambda *a: ran.append("chain") or chain0(*a))
+    monkeypatch.setattr(ge, "_gemv_runs", lambda *a, **kw: ran.append("runs") or runs0(*a, **kw))
+    monkeypatch.setattr(ge, "_chain", lambda *a, **kw: ran.append("chain") or chain0(*a, **kw))
     monkeypatch.setattr(ge, "_RUNS_OK", {})
     y = ge.gemv(x, w, dev(slots), 1, types, torch.float16)
     # the first call at this shape checks the run kernels against the chain, then uses them
     assert ran == ["chain", "runs", "runs"], ran
-    assert "on, bit-equal" in capsys.readouterr().out
+    assert "run kernels in use" in capsys.readouterr().out
     yw = moe.gemv(host(x.float()), src, slots, 1, types)[1]
     assert moe.rel_l2(host(y.float()), yw) < BAR
     for label, args, env in (("topk 2", (x[:12], w, dev(slots), 2), "1"), ("one row", (x[:1], w, dev(slots[:1]), 1), "1"),
@@ -121,8 +125,8 @@ def test_forced_mismatch_turns_the_runs_off(monkeypatch, capsys):
     types, H, I = MIXES[2]
     runs0 = ge._gemv_runs
 
-    def off_by_one_bit(*a):
-        h, y = runs0(*a)
+    def off_by_one_bit(*a, **kw):
+        h, y = runs0(*a, **kw)
         y = y.clone()
         y.view(torch.int16).view(-1)[5] ^= 1
         return h, y
@@ -130,12 +134,60 @@ def test_forced_mismatch_turns_the_runs_off(monkeypatch, capsys):
     monkeypatch.setattr(ge, "_RUNS_OK", {})
     monkeypatch.setattr(ge, "_gemv_runs", off_by_one_bit)
     assert not ge._runs_ok(H, I, types, torch.float16, torch.float16)
-    assert "off: they differ from the decode chain" in capsys.readouterr().out
+    assert "not used" in (out := capsys.readouterr().out) and "output is not bit-identical" in out
     rng = np.random.default_rng(2)
     w = tuple(dev(gguf.random_experts(rng, 3, r, c, t)) for (r, c), t in zip(((I, H), (I, H), (H, I)), types))
     x = dev(rng.standard_normal((6, H)).astype(np.float32)).half()
     ran = []
     chain0 = ge._chain
-    monkeypatch.setattr(ge, "_chain", lambda *a: ran.append("chain") or chain0(*a))
+    monkeypatch.setattr(ge, "_chain", lambda *a, **kw: ran.append("chain") or chain0(*a, **kw))
     ge.gemv(x, w, dev(np.array([0, 0, 1, 1, 2, 2], np.int32)), 1, types, torch.float16)
     assert ran == ["chain"]
+
+
+@pytest.mark.parametrize("types,H,I,topk", [(("Q4_0",) * 3, 2048, 768, 8), (("Q4_K",) * 3, 2048, 512, 10),
+                                            (("Q4_0",) * 3, 4096, 1408, 4), (("Q4_K",) * 3, 4096, 256, 2)])
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.float32])
+def test_fast_chain_topk_vs_oracle(types, H, I, topk, xdt):
+    """gemv() at topk > 1 on the register-resident chain (the form cfg2's and cfg5's decode rows take): every slot's
+    unweighted output against the oracle, h to 1e-5 on the f16 values the kernels see (x is narrowed to f16 once),
+    the outputs to 2e-3 against the oracle on x as given; slots past the experts give zero rows."""
+    from larder_amd import gguf_experts as ge
+    assert ge.fast_form(H, I, types)
+    rng = np.random.default_rng(H + I + topk)
+    E = 12
+    src = tuple(gguf.random_experts(rng, E, r, c, t) for (r, c), t in zip(((I, H), (I, H), (H, I)), types))
+    w = tuple(dev(b) for b in src)
+    T = 3
+    slots = np.stack([rng.permutation(E + 1)[:topk] for _ in range(T)]).reshape(-1).astype(np.int32)  # E: none
+    x = dev(rng.standard_normal((T, H)).astype(np.float32)).to(xdt)
+    h, y = ge._chain(x, w, dev(slots), topk, types, torch.float32)
+    xs = host(x.float())
+    hw16, _ = moe.gemv(host(x.half().float()), src, slots, topk, types)
+    hw, yw = moe.gemv(xs, src, slots, topk, types)
+    assert moe.rel_l2(host(h), hw16) < 1e-5
+    assert moe.rel_l2(host(y), yw) < BAR
+    off = slots >= E
+    assert (host(h)[off] == 0).all() and (host(y)[off] == 0).all()
+    # gemv() itself (no h asked for) gives the same bits
+    assert same_bits(ge.gemv(x, w, dev(slots), topk, types, torch.float32), y)
+
+
+@pytest.mark.parametrize("types,H,I", [(("Q4_0",) * 3, 2048, 768), (("Q4_K",) * 3, 2048, 512),
+                                       (("Q4_0",) * 3, 2048, 1408), (("Q4_0",) * 3, 4096, 4608)])
+def test_fast_chain_slot_bits_do_not_depend_on_the_call(types, H, I):
+    """A slot's output is the same bits at topk 8 as at topk 1 with x repeated a slot, and alone: the chain's down
+    sums each slot over its own lane group (16, 32 or 64 lanes), and gate/up is one workgroup row a slot."""
+    from larder_amd import gguf_experts as ge
+    rng = np.random.default_rng(I)
+    E = 10
+    w = tuple(dev(gguf.random_experts(rng, E, r, c, t)) for (r, c), t in zip(((I, H), (I, H), (H, I)), types))
+    T, k = 2, 8
+    slots = np.concatenate([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    x = dev(rng.standard_normal((T, H)).astype(np.float32)).half()
+    h8, y8 = ge._chain(x, w, dev(slots), k, types, torch.float32)
+    h1, y1 = ge._chain(x.repeat_interleave(k, 0), w, dev(slots), 1, types, torch.float32)
+    assert same_bits(h8, h1) and same_bits(y8, y1)
+    for s in (0, 5, 11):
+        hs, ys = ge._chain(x[s // k:s // k + 1], w, dev(slots[s:s + 1]), 1, types, torch.float32)
+        assert same_bits(hs[0], h8[s]) and same_bits(ys[0], y8[s])
