@@ -968,17 +968,17 @@ k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const
     tab[nb] = kTab + kKTabRow * f;
   }
   // Step kk out of stage s: per fragment the two qs words and the step's two scale pairs, both K slices' weights
-  // decoded, each meeting the tile's A fragments (QN pairs of 16-row blocks)
-  auto compute = [&](int s, int kk, auto qn) {
-    constexpr int QN = decltype(qn)::value;
+  // decoded, each meeting the tile's A fragments (NMB 16-row blocks: a 40-row group multiplies 48 rows, not 64)
+  auto compute = [&](int s, int kk, auto nmb) {
+    constexpr int NMB = decltype(nmb)::value;
     const uint8_t *st = lds + s * kStage;
     const u32x4 *as = reinterpret_cast<const u32x4 *>(st);
     const int pr = kk & 3;  // the step's sub-block pair: sub-blocks 2 pr (low nibbles) and 2 pr + 1 (high)
-    half8 xf[2][2 * QMAX];
+    half8 xf[2][MB];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int mb = 0; mb < 2 * QN; ++mb) xf[ks][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 * ks + g)]);
+      for (int mb = 0; mb < NMB; ++mb) xf[ks][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 * ks + g)]);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const uint32_t lo = *reinterpret_cast<const uint32_t *>(st + qlo[nb]);
@@ -990,7 +990,7 @@ k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const
                                    : ((lo >> 4) & 0x0F0F0F0Fu) | (hi & 0xF0F0F0F0u);
         const half8 wf = decode8<LMOE_Q4_K>(x, ks == 0 ? uint32_t(sp[0]) : uint32_t(sp[1]), 0);
 #pragma unroll
-        for (int mb = 0; mb < 2 * QN; ++mb)
+        for (int mb = 0; mb < NMB; ++mb)
           acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, xf[ks][mb], acc[nb][mb], 0, 0, 0);
       }
     }
@@ -1030,13 +1030,11 @@ k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const
       }
     }
   };
-  if constexpr (QMAX == 1) {
-    run(IC<1>{});
-  } else {
-    if (t.rows <= 32)  // uniform across the workgroup
-      run(IC<1>{});
-    else
-      run(IC<2>{});
+  switch ((t.rows + 15) / 16) {  // uniform across the workgroup
+    case 1: run(IC<1>{}); break;
+    case 2: run(IC<(MB >= 2 ? 2 : MB)>{}); break;
+    case 3: run(IC<(MB >= 3 ? 3 : MB)>{}); break;
+    default: run(IC<MB>{}); break;
   }
   store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
 }
