@@ -67,7 +67,11 @@ int lmoe_router_topk_shared(const float *logits, int T, int E, int k, int norm, 
 
 /* Prepared activation rows: an activation row of 64 P values as P units of 36 dwords (32 dwords of f16 pairs in
  * the nibble order of block type qtype, the sums of the unit's two 32-value halves as fp32, two zero dwords), the
- * form the expert kernels read. x [rows][H] in xdtype -> xprep [rows][H / 64 * 36] uint32. */
+ * form the expert kernels read. x [rows][H] in xdtype -> xprep [rows][H / 64 * 36] uint32.
+ * Range: every value is rounded to f16 once (exact for f16 x, and for bf16 x inside f16's normal range), so an |x|
+ * above 65504 becomes inf, and so does an |h| above 65504 in the prepared h rows the gate/up entries write: the
+ * expert rows fed by such a value come out non-finite. The reference stages x and h as f32 (gguf_experts.py:452-526);
+ * the general kernels (raw x, fp32 h) keep that range. */
 int lmoe_prep_x(const void *x, int xdtype, int rows, int H, int qtype, uint32_t *xprep, void *stream);
 
 /* Router GEMV: logits[t][e] = x[t] . wr[e] (fp32 accumulation), and when wsg is given the shared-expert gate logit

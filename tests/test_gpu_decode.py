@@ -374,3 +374,43 @@ def test_router_gemv_rank_vs_oracle(E, k, norm, T, shared, H):
         assert np.array_equal(lg[:, E:].view(np.uint32), gate.view(np.uint32))
         assert (ids[:, k:] == E + np.arange(shared)).all()
         assert np.allclose(sc[:, k:], moe.sigmoid(gate[:, :1]), rtol=1e-6)
+
+
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+def test_decode_f16_range_limit(xdt):
+    """The decode chain's stated limit: x and h meet the weights as f16 (the reference stages both as f32,
+    gguf_experts.py:452-526). Inside f16's range the layer and the drop-in gemv hold the bar; an |x| past 65,504
+    (bf16 / f32 x) or an |h| past it (x inside the range, weights large enough) makes the rows it feeds non-finite,
+    while the router, which reads x as given, still routes as the oracle does."""
+    from larder_amd import gguf_experts as ge, layer as lay, workloads
+    cfg = dict(workloads.CONFIGS[2], E=16)
+    L = _layer_from_device(cfg, 4)
+    rng = np.random.default_rng(17)
+    H = cfg["H"]
+    w = tuple(host(b) for b in (L.wg, L.wu, L.wd))
+    base = rng.standard_normal((2, H)).astype(np.float32)
+    cases = {"inside": base * 8.0, "x_past_f16": base.copy(), "h_past_f16": base * 300.0}
+    cases["x_past_f16"][:, ::97] = 1.0e5
+    for name, xa in cases.items():
+        x = dev(xa).to(xdt)
+        xs = host(x.float())
+        B = lay.DecodeBuffers(L, 2)
+        out = torch.empty((2, H), dtype=torch.float32, device="cuda")
+        lay.decode(L, x, B, out)
+        torch.cuda.synchronize()
+        if xdt == torch.bfloat16:  # routing pinned from x (bf16 x widened exactly; every product exact in fp32)
+            lg = moe.router_logits_gemv(xs, host(L.wr))
+            assert np.array_equal(host(B.logits).view(np.uint32), lg.view(np.uint32)), name
+        else:  # f32 x: the router's fma products round, which the oracle's order does not restate; its ids from them
+            lg = host(B.logits)
+        ids, _, want = moe.layer(xs, lg, w, cfg["types"], cfg["k"], cfg["norm"])
+        assert (host(B.ids).astype(np.uint32) == ids).all(), name
+        slots = torch.from_numpy(ids.reshape(-1).astype(np.int32)).cuda()
+        y = host(ge.gemv(x, (L.wg, L.wu, L.wd), slots, cfg["k"], cfg["types"], torch.float32))
+        hw, yw = moe.gemv(xs, w, ids.reshape(-1), cfg["k"], cfg["types"])
+        if name == "inside":
+            assert np.abs(hw).max() < 65504 and moe.rel_l2(host(out), want) < BAR and moe.rel_l2(y, yw) < BAR
+        else:
+            if name == "h_past_f16":  # the premise: x inside f16's range, h past it
+                assert np.abs(xs).max() < 65504 and np.abs(hw).max() > 65504
+            assert not np.isfinite(host(out)).all() and not np.isfinite(y).all(), name

@@ -57,8 +57,10 @@ CASES = [
     # 768), and with one that folds
     (("Q4_0", "Q4_0", "Q8_0"), 2048, 768, 12, 4, False, 1024),
     (("Q4_0", "Q4_0", "Q8_0"), 4096, 512, 10, 3, True, 1024),
-    # a Q5_K down under Q4_K gate/up: fp32 h (lmoe_moe_gate_up_h), the general down
+    # a Q5_K down under Q4_K gate/up: fp32 h (lmoe_moe_gate_up_h), the general down; then the same with a folded
+    # shared expert (m = 2 slices: lmoe_moe_gate_up_h's sigmoid-weighted slots E, E + 1 and their fp32 h rows)
     (("Q4_K", "Q4_K", "Q5_K"), 2048, 512, 12, 4, True, 0),
+    (("Q4_K", "Q4_K", "Q5_K"), 2048, 512, 12, 4, True, 1024),
     # gate/up beyond Q4 (the general gate/up from raw x), down Q6_K or Q4_0
     (("Q6_K", "Q6_K", "Q6_K"), 1024, 512, 8, 2, True, 0),
     (("Q8_0", "Q8_0", "Q4_0"), 2048, 768, 10, 3, True, 0),
