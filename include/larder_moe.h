@@ -227,82 +227,6 @@ int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sums, const ui
                                    const float *shared, const float *gate, int gate_stride, const void *residual,
                                    int rdtype, void *out, int odtype, void *stream);
 
-/* The decode layer's gate/up + SwiGLU and down + weighted combine (+ residual) in ONE launch: the work of
- * lmoe_moe_gate_up_ext (m = n_shared folded shared-expert slices, 0 for none) followed by
- * lmoe_gemv_down_combine_prepped, with the same ids [T][k + m], scores [T][k + m] and out [T][H] bit for bit. The down
- * workgroups rank the logits themselves and request their weights at once; h passes between the two kinds of
- * workgroup inside the launch as epoch-tagged words in the workspace. Replaces route_cuda.probs plus gguf_gate_up and
- * gguf_down with the block's combine on decode rows (route_cuda.py:433-444; gguf_experts.py:452-526;
- * stream_fast.py:4372-4376); the single launch has no counterpart in the reference.
- * logits [T][ld_stride] (E routed, then the shared gate's logit when n_shared > 0), x_prep [T][H / 64 * 36] prepared
- * for type_gu (lmoe_router_gemv / lmoe_prep_x), wg / wu [E + m][I][.] of type_gu, wd [E + m][H][.] of type_d (the
- * same type: all three Q4_0 or all Q4_K), hprep [T (k + m)][I / 64 * 36] (NULL: not written). H 2048 or 4096, T <= 16, k <= 32, E <= 1024,
- * (k + m) I / 64 <= 128. The workspace (lmoe_moe_fused_workspace_bytes) is zeroed once before its first use and keeps
- * per-workgroup launch counts between calls: every call on one workspace must have the same T, k, m, H and I, and the
- * calls must be ordered (one stream). Each wait for h is bounded (0.2 s); a launch whose wait ran out writes NaN
- * output rows and leaves its epoch in the status word (lmoe_moe_fused_status); later launches run normally.
- * Measured on MI355X it is slower than the two launches it replaces (cfg2: 16.2 against 14.7 us a layer: the in-grid
- * hand-off of h costs as much as the kernel boundary), so the Python decode uses it only with LMOE_FUSED=1. */
-size_t lmoe_moe_fused_workspace_bytes(int T, int k, int n_shared, int H, int I);
-int lmoe_moe_fused(const float *logits, int ld_stride, int T, int k, int norm, const uint32_t *x_prep,
-                   const uint8_t *wg, const uint8_t *wu, const uint8_t *wd, int type_gu, int type_d, int n_experts,
-                   int H, int I, int n_shared, uint32_t *ids, float *scores, uint32_t *hprep, const void *residual,
-                   int rdtype, void *out, int odtype, void *workspace, size_t workspace_bytes, void *stream);
-/* The status word of a fused-decode workspace: 0, or the epoch of the last launch whose wait ran out. Synchronises
- * the stream. */
-int lmoe_moe_fused_status(const void *workspace, uint32_t *status, void *stream);
-
-/* The decode chain with the router GEMV folded into its neighbours (a stack of layers: two launches a layer instead
- * of three). The router's logits are sums over 8-element items of x: lmoe_router_gemv forms each item's products as
- * one fma chain from zero and adds the chains in a fixed tree (per wavefront a balanced tree over 64 items, then the
- * four wavefronts in order). At H = 2048 each of its threads holds exactly one item, so those item chains, the
- * router partials part [T][256][R] (R = E rows, plus the shared gate row last when wsg is given), rebuild the
- * logits bit for bit. Replaces the block's gate linear and top-k as in lmoe_router_gemv / lmoe_moe_gate_up
- * (stream_fast.py:4358-4370, route_cuda.py:433-444); the split into partials has no counterpart in the reference.
- *   lmoe_router_part: the partials of x [T][H] against wr [E][H] (+ wsg [H]), for the first layer of a stack.
- *   lmoe_moe_gate_up_part: lmoe_moe_gate_up_ext's work (ids / scores [T][k + m], hprep [T (k + m)][I / 64 * 36])
- *     with the logits summed from part and x [T][H] raw in xdtype (prepared in-kernel); the ids are those
- *     lmoe_router_gemv + lmoe_moe_gate_up give, bit for bit. m = shared_slices (0: none; else the router's R
- *     includes the gate row). H = 2048, E + (m > 0) <= 256, one type for gate and up.
- *   lmoe_gemv_down_combine_part: lmoe_gemv_down_combine_prepped (no separate shared row) whose output rows, as
- *     stored in odtype, also give the NEXT layer's partials against wr_next [e_next][H] (+ wsg_next) into part. It
- *     takes the one-wavefront-a-row-pair form: at most 128 h units a token (k I / 64), I / 64 even.
- * Measured on MI355X at cfg2's shape (48 layers, E 128, k 8, one token) the three entries run a layer in 22.2 us
- * against 15.0 for the three-launch chain: every gate/up workgroup (16 wavefronts) reads all 256 x R partials, and
- * the wider workgroups with their in-kernel x preparation cost more than the router launch they remove. */
-int lmoe_router_part(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T, int H, int E,
-                     float *part, void *stream);
-int lmoe_moe_gate_up_part(const float *part, const void *x, int xdtype, int T, int k, int norm, const uint8_t *wg,
-                          const uint8_t *wu, int type_g, int type_u, int n_experts, int H, int I, uint32_t *ids,
-                          float *scores, uint32_t *hprep, int type_d, int shared_slices, void *stream);
-int lmoe_gemv_down_combine_part(const uint32_t *hprep, const uint32_t *ids, const float *scores, int T, int k,
-                                const uint8_t *wd, int type_d, int n_experts, int I, int H, const void *residual,
-                                int rdtype, void *out, int odtype, const void *wr_next, const void *wsg_next,
-                                int wdtype_next, int e_next, float *part, void *stream);
-
-/* Batch-1 decode through a stack of L MoE layers of one shape in ONE kernel launch: x_{l+1} = x_l + moe_l(x_l),
- * moe_l = router logits (f16 router weight, plus the shared gate row when Is > 0), softmax top-k (ties to the
- * lowest index), the k experts' gate/up + SwiGLU and down read from GGUF blocks, weighted by the softmax scores
- * (renormalised when norm), plus sigmoid(x . wsg) times the shared expert when Is > 0. This is the decode loop of
- * the reference's layer stack (stream_fast.py:4352-4377 over gguf_experts.experts, gguf_experts.py:803-819) with
- * the layer boundary moved inside the kernel; it has no single counterpart in the reference. One cooperative launch
- * of one workgroup a CU; the layers' hand-offs go through the workspace. x and out: [H] f16 (one token).
- * wg / wu / wd / wr / wsg / sg / su / sd: DEVICE arrays of L device pointers: wg[l], wu[l] [E][I][36 H / 64],
- * wd[l] [E][H][36 I / 64], wr[l] [E][H] f16, and (Is > 0) wsg[l] [H] f16, sg[l], su[l] [Is][36 H / 64],
- * sd[l] [H][36 Is / 64], all Q4_0 or all Q4_K (qtype). H 2048 or 4096, E <= 512, k <= 16, I and Is multiples of
- * 128 (256 for Q4_K). y [L][H] f32 (each layer's MoE output before the residual), ids [L][k], scores [L][k]:
- * optional (NULL). The workspace (lmoe_stack_workspace_bytes) must be zeroed once before its first use and keeps
- * state between calls (a launch epoch); calls sharing one workspace must be ordered on one stream. Each internal
- * wait is bounded (0.2 s); a launch whose wait ran out sets a status word that lmoe_stack_status reads, and the
- * workspace must then be zeroed again before it is reused (launches on it do nothing until then). */
-size_t lmoe_stack_workspace_bytes(int L, int H, int E, int k, int I, int Is);
-int lmoe_stack_decode(int L, int H, int E, int k, int I, int Is, int qtype, int norm, const void *const *wg,
-                      const void *const *wu, const void *const *wd, const void *const *wr, const void *const *wsg,
-                      const void *const *sg, const void *const *su, const void *const *sd, const void *x, void *out,
-                      void *workspace, float *y, uint32_t *ids, float *scores, void *stream);
-/* The status word of a stack workspace (0: every wait of every launch ended in time); synchronises the stream. */
-int lmoe_stack_status(const void *workspace, uint32_t *status, void *stream);
-
 /* Device-side ragged grouping: the stable counting sort of the flattened (token, k) expert ids, the device
  * form of stream_fast.py:5466-5471 (argsort of the flat ids and its inverse) and gguf_experts.py:702-713.
  * ids [R] -> counts [E], offsets [E + 1], order [R] (rows of expert 0 in flat order, then expert 1, ...; ids >= E

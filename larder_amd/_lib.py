@@ -49,15 +49,7 @@ SIGNATURES = {
     "lmoe_gemv_down_combine": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I, _P]),
     "lmoe_gemv_down_combine_prepped": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _P, _I,
                                             _P]),
-    "lmoe_moe_fused_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
-    "lmoe_moe_fused": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _I, _P,
-                            _SZ, _P]),
-    "lmoe_moe_fused_status": (_I, [_P, _P, _P]),
     "lmoe_topk_and_gemm_f16": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _LL, _P, _P]),
-    "lmoe_router_part": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P]),
-    "lmoe_moe_gate_up_part": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P]),
-    "lmoe_gemv_down_combine_part": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _I, _P, _I, _P, _P, _I, _I, _P,
-                                         _P]),
     "lmoe_gemv_gate_up_runs": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "lmoe_gemv_down_runs": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _I, _P, _I, _P]),
     "lmoe_gemv_chain_gate_up": (_I, [_P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
@@ -101,9 +93,6 @@ SIGNATURES = {
     "lmoe_grouped_down_f16w": (_I, [_P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P, _I, _P]),
     "lmoe_quantize_q4_0": (_I, [_P, _I, _LL, _I, _P, _P]),
     "lmoe_quantize_q4_k": (_I, [_P, _I, _LL, _I, _P, _P]),
-    "lmoe_stack_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
-    "lmoe_stack_decode": (_I, [_I] * 8 + [_P] * 8 + [_P] * 7),
-    "lmoe_stack_status": (_I, [_P, _P, _P]),
 }
 
 _LIB = None

@@ -280,24 +280,17 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // (n_experts + j, sigmoid(logits[t][n_experts])) for the down kernel to weight them like routed experts: the shared
 // expert's down is linear in its intermediate features, so the m weighted slices sum to the gated shared row.
 //
-// RP (NW >= 8, H = 2048): the logits are rebuilt from the router partials part [T][256][n_experts + 1 when the
-// shared gate row is there (ks > topk), else n_experts] in k_router_gemv's order, and x comes raw (dtype xdt) and
-// is prepared here: one workgroup barrier after the partials' first tree level, one after the logits, one after the
-// prepared row (the three share LDS with the wavefronts' stages, which are written only after the last barrier).
-// Wavefront w takes the first-level tasks (item row r of 16 items, block of 64 router rows) w, w + NW, ...
-//
 // RAW (slots given, NPL = 0): x comes raw (dtype xdt) and each workgroup prepares its row in LDS with prep_dword,
 // the bits lmoe_prep_x writes, so the launch before it is saved: the drop-in chain's form.
-template <int TQ, int P, int RB, int NPL, bool RANKWG, int NW = 4, bool RP = false, bool RAW = false>
-__global__ void __launch_bounds__(64 * NW)
+template <int TQ, int P, int RB, int NPL, bool RANKWG, bool RAW = false>
+__global__ void __launch_bounds__(256)
     k_gate_up_xr(const uint32_t *xprep, const uint32_t *slots, int topk, const uint8_t *wg, const uint8_t *wu,
                  int n_experts, int I, float *h, uint32_t *hprep, int td, const float *logits, int ld_stride,
-                 int norm, uint32_t *ids_out, float *scores_out, int ks, const float *part, const void *x, int xdt) {
-  constexpr int G = 64 / P, RG = RB / G;
+                 int norm, uint32_t *ids_out, float *scores_out, int ks, const void *x, int xdt) {
+  constexpr int NW = 4, G = 64 / P, RG = RB / G;
   static_assert(P == 32 || P == 64, "32 or 64 units a row");
   static_assert(RB % G == 0, "rows split evenly over the lane groups");
-  static_assert(!RP || (NW >= 8 && P == 32 && NPL > 0 && NPL <= 4 && !RANKWG), "partials: H 2048, 8+ wavefronts");
-  static_assert(!RAW || (!RP && NPL == 0), "raw x: slots given");
+  static_assert(!RAW || NPL == 0, "raw x: slots given");
   static_assert(!RAW || NW * 2 * RB * 9 * P >= 64 * P, "the stages hold the raw row (f32 at most)");
   constexpr int C = RB * 9 * P / 4;  // 16-byte chunks of RB rows of one matrix
   constexpr int NC = (C + 63) / 64;
@@ -325,60 +318,11 @@ __global__ void __launch_bounds__(64 * NW)
   float v[NPL > 0 ? NPL : 1];
   float lv[2];
   uint32_t e = 0;
-  // RP's LDS, over the stages: first-level sums [16][256], logits [256], the raw x row (H = 2048, <= 8 KB)
-  float *red = reinterpret_cast<float *>(lds4 + XC);
-  float *lgl = red + 16 * kPartRows;
-  u32x4 *xraw = RAW ? lds4 + XC : reinterpret_cast<u32x4 *>(lgl + kPartRows);
+  // RAW: the raw x row, over the stages (written only after the row is prepared)
+  u32x4 *xraw = lds4 + XC;
   constexpr int XRR = RAW ? (16 * P + NT - 1) / NT : 1;  // raw 16-byte chunks a thread (f32 at most)
   u32x4 xr4[XRR];
-  static_assert(!RP || NW * STAGE >= 17 * kPartRows + 2048, "the stages hold RP's scratch");
-  if (RP) {
-    const int rows = n_experts + (ks > topk ? 1 : 0), nb = (rows + 63) / 64;
-    const float *pt = part + xrow * kPartItems * rows;
-    // the raw x row (256 chunks f16 / bf16, 512 f32) and this wavefront's first-level tasks, all loads first
-    const int xch = xdt == LMOE_F32 ? 512 : 256;
-    constexpr int XR = (512 + NT - 1) / NT;
-    u32x4 xq[XR];
-#pragma unroll
-    for (int i = 0; i < XR; ++i)
-      xq[i] = reinterpret_cast<const u32x4 *>(static_cast<const char *>(x) + xrow * (xch * 16))[min(
-          int(threadIdx.x) + NT * i, xch - 1)];
-    constexpr int TPW = (16 * 4 + NW - 1) / NW;  // tasks a wavefront at most (4 blocks of 64 rows)
-    float q[TPW][16];
-#pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const int task = min(wave + NW * j, 16 * nb - 1), r = task / nb, b = task - r * nb;
-      const int col = min(64 * b + lane, rows - 1);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) q[j][i] = pt[size_t(16 * r + i) * rows + col];
-    }
-#pragma unroll
-    for (int i = 0; i < XR; ++i)
-      if (int(threadIdx.x) + NT * i < xch) xraw[threadIdx.x + NT * i] = xq[i];
-#pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-      const int task = wave + NW * j, r = task / nb, b = task - r * nb;
-      float t8[8], t4[4];  // the balanced tree over the row's 16 items, neighbours first (sum16's order)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) t8[i] = q[j][2 * i] + q[j][2 * i + 1];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) t4[i] = t8[2 * i] + t8[2 * i + 1];
-      if (task < 16 * nb) red[r * kPartRows + 64 * b + lane] = (t4[0] + t4[1]) + (t4[2] + t4[3]);
-    }
-    __syncthreads();
-    if (int(threadIdx.x) < rows) {  // each wavefront's four rows of 16 (wave_sum), then the wavefronts in order
-      float w4[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float *rr = red + 4 * c * kPartRows + threadIdx.x;
-        w4[c] = (rr[0] + rr[kPartRows]) + (rr[2 * kPartRows] + rr[3 * kPartRows]);
-      }
-      lgl[threadIdx.x] = ((w4[0] + w4[1]) + w4[2]) + w4[3];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) v[j] = lgl[min(lane + 64 * j, n_experts - 1)];
-  } else if (RAW) {  // the raw row's chunks first, then the slot's expert
+  if (RAW) {  // the raw row's chunks first, then the slot's expert
     const int xch = xdt == LMOE_F32 ? 16 * P : 8 * P;
     const u32x4 *xs4 = reinterpret_cast<const u32x4 *>(static_cast<const char *>(x) + xrow * (size_t(xch) * 16));
 #pragma unroll
@@ -396,8 +340,8 @@ __global__ void __launch_bounds__(64 * NW)
     e = slots[s];
   }
   const u32x4 *xg4 = reinterpret_cast<const u32x4 *>(xprep + xrow * P * XS);
-  u32x4 xc[RP || RAW ? 1 : XPT];
-  if (!RP && !RAW) {
+  u32x4 xc[RAW ? 1 : XPT];
+  if (!RAW) {
 #pragma unroll
     for (int i = 0; i < XPT; ++i) xc[i] = xg4[min(int(threadIdx.x) + NT * i, XC - 1)];
   }
@@ -405,7 +349,7 @@ __global__ void __launch_bounds__(64 * NW)
     e = uint32_t(n_experts + jslot - topk);
     if (blockIdx.x == 0 && wave == 0 && lane == 0) {
       ids_out[s] = e;
-      scores_out[s] = sigmoidf_(RP ? lgl[n_experts] : logits[xrow * ld_stride + n_experts]);
+      scores_out[s] = sigmoidf_(logits[xrow * ld_stride + n_experts]);
     }
   } else if (RANK) {  // uniform across the workgroup (the slot is blockIdx.y)
 #pragma unroll
@@ -447,7 +391,7 @@ __global__ void __launch_bounds__(64 * NW)
     vg[i] = __builtin_nontemporal_load(gsrc + c);
     vu[i] = __builtin_nontemporal_load(usrc + c);
   }
-  // the activation row into LDS (a thread past the end rewrites the last chunk with its own value; RP: prepared
+  // the activation row into LDS (a thread past the end rewrites the last chunk with its own value; RAW: prepared
   // here from the raw row), then the weights into the wavefront's stage, with no branch between loads and stores so
   // that no load is sunk into a conditional block behind the others' wait
   if (RAW) {
@@ -457,18 +401,7 @@ __global__ void __launch_bounds__(64 * NW)
       if (int(threadIdx.x) + NT * i < xch) xraw[threadIdx.x + NT * i] = xr4[i];
     __syncthreads();
   }
-  if (RP) {
-    const _Float16 *xh = reinterpret_cast<const _Float16 *>(xraw);
-    const uint16_t *xb = reinterpret_cast<const uint16_t *>(xraw);
-    const float *xf = reinterpret_cast<const float *>(xraw);
-    uint32_t *xd = reinterpret_cast<uint32_t *>(xl);
-    for (int idx = threadIdx.x; idx < P * XS; idx += NT) {
-      const int pu = idx / XS, dw = idx - pu * XS;
-      xd[idx] = prep_dword<TQ>(
-          [&](int i) { return xdt == LMOE_F16 ? float(xh[i]) : xdt == LMOE_BF16 ? bf16_to_f32(xb[i]) : xf[i]; }, pu,
-          dw);
-    }
-  } else if (RAW) {  // the pair dwords, then each unit's two sums and two pads (no thread mixes the two kinds)
+  if (RAW) {  // the pair dwords, then each unit's two sums and two pads (no thread mixes the two kinds)
     const _Float16 *xh = reinterpret_cast<const _Float16 *>(xraw);
     const uint16_t *xb = reinterpret_cast<const uint16_t *>(xraw);
     const float *xf = reinterpret_cast<const float *>(xraw);
@@ -695,17 +628,11 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // wavefront finish on DPP / permlane swaps, then the gated shared-expert row and the residual are added. Memory order:
 // h units, ids and scores (one a lane), then the weights, whose addresses need only the ids; no load is predicated
 // (clamped indices; expert 0 stands in for an id past the experts, with a zero weight).
-// RP (KS = 1 only): the workgroup's 8 output rows are item blockIdx.x of the next layer's router, so it also writes
-// that item's partials against the next router's rows (wrn [en][H], then wsgn, element type wdtn) into
-// part [T][H / 8][rows], from the rows as stored (rounded to odt); each thread takes one router row, whose 8 weights
-// it loads behind the experts' weights.
-template <int TD, int NU, int NCW, int KS = 1, bool RP = false>
+template <int TD, int NU, int NCW, int KS = 1>
 __global__ void __launch_bounds__(256)
     k_down_xr(const uint32_t *hprep, const uint32_t *ids, const float *scores, int k, const uint8_t *wd,
               int n_experts, int I, int H, const float *shared, const float *gate, int gate_stride,
-              const void *residual, int rdt, void *out, int odt, const void *wrn, const void *wsgn, int wdtn, int en,
-              float *part) {
-  static_assert(!RP || KS == 1, "router partials take one wavefront a row pair");
+              const void *residual, int rdt, void *out, int odt) {
   constexpr int RB = 2;
   // KS = 2 (a token's units past 128): wavefronts 2 q and 2 q + 1 share rows [(2 bx + q) RB, +RB), each over half of
   // the experts (the first ceil(k / 2), the rest), and add their two row sums through LDS
@@ -746,15 +673,6 @@ __global__ void __launch_bounds__(256)
     uint32_t e = uint32_t(__shfl(int(my_id), j0 + j, 64));
     e = e < uint32_t(n_experts) ? e : 0u;
     w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wd + (size_t(e) * H + nsafe) * rowb) + cc);
-  }
-  const int prow = RP ? en + (wsgn ? 1 : 0) : 0;  // the next router's rows
-  u32x4 rw0, rw1;
-  if (RP) {  // this thread's router row, its 8 weights at the workgroup's item (clamped, not predicated)
-    const int r = min(int(threadIdx.x), prow - 1), esz = wdtn == LMOE_F32 ? 4 : 2;
-    const char *wr = (r < en ? static_cast<const char *>(wrn) + size_t(r) * H * esz : static_cast<const char *>(wsgn)) +
-                     size_t(8) * blockIdx.x * esz;
-    rw0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wr));
-    rw1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wr + 16 * (esz / 4)));
   }
   asm volatile("" ::: "memory");
   // 3. each unit's expert, weight (0 past the units or the experts) and half-unit sums
@@ -814,7 +732,6 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int r = 0; r < RB; ++r) acc[r] += part[(wave >> 1) * RB + r];
   }
-  __shared__ float xr[RP ? 4 * RB : 1];
   if (lane < RB) {
     float v = acc[0];
 #pragma unroll
@@ -823,12 +740,6 @@ __global__ void __launch_bounds__(256)
     if (shared) v += sigmoidf_(gate[size_t(t) * gate_stride]) * shared[o];
     if (residual) v += load_elt(residual, o, rdt);
     store_elt(out, o, v, odt);
-    if (RP) xr[wave * RB + lane] = round_elt(v, odt);
-  }
-  if (RP) {  // 7. the next router's partials of this item (rows n0 of waves 0..3: elements [8 bx, 8 bx + 8))
-    __syncthreads();
-    if (int(threadIdx.x) < prow)
-      part[(size_t(t) * (H / 8) + blockIdx.x) * prow + threadIdx.x] = part_chain(xr, rw0, rw1, wdtn);
   }
 }
 
@@ -1398,7 +1309,6 @@ struct GateUpArgs {
   uint32_t *ids_out;
   float *scores_out;
   int ks = 0;  // slots a token when a shared expert is folded in (topk + 1); 0: topk
-  const float *part = nullptr;  // router partials [T][256][rows] in place of logits (x raw, prepared in-kernel)
 };
 
 template <int TG, int TU, int RB, int NC, int NW>
@@ -1435,7 +1345,7 @@ static int launch_gate_up_xr(const GateUpArgs &a, hipStream_t st) {
   auto kern = gate_up_rank_wg() ? k_gate_up_xr<TQ, P, RB, NPL, true> : k_gate_up_xr<TQ, P, RB, NPL, false>;
   launch(kern, grid, dim3(256), 0, st, a.xg_prep, a.slots, a.topk, a.wg, a.wu,
          a.n_experts, a.I, a.h, a.hprep, a.td, a.logits, a.ld_stride, a.norm, a.ids_out, a.scores_out,
-         a.ks ? a.ks : a.topk, nullptr, nullptr, 0);
+         a.ks ? a.ks : a.topk, nullptr, 0);
   LMOE_LAUNCHED("lmoe_gemv_gate_up");
   return 0;
 }
@@ -1445,36 +1355,9 @@ template <int TQ, int P>
 static int launch_gate_up_xr_raw(const GateUpArgs &a, hipStream_t st) {
   constexpr int RB = 2;
   const dim3 grid((a.I + 4 * RB - 1) / (4 * RB), a.n_slots);
-  launch(k_gate_up_xr<TQ, P, RB, 0, false, 4, false, true>, grid, dim3(256), 0, st, nullptr, a.slots, a.topk, a.wg,
-         a.wu, a.n_experts, a.I, a.h, a.hprep, a.td, nullptr, 0, 0, nullptr, nullptr, a.topk, nullptr, a.x, a.xdt);
+  launch(k_gate_up_xr<TQ, P, RB, 0, false, true>, grid, dim3(256), 0, st, nullptr, a.slots, a.topk, a.wg, a.wu,
+         a.n_experts, a.I, a.h, a.hprep, a.td, nullptr, 0, 0, nullptr, nullptr, a.topk, a.x, a.xdt);
   LMOE_LAUNCHED("lmoe_gemv_chain_gate_up");
-  return 0;
-}
-
-// Waves a workgroup of the partials kernel: 16 (192 workgroups at cfg2's shape) unless LMOE_PART_WAVES=8.
-static int part_waves() {
-  static const int nw = [] {
-    const char *v = getenv("LMOE_PART_WAVES");
-    return v && v[0] == '8' && v[1] == 0 ? 8 : 16;
-  }();
-  return nw;
-}
-
-template <int TQ, int NPL>
-static int launch_gate_up_rp(const GateUpArgs &a, hipStream_t st) {
-  constexpr int RB = 2;
-  auto go = [&](auto nw) {
-    constexpr int NW = decltype(nw)::value;
-    const dim3 grid((a.I + NW * RB - 1) / (NW * RB), a.n_slots);
-    launch(k_gate_up_xr<TQ, 32, RB, NPL, false, NW, true>, grid, dim3(64 * NW), 0, st, nullptr, nullptr, a.topk,
-           a.wg, a.wu, a.n_experts, a.I, a.h, a.hprep, a.td, nullptr, 0, a.norm, a.ids_out, a.scores_out,
-           a.ks ? a.ks : a.topk, a.part, a.x, a.xdt);
-  };
-  if (part_waves() == 8)
-    go(std::integral_constant<int, 8>());
-  else
-    go(std::integral_constant<int, 16>());
-  LMOE_LAUNCHED("lmoe_moe_gate_up_part");
   return 0;
 }
 
@@ -1491,14 +1374,6 @@ static int gate_up_xr_npl(const GateUpArgs &a, hipStream_t st) {
 template <int TG, int TU>
 static int gate_up_p(const GateUpArgs &a, hipStream_t st) {
   const int P = a.H / 64;
-  if (a.part) {  // router partials and raw x: the register-resident kernel, H = 2048, one type
-    if (TG != TU || P != 32 || a.I % 2 != 0 || !a.hprep)
-      return fail(LMOE_ESHAPE, "lmoe_moe_gate_up_part: takes hidden 2048, one type for gate and up, an even width "
-                               "and prepared h out (got hidden %d, width %d)", a.H, a.I);
-    if (a.n_experts <= 64) return launch_gate_up_rp<TG, 1>(a, st);
-    if (a.n_experts <= 128) return launch_gate_up_rp<TG, 2>(a, st);
-    return launch_gate_up_rp<TG, 4>(a, st);
-  }
   // prepared activations, one block type, 32 or 64 units a row: the register-resident kernel
   if (TG == TU && a.xg_prep && a.I % 2 == 0) {
     if (P == 32) return gate_up_xr_npl<TG, 32, 2>(a, st);
@@ -1555,8 +1430,8 @@ static int gate_up(const char *fn, const GateUpArgs &a_in, int type_g, int type_
   LMOE_REQUIRE(!a.hprep || (a.I % 64 == 0 && (a.td != LMOE_Q4_K || a.I % 256 == 0)), LMOE_ESHAPE,
                "%s: width %d cannot be prepared for ggml type %d", fn, a.I, a.td);
   if (a.n_slots == 0) return 0;
-  LMOE_REQUIRE((a.slots || a.logits || a.part) && (a.h || a.hprep), LMOE_EINVAL, "%s: null pointer", fn);
-  LMOE_REQUIRE(!(a.logits || a.part) || (a.ids_out && a.scores_out && a.topk <= 32 && a.topk <= a.n_experts &&
+  LMOE_REQUIRE((a.slots || a.logits) && (a.h || a.hprep), LMOE_EINVAL, "%s: null pointer", fn);
+  LMOE_REQUIRE(!a.logits || (a.ids_out && a.scores_out && a.topk <= 32 && a.topk <= a.n_experts &&
                                          a.n_experts <= 1024),
                LMOE_ESHAPE, "%s: top-k %d of %d experts is outside what the fused router takes", fn, a.topk,
                a.n_experts);
@@ -1582,10 +1457,6 @@ struct DownArgs {
   int rdt;
   void *out;
   int odt;
-  // the next layer's router partials (k_down_xr's RP epilogue); part null: none
-  const void *wrn = nullptr, *wsgn = nullptr;
-  int wdtn = 0, en = 0;
-  float *part = nullptr;
 };
 
 static int down(const char *fn, const DownArgs &a, void *stream) {
@@ -1595,7 +1466,7 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   LMOE_REQUIRE(!a.shared == !a.gate, LMOE_EINVAL, "%s: shared and gate go together", fn);
   if (!qtype_ok(a.type_d)) {  // a type beyond Q4_0 / Q4_K: the general chain
     // Q6_K and Q8_0 also read h prepared in the Q4_K / Q4_0 order
-    if (a.hprep && (a.type_d == LMOE_Q6_K || a.type_d == LMOE_Q8_0) && !a.part)
+    if (a.hprep && (a.type_d == LMOE_Q6_K || a.type_d == LMOE_Q8_0))
       return down_packed_prepped(fn, a.type_d, a.hprep, a.ids, a.scores, a.T, a.k, a.wd, a.n_experts, a.I, a.H,
                                  a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt,
                                  (hipStream_t)stream);
@@ -1613,16 +1484,6 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   {  // prepared h, at most 128 units a token, P even, H a multiple of 8: the register-resident kernel
     const int P = a.I / 64, U = a.k * P, CW = a.k * 9 * P / 2;
     const int kh = (a.k + 1) / 2, Uh = kh * P, CWh = kh * 9 * P / 2;
-    if (a.part) {
-      LMOE_REQUIRE(a.hprep && U <= 128 && P % 2 == 0 && a.H % 8 == 0 && CW <= 64 * 9, LMOE_ESHAPE,
-                   "%s: the next router's partials need the one-wavefront-a-row-pair kernel: at most 128 h units a "
-                   "token (got %d slots of %d units) and an even unit count", fn, a.k, P);
-      LMOE_REQUIRE(a.H / 8 <= kPartItems && a.en > 0 && a.en + (a.wsgn ? 1 : 0) <= kPartRows, LMOE_ESHAPE,
-                   "%s: router partials take hidden <= %d and 1..%d router rows (got %d, %d)", fn, 8 * kPartItems,
-                   kPartRows, a.H, a.en + (a.wsgn ? 1 : 0));
-      LMOE_REQUIRE(dtype_ok(a.wdtn) && a.wrn && aligned16(a.wrn) && (!a.wsgn || aligned16(a.wsgn)), LMOE_EALIGN,
-                   "%s: the next router's weights must be given, 16-byte aligned, of a known dtype", fn);
-    }
     if (a.hprep && !(U <= 128 && CW <= 64 * 9) && Uh <= 128 && P % 2 == 0 && a.H % 4 == 0 && CWh <= 64 * 9) {
       // up to 256 units: two wavefronts a row pair, half of the experts each (config 1 with its shared expert
       // folded in as four slices: 8 experts of 22 units)
@@ -1631,7 +1492,7 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
         constexpr int TD = decltype(td)::value, N = decltype(nu)::value, C = decltype(nc)::value;
         launch(k_down_xr<TD, N, C, 2>, dim3(a.H / 4, a.T), dim3(256), size_t(4) * 4 * CWh * 4, st, a.hprep, a.ids,
                a.scores, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt,
-               a.out, a.odt, nullptr, nullptr, 0, 0, nullptr);
+               a.out, a.odt);
       };
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;
@@ -1658,14 +1519,9 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
       const int NU = U <= 64 ? 1 : 2, ncw = (CW + 63) / 64;
       auto go = [&](auto td, auto nu, auto nc) {
         constexpr int TD = decltype(td)::value, N = decltype(nu)::value, C = decltype(nc)::value;
-        if (a.part)
-          launch(k_down_xr<TD, N, C, 1, true>, dim3(a.H / 8, a.T), dim3(256), size_t(4) * 4 * CW * 4, st, a.hprep,
-                 a.ids, a.scores, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual,
-                 a.rdt, a.out, a.odt, a.wrn, a.wsgn, a.wdtn, a.en, a.part);
-        else
-          launch(k_down_xr<TD, N, C>, dim3(a.H / 8, a.T), dim3(256), size_t(4) * 4 * CW * 4, st, a.hprep, a.ids,
-                 a.scores, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt,
-                 a.out, a.odt, nullptr, nullptr, 0, 0, nullptr);
+        launch(k_down_xr<TD, N, C>, dim3(a.H / 8, a.T), dim3(256), size_t(4) * 4 * CW * 4, st, a.hprep, a.ids,
+               a.scores, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out,
+               a.odt);
       };
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;
@@ -2060,27 +1916,6 @@ extern "C" int lmoe_moe_gate_up_h(const float *logits, int ld_stride, int T, int
   return gate_up(fn, a, type, type, stream);
 }
 
-extern "C" int lmoe_moe_gate_up_part(const float *part, const void *x, int xdtype, int T, int k, int norm,
-                                     const uint8_t *wg, const uint8_t *wu, int type_g, int type_u, int n_experts,
-                                     int H, int I, uint32_t *ids, float *scores, uint32_t *hprep, int type_d,
-                                     int shared_slices, void *stream) {
-  const char *fn = "lmoe_moe_gate_up_part";
-  LMOE_REQUIRE(dtype_ok(xdtype), LMOE_EINVAL, "%s: x dtype %d is not F32, F16 or BF16", fn, xdtype);
-  LMOE_REQUIRE(shared_slices >= 0 && k >= 1 && k + shared_slices <= 64, LMOE_ESHAPE,
-               "%s: k %d with %d shared slices", fn, k, shared_slices);
-  LMOE_REQUIRE(H == 8 * kPartItems, LMOE_ESHAPE, "%s: router partials take hidden %d (got %d)", fn, 8 * kPartItems,
-               H);
-  LMOE_REQUIRE(n_experts > 0 && n_experts + (shared_slices ? 1 : 0) <= kPartRows, LMOE_ESHAPE,
-               "%s: %d router rows is outside 1..%d", fn, n_experts + (shared_slices ? 1 : 0), kPartRows);
-  LMOE_REQUIRE(T == 0 || (part && x && aligned16(x) && aligned16(part)), LMOE_EALIGN,
-               "%s: partials and a 16-byte aligned x must be given", fn);
-  LMOE_REQUIRE(!shared_slices || type_g == type_u, LMOE_ETYPE, "%s: a folded shared expert takes one type", fn);
-  const int ks = k + shared_slices;
-  GateUpArgs a{nullptr, nullptr, x, xdtype, nullptr, T * ks, k, wg, wu, n_experts, H, I, nullptr, hprep, type_d,
-               nullptr, 0, norm, ids, scores, shared_slices ? ks : 0, part};
-  return gate_up(fn, a, type_g, type_u, stream);
-}
-
 extern "C" int lmoe_gemv_down_combine(const float *h, const uint32_t *ids, const float *scores, int T, int k,
                                       const uint8_t *wd, int type_d, int n_experts, int I, int H, const float *shared,
                                       const float *gate, int gate_stride, const void *residual, int rdtype,
@@ -2099,19 +1934,6 @@ extern "C" int lmoe_gemv_down_combine_prepped(const uint32_t *hprep, int has_sum
   DownArgs a{hprep, has_sums, nullptr, ids, scores, T, k, wd, type_d, n_experts, I, H, shared, gate, gate_stride,
              residual, rdtype, out, odtype};
   return down("lmoe_gemv_down_combine_prepped", a, stream);
-}
-
-extern "C" int lmoe_gemv_down_combine_part(const uint32_t *hprep, const uint32_t *ids, const float *scores, int T,
-                                           int k, const uint8_t *wd, int type_d, int n_experts, int I, int H,
-                                           const void *residual, int rdtype, void *out, int odtype, const void *wr_next,
-                                           const void *wsg_next, int wdtype_next, int e_next, float *part,
-                                           void *stream) {
-  const char *fn = "lmoe_gemv_down_combine_part";
-  LMOE_REQUIRE(hprep && part, LMOE_EINVAL, "%s: null pointer", fn);
-  LMOE_REQUIRE(qtype_ok(type_d), LMOE_ETYPE, "%s: ggml type %d is not supported (Q4_0 = 2, Q4_K = 12)", fn, type_d);
-  DownArgs a{hprep, 0, nullptr, ids, scores, T, k, wd, type_d, n_experts, I, H, nullptr, nullptr, 0, residual,
-             rdtype, out, odtype, wr_next, wsg_next, wdtype_next, e_next, part};
-  return down(fn, a, stream);
 }
 
 extern "C" int lmoe_gemv_gate_up_runs(const void *x, int xdtype, const uint32_t *slots, int n, int run_rows,

@@ -550,13 +550,6 @@ __device__ __forceinline__ void unpack8(const u32x4 &a, const u32x4 &b, int dt, 
   }
 }
 
-// v as the element it becomes when stored as dtype dt and read back (the value a later kernel reads)
-__device__ __forceinline__ float round_elt(float v, int dt) {
-  if (dt == LMOE_F32) return v;
-  if (dt == LMOE_F16) return float(_Float16(v));
-  return bf16_to_f32(f32_to_bf16(v));
-}
-
 // Position of natural element n (a multiple of 4) of a row in the GEMMs' K order: within each 32-wide block,
 // group n4 = (n % 32) / 4 sits at 8 n4 (n4 < 4) or 8 (n4 - 4) + 4
 __device__ __forceinline__ int kperm4(int n) {
@@ -578,28 +571,6 @@ __device__ __forceinline__ void to_f16_kperm(int block, const void *x, int dt, l
     *reinterpret_cast<u32x2 *>(out + b + kperm4(int(i0 & 31) + 4 * h)) =
         u32x2{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1)};
   }
-}
-
-// ---- router partials -------------------------------------------------------------------------------------------
-//
-// The decode router's logits are sums over 8-element items of x (item i: elements [8 i, 8 i + 8)). k_router_gemv
-// (router.hip) forms each item's products as one fma chain from zero, adds the chains of its 256 threads as a
-// balanced tree over each wavefront's 64 items, then the four wavefront totals left to right. When H / 8 <= 256 each
-// thread holds exactly one item, so the logits can be rebuilt bit for bit from the item chains alone: partials
-// [T][H / 8][R] (R router rows, the shared expert's gate row last) written by whoever owns the item's 8 values, then
-// summed in that same tree (items past H / 8 add a +0). That lets the kernel that produces x (the previous layer's
-// down) emit the next router's partials, and the kernel that consumes the logits (gate/up) finish them.
-constexpr int kPartItems = 256;  // items a token at most: H <= 2048
-constexpr int kPartRows = 256;   // router rows at most (experts + the shared expert's gate)
-
-// item i's fma chain against router row r (8 weights of element type wdt: one 16-byte chunk, two for f32)
-__device__ __forceinline__ float part_chain(const float *x8, const u32x4 &w0, const u32x4 &w1, int wdt) {
-  float w[8];
-  unpack8(w0, w1, wdt, w);
-  float acc = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc = fmaf(x8[e], w[e], acc);
-  return acc;
 }
 
 // ---- x arrangement ----------------------------------------------------------------------------------------------

@@ -140,26 +140,6 @@ __global__ void __launch_bounds__(256)
         ((part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x]) + part[3][threadIdx.x];
 }
 
-// Router partials of x on their own (the first layer of a stack, whose x comes from outside): workgroup (i, t)
-// forms item i of token t against every router row (thread r: row r, r + 256, ...; the shared expert's gate row E
-// when wsg is given), the same fma chain k_router_gemv's thread i forms.
-__global__ void __launch_bounds__(256) k_router_part(const void *x, int xdt, const void *wr, const void *wsg, int wdt,
-                                                     int H, int E, float *part) {
-  const int i = blockIdx.x, t = blockIdx.y, nit = H / 8, rows = E + (wsg ? 1 : 0);
-  const int esz = wdt == LMOE_F32 ? 4 : 2, xsz = xdt == LMOE_F32 ? 4 : 2;
-  const char *xi = static_cast<const char *>(x) + (size_t(t) * H + 8 * i) * xsz;
-  const u32x4 x0 = *reinterpret_cast<const u32x4 *>(xi), x1 = *reinterpret_cast<const u32x4 *>(xi + 16 * (xsz / 4));
-  float xv[8];
-  unpack8(x0, x1, xdt, xv);
-  for (int r = threadIdx.x; r < rows; r += 256) {
-    const char *w = (r < E ? static_cast<const char *>(wr) + size_t(r) * H * esz : static_cast<const char *>(wsg)) +
-                    size_t(8) * i * esz;
-    const u32x4 w0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w));
-    const u32x4 w1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w + 16 * (esz / 4)));
-    part[(size_t(t) * nit + i) * rows + r] = part_chain(xv, w0, w1, wdt);
-  }
-}
-
 // Prepared activation rows on their own: one workgroup a row, one thread a unit dword.
 template <int TQ>
 __global__ void __launch_bounds__(256) k_prep_x(const void *x, int xdt, int H, uint32_t *xprep) {
@@ -739,24 +719,6 @@ extern "C" int lmoe_router_gemv(const void *x, int xdtype, const void *wr, const
     launch_router<LMOE_BF16>(qtype, grid, block, st, x, xdtype, wr, wsg, T, H, E, logits, xprep);
   else
     launch_router<LMOE_F32>(qtype, grid, block, st, x, xdtype, wr, wsg, T, H, E, logits, xprep);
-  LMOE_LAUNCHED(fn);
-  return 0;
-}
-
-extern "C" int lmoe_router_part(const void *x, int xdtype, const void *wr, const void *wsg, int wdtype, int T, int H,
-                                int E, float *part, void *stream) {
-  const char *fn = "lmoe_router_part";
-  LMOE_REQUIRE(dtype_ok(xdtype) && dtype_ok(wdtype), LMOE_EINVAL, "%s: bad dtype", fn);
-  LMOE_REQUIRE(T > 0 && T <= kRouterMaxT, LMOE_ESHAPE, "%s: %d tokens is outside 1..%d", fn, T, kRouterMaxT);
-  LMOE_REQUIRE(H > 0 && H % 64 == 0 && H / 8 <= kPartItems, LMOE_ESHAPE,
-               "%s: hidden %d is not a multiple of 64 up to %d (one 8-element item a router thread)", fn, H,
-               8 * kPartItems);
-  LMOE_REQUIRE(E > 0 && E + (wsg ? 1 : 0) <= kPartRows, LMOE_ESHAPE, "%s: %d router rows is outside 1..%d", fn,
-               E + (wsg ? 1 : 0), kPartRows);
-  LMOE_REQUIRE(x && wr && part, LMOE_EINVAL, "%s: null pointer", fn);
-  LMOE_REQUIRE(aligned16(x) && aligned16(wr) && (!wsg || aligned16(wsg)), LMOE_EALIGN,
-               "%s: x, wr and wsg must be 16-byte aligned", fn);
-  launch(k_router_part, dim3(H / 8, T), dim3(256), 0, (hipStream_t)stream, x, xdtype, wr, wsg, wdtype, H, E, part);
   LMOE_LAUNCHED(fn);
   return 0;
 }

@@ -26,29 +26,6 @@ from ._lib import call, dcode, ptr, qcode, stream
 RANKED_ROUTER = False
 RANK_MAX_E, RANK_MAX_K = 512, 16  # the router-and-rank kernel's limits
 
-# Whether a decode layer on the prepared chain runs gate/up and down as one launch (lmoe_moe_fused: the down
-# workgroups rank the logits themselves and wait for h in the same grid) instead of two. Off unless LMOE_FUSED=1: on
-# cfg2's 48-layer graph it measured 16.2 us a layer (down's weights requested early; 20.5 requested once h is complete)
-# against 14.7 for the two launches. A workgroup's stamps put the loss in the hand-off: a device-coherent store seen by
-# a poller on another XCD takes 1.5-3 us while the weights stream, as long as the kernel boundary it replaces. Tests
-# switch it through this flag.
-FUSED = os.environ.get("LMOE_FUSED", "0") == "1"
-
-
-def fused_ok(layer, T):
-    """Whether ``layer`` at T tokens fits the one-launch gate/up + down (lmoe_moe_fused): all three projections of
-    one Q4 type, hidden 2048 or 4096, any shared expert folded in, at most 128 h units a token."""
-    L = layer
-    t = L.types
-    if not (t[0] == t[1] == t[2] and t[0] in _lib.Q4_TYPES):
-        return False
-    if L.H not in (2048, 4096) or L.I % 64 or (t[2] == "Q4_K" and L.I % 256) or L.I % 16:
-        return False
-    if L.shared is not None and L.folded is None:
-        return False
-    ks = L.k + L.n_shared
-    return 1 <= T <= 16 and ks * (L.I // 64) <= 128 and L.k <= 32 and ks <= 64 and L.E <= 1024
-
 
 class MoELayer:
     """A layer's weights (all on the GPU):
@@ -219,21 +196,6 @@ class DecodeBuffers:
             self.h32 = torch.empty((T * ks, L.I), **f32)
             if L.shared is not None and L.folded is None:
                 self.h32_s = torch.empty((T, L.Is), **f32)
-        # the one-launch gate/up + down's workspace (status, per-workgroup launch counts, epoch-tagged h words),
-        # zeroed once; its grid is this buffer's T and the layer shape, which every call over it keeps
-        self.fused_ws = None
-        if fused_ok(L, T):
-            n = _lib.lib().lmoe_moe_fused_workspace_bytes(T, L.k, L.n_shared, L.H, L.I)
-            self.fused_ws = torch.zeros(n // 4, dtype=torch.int32, device=device)
-
-    def fused_status(self):
-        """0, or the epoch of the last one-launch gate/up + down whose wait for h ran out (its output rows are NaN).
-        Synchronises the current stream."""
-        if self.fused_ws is None:
-            return 0
-        v = ctypes.c_uint32(0)
-        call("lmoe_moe_fused_status", ptr(self.fused_ws), ctypes.byref(v), stream())
-        return int(v.value)
 
 
 def prepared_chain(layer):
@@ -355,13 +317,6 @@ def decode(layer, x, bufs, out, residual=None, logits=None):
     if B.xprep_u is not None:
         call("lmoe_prep_x", ptr(x), xd, T, L.H, tu, ptr(B.xprep_u), st)
         xu = B.xprep_u
-    if FUSED and not ranked and B.fused_ws is not None and T == B.T:
-        wg, wu, wd = L.folded if L.folded is not None else (L.wg, L.wu, L.wd)
-        call("lmoe_moe_fused", ptr(lg), stride, T, L.k, int(L.norm), ptr(B.xprep), ptr(wg), ptr(wu), ptr(wd), tg,
-             td, L.E, L.H, L.I, L.n_shared, ptr(B.ids_ext), ptr(B.scores_ext), None, ptr(residual),
-             dcode(residual.dtype) if residual is not None else 0, ptr(out), dcode(out.dtype), ptr(B.fused_ws),
-             B.fused_ws.numel() * 4, st)
-        return out
     if L.folded is not None:  # the shared expert's m slices as slots k .. k + m - 1: gate/up, then down + combine
         fg, fu, fd = L.folded
         ks = L.k + L.n_shared
@@ -398,59 +353,6 @@ def decode(layer, x, bufs, out, residual=None, logits=None):
     return out
 
 
-# Router partials (lmoe_router_part / lmoe_moe_gate_up_part / lmoe_gemv_down_combine_part): hidden 2048 (one 8-value
-# item a router thread), at most 256 router rows, and the down kernel that takes a row pair a wavefront.
-PART_ITEMS, PART_ROWS = 256, 256
-# Whether a DecodeStack whose layers all allow it folds each router GEMV into its neighbours: the previous layer's
-# down writes the item partials of the next router, gate/up sums them (two launches a layer instead of three, the
-# same bits). Off unless LMOE_ROUTER_PARTS=1: on cfg2's 48-layer graph it measured 22.2 us a layer against 15.0
-# for the three-launch chain (every 16-wavefront gate/up workgroup reads all 256 x E partials, written by other
-# XCDs, and the wider workgroups, the in-kernel x preparation and the extra barriers cost more than the launch).
-ROUTER_PARTS = os.environ.get("LMOE_ROUTER_PARTS", "0") == "1"
-
-
-def part_ok(layer):
-    """Whether ``layer`` can take its logits as router partials (and its down can emit the next layer's)."""
-    L = layer
-    if L.wr is None or (L.shared is not None and L.folded is None) or L.H != 8 * PART_ITEMS:
-        return False
-    if (L.wsg is not None) != (L.folded is not None):  # the gate row travels with the folded shared expert only
-        return False
-    if L.E + (1 if L.wsg is not None else 0) > PART_ROWS or L.types[0] != L.types[1]:
-        return False
-    if any(t not in ("Q4_0", "Q4_K") for t in L.types) or L.I % 64 or (L.types[2] == "Q4_K" and L.I % 256):
-        return False
-    ks, P = L.k + L.n_shared, L.I // 64
-    return P % 2 == 0 and ks * P <= 128 and ks * 9 * P // 2 <= 576 and ks <= 64 and L.k <= 32
-
-
-def decode_part(layer, x, bufs, out, part, nxt=None):
-    """out = x + layer(x) with the router logits summed from ``part`` (the item partials of x against this layer's
-    router, written by lmoe_router_part or the previous layer's down), gate/up then down; when ``nxt`` is given the
-    down also writes x_out's partials against nxt's router into ``part`` (after gate/up has read them, in stream
-    order). Same bits as ``decode(layer, x, bufs, out, residual=x)``."""
-    L, B = layer, bufs
-    T = x.shape[0]
-    st = stream()
-    tg, tu, td = (qcode(t) for t in L.types)
-    xd = dcode(x.dtype)
-    if L.folded is not None:
-        (wg, wu, wd), m = L.folded, L.n_shared
-    else:
-        wg, wu, wd, m = L.wg, L.wu, L.wd, 0
-    ks = L.k + m
-    call("lmoe_moe_gate_up_part", ptr(part), ptr(x), xd, T, L.k, int(L.norm), ptr(wg), ptr(wu), tg, tu, L.E, L.H,
-         L.I, ptr(B.ids_ext), ptr(B.scores_ext), ptr(B.hprep), td, m, st)
-    if nxt is None:
-        call("lmoe_gemv_down_combine_prepped", ptr(B.hprep), 0, ptr(B.ids_ext), ptr(B.scores_ext), T, ks, ptr(wd), td,
-             L.E + m, L.I, L.H, None, None, 0, ptr(x), xd, ptr(out), dcode(out.dtype), st)
-    else:
-        call("lmoe_gemv_down_combine_part", ptr(B.hprep), ptr(B.ids_ext), ptr(B.scores_ext), T, ks, ptr(wd), td,
-             L.E + m, L.I, L.H, ptr(x), xd, ptr(out), dcode(out.dtype), ptr(nxt.wr), ptr(nxt.wsg),
-             dcode(nxt.wr.dtype), nxt.E, ptr(part), st)
-    return out
-
-
 def _ptr_offset(t, elems):
     """Device pointer ``elems`` elements into tensor t."""
     return ctypes.c_void_p(t.data_ptr() + elems * t.element_size())
@@ -461,7 +363,7 @@ class DecodeStack:
     fused into each layer's combine. ``step`` runs eagerly; ``capture`` records one step as a HIP graph reading
     ``self.x_in`` and leaving the result in ``self.x_out``."""
 
-    def __init__(self, layers, T, dtype=torch.float16, device="cuda", parts=None):
+    def __init__(self, layers, T, dtype=torch.float16, device="cuda"):
         self.layers = layers
         self.T = T
         self.bufs = DecodeBuffers(layers[0], T, device)
@@ -470,28 +372,12 @@ class DecodeStack:
         self.ping = torch.empty((T, H), dtype=dtype, device=device)
         self.pong = torch.empty((T, H), dtype=dtype, device=device)
         self.graph = None
-        # the router folded into its neighbours (decode_part) when every layer allows it
-        self.parts = (ROUTER_PARTS if parts is None else parts) and all(part_ok(L) for L in layers)
-        if parts and not self.parts:
-            raise ValueError("router partials need hidden 2048, at most 256 router rows, one gate/up type and at "
-                             "most 128 h units a token in every layer")
-        if self.parts:
-            rows = max(L.E + (1 if L.wsg is not None else 0) for L in layers)
-            self.part = torch.empty(T * PART_ITEMS * rows, dtype=torch.float32, device=device)
 
     def step(self):
         cur = self.x_in
-        if self.parts:
-            L0 = self.layers[0]
-            call("lmoe_router_part", ptr(cur), dcode(cur.dtype), ptr(L0.wr), ptr(L0.wsg), dcode(L0.wr.dtype), self.T,
-                 L0.H, L0.E, ptr(self.part), stream())
         for i, L in enumerate(self.layers):
             nxt = self.ping if i % 2 == 0 else self.pong
-            if self.parts:
-                decode_part(L, cur, self.bufs, nxt, self.part,
-                            self.layers[i + 1] if i + 1 < len(self.layers) else None)
-            else:
-                decode(L, cur, self.bufs, nxt, residual=cur)
+            decode(L, cur, self.bufs, nxt, residual=cur)
             cur = nxt
         self.x_out = cur
         return cur

@@ -60,28 +60,14 @@ def _exact_products(x, w, H):
     return (w[None, :, :] * x[:, None, :]).astype(np.float32)  # [T, E, H]; f16 / bf16 products are exact in fp32
 
 
-def router_logits_stack(x, w, lanes=512):
-    """Router logits [T, E] of x [T, H] and w [E, H] in the fused decode stack's order (larder_amd/csrc/stack.hip,
-    phase A): lane t of ``lanes`` sums the products of elements [C t, C t + C) (C = H / lanes) in element order, the
-    first product alone, then the lanes' partials are added as a balanced binary tree in lane order. Exact for f16
-    or bf16 x and w, whose products float32 holds without rounding (each step then rounds once, as the GPU's fused
-    multiply-add does). This is this build's reduction order, not the reference's: its router is an MLX matmul
-    (stream_fast.py:4352-4356) whose order MLX does not fix."""
-    H = np.asarray(x).shape[-1]
-    C = H // lanes
-    p = _exact_products(x, w, H).reshape(-1, np.asarray(w).reshape(-1, H).shape[0], lanes, C)
-    s = p[..., 0]
-    for j in range(1, C):
-        s = (s + p[..., j]).astype(np.float32)
-    return _tree(s)
-
-
 def router_logits_gemv(x, w):
     """Router logits [T, E] in the order of the per-layer router GEMV (larder_amd/csrc/router.hip k_router_gemv):
     thread i of 256 sums, in order, the products of its 8-element items i, i + 256, ... (item j covers elements
     [8 j, 8 j + 8)), starting from zero; each wavefront's 64 partials are added as a balanced binary tree in lane
-    order; the four wavefronts' totals are added left to right. Exact for f16 / bf16 inputs (see
-    router_logits_stack). Tokens go in chunks and the 256 threads' chains side by side, step by step, so a cfg5
+    order; the four wavefronts' totals are added left to right. Exact for f16 / bf16 inputs, whose products fp32
+    holds without rounding (each step then rounds once, as the GPU's fused multiply-add does); this is this build's
+    order, not the reference's: its router is an MLX matmul (stream_fast.py:4352-4356) whose order MLX does not
+    fix. Tokens go in chunks and the 256 threads' chains side by side, step by step, so a cfg5
     prefill (2048 tokens, 513 rows of 4096) runs in seconds."""
     x = np.asarray(x, np.float32)
     H = x.shape[-1]
@@ -114,35 +100,6 @@ def router_logits_gemv(x, w):
         out[t0:t0 + chunk] = (((waves[..., 0] + waves[..., 1]).astype(np.float32) + waves[..., 2]).astype(np.float32)
                               + waves[..., 3]).astype(np.float32)
     return out
-
-
-def router_partials(x, w):
-    """Item chains [T, H / 8, R] of the router GEMV's order (larder_amd/csrc/router.hip k_router_gemv with one item
-    a thread, H <= 2048; emitted by lmoe_router_part and by the down kernel for the next layer): item i of token t
-    against row r adds the products x[t, 8 i + j] w[r, 8 i + j], j = 0..7, in order from zero in float32. Exact
-    products for f16 / bf16 inputs, so these are the fma chain's bits."""
-    x = np.asarray(x, np.float32)
-    H = x.shape[-1]
-    p = _exact_products(x, w, H)
-    T, R = p.shape[:2]
-    p = p.reshape(T, R, H // 8, 8)
-    acc = np.zeros((T, R, H // 8), np.float32)
-    for j in range(8):
-        acc = (acc + p[..., j]).astype(np.float32)
-    return np.ascontiguousarray(acc.transpose(0, 2, 1))
-
-
-def router_logits_from_partials(part):
-    """Logits [T, R] from item chains [T, n, R] (n <= 256 items; the rest count as +0) in k_router_gemv's tree:
-    a balanced tree over each wavefront's 64 items, then the four wavefront totals left to right (the sum that
-    lmoe_moe_gate_up_part forms before its top-k)."""
-    part = np.asarray(part, np.float32)
-    T, n, R = part.shape
-    acc = np.zeros((T, R, 256), np.float32)
-    acc[:, :, :n] = part.transpose(0, 2, 1)
-    waves = _tree(acc.reshape(T, R, 4, 64))
-    return (((waves[..., 0] + waves[..., 1]).astype(np.float32) + waves[..., 2]).astype(np.float32)
-            + waves[..., 3]).astype(np.float32)
 
 
 def group_rows(ids, n_experts):

@@ -125,32 +125,20 @@ def test_refusals_without_a_gpu(built_lib):
     assert rc == _lib.ESHAPE and b"top-k 33" in L.lmoe_error()
     rc = L.lmoe_router_gemm_topk(p, 64, 2048, p, 128, 0, p, p, None, 8, 1, 1, p, p, None)
     assert rc == _lib.EINVAL and b"gate row" in L.lmoe_error()
-    # router partials: hidden 2048 (one item a router thread), at most 256 router rows, the row-pair down kernel
-    rc = L.lmoe_router_part(p, _lib.F16, p, None, _lib.F16, 1, 4096, 128, p, None)
-    assert rc == _lib.ESHAPE and b"one 8-element item" in L.lmoe_error()
-    rc = L.lmoe_router_part(p, _lib.F16, p, p, _lib.F16, 1, 2048, 256, p, None)
-    assert rc == _lib.ESHAPE and b"257 router rows" in L.lmoe_error()
-    rc = L.lmoe_router_part(ctypes.c_void_p(18), _lib.F16, p, None, _lib.F16, 1, 2048, 128, p, None)
-    assert rc == _lib.EALIGN
-    rc = L.lmoe_moe_gate_up_part(p, p, _lib.F16, 1, 8, 1, p, p, _lib.Q4_K, _lib.Q4_K, 512, 4096, 512, p, p, p,
-                                 _lib.Q4_K, 1, None)
-    assert rc == _lib.ESHAPE and b"hidden 2048" in L.lmoe_error()
-    rc = L.lmoe_moe_gate_up_part(p, p, _lib.F16, 1, 8, 1, p, p, _lib.Q4_0, _lib.Q4_0, 256, 2048, 768, p, p, p,
-                                 _lib.Q4_0, 1, None)
-    assert rc == _lib.ESHAPE and b"257 router rows" in L.lmoe_error()
-    rc = L.lmoe_moe_gate_up_part(p, p, _lib.F16, 1, 8, 1, p, p, _lib.Q4_0, _lib.Q4_K, 128, 2048, 768, p, p, p,
-                                 _lib.Q4_0, 0, None)
-    assert rc == _lib.ESHAPE and b"one type" in L.lmoe_error()
-    # 8 slots of 22 units (cfg1's folded shape) need two wavefronts a row pair: no partials there
-    rc = L.lmoe_gemv_down_combine_part(p, p, p, 1, 8, p, _lib.Q4_0, 64, 1408, 2048, p, _lib.F16, p, _lib.F16, p,
-                                       p, _lib.F16, 60, p, None)
-    assert rc == _lib.ESHAPE and b"128 h units" in L.lmoe_error()
-    rc = L.lmoe_gemv_down_combine_part(p, p, p, 1, 8, p, _lib.Q4_0, 128, 768, 2048, p, _lib.F16, p, _lib.F16, p,
-                                       None, _lib.F16, 300, p, None)
-    assert rc == _lib.ESHAPE and b"router rows" in L.lmoe_error()
-    rc = L.lmoe_gemv_down_combine_part(p, p, p, 1, 8, p, _lib.Q4_0, 128, 768, 2048, p, _lib.F16, p, _lib.F16,
-                                       ctypes.c_void_p(18), None, _lib.F16, 128, p, None)
-    assert rc == _lib.EALIGN
+    # the drop-in chain's register-resident form: hidden 2048 / 4096, one Q4 type, h or its prepared rows asked for;
+    # its down: a width that is a multiple of 128 up to 8192
+    rc = L.lmoe_gemv_chain_gate_up(p, _lib.F16, p, 8, 8, p, p, _lib.Q4_0, 128, 1024, 768, p, p, _lib.Q4_0, None)
+    assert rc == _lib.ESHAPE and b"hidden 2048 or 4096" in L.lmoe_error()
+    rc = L.lmoe_gemv_chain_gate_up(p, _lib.F16, p, 8, 8, p, p, 14, 128, 2048, 768, p, p, _lib.Q4_0, None)
+    assert rc == _lib.ETYPE
+    rc = L.lmoe_gemv_chain_gate_up(p, _lib.F16, p, 8, 8, p, p, _lib.Q4_0, 128, 2048, 768, None, None, _lib.Q4_0, None)
+    assert rc == _lib.EINVAL and b"neither h" in L.lmoe_error()
+    rc = L.lmoe_gemv_chain_down(p, p, 8, p, _lib.Q4_0, 128, 704, 2048, p, _lib.F16, None)
+    assert rc == _lib.ESHAPE and b"multiple of 128" in L.lmoe_error()
+    rc = L.lmoe_gemv_down_runs_prepped(p, p, 8, 4, p, _lib.Q4_0, 128, 704, 2048, p, _lib.F16, None)
+    assert rc == _lib.ESHAPE and b"multiple of 128" in L.lmoe_error()
+    rc = L.lmoe_gemv_gate_up_runs_prepped(p, p, 8, 4, p, p, _lib.Q4_K, 128, 2048, 767, p, None, _lib.Q4_K, None)
+    assert rc == _lib.ESHAPE and b"even width" in L.lmoe_error()
 
 
 def test_grouped_refusals_without_a_gpu(built_lib):

@@ -1,4 +1,4 @@
-"""Pins of the oracle's two router-logit restatements (oracle.moe.router_logits_stack / router_logits_gemv).
+"""Pins of the oracle's router-logit restatement (oracle.moe.router_logits_gemv).
 
 The GPU kernels sum x . w in a fixed order, and the oracle restates that order so that the expert ids can be
 checked bit for bit from x and the router weight. These cases are built so that the order decides the result
@@ -24,39 +24,13 @@ def _one_hot_products(H, placements):
     return x, w
 
 
-def test_stack_order_small_integers_equal_exact_dot():
+def test_gemv_order_small_integers_equal_exact_dot():
     rng = np.random.default_rng(0)
     for H in (2048, 4096):
         x = rng.integers(-3, 4, (3, H)).astype(np.float16)
         w = rng.integers(-3, 4, (5, H)).astype(np.float16)
         want = x.astype(np.float64) @ w.astype(np.float64).T
-        assert np.array_equal(moe.router_logits_stack(x, w), want.astype(np.float32))
         assert np.array_equal(moe.router_logits_gemv(x, w), want.astype(np.float32))
-
-
-def test_stack_order_chunk_then_tree():
-    # H 2048, 512 lanes of C = 4. Lane 0: 2^24 then three 1s -> each +1 rounds back: 2^24. Lane 1: 1,1,1,1 -> 4.
-    # Tree: ((2^24 + 4) + 0 ...) = 2^24 + 4 exactly. Sequential over all elements would lose lane 1's ones too
-    # (2^24); a tree over single elements would give 2^24 + 2 + 2 + ... = 2^24 + 6 + ... paths.
-    x, w = _one_hot_products(2048, [(0, BIG), (1, 1), (2, 1), (3, 1), (4, 1), (5, 1), (6, 1), (7, 1)])
-    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24 + 4)
-    # the same products with lane 1's ones moved to lane 256 (the other half of the tree): still 2^24 + 4
-    x, w = _one_hot_products(2048, [(0, BIG), (1, 1), (2, 1), (3, 1), (1024, 1), (1025, 1), (1026, 1), (1027, 1)])
-    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24 + 4)
-    # H 4096: C = 8. Lane 0 holds elements 0..7: 2^24 + seven 1s -> 2^24; lane 1 (elements 8..15) eight 1s -> 8
-    x, w = _one_hot_products(4096, [(0, BIG)] + [(i, 1) for i in range(1, 16)])
-    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24 + 8)
-
-
-def test_stack_order_tree_pairs_neighbours():
-    # partials: lane 0 = 2^24, lanes 1 and 2 = 1 each (others 0). Tree: (2^24 + 1) + (1 + 0) -> 2^24 + 1 = 2^24 at
-    # the first level (round to even), then 2^24 + 1 -> 2^24. Result 2^24. If the tree paired lane 0 with lane 256
-    # first, the ones would meet each other first and give 2^24 + 2.
-    x, w = _one_hot_products(2048, [(0, BIG), (4, 1), (8, 1)])
-    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24)
-    # lanes 2 and 3 = 1 each: (2^24 + 0) + (1 + 1) = 2^24 + 2
-    x, w = _one_hot_products(2048, [(0, BIG), (8, 1), (12, 1)])
-    assert moe.router_logits_stack(x, w)[0, 0] == np.float32(2.0 ** 24 + 2)
 
 
 def test_gemv_order_waves_left_to_right():
@@ -82,44 +56,15 @@ def test_gemv_order_items_of_a_thread():
 
 
 def test_planted_order_mistake_is_caught():
-    """A restatement that sums a lane's chunk as a tree instead of in element order gives a different value on the
-    case above: the pins would catch that mistake."""
-    x, w = _one_hot_products(2048, [(0, BIG), (1, 1), (2, 1), (3, 1), (4, 1), (5, 1), (6, 1), (7, 1)])
-    p = (x.astype(np.float32) * w.astype(np.float32)).reshape(512, 4)
-    wrong = moe._tree(moe._tree(p))   # tree inside the chunk: (2^24 + 1) + (1 + 1) = 2^24 + 2 for lane 0
-    assert wrong != moe.router_logits_stack(x, w)[0, 0]
-
-
-def test_partials_rebuild_the_gemv_order():
-    """The item chains (oracle.moe.router_partials, the decode stack's router partials) summed in the router's tree
-    give router_logits_gemv's bits: on random f16 rows (H 2048: 256 items; H 1024: items past 128 count as +0) and
-    on the order-deciding one-hot cases above."""
-    rng = np.random.default_rng(7)
-    for H in (2048, 1024):
-        x = (rng.standard_normal((3, H)) * 4).astype(np.float16)
-        w = (rng.standard_normal((9, H)) * 4).astype(np.float16)
-        part = moe.router_partials(x, w)
-        assert part.shape == (3, H // 8, 9)
-        assert np.array_equal(moe.router_logits_from_partials(part), moe.router_logits_gemv(x, w))
-    for placements in ([(0, BIG), (512, 1), (1024, 1), (1536, 1)], [(0, BIG), (8, 1), (16, 1)],
-                       [(0, BIG), (512, 2)]):
-        x, w = _one_hot_products(2048, placements)
-        assert np.array_equal(moe.router_logits_from_partials(moe.router_partials(x, w)),
-                              moe.router_logits_gemv(x, w))
-
-
-def test_partials_chain_in_element_order():
-    # item 0 = elements 0..7 with products 2^24, 1, 1, 1, 1, 1, 1, 1: added in order from zero every +1 rounds back
-    # (2^24 + 1 -> 2^24, ties to even), so the chain is 2^24; a tree over the item would keep the ones (2^24 + 6)
+    """A restatement that sums an item's 8 products as a tree instead of a chain from zero keeps the ones that the
+    chain loses (2^24 + 1 rounds back to 2^24, ties to even): the pins above and below would catch that mistake."""
     x, w = _one_hot_products(2048, [(0, BIG)] + [(i, 1) for i in range(1, 8)])
-    part = moe.router_partials(x, w)
-    assert part[0, 0, 0] == BIG and part[0, 1, 0] == 0
+    assert moe.router_logits_gemv(x, w)[0, 0] == BIG
     p = (x.astype(np.float32) * w.astype(np.float32))[0, :8]
-    assert moe._tree(p) == np.float32(2.0 ** 24 + 6) != part[0, 0, 0]
-    # the ones of item 1 (elements 8..15) stay in their own chain: 8, and the tree then gives (2^24 + 8)
+    assert moe._tree(p) == np.float32(2.0 ** 24 + 6) != moe.router_logits_gemv(x, w)[0, 0]
+    # the ones of item 1 (elements 8..15) stay in their own chain (8), then meet 2^24 in the wave tree: 2^24 + 8
     x, w = _one_hot_products(2048, [(0, BIG)] + [(i, 1) for i in range(8, 16)])
-    part = moe.router_partials(x, w)
-    assert part[0, 1, 0] == 8 and moe.router_logits_from_partials(part)[0, 0] == np.float32(2.0 ** 24 + 8)
+    assert moe.router_logits_gemv(x, w)[0, 0] == np.float32(2.0 ** 24 + 8)
 
 
 def _gemv_order_loops(x, w):
