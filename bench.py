@@ -198,7 +198,7 @@ def grouped_leg():
     """The other configurations (BASELINE.json configs[0] and [2..4]), reported beside the decode line:
     cfg3 = one 8192-token bf16 prefill chunk through one cfg-2 layer with skewed router logits (MFMA roofline over
     the routed experts' 2 R 3 H I flops); cfg4 = 512 steps of 64 tokens with a fresh Zipf-prior draw each step
-    (HBM roofline over the unique experts touched); cfg1 = batch-1 decode through 8 layers with a 5,632-wide shared
+    (HBM roofline over the unique experts touched); cfg1 = batch-1 decode through 16 layers with a 5,632-wide shared
     expert; cfg5 = the 512-expert Q4_K layer at T = 1 (decode chain) and T = 2048 (grouped path)."""
     import ctypes
 
@@ -326,12 +326,12 @@ def grouped_leg():
         note="the grouped GEMMs read a second, reordered copy of the Q4_0 experts (MoELayer.keep_stream); same bits")
     L.drop_stream()
     del B4, xs, lgs, packed
-    # cfg1: E 60, top-4 without renorm, I 1408, a 5,632-wide shared expert (not foldable) with a sigmoid gate, Q4_0;
-    # batch-1 decode through 8 such layers (2.5 GB: no layer stays in the 256 MB MALL), one HIP graph a step.
+    # cfg1: E 60, top-4 without renorm, I 1408, a 5,632-wide shared expert with a sigmoid gate, Q4_0; batch-1 decode
+    # through 16 such layers (each step touches 16 x 39.2 MB, over twice the 256 MB MALL), one HIP graph a step.
     from larder_amd import layer as lay
     log("[bench] cfg1 decode stack: start")
     cfg1 = workloads.CONFIGS[1]
-    L1s = [workloads.make_layer(cfg1, g) for _ in range(8)]
+    L1s = [workloads.make_layer(cfg1, g) for _ in range(16)]  # 627 MB a step: over twice the 256 MB MALL
     st1 = lay.DecodeStack(L1s, 1)
     st1.capture()
     n1 = 128
@@ -350,7 +350,7 @@ def grouped_leg():
     b1 = workloads.decode_bytes(cfg1, cfg1["k"]) + 2 * cfg1["H"] * 2
     out["cfg1_decode_T1"] = {"us_per_layer": round(us1, 2), "bytes_per_layer": b1,
                              "hbm_frac": round(b1 / (us1 * 1e-6) / HBM_PEAK, 4),
-                             "note": "8-layer stack; the 5,632-wide shared expert folded into the decode kernels as four slices of the routed width (3 launches a layer)"}
+                             "note": "16-layer stack; the 5,632-wide shared expert folded into the decode kernels as four slices of the routed width (3 launches a layer)"}
     del st1, L1s, x1
     # cfg5: H 4096, 512 experts top-10, I 512, shared expert, Q4_K. T = 1 through the decode chain (one layer as a
     # HIP graph, a fresh x each step so the touched experts change), T = 2048 through the grouped path.
