@@ -35,6 +35,15 @@ namespace lmoe {
 template <int N>
 using IC = std::integral_constant<int, N>;
 
+// f(IC<0>), f(IC<1>), ..., f(IC<N - 1>): a loop whose index is a compile-time constant in the body
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (I < N) {
+    f(IC<I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -459,7 +468,10 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const Q0Lane ql = q0_lane<MODE, GMT>(wave, fr, g);
-  auto compute = [&](int s, auto qn) { q0_step<decltype(qn)::value, MB>(lds + s * kQ0Stage, ql, fr, g, acc); };
+  // the stage as a compile-time index: every LDS address of a step is then a lane offset plus an immediate
+  auto compute = [&](auto s, auto qn) {
+    q0_step<decltype(qn)::value, MB>(lds + decltype(s)::value * kQ0Stage, ql, fr, g, acc);
+  };
 
   // Step kk: the copies of step kk + NST - 1 go out, step kk multiplies out of its stage, then each wavefront waits
   // for its own copies of step kk + 1 (the counter counts in issue order: the copies of the steps after kk + 1 may
@@ -482,13 +494,18 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
   wait_steps(pre - 1);
   barrier_lds();
   auto run = [&](auto qn) {
-    for (int kk = 0; kk < nk; ++kk) {
-      if (kk + NST - 1 < nk) issue(kk + NST - 1);
-      compute(kk % NST, qn);
-      if (kk + 1 < nk) {
-        wait_steps(min(kk + NST - 1, nk - 1) - (kk + 1));
-        barrier_lds();
-      }
+    for (int kb = 0; kb < nk; kb += NST) {  // NST steps a pass, so step kb + j reads stage j
+      static_for<0, NST>([&](auto j) {
+        const int kk = kb + decltype(j)::value;
+        if (kk < nk) {
+          if (kk + NST - 1 < nk) issue(kk + NST - 1);
+          compute(j, qn);
+          if (kk + 1 < nk) {
+            wait_steps(min(kk + NST - 1, nk - 1) - (kk + 1));
+            barrier_lds();
+          }
+        }
+      });
     }
   };
   if constexpr (QMAX == 1) {
@@ -969,9 +986,9 @@ k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const
   }
   // Step kk out of stage s: per fragment the two qs words and the step's two scale pairs, both K slices' weights
   // decoded, each meeting the tile's A fragments (NMB 16-row blocks: a 40-row group multiplies 48 rows, not 64)
-  auto compute = [&](int s, int kk, auto nmb) {
+  auto compute = [&](auto s, int kk, auto nmb) {  // s: the stage, a compile-time index (immediate LDS offsets)
     constexpr int NMB = decltype(nmb)::value;
-    const uint8_t *st = lds + s * kStage;
+    const uint8_t *st = lds + decltype(s)::value * kStage;
     const u32x4 *as = reinterpret_cast<const u32x4 *>(st);
     const int pr = kk & 3;  // the step's sub-block pair: sub-blocks 2 pr (low nibbles) and 2 pr + 1 (high)
     half8 xf[2][MB];
@@ -1017,17 +1034,22 @@ k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const
   wait_steps(pre - 1);
   barrier_lds();
   auto run = [&](auto qn) {
-    for (int kk = 0; kk < nk; ++kk) {
-      if ((kk & 3) == 0) {  // the super-block's header landed with this step: its scale table, then a barrier
-        fill_table();
-        barrier_lds();
-      }
-      if (kk + NST - 1 < nk) issue(kk + NST - 1);
-      compute(kk % NST, kk, qn);
-      if (kk + 1 < nk) {
-        wait_steps(min(kk + NST - 1, nk - 1) - (kk + 1));
-        barrier_lds();
-      }
+    for (int kb = 0; kb < nk; kb += NST) {  // NST steps a pass, so step kb + j reads stage j
+      static_for<0, NST>([&](auto j) {
+        const int kk = kb + decltype(j)::value;
+        if (kk < nk) {
+          if ((kk & 3) == 0) {  // the super-block's header landed with this step: its scale table, then a barrier
+            fill_table();
+            barrier_lds();
+          }
+          if (kk + NST - 1 < nk) issue(kk + NST - 1);
+          compute(j, kk, qn);
+          if (kk + 1 < nk) {
+            wait_steps(min(kk + NST - 1, nk - 1) - (kk + 1));
+            barrier_lds();
+          }
+        }
+      });
     }
   };
   switch ((t.rows + 15) / 16) {  // uniform across the workgroup
