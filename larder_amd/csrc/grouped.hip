@@ -324,16 +324,13 @@ __device__ __forceinline__ Q0Lane q0_lane(int wave, int fr, int g) {
 // slice's A fragments two fragments ahead of their use. sched_barrier keeps the compiler from regrouping them.
 // QN: the 32-row pairs of fragments the tile has rows in (a tile's last m-tile is often short): the MFMAs and A
 // reads of empty pairs are left out.
-template <int QN, int MB>
-__device__ __forceinline__ void q0_step(const uint8_t *st, const Q0Lane &L, int fr, int g, f32x4 (&acc)[4][MB]) {
+// The step body, over any weight layout: word(i) / scale(i) give fragment i's nibble word and the word holding its
+// block scale (low half for K slice 0, high half for K slice 1); sa is the step's A stage.
+template <int QN, int MB, typename Word, typename Scale>
+__device__ __forceinline__ void q0_mfma_step(const uint8_t *sa, Word word, Scale scale, int fr, int g,
+                                             f32x4 (&acc)[4][MB]) {
   __builtin_amdgcn_s_setprio(1);  // the other workgroup's wavefront on this SIMD yields while this one multiplies
-  const u32x4 *as = reinterpret_cast<const u32x4 *>(st);
-  auto at = [&](int byte) -> uint32_t { return *reinterpret_cast<const uint32_t *>(st + byte); };
-  auto word = [&](int i) -> uint32_t {
-    const int ks = i / 4, nb = i % 4;
-    return ks == 0 ? __builtin_amdgcn_alignbyte(at(L.head[nb] + L.w1_of), at(L.head[nb] + 4 * g), 2) : at(L.blk1[nb]);
-  };
-  auto scale = [&](int i) -> uint32_t { return at(L.head[i % 4] + 256 * (i / 4)); };
+  const u32x4 *as = reinterpret_cast<const u32x4 *>(sa);
   const h2_t bias = {_Float16(1032.0f), _Float16(1032.0f)};
   half8 xf[2][8];
 #pragma unroll
@@ -381,6 +378,66 @@ __device__ __forceinline__ void q0_step(const uint8_t *st, const Q0Lane &L, int 
     if (i + 1 < 8) wcur = wnext;
   }
   __builtin_amdgcn_s_setprio(0);
+}
+
+template <int QN, int MB>
+__device__ __forceinline__ void q0_step(const uint8_t *st, const Q0Lane &L, int fr, int g, f32x4 (&acc)[4][MB]) {
+  auto at = [&](int byte) -> uint32_t { return *reinterpret_cast<const uint32_t *>(st + byte); };
+  auto word = [&](int i) -> uint32_t {
+    const int ks = i / 4, nb = i % 4;
+    return ks == 0 ? __builtin_amdgcn_alignbyte(at(L.head[nb] + L.w1_of), at(L.head[nb] + 4 * g), 2) : at(L.blk1[nb]);
+  };
+  auto scale = [&](int i) -> uint32_t { return at(L.head[i % 4] + 256 * (i / 4)); };
+  q0_mfma_step<QN, MB>(st, word, scale, fr, g, acc);
+}
+
+// ---- Q4_0 on the GGUF layout, two units a step -------------------------------------------------------------------
+//
+// In the GGUF layout a one-unit step copies 36 bytes of each of 256 weight rows, a 128-byte line a row for 32 of its
+// bytes, and the line is gone from L1 before the next step wants the rest of it (rocprofv3 on cfg4's 32-row tiles:
+// 5.3x the L1-to-L2 requests of the stream copies, the texture unit stalled on L1 tags). A step of two units (K 128)
+// copies 72 contiguous bytes a row: a 16-byte copy instruction takes 16 rows x 64 bytes (four lanes a row), a 4-byte
+// one 32 rows x 8 bytes. LDS a stage: the one-unit kernel's A stage twice (K 0-63, 64-127), then wavefront w's copy
+// rows (tile features 64 w .. 64 w + 63) as 4 blocks of 16 rows x 64 bytes, each padded to kW2Blk bytes, then 8
+// blocks of 32 rows x 8 bytes (piece bytes 64-71). Feature 16 q + 4 i + j (q, i, j < 4) of a wavefront sits in block
+// i, slot 4 q + j, so the 16 features of an MFMA fragment (q fixed) lie kW2Blk i + 64 j apart: 16 different groups
+// of four banks. Same arithmetic as two one-unit steps, so the same bits.
+constexpr int kW2Blk = 1040, kW2X4 = 4 * 4 * kW2Blk, kW2Dw = 8 * 256;
+template <int GMT> constexpr int q0w2_stage() { return 2 * q0_astage<GMT>() + kW2X4 + kW2Dw; }
+
+// Lane (fr, g)'s addresses in a two-unit stage for fragment nb: x = the feature's 64-byte run, xg = x + 4 g,
+// b1 = unit 1's block-1 word 5 + g (piece word 14 + g: in the run for g < 2, else in the 8-byte tail)
+struct Q0Lane2 {
+  int x[4], xg[4], b1[4];
+};
+
+template <int MODE, int GMT>
+__device__ __forceinline__ Q0Lane2 q0_lane2(int wave, int fr, int g) {
+  Q0Lane2 L;
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int f = frag_feature<MODE>(wave, nb) + fr;
+    const int cw = f >> 6, fl = f & 63, q = fl >> 4, i = (fl >> 2) & 3, j = fl & 3;
+    const int x = 2 * q0_astage<GMT>() + cw * 4 * kW2Blk + i * kW2Blk + 64 * (4 * q + j);
+    const int d = 2 * q0_astage<GMT>() + kW2X4 + (2 * cw + (fl >> 5)) * 256 + 8 * (fl & 31);
+    L.x[nb] = x;
+    L.xg[nb] = x + 4 * g;
+    L.b1[nb] = g < 2 ? x + 4 * (14 + g) : d + 4 * (g - 2);
+  }
+  return L;
+}
+
+// Unit U (0, 1) of a two-unit stage: unit words w are piece words 9 U + w
+template <int QN, int MB, int U>
+__device__ __forceinline__ void q0_step2(const uint8_t *st, const Q0Lane2 &L, int fr, int g, f32x4 (&acc)[4][MB]) {
+  auto at = [&](int byte) -> uint32_t { return *reinterpret_cast<const uint32_t *>(st + byte); };
+  auto word = [&](int i) -> uint32_t {
+    const int ks = i / 4, nb = i % 4;
+    if (ks == 0) return __builtin_amdgcn_alignbyte(at(L.xg[nb] + 36 * U + 4), at(L.xg[nb] + 36 * U), 2);
+    return U == 0 ? at(L.xg[nb] + 20) : at(L.b1[nb]);
+  };
+  auto scale = [&](int i) -> uint32_t { return at(L.x[i % 4] + 36 * U + 16 * (i / 4)); };
+  q0_mfma_step<QN, MB>(st + U * q0_astage<MB * 16>(), word, scale, fr, g, acc);
 }
 
 // Grid: n_ntile * max_tiles workgroups of 256 threads, two a CU. GATE_UP: n-tile j covers intermediate features
@@ -536,6 +593,146 @@ k_grouped_q4_0(const _Float16 *a_src, int topk, const uint32_t *order, const uin
         const int n = MODE == MODE_GATE_UP ? (f < GN / 2 ? t.nt * (GN / 2) + f : ldw / 2 + t.nt * (GN / 2) + f - GN / 2)
                                            : t.nt * GN + f;
         *reinterpret_cast<f32x4 *>(wrow + n) = acc[nb][mb];
+      }
+    }
+    return;
+  }
+  store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
+}
+
+// k_grouped_q4_0 on the GGUF layout with two-unit steps (K 128, the stage above): grid, arguments and results as
+// k_grouped_q4_0<MODE, GMT> (the same bits); host guarantees K % (128 ksplit) == 0. NST = 3 stages (79 KB, two
+// workgroups a CU) or 2 (53 KB, three a CU: the next step's copies fly while this one multiplies).
+template <int MODE, int GMT, int NST>
+__global__ void __launch_bounds__(kThreads, NST == 2 ? 3 : 2)
+k_grouped_q4_0_w2(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
+                  const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
+                  int K, int n_rows, void *out, int ldo, int odt, int ksplit = 1, float *ws = nullptr, int R = 0,
+                  int ldw = 0) {
+  constexpr int kAStage = q0_astage<GMT>(), kStage = q0w2_stage<GMT>(), kDmaA = q0_dma_a<GMT>();
+  constexpr int MB = GMT / 16, QMAX = GMT / 32;
+  static_assert(kDmaA >= 1 && (NST == 2 || NST == 3) && NST * kStage <= 81920, "tile and pipeline shape");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[NST * kStage];
+  Tile t;
+  if (!tile_of<GMT>(offsets, tiles, n_tiles, n_ntile, &t, ksplit)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, g = lane >> 4;
+  const uint32_t wrow = 36u * uint32_t(K / 64);
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(lds));
+
+  // A: as in k_grouped_q4_0, once for each 64-K half of the step
+  uint32_t a_off[kDmaA];
+#pragma unroll
+  for (int i = 0; i < kDmaA; ++i) {
+    const int q = 64 * (kDmaA * wave + i) + lane, r = q >> 3, c = (q & 7) ^ (r & 7);
+    const int p = t.row0 + (r < t.rows ? r : 0);
+    const uint32_t row = MODE == MODE_GATE_UP ? order[p] / uint32_t(topk) : uint32_t(p);
+    a_off[i] = row * uint32_t(K) * 2u + 16u * uint32_t(c);
+  }
+  const uint32_t a_live = a_live_mask<kDmaA>(wave, t.rows);
+  // weights: wavefront w copies tile features 64 w .. 64 w + 63 (gate/up: waves 0-1 gate rows, 2-3 up rows).
+  // 16-byte copy i: lane l takes bytes 16 (l % 4) .. of the step's piece of feature 16 (s / 4) + 4 i + s % 4,
+  // s = l / 4; 4-byte copy j: lane l takes piece bytes 64 + 4 (l % 2) of feature 32 j + l / 2.
+  const uint8_t *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
+  const int row_base = (MODE == MODE_GATE_UP ? t.nt * (GN / 2) - (wave >= 2 ? GN / 2 : 0) : t.nt * GN) + 64 * wave;
+  const uint8_t *wbase = m + (size_t(t.e) * n_rows) * wrow;
+  uint32_t w_off[4], d_off[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int s = lane >> 2, fl = 16 * (s >> 2) + 4 * i + (s & 3);
+    w_off[i] = uint32_t(row_base + fl) * wrow + 16u * uint32_t(lane & 3);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) d_off[j] = uint32_t(row_base + 32 * j + (lane >> 1)) * wrow + 64u + 4u * uint32_t(lane & 1);
+  const int nk = K / (2 * GK) / ksplit, k0 = t.kpart * nk;  // this workgroup's two-unit steps: k0 .. k0 + nk - 1
+  auto issue = [&](int kk) {  // step kk (of the slice) into stage kk % NST
+    const uint32_t st = lds0 + uint32_t(kk % NST) * kStage;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const _Float16 *ab = a_src + size_t(2 * (k0 + kk) + h) * GK;
+#pragma unroll
+      for (int i = 0; i < kDmaA; ++i)
+        dma_a(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + uint32_t(h * kAStage) + 1024u * uint32_t(kDmaA * wave + i)),
+              a_live >> i & 1u);
+    }
+    const uint8_t *wb = wbase + size_t(k0 + kk) * 72;
+    const uint32_t sw = st + 2u * kAStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma<16>(wb, w_off[i], __builtin_amdgcn_readfirstlane(sw + uint32_t(wave * 4 * kW2Blk + i * kW2Blk)));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      dma<4>(wb, d_off[j], __builtin_amdgcn_readfirstlane(sw + uint32_t(kW2X4) + 256u * uint32_t(2 * wave + j)));
+  };
+
+  f32x4 acc[4][MB];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const Q0Lane2 ql = q0_lane2<MODE, GMT>(wave, fr, g);
+  auto compute = [&](auto s, auto qn) {
+    const uint8_t *st = lds + decltype(s)::value * kStage;
+    q0_step2<decltype(qn)::value, MB, 0>(st, ql, fr, g, acc);
+    q0_step2<decltype(qn)::value, MB, 1>(st, ql, fr, g, acc);
+  };
+
+  constexpr int C = 2 * kDmaA + 6;  // copies a lane a step
+  static_assert(3 * C <= 63, "the wait counts below");
+  auto wait_steps = [&](int later) {  // until at most `later` steps' copies are still out
+    if (later <= 0)
+      wait_vm<0>();
+    else if (later == 1)
+      wait_vm<C>();
+    else
+      wait_vm<2 * C>();
+  };
+  const int pre = min(NST - 1, nk);
+  for (int j = 0; j < pre; ++j) issue(j);
+  wait_steps(pre - 1);
+  barrier_lds();
+  auto run = [&](auto qn) {
+    for (int kb = 0; kb < nk; kb += NST) {
+      static_for<0, NST>([&](auto j) {
+        const int kk = kb + decltype(j)::value;
+        if (kk < nk) {
+          if (kk + NST - 1 < nk) issue(kk + NST - 1);
+          compute(j, qn);
+          if (kk + 1 < nk) {
+            wait_steps(min(kk + NST - 1, nk - 1) - (kk + 1));
+            barrier_lds();
+          }
+        }
+      });
+    }
+  };
+  if constexpr (QMAX == 1) {
+    run(IC<1>{});
+  } else if constexpr (QMAX == 2) {
+    if (t.rows <= 32)
+      run(IC<1>{});
+    else
+      run(IC<2>{});
+  } else {
+    switch ((t.rows + 31) / 32) {
+      case 1: run(IC<1>{}); break;
+      case 2: run(IC<2>{}); break;
+      case 3: run(IC<3>{}); break;
+      default: run(IC<4>{}); break;
+    }
+  }
+  if (ksplit > 1) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int mrow = 16 * mb + fr;
+      if (mrow >= t.rows) continue;
+      float *wrw = ws + (size_t(t.kpart) * R + t.row0 + mrow) * ldw;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const int f = frag_feature<MODE>(wave, nb) + 4 * g;
+        const int n = MODE == MODE_GATE_UP ? (f < GN / 2 ? t.nt * (GN / 2) + f : ldw / 2 + t.nt * (GN / 2) + f - GN / 2)
+                                           : t.nt * GN + f;
+        *reinterpret_cast<f32x4 *>(wrw + n) = acc[nb][mb];
       }
     }
     return;
@@ -1364,6 +1561,15 @@ static int q0_stages32() {
   return v == 4 || v == 5 ? v : 3;
 }
 
+// The two-unit-step kernel (k_grouped_q4_0_w2) takes the 32-row tiles on the GGUF layout wherever the K steps of
+// each slice pair up: its stage count, 2 by default (cfg4 129.8 -> 112.6 us a step, the same bits; 3 stages:
+// 116.4), or 0 for the one-unit kernel. LMOE_Q0_W2=1 keeps the one-unit kernel, 3 takes three stages.
+static int q0_two_unit(bool sl, int bm, int nst, int K, int ksplit) {
+  const int v = env_knob("LMOE_Q0_W2");
+  if (sl || bm != 32 || nst != 3 || (K / GK) % (2 * ksplit) != 0 || v == 1) return 0;
+  return v == 3 ? 3 : 2;
+}
+
 static int grouped_gate_up(const char *fn, bool sl, const void *x, int xdtype, int T, int topk, const uint32_t *order,
                            const uint32_t *offsets, const uint32_t *tiles, const uint32_t *n_tiles, int max_tiles,
                            int bm, int ksplit, float *ws, const uint8_t *wg, const uint8_t *wu, int type_g,
@@ -1407,6 +1613,8 @@ static int grouped_gate_up(const char *fn, bool sl, const void *x, int xdtype, i
                                               : k_grouped_q4_0<MODE_GATE_UP, 32, 5>)
                       : bm == 64 ? k_grouped_q4_0<MODE_GATE_UP, 64, 4>
                                  : k_grouped_q4_0<MODE_GATE_UP>);
+    if (const int w2 = q0_two_unit(sl, bm, nst, H, ksplit))
+      kern = w2 == 2 ? k_grouped_q4_0_w2<MODE_GATE_UP, 32, 2> : k_grouped_q4_0_w2<MODE_GATE_UP, 32, 3>;
     launch(kern, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg,
            wu, H, I, h, I, int(LMOE_F16), ksplit, ws, R, 2 * I);
     if (ksplit > 1) {
@@ -1465,6 +1673,8 @@ static int grouped_down(const char *fn, bool sl, const void *h, int R, const uin
                                               : k_grouped_q4_0<MODE_DOWN, 32, 5>)
                       : bm == 64 ? k_grouped_q4_0<MODE_DOWN, 64, 4>
                                  : k_grouped_q4_0<MODE_DOWN>);
+    if (const int w2 = q0_two_unit(sl, bm, nst, I, ksplit))
+      kern = w2 == 2 ? k_grouped_q4_0_w2<MODE_DOWN, 32, 2> : k_grouped_q4_0_w2<MODE_DOWN, 32, 3>;
     launch(kern, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets,
            tiles, n_tiles, n_ntile, wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype, ksplit, ws, R,
            H);

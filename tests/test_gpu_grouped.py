@@ -432,3 +432,40 @@ def test_q4_0_tile_rows_both_kernels(t, bm, ks):
     assert moe.rel_l2(got_y, yw[order][valid]) < BAR
     assert rows_ok(got_y, yw[order][valid]) < ROW_BAR
 
+
+
+@pytest.mark.parametrize("H,I,E,ks", [(2048, 768, 9, 1), (2048, 768, 9, 2), (4096, 1408, 7, 2), (2048, 1408, 9, 1),
+                                      (512, 640, 5, 1), (2048, 768, 9, 4)])
+def test_q4_0_two_unit_steps_same_bits(H, I, E, ks, monkeypatch):
+    """The 32-row Q4_0 GEMMs on the GGUF layout take two units (K 128) a step where the slices' K steps pair up,
+    over 2 LDS stages (default) or 3 (LMOE_Q0_W2=3); else, or with LMOE_Q0_W2=1, the one-unit kernel runs: h and
+    y bit-equal to the one-unit kernel's, gate/up and down, with and without split-K, on groups of 0, 1, 31, 32,
+    33, 64 and 200 rows and a slot past the experts."""
+    from larder_amd import grouped
+    types = ("Q4_0",) * 3
+    w = tuple(dev(b) for b in experts(types, H, I, E, 91))
+    rng = np.random.default_rng(H + I + ks)
+    sizes = [0, 1, 31, 32, 33, 64, 200, 5, 2][:E]
+    slots = np.concatenate([np.full(n, e) for e, n in enumerate(sizes)]).astype(np.int32)
+    rng.shuffle(slots)
+    slots[3] = E + 1
+    R = slots.size
+    x = dev(rng.standard_normal((R, H)).astype(np.float16))
+    G = grouped.Grouping(R, E, bm=32).run(dev(slots))
+    outs = []
+    for knob in ("1", "", "3"):
+        monkeypatch.setenv("LMOE_Q0_W2", knob)
+        h = torch.empty((R, I), dtype=torch.float16, device="cuda")
+        y = torch.empty((R, H), dtype=torch.float32, device="cuda")
+        grouped.gate_up(x, G, 1, w[0], w[1], types, h, ksplit=ks)
+        grouped.down(h, G, w[2], types[2], y, ksplit=ks)
+        torch.cuda.synchronize()
+        outs.append((host(h), host(y)))
+    order = host(G.order)
+    valid = slots[order] < E
+    h0, y0 = outs[0]
+    for h1, y1 in outs[1:]:
+        assert np.array_equal(h0.view(np.uint16)[valid], h1.view(np.uint16)[valid])
+        assert np.array_equal(y0.view(np.uint32)[valid], y1.view(np.uint32)[valid])
+    _, yw = moe.gemv(host(x.float()), tuple(host(b) for b in w), slots, 1, types)
+    assert moe.rel_l2(y1[valid], yw[order][valid]) < BAR
