@@ -1258,6 +1258,177 @@ k_grouped_q4_k_dma(const _Float16 *a_src, int topk, const uint32_t *order, const
   store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
 }
 
+// k_grouped_q4_k_dma<MODE, 64> on the GGUF layout with the weights staged two steps at a time. A one-step stage
+// copies 32 qs bytes of each of 256 weight rows (a 128-byte line a row for 32 of its bytes) and the line has left
+// L1 before the next step wants its neighbour; a step pair's 64 qs bytes are contiguous (runs 2j, 2j + 1 of a
+// super-block). LDS: four one-step A stages (three steps ahead, 8 KB each), two pair stages of weights (one pair
+// ahead: wavefront w's rows as 4 blocks of 16 rows x 64 bytes padded to 1,040 bytes, feature 16 q + 4 i + j at
+// block i slot 4 q + j, so an MFMA fragment's 16 features sit in 16 different 4-bank groups), the header buffer
+// and the scale table of k_grouped_q4_k_dma. Arithmetic and order as k_grouped_q4_k_dma<MODE, 64, 4>: the same
+// bits. Grid, arguments and host guarantees as there.
+constexpr int kKW2Stage = 4 * 4 * kW2Blk;  // a pair stage: 4 wavefronts x 4 blocks
+template <int MODE>
+__global__ void __launch_bounds__(kThreads, 2)
+k_grouped_q4_k_w2(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
+                  const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
+                  int K, int n_rows, void *out, int ldo, int odt) {
+  constexpr int GMT = 64, NA = 4;
+  constexpr int kAStage = qk_astage<GMT>(), kDmaA = GMT * 128 / 1024 / 4;
+  constexpr int kW = NA * kAStage, kHd = kW + 2 * kKW2Stage, kTab = kHd + kKHd;
+  constexpr int MB = GMT / 16;
+  static_assert(kTab + kKTab <= 81920, "two workgroups a CU");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kTab + kKTab];
+  Tile t;
+  if (!tile_of<GMT>(offsets, tiles, n_tiles, n_ntile, &t)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, g = lane >> 4;
+  const uint32_t wrow = 144u * uint32_t(K / 256);
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(lds));
+
+  uint32_t a_off[kDmaA];  // A: as in k_grouped_q4_0
+#pragma unroll
+  for (int i = 0; i < kDmaA; ++i) {
+    const int q = 64 * (kDmaA * wave + i) + lane, r = q >> 3, c = (q & 7) ^ (r & 7);
+    const int p = t.row0 + (r < t.rows ? r : 0);
+    const uint32_t row = MODE == MODE_GATE_UP ? order[p] / uint32_t(topk) : uint32_t(p);
+    a_off[i] = row * uint32_t(K) * 2u + 16u * uint32_t(c);
+  }
+  const uint32_t a_live = a_live_mask<kDmaA>(wave, t.rows);
+  // weights: wavefront w copies tile features 64 w .. 64 w + 63 (gate/up: waves 0-1 gate rows, 2-3 up rows). Pair
+  // copy i: lane l takes bytes 16 (l % 4) .. of the pair's 64 qs bytes of feature 16 (s / 4) + 4 i + s % 4,
+  // s = l / 4. Header copy: feature 64 w + lane's first 16 bytes of the super-block.
+  const uint8_t *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
+  const int row_base = (MODE == MODE_GATE_UP ? t.nt * (GN / 2) - (wave >= 2 ? GN / 2 : 0) : t.nt * GN) + 64 * wave;
+  const uint8_t *wbase = m + (size_t(t.e) * n_rows) * wrow;
+  uint32_t q_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int s = lane >> 2, fl = 16 * (s >> 2) + 4 * i + (s & 3);
+    q_off[i] = uint32_t(row_base + fl) * wrow + 16u + 16u * uint32_t(lane & 3);
+  }
+  const uint32_t h_off = uint32_t(row_base + lane) * wrow;
+  const int nk = K / GK, np = nk / 2;
+  auto issue_a = [&](int kk) {  // step kk's A into A stage kk % NA
+    const uint32_t st = lds0 + uint32_t(kk % NA) * kAStage;
+    const _Float16 *ab = a_src + size_t(kk) * GK;
+#pragma unroll
+    for (int i = 0; i < kDmaA; ++i)
+      dma_a(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kDmaA * wave + i)), a_live >> i & 1u);
+  };
+  auto issue_w = [&](int p) {  // pair p's qs into pair stage p % 2, then its super-block's header when p is even
+    const uint8_t *sb = wbase + size_t(p >> 1) * 144;
+    const uint8_t *qb = sb + 64 * (p & 1);
+    const uint32_t sw = lds0 + uint32_t(kW + (p & 1) * kKW2Stage + wave * 4 * kW2Blk);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma<16>(qb, q_off[i], __builtin_amdgcn_readfirstlane(sw + uint32_t(i * kW2Blk)));
+    if ((p & 1) == 0) dma<16>(sb, h_off, __builtin_amdgcn_readfirstlane(lds0 + kHd + 1024u * uint32_t(wave)));
+  };
+  auto fill_table = [&] {  // as in k_grouped_q4_k_dma
+    const u32x4 h = *reinterpret_cast<const u32x4 *>(lds + kHd + 16 * tid);
+    const uint32_t h0 = h[0], h1 = h[1], h2 = h[2], h3 = h[3];
+    const float d = half_lo(h0), dmin = half_hi(h0);
+    uint32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float sc, mn;
+      k4_scale_min(h1, h2, h3, j, &sc, &mn);
+      v[j] = __builtin_bit_cast(uint32_t, h2_t{_Float16(d * sc), _Float16(dmin * mn)});
+    }
+    uint32_t *row = reinterpret_cast<uint32_t *>(lds + kTab + kKTabRow * tid);
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) *reinterpret_cast<u32x2 *>(row + j) = u32x2{v[j], v[j + 1]};
+  };
+
+  f32x4 acc[4][MB];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // lane (fr, g) of fragment nb: feature f = frag_feature(nb) + fr; its qs words g and g + 4 of run u of the pair
+  // at qx[nb] + 32 u and qx[nb] + 32 u + 16 of a pair stage, its scale pairs in table row f
+  int qx[4], tab[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int f = frag_feature<MODE>(wave, nb) + fr;
+    const int cw = f >> 6, fl = f & 63, q = fl >> 4, i = (fl >> 2) & 3, j = fl & 3;
+    qx[nb] = kW + cw * 4 * kW2Blk + i * kW2Blk + 64 * (4 * q + j) + 4 * g;
+    tab[nb] = kTab + kKTabRow * f;
+  }
+  // step kk = 4 b + J: A stage J, pair stage J / 2, run J % 2 of the pair, sub-block pair J of the super-block
+  auto compute = [&](auto jj, auto nmb) {
+    constexpr int J = decltype(jj)::value, NMB = decltype(nmb)::value;
+    const u32x4 *as = reinterpret_cast<const u32x4 *>(lds + J * kAStage);
+    const uint8_t *sq = lds + (J / 2) * kKW2Stage + 32 * (J % 2);
+    half8 xf[2][MB];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) xf[ks][mb] = __builtin_bit_cast(half8, as[achunk(16 * mb + fr, 4 * ks + g)]);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const uint32_t lo = *reinterpret_cast<const uint32_t *>(sq + qx[nb]);
+      const uint32_t hi = *reinterpret_cast<const uint32_t *>(sq + qx[nb] + 16);
+      const u32x2 sp = *reinterpret_cast<const u32x2 *>(lds + tab[nb] + 8 * J);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint32_t x = ks == 0 ? (lo & 0x0F0F0F0Fu) | ((hi & 0x0F0F0F0Fu) << 4)
+                                   : ((lo >> 4) & 0x0F0F0F0Fu) | (hi & 0xF0F0F0F0u);
+        const half8 wf = decode8<LMOE_Q4_K>(x, ks == 0 ? uint32_t(sp[0]) : uint32_t(sp[1]), 0);
+#pragma unroll
+        for (int mb = 0; mb < NMB; ++mb)
+          acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf, xf[ks][mb], acc[nb][mb], 0, 0, 0);
+      }
+    }
+  };
+
+  // Step kk: A of step kk + 3 goes out, and on even kk the weights of pair kk / 2 + 1 (the pair stage that pair
+  // kk / 2 - 1 left); step kk multiplies; then each wavefront waits for its own copies of step kk + 1 and the
+  // barrier publishes them. The counter counts in issue order. Copies a lane: CA a step, 4 a pair, 1 a header.
+  // Before step kk + 1 (odd kk) the last copies that may still be out are A of step kk + 3 (CA); before step
+  // kk + 1 (even kk) those of steps kk + 2 and kk + 3 and pair kk / 2 + 1 (2 CA + 4, or one more with a header:
+  // waiting for 2 CA + 4 then also waits for one later copy, never too little). With fewer than 3 steps left
+  // nothing is counted: the wait is for every copy.
+  constexpr int CA = kDmaA;
+  static_assert(2 * CA + 5 <= 63, "the wait counts below");
+  issue_a(0);
+  issue_a(1);
+  issue_w(0);
+  if (nk > 2) issue_a(2);
+  wait_vm<0>();
+  barrier_lds();
+  auto run = [&](auto nmb) {
+    for (int kb = 0; kb < nk; kb += 4) {  // K % 256 == 0: whole super-blocks, four steps a pass
+      static_for<0, 4>([&](auto j) {
+        constexpr int J = decltype(j)::value;
+        const int kk = kb + J;
+        if constexpr (J == 0) {  // the super-block's header landed with its first pair: its scale table
+          fill_table();
+          barrier_lds();
+        }
+        if (kk + 3 < nk) issue_a(kk + 3);
+        if (J % 2 == 0 && kk / 2 + 1 < np) issue_w(kk / 2 + 1);
+        compute(j, nmb);
+        if (kk + 1 < nk) {
+          if (kk + 3 >= nk)
+            wait_vm<0>();
+          else if (J % 2 == 1)
+            wait_vm<CA>();
+          else
+            wait_vm<2 * CA + 4>();
+          barrier_lds();
+        }
+      });
+    }
+  };
+  switch ((t.rows + 15) / 16) {  // uniform across the workgroup
+    case 1: run(IC<1>{}); break;
+    case 2: run(IC<2>{}); break;
+    case 3: run(IC<3>{}); break;
+    default: run(IC<MB>{}); break;
+  }
+  store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
+}
+
 // x [n] in dt -> f16 (round to nearest even), 8 elements a thread (vector loads when the whole range allows).
 // kperm: element i lands at its position in the grouped GEMMs' K order (n % 32 == 0, vector path only).
 __global__ void __launch_bounds__(256) k_to_f16(const void *x, int dt, long long n, _Float16 *out, int vec,
@@ -1564,6 +1735,10 @@ static int q0_stages32() {
 // The two-unit-step kernel (k_grouped_q4_0_w2) takes the 32-row tiles on the GGUF layout wherever the K steps of
 // each slice pair up: its stage count, 2 by default (cfg4 129.8 -> 112.6 us a step, the same bits; 3 stages:
 // 116.4), or 0 for the one-unit kernel. LMOE_Q0_W2=1 keeps the one-unit kernel, 3 takes three stages.
+// The 64-row Q4_K GEMMs on the GGUF layout stage their weights two steps at a time (k_grouped_q4_k_w2: cfg5 prefill
+// 817 -> 761 us, gate/up 421 -> 390, down 252 -> 227, the same bits); LMOE_QK_W2=1 keeps one step at a time.
+static bool qk_pairs() { return env_knob("LMOE_QK_W2") != 1; }
+
 static int q0_two_unit(bool sl, int bm, int nst, int K, int ksplit) {
   const int v = env_knob("LMOE_Q0_W2");
   if (sl || bm != 32 || nst != 3 || (K / GK) % (2 * ksplit) != 0 || v == 1) return 0;
@@ -1625,7 +1800,7 @@ static int grouped_gate_up(const char *fn, bool sl, const void *x, int xdtype, i
   } else {
     launch(sl           ? k_grouped_q4_k_dma<MODE_GATE_UP, 64, 4, true>
            : bm == 32   ? k_grouped_q4_k<MODE_GATE_UP, 32, 3>
-           : bm == 64   ? k_grouped_q4_k_dma<MODE_GATE_UP>
+           : bm == 64   ? (qk_pairs() ? k_grouped_q4_k_w2<MODE_GATE_UP> : k_grouped_q4_k_dma<MODE_GATE_UP>)
                         : k_grouped_q4_k<MODE_GATE_UP>,
            dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg, wu, H,
            I, h, I, int(LMOE_F16));
@@ -1686,7 +1861,7 @@ static int grouped_down(const char *fn, bool sl, const void *h, int R, const uin
   } else {
     launch(sl           ? k_grouped_q4_k_dma<MODE_DOWN, 64, 4, true>
            : bm == 32   ? k_grouped_q4_k<MODE_DOWN, 32, 3>
-           : bm == 64   ? k_grouped_q4_k_dma<MODE_DOWN>
+           : bm == 64   ? (qk_pairs() ? k_grouped_q4_k_w2<MODE_DOWN> : k_grouped_q4_k_dma<MODE_DOWN>)
                         : k_grouped_q4_k<MODE_DOWN>,
            dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets, tiles,
            n_tiles, n_ntile, wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype);

@@ -469,3 +469,37 @@ def test_q4_0_two_unit_steps_same_bits(H, I, E, ks, monkeypatch):
         assert np.array_equal(y0.view(np.uint32)[valid], y1.view(np.uint32)[valid])
     _, yw = moe.gemv(host(x.float()), tuple(host(b) for b in w), slots, 1, types)
     assert moe.rel_l2(y1[valid], yw[order][valid]) < BAR
+
+
+@pytest.mark.parametrize("H,I,E", [(1024, 512, 9), (2048, 768, 7), (4096, 256, 5), (512, 1536, 9)])
+def test_q4_k_pair_staging_same_bits(H, I, E, monkeypatch):
+    """The 64-row Q4_K GEMMs on the GGUF layout with the weights staged two steps at a time (the default): h and y
+    bit-equal to the one-step kernel's (LMOE_QK_W2=1), gate/up and down, on groups of 0, 1, 31, 32, 33, 64 and 200 rows and a slot
+    past the experts; K from one super-block (down at I = 256) up."""
+    from larder_amd import grouped
+    types = ("Q4_K",) * 3
+    w = tuple(dev(b) for b in experts(types, H, I, E, 93))
+    rng = np.random.default_rng(H + 3 * I)
+    sizes = [0, 1, 31, 32, 33, 64, 200, 5, 2][:E]
+    slots = np.concatenate([np.full(n, e) for e, n in enumerate(sizes)]).astype(np.int32)
+    rng.shuffle(slots)
+    slots[3] = E + 1
+    R = slots.size
+    x = dev(rng.standard_normal((R, H)).astype(np.float16))
+    G = grouped.Grouping(R, E, bm=64).run(dev(slots))
+    outs = []
+    for knob in ("1", ""):
+        monkeypatch.setenv("LMOE_QK_W2", knob)
+        h = torch.empty((R, I), dtype=torch.float16, device="cuda")
+        y = torch.empty((R, H), dtype=torch.float32, device="cuda")
+        grouped.gate_up(x, G, 1, w[0], w[1], types, h)
+        grouped.down(h, G, w[2], types[2], y)
+        torch.cuda.synchronize()
+        outs.append((host(h), host(y)))
+    order = host(G.order)
+    valid = slots[order] < E
+    (h0, y0), (h1, y1) = outs
+    assert np.array_equal(h0.view(np.uint16)[valid], h1.view(np.uint16)[valid])
+    assert np.array_equal(y0.view(np.uint32)[valid], y1.view(np.uint32)[valid])
+    _, yw = moe.gemv(host(x.float()), tuple(host(b) for b in w), slots, 1, types)
+    assert moe.rel_l2(y1[valid], yw[order][valid]) < BAR
