@@ -411,15 +411,16 @@ struct Q0Lane2 {
   int x[4], xg[4], b1[4];
 };
 
-template <int MODE, int GMT>
-__device__ __forceinline__ Q0Lane2 q0_lane2(int wave, int fr, int g) {
+// base: the byte offset of the weight area (the 16-byte blocks, then the 8-byte tails) from the stage's start
+template <int MODE>
+__device__ __forceinline__ Q0Lane2 q0_lane2(int wave, int fr, int g, int base) {
   Q0Lane2 L;
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) {
     const int f = frag_feature<MODE>(wave, nb) + fr;
     const int cw = f >> 6, fl = f & 63, q = fl >> 4, i = (fl >> 2) & 3, j = fl & 3;
-    const int x = 2 * q0_astage<GMT>() + cw * 4 * kW2Blk + i * kW2Blk + 64 * (4 * q + j);
-    const int d = 2 * q0_astage<GMT>() + kW2X4 + (2 * cw + (fl >> 5)) * 256 + 8 * (fl & 31);
+    const int x = base + cw * 4 * kW2Blk + i * kW2Blk + 64 * (4 * q + j);
+    const int d = base + kW2X4 + (2 * cw + (fl >> 5)) * 256 + 8 * (fl & 31);
     L.x[nb] = x;
     L.xg[nb] = x + 4 * g;
     L.b1[nb] = g < 2 ? x + 4 * (14 + g) : d + 4 * (g - 2);
@@ -427,17 +428,24 @@ __device__ __forceinline__ Q0Lane2 q0_lane2(int wave, int fr, int g) {
   return L;
 }
 
-// Unit U (0, 1) of a two-unit stage: unit words w are piece words 9 U + w
+// Unit U (0, 1) of a two-unit weight stage at sw (unit words w are piece words 9 U + w) against the A stage at sa
 template <int QN, int MB, int U>
-__device__ __forceinline__ void q0_step2(const uint8_t *st, const Q0Lane2 &L, int fr, int g, f32x4 (&acc)[4][MB]) {
-  auto at = [&](int byte) -> uint32_t { return *reinterpret_cast<const uint32_t *>(st + byte); };
+__device__ __forceinline__ void q0_step_pair(const uint8_t *sa, const uint8_t *sw, const Q0Lane2 &L, int fr, int g,
+                                             f32x4 (&acc)[4][MB]) {
+  auto at = [&](int byte) -> uint32_t { return *reinterpret_cast<const uint32_t *>(sw + byte); };
   auto word = [&](int i) -> uint32_t {
     const int ks = i / 4, nb = i % 4;
     if (ks == 0) return __builtin_amdgcn_alignbyte(at(L.xg[nb] + 36 * U + 4), at(L.xg[nb] + 36 * U), 2);
     return U == 0 ? at(L.xg[nb] + 20) : at(L.b1[nb]);
   };
   auto scale = [&](int i) -> uint32_t { return at(L.x[i % 4] + 36 * U + 16 * (i / 4)); };
-  q0_mfma_step<QN, MB>(st + U * q0_astage<MB * 16>(), word, scale, fr, g, acc);
+  q0_mfma_step<QN, MB>(sa, word, scale, fr, g, acc);
+}
+
+// Unit U of a two-unit stage (A of both units, then the weights, at st)
+template <int QN, int MB, int U>
+__device__ __forceinline__ void q0_step2(const uint8_t *st, const Q0Lane2 &L, int fr, int g, f32x4 (&acc)[4][MB]) {
+  q0_step_pair<QN, MB, U>(st + U * q0_astage<MB * 16>(), st, L, fr, g, acc);
 }
 
 // Grid: n_ntile * max_tiles workgroups of 256 threads, two a CU. GATE_UP: n-tile j covers intermediate features
@@ -670,7 +678,7 @@ k_grouped_q4_0_w2(const _Float16 *a_src, int topk, const uint32_t *order, const 
   for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const Q0Lane2 ql = q0_lane2<MODE, GMT>(wave, fr, g);
+  const Q0Lane2 ql = q0_lane2<MODE>(wave, fr, g, 2 * kAStage);
   auto compute = [&](auto s, auto qn) {
     const uint8_t *st = lds + decltype(s)::value * kStage;
     q0_step2<decltype(qn)::value, MB, 0>(st, ql, fr, g, acc);
@@ -736,6 +744,128 @@ k_grouped_q4_0_w2(const _Float16 *a_src, int topk, const uint32_t *order, const 
       }
     }
     return;
+  }
+  store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
+}
+
+// k_grouped_q4_0<MODE, GMT> on the GGUF layout for the tall tiles (128 or 64 rows, no split-K), with the weights
+// staged two units at a time and A one unit at a time. A two-unit stage of A and weights for 128 rows (51 KB) leaves
+// room for one stage at two workgroups a CU, so the ring is split: two A stages (one K step ahead) and two
+// two-unit weight stages (the layout of k_grouped_q4_0_w2's weight area; one pair ahead). At step kk the A of step
+// kk + 1 goes out, and on even kk the weights of pair kk / 2 + 1. The same arithmetic as k_grouped_q4_0: the same
+// bits. Arguments as k_grouped_q4_0 (the split-K ones unused: one K slice). Host guarantees: K % 128 == 0, and
+// those of k_grouped_q4_0.
+constexpr int kP2WStage = kW2X4 + kW2Dw;  // a two-unit weight stage
+template <int MODE, int GMT>
+__global__ void __launch_bounds__(kThreads, 2)
+k_grouped_q4_0_p2(const _Float16 *a_src, int topk, const uint32_t *order, const uint32_t *offsets,
+                  const uint32_t *tiles, const uint32_t *n_tiles, int n_ntile, const uint8_t *w0, const uint8_t *w1,
+                  int K, int n_rows, void *out, int ldo, int odt, int /*ksplit: 1*/, float * /*ws*/, int /*R*/,
+                  int /*ldw*/) {
+  constexpr int kAStage = q0_astage<GMT>(), kDmaA = q0_dma_a<GMT>();
+  constexpr int kW = 2 * kAStage;  // the weight stages follow the two A stages
+  constexpr int MB = GMT / 16, QMAX = GMT / 32;
+  static_assert(kDmaA >= 1 && kW + 2 * kP2WStage <= 81920, "two workgroups a CU");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kW + 2 * kP2WStage];
+  Tile t;
+  if (!tile_of<GMT>(offsets, tiles, n_tiles, n_ntile, &t)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, g = lane >> 4;
+  const uint32_t wrow = 36u * uint32_t(K / 64);
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(lds));
+
+  uint32_t a_off[kDmaA];  // A: as in k_grouped_q4_0
+#pragma unroll
+  for (int i = 0; i < kDmaA; ++i) {
+    const int q = 64 * (kDmaA * wave + i) + lane, r = q >> 3, c = (q & 7) ^ (r & 7);
+    const int p = t.row0 + (r < t.rows ? r : 0);
+    const uint32_t row = MODE == MODE_GATE_UP ? order[p] / uint32_t(topk) : uint32_t(p);
+    a_off[i] = row * uint32_t(K) * 2u + 16u * uint32_t(c);
+  }
+  const uint32_t a_live = a_live_mask<kDmaA>(wave, t.rows);
+  // weights: as in k_grouped_q4_0_w2 (wavefront w copies tile features 64 w .. 64 w + 63)
+  const uint8_t *m = MODE == MODE_GATE_UP && wave >= 2 ? w1 : w0;
+  const int row_base = (MODE == MODE_GATE_UP ? t.nt * (GN / 2) - (wave >= 2 ? GN / 2 : 0) : t.nt * GN) + 64 * wave;
+  const uint8_t *wbase = m + (size_t(t.e) * n_rows) * wrow;
+  uint32_t w_off[4], d_off[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int s = lane >> 2, fl = 16 * (s >> 2) + 4 * i + (s & 3);
+    w_off[i] = uint32_t(row_base + fl) * wrow + 16u * uint32_t(lane & 3);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) d_off[j] = uint32_t(row_base + 32 * j + (lane >> 1)) * wrow + 64u + 4u * uint32_t(lane & 1);
+  const int nk = K / GK, np = nk / 2;
+  auto issue_a = [&](int kk) {  // step kk's A into A stage kk % 2
+    const uint32_t st = lds0 + uint32_t(kk & 1) * kAStage;
+    const _Float16 *ab = a_src + size_t(kk) * GK;
+#pragma unroll
+    for (int i = 0; i < kDmaA; ++i)
+      dma_a(ab, a_off[i], __builtin_amdgcn_readfirstlane(st + 1024u * uint32_t(kDmaA * wave + i)), a_live >> i & 1u);
+  };
+  auto issue_w = [&](int p) {  // pair p's weights into weight stage p % 2
+    const uint8_t *wb = wbase + size_t(p) * 72;
+    const uint32_t sw = lds0 + uint32_t(kW + (p & 1) * kP2WStage);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma<16>(wb, w_off[i], __builtin_amdgcn_readfirstlane(sw + uint32_t(wave * 4 * kW2Blk + i * kW2Blk)));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      dma<4>(wb, d_off[j], __builtin_amdgcn_readfirstlane(sw + uint32_t(kW2X4) + 256u * uint32_t(2 * wave + j)));
+  };
+
+  f32x4 acc[4][MB];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const Q0Lane2 ql = q0_lane2<MODE>(wave, fr, g, 0);
+  // step kk = 4 b + J: A stage J % 2, weight stage J / 2, unit J % 2 of the pair (compile-time LDS offsets)
+  auto compute = [&](auto jj, auto qn) {
+    constexpr int J = decltype(jj)::value, QN = decltype(qn)::value;
+    q0_step_pair<QN, MB, J % 2>(lds + (J % 2) * kAStage, lds + kW + (J / 2) * kP2WStage, ql, fr, g, acc);
+  };
+
+  // Before step kk + 1 every wavefront waits for its copies of A(kk + 1), issued at the start of step kk, and of
+  // the weights of pair (kk + 1) / 2, issued at step kk - 1 or earlier. The counter counts in issue order: on even
+  // kk the 6 copies of pair kk / 2 + 1 went out after A(kk + 1) and may stay out; on odd kk nothing did.
+  issue_a(0);
+  issue_w(0);
+  wait_vm<0>();
+  barrier_lds();
+  auto run = [&](auto qn) {
+    for (int kb = 0; kb < nk; kb += 4) {
+      static_for<0, 4>([&](auto j) {
+        constexpr int J = decltype(j)::value;
+        const int kk = kb + J;
+        if (kk < nk) {
+          if (kk + 1 < nk) issue_a(kk + 1);
+          const bool w_out = J % 2 == 0 && kk / 2 + 1 < np;
+          if (w_out) issue_w(kk / 2 + 1);
+          compute(j, qn);
+          if (kk + 1 < nk) {
+            if (w_out)
+              wait_vm<6>();
+            else
+              wait_vm<0>();
+            barrier_lds();
+          }
+        }
+      });
+    }
+  };
+  if constexpr (QMAX == 2) {
+    if (t.rows <= 32)  // uniform across the workgroup
+      run(IC<1>{});
+    else
+      run(IC<2>{});
+  } else {
+    switch ((t.rows + 31) / 32) {  // uniform across the workgroup
+      case 1: run(IC<1>{}); break;
+      case 2: run(IC<2>{}); break;
+      case 3: run(IC<3>{}); break;
+      default: run(IC<4>{}); break;
+    }
   }
   store_tile<MODE, MB>(acc, t, wave, fr, g, out, ldo, odt);
 }
@@ -1739,6 +1869,13 @@ static int q0_stages32() {
 // 817 -> 761 us, gate/up 421 -> 390, down 252 -> 227, the same bits); LMOE_QK_W2=1 keeps one step at a time.
 static bool qk_pairs() { return env_knob("LMOE_QK_W2") != 1; }
 
+// The tall-tile Q4_0 GEMMs on the GGUF layout stage their weights two units at a time (k_grouped_q4_0_p2) where
+// K % 128 == 0: cfg3 chunk 750-756 -> 717-721 us (gate/up 414-420 -> 394-405, down 250-261 -> 235-242), the same
+// bits. LMOE_Q0_P2=1 keeps the one-unit kernel.
+static bool q0_tall_pairs(bool sl, int bm, int K, int ksplit) {
+  return !sl && (bm == GM || bm == 64) && ksplit == 1 && (K / GK) % 2 == 0 && env_knob("LMOE_Q0_P2") != 1;
+}
+
 static int q0_two_unit(bool sl, int bm, int nst, int K, int ksplit) {
   const int v = env_knob("LMOE_Q0_W2");
   if (sl || bm != 32 || nst != 3 || (K / GK) % (2 * ksplit) != 0 || v == 1) return 0;
@@ -1790,6 +1927,8 @@ static int grouped_gate_up(const char *fn, bool sl, const void *x, int xdtype, i
                                  : k_grouped_q4_0<MODE_GATE_UP>);
     if (const int w2 = q0_two_unit(sl, bm, nst, H, ksplit))
       kern = w2 == 2 ? k_grouped_q4_0_w2<MODE_GATE_UP, 32, 2> : k_grouped_q4_0_w2<MODE_GATE_UP, 32, 3>;
+    if (q0_tall_pairs(sl, bm, H, ksplit))
+      kern = bm == 64 ? k_grouped_q4_0_p2<MODE_GATE_UP, 64> : k_grouped_q4_0_p2<MODE_GATE_UP, GM>;
     launch(kern, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, topk, order, offsets, tiles, n_tiles, n_ntile, wg,
            wu, H, I, h, I, int(LMOE_F16), ksplit, ws, R, 2 * I);
     if (ksplit > 1) {
@@ -1850,6 +1989,8 @@ static int grouped_down(const char *fn, bool sl, const void *h, int R, const uin
                                  : k_grouped_q4_0<MODE_DOWN>);
     if (const int w2 = q0_two_unit(sl, bm, nst, I, ksplit))
       kern = w2 == 2 ? k_grouped_q4_0_w2<MODE_DOWN, 32, 2> : k_grouped_q4_0_w2<MODE_DOWN, 32, 3>;
+    if (q0_tall_pairs(sl, bm, I, ksplit))
+      kern = bm == 64 ? k_grouped_q4_0_p2<MODE_DOWN, 64> : k_grouped_q4_0_p2<MODE_DOWN, GM>;
     launch(kern, dim3(unsigned(grid)), dim3(kThreads), 0, st, a, 1, static_cast<const uint32_t *>(nullptr), offsets,
            tiles, n_tiles, n_ntile, wd, static_cast<const uint8_t *>(nullptr), I, H, y, H, ydtype, ksplit, ws, R,
            H);

@@ -503,3 +503,37 @@ def test_q4_k_pair_staging_same_bits(H, I, E, monkeypatch):
     assert np.array_equal(y0.view(np.uint32)[valid], y1.view(np.uint32)[valid])
     _, yw = moe.gemv(host(x.float()), tuple(host(b) for b in w), slots, 1, types)
     assert moe.rel_l2(y1[valid], yw[order][valid]) < BAR
+
+
+@pytest.mark.parametrize("bm,H,I,E", [(128, 2048, 768, 9), (64, 2048, 768, 9), (128, 512, 1408, 5), (128, 256, 128, 4)])
+def test_q4_0_tall_pair_staging_same_bits(bm, H, I, E, monkeypatch):
+    """The 128- and 64-row Q4_0 GEMMs on the GGUF layout with the weights staged two units at a time (the
+    default): h and y bit-equal to the one-unit kernel's (LMOE_Q0_P2=1), gate/up and down, on groups of 0, 1, 31, 32, 33, 64
+    and 200 rows and a slot past the experts; K from two units (down at I = 128) up."""
+    from larder_amd import grouped
+    types = ("Q4_0",) * 3
+    w = tuple(dev(b) for b in experts(types, H, I, E, 95))
+    rng = np.random.default_rng(bm + H + I)
+    sizes = [0, 1, 31, 32, 33, 64, 200, 5, 2][:E]
+    slots = np.concatenate([np.full(n, e) for e, n in enumerate(sizes)]).astype(np.int32)
+    rng.shuffle(slots)
+    slots[3] = E + 1
+    R = slots.size
+    x = dev(rng.standard_normal((R, H)).astype(np.float16))
+    G = grouped.Grouping(R, E, bm=bm).run(dev(slots))
+    outs = []
+    for knob in ("1", ""):
+        monkeypatch.setenv("LMOE_Q0_P2", knob)
+        h = torch.empty((R, I), dtype=torch.float16, device="cuda")
+        y = torch.empty((R, H), dtype=torch.float32, device="cuda")
+        grouped.gate_up(x, G, 1, w[0], w[1], types, h, ksplit=1)
+        grouped.down(h, G, w[2], types[2], y, ksplit=1)
+        torch.cuda.synchronize()
+        outs.append((host(h), host(y)))
+    order = host(G.order)
+    valid = slots[order] < E
+    (h0, y0), (h1, y1) = outs
+    assert np.array_equal(h0.view(np.uint16)[valid], h1.view(np.uint16)[valid])
+    assert np.array_equal(y0.view(np.uint32)[valid], y1.view(np.uint32)[valid])
+    _, yw = moe.gemv(host(x.float()), tuple(host(b) for b in w), slots, 1, types)
+    assert moe.rel_l2(y1[valid], yw[order][valid]) < BAR
