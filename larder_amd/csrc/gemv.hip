@@ -634,16 +634,18 @@ __global__ void __launch_bounds__(256)
               int n_experts, int I, int H, const float *shared, const float *gate, int gate_stride,
               const void *residual, int rdt, void *out, int odt) {
   constexpr int RB = 2;
-  // KS = 2 (a token's units past 128): wavefronts 2 q and 2 q + 1 share rows [(2 bx + q) RB, +RB), each over half of
-  // the experts (the first ceil(k / 2), the rest), and add their two row sums through LDS
+  static_assert(KS == 1 || KS == 2, "experts split over 1 or 2 wavefronts");
+  // KS = 2: wavefronts 2 g and 2 g + 1 share rows [(2 bx + g) RB, +RB), wavefront 2 g + q over experts
+  // [q kh, q kh + kh) (kh = ceil(k / 2); k >= 2, so both shares hold experts), and the second share's row sums are
+  // added to the first's through LDS
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int half = KS == 2 ? (wave & 1) : 0;
-  const int kh = KS == 2 ? (k + 1) / 2 : k;
-  const int j0 = half * kh, kj = KS == 2 ? (half ? k - kh : kh) : k;  // this wavefront's experts [j0, j0 + kj)
+  const int q = KS > 1 ? wave % KS : 0;
+  const int kh = KS > 1 ? (k + KS - 1) / KS : k;
+  const int j0 = q * kh, kj = KS > 1 ? min(kh, k - j0) : k;  // this wavefront's experts [j0, j0 + kj)
   const int P = I / 64, U = kj * P;
   const int CJ = RB * 9 * P / 4, CW = kj * CJ;  // 16-byte chunks of one expert's RB rows, of this wavefront's
   const int t = blockIdx.y;
-  const int n0 = KS == 2 ? (blockIdx.x * 2 + (wave >> 1)) * RB : (blockIdx.x * 4 + wave) * RB;
+  const int n0 = (blockIdx.x * (4 / KS) + wave / KS) * RB;
   extern __shared__ u32x4 lds4[];
   uint32_t *stage = reinterpret_cast<uint32_t *>(lds4) + wave * (kh * CJ * 4);
 
@@ -721,16 +723,16 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int r = 0; r < RB; ++r)
       acc[r] = fmaf(fa[a], row_unit_dot_r<TD>(stage + (ja[a] * RB + r) * 9 * P, pa[a], xv[a], s0[a], s1[a]), acc[r]);
-  // 6. the rows' sums (KS = 2: the second half's through LDS into the first's), then shared expert and residual
+  // 6. the rows' sums (KS = 2: the second share's through LDS into the first's), then shared expert and residual
 #pragma unroll
   for (int r = 0; r < RB; ++r) acc[r] = wave_sum(acc[r]);
   if (KS == 2) {
-    __shared__ float part[2 * RB];
-    if (half == 1 && lane < RB) part[(wave >> 1) * RB + lane] = lane == 0 ? acc[0] : acc[1];
+    __shared__ float part[4 * RB];  // [wavefront][row]
+    if (q == 1 && lane < RB) part[wave * RB + lane] = lane == 0 ? acc[0] : acc[1];
     __syncthreads();
-    if (half == 1) return;
+    if (q == 1) return;
 #pragma unroll
-    for (int r = 0; r < RB; ++r) acc[r] += part[(wave >> 1) * RB + r];
+    for (int r = 0; r < RB; ++r) acc[r] += part[(wave + 1) * RB + r];
   }
   if (lane < RB) {
     float v = acc[0];
@@ -1484,9 +1486,14 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
   {  // prepared h, at most 128 units a token, P even, H a multiple of 8: the register-resident kernel
     const int P = a.I / 64, U = a.k * P, CW = a.k * 9 * P / 2;
     const int kh = (a.k + 1) / 2, Uh = kh * P, CWh = kh * 9 * P / 2;
-    if (a.hprep && !(U <= 128 && CW <= 64 * 9) && Uh <= 128 && P % 2 == 0 && a.H % 4 == 0 && CWh <= 64 * 9) {
-      // up to 256 units: two wavefronts a row pair, half of the experts each (config 1 with its shared expert
-      // folded in as four slices: 8 experts of 22 units)
+    // Two wavefronts a row pair, half of the experts each, wherever both halves fit (k >= 2): twice the workgroups
+    // of one wavefront a row pair, so two wavefronts a SIMD have their loads in flight (cfg2 48-layer graph 14.72 ->
+    // 14.39 us a layer, cfg5 24.15 -> 23.62; four wavefronts a row pair measured 15.21 and 25.5). Up to 256 units a
+    // token it is the only register-resident form (cfg1 with its shared expert folded in: 8 experts of 22 units).
+    // LMOE_DOWN_KS=1 keeps one wavefront a row pair where a token has at most 128 units.
+    const char *ks_env = getenv("LMOE_DOWN_KS");
+    const bool ks1 = ks_env && atoi(ks_env) == 1 && U <= 128 && CW <= 64 * 9;
+    if (a.hprep && a.k >= 2 && !ks1 && Uh <= 128 && P % 2 == 0 && a.H % 4 == 0 && CWh <= 64 * 9) {
       const int NU = Uh <= 64 ? 1 : 2, ncw = (CWh + 63) / 64;
       auto go = [&](auto td, auto nu, auto nc) {
         constexpr int TD = decltype(td)::value, N = decltype(nu)::value, C = decltype(nc)::value;
