@@ -374,8 +374,8 @@ __global__ void __launch_bounds__(256)
         scores_out[s] = sc;
       }
       id = uint32_t(__builtin_amdgcn_readlane(int(id), j));
-    } else {  // only the slot's own pick
-      topk_wave<N, false>(v, n_experts, topk, norm, scr, &id, nullptr, j);
+    } else {  // only the slot's own pick: the expert of rank j
+      id = rank_pick_wave<N>(v, n_experts, j);
     }
     e = id;
   }

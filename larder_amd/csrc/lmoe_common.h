@@ -386,6 +386,66 @@ __device__ __forceinline__ void topk_wave(const float *v, int E, int k, int norm
   *score_out = mine;
 }
 
+// The expert of rank `want` (0-based; larger logit first, equal logits by lower index) of a token's logits
+// v[j] = row[lane + 64 j] (j < NPL, E <= 64 NPL), in every lane: the pick topk_wave<NPL, false> returns for that rank,
+// without its compaction and ranking (no LDS). The one-bit search of topk_wave for the (want + 1)-th largest key:
+//   * stopped at a prefix with exactly want + 1 keys at or above it, those keys are ranks 0 .. want, so rank want is
+//     the smallest of them, the highest index among equal ones;
+//   * run to the end, the prefix is the (want + 1)-th largest key itself, and rank want is the
+//     (want + 1 - #keys above it)-th lowest index holding it.
+// Emulated on the CPU against the oracle on tie-heavy rows (tests/emul/topk_wave.cpp, rank_pick). 0xFFFFFFFF when no
+// key qualifies (E <= want).
+template <int NPL>
+__device__ __forceinline__ uint32_t rank_pick_wave(const float *v, int E, int want) {
+  const int lane = threadIdx.x & 63;
+  uint32_t key[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) key[j] = lane + 64 * j < E ? logit_key(v[j]) : 0u;
+  const int need = want + 1;
+  uint32_t thr = 0;
+  bool exact = false;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = thr | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) cnt += __popcll(__ballot(key[j] >= cand));
+    if (cnt >= need) {  // wavefront-uniform: a scalar branch
+      thr = cand;
+      if (cnt == need) {
+        exact = true;
+        break;
+      }
+    }
+  }
+  if (exact) {
+    uint32_t m = 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) m = min(m, key[j] >= thr ? key[j] : 0xFFFFFFFFu);
+    m = wave_min_u32(m);
+#pragma unroll
+    for (int j = NPL - 1; j >= 0; --j) {
+      const uint64_t eq = __ballot(key[j] == m);
+      if (eq) return uint32_t(64 * j + 63 - __builtin_clzll(eq));
+    }
+    return 0xFFFFFFFFu;
+  }
+  int n_gt = 0;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) n_gt += __popcll(__ballot(key[j] > thr));
+  int rem = need - n_gt;  // >= 1: fewer than want + 1 keys lie above the (want + 1)-th largest
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    uint64_t eq = __ballot(key[j] == thr);
+    const int c = __popcll(eq);
+    if (rem <= c) {
+      for (int i = 1; i < rem; ++i) eq &= eq - 1;  // clear the rem - 1 lowest holders
+      return uint32_t(64 * j + __builtin_ctzll(eq));
+    }
+    rem -= c;
+  }
+  return 0xFFFFFFFFu;
+}
+
 // Entries of ck[f0, f0 + 2 N) (composite keys, 16-byte aligned) above `me`. Composite key: order-preserving logit
 // key in the high half, 0xFFFFFFFF - expert in the low half, so a larger composite is the better pick (larger logit,
 // or equal logit and lower index) and no two experts tie; 0 pads an empty slot below every expert.

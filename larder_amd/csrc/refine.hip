@@ -187,8 +187,7 @@ __global__ void __launch_bounds__(rf::NT) k_router_refine(RefineArgs a) {
     lo[j] = wide ? -INFINITY : mv[j] - eb;
     hi[j] = wide ? INFINITY : mv[j] + eb;
   }
-  uint32_t kid;
-  topk_wave<NPL, false>(lo, E, a.k, 0, scr[wave], &kid, nullptr, a.k - 1);  // the expert holding the k-th lo
+  const uint32_t kid = rank_pick_wave<NPL>(lo, E, a.k - 1);  // the expert holding the k-th lo
   float tau = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {

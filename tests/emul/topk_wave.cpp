@@ -1,12 +1,13 @@
 // Host emulation of the wavefront top-k (larder_amd/csrc/lmoe_common.h, topk_wave): 64 lanes as loops, a ballot
 // as a 64-bit mask, the LDS pick area as an array of 64 words. Two threshold searches: the kernel's, one bit a
 // step (up to 32 steps, stopping once exactly k keys are at or above the prefix), and a two-bits-a-step form (16
-// steps, three candidates a step). Used by
+// steps, three candidates a step). A third form emulates rank_pick_wave (the pick of one rank, no compaction). Used by
 // tests/test_topk_emulation.py to check, on the CPU, that both give the oracle's picks on tie-heavy rows and that
 // the compaction never writes more than k picks.
 //
 // stdin: "rows E k" then rows lines of E float32 bit patterns (hex); stdout per row: "ok|BAD n_picks ids..." for
-// each search. argv[1]: a slip planted in a search (0: none; 1-3 the two-bit one, 4 the one-bit one).
+// each search, then "ok k ids..." of rank_pick_wave for ranks 0 .. k - 1. argv[1]: a slip planted in a search (0:
+// none; 1-3 the two-bit one, 4 the one-bit one, 5-6 rank_pick).
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -117,6 +118,63 @@ static int picks(const std::vector<uint32_t> &key, int E, int k, uint32_t thr, s
   return n_sel;
 }
 
+// rank_pick_wave: the expert of rank `want` (larger logit first, equal logits by lower index) without the top-k's
+// compaction and ranking. The one-bit search for the (want + 1)-th largest key; stopped at a prefix with exactly
+// want + 1 keys at or above it, rank want is the smallest of those keys, the highest index among equal ones; run to
+// the end, the prefix is that key itself and rank want is the (want + 1 - #keys above it)-th lowest index holding it.
+// Slips (planted on the CPU only): 5 = the lowest index among the smallest keys in the stopped case; 6 = the keys
+// above the threshold not subtracted in the full case.
+static uint32_t rank_pick(const std::vector<uint32_t> &key, int want) {
+  const int NPL = int(key.size()) / 64, need = want + 1;
+  uint32_t thr = 0;
+  bool exact = false;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = thr | (1u << b);
+    int cnt = 0;
+    for (uint32_t v : key) cnt += v >= cand;
+    if (cnt >= need) {
+      thr = cand;
+      if (cnt == need) {
+        exact = true;
+        break;
+      }
+    }
+  }
+  if (exact) {
+    uint32_t m = 0xFFFFFFFFu;
+    for (uint32_t v : key)
+      if (v >= thr && v < m) m = v;
+    if (g_slip == 5) {
+      for (int j = 0; j < NPL; ++j)
+        for (int lane = 0; lane < 64; ++lane)
+          if (key[lane + 64 * j] == m) return uint32_t(lane + 64 * j);
+      return 0xFFFFFFFFu;
+    }
+    for (int j = NPL - 1; j >= 0; --j) {
+      uint64_t eq = 0;
+      for (int lane = 0; lane < 64; ++lane)
+        if (key[lane + 64 * j] == m) eq |= uint64_t(1) << lane;
+      if (eq) return uint32_t(64 * j + 63 - __builtin_clzll(eq));
+    }
+    return 0xFFFFFFFFu;
+  }
+  int n_gt = 0;
+  for (uint32_t v : key) n_gt += v > thr;
+  int rem = need - (g_slip == 6 ? 0 : n_gt);
+  for (int j = 0; j < NPL; ++j) {
+    uint64_t eq = 0;
+    for (int lane = 0; lane < 64; ++lane)
+      if (key[lane + 64 * j] == thr) eq |= uint64_t(1) << lane;
+    const int c = popc(eq);
+    if (rem <= c) {
+      for (int i = 1; i < rem; ++i) eq &= eq - 1;
+      return uint32_t(64 * j + __builtin_ctzll(eq));
+    }
+    rem -= c;
+  }
+  return 0xFFFFFFFFu;
+}
+
 int main(int argc, char **argv) {
   if (argc > 1) g_slip = std::atoi(argv[1]);
   int rows, E, k;
@@ -138,8 +196,12 @@ int main(int argc, char **argv) {
       const int n = picks(key, E, k, thr, ids, &overrun);
       std::printf("%s %d", (n == k && overrun == 0) ? "ok" : "BAD", n);
       for (uint32_t i : ids) std::printf(" %u", i);
-      std::printf(form == 0 ? " |" : "\n");
+      std::printf(" |");
     }
+    // the third form: rank_pick for every rank of the top k
+    std::printf(" ok %d", k);
+    for (int w = 0; w < k; ++w) std::printf(" %u", rank_pick(key, w));
+    std::printf("\n");
   }
   return 0;
 }

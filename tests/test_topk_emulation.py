@@ -1,8 +1,10 @@
 """The wavefront top-k's algorithm (larder_amd/csrc/lmoe_common.h, topk_wave) emulated on the CPU
 (tests/emul/topk_wave.cpp: 64 lanes as loops, ballots as masks): its one-bit threshold search (which stops once
-exactly k keys are at or above the prefix) and a two-bits-a-step form both give the oracle's picks (lowest index first among equal logits) on the tie-heavy rows the GPU tests use
-(test_gpu_decode.tie_logits), in float32, float16 and bfloat16, and the compaction writes exactly k picks, so it
-never reaches past the 32-pick LDS area. This is the CPU check a faster top-k must pass before it runs on a GPU."""
+exactly k keys are at or above the prefix) and a two-bits-a-step form both give the oracle's picks (lowest index
+first among equal logits) on the tie-heavy rows the GPU tests use (test_gpu_decode.tie_logits), in float32, float16
+and bfloat16, and the compaction writes exactly k picks, so it never reaches past the 32-pick LDS area. So does
+rank_pick_wave (one rank's pick without the compaction), rank by rank. This is the CPU check a faster top-k must pass
+before it runs on a GPU."""
 import shutil
 import subprocess
 
@@ -64,7 +66,7 @@ def test_wave_topk_emulation_matches_oracle(emul, E, k, dtype):
     lg = rows_for(E, k, dtype)
     want, _ = moe.router(lg, k, False)
     for r, forms in enumerate(run_emul(emul, lg, k)):
-        for name, f in zip(("one-bit", "two-bit"), forms):
+        for name, f in zip(("one-bit", "two-bit", "rank pick"), forms):
             assert f[0] == "ok" and int(f[1]) == k, (name, r, f)
             assert [int(v) for v in f[2:]] == [int(v) for v in want[r]], (name, r)
 
@@ -99,3 +101,18 @@ def test_emulation_catches_an_early_stop_slip(emul):
             wrong += f[0] != "ok" or [int(v) for v in f[2:]] != [int(v) for v in want[r]]
             over += int(f[1]) > k
     assert wrong > 0 and over > 0
+
+
+@pytest.mark.parametrize("slip", [5, 6])
+def test_emulation_catches_rank_pick_slips(emul, slip):
+    """rank_pick_wave (one rank's pick, no compaction) on the tie-heavy rows: a slip planted on the CPU (5: the lowest
+    index among the smallest keys when the search stops early; 6: the keys above the threshold not counted when it
+    runs to the end) gives wrong ids."""
+    wrong = 0
+    for E, k in [(128, 8), (512, 10), (60, 4)]:
+        for dtype in (torch.float32, torch.bfloat16):
+            lg = rows_for(E, k, dtype)
+            want, _ = moe.router(lg, k, False)
+            for r, forms in enumerate(run_emul(emul, lg, k, slip)):
+                wrong += [int(v) for v in forms[2][2:]] != [int(v) for v in want[r]]
+    assert wrong > 0
