@@ -1503,11 +1503,13 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
       };
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;
+      using C4 = std::integral_constant<int, 4>;
       using C5 = std::integral_constant<int, 5>;
       using C7 = std::integral_constant<int, 7>;
       using C9 = std::integral_constant<int, 9>;
       auto by_c = [&](auto td, auto nu) {
-        if (ncw <= 5) go(td, nu, C5());
+        if (ncw <= 4) go(td, nu, C4());
+        else if (ncw <= 5) go(td, nu, C5());
         else if (ncw <= 7) go(td, nu, C7());
         else go(td, nu, C9());
       };
