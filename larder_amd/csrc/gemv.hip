@@ -293,7 +293,7 @@ __global__ void __launch_bounds__(256)
   static_assert(!RAW || NPL == 0, "raw x: slots given");
   static_assert(!RAW || NW * 2 * RB * 9 * P >= 64 * P, "the stages hold the raw row (f32 at most)");
   constexpr int C = RB * 9 * P / 4;  // 16-byte chunks of RB rows of one matrix
-  constexpr int NC = (C + 63) / 64;
+  constexpr int NC2 = (2 * C + 63) / 64;  // of both matrices' rows, a lane
   constexpr int STAGE = 2 * RB * 9 * P;  // dwords a wavefront
   constexpr int XC = 9 * P;              // 16-byte chunks of the prepared activation row
   constexpr int NT = 64 * NW;
@@ -384,12 +384,13 @@ __global__ void __launch_bounds__(256)
   const size_t rsafe = size_t(valid ? e : 0u) * I + min(r0, I - RB);
   const u32x4 *gsrc = reinterpret_cast<const u32x4 *>(wg + rsafe * (36 * P));
   const u32x4 *usrc = reinterpret_cast<const u32x4 *>(wu + rsafe * (36 * P));
-  u32x4 vg[NC], vu[NC];
+  // the gate rows' C chunks then the up rows' as one run of 2 C (a lane past the end reloads the last chunk): stage
+  // chunk q holds gate chunk q (q < C) or up chunk q - C
+  u32x4 vw[NC2];
 #pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int c = min(lane + 64 * i, C - 1);
-    vg[i] = __builtin_nontemporal_load(gsrc + c);
-    vu[i] = __builtin_nontemporal_load(usrc + c);
+  for (int i = 0; i < NC2; ++i) {
+    const int q = min(lane + 64 * i, 2 * C - 1);
+    vw[i] = __builtin_nontemporal_load(q < C ? gsrc + q : usrc + (q - C));
   }
   // the activation row into LDS (a thread past the end rewrites the last chunk with its own value; RAW: prepared
   // here from the raw row), then the weights into the wavefront's stage, with no branch between loads and stores so
@@ -429,11 +430,7 @@ __global__ void __launch_bounds__(256)
   __syncthreads();
   u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
 #pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int c = min(lane + 64 * i, C - 1);
-    st4[c] = vg[i];
-    st4[C + c] = vu[i];
-  }
+  for (int i = 0; i < NC2; ++i) st4[min(lane + 64 * i, 2 * C - 1)] = vw[i];
   __builtin_amdgcn_wave_barrier();
   if (r0 >= I) return;
   if (!valid) {
