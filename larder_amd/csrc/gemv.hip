@@ -616,9 +616,11 @@ __global__ void __launch_bounds__(64 * NW, 3)
 
 // ---- down + combine with the h units in registers ---------------------------------------------------------------
 //
-// For prepared h and k P <= 64 NU (k experts of P = I / 64 units; NU = 1 or 2 units a lane), P even. Grid
+// For prepared h and k P <= 64 NU (k experts of P = I / 64 units; NU = 1 or 2 units a lane), P even. KS = 1: grid
 // (H / (4 RB), T), four independent wavefronts a workgroup (no barrier); wavefront w of block (bx, t) takes output
-// rows [(4 bx + w) RB, +RB) of token t. Lane l holds h units u = l, l + 64 (u = j P + p: expert j, unit p) in
+// rows [(4 bx + w) RB, +RB) of token t. KS = 2 (the host's default where k >= 2): grid (H / (2 RB), T), two
+// wavefronts a row pair over half of the experts each, their sums met through LDS after one barrier (below). The
+// rest is written for KS = 1. Lane l holds h units u = l, l + 64 (u = j P + p: expert j, unit p) in
 // registers and their half-unit sums, computed there while the weights are in flight. The wavefront's RB rows of all
 // k experts (k RB 36 P bytes) come in with 16-byte loads, go to its own LDS region, and each lane dots its units with
 // the RB rows of its expert (a 36-byte unit read a dot), weighted by the router score; the rows' sums over the
