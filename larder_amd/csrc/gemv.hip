@@ -1003,7 +1003,7 @@ __global__ void __launch_bounds__(256)
   static_assert(P == 32 || P == 64, "32 or 64 units a row");
   constexpr int RB = 2, G = 64 / P, RG = RB / G;
   constexpr int C = RB * 9 * P / 4;  // 16-byte chunks of RB rows of one matrix
-  constexpr int NC = (C + 63) / 64;
+  constexpr int NC2 = (2 * C + 63) / 64;  // of both matrices' rows, a lane (one run, as in k_gate_up_xr)
   constexpr int STAGE = 2 * RB * 9 * P;  // dwords a wavefront
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r0 = (blockIdx.x * 4 + wave) * RB;
@@ -1017,16 +1017,15 @@ __global__ void __launch_bounds__(256)
 
   // the first run's rows into registers (clamped, unpredicated) while the window is copied
   const int rs = min(r0, I - RB);
-  u32x4 vg[NC], vu[NC];
+  u32x4 vw[NC2];
   auto fetch = [&](uint32_t e) {
     const size_t base = (size_t(e < uint32_t(n_experts) ? e : 0u) * I + rs) * (36 * P);
     const u32x4 *gs = reinterpret_cast<const u32x4 *>(wg + base);
     const u32x4 *us = reinterpret_cast<const u32x4 *>(wu + base);
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-      const int c = min(lane + 64 * i, C - 1);
-      vg[i] = __builtin_nontemporal_load(gs + c);
-      vu[i] = __builtin_nontemporal_load(us + c);
+    for (int i = 0; i < NC2; ++i) {
+      const int q = min(lane + 64 * i, 2 * C - 1);
+      vw[i] = __builtin_nontemporal_load(q < C ? gs + q : us + (q - C));
     }
   };
   fetch(slots[e0]);
@@ -1045,11 +1044,7 @@ __global__ void __launch_bounds__(256)
     while (r1 < ne && sl[r1] == e) ++r1;
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int i = 0; i < NC; ++i) {
-      const int c = min(lane + 64 * i, C - 1);
-      st4[c] = vg[i];
-      st4[C + c] = vu[i];
-    }
+    for (int i = 0; i < NC2; ++i) st4[min(lane + 64 * i, 2 * C - 1)] = vw[i];
     if (r1 < ne) fetch(sl[r1]);  // the next run's rows, in flight during this one
     __builtin_amdgcn_wave_barrier();
     const bool valid = e < uint32_t(n_experts);
