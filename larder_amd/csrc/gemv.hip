@@ -627,7 +627,7 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // wavefront finish on DPP / permlane swaps, then the gated shared-expert row and the residual are added. Memory order:
 // h units, ids and scores (one a lane), then the weights, whose addresses need only the ids; no load is predicated
 // (clamped indices; expert 0 stands in for an id past the experts, with a zero weight).
-template <int TD, int NU, int NCW, int KS = 1>
+template <int TD, int NU, int NCW, int KS = 1, int HL = 0>
 __global__ void __launch_bounds__(256)
     k_down_xr(const uint32_t *hprep, const uint32_t *ids, const float *scores, int k, const uint8_t *wd,
               int n_experts, int I, int H, const float *shared, const float *gate, int gate_stride,
@@ -647,21 +647,34 @@ __global__ void __launch_bounds__(256)
   const int n0 = (blockIdx.x * (4 / KS) + wave / KS) * RB;
   extern __shared__ u32x4 lds4[];
   uint32_t *stage = reinterpret_cast<uint32_t *>(lds4) + wave * (kh * CJ * 4);
+  // HL > 0: the wavefront's h chunks through LDS, after the four stages: 64 HL chunks a wavefront
+  u32x4 *hst = lds4 + 4 * kh * CJ + wave * 64 * HL;
 
   // 1. the token's ids and scores (lane j < k holds expert j's), then the h units. The empty asm with a memory
   // clobber keeps the compiler from sinking these loads below the weights' (the count of outstanding loads is in
-  // order, so the weight addresses then wait only for the ids and scores, and the h sums only for the h units)
+  // order, so the weight addresses then wait only for the ids and scores, and the h sums only for the h units).
+  // HL = 0: lane l loads its own units' 8 value chunks (8 NU loads); HL > 0: the wavefront's 8 U chunks as one run of
+  // HL loads a lane (ceil(8 U / 64): 6 instead of 8 at 48 units), unit-ordered into LDS below
   const int kl = min(lane, k - 1);
   const uint32_t my_id = ids[size_t(t) * k + kl];
   const float sc_ld = (scores ? scores + size_t(t) * k : reinterpret_cast<const float *>(ids))[kl];
   const float my_sc = scores ? sc_ld : 1.0f;
   const u32x4 *hb = reinterpret_cast<const u32x4 *>(hprep + (size_t(t) * k + j0) * P * XS);
-  u32x4 hq[NU][9];
+  u32x4 hq[NU][8];
+  u32x4 hl[HL > 0 ? HL : 1];
+  if constexpr (HL > 0) {
 #pragma unroll
-  for (int a = 0; a < NU; ++a) {
-    const int u = min(lane + 64 * a, U - 1);
+    for (int i = 0; i < HL; ++i) {
+      const int qc = min(lane + 64 * i, 8 * U - 1);
+      hl[i] = hb[(qc >> 3) * 9 + (qc & 7)];
+    }
+  } else {
 #pragma unroll
-    for (int i = 0; i < 9; ++i) hq[a][i] = hb[u * 9 + i];
+    for (int a = 0; a < NU; ++a) {
+      const int u = min(lane + 64 * a, U - 1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hq[a][i] = hb[u * 9 + i];
+    }
   }
   asm volatile("" ::: "memory");
   // 2. the weights: chunk c of expert j0 + j's block at rows [n0, n0 + RB)
@@ -676,7 +689,23 @@ __global__ void __launch_bounds__(256)
     w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wd + (size_t(e) * H + nsafe) * rowb) + cc);
   }
   asm volatile("" ::: "memory");
-  // 3. each unit's expert, weight (0 past the units or the experts) and half-unit sums
+  // 3. (HL > 0: the h chunks into LDS, chunk c of unit u at 8 u + (c ^ ((u >> 1) & 7)), so that neither the run's
+  // writes nor each lane's reads of its own unit meet twice in a bank group; then each lane's units back), each
+  // unit's expert, weight (0 past the units or the experts) and half-unit sums
+  if constexpr (HL > 0) {
+#pragma unroll
+    for (int i = 0; i < HL; ++i) {
+      const int qc = min(lane + 64 * i, 8 * U - 1), u = qc >> 3;  // a lane past the end rewrites the last chunk
+      hst[8 * u + ((qc & 7) ^ ((u >> 1) & 7))] = hl[i];
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int a = 0; a < NU; ++a) {
+      const int u = min(lane + 64 * a, U - 1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hq[a][i] = hst[8 * u + (i ^ ((u >> 1) & 7))];
+    }
+  }
   int ja[NU], pa[NU];
   float fa[NU], s0[NU], s1[NU];
   uint32_t xv[NU][32];
@@ -1488,12 +1517,24 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
     const char *ks_env = getenv("LMOE_DOWN_KS");
     const bool ks1 = ks_env && atoi(ks_env) == 1 && U <= 128 && CW <= 64 * 9;
     if (a.hprep && a.k >= 2 && !ks1 && Uh <= 128 && P % 2 == 0 && a.H % 4 == 0 && CWh <= 64 * 9) {
-      const int NU = Uh <= 64 ? 1 : 2, ncw = (CWh + 63) / 64;
+      const int NU = Uh <= 64 ? 1 : 2, ncw = (CWh + 63) / 64, hl = (8 * Uh + 63) / 64;
+      // the h chunks as one run through LDS where that saves loads: 6 a lane at 48 units (cfg2, cfg5), 11 at 88
+      // (cfg1), against 8 NU
+      const int HLr = getenv("LMOE_DOWN_HL") && atoi(getenv("LMOE_DOWN_HL")) == 0 ? 0 : hl;
       auto go = [&](auto td, auto nu, auto nc) {
         constexpr int TD = decltype(td)::value, N = decltype(nu)::value, C = decltype(nc)::value;
-        launch(k_down_xr<TD, N, C, 2>, dim3(a.H / 4, a.T), dim3(256), size_t(4) * 4 * CWh * 4, st, a.hprep, a.ids,
-               a.scores, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt,
-               a.out, a.odt);
+        auto run = [&](auto hlc) {
+          constexpr int HLc = decltype(hlc)::value;
+          launch(k_down_xr<TD, N, C, 2, HLc>, dim3(a.H / 4, a.T), dim3(256),
+                 size_t(4) * 16 * (CWh + 64 * HLc), st, a.hprep, a.ids, a.scores, a.k, a.wd, a.n_experts, a.I, a.H,
+                 a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt);
+        };
+        if (N == 1 && HLr == 6)
+          run(std::integral_constant<int, 6>());
+        else if (N == 2 && HLr == 11)
+          run(std::integral_constant<int, 11>());
+        else
+          run(std::integral_constant<int, 0>());
       };
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;
