@@ -1791,15 +1791,16 @@ extern "C" int lmoe_grouped_pick_tile_rows(int R, int E, int type_g, int type_u,
 }
 
 // Split-K slices for one grouped GEMM over K: with 32-row tiles and fewer than 16 rows an expert, few tiles have
-// work and each would walk every K step alone, so a tile is split over 4, 3 or 2 workgroups of at least 4 K steps
-// each; otherwise 1.
+// work and each would walk every K step alone, so a tile is split over 4, 3 or 2 workgroups of at least 8 K steps
+// each (4 steps of the two-unit GGUF-layout kernel); otherwise 1. Shorter slices lose to the finish kernel they need
+// (cfg4's down, 12 K steps: one slice 33.3 us against three slices 30.2 + 4.1 for the finish).
 extern "C" int lmoe_grouped_pick_ksplit(int R, int E, int bm, int K) {
   const int steps = K / GK;
   const int want = env_knob("LMOE_KSPLIT");
   if (want == 1 || (want > 1 && want <= 8 && bm == 32 && steps % want == 0 && R <= 65535)) return want;
   if (bm != 32 || E <= 0 || (long long)R >= 16LL * E) return 1;
   for (int s = 4; s >= 2; --s)
-    if (steps % s == 0 && steps / s >= 4) return s;
+    if (steps % (2 * s) == 0 && steps / s >= 8) return s;
   return 1;
 }
 

@@ -196,7 +196,8 @@ def test_gemm_k_order_index():
 
 def test_grouped_launch_choices(built_lib):
     """lmoe_grouped_pick_tile_rows / pick_ksplit / workspace_bytes (host functions, no GPU): the configurations'
-    choices, and split-K slices that divide K into at least 4 steps each with a workspace that holds them."""
+    choices, and split-K slices that divide K into at least 8 steps each (4 two-unit steps) with a workspace that
+    holds them."""
     from larder_amd import grouped
     q = _lib.qcode
     pick = lambda R, E, ts: built_lib.lmoe_grouped_pick_tile_rows(R, E, *(q(t) for t in ts))  # noqa: E731
@@ -215,10 +216,11 @@ def test_grouped_launch_choices(built_lib):
         if bm != 32 or R >= 16 * E:
             assert ks == 1
         else:
-            assert ks in (1, 2, 3, 4) and (K // 64) % ks == 0 and (ks == 1 or K // 64 // ks >= 4)
-    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 2048) == 4   # 32 steps
-    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 768) == 3    # 12 steps
-    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 256) == 1    # 4 steps: no slice of 4
+            assert ks == 1 or (ks in (2, 3, 4) and (K // 64) % (2 * ks) == 0 and K // 64 // ks >= 8)
+    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 2048) == 4   # 32 steps: 4 slices of 8
+    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 768) == 1    # 12 steps: no slice of 8
+    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 1024) == 2   # 16 steps: 2 slices of 8
+    assert built_lib.lmoe_grouped_pick_ksplit(512, 128, 32, 256) == 1    # 4 steps
     R, E, H, I = 512, 128, 2048, 768
     ku, kd = built_lib.lmoe_grouped_pick_ksplit(R, E, 32, H), built_lib.lmoe_grouped_pick_ksplit(R, E, 32, I)
     assert built_lib.lmoe_grouped_workspace_bytes(R, E, 32, H, I) == 4 * max(ku * R * 2 * I, kd * R * H)
