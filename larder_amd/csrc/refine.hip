@@ -10,9 +10,12 @@
 //       e_j = (g A + C + D) a_j + A d_j + B c_j + c B b_j
 //     with, per token, A = |f16(x)|, B = |x|, C = |f16(x) - x|, D = |f16(x) restricted to f16 subnormals| and, per
 //     router row, a = |f16(w)|, b = |w|, c = |f16(w) - w|, d = |f16(w) restricted to f16 subnormals| (2-norms, which
-//     bound the sums of |x_i w_i| by Cauchy-Schwarz), g = (H + 64) 2^-23 (every addition inside and between the
-//     matrix-core steps and the K slices off by at most 2 units of fp32 rounding, in any order; f16 products are exact
-//     in fp32) and c = 48 2^-24 (the fixed order's additions: at most 32 chain steps, a 6-level tree and 3 more adds).
+//     bound the sums of |x_i w_i| by Cauchy-Schwarz), g = (H / ks + ks + 64) 2^-23 (M is the sum from zero, in slice
+//     order, of ks slices of H / ks exact f16 products each, every slice summed by the matrix core in some order:
+//     any summation tree over n terms is at most n - 1 additions deep, so each product meets at most
+//     H / ks + ks - 2 additions on its way to M, each off by at most 2 units of fp32 rounding; 64 more for the
+//     second-order terms) and c = 48 2^-24 (the fixed order's additions: at most 32 chain steps, a 6-level tree and
+//     3 more adds).
 //     The D and d terms cover a matrix core that flushes f16 subnormal inputs; C and c the f16 rounding of bf16 / f32
 //     inputs. e_j is taken 1 % larger, plus two fp32 units of |M_j|, so that its own rounding cannot shrink it;
 //   * tau = the k-th largest of M_j - e_j; every expert with M_j + e_j >= tau is a candidate. Any expert outside that
@@ -176,7 +179,7 @@ __global__ void __launch_bounds__(rf::NT) k_router_refine(RefineArgs a) {
   // 3. the bound, tau, the candidates, and among them the ones to recompute: those whose interval [M - e, M + e] meets
   // another candidate's (two disjoint intervals order their experts as the exact logits would)
   const float A = nrm[0], B = nrm[1], C = nrm[2], D = nrm[3];
-  const float g = float(H + 64) * 1.1920928955078125e-07f, cg = 48.0f * 5.9604644775390625e-08f;
+  const float g = float(H / KS + KS + 64) * 1.1920928955078125e-07f, cg = 48.0f * 5.9604644775390625e-08f;
   const float s1 = g * A + C + D, s2 = cg * B;
   float lo[NPL], hi[NPL];
 #pragma unroll

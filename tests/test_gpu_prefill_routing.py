@@ -142,7 +142,8 @@ def test_prefill_routing_planted_near_ties(kind):
 
 def test_router_gemm_within_the_bound():
     """The bound's premise, measured: the MFMA router GEMM's logits against the exact dot of the f16 operands, in
-    units of the bound's term g * sum |x_i w_i| (g = (H + 64) 2^-23); the worst token x expert must stay far below 1.
+    units of the bound's term g * sum |x_i w_i| (g = (H / ks + ks + 64) 2^-23 for ks K slices of the GEMM; here
+    ks = 8, 7x tighter than a bound over all H terms in one order); the worst token x expert must stay far below 1.
     Rows with heavy cancellation (x and w of alternating signs) are included."""
     from larder_amd import _lib, grouped
     cfg = dict(H=4096, E=128, k=8, I=512, norm=True, Is=0, types=("Q4_K",) * 3)
@@ -166,7 +167,9 @@ def test_router_gemm_within_the_bound():
     wd = host(L.wr).astype(np.float64)
     exact = xd @ wd.T
     absdot = np.abs(xd) @ np.abs(wd).T
-    gfac = (cfg["H"] + 64) * 2.0 ** -23
+    ks = _lib.lib().lmoe_router_gemm_ksplit(T, cfg["H"], cfg["E"])
+    assert ks == 8
+    gfac = (cfg["H"] // ks + ks + 64) * 2.0 ** -23
     ratio = np.abs(host(lg).astype(np.float64) - exact) / (gfac * absdot)
     print(f"router GEMM error / bound term: max {ratio.max():.3g}, mean {ratio.mean():.3g}", flush=True)
     assert ratio.max() < 0.25
