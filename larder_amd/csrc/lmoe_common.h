@@ -404,6 +404,7 @@ __device__ __forceinline__ uint32_t rank_pick_wave(const float *v, int E, int wa
   const int need = want + 1;
   uint32_t thr = 0;
   bool exact = false;
+#pragma unroll  // straight-line code: each candidate an immediate, the prefix in a scalar register
   for (int b = 31; b >= 0; --b) {
     const uint32_t cand = thr | (1u << b);
     int cnt = 0;
