@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--grouped-only", action="store_true",
                     help="run only the grouped-path lines (cfg3 prefill, cfg4, cfg5) and print them: a short run to "
                          "profile the grouped GEMMs with rocprofv3 counters, not a benchmark line")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only the cfg2 decode stack's per-workgroup phase timeline (the kernels' stamping forms, "
+                         "replayed as one HIP graph a step), one JSON object: a measurement, not a benchmark line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (the scale for rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE counters)")
@@ -110,6 +113,60 @@ def gpu_leg(args):
     dom = max(timing, key=lambda n: timing[n]["us"])
     token_bytes = args.layers * (workloads.decode_bytes(cfg, k) + 2 * H * 2)
     return dict(secs=secs, step_ms=step_ms, timing=timing, dom=dom, token_bytes=token_bytes, cfg=cfg, layers=layers)
+
+
+def timeline_leg(args):
+    """The cfg2 48-layer decode stack captured with the decode kernels' stamping forms (larder_amd.timeline), replayed
+    back to back as in the headline line; after each batch of 16 replays the last replay's stamps are read. Per kernel
+    and phase: the first, median and last workgroup's stamp in µs from the layer's first router workgroup start
+    (medians over layers and batches), and the layer period (one router start to the next)."""
+    import numpy as np
+    import torch
+
+    from larder_amd import layer as lay, timeline, workloads
+
+    cfg = workloads.CONFIGS[2]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    layers = [workloads.make_layer(cfg, g) for _ in range(args.layers)]
+    xs = torch.randn((64, 1, cfg["H"]), generator=g, device="cuda").half()
+    st = lay.DecodeStack(layers, 1)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        st.step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with timeline.Timeline(args.layers * 4096) as tl:
+        with torch.cuda.graph(graph):
+            st.step()
+    if len(tl.launches) != 3 * args.layers:
+        raise RuntimeError(f"{len(tl.launches)} stamped launches, expected {3 * args.layers}")
+    khz = timeline.clock_khz()
+    for i in range(64):
+        st.x_in.copy_(xs[i % 64])
+        graph.replay()
+    torch.cuda.synchronize()
+    per = {name: {p: [] for p in timeline.PHASES} for name in timeline.KERNELS.values()}
+    periods = []
+    for b in range(16):
+        for i in range(16):
+            st.x_in.copy_(xs[(16 * b + i) % 64])
+            graph.replay()
+        torch.cuda.synchronize()
+        stamps = tl.buf.cpu().numpy()
+        res = timeline.layer_phases(stamps, tl.launches, khz)
+        for name in per:
+            for p in per[name]:
+                per[name][p] += res[name][p]
+        starts = [stamps[r0:r0 + n, 0].min() for name, r0, n in tl.launches if name == "router"]
+        periods += list(np.diff(starts) * 1e3 / khz)
+    out = timeline.summary(per)
+    out["layer_period_us"] = round(float(np.median(periods)), 2)
+    out["clock_khz"] = khz
+    out["note"] = (f"cfg2, {args.layers} layers, one HIP graph a step; 16 batches of 16 back-to-back replays, the "
+                   "last replay of each read; µs from the layer's first router workgroup start; each workgroup "
+                   "stamps from its first thread (wavefront 0)")
+    return out
 
 
 def entry_leg(g):
@@ -773,6 +830,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.timeline:
+        log("[bench] cfg2 decode timeline: start")
+        print(json.dumps({"timeline": timeline_leg(args)}), flush=True)
+        return
     if args.grouped_only:
         log("[bench] grouped lines only: start")
         print(json.dumps({"secondary": grouped_leg()}), flush=True)

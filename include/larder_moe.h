@@ -44,6 +44,22 @@ int lmoe_abi_version(void);
 int lmoe_profile_arm(int max_launches);
 int lmoe_profile_read(float *ms, int cap, int *count);
 
+/* Per-workgroup phase timeline of the decode kernels, for benchmarks (no counterpart in the reference). After
+ * lmoe_timeline_arm(buf, rows) (buf: device memory, rows x 8 uint64, zeroed by the caller), the router GEMV
+ * (lmoe_router_gemv), the fused gate/up (lmoe_moe_gate_up*) and the two-wavefront down (lmoe_gemv_down_combine_prepped)
+ * that this thread launches, also into a graph under capture, run their stamping forms (the same results bit for
+ * bit): each workgroup writes the device wall clock (lmoe_timeline_clock_khz ticks a millisecond) into its row at
+ * each phase it reaches: 0 start, 1 inputs in (gate/up: its logits row; down: the token's ids), 2 top-k done
+ * (gate/up), 3 weights in, 4 end; a phase not reached stays as the caller left it. Each launch takes the next rows in
+ * launch order (grid x fastest, then y); a launch that does not fit runs unstamped and is not listed.
+ * lmoe_timeline_disarm writes the number of listed launches into *count and stops stamping new launches (a captured
+ * graph keeps stamping on every replay); lmoe_timeline_launch(i) gives listed launch i's kernel (1 router, 2 gate/up,
+ * 3 down), its first row and its workgroup count. */
+int lmoe_timeline_arm(unsigned long long *buf, long long rows);
+int lmoe_timeline_disarm(int *count);
+int lmoe_timeline_launch(int i, int *kernel, long long *row0, int *n_wg);
+int lmoe_timeline_clock_khz(int *khz);
+
 /* Router top-k over given logits. Replaces route_cuda.probs (route_cuda.py:280-288; kernel moe_probs
  * route_cuda.py:193-254) and the block's softmax/argpartition/take/renorm ops (stream_fast.py:4352-4370).
  * logits [T][E] in ldtype -> ids [T][k] best first (ties: lowest expert index), scores [T][k] fp32 softmax

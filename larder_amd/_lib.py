@@ -34,6 +34,10 @@ SIGNATURES = {
     "lmoe_abi_version": (_I, []),
     "lmoe_profile_arm": (_I, [_I]),
     "lmoe_profile_read": (_I, [_P, _I, _P]),
+    "lmoe_timeline_arm": (_I, [_P, _LL]),
+    "lmoe_timeline_disarm": (_I, [_P]),
+    "lmoe_timeline_launch": (_I, [_I, _P, _P, _P]),
+    "lmoe_timeline_clock_khz": (_I, [_P]),
     "lmoe_router_topk": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "lmoe_router_topk_shared": (_I, [_P, _I, _I, _I, _I, _P, _I, _P, _P, _P]),
     "lmoe_prep_x": (_I, [_P, _I, _I, _I, _I, _P, _P]),

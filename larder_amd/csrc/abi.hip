@@ -50,9 +50,67 @@ bool profile_next(hipEvent_t *a, hipEvent_t *b) {
   return true;
 }
 
+struct TimelineLaunch {
+  int kernel, n_wg;
+  long long row0;
+};
+struct Timeline {
+  unsigned long long *buf = nullptr;
+  long long rows = 0, used = 0;
+  std::vector<TimelineLaunch> launches;
+};
+static thread_local Timeline g_tl;
+constexpr int kTimelineMaxLaunches = 1 << 14;
+
+unsigned long long *timeline_next(int kernel, int n_wg) {
+  Timeline &t = g_tl;
+  if (!t.buf || t.used + n_wg > t.rows || int(t.launches.size()) >= kTimelineMaxLaunches) return nullptr;
+  unsigned long long *p = t.buf + size_t(t.used) * 8;
+  t.launches.push_back({kernel, n_wg, t.used});
+  t.used += n_wg;
+  return p;
+}
+
 }  // namespace lmoe
 
 extern "C" const char *lmoe_error(void) { return lmoe::g_error.c_str(); }
+
+extern "C" int lmoe_timeline_arm(unsigned long long *buf, long long rows) {
+  using namespace lmoe;
+  LMOE_REQUIRE(buf && rows > 0, LMOE_EINVAL, "lmoe_timeline_arm: null buffer or no rows");
+  LMOE_REQUIRE(aligned16(buf), LMOE_EALIGN, "lmoe_timeline_arm: buffer must be 16-byte aligned");
+  g_tl.buf = buf;
+  g_tl.rows = rows;
+  g_tl.used = 0;
+  g_tl.launches.clear();
+  return 0;
+}
+
+extern "C" int lmoe_timeline_disarm(int *count) {
+  using namespace lmoe;
+  if (count) *count = int(g_tl.launches.size());
+  g_tl.buf = nullptr;
+  return 0;
+}
+
+extern "C" int lmoe_timeline_launch(int i, int *kernel, long long *row0, int *n_wg) {
+  using namespace lmoe;
+  LMOE_REQUIRE(i >= 0 && i < int(g_tl.launches.size()), LMOE_EINVAL, "lmoe_timeline_launch: no launch %d", i);
+  const TimelineLaunch &l = g_tl.launches[i];
+  if (kernel) *kernel = l.kernel;
+  if (row0) *row0 = l.row0;
+  if (n_wg) *n_wg = l.n_wg;
+  return 0;
+}
+
+extern "C" int lmoe_timeline_clock_khz(int *khz) {
+  using namespace lmoe;
+  LMOE_REQUIRE(khz, LMOE_EINVAL, "lmoe_timeline_clock_khz: null pointer");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, dev);
+  return e == hipSuccess ? 0 : hip_fail(e, "lmoe_timeline_clock_khz");
+}
 
 extern "C" int lmoe_profile_arm(int max_launches) {
   using namespace lmoe;

@@ -282,16 +282,19 @@ __global__ void __launch_bounds__(64 * NW, 3)
 //
 // RAW (slots given, NPL = 0): x comes raw (dtype xdt) and each workgroup prepares its row in LDS with prep_dword,
 // the bits lmoe_prep_x writes, so the launch before it is saved: the drop-in chain's form.
-template <int TQ, int P, int RB, int NPL, bool RANKWG, bool RAW = false>
+template <int TQ, int P, int RB, int NPL, bool RANKWG, bool RAW = false, bool TL = false>
 __global__ void __launch_bounds__(256)
     k_gate_up_xr(const uint32_t *xprep, const uint32_t *slots, int topk, const uint8_t *wg, const uint8_t *wu,
                  int n_experts, int I, float *h, uint32_t *hprep, int td, const float *logits, int ld_stride,
-                 int norm, uint32_t *ids_out, float *scores_out, int ks, const void *x, int xdt) {
+                 int norm, uint32_t *ids_out, float *scores_out, int ks, const void *x, int xdt,
+                 unsigned long long *tl) {
   constexpr int NW = 4, G = 64 / P, RG = RB / G;
   static_assert(P == 32 || P == 64, "32 or 64 units a row");
   static_assert(RB % G == 0, "rows split evenly over the lane groups");
   static_assert(!RAW || NPL == 0, "raw x: slots given");
   static_assert(!RAW || NW * 2 * RB * 9 * P >= 64 * P, "the stages hold the raw row (f32 at most)");
+  static_assert(!TL || (!RAW && !RANKWG), "stamps in the per-wavefront pick form only");
+  tl_stamp<TL>(tl, 0);
   constexpr int C = RB * 9 * P / 4;  // 16-byte chunks of RB rows of one matrix
   constexpr int NC2 = (2 * C + 63) / 64;  // of both matrices' rows, a lane
   constexpr int STAGE = 2 * RB * 9 * P;  // dwords a wavefront
@@ -345,6 +348,13 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int i = 0; i < XPT; ++i) xc[i] = xg4[min(int(threadIdx.x) + NT * i, XC - 1)];
   }
+  if constexpr (TL) {  // the logits row (slots given: the slot's id) in
+    if constexpr (NPL > 0)
+      asm volatile("" ::"v"(v[0]), "v"(v[NPL > 0 ? NPL - 1 : 0]));
+    else
+      asm volatile("" ::"v"(e));
+    tl_stamp<TL>(tl, 1);
+  }
   if (NPL > 0 && shared_slot) {  // a slice of the folded shared expert: no pick; its id and sigmoid-gated weight
     e = uint32_t(n_experts + jslot - topk);
     if (blockIdx.x == 0 && wave == 0 && lane == 0) {
@@ -378,6 +388,10 @@ __global__ void __launch_bounds__(256)
       id = rank_pick_wave<N>(v, n_experts, j);
     }
     e = id;
+  }
+  if constexpr (TL) {
+    asm volatile("" ::"v"(e));
+    tl_stamp<TL>(tl, 2);
   }
   // no such expert: zero rows (cpu_kern.cpp:316-318); the folded shared expert is expert n_experts
   const bool valid = e < uint32_t(n_experts) || shared_slot;
@@ -432,6 +446,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int i = 0; i < NC2; ++i) st4[min(lane + 64 * i, 2 * C - 1)] = vw[i];
   __builtin_amdgcn_wave_barrier();
+  tl_stamp<TL>(tl, 3);
   if (r0 >= I) return;
   if (!valid) {
     if (lane < RB) {
@@ -483,6 +498,7 @@ __global__ void __launch_bounds__(256)
       }
     }
   }
+  tl_stamp<TL>(tl, 4);
 }
 
 // ---- down + combine -------------------------------------------------------------------------------------------
@@ -627,12 +643,13 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // wavefront finish on DPP / permlane swaps, then the gated shared-expert row and the residual are added. Memory order:
 // h units, ids and scores (one a lane), then the weights, whose addresses need only the ids; no load is predicated
 // (clamped indices; expert 0 stands in for an id past the experts, with a zero weight).
-template <int TD, int NU, int NCW, int KS = 1, int HL = 0>
+template <int TD, int NU, int NCW, int KS = 1, int HL = 0, bool TL = false>
 __global__ void __launch_bounds__(256)
     k_down_xr(const uint32_t *hprep, const uint32_t *ids, const float *scores, int k, const uint8_t *wd,
               int n_experts, int I, int H, const float *shared, const float *gate, int gate_stride,
-              const void *residual, int rdt, void *out, int odt) {
+              const void *residual, int rdt, void *out, int odt, unsigned long long *tl) {
   constexpr int RB = 2;
+  tl_stamp<TL>(tl, 0);
   static_assert(KS == 1 || KS == 2, "experts split over 1 or 2 wavefronts");
   // KS = 2: wavefronts 2 g and 2 g + 1 share rows [(2 bx + g) RB, +RB), wavefront 2 g + q over experts
   // [q kh, q kh + kh) (kh = ceil(k / 2); k >= 2, so both shares hold experts), and the second share's row sums are
@@ -677,6 +694,10 @@ __global__ void __launch_bounds__(256)
     }
   }
   asm volatile("" ::: "memory");
+  if constexpr (TL) {
+    asm volatile("" ::"v"(my_id));
+    tl_stamp<TL>(tl, 1);
+  }
   // 2. the weights: chunk c of expert j0 + j's block at rows [n0, n0 + RB)
   const size_t rowb = size_t(36) * P, nsafe = size_t(min(n0, H - RB));
   u32x4 w[NCW];
@@ -741,6 +762,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int i = 0; i < NCW; ++i) st4[min(lane + 64 * i, CW - 1)] = w[i];
   __builtin_amdgcn_wave_barrier();
+  tl_stamp<TL>(tl, 3);
   if (KS == 1 && n0 >= H) return;  // (KS == 2: the host launches exactly H / 4 workgroups, every row in range)
   // 5. dots
   float acc[RB];
@@ -771,6 +793,7 @@ __global__ void __launch_bounds__(256)
     if (residual) v += load_elt(residual, o, rdt);
     store_elt(out, o, v, odt);
   }
+  tl_stamp<TL>(tl, 4);
 }
 
 // ---- host dispatch ----------------------------------------------------------------------------------------------
@@ -1367,10 +1390,13 @@ static bool gate_up_rank_wg() {
 template <int TQ, int P, int RB, int NPL>
 static int launch_gate_up_xr(const GateUpArgs &a, hipStream_t st) {
   const dim3 grid((a.I + 4 * RB - 1) / (4 * RB), a.n_slots);
-  auto kern = gate_up_rank_wg() ? k_gate_up_xr<TQ, P, RB, NPL, true> : k_gate_up_xr<TQ, P, RB, NPL, false>;
+  unsigned long long *tl = gate_up_rank_wg() ? nullptr : timeline_next(LMOE_TL_GATE_UP, int(grid.x * grid.y));
+  auto kern = tl                 ? k_gate_up_xr<TQ, P, RB, NPL, false, false, true>
+              : gate_up_rank_wg() ? k_gate_up_xr<TQ, P, RB, NPL, true>
+                                  : k_gate_up_xr<TQ, P, RB, NPL, false>;
   launch(kern, grid, dim3(256), 0, st, a.xg_prep, a.slots, a.topk, a.wg, a.wu,
          a.n_experts, a.I, a.h, a.hprep, a.td, a.logits, a.ld_stride, a.norm, a.ids_out, a.scores_out,
-         a.ks ? a.ks : a.topk, nullptr, 0);
+         a.ks ? a.ks : a.topk, nullptr, 0, tl);
   LMOE_LAUNCHED("lmoe_gemv_gate_up");
   return 0;
 }
@@ -1381,7 +1407,8 @@ static int launch_gate_up_xr_raw(const GateUpArgs &a, hipStream_t st) {
   constexpr int RB = 2;
   const dim3 grid((a.I + 4 * RB - 1) / (4 * RB), a.n_slots);
   launch(k_gate_up_xr<TQ, P, RB, 0, false, true>, grid, dim3(256), 0, st, nullptr, a.slots, a.topk, a.wg, a.wu,
-         a.n_experts, a.I, a.h, a.hprep, a.td, nullptr, 0, 0, nullptr, nullptr, a.topk, a.x, a.xdt);
+         a.n_experts, a.I, a.h, a.hprep, a.td, nullptr, 0, 0, nullptr, nullptr, a.topk, a.x, a.xdt,
+         static_cast<unsigned long long *>(nullptr));
   LMOE_LAUNCHED("lmoe_gemv_chain_gate_up");
   return 0;
 }
@@ -1521,13 +1548,14 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
       // the h chunks as one run through LDS where that saves loads: 6 a lane at 48 units (cfg2, cfg5), 11 at 88
       // (cfg1), against 8 NU
       const int HLr = getenv("LMOE_DOWN_HL") && atoi(getenv("LMOE_DOWN_HL")) == 0 ? 0 : hl;
+      unsigned long long *tl = timeline_next(LMOE_TL_DOWN, (a.H / 4) * a.T);
       auto go = [&](auto td, auto nu, auto nc) {
         constexpr int TD = decltype(td)::value, N = decltype(nu)::value, C = decltype(nc)::value;
         auto run = [&](auto hlc) {
           constexpr int HLc = decltype(hlc)::value;
-          launch(k_down_xr<TD, N, C, 2, HLc>, dim3(a.H / 4, a.T), dim3(256),
-                 size_t(4) * 16 * (CWh + 64 * HLc), st, a.hprep, a.ids, a.scores, a.k, a.wd, a.n_experts, a.I, a.H,
-                 a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt);
+          launch(tl ? k_down_xr<TD, N, C, 2, HLc, true> : k_down_xr<TD, N, C, 2, HLc>, dim3(a.H / 4, a.T),
+                 dim3(256), size_t(4) * 16 * (CWh + 64 * HLc), st, a.hprep, a.ids, a.scores, a.k, a.wd, a.n_experts,
+                 a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt, tl);
         };
         if (N == 1 && HLr == 6)
           run(std::integral_constant<int, 6>());
@@ -1565,7 +1593,7 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
         constexpr int TD = decltype(td)::value, N = decltype(nu)::value, C = decltype(nc)::value;
         launch(k_down_xr<TD, N, C>, dim3(a.H / 8, a.T), dim3(256), size_t(4) * 4 * CW * 4, st, a.hprep, a.ids,
                a.scores, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out,
-               a.odt);
+               a.odt, static_cast<unsigned long long *>(nullptr));
       };
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;

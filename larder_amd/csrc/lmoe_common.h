@@ -81,6 +81,22 @@ inline int allow_lds(K kernel, size_t bytes, const char *what) {
 // brackets each kernel with a start / stop event pair recorded by the launch itself.
 bool profile_next(hipEvent_t *start, hipEvent_t *stop);
 
+// Per-workgroup phase stamps of the decode kernels (lmoe_timeline_arm): while armed, the router GEMV, the fused
+// gate/up and the two-wavefront down launch their stamping forms, each workgroup writing the device's constant-rate
+// wall clock into its row of 8 at each phase it reaches (0 start, 1 inputs in: logits or ids, 2 top-k done, 3 weights
+// in, 4 end); a phase a workgroup does not reach stays 0. timeline_next gives a launch of n_wg workgroups its rows
+// (nullptr when disarmed or full).
+enum { LMOE_TL_ROUTER = 1, LMOE_TL_GATE_UP = 2, LMOE_TL_DOWN = 3 };
+unsigned long long *timeline_next(int kernel, int n_wg);
+
+template <bool TL>
+__device__ __forceinline__ void tl_stamp(unsigned long long *tl, int phase) {
+  if constexpr (TL) {
+    if (threadIdx.x == 0)
+      tl[(size_t(blockIdx.y) * gridDim.x + blockIdx.x) * 8 + phase] = (unsigned long long)wall_clock64();
+  }
+}
+
 template <typename K, typename... Args>
 inline void launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
   hipEvent_t a, b;

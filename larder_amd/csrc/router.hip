@@ -77,10 +77,10 @@ constexpr int kRouterMaxNi = 4;  // 8-weight items a thread: H <= 8192
 // straight from memory (no staging); a wavefront sum and a fixed-order sum of the four wavefronts' partials give
 // the logit. Workgroups past the rows write the prepared activation units for block type TQ (when xprep is given),
 // four units a workgroup, one a wavefront through its own LDS. WDT: the weights' element type.
-template <int WDT, int TQ, int NI>
+template <int WDT, int TQ, int NI, bool TL = false>
 __global__ void __launch_bounds__(256)
     k_router_gemv(const void *x, int xdt, const void *wr, const void *wsg, int T, int H, int E, float *logits,
-                  uint32_t *xprep) {
+                  uint32_t *xprep, unsigned long long *tl) {
   constexpr int WQ = WDT == LMOE_F32 ? 2 : 1;  // 16-byte chunks an item of weights
   __shared__ float part[4][kRouterMaxT];
   __shared__ float xu[4][64];
@@ -88,6 +88,7 @@ __global__ void __launch_bounds__(256)
   const int rows = E + (wsg != nullptr ? 1 : 0);
   const int row = blockIdx.x;
   const int nit = H / 8;
+  tl_stamp<TL>(tl, 0);
   if (row >= rows) {  // a prepared-activation workgroup: one unit a wavefront, wavefront-private LDS
     const int P = H / 64;
     const int u = (row - rows) * 4 + wave;
@@ -96,6 +97,7 @@ __global__ void __launch_bounds__(256)
     xu[wave][lane] = load_elt(x, size_t(t) * H + 64 * p + lane, xdt);
     __builtin_amdgcn_wave_barrier();
     if (lane < XS) xprep[size_t(u) * XS + lane] = prep_dword<TQ>([&](int i) { return xu[wave][i]; }, 0, lane);
+    tl_stamp<TL>(tl, 4);
     return;
   }
   const u32x4 *w4 = reinterpret_cast<const u32x4 *>(
@@ -111,6 +113,10 @@ __global__ void __launch_bounds__(256)
   float wv[NI][8];
 #pragma unroll
   for (int i = 0; i < NI; ++i) unpack8(wq[i][0], wq[i][WQ - 1], WDT, wv[i]);
+  if constexpr (TL) {
+    asm volatile("" ::"v"(wv[0][0]), "v"(wv[NI - 1][7]));
+    tl_stamp<TL>(tl, 3);
+  }
   const int xq = xdt == LMOE_F32 ? 2 : 1;  // 16-byte chunks an item of x
   for (int t = 0; t < T; ++t) {
     const u32x4 *x4 = reinterpret_cast<const u32x4 *>(static_cast<const char *>(x) +
@@ -138,6 +144,7 @@ __global__ void __launch_bounds__(256)
   if (threadIdx.x < T)
     logits[size_t(threadIdx.x) * rows + row] =
         ((part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x]) + part[3][threadIdx.x];
+  tl_stamp<TL>(tl, 4);
 }
 
 // Prepared activation rows on their own: one workgroup a row, one thread a unit dword.
@@ -155,12 +162,20 @@ template <int WDT, int TQ>
 static void launch_router_q(dim3 grid, dim3 block, hipStream_t st, const void *x, int xdt, const void *wr,
                             const void *wsg, int T, int H, int E, float *logits, uint32_t *xprep) {
   const int ni = (H / 8 + 255) / 256;
+  unsigned long long *tl = timeline_next(LMOE_TL_ROUTER, int(grid.x * grid.y));
+  auto go = [&](auto nic) {
+    constexpr int NI = decltype(nic)::value;
+    if (tl)
+      launch(k_router_gemv<WDT, TQ, NI, true>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep, tl);
+    else
+      launch(k_router_gemv<WDT, TQ, NI>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep, tl);
+  };
   if (ni <= 1)
-    launch(k_router_gemv<WDT, TQ, 1>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+    go(std::integral_constant<int, 1>());
   else if (ni <= 2)
-    launch(k_router_gemv<WDT, TQ, 2>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+    go(std::integral_constant<int, 2>());
   else
-    launch(k_router_gemv<WDT, TQ, 4>, grid, block, 0, st, x, xdt, wr, wsg, T, H, E, logits, xprep);
+    go(std::integral_constant<int, 4>());
 }
 
 template <int WDT>
