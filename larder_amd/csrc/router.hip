@@ -110,6 +110,21 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int q = 0; q < WQ; ++q) wq[i][q] = __builtin_nontemporal_load(w4 + it * WQ + q);
   }
+  // token t's x items (the first token's go out with the weights, before anything waits on them)
+  const int xq = xdt == LMOE_F32 ? 2 : 1;  // 16-byte chunks an item of x
+  u32x4 xc[NI][2];
+  auto load_x = [&](int t) {
+    const u32x4 *x4 = reinterpret_cast<const u32x4 *>(static_cast<const char *>(x) +
+                                                      size_t(t) * H * (xdt == LMOE_F32 ? 4 : 2));
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int it = min(int(threadIdx.x) + 256 * i, nit - 1);
+      xc[i][0] = x4[it * xq];
+      xc[i][1] = x4[it * xq + xq - 1];
+    }
+  };
+  load_x(0);
+  asm volatile("" ::: "memory");  // keeps them here, not sunk into the dot loop's per-lane branch behind the weights
   float wv[NI][8];
 #pragma unroll
   for (int i = 0; i < NI; ++i) unpack8(wq[i][0], wq[i][WQ - 1], WDT, wv[i]);
@@ -117,17 +132,8 @@ __global__ void __launch_bounds__(256)
     asm volatile("" ::"v"(wv[0][0]), "v"(wv[NI - 1][7]));
     tl_stamp<TL>(tl, 3);
   }
-  const int xq = xdt == LMOE_F32 ? 2 : 1;  // 16-byte chunks an item of x
   for (int t = 0; t < T; ++t) {
-    const u32x4 *x4 = reinterpret_cast<const u32x4 *>(static_cast<const char *>(x) +
-                                                      size_t(t) * H * (xdt == LMOE_F32 ? 4 : 2));
-    u32x4 xc[NI][2];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int it = min(int(threadIdx.x) + 256 * i, nit - 1);
-      xc[i][0] = x4[it * xq];
-      xc[i][1] = x4[it * xq + xq - 1];
-    }
+    if (t > 0) load_x(t);
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
