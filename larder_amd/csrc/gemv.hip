@@ -442,6 +442,20 @@ __global__ void __launch_bounds__(256)
     for (int i = 0; i < XPT; ++i) xl[min(int(threadIdx.x) + NT * i, XC - 1)] = xc[i];
   }
   __syncthreads();
+  // this lane's activation unit out of LDS while the weights are still on their way, then the weights into the stage
+  uint32_t xv[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const u32x4 q = xl[9 * p + i];
+    xv[4 * i] = q.x;
+    xv[4 * i + 1] = q.y;
+    xv[4 * i + 2] = q.z;
+    xv[4 * i + 3] = q.w;
+  }
+  // the two half-unit sums; __uint_as_float, not __builtin_bit_cast: this compiler lowers a bit cast of an
+  // ext_vector element lvalue (qs.y) to element 0
+  const u32x4 qs = xl[9 * p + 8];
+  const float sx0 = __uint_as_float(qs.x), sx1 = __uint_as_float(qs.y);
   u32x4 *st4 = reinterpret_cast<u32x4 *>(stage);
 #pragma unroll
   for (int i = 0; i < NC2; ++i) st4[min(lane + 64 * i, 2 * C - 1)] = vw[i];
@@ -460,19 +474,6 @@ __global__ void __launch_bounds__(256)
     }
     return;
   }
-  uint32_t xv[32];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const u32x4 q = xl[9 * p + i];
-    xv[4 * i] = q.x;
-    xv[4 * i + 1] = q.y;
-    xv[4 * i + 2] = q.z;
-    xv[4 * i + 3] = q.w;
-  }
-  // the two half-unit sums; __uint_as_float, not __builtin_bit_cast: this compiler lowers a bit cast of an
-  // ext_vector element lvalue (qs.y) to element 0
-  const u32x4 qs = xl[9 * p + 8];
-  const float sx0 = __uint_as_float(qs.x), sx1 = __uint_as_float(qs.y);
   float pg[RG], pu[RG];
 #pragma unroll
   for (int i = 0; i < RG; ++i) {
