@@ -342,6 +342,9 @@ __global__ void __launch_bounds__(256)
   } else {
     e = slots[s];
   }
+  // the logits (or the slot id) go out before the activation row: the count of outstanding loads is in order, so
+  // the top-k then waits for the logits alone, not for the row behind them
+  asm volatile("" ::: "memory");
   const u32x4 *xg4 = reinterpret_cast<const u32x4 *>(xprep + xrow * P * XS);
   u32x4 xc[RAW ? 1 : XPT];
   if (!RAW) {
