@@ -668,8 +668,12 @@ __global__ void __launch_bounds__(256)
   const int n0 = (blockIdx.x * (4 / KS) + wave / KS) * RB;
   extern __shared__ u32x4 lds4[];
   uint32_t *stage = reinterpret_cast<uint32_t *>(lds4) + wave * (kh * CJ * 4);
-  // HL > 0: the wavefront's h chunks through LDS, after the four stages: 64 HL chunks a wavefront
-  u32x4 *hst = lds4 + 4 * kh * CJ + wave * 64 * HL;
+  // HL > 0: the wavefront's h chunks through LDS, after the four stages: 64 HL chunks a wavefront. KS = 2: the two
+  // wavefronts over the same experts (one a row pair) share one copy, each loading every other 64-chunk block of it
+  constexpr bool SH = KS == 2 && HL > 0;
+  constexpr int HLS = SH ? (HL + 1) / 2 : HL;  // h loads a lane
+  const int hblk = SH ? wave / 2 : 0;           // this wavefront's blocks: 2 i + hblk (SH), else i
+  u32x4 *hst = lds4 + 4 * kh * CJ + (SH ? q : wave) * 64 * HL;
 
   // 1. the token's ids and scores (lane j < k holds expert j's), then the h units. The empty asm with a memory
   // clobber keeps the compiler from sinking these loads below the weights' (the count of outstanding loads is in
@@ -682,11 +686,11 @@ __global__ void __launch_bounds__(256)
   const float my_sc = scores ? sc_ld : 1.0f;
   const u32x4 *hb = reinterpret_cast<const u32x4 *>(hprep + (size_t(t) * k + j0) * P * XS);
   u32x4 hq[NU][8];
-  u32x4 hl[HL > 0 ? HL : 1];
+  u32x4 hl[HL > 0 ? HLS : 1];
   if constexpr (HL > 0) {
 #pragma unroll
-    for (int i = 0; i < HL; ++i) {
-      const int qc = min(lane + 64 * i, 8 * U - 1);
+    for (int i = 0; i < HLS; ++i) {
+      const int qc = min(lane + 64 * (SH ? 2 * i + hblk : i), 8 * U - 1);
       hl[i] = hb[(qc >> 3) * 9 + (qc & 7)];
     }
   } else {
@@ -737,11 +741,14 @@ __global__ void __launch_bounds__(256)
   // unit's expert, weight (0 past the units or the experts) and half-unit sums
   if constexpr (HL > 0) {
 #pragma unroll
-    for (int i = 0; i < HL; ++i) {
-      const int qc = min(lane + 64 * i, 8 * U - 1), u = qc >> 3;  // a lane past the end rewrites the last chunk
+    for (int i = 0; i < HLS; ++i) {  // a lane past the end rewrites the last chunk (the same value)
+      const int qc = min(lane + 64 * (SH ? 2 * i + hblk : i), 8 * U - 1), u = qc >> 3;
       hst[8 * u + ((qc & 7) ^ ((u >> 1) & 7))] = hl[i];
     }
-    __builtin_amdgcn_wave_barrier();
+    if constexpr (SH)
+      __syncthreads();
+    else
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int a = 0; a < NU; ++a) {
       const int u = min(lane + 64 * a, U - 1);
