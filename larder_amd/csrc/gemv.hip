@@ -647,14 +647,15 @@ __global__ void __launch_bounds__(64 * NW, 3)
 // wavefront finish on DPP / permlane swaps, then the gated shared-expert row and the residual are added. Memory order:
 // h units, ids and scores (one a lane), then the weights, whose addresses need only the ids; no load is predicated
 // (clamped indices; expert 0 stands in for an id past the experts, with a zero weight).
-template <int TD, int NU, int NCW, int KS = 1, int HL = 0, bool TL = false>
-__global__ void __launch_bounds__(256)
+template <int TD, int NU, int NCW, int KS = 1, int HL = 0, bool TL = false, int NWG = 4>
+__global__ void __launch_bounds__(64 * NWG)
     k_down_xr(const uint32_t *hprep, const uint32_t *ids, const float *scores, int k, const uint8_t *wd,
               int n_experts, int I, int H, const float *shared, const float *gate, int gate_stride,
               const void *residual, int rdt, void *out, int odt, unsigned long long *tl) {
   constexpr int RB = 2;
   tl_stamp<TL>(tl, 0);
   static_assert(KS == 1 || KS == 2, "experts split over 1 or 2 wavefronts");
+  static_assert(NWG == 4 || (NWG == 8 && KS == 2), "4 wavefronts a workgroup, or 8 (4 row pairs) with KS = 2");
   // KS = 2: wavefronts 2 g and 2 g + 1 share rows [(2 bx + g) RB, +RB), wavefront 2 g + q over experts
   // [q kh, q kh + kh) (kh = ceil(k / 2); k >= 2, so both shares hold experts), and the second share's row sums are
   // added to the first's through LDS
@@ -665,15 +666,17 @@ __global__ void __launch_bounds__(256)
   const int P = I / 64, U = kj * P;
   const int CJ = RB * 9 * P / 4, CW = kj * CJ;  // 16-byte chunks of one expert's RB rows, of this wavefront's
   const int t = blockIdx.y;
-  const int n0 = (blockIdx.x * (4 / KS) + wave / KS) * RB;
+  const int n0 = (blockIdx.x * (NWG / KS) + wave / KS) * RB;
   extern __shared__ u32x4 lds4[];
   uint32_t *stage = reinterpret_cast<uint32_t *>(lds4) + wave * (kh * CJ * 4);
-  // HL > 0: the wavefront's h chunks through LDS, after the four stages: 64 HL chunks a wavefront. KS = 2: the two
-  // wavefronts over the same experts (one a row pair) share one copy, each loading every other 64-chunk block of it
+  // HL > 0: the wavefront's h chunks through LDS, after the NWG stages: 64 HL chunks a wavefront. KS = 2: the NWG / 2
+  // wavefronts over the same experts (one a row pair each) share one copy, each loading every (NWG / 2)-th 64-chunk
+  // block of it
   constexpr bool SH = KS == 2 && HL > 0;
-  constexpr int HLS = SH ? (HL + 1) / 2 : HL;  // h loads a lane
-  const int hblk = SH ? wave / 2 : 0;           // this wavefront's blocks: 2 i + hblk (SH), else i
-  u32x4 *hst = lds4 + 4 * kh * CJ + (SH ? q : wave) * 64 * HL;
+  constexpr int HW = SH ? NWG / 2 : 1;         // wavefronts sharing one copy
+  constexpr int HLS = (HL + HW - 1) / HW;      // h loads a lane
+  const int hblk = SH ? wave / 2 : 0;          // this wavefront's blocks: HW i + hblk
+  u32x4 *hst = lds4 + NWG * kh * CJ + (SH ? q : wave) * 64 * HL;
 
   // 1. the token's ids and scores (lane j < k holds expert j's), then the h units. The empty asm with a memory
   // clobber keeps the compiler from sinking these loads below the weights' (the count of outstanding loads is in
@@ -690,7 +693,7 @@ __global__ void __launch_bounds__(256)
   if constexpr (HL > 0) {
 #pragma unroll
     for (int i = 0; i < HLS; ++i) {
-      const int qc = min(lane + 64 * (SH ? 2 * i + hblk : i), 8 * U - 1);
+      const int qc = min(lane + 64 * (HW * i + hblk), 8 * U - 1);
       hl[i] = hb[(qc >> 3) * 9 + (qc & 7)];
     }
   } else {
@@ -742,7 +745,7 @@ __global__ void __launch_bounds__(256)
   if constexpr (HL > 0) {
 #pragma unroll
     for (int i = 0; i < HLS; ++i) {  // a lane past the end rewrites the last chunk (the same value)
-      const int qc = min(lane + 64 * (SH ? 2 * i + hblk : i), 8 * U - 1), u = qc >> 3;
+      const int qc = min(lane + 64 * (HW * i + hblk), 8 * U - 1), u = qc >> 3;
       hst[8 * u + ((qc & 7) ^ ((u >> 1) & 7))] = hl[i];
     }
     if constexpr (SH)
@@ -806,7 +809,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int r = 0; r < RB; ++r) acc[r] = wave_sum(acc[r]);
   if (KS == 2) {
-    __shared__ float part[4 * RB];  // [wavefront][row]
+    __shared__ float part[NWG * RB];  // [wavefront][row]
     if (q == 1 && lane < RB) part[wave * RB + lane] = lane == 0 ? acc[0] : acc[1];
     __syncthreads();
     if (q == 1) return;
@@ -1582,14 +1585,24 @@ static int down(const char *fn, const DownArgs &a, void *stream) {
       // the h chunks as one run through LDS where that saves loads: 6 a lane at 48 units (cfg2, cfg5), 11 at 88
       // (cfg1), against 8 NU
       const int HLr = getenv("LMOE_DOWN_HL") && atoi(getenv("LMOE_DOWN_HL")) == 0 ? 0 : hl;
-      unsigned long long *tl = timeline_next(LMOE_TL_DOWN, (a.H / 4) * a.T);
+      // eight wavefronts a workgroup (four row pairs) where H allows: the four over the same experts share one copy
+      // of their h half, half the h reads of four (LMOE_DOWN_WG8=0 keeps four)
+      const bool wg8 = a.H % 8 == 0 && !(getenv("LMOE_DOWN_WG8") && atoi(getenv("LMOE_DOWN_WG8")) == 0);
+      const int nwg = wg8 ? 8 : 4;
+      unsigned long long *tl = timeline_next(LMOE_TL_DOWN, (a.H / nwg) * a.T);
       auto go = [&](auto td, auto nu, auto nc) {
         constexpr int TD = decltype(td)::value, N = decltype(nu)::value, C = decltype(nc)::value;
         auto run = [&](auto hlc) {
           constexpr int HLc = decltype(hlc)::value;
-          launch(tl ? k_down_xr<TD, N, C, 2, HLc, true> : k_down_xr<TD, N, C, 2, HLc>, dim3(a.H / 4, a.T),
-                 dim3(256), size_t(4) * 16 * (CWh + 64 * HLc), st, a.hprep, a.ids, a.scores, a.k, a.wd, a.n_experts,
-                 a.I, a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt, tl);
+          const size_t lds = size_t(16) * (size_t(nwg) * CWh + (HLc > 0 ? 2 : nwg) * 64 * HLc);
+          if (wg8)
+            launch(tl ? k_down_xr<TD, N, C, 2, HLc, true, 8> : k_down_xr<TD, N, C, 2, HLc, false, 8>,
+                   dim3(a.H / 8, a.T), dim3(512), lds, st, a.hprep, a.ids, a.scores, a.k, a.wd, a.n_experts, a.I,
+                   a.H, a.shared, a.gate, a.gate_stride, a.residual, a.rdt, a.out, a.odt, tl);
+          else
+            launch(tl ? k_down_xr<TD, N, C, 2, HLc, true> : k_down_xr<TD, N, C, 2, HLc>, dim3(a.H / 4, a.T),
+                   dim3(256), lds, st, a.hprep, a.ids, a.scores, a.k, a.wd, a.n_experts, a.I, a.H, a.shared, a.gate,
+                   a.gate_stride, a.residual, a.rdt, a.out, a.odt, tl);
         };
         if (N == 1 && HLr == 6)
           run(std::integral_constant<int, 6>());
