@@ -24,7 +24,7 @@ HBM_PEAK = 8.0e12  # MI355X published HBM3E bandwidth, bytes/s
 MFMA_PEAK = 2.5e15  # MI355X dense f16 / bf16 matrix peak, flop/s
 # HBM bytes a launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled by a 256 MiB copy) at the cfg2 shape,
 # per kernel; see profiles/decode_cfg2_traffic.md for the commands. Reported as roofline.traffic for that kernel.
-MEASURED_TRAFFIC = {"k_gate_up_xr": 14371200, "k_down_xr": 7593984, "k_router_gemv": 622080}
+MEASURED_TRAFFIC = {"k_gate_up_xr": 14350080, "k_down_xr": 7321600, "k_router_gemv": 622080}
 
 
 def parse():
