@@ -406,7 +406,8 @@ int lmoe_router_gemm_topk(const void *xh, int T, int H, const void *wk, int E, i
  * [T] (optional) the gate row's fixed-order logit; n_cand [T] (optional) the candidate counts. H % 8 == 0, H <= 8192,
  * E <= 1024, k <= 32, k + m <= 64, wr / wsg / norms 16-byte aligned. No counterpart in the reference.
  * lmoe_router_gemm_refine: lmoe_router_gemm (without its finish) then lmoe_router_refine on its slices; n_gate == 1
- * exactly when wsg is given. */
+ * exactly when wsg is given (the GEMM then leaves the gate row out, since the refine recomputes it, but splits K as
+ * for E + 1 rows; ws is sized by lmoe_router_gemm_workspace_bytes(T, H, E + n_gate) as before). ldp >= E. */
 int lmoe_router_norms(const void *wr, const void *wsg, int wdtype, int E, int H, float *norms, void *stream);
 int lmoe_router_refine(const float *part, int ksplit, int ldp, const void *x, int xdtype, int T, int H, const void *wr,
                        const void *wsg, int wdtype, int E, const float *norms, int k, int norm, int m, uint32_t *ids,

@@ -2163,9 +2163,11 @@ extern "C" size_t lmoe_router_gemm_workspace_bytes(int T, int H, int En) {
   return size_t(s) * size_t(T) * size_t((En + kRgN - 1) / kRgN * kRgN) * sizeof(float);
 }
 
-// The router GEMM's launch; with finish false and a K split, the slices stay in ws for the caller (*ks_out, *ldp_out)
+// The router GEMM's launch; with finish false and a K split, the slices stay in ws for the caller (*ks_out, *ldp_out).
+// split_rows (> 0): the row count the K split is chosen for, in place of E + n_gate.
 static int router_gemm(const char *fn, const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws,
-                       float *logits, float *gate, bool finish, int *ks_out, int *ldp_out, hipStream_t st) {
+                       float *logits, float *gate, bool finish, int *ks_out, int *ldp_out, hipStream_t st,
+                       int split_rows = 0) {
   LMOE_REQUIRE(T >= 0 && E > 0 && (n_gate == 0 || n_gate == 1), LMOE_ESHAPE, "%s: bad shape", fn);
   LMOE_REQUIRE(H > 0 && H % GK == 0, LMOE_ESHAPE, "%s: hidden size %d is not a multiple of %d", fn, H, GK);
   if (T == 0) return 0;
@@ -2174,7 +2176,7 @@ static int router_gemm(const char *fn, const void *xh, int T, int H, const void 
   const int En = E + n_gate;
   LMOE_REQUIRE((long long)T * H * 2 <= 0xFFFFFFFFll && (long long)En * H * 2 <= 0xFFFFFFFFll, LMOE_ESHAPE,
                "%s: x or the weight exceeds 4 GiB", fn);
-  const int ks = lmoe_router_gemm_ksplit(T, H, En);
+  const int ks = lmoe_router_gemm_ksplit(T, H, split_rows > 0 ? split_rows : En);
   const int n_ntile = (En + kRgN - 1) / kRgN, ldp = n_ntile * kRgN;
   LMOE_REQUIRE(ks == 1 || (ws && aligned16(ws)), LMOE_EWORKSPACE,
                "%s: needs a 16-byte aligned workspace of lmoe_router_gemm_workspace_bytes", fn);
@@ -2206,7 +2208,10 @@ extern "C" int lmoe_router_refine(const float *part, int ksplit, int ldp, const 
                                   int *n_cand, void *stream);
 
 // The router GEMM, then its picks made exact by lmoe_router_refine (refine.hip) straight from the K slices (or the
-// logits, unsplit): ids equal to the top-k of the decode router's fixed-order logits on the same x.
+// logits, unsplit): ids equal to the top-k of the decode router's fixed-order logits on the same x. The shared
+// expert's gate row is left out of the GEMM: the refine recomputes it in the fixed order for every token (at E = 512
+// that row alone was a fifth of the GEMM's tiles). The K split is still chosen for E + n_gate rows, so the slices,
+// and everything the refine derives from them, are those of the GEMM with the row.
 extern "C" int lmoe_router_gemm_refine(const void *xh, int T, int H, const void *wk, int E, int n_gate, float *ws,
                                        const void *x, int xdtype, const void *wr, const void *wsg, int wdtype,
                                        const float *norms, int k, int norm, int m, uint32_t *ids, float *scores,
@@ -2215,7 +2220,7 @@ extern "C" int lmoe_router_gemm_refine(const void *xh, int T, int H, const void 
   LMOE_REQUIRE((n_gate == 1) == (wsg != nullptr), LMOE_EINVAL, "%s: the gate row and wsg go together", fn);
   hipStream_t st = (hipStream_t)stream;
   int ks = 1, ldp = 0;
-  if (int rc = router_gemm(fn, xh, T, H, wk, E, n_gate, ws, logits, gate, false, &ks, &ldp, st)) return rc;
+  if (int rc = router_gemm(fn, xh, T, H, wk, E, 0, ws, logits, nullptr, false, &ks, &ldp, st, E + n_gate)) return rc;
   if (T == 0) return 0;
   return lmoe_router_refine(ks > 1 ? ws : logits, ks, ks > 1 ? ldp : E, x, xdtype, T, H, wr, wsg, wdtype, E, norms,
                             k, norm, m, ids, scores, logits, gate, n_cand, stream);

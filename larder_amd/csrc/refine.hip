@@ -376,7 +376,7 @@ extern "C" int lmoe_router_refine(const float *part, int ksplit, int ldp, const 
   LMOE_REQUIRE(E > 0 && E <= rf::kMaxE && k > 0 && k <= E && k <= 32 && m >= 0 && k + m <= 64, LMOE_ESHAPE,
                "%s: top-%d of %d experts with %d shared slices", fn, k, E, m);
   LMOE_REQUIRE(ksplit == 1 || ksplit == 2 || ksplit == 4 || ksplit == 8, LMOE_ESHAPE, "%s: K split %d", fn, ksplit);
-  LMOE_REQUIRE(ldp >= E + (wsg ? 1 : 0) || (ksplit == 1 && ldp >= E), LMOE_ESHAPE, "%s: row stride %d", fn, ldp);
+  LMOE_REQUIRE(ldp >= E, LMOE_ESHAPE, "%s: row stride %d", fn, ldp);  // only the E experts' columns are read
   LMOE_REQUIRE(m == 0 || wsg, LMOE_EINVAL, "%s: shared slices need the gate row", fn);
   if (T == 0) return 0;
   LMOE_REQUIRE(part && x && wr && norms && ids && scores, LMOE_EINVAL, "%s: null pointer", fn);
